@@ -1,0 +1,239 @@
+#!/usr/bin/env python3
+"""Benchmark of the qvx engine on one MI355X, against the BASELINE.json metric:
+"Q4_K GEMV HBM GB/s (% of peak) at M=1; Q4_K prefill GEMM TFLOPS (% MFMA)".
+
+A step is one Q4_K GEMV 4096 -> 14336 at M=1 (gate/up shape) over one of
+`--copies` distinct seeded weight copies (>= 1 GiB in total, so every timed read comes from HBM
+rather than the 256 MB Infinity Cache).  `value` is algorithmic bytes per step (weights +
+activation + output) / time per step, with inputs resident in HBM.  The prefill GEMM
+(Q4_K 4096 -> 14336, fp16 X, M = 2048, bf16 MFMA) is reported beside it.
+`cpu_baseline` times the reference's own CPU qmatmul (oracle/_ref, built from the reference's
+sources) on the same weights on this host's cores.
+
+Prints exactly one JSON line on stdout; diagnostics go to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 / fp16 MFMA
+ROWS, COLS = 14336, 4096       # Q4_K gate/up projection of Llama-3-8B
+Q4K_ROW_BYTES = COLS // 256 * 144
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def algorithmic_bytes(rows, cols, m, wbytes):
+    return wbytes + 4 * m * cols + 4 * m * rows
+
+
+def cpu_baseline(w_host, x_host, rows, cols, budget_s=10.0):
+    """The reference's CPU qmatmul (oracle/_ref, else the C restatement) on this host's cores."""
+    import numpy as np
+    import oracle
+    kind, fn = "reference", None
+    so = oracle.ref_lib()
+    if so is not None:
+        fn = so.qvxr_qmatmul
+        dot = so.qvxr_dot_kernel().decode()
+    else:
+        kind = "port"
+        so = oracle.lib()
+        fn = so.qvxo_qmatmul
+        dot = so.qvxo_dot_kernel().decode()
+    out = np.zeros(rows, np.float32)
+    wp = w_host.ctypes.data
+    fn(out, wp, 12, x_host, rows, cols)  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 200):
+        t0 = time.perf_counter()
+        fn(out, wp, 12, x_host, rows, cols)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    cores = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or len(os.sched_getaffinity(0))
+    nbytes = algorithmic_bytes(rows, cols, 1, w_host.size)
+    return {
+        "value": round(nbytes / med / 1e9, 3),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": kind,
+        "sample": f"Q4_K GEMV {cols}->{rows} M=1, same seeded blocks, 1 warm-up + median of {len(times)} runs "
+                  f"({sum(times):.1f} s), OpenMP threads={cores}, dot kernel={dot}",
+        "ms_per_gemv": round(med * 1e3, 3),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--copies", type=int, default=40, help="distinct weight copies cycled per step")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--gemm-steps", type=int, default=20)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the qvx engine has no multi-GPU "
+              "path in this build.", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import qorvix_amd as qvx
+
+    assert torch.cuda.is_available(), "no GPU visible"
+    qvx.lib()  # fails loudly if libqvx.so was not built
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream()
+    t = qvx.Q4_K
+    wbytes = qvx.weight_bytes(t, ROWS, COLS)
+
+    # ---- data: seeded synthetic Q4_K blocks and x ~ N(0,1) ----------------
+    copies = [qvx.empty_weight(t, ROWS, COLS, dev) for _ in range(args.copies)]
+    for i, w in enumerate(copies):
+        qvx.fill_synthetic_t(w, t, ROWS, COLS, seed=1000 + i, scale_mul=1e-3)
+    x = torch.empty(COLS, dtype=torch.float32, device=dev)
+    qvx.fill_normal_t(x, seed=7)
+    out = torch.empty(ROWS, dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    log(f"[bench] {args.copies} Q4_K copies x {wbytes / 2**20:.1f} MiB = {args.copies * wbytes / 2**30:.2f} GiB")
+
+    lib = qvx.lib()
+    sh = stream.cuda_stream
+    xp, op = x.data_ptr(), out.data_ptr()
+    wps = [w.data_ptr() for w in copies]
+
+    def step(i):
+        rc = lib.qvx_qmatmul(op, wps[i % len(wps)], t, xp, ROWS, COLS, sh)
+        if rc != 0:
+            raise RuntimeError(f"qvx_qmatmul failed: {qvx.strerror(rc)}")
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    # ---- timed region: K steps between two events on the launch stream -------------------------
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_total = ev0.elapsed_time(ev1)
+    ms_per_step = ms_total / args.steps
+    nbytes = algorithmic_bytes(ROWS, COLS, 1, wbytes)
+    gbs = nbytes / (ms_per_step * 1e-3) / 1e9
+    log(f"[bench] GEMV: {args.steps} steps in {ms_total:.3f} ms (wall {wall * 1e3:.1f} ms): "
+        f"{ms_per_step * 1e3:.2f} us/step, {gbs:.0f} GB/s")
+
+    # per-launch event pairs (kernel duration incl. event overhead), for the roofline line
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(64)]
+    for i, (a, b) in enumerate(evs):
+        a.record(stream)
+        step(i + 7)
+        b.record(stream)
+    torch.cuda.synchronize()
+    pair_us = sorted(a.elapsed_time(b) * 1e3 for a, b in evs)
+    pair_med = statistics.median(pair_us)
+    log(f"[bench] GEMV per-launch event pairs: median {pair_med:.2f} us, min {pair_us[0]:.2f} us")
+
+    # ---- prefill GEMM ----------------------------------------------------
+    gemm = {}
+    try:
+        for M in (2048, 512, 128):
+            X = torch.empty((M, COLS), dtype=torch.float16, device=dev)
+            qvx.fill_normal_t(X, seed=11, mul=0.5)
+            Y = torch.empty((M, ROWS), dtype=torch.float32, device=dev)
+            for name, var in (("bf16", qvx.GEMM_BF16), ("f16", qvx.GEMM_F16)):
+                def g(i):
+                    rc = lib.qvx_qgemm_f16(Y.data_ptr(), wps[i % len(wps)], t, X.data_ptr(), M, ROWS, COLS, var, sh)
+                    if rc != 0:
+                        raise RuntimeError(f"qvx_qgemm_f16 failed: {qvx.strerror(rc)}")
+                for i in range(3):
+                    g(i)
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for i in range(args.gemm_steps):
+                    g(i)
+                e1.record(stream)
+                torch.cuda.synchronize()
+                ms = e0.elapsed_time(e1) / args.gemm_steps
+                tflops = 2.0 * M * ROWS * COLS / (ms * 1e-3) / 1e12
+                gemm[f"{name}_M{M}"] = {"ms": round(ms, 4), "tflops": round(tflops, 1),
+                                        "frac_of_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4)}
+                log(f"[bench] GEMM {name} M={M}: {ms * 1e3:.1f} us, {tflops:.1f} TFLOP/s "
+                    f"({100 * tflops / BF16_PEAK_TFLOPS:.1f}% of bf16 peak)")
+            del X, Y
+    except RuntimeError as e:  # report, never hide: the JSON carries the error
+        gemm["error"] = str(e)
+        log(f"[bench] GEMM failed: {e}")
+
+    # ---- CPU baseline (reference CPU operator on this host) ------------------------------------
+    cpu = None
+    if not args.no_cpu:
+        w_host = copies[0].cpu().numpy()
+        x_host = x.cpu().numpy()
+        cpu = cpu_baseline(w_host, x_host, ROWS, COLS)
+        log(f"[bench] CPU baseline ({cpu['kind']}): {cpu['value']} GB/s, {cpu['ms_per_gemv']} ms/GEMV")
+
+    achieved = nbytes / (ms_per_step * 1e-3) / 1e9
+    g2048 = gemm.get("bf16_M2048", {})
+    result = {
+        "metric": "Q4_K GEMV HBM GB/s (% of peak) at M=1; Q4_K prefill GEMM TFLOPS (% MFMA)",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded Q4_K blocks: fp16 d, dmin = |N(0,1)|*1e-3, uniform scale/quant bytes; x ~ N(0,1))",
+        "config": {
+            "workload": "Q4_K GEMV 4096->14336, M=1 (BASELINE configs[2]); one step = one GEMV",
+            "rows": ROWS, "cols": COLS, "M": 1, "weight_copies": args.copies,
+            "weight_bytes": wbytes, "algorithmic_bytes_per_step": nbytes,
+        },
+        "percent_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "k_gemv<12,1,RL>",
+            "per_launch_event_pair_us": round(pair_med, 3),
+        },
+        "gemm": {
+            "workload": "Q4_K 4096->14336 GEMM, X fp16 [M,4096], fp32 out (BASELINE configs[3])",
+            "tflops_bf16_M2048": g2048.get("tflops"),
+            "percent_of_bf16_peak_M2048": round(100 * g2048["frac_of_bf16_peak"], 2) if g2048 else None,
+            "runs": gemm,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,129 @@
+/*
+ * qvx.h -- C ABI of the MI355X (gfx950) GGUF quantized-matmul engine (libqvx.so).
+ *
+ * The engine computes the QorVix weight x activation operator on the GPU:
+ *   out[v, r] = sum_k dequant(W)[r, k] * X[v, k]
+ * with W in raw GGUF block layout (row r starts at r * (cols / blockSize) * typeSize bytes),
+ * X fp32 [n_vec, cols] row-major and out fp32 [n_vec, rows] row-major -- the reference's
+ * qmatmul / qmatmulN contract (runtime/include/qorvix/runtime/qmatmul.hpp:14-36).
+ *
+ * Conventions
+ *  - `type` is the raw on-disk ggml type id (Q4_0 = 2, Q8_0 = 8, Q4_K = 12, Q6_K = 14, F32 = 0, ...).
+ *  - Every call returns QVX_OK (0) or a negative QVX_E_* code.  All argument checks run before any
+ *    device work, so `out` is untouched on failure -- the reference's `false` cases map one for one:
+ *      unknown / unsupported type        -> QVX_E_TYPE   (qmatmul.cpp:30-31)
+ *      blockSize > 256 or cols % bs != 0 -> QVX_E_SHAPE  (qmatmul.cpp:32-33, :70-72)
+ *      n_vec <= 0                        -> QVX_E_NVEC   (qmatmul.cpp:66)
+ *    rows <= 0 is a successful no-op and cols == 0 writes zeros, as the reference's loops do.
+ *  - Device entry points take device pointers and a hipStream_t passed as `void*` (NULL = the
+ *    null stream).  They are asynchronous and stream-ordered, like the CUDA backend's matmulS
+ *    launch (cuda/src/cuda_backend.cu:1534-1542).  They allocate no device memory, except
+ *    qvx_qgemm_f16 with QVX_GEMM_I8, which keeps a per-device workspace that grows on demand.
+ *  - Entry points ending in _host take host pointers and are synchronous: the exact calling
+ *    convention of the reference's CPU operator, for a CPU-side drop-in.
+ *  - Calls that overlap on one device are safe for distinct outputs; the library holds no
+ *    mutable per-call state except the I8 workspace (serialised by a mutex).
+ */
+#ifndef QVX_H
+#define QVX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QVX_OK 0
+#define QVX_E_TYPE (-1)    /* unknown ggml type, or one this engine does not compute */
+#define QVX_E_SHAPE (-2)   /* cols not a multiple of the block size, block size > 256, bad M/K */
+#define QVX_E_NVEC (-3)    /* n_vec <= 0 */
+#define QVX_E_NULL (-4)    /* a required pointer is NULL */
+#define QVX_E_HIP (-5)     /* the HIP runtime reported an error (launch, copy, allocation) */
+#define QVX_E_VARIANT (-6) /* unknown GEMM variant */
+#define QVX_E_RANGE (-7)   /* row index out of range, n not a whole number of blocks, size overflow */
+
+/* GEMM variants for qvx_qgemm_f16 */
+#define QVX_GEMM_BF16 0 /* weights dequantised to bf16 tiles in LDS, X rounded to bf16, bf16 MFMA */
+#define QVX_GEMM_I8 1   /* X quantised per 32 to int8 (Q8), weight quants as int8, int8 MFMA */
+#define QVX_GEMM_F16 2  /* weights dequantised to fp16 tiles, X kept fp16, fp16 MFMA */
+
+/* Version string of the engine, e.g. "qvx 0.1 gfx950". */
+const char* qvx_version(void);
+
+/* Message of a QVX_E_* code. */
+const char* qvx_strerror(int code);
+
+/* 1 if the GEMV / GEMM kernels compute `type` (qmatmul.cpp:24-26, qmatmulSupports).
+ * Types the reference also dequantises (F16, BF16, Q4_1, Q5_0, Q5_1, Q8_1, Q5_K) return 0 here:
+ * a caller falls back for them, and qvx_dequantize still handles them bit-exactly. */
+int qvx_supports(uint32_t type);
+
+/* 1 if qvx_dequantize handles `type` (dequant.cpp:257-275, canDequantize). */
+int qvx_can_dequantize(uint32_t type);
+
+/* Elements per block and bytes per block of a ggml type; 0 if unknown (gguf_types.cpp:49-54). */
+int qvx_type_traits(uint32_t type, uint32_t* block_size, uint32_t* type_size);
+
+/* Exact IEEE half -> single (dequant.cpp:222-248, fp16ToFloat).  Host function. */
+float qvx_fp16_to_float(uint16_t h);
+
+/* ---- device entry points (device pointers, stream-ordered) --------------------------------- */
+
+/* out[r] = dot(dequant(row r of W), x), r < rows.  Replaces qmatmul (qmatmul.cpp:28-62).
+ * fp32 accumulation; within max|y-ref|/max|ref| <= 1e-3 of the exact sum. */
+int qvx_qmatmul(float* d_out, const void* d_w, uint32_t type, const float* d_x, int rows, int cols,
+                void* stream);
+
+/* out[v * rows + r] for v < n_vec.  Replaces qmatmulN (qmatmul.cpp:64-115).  Each output is
+ * bit-identical to qvx_qmatmul on that vector, as the reference promises (qmatmul.hpp:31-32). */
+int qvx_qmatmul_n(float* d_out, const void* d_w, uint32_t type, const float* d_X, int n_vec,
+                  int rows, int cols, void* stream);
+
+/* Dequantise n elements (n a whole number of blocks) of `type` to fp32, bit-exact with the
+ * reference's dequantize (dequant.cpp:277-296) for every value but NaN payloads. */
+int qvx_dequantize(uint32_t type, const void* d_src, float* d_dst, size_t n, void* stream);
+
+/* Dequantise row `row` (cols elements) of W.  Replaces dequantRow (qmatmul.cpp:117-126); as
+ * there, the caller guarantees the row exists.  row < 0 -> QVX_E_RANGE. */
+int qvx_dequant_row(const void* d_w, uint32_t type, int cols, int row, float* d_dst, void* stream);
+
+/* Prefill GEMM: out[m * rows + r] = sum_k X[m, k] * dequant(W)[r, k] for m < M, X fp16 [M, cols].
+ * No reference counterpart (the reference prefills token by token); semantics are qmatmulN's
+ * with X converted fp16 -> fp32 exactly.  variant = QVX_GEMM_BF16 | QVX_GEMM_F16 | QVX_GEMM_I8;
+ * tolerance 2e-2 max-relative against the exact sum.  type: Q4_K, Q4_0, Q8_0, Q6_K. */
+int qvx_qgemm_f16(float* d_out, const void* d_w, uint32_t type, const uint16_t* d_X, int M,
+                  int rows, int cols, int variant, void* stream);
+
+/* Per-32 Q8 activation quantiser used by QVX_GEMM_I8 (no reference counterpart): for row m and
+ * block j, scale = amax/127, q = round-half-away(x * 127/amax) clamped to +-127, qsum = sum q.
+ * d_q int8 [M, K], d_scale fp32 [M, K/32], d_qsum int32 [M, K/32]; K % 32 == 0. */
+int qvx_quantize_act_q8(const uint16_t* d_X, int M, int K, int8_t* d_q, float* d_scale,
+                        int32_t* d_qsum, void* stream);
+
+/* Fill a [rows, cols] weight of `type` with seeded synthetic blocks on the device (benchmark and
+ * test data; no reference counterpart).  Scales are fp16(|N(0,1)| * scale_mul) (Q4_K: d and dmin;
+ * Q6_K: d), quant bytes uniform, Q6_K int8 sub-scales uniform over [-128, 127].  Deterministic in
+ * (seed, byte position). */
+int qvx_fill_synthetic(void* d_w, uint32_t type, int rows, int cols, uint64_t seed, float scale_mul,
+                       void* stream);
+
+/* Fill n fp32 values with N(0,1) * mul (seeded, deterministic), or n fp16 values. */
+int qvx_fill_normal_f32(float* d_x, size_t n, uint64_t seed, float mul, void* stream);
+int qvx_fill_normal_f16(uint16_t* d_x, size_t n, uint64_t seed, float mul, void* stream);
+
+/* ---- host entry points (host pointers, synchronous) --------------------------------------- */
+/* The reference's CPU signatures (qmatmul.hpp:14-36, dequant.hpp:12-21) over the GPU kernels:
+ * weight, x and out live in host memory; the call uploads, computes on the current device and
+ * downloads before returning. */
+int qvx_qmatmul_host(float* out, const void* w, uint32_t type, const float* x, int rows, int cols);
+int qvx_qmatmul_n_host(float* out, const void* w, uint32_t type, const float* X, int n_vec, int rows,
+                       int cols);
+int qvx_dequantize_host(uint32_t type, const void* src, float* dst, size_t n);
+int qvx_dequant_row_host(const void* w, uint32_t type, int cols, int row, float* dst);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QVX_H */

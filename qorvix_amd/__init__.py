@@ -1,0 +1,228 @@
+"""qorvix_amd -- MI355X (gfx950) engine for the QorVix GGUF quantized matmul.
+
+Host-side Python mirror of the reference operator (``runtime/include/qorvix/runtime/qmatmul.hpp``
+and ``dequant.hpp``) over the C ABI of ``libqvx.so`` (``include/qvx.h``).  The functions keep the
+reference's names, argument meaning and error behaviour: the reference returns ``false`` where
+these return ``False`` (or raise, for the ``*_t`` tensor helpers), with the same cases rejected
+before any device work.
+
+Two layers:
+
+* raw-pointer functions (``qmatmul``, ``qmatmul_n``, ``dequantize``, ``dequant_row``,
+  ``qgemm_f16`` ...) taking device addresses and a HIP stream handle -- the C ABI as is;
+* torch helpers (``qmatmul_t`` ...) taking ``torch.Tensor``s on ``cuda`` and launching on the
+  current torch stream; PyTorch is only the device-memory and stream plumbing.
+
+There is no CPU fallback: if ``libqvx.so`` is missing or no GPU is present, calls raise.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libqvx.so")
+
+# ggml type ids (public GGUF format)
+F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q8_1, Q4_K, Q5_K, Q6_K, BF16 = 0, 1, 2, 3, 6, 7, 8, 9, 12, 13, 14, 30
+TYPE_NAMES = {0: "F32", 1: "F16", 2: "Q4_0", 3: "Q4_1", 6: "Q5_0", 7: "Q5_1", 8: "Q8_0", 9: "Q8_1",
+              12: "Q4_K", 13: "Q5_K", 14: "Q6_K", 30: "BF16"}
+
+# status codes (include/qvx.h)
+OK, E_TYPE, E_SHAPE, E_NVEC, E_NULL, E_HIP, E_VARIANT, E_RANGE = 0, -1, -2, -3, -4, -5, -6, -7
+# GEMM variants
+GEMM_BF16, GEMM_I8, GEMM_F16 = 0, 1, 2
+
+# The C ABI: name -> (argtypes, restype).  tests/test_capi.py checks this table against qvx.h.
+_vp, _u32, _i32, _sz, _u64, _f32 = C.c_void_p, C.c_uint32, C.c_int, C.c_size_t, C.c_uint64, C.c_float
+SIGNATURES = {
+    "qvx_version": ([], C.c_char_p),
+    "qvx_strerror": ([_i32], C.c_char_p),
+    "qvx_supports": ([_u32], _i32),
+    "qvx_can_dequantize": ([_u32], _i32),
+    "qvx_type_traits": ([_u32, C.POINTER(_u32), C.POINTER(_u32)], _i32),
+    "qvx_fp16_to_float": ([C.c_uint16], _f32),
+    "qvx_qmatmul": ([_vp, _vp, _u32, _vp, _i32, _i32, _vp], _i32),
+    "qvx_qmatmul_n": ([_vp, _vp, _u32, _vp, _i32, _i32, _i32, _vp], _i32),
+    "qvx_dequantize": ([_u32, _vp, _vp, _sz, _vp], _i32),
+    "qvx_dequant_row": ([_vp, _u32, _i32, _i32, _vp, _vp], _i32),
+    "qvx_qgemm_f16": ([_vp, _vp, _u32, _vp, _i32, _i32, _i32, _i32, _vp], _i32),
+    "qvx_quantize_act_q8": ([_vp, _i32, _i32, _vp, _vp, _vp, _vp], _i32),
+    "qvx_fill_synthetic": ([_vp, _u32, _i32, _i32, _u64, _f32, _vp], _i32),
+    "qvx_fill_normal_f32": ([_vp, _sz, _u64, _f32, _vp], _i32),
+    "qvx_fill_normal_f16": ([_vp, _sz, _u64, _f32, _vp], _i32),
+    "qvx_qmatmul_host": ([_vp, _vp, _u32, _vp, _i32, _i32], _i32),
+    "qvx_qmatmul_n_host": ([_vp, _vp, _u32, _vp, _i32, _i32, _i32], _i32),
+    "qvx_dequantize_host": ([_u32, _vp, _vp, _sz], _i32),
+    "qvx_dequant_row_host": ([_vp, _u32, _i32, _i32, _vp], _i32),
+}
+
+_lib = None
+
+
+class QvxError(RuntimeError):
+    """A qvx entry point returned a negative status."""
+
+    def __init__(self, code: int, what: str = ""):
+        self.code = code
+        super().__init__(f"{what}: qvx status {code} ({strerror(code)})" if what else strerror(code))
+
+
+def lib():
+    """Loads libqvx.so (raises if it was never built: there is no fallback path)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is missing; run __graft_entry__.build() or "
+                              "python qorvix_amd/buildlib.py first")
+        so = C.CDLL(LIB_PATH)
+        for name, (argtypes, restype) in SIGNATURES.items():
+            fn = getattr(so, name)
+            fn.argtypes = argtypes
+            fn.restype = restype
+        _lib = so
+    return _lib
+
+
+def build() -> str:
+    """Compile libqvx.so in-tree (hipcc, gfx950) and return its path."""
+    from . import buildlib
+    global _lib
+    _lib = None
+    return buildlib.build()
+
+
+def strerror(code: int) -> str:
+    try:
+        return lib().qvx_strerror(code).decode()
+    except ImportError:
+        return f"status {code}"
+
+
+def version() -> str:
+    return lib().qvx_version().decode()
+
+
+# ---- reference-shaped API (raw device pointers; bool results like the reference) -----------------
+
+def supports(ggml_type: int) -> bool:
+    """qmatmulSupports (runtime/src/qmatmul.cpp:24-26) for the GPU kernels."""
+    return bool(lib().qvx_supports(ggml_type))
+
+
+def can_dequantize(ggml_type: int) -> bool:
+    """canDequantize (runtime/src/dequant.cpp:257-275)."""
+    return bool(lib().qvx_can_dequantize(ggml_type))
+
+
+def type_traits(ggml_type: int):
+    """(block_size, type_size) or None (gguf/src/gguf_types.cpp:49-54)."""
+    b, n = C.c_uint32(), C.c_uint32()
+    if not lib().qvx_type_traits(ggml_type, C.byref(b), C.byref(n)):
+        return None
+    return b.value, n.value
+
+
+def fp16_to_float(h: int) -> float:
+    """fp16ToFloat (runtime/src/dequant.cpp:222-248)."""
+    return lib().qvx_fp16_to_float(h)
+
+
+def row_bytes(ggml_type: int, cols: int) -> int:
+    bs, ts = type_traits(ggml_type)
+    return cols // bs * ts
+
+
+def weight_bytes(ggml_type: int, rows: int, cols: int) -> int:
+    return rows * row_bytes(ggml_type, cols)
+
+
+def qmatmul(out: int, weight: int, ggml_type: int, x: int, rows: int, cols: int, stream: int = 0) -> int:
+    """out[r] = dot(dequant(row r), x) on device pointers (runtime/src/qmatmul.cpp:28-62). Status."""
+    return lib().qvx_qmatmul(out, weight, ggml_type, x, rows, cols, stream)
+
+
+def qmatmul_n(out: int, weight: int, ggml_type: int, X: int, nvec: int, rows: int, cols: int,
+              stream: int = 0) -> int:
+    """Batched form (runtime/src/qmatmul.cpp:64-115); out [nvec, rows]. Status."""
+    return lib().qvx_qmatmul_n(out, weight, ggml_type, X, nvec, rows, cols, stream)
+
+
+def dequantize(ggml_type: int, src: int, dst: int, n: int, stream: int = 0) -> int:
+    """dequantize (runtime/src/dequant.cpp:277-296) on device pointers. Status."""
+    return lib().qvx_dequantize(ggml_type, src, dst, n, stream)
+
+
+def dequant_row(weight: int, ggml_type: int, cols: int, row: int, dst: int, stream: int = 0) -> int:
+    """dequantRow (runtime/src/qmatmul.cpp:117-126) on device pointers. Status."""
+    return lib().qvx_dequant_row(weight, ggml_type, cols, row, dst, stream)
+
+
+def qgemm_f16(out: int, weight: int, ggml_type: int, X: int, M: int, rows: int, cols: int,
+              variant: int = GEMM_BF16, stream: int = 0) -> int:
+    """Prefill GEMM, X fp16 [M, cols] -> out fp32 [M, rows] on the matrix cores. Status."""
+    return lib().qvx_qgemm_f16(out, weight, ggml_type, X, M, rows, cols, variant, stream)
+
+
+# ---- torch helpers (device tensors, current stream; raise on failure) ------------------------------
+
+def _stream():
+    import torch
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != OK:
+        raise QvxError(rc, what)
+
+
+def empty_weight(ggml_type: int, rows: int, cols: int, device="cuda"):
+    """A uint8 device tensor sized for a [rows, cols] weight of ggml_type."""
+    import torch
+    return torch.empty(weight_bytes(ggml_type, rows, cols), dtype=torch.uint8, device=device)
+
+
+def fill_synthetic_t(w, ggml_type: int, rows: int, cols: int, seed: int, scale_mul: float):
+    _check(lib().qvx_fill_synthetic(w.data_ptr(), ggml_type, rows, cols, seed, scale_mul, _stream()),
+           "qvx_fill_synthetic")
+    return w
+
+
+def fill_normal_t(x, seed: int, mul: float = 1.0):
+    import torch
+    if x.dtype == torch.float32:
+        _check(lib().qvx_fill_normal_f32(x.data_ptr(), x.numel(), seed, mul, _stream()), "fill_normal_f32")
+    elif x.dtype == torch.float16:
+        _check(lib().qvx_fill_normal_f16(x.data_ptr(), x.numel(), seed, mul, _stream()), "fill_normal_f16")
+    else:
+        raise TypeError("fill_normal_t takes float32 or float16 tensors")
+    return x
+
+
+def qmatmul_t(w, ggml_type: int, x, rows: int, cols: int, out=None):
+    """out[rows] fp32 = W x for a device weight tensor and fp32 x [cols] (or [n, cols])."""
+    import torch
+    nvec = 1 if x.dim() == 1 else x.shape[0]
+    if out is None:
+        out = torch.empty((nvec, rows) if x.dim() > 1 else (rows,), dtype=torch.float32, device=x.device)
+    _check(lib().qvx_qmatmul_n(out.data_ptr(), w.data_ptr(), ggml_type, x.data_ptr(), nvec, rows, cols,
+                               _stream()), "qvx_qmatmul_n")
+    return out
+
+
+def dequantize_t(w, ggml_type: int, n: int, out=None):
+    import torch
+    if out is None:
+        out = torch.empty(n, dtype=torch.float32, device=w.device)
+    _check(lib().qvx_dequantize(ggml_type, w.data_ptr(), out.data_ptr(), n, _stream()), "qvx_dequantize")
+    return out
+
+
+def qgemm_t(w, ggml_type: int, X, rows: int, cols: int, variant: int = GEMM_BF16, out=None):
+    import torch
+    M = X.shape[0]
+    if out is None:
+        out = torch.empty((M, rows), dtype=torch.float32, device=X.device)
+    _check(lib().qvx_qgemm_f16(out.data_ptr(), w.data_ptr(), ggml_type, X.data_ptr(), M, rows, cols, variant,
+                               _stream()), "qvx_qgemm_f16")
+    return out

@@ -1,0 +1,285 @@
+// qvx_api.hip -- the extern "C" boundary of libqvx.so (declared in include/qvx.h).
+//
+// Argument checks mirror the reference's operator (runtime/src/qmatmul.cpp:24-126) one for one
+// and run before any device work; then the call dispatches on the ggml type to the gfx950
+// kernels.  The engine never falls back to the CPU: a missing device or a failed launch is an
+// error code.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "../../include/qvx.h"
+#include "qvx_common.hpp"
+
+namespace qvx {
+bool launch_dequant(uint32_t t, const void* src, float* dst, size_t n, hipStream_t s);
+bool launch_gemv_generic(uint32_t t, const void* w, const float* X, float* Y, int rows, int cols, int nvec,
+                         size_t row_bytes, hipStream_t s);
+bool launch_gemv_fast(uint32_t t, const void* w, const float* X, float* Y, int nvec, int rows, int cols,
+                      size_t row_bytes, hipStream_t s);
+bool launch_fill_synthetic(void* w, uint32_t t, size_t nblk, uint64_t seed, float mul, hipStream_t s);
+void launch_fill_normal_f32(float* x, size_t n, uint64_t seed, float mul, hipStream_t s);
+void launch_fill_normal_f16(uint16_t* x, size_t n, uint64_t seed, float mul, hipStream_t s);
+int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M, int rows, int cols,
+                 int variant, hipStream_t s);
+int launch_quantize_act_q8(const uint16_t* X, int M, int K, int8_t* q, float* scale, int32_t* qsum,
+                           hipStream_t s);
+void launch_zero(float* p, size_t n, hipStream_t s);
+}  // namespace qvx
+
+using namespace qvx;
+
+namespace {
+
+constexpr int kMaxBlock = 256;  // largest block the operator accepts (qmatmul.cpp:11)
+
+inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+inline int hip_status() {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    std::fprintf(stderr, "qvx: HIP error %d (%s)\n", (int)e, hipGetErrorString(e));
+    return QVX_E_HIP;
+  }
+  return QVX_OK;
+}
+
+// Shape checks shared by qmatmul / qmatmul_n / qgemm: the reference's order of tests.
+inline int check_matmul(uint32_t type, int cols, const TypeInfo** ti) {
+  const TypeInfo* t = type_info(type);
+  if (!t || !can_dequantize(type) || !gemv_supports(type)) return QVX_E_TYPE;
+  if (t->block == 0 || (int)t->block > kMaxBlock || cols % (int)t->block != 0) return QVX_E_SHAPE;
+  *ti = t;
+  return QVX_OK;
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int rows, int cols, hipStream_t s) {
+  const TypeInfo* ti = nullptr;
+  if (nvec <= 0) return QVX_E_NVEC;
+  if (int rc = check_matmul(type, cols, &ti); rc != QVX_OK) return rc;
+  if (rows <= 0) return QVX_OK;
+  if (!out) return QVX_E_NULL;
+  if (cols <= 0) {  // no columns: every dot product is empty (the reference writes 0.0f)
+    launch_zero(out, (size_t)rows * (size_t)nvec, s);
+    return hip_status();
+  }
+  if (!w || !X) return QVX_E_NULL;
+  const size_t row_bytes = (size_t)(cols / (int)ti->block) * ti->bytes;
+  const bool fast = type != T_F32 && aligned16(w) && aligned16(X) && row_bytes % 16 == 0;
+  for (int v0 = 0; v0 < nvec; v0 += 16) {
+    const int nv = nvec - v0 < 16 ? nvec - v0 : 16;
+    const float* Xv = X + (size_t)v0 * cols;
+    float* Yv = out + (size_t)v0 * rows;
+    const bool ok = fast ? launch_gemv_fast(type, w, Xv, Yv, nv, rows, cols, row_bytes, s)
+                         : launch_gemv_generic(type, w, Xv, Yv, rows, cols, nv, row_bytes, s);
+    if (!ok) return QVX_E_TYPE;
+  }
+  return hip_status();
+}
+
+// Device buffer reused by the synchronous host-pointer entry points (one per calling thread).
+struct HostStage {
+  void* p = nullptr;
+  size_t cap = 0;
+  ~HostStage() {
+    if (p) (void)hipFree(p);
+  }
+  void* get(size_t n) {
+    if (n <= cap) return p;
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    cap = 0;
+    if (hipMalloc(&p, n) != hipSuccess) return nullptr;
+    cap = n;
+    return p;
+  }
+};
+thread_local HostStage g_stage;
+
+inline size_t align_up(size_t n) { return (n + 255) & ~size_t(255); }
+
+}  // namespace
+
+#pragma GCC visibility push(default)
+extern "C" {
+
+const char* qvx_version(void) { return "qvx 0.1 gfx950"; }
+
+const char* qvx_strerror(int code) {
+  switch (code) {
+    case QVX_OK: return "ok";
+    case QVX_E_TYPE: return "unsupported ggml type";
+    case QVX_E_SHAPE: return "cols is not a whole number of blocks (or bad shape)";
+    case QVX_E_NVEC: return "n_vec must be positive";
+    case QVX_E_NULL: return "null pointer argument";
+    case QVX_E_HIP: return "HIP runtime error";
+    case QVX_E_VARIANT: return "unknown GEMM variant";
+    case QVX_E_RANGE: return "index or size out of range";
+    default: return "unknown qvx status";
+  }
+}
+
+int qvx_supports(uint32_t type) { return type_info(type) && can_dequantize(type) && gemv_supports(type); }
+
+int qvx_can_dequantize(uint32_t type) { return can_dequantize(type) ? 1 : 0; }
+
+int qvx_type_traits(uint32_t type, uint32_t* block_size, uint32_t* type_size) {
+  const TypeInfo* t = type_info(type);
+  if (!t) return 0;
+  if (block_size) *block_size = t->block;
+  if (type_size) *type_size = t->bytes;
+  return 1;
+}
+
+float qvx_fp16_to_float(uint16_t h) { return f16_bits_to_f32(h); }
+
+int qvx_qmatmul(float* d_out, const void* d_w, uint32_t type, const float* d_x, int rows, int cols, void* stream) {
+  return gemv(d_out, d_w, type, d_x, 1, rows, cols, as_stream(stream));
+}
+
+int qvx_qmatmul_n(float* d_out, const void* d_w, uint32_t type, const float* d_X, int n_vec, int rows, int cols,
+                  void* stream) {
+  return gemv(d_out, d_w, type, d_X, n_vec, rows, cols, as_stream(stream));
+}
+
+int qvx_dequantize(uint32_t type, const void* d_src, float* d_dst, size_t n, void* stream) {
+  const TypeInfo* t = type_info(type);
+  if (!t || !can_dequantize(type)) return QVX_E_TYPE;
+  if (n % t->block != 0) return QVX_E_RANGE;  // the reference floors silently; this engine refuses
+  if (n == 0) return QVX_OK;
+  if (!d_src || !d_dst) return QVX_E_NULL;
+  if (!launch_dequant(type, d_src, d_dst, n, as_stream(stream))) return QVX_E_TYPE;
+  return hip_status();
+}
+
+int qvx_dequant_row(const void* d_w, uint32_t type, int cols, int row, float* d_dst, void* stream) {
+  const TypeInfo* t = type_info(type);
+  if (!t || !can_dequantize(type)) return QVX_E_TYPE;
+  if (t->block == 0 || cols % (int)t->block != 0) return QVX_E_SHAPE;
+  if (row < 0 || cols < 0) return QVX_E_RANGE;
+  if (cols == 0) return QVX_OK;
+  if (!d_w || !d_dst) return QVX_E_NULL;
+  const size_t row_bytes = (size_t)(cols / (int)t->block) * t->bytes;
+  const auto* src = static_cast<const uint8_t*>(d_w) + (size_t)row * row_bytes;
+  if (!launch_dequant(type, src, d_dst, (size_t)cols, as_stream(stream))) return QVX_E_TYPE;
+  return hip_status();
+}
+
+int qvx_qgemm_f16(float* d_out, const void* d_w, uint32_t type, const uint16_t* d_X, int M, int rows, int cols,
+                  int variant, void* stream) {
+  const TypeInfo* ti = nullptr;
+  if (M <= 0) return QVX_E_NVEC;
+  if (variant != QVX_GEMM_BF16 && variant != QVX_GEMM_I8 && variant != QVX_GEMM_F16) return QVX_E_VARIANT;
+  if (int rc = check_matmul(type, cols, &ti); rc != QVX_OK) return rc;
+  if (type == T_F32) return QVX_E_TYPE;
+  if (rows <= 0) return QVX_OK;
+  if (!d_out) return QVX_E_NULL;
+  if (cols <= 0) {
+    launch_zero(d_out, (size_t)rows * (size_t)M, as_stream(stream));
+    return hip_status();
+  }
+  if (!d_w || !d_X) return QVX_E_NULL;
+  const int rc = launch_qgemm(d_out, d_w, type, d_X, M, rows, cols, variant, as_stream(stream));
+  if (rc != QVX_OK) return rc;
+  return hip_status();
+}
+
+int qvx_quantize_act_q8(const uint16_t* d_X, int M, int K, int8_t* d_q, float* d_scale, int32_t* d_qsum,
+                        void* stream) {
+  if (M <= 0 || K <= 0 || K % 32 != 0) return QVX_E_SHAPE;
+  if (!d_X || !d_q || !d_scale || !d_qsum) return QVX_E_NULL;
+  const int rc = launch_quantize_act_q8(d_X, M, K, d_q, d_scale, d_qsum, as_stream(stream));
+  if (rc != QVX_OK) return rc;
+  return hip_status();
+}
+
+int qvx_fill_synthetic(void* d_w, uint32_t type, int rows, int cols, uint64_t seed, float scale_mul, void* stream) {
+  const TypeInfo* t = type_info(type);
+  if (!t || (type != T_Q8_0 && type != T_Q4_0 && type != T_Q4_K && type != T_Q6_K)) return QVX_E_TYPE;
+  if (rows < 0 || cols < 0 || cols % (int)t->block != 0) return QVX_E_SHAPE;
+  if (!d_w) return QVX_E_NULL;
+  const size_t nblk = (size_t)rows * (size_t)(cols / (int)t->block);
+  if (!launch_fill_synthetic(d_w, type, nblk, seed, scale_mul, as_stream(stream))) return QVX_E_TYPE;
+  return hip_status();
+}
+
+int qvx_fill_normal_f32(float* d_x, size_t n, uint64_t seed, float mul, void* stream) {
+  if (n && !d_x) return QVX_E_NULL;
+  launch_fill_normal_f32(d_x, n, seed, mul, as_stream(stream));
+  return hip_status();
+}
+
+int qvx_fill_normal_f16(uint16_t* d_x, size_t n, uint64_t seed, float mul, void* stream) {
+  if (n && !d_x) return QVX_E_NULL;
+  launch_fill_normal_f16(d_x, n, seed, mul, as_stream(stream));
+  return hip_status();
+}
+
+// ---- synchronous host-pointer forms --------------------------------------------------------------
+
+int qvx_qmatmul_n_host(float* out, const void* w, uint32_t type, const float* X, int n_vec, int rows, int cols) {
+  const TypeInfo* ti = nullptr;
+  if (n_vec <= 0) return QVX_E_NVEC;
+  if (int rc = check_matmul(type, cols, &ti); rc != QVX_OK) return rc;
+  if (rows <= 0) return QVX_OK;
+  if (!out) return QVX_E_NULL;
+  if (cols <= 0) {
+    std::memset(out, 0, sizeof(float) * (size_t)rows * (size_t)n_vec);
+    return QVX_OK;
+  }
+  if (!w || !X) return QVX_E_NULL;
+  const size_t wb = (size_t)rows * (size_t)(cols / (int)ti->block) * ti->bytes;
+  const size_t xb = sizeof(float) * (size_t)n_vec * (size_t)cols;
+  const size_t ob = sizeof(float) * (size_t)n_vec * (size_t)rows;
+  auto* base = static_cast<uint8_t*>(g_stage.get(align_up(wb) + align_up(xb) + align_up(ob)));
+  if (!base) return QVX_E_HIP;
+  void* dw = base;
+  auto* dx = reinterpret_cast<float*>(base + align_up(wb));
+  auto* dout = reinterpret_cast<float*>(base + align_up(wb) + align_up(xb));
+  if (hipMemcpy(dw, w, wb, hipMemcpyHostToDevice) != hipSuccess) return hip_status();
+  if (hipMemcpy(dx, X, xb, hipMemcpyHostToDevice) != hipSuccess) return hip_status();
+  const int rc = gemv(dout, dw, type, dx, n_vec, rows, cols, nullptr);
+  if (rc != QVX_OK) return rc;
+  if (hipMemcpy(out, dout, ob, hipMemcpyDeviceToHost) != hipSuccess) return hip_status();
+  return QVX_OK;
+}
+
+int qvx_qmatmul_host(float* out, const void* w, uint32_t type, const float* x, int rows, int cols) {
+  return qvx_qmatmul_n_host(out, w, type, x, 1, rows, cols);
+}
+
+int qvx_dequantize_host(uint32_t type, const void* src, float* dst, size_t n) {
+  const TypeInfo* t = type_info(type);
+  if (!t || !can_dequantize(type)) return QVX_E_TYPE;
+  if (n % t->block != 0) return QVX_E_RANGE;
+  if (n == 0) return QVX_OK;
+  if (!src || !dst) return QVX_E_NULL;
+  const size_t sb = n / t->block * t->bytes, db = n * sizeof(float);
+  auto* base = static_cast<uint8_t*>(g_stage.get(align_up(sb) + align_up(db)));
+  if (!base) return QVX_E_HIP;
+  auto* ddst = reinterpret_cast<float*>(base + align_up(sb));
+  if (hipMemcpy(base, src, sb, hipMemcpyHostToDevice) != hipSuccess) return hip_status();
+  if (!launch_dequant(type, base, ddst, n, nullptr)) return QVX_E_TYPE;
+  if (int rc = hip_status(); rc != QVX_OK) return rc;
+  if (hipMemcpy(dst, ddst, db, hipMemcpyDeviceToHost) != hipSuccess) return hip_status();
+  return QVX_OK;
+}
+
+int qvx_dequant_row_host(const void* w, uint32_t type, int cols, int row, float* dst) {
+  const TypeInfo* t = type_info(type);
+  if (!t || !can_dequantize(type)) return QVX_E_TYPE;
+  if (t->block == 0 || cols % (int)t->block != 0) return QVX_E_SHAPE;
+  if (row < 0 || cols < 0) return QVX_E_RANGE;
+  if (cols == 0) return QVX_OK;
+  if (!w || !dst) return QVX_E_NULL;
+  const size_t row_bytes = (size_t)(cols / (int)t->block) * t->bytes;
+  return qvx_dequantize_host(type, static_cast<const uint8_t*>(w) + (size_t)row * row_bytes, dst, (size_t)cols);
+}
+
+}  // extern "C"
+#pragma GCC visibility pop

@@ -1,0 +1,121 @@
+// qvx_common.hpp -- ggml type table and device helpers shared by the qvx HIP kernels (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace qvx {
+
+// On-disk ggml type ids (public GGUF format; gguf/include/qorvix/gguf/gguf_types.hpp:17-45).
+enum : uint32_t {
+  T_F32 = 0,
+  T_F16 = 1,
+  T_Q4_0 = 2,
+  T_Q4_1 = 3,
+  T_Q5_0 = 6,
+  T_Q5_1 = 7,
+  T_Q8_0 = 8,
+  T_Q8_1 = 9,
+  T_Q4_K = 12,
+  T_Q5_K = 13,
+  T_Q6_K = 14,
+  T_BF16 = 30,
+};
+
+struct TypeInfo {
+  uint32_t id, block, bytes;
+};
+
+// Elements / bytes per block of every id the GGUF format defines (gguf/src/gguf_types.cpp:15-45).
+inline constexpr TypeInfo kTypeTable[] = {
+    {0, 1, 4},      {1, 1, 2},      {2, 32, 18},    {3, 32, 20},    {6, 32, 22},    {7, 32, 24},
+    {8, 32, 34},    {9, 32, 36},    {10, 256, 84},  {11, 256, 110}, {12, 256, 144}, {13, 256, 176},
+    {14, 256, 210}, {15, 256, 292}, {16, 256, 66},  {17, 256, 74},  {18, 256, 98},  {19, 256, 50},
+    {20, 32, 18},   {21, 256, 110}, {22, 256, 82},  {23, 256, 136}, {24, 1, 1},     {25, 1, 2},
+    {26, 1, 4},     {27, 1, 8},     {28, 1, 8},     {29, 256, 56},  {30, 1, 2},
+};
+
+inline const TypeInfo* type_info(uint32_t t) {
+  for (const auto& e : kTypeTable)
+    if (e.id == t) return &e;
+  return nullptr;
+}
+
+// Types whose dequantisation this engine implements (the reference's canDequantize set).
+inline bool can_dequantize(uint32_t t) {
+  switch (t) {
+    case T_F32: case T_F16: case T_BF16: case T_Q8_0: case T_Q8_1: case T_Q4_0: case T_Q4_1:
+    case T_Q5_0: case T_Q5_1: case T_Q4_K: case T_Q5_K: case T_Q6_K:
+      return true;
+    default:
+      return false;
+  }
+}
+
+// Types the GEMV / GEMM kernels compute.
+inline bool gemv_supports(uint32_t t) {
+  return t == T_Q8_0 || t == T_Q4_0 || t == T_Q4_K || t == T_Q6_K || t == T_F32;
+}
+
+// Block geometry of the four GEMV formats.  A "panel" is PB consecutive blocks of a row: 2048
+// elements, PB*BB bytes, always a multiple of 16 so panels of 16-byte-aligned rows stay aligned.
+template <uint32_t T> struct Fmt;
+template <> struct Fmt<T_Q8_0> { static constexpr int QK = 32, BB = 34, PB = 64; };
+template <> struct Fmt<T_Q4_0> { static constexpr int QK = 32, BB = 18, PB = 64; };
+template <> struct Fmt<T_Q4_K> { static constexpr int QK = 256, BB = 144, PB = 8; };
+template <> struct Fmt<T_Q6_K> { static constexpr int QK = 256, BB = 210, PB = 8; };
+
+// ---- device helpers -------------------------------------------------------------------------
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+// Exact IEEE half -> single by bit manipulation (subnormals normalised, Inf/NaN payload kept),
+// the definition the reference's fp16ToFloat follows (runtime/src/dequant.cpp:222-248).
+__host__ __device__ inline float f16_bits_to_f32(uint32_t h) {
+  uint32_t sign = (h & 0x8000u) << 16;
+  uint32_t e = (h >> 10) & 0x1Fu;
+  uint32_t m = h & 0x3FFu;
+  uint32_t bits;
+  if (e == 0) {
+    if (m == 0) {
+      bits = sign;
+    } else {
+      uint32_t fe = 113;
+      while (!(m & 0x400u)) {
+        m <<= 1;
+        fe--;
+      }
+      bits = sign | (fe << 23) | ((m & 0x3FFu) << 13);
+    }
+  } else if (e == 31) {
+    bits = sign | 0x7F800000u | (m << 13);
+  } else {
+    bits = sign | ((e + 112u) << 23) | (m << 13);
+  }
+  return __builtin_bit_cast(float, bits);
+}
+
+// Hardware half -> single for finite values (exact, subnormals included).
+__device__ inline float f16lo(uint32_t w) {
+  return (float)__builtin_bit_cast(half2_t, w).x;
+}
+__device__ inline float f16hi(uint32_t w) {
+  return (float)__builtin_bit_cast(half2_t, w).y;
+}
+
+// ((hi:lo) >> 8*s)[31:0] for s in 0..3: realigns a byte stream read as aligned dwords.
+__device__ inline uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32_t s) {
+  return __builtin_amdgcn_alignbyte(hi, lo, s);
+}
+
+// SplitMix64 finaliser (Steele, Lea, Flood 2014): a counter-based 64-bit hash for seeded data.
+__host__ __device__ inline uint64_t splitmix64(uint64_t z) {
+  z += 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+}  // namespace qvx

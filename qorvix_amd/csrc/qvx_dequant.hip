@@ -1,0 +1,174 @@
+// qvx_dequant.hip -- GGUF block dequantisation to fp32 on gfx950, bit-exact with the reference.
+//
+// One thread per output element: each thread decodes its element from its block's bytes (block
+// headers are re-read by neighbouring threads and served from L1), so the fp32 stores of a wave
+// are one contiguous 256-byte run.  Every formula is the public ggml block definition as the
+// reference states it in runtime/src/dequant.cpp:38-210; the products are exact in fp32, so the
+// single rounding (Q4_K / Q5_K subtract, Q4_1 / Q5_1 add) gives the same value in any order.
+#include "qvx_common.hpp"
+
+namespace qvx {
+
+__device__ inline uint32_t ld16(const uint8_t* p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8); }
+
+__device__ inline void k4_scale_min(int j, const uint8_t* q, uint32_t& sc, uint32_t& m) {
+  if (j < 4) {
+    sc = q[j] & 63;
+    m = q[j + 4] & 63;
+  } else {
+    sc = (q[j + 4] & 15) | ((q[j - 4] >> 6) << 4);
+    m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+  }
+}
+
+template <uint32_t T>
+__device__ inline float deq_elem(const uint8_t* b, int e);
+
+template <> __device__ inline float deq_elem<T_Q8_0>(const uint8_t* b, int e) {
+  return f16_bits_to_f32(ld16(b)) * (float)(int8_t)b[2 + e];
+}
+template <> __device__ inline float deq_elem<T_Q8_1>(const uint8_t* b, int e) {
+  return f16_bits_to_f32(ld16(b)) * (float)(int8_t)b[4 + e];
+}
+template <> __device__ inline float deq_elem<T_Q4_0>(const uint8_t* b, int e) {
+  const int q = e < 16 ? (b[2 + e] & 15) : (b[2 + e - 16] >> 4);
+  return (float)(q - 8) * f16_bits_to_f32(ld16(b));
+}
+template <> __device__ inline float deq_elem<T_Q4_1>(const uint8_t* b, int e) {
+  const int q = e < 16 ? (b[4 + e] & 15) : (b[4 + e - 16] >> 4);
+  return (float)q * f16_bits_to_f32(ld16(b)) + f16_bits_to_f32(ld16(b + 2));
+}
+template <> __device__ inline float deq_elem<T_Q5_0>(const uint8_t* b, int e) {
+  const uint32_t qh = b[2] | (b[3] << 8) | (b[4] << 16) | ((uint32_t)b[5] << 24);
+  const int lo = e < 16 ? (b[6 + e] & 15) : (b[6 + e - 16] >> 4);
+  const int q = lo | (int)(((qh >> e) & 1u) << 4);
+  return (float)(q - 16) * f16_bits_to_f32(ld16(b));
+}
+template <> __device__ inline float deq_elem<T_Q5_1>(const uint8_t* b, int e) {
+  const uint32_t qh = b[4] | (b[5] << 8) | (b[6] << 16) | ((uint32_t)b[7] << 24);
+  const int lo = e < 16 ? (b[8 + e] & 15) : (b[8 + e - 16] >> 4);
+  const int q = lo | (int)(((qh >> e) & 1u) << 4);
+  return (float)q * f16_bits_to_f32(ld16(b)) + f16_bits_to_f32(ld16(b + 2));
+}
+template <> __device__ inline float deq_elem<T_Q4_K>(const uint8_t* b, int e) {
+  const int c = e >> 6, l = e & 63, hi = l >> 5;
+  const uint8_t byte = b[16 + 32 * c + (l & 31)];
+  const int nib = hi ? (byte >> 4) : (byte & 15);
+  uint32_t sc, m;
+  k4_scale_min(2 * c + hi, b + 4, sc, m);
+  const float ds = f16_bits_to_f32(ld16(b)) * (float)sc;
+  const float dm = f16_bits_to_f32(ld16(b + 2)) * (float)m;
+  return ds * (float)nib - dm;
+}
+template <> __device__ inline float deq_elem<T_Q5_K>(const uint8_t* b, int e) {
+  const int c = e >> 6, l = e & 63, hi = l >> 5;
+  const uint8_t byte = b[48 + 32 * c + (l & 31)];
+  int q = hi ? (byte >> 4) : (byte & 15);
+  if (b[16 + (l & 31)] & (1u << (2 * c + hi))) q += 16;
+  uint32_t sc, m;
+  k4_scale_min(2 * c + hi, b + 4, sc, m);
+  const float ds = f16_bits_to_f32(ld16(b)) * (float)sc;
+  const float dm = f16_bits_to_f32(ld16(b + 2)) * (float)m;
+  return ds * (float)q - dm;
+}
+template <> __device__ inline float deq_elem<T_Q6_K>(const uint8_t* b, int e) {
+  const int h = e >> 7, p = e & 127, quarter = p >> 5, l = p & 31;
+  const uint8_t* ql = b + 64 * h;
+  const uint8_t* qh = b + 128 + 32 * h;
+  const int8_t* sc = (const int8_t*)(b + 192 + 8 * h);
+  const uint8_t lob = (quarter & 1) ? ql[l + 32] : ql[l];
+  const int nib = (quarter & 2) ? (lob >> 4) : (lob & 15);
+  const int q = nib | (((qh[l] >> (2 * quarter)) & 3) << 4);
+  const float d = f16_bits_to_f32(ld16(b + 208));
+  return d * (float)sc[(l >> 4) + 2 * quarter] * (float)(q - 32);
+}
+template <> __device__ inline float deq_elem<T_F16>(const uint8_t* b, int e) {
+  return f16_bits_to_f32(ld16(b + 2 * e));
+}
+template <> __device__ inline float deq_elem<T_BF16>(const uint8_t* b, int e) {
+  return __builtin_bit_cast(float, ld16(b + 2 * e) << 16);
+}
+
+// dst[i] = dequant(src)[i] for i < n; QK / BB are the type's block geometry.
+template <uint32_t T, int QK, int BB>
+__global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ src, float* __restrict__ dst,
+                                                 size_t n) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const size_t blk = i / QK;
+  const int e = (int)(i - blk * QK);
+  dst[i] = deq_elem<T>(src + blk * BB, e);
+}
+
+__global__ __launch_bounds__(256) void k_copy_f32(const uint32_t* __restrict__ src, uint32_t* __restrict__ dst,
+                                                  size_t n) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) dst[i] = src[i];
+}
+
+// Host launcher: returns false for a type outside the dequantisable set.
+bool launch_dequant(uint32_t t, const void* src, float* dst, size_t n, hipStream_t s) {
+  const size_t grid = (n + 255) / 256;
+  if (n == 0) return true;
+  const auto* b = static_cast<const uint8_t*>(src);
+  switch (t) {
+    case T_F32: k_copy_f32<<<grid, 256, 0, s>>>((const uint32_t*)src, (uint32_t*)dst, n); return true;
+    case T_F16: k_dequant<T_F16, 1, 0><<<grid, 256, 0, s>>>(b, dst, n); return true;
+    case T_BF16: k_dequant<T_BF16, 1, 0><<<grid, 256, 0, s>>>(b, dst, n); return true;
+    case T_Q8_0: k_dequant<T_Q8_0, 32, 34><<<grid, 256, 0, s>>>(b, dst, n); return true;
+    case T_Q8_1: k_dequant<T_Q8_1, 32, 36><<<grid, 256, 0, s>>>(b, dst, n); return true;
+    case T_Q4_0: k_dequant<T_Q4_0, 32, 18><<<grid, 256, 0, s>>>(b, dst, n); return true;
+    case T_Q4_1: k_dequant<T_Q4_1, 32, 20><<<grid, 256, 0, s>>>(b, dst, n); return true;
+    case T_Q5_0: k_dequant<T_Q5_0, 32, 22><<<grid, 256, 0, s>>>(b, dst, n); return true;
+    case T_Q5_1: k_dequant<T_Q5_1, 32, 24><<<grid, 256, 0, s>>>(b, dst, n); return true;
+    case T_Q4_K: k_dequant<T_Q4_K, 256, 144><<<grid, 256, 0, s>>>(b, dst, n); return true;
+    case T_Q5_K: k_dequant<T_Q5_K, 256, 176><<<grid, 256, 0, s>>>(b, dst, n); return true;
+    case T_Q6_K: k_dequant<T_Q6_K, 256, 210><<<grid, 256, 0, s>>>(b, dst, n); return true;
+    default: return false;
+  }
+}
+
+// ---- generic GEMV: any alignment, any supported type ---------------------------------------------
+// One wave per (row, vector); lane-strided elements dequantised with deq_elem; used only when a
+// weight's base or row pitch is not 16-byte aligned (the fast kernels in qvx_gemv.hip need both).
+// Bit-identity across n_vec holds here too: each output is the same lane sums and the same tree.
+template <uint32_t T, int QK, int BB>
+__global__ __launch_bounds__(256) void k_gemv_generic(const uint8_t* __restrict__ W, const float* __restrict__ X,
+                                                      float* __restrict__ Y, int rows, int cols, int nvec,
+                                                      size_t row_bytes) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const long task = (long)blockIdx.x * 4 + wave;
+  if (task >= (long)rows * nvec) return;
+  const int v = (int)(task / rows), r = (int)(task - (long)v * rows);
+  const uint8_t* rp = W + (size_t)r * row_bytes;
+  const float* x = X + (size_t)v * cols;
+  float acc = 0.0f;
+  for (int k = lane; k < cols; k += 64) {
+    const int blk = k / QK;
+    float w;
+    if constexpr (T == T_F32)
+      w = ((const float*)rp)[k];
+    else
+      w = deq_elem<T>(rp + (size_t)blk * BB, k - blk * QK);
+    acc = __builtin_fmaf(w, x[k], acc);
+  }
+  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if (lane == 0) Y[(size_t)v * rows + r] = acc;
+}
+
+bool launch_gemv_generic(uint32_t t, const void* w, const float* X, float* Y, int rows, int cols, int nvec,
+                         size_t row_bytes, hipStream_t s) {
+  const long tasks = (long)rows * nvec;
+  const unsigned grid = (unsigned)((tasks + 3) / 4);
+  const auto* b = static_cast<const uint8_t*>(w);
+  switch (t) {
+    case T_F32: k_gemv_generic<T_F32, 1, 4><<<grid, 256, 0, s>>>(b, X, Y, rows, cols, nvec, row_bytes); return true;
+    case T_Q8_0: k_gemv_generic<T_Q8_0, 32, 34><<<grid, 256, 0, s>>>(b, X, Y, rows, cols, nvec, row_bytes); return true;
+    case T_Q4_0: k_gemv_generic<T_Q4_0, 32, 18><<<grid, 256, 0, s>>>(b, X, Y, rows, cols, nvec, row_bytes); return true;
+    case T_Q4_K: k_gemv_generic<T_Q4_K, 256, 144><<<grid, 256, 0, s>>>(b, X, Y, rows, cols, nvec, row_bytes); return true;
+    case T_Q6_K: k_gemv_generic<T_Q6_K, 256, 210><<<grid, 256, 0, s>>>(b, X, Y, rows, cols, nvec, row_bytes); return true;
+    default: return false;
+  }
+}
+
+}  // namespace qvx

@@ -1,0 +1,319 @@
+"""GPU parity tests: the gfx950 kernels through the C ABI against the oracle (oracle/qvx_oracle.c)
+and the reference's own outputs (tests/golden).
+
+Bars: dequantisation bit-exact; GEMV max|y-ref|/max|ref| <= 1e-3 against the
+fp64 sum of exact dequant values (fp32 accumulation); GEMM <= 2e-2 (16-bit MFMA path).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+import qorvix_amd as qvx
+from conftest import golden, load_npz, max_rel
+
+pytestmark = pytest.mark.gpu
+
+GEMV_TOL = 1e-3
+GEMM_TOL = 2e-2
+BLOCK = {qvx.Q4_0: (32, 18), qvx.Q4_1: (32, 20), qvx.Q5_0: (32, 22), qvx.Q5_1: (32, 24), qvx.Q8_0: (32, 34),
+         qvx.Q8_1: (32, 36), qvx.Q4_K: (256, 144), qvx.Q5_K: (256, 176), qvx.Q6_K: (256, 210),
+         qvx.F16: (1, 2), qvx.BF16: (1, 2), qvx.F32: (1, 4)}
+HALF_OFFS = {qvx.Q4_0: [0], qvx.Q4_1: [0, 2], qvx.Q5_0: [0], qvx.Q5_1: [0, 2], qvx.Q8_0: [0], qvx.Q8_1: [0, 2],
+             qvx.Q4_K: [0, 2], qvx.Q5_K: [0, 2], qvx.Q6_K: [208]}
+GEMV_TYPES = [qvx.Q8_0, qvx.Q4_0, qvx.Q4_K, qvx.Q6_K]
+
+
+def f32bits(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+def random_weight(t, rows, cols, rng, scale=0.01):
+    bs, bb = BLOCK[t]
+    nblk = rows * cols // bs
+    if bs == 1:
+        if t == qvx.F32:
+            return rng.standard_normal(rows * cols).astype(np.float32).view(np.uint8)
+        if t == qvx.F16:
+            return rng.standard_normal(rows * cols).astype(np.float16).view(np.uint8)
+        return (rng.standard_normal(rows * cols).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16).view(np.uint8)
+    w = rng.integers(0, 256, size=(nblk, bb), dtype=np.uint8)
+    for o in HALF_OFFS[t]:
+        hv = (np.abs(rng.standard_normal(nblk)) * scale + 1e-4).astype(np.float16).view(np.uint16)
+        w[:, o] = hv & 0xFF
+        w[:, o + 1] = hv >> 8
+    return w.reshape(-1)
+
+
+def dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def run_gemv(torch, w_np, t, X_np, rows, cols, offset=0):
+    """qvx_qmatmul_n on device copies; offset shifts the weight base (alignment cases)."""
+    nvec = X_np.shape[0]
+    buf = torch.zeros(w_np.size + 64, dtype=torch.uint8, device="cuda")
+    buf[offset:offset + w_np.size] = dev(torch, w_np)
+    X = dev(torch, X_np.astype(np.float32))
+    out = torch.full((nvec, rows), float("nan"), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    if nvec == 1:
+        rc = qvx.qmatmul(out.data_ptr(), buf.data_ptr() + offset, t, X.data_ptr(), rows, cols, stream)
+    else:
+        rc = qvx.qmatmul_n(out.data_ptr(), buf.data_ptr() + offset, t, X.data_ptr(), nvec, rows, cols, stream)
+    assert rc == qvx.OK, qvx.strerror(rc)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+# ---- dequantisation: bit-exact --------------------------------------------------------------------
+
+@pytest.mark.parametrize("t", sorted(BLOCK))
+def test_dequant_bit_exact(cuda, t):
+    rng = np.random.default_rng(40 + t)
+    bs, bb = BLOCK[t]
+    rows, cols = 33, (1024 if bs > 1 else 1000)
+    w = random_weight(t, rows, cols, rng)
+    n = rows * cols
+    got = qvx.dequantize_t(dev(cuda, w), t, n)
+    cuda.cuda.synchronize()
+    want = oracle.dequantize(t, w, n)
+    np.testing.assert_array_equal(f32bits(got.cpu().numpy()), f32bits(want))
+
+
+def test_dequant_fp16_scale_edge_values(cuda):
+    """Scales at fp16 extremes: subnormal, smallest normal, max, negative, zero; quants at 0/15/63."""
+    t = qvx.Q4_K
+    specials = [0x0001, 0x03FF, 0x0400, 0x7BFF, 0x8001, 0xFBFF, 0x0000, 0x8000, 0x3C00]
+    rng = np.random.default_rng(5)
+    blocks = []
+    for d in specials:
+        for dm in specials:
+            b = rng.integers(0, 256, 144, dtype=np.uint8)
+            b[0], b[1], b[2], b[3] = d & 0xFF, d >> 8, dm & 0xFF, dm >> 8
+            blocks.append(b)
+    w = np.concatenate(blocks)
+    n = len(blocks) * 256
+    got = qvx.dequantize_t(dev(cuda, w), t, n).cpu().numpy()
+    np.testing.assert_array_equal(f32bits(got), f32bits(oracle.dequantize(t, w, n)))
+    # Q6_K / Q8_0 with the same scale set and extreme quants
+    for t, off, bb in ((qvx.Q6_K, 208, 210), (qvx.Q8_0, 0, 34), (qvx.Q4_0, 0, 18)):
+        blocks = []
+        for d in specials:
+            for fill in (0x00, 0xFF, 0x80, 0x7F):
+                b = np.full(bb, fill, np.uint8)
+                b[off], b[off + 1] = d & 0xFF, d >> 8
+                blocks.append(b)
+        w = np.concatenate(blocks)
+        n = len(blocks) * BLOCK[t][0]
+        got = qvx.dequantize_t(dev(cuda, w), t, n).cpu().numpy()
+        np.testing.assert_array_equal(f32bits(got), f32bits(oracle.dequantize(t, w, n)))
+
+
+@pytest.mark.parametrize("path", golden("kat_dequant_*.npz"))
+def test_golden_dequant(cuda, path):
+    d = load_npz(path)
+    t, n = int(d["type"]), int(d["n"])
+    got = qvx.dequantize_t(dev(cuda, d["w"]), t, n).cpu().numpy()
+    np.testing.assert_array_equal(f32bits(got), f32bits(d["expected"]))
+
+
+def test_dequant_row(cuda):
+    rng = np.random.default_rng(9)
+    for t in GEMV_TYPES:
+        rows, cols = 7, 512
+        w = random_weight(t, rows, cols, rng)
+        W = dev(cuda, w)
+        for row in (0, 3, 6):
+            out = cuda.zeros(cols, dtype=cuda.float32, device="cuda")
+            rc = qvx.dequant_row(W.data_ptr(), t, cols, row, out.data_ptr(), cuda.cuda.current_stream().cuda_stream)
+            assert rc == qvx.OK
+            cuda.cuda.synchronize()
+            np.testing.assert_array_equal(f32bits(out.cpu().numpy()), f32bits(oracle.dequant_row(w, t, cols, row)))
+
+
+# ---- GEMV ----------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("path", golden("kat_qmatmul_*.npz") + golden("kat_selftest_*.npz") + golden("rand_*.npz"))
+def test_golden_gemv(cuda, path):
+    d = load_npz(path)
+    t, rows, cols, X = int(d["type"]), int(d["rows"]), int(d["cols"]), d["X"]
+    got = run_gemv(cuda, d["w"], t, X, rows, cols)
+    ref = oracle.matmul_f64(d["w"], t, X, X.shape[0], rows, cols)
+    assert max_rel(got, ref) <= GEMV_TOL
+    assert max_rel(got, d["expected"].reshape(got.shape)) <= GEMV_TOL  # the reference's own output
+    if "f64ref" in d:
+        assert max_rel(got[0], d["f64ref"]) <= GEMV_TOL
+
+
+SHAPES = [
+    (1, 256), (3, 512), (17, 2048), (64, 2304), (100, 4096), (257, 4352),  # ragged rows, partial panels
+    (4096, 4096), (1024, 14336),
+]
+
+
+@pytest.mark.parametrize("t", GEMV_TYPES)
+@pytest.mark.parametrize("rows,cols", SHAPES)
+def test_gemv_m1_parity(cuda, t, rows, cols):
+    bs, _ = BLOCK[t]
+    if cols % bs:
+        pytest.skip("shape not a whole number of blocks")
+    rng = np.random.default_rng(rows * 7 + cols + t)
+    w = random_weight(t, rows, cols, rng)
+    x = rng.standard_normal((1, cols)).astype(np.float32)
+    got = run_gemv(cuda, w, t, x, rows, cols)
+    ref = oracle.matmul_f64(w, t, x, 1, rows, cols)
+    assert max_rel(got, ref) <= GEMV_TOL
+
+
+@pytest.mark.parametrize("t", GEMV_TYPES)
+@pytest.mark.parametrize("nvec", [2, 3, 4, 7, 8, 16, 17, 33])
+def test_gemv_batched_parity_and_bit_identity(cuda, t, nvec):
+    rng = np.random.default_rng(100 + nvec + t)
+    rows, cols = 300, 4096
+    w = random_weight(t, rows, cols, rng)
+    X = rng.standard_normal((nvec, cols)).astype(np.float32)
+    got = run_gemv(cuda, w, t, X, rows, cols)
+    assert max_rel(got, oracle.matmul_f64(w, t, X, nvec, rows, cols)) <= GEMV_TOL
+    # each vector bit-identical to the single-vector GEMV (qmatmul.hpp:31-32)
+    for v in range(nvec):
+        single = run_gemv(cuda, w, t, X[v:v + 1], rows, cols)
+        np.testing.assert_array_equal(f32bits(got[v]), f32bits(single[0]))
+
+
+@pytest.mark.parametrize("t", GEMV_TYPES)
+def test_gemv_unaligned_weight_uses_generic_path(cuda, t):
+    rng = np.random.default_rng(77 + t)
+    bs, _ = BLOCK[t]
+    rows, cols = 45, 5 * bs  # row pitch not a multiple of 16 for the 32-blocks
+    w = random_weight(t, rows, cols, rng)
+    X = rng.standard_normal((3, cols)).astype(np.float32)
+    ref = oracle.matmul_f64(w, t, X, 3, rows, cols)
+    for off in (0, 2, 6):
+        got = run_gemv(cuda, w, t, X, rows, cols, offset=off)
+        assert max_rel(got, ref) <= GEMV_TOL
+
+
+def test_gemv_f32_weight(cuda):
+    rng = np.random.default_rng(4)
+    rows, cols = 33, 96
+    w = rng.standard_normal(rows * cols).astype(np.float32)
+    X = rng.standard_normal((2, cols)).astype(np.float32)
+    got = run_gemv(cuda, w.view(np.uint8), qvx.F32, X, rows, cols)
+    assert max_rel(got, X.astype(np.float64) @ w.reshape(rows, cols).astype(np.float64).T) <= 1e-5
+
+
+def test_gemv_zero_cols_writes_zeros(cuda):
+    out = cuda.full((5,), 3.0, dtype=cuda.float32, device="cuda")
+    rc = qvx.qmatmul(out.data_ptr(), 0, qvx.Q4_K, 0, 5, 0, cuda.cuda.current_stream().cuda_stream)
+    assert rc == qvx.OK
+    cuda.cuda.synchronize()
+    assert np.all(out.cpu().numpy() == 0)
+
+
+@pytest.mark.parametrize("t", GEMV_TYPES)
+def test_gemv_linearity_full_size(cuda, t):
+    """Size-independent property at a BASELINE shape: W(a x + b y) = a Wx + b Wy (fp32 tolerance)."""
+    rng = np.random.default_rng(900 + t)
+    rows, cols = 14336, 4096
+    w = random_weight(t, rows, cols, rng)
+    x = rng.standard_normal(cols).astype(np.float32)
+    y = rng.standard_normal(cols).astype(np.float32)
+    X = np.stack([x, y, (2 * x - 3 * y).astype(np.float32)])
+    out = run_gemv(cuda, w, t, X, rows, cols)
+    assert max_rel(out[2], 2 * out[0].astype(np.float64) - 3 * out[1]) <= 2 * GEMV_TOL
+    assert max_rel(out, oracle.matmul_f64(w, t, X, 3, rows, cols)) <= GEMV_TOL
+
+
+def test_host_pointer_entry_points(cuda):
+    rng = np.random.default_rng(12)
+    lib = qvx.lib()
+    for t in GEMV_TYPES:
+        rows, cols = 40, 1024
+        w = random_weight(t, rows, cols, rng)
+        X = rng.standard_normal((3, cols)).astype(np.float32)
+        out = np.zeros((3, rows), np.float32)
+        assert lib.qvx_qmatmul_n_host(out.ctypes.data, w.ctypes.data, t, X.ctypes.data, 3, rows, cols) == qvx.OK
+        assert max_rel(out, oracle.matmul_f64(w, t, X, 3, rows, cols)) <= GEMV_TOL
+        deq = np.zeros(rows * cols, np.float32)
+        assert lib.qvx_dequantize_host(t, w.ctypes.data, deq.ctypes.data, rows * cols) == qvx.OK
+        np.testing.assert_array_equal(f32bits(deq), f32bits(oracle.dequantize(t, w, rows * cols)))
+        row = np.zeros(cols, np.float32)
+        assert lib.qvx_dequant_row_host(w.ctypes.data, t, cols, 7, row.ctypes.data) == qvx.OK
+        np.testing.assert_array_equal(f32bits(row), f32bits(deq[7 * cols:8 * cols]))
+
+
+# ---- GEMM ----------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("variant", [qvx.GEMM_BF16, qvx.GEMM_F16])
+@pytest.mark.parametrize("M,rows,cols", [(128, 512, 1024), (200, 300, 768), (512, 1024, 4096), (37, 256, 256)])
+def test_gemm_q4k_parity(cuda, variant, M, rows, cols):
+    rng = np.random.default_rng(M + rows + cols + variant)
+    t = qvx.Q4_K
+    w = random_weight(t, rows, cols, rng, scale=0.002)
+    X16 = (rng.standard_normal((M, cols)) * 0.5).astype(np.float16)
+    X = dev(cuda, X16.view(np.uint16))
+    out = qvx.qgemm_t(dev(cuda, w), t, X, rows, cols, variant)
+    cuda.cuda.synchronize()
+    ref = oracle.matmul_f64(w, t, X16.astype(np.float32), M, rows, cols)
+    assert max_rel(out.cpu().numpy(), ref) <= GEMM_TOL
+
+
+def test_gemm_q4k_config4_shape(cuda):
+    """BASELINE config 4 (Q4_K 4096 -> 14336, M = 128) against the fp64 oracle."""
+    rng = np.random.default_rng(2024)
+    t, M, rows, cols = qvx.Q4_K, 128, 14336, 4096
+    W = qvx.empty_weight(t, rows, cols)
+    qvx.fill_synthetic_t(W, t, rows, cols, seed=31, scale_mul=1e-3)
+    X = cuda.empty((M, cols), dtype=cuda.float16, device="cuda")
+    qvx.fill_normal_t(X, seed=32, mul=0.5)
+    for variant in (qvx.GEMM_BF16, qvx.GEMM_F16):
+        out = qvx.qgemm_t(W, t, X, rows, cols, variant)
+        cuda.cuda.synchronize()
+        w = W.cpu().numpy()
+        ref = oracle.matmul_f64(w, t, X.cpu().numpy().astype(np.float32), M, rows, cols)
+        assert max_rel(out.cpu().numpy(), ref) <= GEMM_TOL
+
+
+def test_quantize_act_q8_matches_oracle(cuda):
+    rng = np.random.default_rng(8)
+    M, K = 19, 512
+    X16 = (rng.standard_normal((M, K)) * 0.5).astype(np.float16)
+    X16[3, 64:96] = 0
+    X = dev(cuda, X16.view(np.uint16))
+    q = cuda.empty((M, K), dtype=cuda.int8, device="cuda")
+    s = cuda.empty((M, K // 32), dtype=cuda.float32, device="cuda")
+    qs = cuda.empty((M, K // 32), dtype=cuda.int32, device="cuda")
+    rc = qvx.lib().qvx_quantize_act_q8(X.data_ptr(), M, K, q.data_ptr(), s.data_ptr(), qs.data_ptr(),
+                                       cuda.cuda.current_stream().cuda_stream)
+    assert rc == qvx.OK
+    cuda.cuda.synchronize()
+    oq, os_, oqs = oracle.quantize_q8_act(X16.astype(np.float32))
+    np.testing.assert_array_equal(q.cpu().numpy(), oq)
+    np.testing.assert_array_equal(f32bits(s.cpu().numpy()), f32bits(os_))
+    np.testing.assert_array_equal(qs.cpu().numpy(), oqs)
+
+
+# ---- synthetic data generator ---------------------------------------------------------------------
+
+def test_synthetic_blocks_are_well_formed(cuda):
+    for t, mul in ((qvx.Q8_0, 0.01), (qvx.Q4_0, 0.02), (qvx.Q4_K, 1e-3), (qvx.Q6_K, 1e-3)):
+        rows, cols = 64, 4096
+        W = qvx.empty_weight(t, rows, cols)
+        qvx.fill_synthetic_t(W, t, rows, cols, seed=5, scale_mul=mul)
+        W2 = qvx.empty_weight(t, rows, cols)
+        qvx.fill_synthetic_t(W2, t, rows, cols, seed=5, scale_mul=mul)
+        cuda.cuda.synchronize()
+        a, b = W.cpu().numpy(), W2.cpu().numpy()
+        np.testing.assert_array_equal(a, b)  # deterministic
+        deq = oracle.dequantize(t, a, rows * cols)
+        assert np.all(np.isfinite(deq))
+        bs, bb = BLOCK[t]
+        blk = a.reshape(-1, bb)
+        off = 208 if t == qvx.Q6_K else 0
+        d = blk[:, off:off + 2].copy().view(np.float16).astype(np.float64).ravel()
+        assert np.all(d >= 0) and 0.5 * mul < d.mean() < 1.1 * mul  # E|N(0,1)| = 0.798
+        if t == qvx.Q8_0:
+            q = blk[:, 2:].view(np.int8)
+            assert q.min() == -127 and q.max() == 127
