@@ -38,7 +38,7 @@ def algorithmic_bytes(rows, cols, m, wbytes):
     return wbytes + 4 * m * cols + 4 * m * rows
 
 
-def cpu_baseline(w_host, x_host, rows, cols, budget_s=10.0):
+def cpu_baseline(w_host, x_host, rows, cols, budget_s=5.0):
     """The reference's CPU qmatmul (oracle/_ref, else the C restatement) on this host's cores."""
     import numpy as np
     import oracle
@@ -57,7 +57,7 @@ def cpu_baseline(w_host, x_host, rows, cols, budget_s=10.0):
     fn(out, wp, 12, x_host, rows, cols)  # warm-up
     times = []
     t_end = time.perf_counter() + budget_s
-    while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 200):
+    while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 2000):
         t0 = time.perf_counter()
         fn(out, wp, 12, x_host, rows, cols)
         times.append(time.perf_counter() - t0)
@@ -83,6 +83,9 @@ def main():
     ap.add_argument("--copies", type=int, default=40, help="distinct weight copies cycled per step")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--gemm-steps", type=int, default=20)
+    ap.add_argument("--gemv-only", action="store_true", help="only the GEMV leg (for profiler passes)")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MiB",
+                    help="also run one plain device copy of this many MiB (PMC byte-counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the qvx engine has no multi-GPU "
@@ -153,10 +156,21 @@ def main():
     pair_med = statistics.median(pair_us)
     log(f"[bench] GEMV per-launch event pairs: median {pair_med:.2f} us, min {pair_us[0]:.2f} us")
 
+    if args.calibrate_copy:
+        n = args.calibrate_copy << 20
+        a = torch.empty(n, dtype=torch.uint8, device=dev)
+        b = torch.empty(n, dtype=torch.uint8, device=dev)
+        a.fill_(1)
+        torch.cuda.synchronize()
+        b.copy_(a)
+        torch.cuda.synchronize()
+        log(f"[bench] calibration copy of {args.calibrate_copy} MiB done")
+        del a, b
+
     # ---- prefill GEMM ----------------------------------------------------
     gemm = {}
     try:
-        for M in (2048, 512, 128):
+        for M in ((2048, 512, 128) if not args.gemv_only else ()):
             X = torch.empty((M, COLS), dtype=torch.float16, device=dev)
             qvx.fill_normal_t(X, seed=11, mul=0.5)
             Y = torch.empty((M, ROWS), dtype=torch.float32, device=dev)
@@ -187,7 +201,7 @@ def main():
 
     # ---- CPU baseline (reference CPU operator on this host) ------------------------------------
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and not args.gemv_only:
         w_host = copies[0].cpu().numpy()
         x_host = x.cpu().numpy()
         cpu = cpu_baseline(w_host, x_host, ROWS, COLS)
@@ -221,7 +235,7 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": "k_gemv<12,1,RL>",
+            "kernel": "qvx::k_gemv<12, 1, RL>",
             "per_launch_event_pair_us": round(pair_med, 3),
         },
         "gemm": {

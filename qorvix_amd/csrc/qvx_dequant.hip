@@ -82,6 +82,7 @@ template <> __device__ inline float deq_elem<T_Q6_K>(const uint8_t* b, int e) {
   const float d = f16_bits_to_f32(ld16(b + 208));
   return d * (float)sc[(l >> 4) + 2 * quarter] * (float)(q - 32);
 }
+// F16 / BF16 have one element per 2-byte block, so e is always 0 here.
 template <> __device__ inline float deq_elem<T_F16>(const uint8_t* b, int e) {
   return f16_bits_to_f32(ld16(b + 2 * e));
 }
@@ -113,8 +114,8 @@ bool launch_dequant(uint32_t t, const void* src, float* dst, size_t n, hipStream
   const auto* b = static_cast<const uint8_t*>(src);
   switch (t) {
     case T_F32: k_copy_f32<<<grid, 256, 0, s>>>((const uint32_t*)src, (uint32_t*)dst, n); return true;
-    case T_F16: k_dequant<T_F16, 1, 0><<<grid, 256, 0, s>>>(b, dst, n); return true;
-    case T_BF16: k_dequant<T_BF16, 1, 0><<<grid, 256, 0, s>>>(b, dst, n); return true;
+    case T_F16: k_dequant<T_F16, 1, 2><<<grid, 256, 0, s>>>(b, dst, n); return true;
+    case T_BF16: k_dequant<T_BF16, 1, 2><<<grid, 256, 0, s>>>(b, dst, n); return true;
     case T_Q8_0: k_dequant<T_Q8_0, 32, 34><<<grid, 256, 0, s>>>(b, dst, n); return true;
     case T_Q8_1: k_dequant<T_Q8_1, 32, 36><<<grid, 256, 0, s>>>(b, dst, n); return true;
     case T_Q4_0: k_dequant<T_Q4_0, 32, 18><<<grid, 256, 0, s>>>(b, dst, n); return true;
