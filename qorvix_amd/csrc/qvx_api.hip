@@ -71,13 +71,14 @@ int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int
   if (!w || !X) return QVX_E_NULL;
   const size_t row_bytes = (size_t)(cols / (int)ti->block) * ti->bytes;
   const bool fast = type != T_F32 && aligned16(w) && aligned16(X) && row_bytes % 16 == 0;
+  // The fast kernel takes any number of vectors (a few per launch, each vector's arithmetic the same
+  // in every launch, so batches stay bit-identical to single vectors); shapes it does not cover go
+  // to the generic kernel.
+  if (fast && launch_gemv_fast(type, w, X, out, nvec, rows, cols, row_bytes, s)) return hip_status();
   for (int v0 = 0; v0 < nvec; v0 += 16) {
     const int nv = nvec - v0 < 16 ? nvec - v0 : 16;
-    const float* Xv = X + (size_t)v0 * cols;
-    float* Yv = out + (size_t)v0 * rows;
-    const bool ok = fast ? launch_gemv_fast(type, w, Xv, Yv, nv, rows, cols, row_bytes, s)
-                         : launch_gemv_generic(type, w, Xv, Yv, rows, cols, nv, row_bytes, s);
-    if (!ok) return QVX_E_TYPE;
+    if (!launch_gemv_generic(type, w, X + (size_t)v0 * cols, out + (size_t)v0 * rows, rows, cols, nv, row_bytes, s))
+      return QVX_E_TYPE;
   }
   return hip_status();
 }

@@ -1,37 +1,51 @@
 // qvx_gemv.hip -- decode GEMV (M = 1..16) over raw GGUF blocks on gfx950.
 //
 // out[v, r] = sum_k dequant(W)[r, k] * X[v, k]   (the reference's qmatmul / qmatmulN,
-// runtime/src/qmatmul.cpp:28-115), fp32 activations, fp32 accumulation.
+// runtime/src/qmatmul.cpp:28-115), fp32 activations in, fp32 out.
+//
+// Arithmetic: integer dot products on the quant codes.
+//  * A row of K = cols elements is cut into S "slots" of R runs of 16 elements: R = 4 (64
+//    elements: one 64-element scale group of a Q4_K super-block, or two Q4_0 / Q8_0 blocks) or
+//    R = 2 (Q6_K: two quarter-runs that share a 16-element column range).
+//  * Each workgroup first converts the activations of every slot to 15-bit fixed point,
+//    q = rn(x / amax * 16383) with amax the slot's largest |x| (v_cvt_pknorm_i16_f32), so
+//    x = q * sx + e with sx = amax / 16383 and |e| <= sx / 2 (at most 3.1e-5 of the slot's
+//    largest activation).  q is split as q = 128 qh + ql with qh = q >> 7 in [-128, 127] and
+//    ql = q & 127, both signed bytes, and stored in LDS with the run sums of q.
+//  * Quant codes are unpacked in registers to signed bytes and multiplied with v_dot4_i32_i8
+//    against qh and ql: T = sum(code q) over a run is exact in int32.  High nibbles are taken in
+//    place as 16 (n - 8) (one v_bitop3: (w & 0xF0) ^ 0x80), so sum(n q) = (T + 128 Q) / 16 with
+//    Q = sum(q) over the run.  The block's affine map is applied once per slot:
+//      Q4_K  d*(sc_a Ta + sc_b Tb) - dmin*(m_a Qa + m_b Qb)          (sub-blocks a, b of the group)
+//      Q6_K  d*(sc_a (Ta - 32 Qa) + sc_b (Tb - 32 Qb))
+//      Q4_0  d*sum((n - 8) q)   Q8_0  d*sum(c q)                       (per block)
+//    and each row's partial is scaled by sx once.  The only error beyond fp32 rounding is the
+//    activations' fixed-point step, far inside the 1e-3 max-relative bound of the operator.
 //
 // Work decomposition:
-//  * A row of K = cols elements is cut into S = K/32 "slots" of 32 elements (one Q4_0 / Q8_0
-//    block, or one eighth of a Q4_K / Q6_K super-block).  A workgroup has G groups of S' lanes
-//    (S' = S rounded up to a multiple of 64, or to a power of two when S < 64); lane j of a group
-//    owns slot j for the whole kernel, so its activation values (32 floats per vector) and their
-//    run sums are loaded and formed once and reused for every row it touches.
-//  * Each lane walks RL rows (group g takes rows g, g+G, ... of the workgroup's G*RL rows).  All
-//    RL rows' quant bytes are requested up front with direct global loads into registers
-//    (16-byte loads where the block layout is 16-byte aligned -- Q4_K -- and dword-aligned
-//    dwordx4 + tail loads realigned with v_alignbyte where it is not), then consumed in issue
-//    order, so each row is computed as soon as its bytes land while later rows are in flight.
-//  * Quant fields are unpacked in registers into packed fp16 pairs whose bit patterns are the
-//    small integers themselves (fp16 subnormals q * 2^-24, exact); v_fma_mix_f32 multiplies them
-//    straight into fp32 sums with the fp32 activations.  Per run of 16 the integer sums are
-//    rescaled once:  Q4_K: d*sc*sum(n x) - dmin*m*sum(x);  Q6_K: d*sc*(sum(q x) - 32 sum(x));
-//    Q4_0: d*(sum(n x) - 8 sum(x));  Q8_0: d*(sum((q+128) x) - 128 sum(x)).  Every product is
-//    exact, so only fp32 summation error enters (checked at 1e-3 max-relative).
-//  * Each output's S' lane partials are summed by a fixed xor butterfly inside each wave and, for
-//    groups wider than a wave, by one thread over the wave sums in wave order.  None of this
-//    depends on NV, so qvx_qmatmul_n is bit-identical to qvx_qmatmul per vector, the reference's
-//    promise for qmatmulN (runtime/include/qorvix/runtime/qmatmul.hpp:31-32).
+//  * A workgroup has G groups of S' lanes (S' = S rounded up to a multiple of 64, or to a power of
+//    two >= 8 when S < 64); lane j of a group owns slot j for the whole kernel and keeps its
+//    fixed-point activations in registers.  Workgroup b owns the contiguous rows
+//    [rows*b/nwg, rows*(b+1)/nwg); group g takes rows g, g+G, ... of them (n <= RMAX rows).
+//  * A lane requests its activations first and then the quant bytes of all its rows, with no
+//    branches between the loads, so the conversion waits only for the activations and each row's
+//    arithmetic only for that row's bytes while later rows are still arriving.
+//  * Each output's S' lane partials are summed with DPP / permlane swaps inside each wave (only
+//    commutative adds, so every lane holds the same bits) and, for groups wider than a wave, by
+//    one thread over the wave sums in wave order.  No step depends on NV, so qvx_qmatmul_n is
+//    bit-identical to qvx_qmatmul per vector, the reference's promise for qmatmulN
+//    (runtime/include/qorvix/runtime/qmatmul.hpp:31-32).
 //
 // Requirements checked by the launcher: W and X 16-byte aligned, row pitch a multiple of 16 bytes,
-// S' <= 1024.  Other shapes go to the generic kernel in qvx_dequant.hip.
+// K a whole number of slots, S' <= 1024.  Other shapes go to the generic kernel in qvx_dequant.hip.
+#include <algorithm>
+
 #include "qvx_common.hpp"
 
 namespace qvx {
 
 typedef uint32_t u32x4a4_t __attribute__((ext_vector_type(4), aligned(4)));  // dword-aligned 16 bytes
+typedef short short2_t __attribute__((ext_vector_type(2)));
 
 __device__ inline uint4 ldg16(const uint8_t* p) {  // p 16-byte aligned
   return *reinterpret_cast<const uint4*>(p);
@@ -50,88 +64,104 @@ __device__ inline void realign16(const u32x4a4_t& w, uint32_t e, uint32_t s, uin
   q[3] = align_bytes(e, w.w, s);
 }
 
-// ---- a slot: 2 runs x 16 elements as packed fp16 integer pairs + per-run scales --------------
-struct Slot {
-  uint32_t a[8], b[8];  // pairs: a[2j] = elems (4j, 4j+2), a[2j+1] = elems (4j+1, 4j+3) of run A
-  float ka, kb;         // factors turning the raw fp16-subnormal dot of run A / B into sum(q x)
-  float ca, cb;         // coefficients of sum(x) over run A / B (offsets and minimums, scaled)
-  float d;              // scale of the quant sums
+// High nibbles of four bytes in place, as signed bytes 16 (n - 8).
+__device__ inline uint32_t hi_codes(uint32_t w) { return (w & 0xF0F0F0F0u) ^ 0x80808080u; }
+
+// ---- activations of one slot in 15-bit fixed point --------------------------------------------
+template <int R>
+struct XQ {
+  uint32_t h[4 * R], l[4 * R];  // qh / ql as signed bytes, 4 consecutive elements per dword; run r at [4r, 4r+4)
+  int q[R];                     // sum of q over each run
+  float sx;                     // x = q * sx (NaN when the slot holds a non-finite activation)
 };
-
-// Low nibbles of 4 bytes as two packed-half dwords (fp16 subnormals n * 2^-24).
-__device__ inline void nib_lo(uint32_t w, uint32_t& p02, uint32_t& p13) {
-  p02 = w & 0x000F000Fu;
-  p13 = (w >> 8) & 0x000F000Fu;
-}
-// High nibbles left in place (16 * n as fp16 subnormal): the caller scales by 2^20.
-__device__ inline void nib_hi(uint32_t w, uint32_t& p02, uint32_t& p13) {
-  p02 = w & 0x00F000F0u;
-  p13 = (w >> 8) & 0x00F000F0u;
+// LDS words per (vector, slot): h[4R], l[4R], q[R], sx, padded to a multiple of 4 words
+template <int R>
+constexpr int xq_words() {
+  return (9 * R + 1 + 3) & ~3;
 }
 
-constexpr float k2p24 = 16777216.0f;  // 2^24
-constexpr float k2p20 = 1048576.0f;   // 2^20
+// sum(code * q) over N dwords of signed byte codes (4N elements).
+template <int N>
+__device__ inline int dotq(const uint32_t* c, const uint32_t* h, const uint32_t* l) {
+  int s = 0;
+#pragma unroll
+  for (int j = 0; j < N; ++j) s = __builtin_amdgcn_sdot4((int)c[j], (int)h[j], s, false);
+  s = (int)((uint32_t)s << 7);
+#pragma unroll
+  for (int j = 0; j < N; ++j) s = __builtin_amdgcn_sdot4((int)c[j], (int)l[j], s, false);
+  return s;
+}
 
-// Per-type lane logic: Raw = the registers one row's slot needs; load() issues the global loads
-// (rows are 16-byte aligned; offsets below are row-relative); unpack() turns Raw into a Slot;
-// xoff() is the slot's run-A offset within the row (run B = run A + kXB).
+// Per-type lane logic.  kR runs of 16 elements per slot; xoff(sig, r) = element offset of run r of
+// slot sig within the row; Raw = the registers one row's slot needs; load() issues its global
+// loads (rows are 16-byte aligned; offsets are row-relative); row() returns the slot's partial
+// dot product with the activations, in units of sx.
 template <uint32_t T> struct Lane;
 
-// Q4_K: slot = super-block b = sig/8, 16-byte quant chunk k = sig%8 of its 128 qs bytes.  Chunk k
-// holds bytes l = 16(k%2)..+15 of 64-element group c = k/2: low nibbles are sub-block 2c
-// (elements 64c + l), high nibbles sub-block 2c+1 (elements 64c + 32 + l).
+// Q4_K: slot sig = scale group c = sig%4 (64 elements) of super-block b = sig/4: bytes 32c..32c+31
+// of the 128 qs bytes; low nibbles are sub-block 2c (elements 64c + l, l = 0..31), high nibbles
+// sub-block 2c+1 (elements 64c + 32 + l).  Runs: 0, 1 = sub-block 2c, 2, 3 = sub-block 2c+1.
 template <> struct Lane<T_Q4_K> {
-  static constexpr int kSPB = 8, kXB = 32;
+  static constexpr int kR = 4;
+  static constexpr int kSlotElems = 64;
   struct Raw {
-    uint4 q, h;
+    uint4 h, q0, q1;
   };
-  static __device__ inline int xoff(int sig) { return 256 * (sig >> 3) + 64 * ((sig & 7) >> 1) + 16 * (sig & 1); }
+  static __device__ inline int xoff(int sig, int run) { return 256 * (sig >> 2) + 64 * (sig & 3) + 16 * run; }
   static __device__ inline void load(const uint8_t* row, int sig, Raw& r) {
-    const uint8_t* blk = row + 144 * (sig >> 3);
+    const uint8_t* blk = row + 144 * (sig >> 2);
     r.h = ldg16(blk);
-    r.q = ldg16(blk + 16 + 16 * (sig & 7));
+    r.q0 = ldg16(blk + 16 + 32 * (sig & 3));
+    r.q1 = ldg16(blk + 32 + 32 * (sig & 3));
   }
-  static __device__ inline void unpack(const Raw& r, int sig, Slot& o) {
-    const uint32_t qq[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+  static __device__ inline float row(const Raw& r, int sig, const XQ<4>& x) {
+    const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+    uint32_t lo[8], hi[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      nib_lo(qq[j], o.a[2 * j], o.a[2 * j + 1]);
-      nib_hi(qq[j], o.b[2 * j], o.b[2 * j + 1]);
+    for (int j = 0; j < 8; ++j) {
+      lo[j] = q[j] & 0x0F0F0F0Fu;
+      hi[j] = hi_codes(q[j]);
     }
-    // 6-bit (scale, min) of sub-blocks 2c, 2c+1 as byte pairs (public K-quant scale packing):
-    // c < 2: sc = s[2c..] & 63, m = s[2c+4..] & 63; c >= 2: low 4 bits from s[2c+4..], high 2 bits
-    // from bits 6-7 of s[2c-4..] (scale) and s[2c..] (min).  Branch-free: c is lane-constant.
-    const int c = (sig & 7) >> 1;
-    const bool hi = c >= 2;
-    const uint32_t sh = 16u * (uint32_t)(c & 1);
-    const uint32_t m1 = hi ? 0x0F0Fu : 0x3F3Fu, m2 = hi ? 0x3030u : 0u;
-    const uint32_t scp = (((hi ? r.h.w : r.h.y) >> sh) & m1) | ((r.h.y >> (sh + 2)) & m2);
-    const uint32_t mp = (((hi ? r.h.w : r.h.z) >> (sh + (hi ? 4u : 0u))) & m1) | ((r.h.z >> (sh + 2)) & m2);
-    o.ka = (float)(scp & 0xFFu) * k2p24;
-    o.kb = (float)(scp >> 8) * k2p20;
-    const float dmin = f16hi(r.h.x);
-    o.d = f16lo(r.h.x);
-    o.ca = -dmin * (float)(mp & 0xFFu);  // dmin * m is exact in fp32
-    o.cb = -dmin * (float)(mp >> 8);
+    const int qa = x.q[0] + x.q[1], qb = x.q[2] + x.q[3];
+    const int ta = dotq<8>(lo, x.h, x.l);                    // sum n q over sub-block 2c
+    const int tb = dotq<8>(hi, x.h + 8, x.l + 8) + 128 * qb;  // 16 * sum n q over sub-block 2c+1
+    // 6-bit (scale, min) of sub-blocks 2c, 2c+1 (public K-quant scale packing, scale bytes
+    // s[0..11] = h.y, h.z, h.w): c < 2: sc = s[2c..2c+1] & 63, m = s[2c+4..] & 63; c >= 2: low 4
+    // bits from s[2c+4..] (sc: low nibble, m: high nibble), high 2 bits from bits 6-7 of s[2c-4..]
+    // (sc) and s[2c..] (m).  With j = 2(c%2): p1 = [y_j, y_j+1, z_j, z_j+1], p2 = [w_j, w_j+1,
+    // w_j, w_j+1], and the packed result sm = [sc_a, sc_b, m_a, m_b].  Masks are lane-constant.
+    const int c = sig & 3;
+    const uint32_t j = 2u * (uint32_t)(c & 1);
+    const uint32_t p1 = __builtin_amdgcn_perm(r.h.z, r.h.y, j | (j + 1) << 8 | (j + 4) << 16 | (j + 5) << 24);
+    const uint32_t p2 = __builtin_amdgcn_perm(r.h.w, r.h.w, j | (j + 1) << 8 | j << 16 | (j + 1) << 24);
+    const bool up = c >= 2;
+    const uint32_t sm = (p1 & (up ? 0u : 0x3F3F3F3Fu)) | ((p1 >> 2) & (up ? 0x30303030u : 0u)) |
+                        (p2 & (up ? 0x00000F0Fu : 0u)) | ((p2 >> 4) & (up ? 0x0F0F0000u : 0u));
+    const float sca = (float)(sm & 0xFFu), scb = (float)((sm >> 8) & 0xFFu);  // v_cvt_f32_ubyte0..3
+    const float mna = (float)((sm >> 16) & 0xFFu), mnb = (float)(sm >> 24);
+    const float t = __builtin_fmaf((float)tb * 0.0625f, scb, (float)ta * sca);
+    const float u = __builtin_fmaf((float)qb, mnb, (float)qa * mna);
+    return __builtin_fmaf(f16lo(r.h.x), t, -f16hi(r.h.x) * u);
   }
 };
 
 // Q6_K: slot = super-block b = sig/8, u = sig%8 -> half h = u/4, l-group t = (u/2)%2, e = u%2.
-// It covers quarter e (low nibbles of ql[64h + 32e + 16t ..+16]) and quarter e+2 (their high
-// nibbles) with 2-bit high parts from qh[32h + 16t ..+16], bits (2e, 2e+1) and (2e+4, 2e+5);
+// Run 0 is quarter e (low nibbles of ql[64h + 32e + 16t ..+16]), run 1 quarter e+2 (their high
+// nibbles), with 2-bit high parts from qh[32h + 16t ..+16], bits (2e, 2e+1) and (2e+4, 2e+5);
 // scales sc[8h + t + 2e] and sc[8h + t + 2e + 4].  Super-blocks are 2-byte aligned: each 16-byte
 // piece is read as a dword-aligned 20-byte window (never past its super-block) and realigned.
 template <> struct Lane<T_Q6_K> {
-  static constexpr int kSPB = 8, kXB = 64;
+  static constexpr int kR = 2;
+  static constexpr int kSlotElems = 32;
   struct Raw {
     u32x4a4_t l, h;
     uint32_t le, he, s0, s1, dd;
-    uint32_t sh;  // byte misalignment of the pieces (0 or 2)
-    uint32_t ssh; // byte position of the first scale inside s0
+    uint32_t sh;   // byte misalignment of the pieces (0 or 2)
+    uint32_t ssh;  // byte position of the first scale inside s0
   };
-  static __device__ inline int xoff(int sig) {
+  static __device__ inline int xoff(int sig, int run) {
     const int u = sig & 7;
-    return 256 * (sig >> 3) + 128 * (u >> 2) + 32 * (u & 1) + 16 * ((u >> 1) & 1);
+    return 256 * (sig >> 3) + 128 * (u >> 2) + 32 * (u & 1) + 16 * ((u >> 1) & 1) + 64 * run;
   }
   static __device__ inline void load(const uint8_t* row, int sig, Raw& r) {
     const int b = sig >> 3, u = sig & 7, h = u >> 2, t = (u >> 1) & 1, e = u & 1;
@@ -148,248 +178,309 @@ template <> struct Lane<T_Q6_K> {
     r.s1 = ldg4(row + (os & ~3) + 4);
     r.dd = ldg2(row + base + 208);
   }
-  static __device__ inline void unpack(const Raw& r, int sig, Slot& o) {
+  static __device__ inline float row(const Raw& r, int sig, const XQ<2>& x) {
     const uint32_t e = (uint32_t)(sig & 1);
-    uint32_t ql[4], qh[4];
+    uint32_t ql[4], qh[4], a[4], b[4];
     realign16(r.l, r.le, r.sh, ql);
     realign16(r.h, r.he, r.sh, qh);
     const uint32_t shl = 4u - 2u * e, shr = 2u * e;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t ha = qh[j] << shl;  // bits (2e, 2e+1) of each byte -> bits 4..5
-      const uint32_t hb = qh[j] >> shr;  // bits (2e+4, 2e+5) of each byte -> bits 4..5
-      o.a[2 * j] = (ql[j] & 0x000F000Fu) | (ha & 0x00300030u);
-      o.a[2 * j + 1] = ((ql[j] >> 8) & 0x000F000Fu) | ((ha >> 8) & 0x00300030u);
-      o.b[2 * j] = ((ql[j] >> 4) & 0x000F000Fu) | (hb & 0x00300030u);
-      o.b[2 * j + 1] = ((ql[j] >> 12) & 0x000F000Fu) | ((hb >> 8) & 0x00300030u);
+    for (int j = 0; j < 4; ++j) {  // 6-bit codes 0..63
+      a[j] = (ql[j] & 0x0F0F0F0Fu) | ((qh[j] << shl) & 0x30303030u);         // bits (2e, 2e+1) -> 4..5
+      b[j] = ((ql[j] >> 4) & 0x0F0F0F0Fu) | ((qh[j] >> shr) & 0x30303030u);  // bits (2e+4, 2e+5) -> 4..5
     }
-    // sc[.. + 4] is 4 bytes later: same byte position in the next dword.
+    const int ta = dotq<4>(a, x.h, x.l) - 32 * x.q[0];  // sum (code - 32) q, exact in int32
+    const int tb = dotq<4>(b, x.h + 4, x.l + 4) - 32 * x.q[1];
+    // sc[.. + 4] is 4 bytes later: same byte position in the next dword.  The builtin's result
+    // type is unsigned: the (int) keeps the conversion signed.
     const float sa = (float)(int)__builtin_amdgcn_sbfe((int)r.s0, 8u * r.ssh, 8u);
     const float sb = (float)(int)__builtin_amdgcn_sbfe((int)r.s1, 8u * r.ssh, 8u);
-    o.d = f16lo(r.dd);
-    o.ka = sa * k2p24;
-    o.kb = sb * k2p24;
-    o.ca = -32.0f * (o.d * sa);  // d * int8 scale * 32: exact
-    o.cb = -32.0f * (o.d * sb);
+    return f16lo(r.dd) * __builtin_fmaf(sb, (float)tb, sa * (float)ta);
   }
 };
 
-// Q4_0: slot = block sig; low nibbles of qs[i] are element i (run A), high nibbles element 16+i.
+// Q4_0: slot sig = blocks 2 sig, 2 sig + 1 (36 bytes at 36 sig, dword aligned): block k holds its
+// fp16 scale at bytes 18k..18k+1 and qs at 18k+2..18k+17; low nibbles of qs[i] are element i,
+// high nibbles element 16 + i.  Runs: 0, 1 = block 0 (low, high), 2, 3 = block 1.
 template <> struct Lane<T_Q4_0> {
-  static constexpr int kSPB = 1, kXB = 16;
+  static constexpr int kR = 4;
+  static constexpr int kSlotElems = 64;
   struct Raw {
-    u32x4a4_t q;
-    uint32_t qe, dd, sh;
+    u32x4a4_t a, b;
+    uint32_t e;
   };
-  static __device__ inline int xoff(int sig) { return 32 * sig; }
+  static __device__ inline int xoff(int sig, int run) { return 64 * sig + 16 * run; }
   static __device__ inline void load(const uint8_t* row, int sig, Raw& r) {
-    const int base = 18 * sig, o = base + 2;
-    r.sh = (uint32_t)(o & 3);
-    r.q = ldg16a4(row + (o & ~3));
-    r.qe = ldg2(row + (o & ~3) + 16);  // 2 bytes: the window never passes the block's end
-    r.dd = ldg2(row + base);
+    const uint8_t* p = row + 36 * sig;
+    r.a = ldg16a4(p);
+    r.b = ldg16a4(p + 16);
+    r.e = ldg4(p + 32);
   }
-  static __device__ inline void unpack(const Raw& r, int, Slot& o) {
-    uint32_t q[4];
-    realign16(r.q, r.qe, r.sh, q);
+  // 16 * sum((n - 8) q) over one block
+  static __device__ inline int block(const uint32_t (&qs)[4], const uint32_t* h, const uint32_t* l, int q_lo) {
+    uint32_t lo[4], hi[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      nib_lo(q[j], o.a[2 * j], o.a[2 * j + 1]);
-      nib_hi(q[j], o.b[2 * j], o.b[2 * j + 1]);
+      lo[j] = qs[j] & 0x0F0F0F0Fu;
+      hi[j] = hi_codes(qs[j]);
     }
-    o.d = f16lo(r.dd);
-    o.ka = k2p24;
-    o.kb = k2p20;
-    o.ca = -8.0f * o.d;
-    o.cb = o.ca;
+    return 16 * dotq<4>(lo, h, l) + dotq<4>(hi, h + 4, l + 4) - 128 * q_lo;
+  }
+  static __device__ inline float row(const Raw& r, int, const XQ<4>& x) {
+    const uint32_t q0[4] = {align_bytes(r.a.y, r.a.x, 2), align_bytes(r.a.z, r.a.y, 2), align_bytes(r.a.w, r.a.z, 2),
+                            align_bytes(r.b.x, r.a.w, 2)};
+    const uint32_t q1[4] = {r.b.y, r.b.z, r.b.w, r.e};
+    const int v0 = block(q0, x.h, x.l, x.q[0]);
+    const int v1 = block(q1, x.h + 8, x.l + 8, x.q[2]);
+    return 0.0625f * __builtin_fmaf(f16hi(r.b.x), (float)v1, f16lo(r.a.x) * (float)v0);
   }
 };
 
-// Q8_0: slot = block sig; int8 quants biased to q+128 (one xor) so they are unsigned fp16
-// subnormals; run A = elements 0..15, run B = 16..31.
+// Q8_0: slot sig = blocks 2 sig, 2 sig + 1 (68 bytes at 68 sig, dword aligned): block k holds its
+// fp16 scale at bytes 34k..34k+1 and 32 signed codes at 34k+2..34k+33.  Runs 0, 1 = block 0.
 template <> struct Lane<T_Q8_0> {
-  static constexpr int kSPB = 1, kXB = 16;
+  static constexpr int kR = 4;
+  static constexpr int kSlotElems = 64;
   struct Raw {
-    u32x4a4_t q0, q1;
-    uint32_t qe, dd, sh;
+    u32x4a4_t a, b, c, d;
+    uint32_t e;
   };
-  static __device__ inline int xoff(int sig) { return 32 * sig; }
+  static __device__ inline int xoff(int sig, int run) { return 64 * sig + 16 * run; }
   static __device__ inline void load(const uint8_t* row, int sig, Raw& r) {
-    const int base = 34 * sig, o = base + 2;
-    const uint8_t* a = row + (o & ~3);
-    r.sh = (uint32_t)(o & 3);
-    r.q0 = ldg16a4(a);
-    r.q1 = ldg16a4(a + 16);
-    r.qe = ldg2(a + 32);  // 2 bytes: the window never passes the block's end
-    r.dd = ldg2(row + base);
+    const uint8_t* p = row + 68 * sig;
+    r.a = ldg16a4(p);
+    r.b = ldg16a4(p + 16);
+    r.c = ldg16a4(p + 32);
+    r.d = ldg16a4(p + 48);
+    r.e = ldg4(p + 64);
   }
-  static __device__ inline void unpack(const Raw& r, int, Slot& o) {
-    uint32_t q0[4], q1[4];
-    realign16(r.q0, r.q1.x, r.sh, q0);
-    realign16(r.q1, r.qe, r.sh, q1);
+  static __device__ inline float row(const Raw& r, int, const XQ<4>& x) {
+    const uint32_t w[17] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w, r.c.x,
+                            r.c.y, r.c.z, r.c.w, r.d.x, r.d.y, r.d.z, r.d.w, r.e};
+    uint32_t q0[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t u0 = q0[j] ^ 0x80808080u, u1 = q1[j] ^ 0x80808080u;
-      o.a[2 * j] = u0 & 0x00FF00FFu;
-      o.a[2 * j + 1] = (u0 >> 8) & 0x00FF00FFu;
-      o.b[2 * j] = u1 & 0x00FF00FFu;
-      o.b[2 * j + 1] = (u1 >> 8) & 0x00FF00FFu;
-    }
-    o.d = f16lo(r.dd);
-    o.ka = k2p24;
-    o.kb = k2p24;
-    o.ca = -128.0f * o.d;
-    o.cb = o.ca;
+    for (int j = 0; j < 8; ++j) q0[j] = align_bytes(w[j + 1], w[j], 2);  // bytes 2..33
+    const int t0 = dotq<8>(q0, x.h, x.l);
+    const int t1 = dotq<8>(w + 9, x.h + 8, x.l + 8);  // bytes 36..67
+    return __builtin_fmaf(f16hi(w[8]), (float)t1, f16lo(w[0]) * (float)t0);
   }
 };
 
-// Sum over 16 elements of (packed fp16 integer) * x in element order, fp32 fused steps.
-__device__ inline float dot16(const uint32_t (&p)[8], const float (&x)[16]) {
-  float acc = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    acc = __builtin_fmaf(f16lo(p[2 * j]), x[4 * j + 0], acc);
-    acc = __builtin_fmaf(f16lo(p[2 * j + 1]), x[4 * j + 1], acc);
-    acc = __builtin_fmaf(f16hi(p[2 * j]), x[4 * j + 2], acc);
-    acc = __builtin_fmaf(f16hi(p[2 * j + 1]), x[4 * j + 3], acc);
-  }
-  return acc;
+// ---- cross-lane sums (every lane of the span ends with the same bits: only commutative adds) --
+template <int CTRL>
+__device__ inline float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
+template <int CTRL>
+__device__ inline int dpp(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+constexpr int kXor1 = 0xB1, kXor2 = 0x4E;            // quad_perm [1,0,3,2] / [2,3,0,1]
+constexpr int kHalfMirror = 0x141, kMirror = 0x140;  // lane i <-> 7-i of 8 / 15-i of 16
 
-__device__ inline float sum16(const float (&x)[16]) {
-  float s = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) s += x[i];
+// Sum over aligned spans of `width` lanes (8, 16, 32 or 64).
+__device__ inline float span_sum(float s, int width) {
+  s += dpp<kXor1>(s);
+  s += dpp<kXor2>(s);
+  s += dpp<kHalfMirror>(s);
+  if (width > 8) s += dpp<kMirror>(s);
+  if (width > 16) {  // rows of 16: swap odd rows of one copy with even rows of the other
+    const auto a = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, s), __builtin_bit_cast(int, s), false, false);
+    s = __builtin_bit_cast(float, (int)a[0]) + __builtin_bit_cast(float, (int)a[1]);
+  }
+  if (width > 32) {  // halves of the wave
+    const auto a = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, s), __builtin_bit_cast(int, s), false, false);
+    s = __builtin_bit_cast(float, (int)a[0]) + __builtin_bit_cast(float, (int)a[1]);
+  }
   return s;
 }
 
-__device__ inline void load16(const float* p, float (&x)[16]) {
+// ---- activation conversion (whole workgroup, into LDS) ---------------------------------------
+// A task converts 8 elements: half `hf` of run `run` of (vector, slot) vs, task t = 2R vs + 2 run + hf.
+// The 2R tasks of a slot are 2R aligned lanes of one wave (blockDim is a multiple of 8).  A
+// thread's tasks are t = tid + k*blockDim (k < TPT); tasks past the end are clamped to the last
+// (same data, results not stored) so every load is unconditional.
+template <uint32_t T, int NV>
+__device__ inline const float* task_x(const float* X, int cols, int S, int t) {
+  using L = Lane<T>;
+  static_assert(NV == 1 || NV == 2, "one or two vectors per launch");
+  constexpr int R = L::kR;
+  const int vs = t / (2 * R), part = t % (2 * R);
+  const int v = (NV == 2 && vs >= S) ? 1 : 0, s = vs - v * S;
+  return X + (size_t)v * cols + L::xoff(s, part >> 1) + 8 * (part & 1);
+}
+
+template <int R>
+__device__ inline void convert_task(const float4 x0, const float4 x1, int t, bool store, uint32_t* xs) {
+  const int vs = t / (2 * R), part = t % (2 * R), run = part >> 1, hf = part & 1;
+  float a = fmaxf(fmaxf(fmaxf(fabsf(x0.x), fabsf(x0.y)), fmaxf(fabsf(x0.z), fabsf(x0.w))),
+                  fmaxf(fmaxf(fabsf(x1.x), fabsf(x1.y)), fmaxf(fabsf(x1.z), fabsf(x1.w))));
+  // 0 when the eight elements are finite, NaN otherwise (x * 0 is NaN for +-Inf and NaN)
+  float z = __builtin_fmaf(x0.x, 0.0f, __builtin_fmaf(x0.y, 0.0f, __builtin_fmaf(x0.z, 0.0f, x0.w * 0.0f)));
+  z = __builtin_fmaf(x1.x, 0.0f, __builtin_fmaf(x1.y, 0.0f, __builtin_fmaf(x1.z, 0.0f, __builtin_fmaf(x1.w, 0.0f, z))));
+  a = fmaxf(a, dpp<kXor1>(a));
+  a = fmaxf(a, dpp<kXor2>(a));
+  z += dpp<kXor1>(z);
+  z += dpp<kXor2>(z);
+  if constexpr (R == 4) {
+    a = fmaxf(a, dpp<kHalfMirror>(a));
+    z += dpp<kHalfMirror>(z);
+  }
+  // k = 16383 / (32767 amax): v_cvt_pknorm_i16_f32 returns rn(clamp(y, -1, 1) * 32767)
+  const float k = (a > 0.0f && a <= 3.402823466e38f) ? __builtin_amdgcn_rcpf(a) * (16383.0f / 32767.0f) : 0.0f;
+  const uint32_t p[4] = {
+      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pknorm_i16(x0.x * k, x0.y * k)),
+      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pknorm_i16(x0.z * k, x0.w * k)),
+      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pknorm_i16(x1.x * k, x1.y * k)),
+      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pknorm_i16(x1.z * k, x1.w * k))};
+  uint32_t hs[4], ls[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float4 v = reinterpret_cast<const float4*>(p)[i];
-    x[4 * i] = v.x;
-    x[4 * i + 1] = v.y;
-    x[4 * i + 2] = v.z;
-    x[4 * i + 3] = v.w;
+    hs[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(short2_t, p[i]) >> (short)7);  // q >> 7 per half
+    ls[i] = p[i] & 0x007F007Fu;                                                              // q & 127 per half
+  }
+  const short2_t ones = {1, 1};
+  int sq = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) sq = __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, p[i]), ones, sq, false);
+  sq += dpp<kXor1>(sq);  // the other half of the run
+  if (store) {
+    uint32_t* o = xs + (size_t)vs * xq_words<R>();
+    const int w = 4 * run + 2 * hf;
+    o[w] = __builtin_amdgcn_perm(hs[1], hs[0], 0x06040200u);  // low bytes of the four 16-bit lanes
+    o[w + 1] = __builtin_amdgcn_perm(hs[3], hs[2], 0x06040200u);
+    o[4 * R + w] = __builtin_amdgcn_perm(ls[1], ls[0], 0x06040200u);
+    o[4 * R + w + 1] = __builtin_amdgcn_perm(ls[3], ls[2], 0x06040200u);
+    if (hf == 0) o[8 * R + run] = (uint32_t)sq;
+    if (part == 0) o[9 * R] = __builtin_bit_cast(uint32_t, a * (1.0f / 16383.0f) + z);
   }
 }
 
-// acc + d*(ka*dotA + kb*dotB) + (ca*sxA + cb*sxB), in a fixed sequence of fused steps.
-__device__ inline float combine(const Slot& o, float dA, float dB, float sxA, float sxB, float acc) {
-  float t = o.ka * dA;
-  t = __builtin_fmaf(o.kb, dB, t);
-  float u = o.ca * sxA;
-  u = __builtin_fmaf(o.cb, sxB, u);
-  return __builtin_fmaf(o.d, t, acc) + u;
-}
-
-// Fixed xor butterfly over the low `width` lanes' partner set (width = 64 or a power of two < 64).
-__device__ inline float group_sum(float v, int width) {
+template <int R>
+__device__ inline void read_xq(const uint32_t* xs, XQ<R>& x) {
+  const uint4* p = reinterpret_cast<const uint4*>(xs);
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1)
-    if (off < width) v += __shfl_xor(v, off, 64);
-  return v;
+  for (int i = 0; i < R; ++i) {
+    const uint4 h = p[i], l = p[R + i];
+    x.h[4 * i] = h.x; x.h[4 * i + 1] = h.y; x.h[4 * i + 2] = h.z; x.h[4 * i + 3] = h.w;
+    x.l[4 * i] = l.x; x.l[4 * i + 1] = l.y; x.l[4 * i + 2] = l.z; x.l[4 * i + 3] = l.w;
+  }
+  if constexpr (R == 2) {
+    const uint4 m = p[4];
+    x.q[0] = (int)m.x;
+    x.q[1] = (int)m.y;
+    x.sx = __builtin_bit_cast(float, m.z);
+  } else {
+    const uint4 m = p[8];
+    x.q[0] = (int)m.x;
+    x.q[1] = (int)m.y;
+    x.q[2] = (int)m.z;
+    x.q[3] = (int)m.w;
+    x.sx = __builtin_bit_cast(float, xs[36]);
+  }
 }
 
-template <uint32_t T, int NV, int RL>
+// Dynamic LDS bytes of the kernel: the converted activations.
+template <uint32_t T>
+inline size_t gemv_lds_bytes(int nv, int S) {
+  return (size_t)nv * S * xq_words<Lane<T>::kR>() * 4;
+}
+
+// Launch geometry: blockDim = (Sp, G); workgroup b owns rows [rb, rb + cnt) with
+// rb = b*base + min(b, rem), cnt = base + (b < rem).
+struct Geo {
+  int S, Sp, G;
+  int base, rem;
+  uint32_t row_bytes;
+};
+
+// One workgroup: G groups of Sp lanes; group g computes rows rb + g + G*i (i < RMAX, g + G*i < cnt).
+// TPT = conversion tasks per thread (NV * S * 2R <= TPT * blockDim).  Every global load is issued
+// unconditionally (rows past the workgroup's last are clamped to it and their results dropped):
+// activations first, then the first PF rows, and each later row PF rows ahead of its use, so a
+// row's arithmetic waits only for its own bytes while the next ones are arriving.
+template <uint32_t T, int NV, int RMAX, int TPT, int PF>
 __global__ __launch_bounds__(1024) void k_gemv(const uint8_t* __restrict__ W, const float* __restrict__ X,
-                                               float* __restrict__ Y, int rows, int cols, size_t row_bytes,
-                                               int S, int Sp, int G) {
+                                               float* __restrict__ Y, int rows, int cols, Geo geo) {
   using L = Lane<T>;
+  constexpr int R = L::kR;
+  extern __shared__ uint4 xs_lds[];
   __shared__ float red[16][16];  // [output of the group][wave of the group] for groups wider than a wave
-  const int tid = threadIdx.x;
-  const int g = tid / Sp, sig = tid - g * Sp;
-  const int row0 = blockIdx.x * G * RL;
-  const bool active = sig < S;
-  float acc[RL][NV];
-#pragma unroll
-  for (int i = 0; i < RL; ++i)
-#pragma unroll
-    for (int v = 0; v < NV; ++v) acc[i][v] = 0.0f;
+  uint32_t* xs = reinterpret_cast<uint32_t*>(xs_lds);
+  const int S = geo.S, Sp = geo.Sp, G = geo.G;
+  const int sig0 = threadIdx.x, g = threadIdx.y, tid = g * Sp + sig0, nthr = Sp * G;
+  const int sig = min(sig0, S - 1);  // padding lanes mirror the last slot; their partials are zeroed
+  const int b = blockIdx.x;
+  const int rb = b * geo.base + min(b, geo.rem), cnt = geo.base + (b < geo.rem ? 1 : 0);
+  const uint8_t* wb = W + (size_t)rb * geo.row_bytes;
+  const int ntask = NV * S * 2 * R;
 
-  if (active) {
-    // this lane's rows: row0 + g + G*i; issue every row's loads before using any of them
-    typename L::Raw raw[RL];
+  // 1. activations of this thread's conversion tasks
+  float4 xr[TPT][2];
 #pragma unroll
-    for (int i = 0; i < RL; ++i) {
-      const int r = min(row0 + g + G * i, rows - 1);  // clamp: past-the-end rows recompute a valid row
-      L::load(W + (size_t)r * row_bytes, sig, raw[i]);
-    }
-    const float* xp = X + L::xoff(sig);
-    if constexpr (NV <= 2) {
-      float xa[NV][16], xb[NV][16], sa[NV], sb[NV];
-#pragma unroll
-      for (int v = 0; v < NV; ++v) {
-        load16(xp + (size_t)v * cols, xa[v]);
-        load16(xp + (size_t)v * cols + L::kXB, xb[v]);
-        sa[v] = sum16(xa[v]);
-        sb[v] = sum16(xb[v]);
-      }
-#pragma unroll
-      for (int i = 0; i < RL; ++i) {
-        Slot o;
-        L::unpack(raw[i], sig, o);
-#pragma unroll
-        for (int v = 0; v < NV; ++v)
-          acc[i][v] = combine(o, dot16(o.a, xa[v]), dot16(o.b, xb[v]), sa[v], sb[v], acc[i][v]);
-      }
-    } else {
-      float sa[NV], sb[NV];
-#pragma unroll
-      for (int v = 0; v < NV; ++v) {
-        float xa[16], xb[16];
-        load16(xp + (size_t)v * cols, xa);
-        load16(xp + (size_t)v * cols + L::kXB, xb);
-        sa[v] = sum16(xa);
-        sb[v] = sum16(xb);
-      }
-#pragma unroll
-      for (int i = 0; i < RL; ++i) {
-        Slot o;
-        L::unpack(raw[i], sig, o);
-#pragma unroll
-        for (int v = 0; v < NV; ++v) {
-          float xa[16], xb[16];
-          load16(xp + (size_t)v * cols, xa);
-          load16(xp + (size_t)v * cols + L::kXB, xb);
-          acc[i][v] = combine(o, dot16(o.a, xa), dot16(o.b, xb), sa[v], sb[v], acc[i][v]);
-        }
-      }
-    }
+  for (int k = 0; k < TPT; ++k) {
+    const float4* p = reinterpret_cast<const float4*>(task_x<T, NV>(X, cols, S, min(tid + k * nthr, ntask - 1)));
+    xr[k][0] = p[0];
+    xr[k][1] = p[1];
   }
 
-  // ---- reduction over the group's S' lanes (fixed order) -----------------------------------
-  const int lane = tid & 63;
+  // 2. the quant bytes of the first PF rows (row offsets within the workgroup fit 32 bits)
+  typename L::Raw raw[PF];
+#pragma unroll
+  for (int i = 0; i < PF; ++i) L::load(wb + (uint32_t)min(g + G * i, cnt - 1) * geo.row_bytes, sig, raw[i]);
+
+  // 3. fixed-point activations into LDS
+#pragma unroll
+  for (int k = 0; k < TPT; ++k) {
+    const int t = tid + k * nthr;
+    convert_task<R>(xr[k][0], xr[k][1], min(t, ntask - 1), t < ntask, xs);
+  }
+  __syncthreads();
+
+  // 4. rows in arrival order
+  XQ<R> x[NV];
+#pragma unroll
+  for (int v = 0; v < NV; ++v) read_xq<R>(xs + ((size_t)v * S + sig) * xq_words<R>(), x[v]);
+  const float keep = sig0 < S ? 1.0f : 0.0f;
+  float p[RMAX][NV];
+#pragma unroll
+  for (int i = 0; i < RMAX; ++i) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) p[i][v] = L::row(raw[i % PF], sig, x[v]) * (x[v].sx * keep);
+    if (i + PF < RMAX) L::load(wb + (uint32_t)min(g + G * (i + PF), cnt - 1) * geo.row_bytes, sig, raw[i % PF]);
+  }
+
+  // 5. reduction over the group's S' lanes (fixed order)
   if (Sp <= 64) {
 #pragma unroll
-    for (int i = 0; i < RL; ++i) {
-      const int r = row0 + g + G * i;
+    for (int i = 0; i < RMAX; ++i) {
 #pragma unroll
       for (int v = 0; v < NV; ++v) {
-        const float s = group_sum(acc[i][v], Sp);
-        if (sig == 0 && r < rows) Y[(size_t)v * rows + r] = s;
+        const float s = span_sum(p[i][v], Sp);
+        if (sig0 == 0 && g + G * i < cnt) Y[(size_t)v * rows + rb + g + G * i] = s;
       }
     }
   } else {
-    const int wig = sig >> 6, nw = Sp >> 6;  // wave index within the group, waves per group
-    // outputs in chunks of 16 so the LDS table stays small for any RL * NV
-    constexpr int NO = RL * NV;
+    const int wig = sig0 >> 6, nw = Sp >> 6;  // wave index within the group, waves per group
+    // outputs in chunks of 16 so the LDS table stays small for any RMAX * NV
+    constexpr int NO = RMAX * NV;
 #pragma unroll
     for (int o0 = 0; o0 < NO; o0 += 16) {
 #pragma unroll
       for (int o = o0; o < NO && o < o0 + 16; ++o) {
-        const float s = group_sum(acc[o / NV][o % NV], 64);
-        if (lane == 0) red[o - o0][g * nw + wig] = s;
+        const float s = span_sum(p[o / NV][o % NV], 64);
+        if ((sig0 & 63) == 0) red[o - o0][g * nw + wig] = s;
       }
       __syncthreads();
       // one thread per (group, output): sum the group's wave partials in wave order
-      const int gg = tid / 16, oo = tid % 16;
+      const int gg = tid >> 4, oo = tid & 15;
       if (gg < G && o0 + oo < NO) {
-        float s = 0.0f;
-        for (int w = 0; w < nw; ++w) s += red[oo][gg * nw + w];
         const int i = (o0 + oo) / NV, v = (o0 + oo) % NV;
-        const int r = row0 + gg + G * i;
-        if (r < rows) Y[(size_t)v * rows + r] = s;
+        if (gg + G * i < cnt) {
+          float s = 0.0f;
+          for (int w = 0; w < nw; ++w) s += red[oo][gg * nw + w];
+          Y[(size_t)v * rows + rb + gg + G * i] = s;
+        }
       }
       __syncthreads();
     }
@@ -398,84 +489,123 @@ __global__ __launch_bounds__(1024) void k_gemv(const uint8_t* __restrict__ W, co
 
 // ---- launch ---------------------------------------------------------------------------------
 
-template <uint32_t T, int NV, int RL>
-static void launch_t(const void* w, const float* X, float* Y, int rows, int cols, size_t row_bytes, int S, int Sp,
-                     int G, hipStream_t s) {
-  const int rt = G * RL;
-  const unsigned grid = (unsigned)((rows + rt - 1) / rt);
-  k_gemv<T, NV, RL><<<grid, G * Sp, 0, s>>>(static_cast<const uint8_t*>(w), X, Y, rows, cols, row_bytes, S, Sp, G);
+constexpr int kCUs = 256;  // MI355X compute units
+
+// Rows a group keeps in flight ahead of the one being computed (measured per type: the 6-bit
+// formats, with the most registers per row, do best with one).
+template <uint32_t T>
+constexpr int prefetch_rows() {
+  return T == T_Q6_K ? 1 : 2;
 }
 
-// Rows per lane: enough rows in flight per lane to cover HBM latency, few enough to keep
-// 2-4 waves per SIMD resident and >= ~2 workgroups per CU.
-template <uint32_t T, int NV>
-static void launch_nv(const void* w, const float* X, float* Y, int rows, int cols, size_t row_bytes, int S, int Sp,
-                      int G, hipStream_t s) {
-  constexpr bool big = T == T_Q4_K || T == T_Q4_0;  // fewer raw registers per row
-  if constexpr (NV == 1) {
-    if (rows >= 256 * 8 * G) return launch_t<T, NV, big ? 8 : 4>(w, X, Y, rows, cols, row_bytes, S, Sp, G, s);
-    if (rows >= 256 * 4 * G) return launch_t<T, NV, 4>(w, X, Y, rows, cols, row_bytes, S, Sp, G, s);
-    return launch_t<T, NV, 2>(w, X, Y, rows, cols, row_bytes, S, Sp, G, s);
-  } else if constexpr (NV == 2) {
-    if (big && rows >= 256 * 4 * G) return launch_t<T, NV, 4>(w, X, Y, rows, cols, row_bytes, S, Sp, G, s);
-    return launch_t<T, NV, 2>(w, X, Y, rows, cols, row_bytes, S, Sp, G, s);
-  } else if constexpr (NV <= 8) {
-    return launch_t<T, NV, 2>(w, X, Y, rows, cols, row_bytes, S, Sp, G, s);
-  } else {
-    return launch_t<T, NV, 1>(w, X, Y, rows, cols, row_bytes, S, Sp, G, s);
+template <uint32_t T, int NV, int RMAX, int TPT>
+static void launch_t(const void* w, const float* X, float* Y, int rows, int cols, const Geo& geo, int nwg,
+                     hipStream_t s) {
+  constexpr int PF = prefetch_rows<T>() < RMAX ? prefetch_rows<T>() : RMAX;
+  auto kern = &k_gemv<T, NV, RMAX, TPT, PF>;
+  const size_t lds = gemv_lds_bytes<T>(NV, geo.S);
+  if (lds > 64 * 1024)
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)lds);
+  kern<<<(unsigned)nwg, dim3((unsigned)geo.Sp, (unsigned)geo.G), lds, s>>>(static_cast<const uint8_t*>(w), X, Y,
+                                                                           rows, cols, geo);
+}
+
+// Rows per group RMAX (1..RM), rounded up to an instantiated value.
+template <uint32_t T, int NV, int TPT, int RM>
+static void launch_r(int rmax, const void* w, const float* X, float* Y, int rows, int cols, const Geo& geo, int nwg,
+                     hipStream_t s) {
+  if constexpr (RM > 1) {
+    if (rmax < RM) return launch_r<T, NV, TPT, RM - 1>(rmax, w, X, Y, rows, cols, geo, nwg, s);
   }
+  launch_t<T, NV, RM, TPT>(w, X, Y, rows, cols, geo, nwg, s);
+}
+
+// Most rows a group takes (its partial sums stay in registers until the end).
+template <int NV, int TPT>
+constexpr int max_rows() {
+  return NV == 1 && TPT < 8 ? 8 : 4;
+}
+
+template <uint32_t T, int NV, int TPT>
+static void launch_tpt(const void* w, const float* X, float* Y, int rows, int cols, Geo geo, hipStream_t s) {
+  constexpr int rm = max_rows<NV, TPT>();
+  const int G = geo.G, waves = geo.Sp * G / 64;
+  // one pass of workgroups over the chip (16 waves per CU), at least one row per group on
+  // average, and never more than rm rows per group
+  int64_t nwg = (int64_t)kCUs * (waves >= 16 ? 1 : 16 / waves);
+  nwg = std::min<int64_t>(nwg, ((int64_t)rows + G - 1) / G);
+  nwg = std::max<int64_t>(nwg, ((int64_t)rows + (int64_t)G * rm - 1) / ((int64_t)G * rm));
+  geo.base = (int)(rows / nwg);
+  geo.rem = (int)(rows % nwg);
+  const int rmax = (geo.base + (geo.rem ? 1 : 0) + G - 1) / G;
+  launch_r<T, NV, TPT, rm>(rmax, w, X, Y, rows, cols, geo, (int)nwg, s);
+}
+
+template <uint32_t T, int NV>
+static void launch_nv(const void* w, const float* X, float* Y, int rows, int cols, const Geo& geo, hipStream_t s) {
+  const int threads = geo.G * geo.Sp;
+  const int tpt = (NV * geo.S * 2 * Lane<T>::kR + threads - 1) / threads;
+  if (tpt <= 1) return launch_tpt<T, NV, 1>(w, X, Y, rows, cols, geo, s);
+  if (tpt <= 2) return launch_tpt<T, NV, 2>(w, X, Y, rows, cols, geo, s);
+  if (tpt <= 4) return launch_tpt<T, NV, 4>(w, X, Y, rows, cols, geo, s);
+  return launch_tpt<T, NV, 8>(w, X, Y, rows, cols, geo, s);
 }
 
 template <uint32_t T>
-static void launch_type(const void* w, const float* X, float* Y, int nvec, int rows, int cols, size_t row_bytes,
-                        int S, int Sp, int G, hipStream_t s) {
-  switch (nvec) {
-    case 1: return launch_nv<T, 1>(w, X, Y, rows, cols, row_bytes, S, Sp, G, s);
-    case 2: return launch_nv<T, 2>(w, X, Y, rows, cols, row_bytes, S, Sp, G, s);
-    case 3: return launch_nv<T, 3>(w, X, Y, rows, cols, row_bytes, S, Sp, G, s);
-    case 4: return launch_nv<T, 4>(w, X, Y, rows, cols, row_bytes, S, Sp, G, s);
-    case 5: return launch_nv<T, 5>(w, X, Y, rows, cols, row_bytes, S, Sp, G, s);
-    case 6: return launch_nv<T, 6>(w, X, Y, rows, cols, row_bytes, S, Sp, G, s);
-    case 7: return launch_nv<T, 7>(w, X, Y, rows, cols, row_bytes, S, Sp, G, s);
-    case 8: return launch_nv<T, 8>(w, X, Y, rows, cols, row_bytes, S, Sp, G, s);
-    case 9: return launch_nv<T, 9>(w, X, Y, rows, cols, row_bytes, S, Sp, G, s);
-    case 10: return launch_nv<T, 10>(w, X, Y, rows, cols, row_bytes, S, Sp, G, s);
-    case 11: return launch_nv<T, 11>(w, X, Y, rows, cols, row_bytes, S, Sp, G, s);
-    case 12: return launch_nv<T, 12>(w, X, Y, rows, cols, row_bytes, S, Sp, G, s);
-    case 13: return launch_nv<T, 13>(w, X, Y, rows, cols, row_bytes, S, Sp, G, s);
-    case 14: return launch_nv<T, 14>(w, X, Y, rows, cols, row_bytes, S, Sp, G, s);
-    case 15: return launch_nv<T, 15>(w, X, Y, rows, cols, row_bytes, S, Sp, G, s);
-    default: return launch_nv<T, 16>(w, X, Y, rows, cols, row_bytes, S, Sp, G, s);
+static void launch_type(const void* w, const float* X, float* Y, int nvec, int rows, int cols, const Geo& geo,
+                        hipStream_t s) {
+  for (int v0 = 0; v0 < nvec; v0 += 2) {
+    const float* Xv = X + (size_t)v0 * cols;
+    float* Yv = Y + (size_t)v0 * rows;
+    if (nvec - v0 >= 2)
+      launch_nv<T, 2>(w, Xv, Yv, rows, cols, geo, s);
+    else
+      launch_nv<T, 1>(w, Xv, Yv, rows, cols, geo, s);
   }
 }
 
 // Slot geometry of a row: S slots, padded group width Sp, groups per workgroup G.  Returns false
-// when a row has more than 1024 slots (K > 32768): the generic kernel takes those.
-bool gemv_geometry(uint32_t t, int cols, int& S, int& Sp, int& G) {
-  const int spb = (t == T_Q4_K || t == T_Q6_K) ? 8 : 1;
-  const int qk = (t == T_Q4_K || t == T_Q6_K) ? 256 : 32;
-  S = cols / qk * spb;
-  if (S <= 0 || S > 1024) return false;
+// when K is not a whole number of slots, a row has more than 1024 slots, or two vectors'
+// converted activations do not fit in LDS: the generic kernel takes those.
+template <uint32_t T>
+static bool geometry(int cols, size_t row_bytes, Geo& geo) {
+  constexpr int E = Lane<T>::kSlotElems;
+  if (cols % E != 0 || row_bytes > 0xFFFFFFFFull / 1024) return false;
+  const int S = cols / E;
+  if (S <= 0 || S > 1024 || gemv_lds_bytes<T>(2, S) > 150 * 1024) return false;
+  int Sp;
   if (S <= 64) {
-    Sp = 1;
+    Sp = 8;
     while (Sp < S) Sp <<= 1;
   } else {
     Sp = (S + 63) & ~63;
   }
-  G = Sp >= 256 ? 1 : 256 / Sp;
+  geo.S = S;
+  geo.Sp = Sp;
+  geo.G = 1024 / Sp;
+  geo.row_bytes = (uint32_t)row_bytes;
   return true;
 }
 
-// Fast-path GEMV for 1 <= nvec <= 16 on 16-byte-aligned rows of Q8_0 / Q4_0 / Q4_K / Q6_K.
+template <uint32_t T>
+static bool launch_fast_t(const void* w, const float* X, float* Y, int nvec, int rows, int cols, size_t row_bytes,
+                          hipStream_t s) {
+  Geo geo{};
+  if (!geometry<T>(cols, row_bytes, geo)) return false;
+  launch_type<T>(w, X, Y, nvec, rows, cols, geo, s);
+  return true;
+}
+
+// Fast-path GEMV for nvec >= 1 on 16-byte-aligned rows of Q8_0 / Q4_0 / Q4_K / Q6_K.  Returns
+// false, having launched nothing, when the shape needs the generic kernel.
 bool launch_gemv_fast(uint32_t t, const void* w, const float* X, float* Y, int nvec, int rows, int cols,
                       size_t row_bytes, hipStream_t s) {
-  int S, Sp, G;
-  if (!gemv_geometry(t, cols, S, Sp, G)) return false;
   switch (t) {
-    case T_Q4_K: launch_type<T_Q4_K>(w, X, Y, nvec, rows, cols, row_bytes, S, Sp, G, s); return true;
-    case T_Q6_K: launch_type<T_Q6_K>(w, X, Y, nvec, rows, cols, row_bytes, S, Sp, G, s); return true;
-    case T_Q4_0: launch_type<T_Q4_0>(w, X, Y, nvec, rows, cols, row_bytes, S, Sp, G, s); return true;
-    case T_Q8_0: launch_type<T_Q8_0>(w, X, Y, nvec, rows, cols, row_bytes, S, Sp, G, s); return true;
+    case T_Q4_K: return launch_fast_t<T_Q4_K>(w, X, Y, nvec, rows, cols, row_bytes, s);
+    case T_Q6_K: return launch_fast_t<T_Q6_K>(w, X, Y, nvec, rows, cols, row_bytes, s);
+    case T_Q4_0: return launch_fast_t<T_Q4_0>(w, X, Y, nvec, rows, cols, row_bytes, s);
+    case T_Q8_0: return launch_fast_t<T_Q8_0>(w, X, Y, nvec, rows, cols, row_bytes, s);
     default: return false;
   }
 }
