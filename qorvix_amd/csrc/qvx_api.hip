@@ -20,6 +20,9 @@ bool launch_gemv_generic(uint32_t t, const void* w, const float* X, float* Y, in
                          size_t row_bytes, hipStream_t s);
 bool launch_gemv_fast(uint32_t t, const void* w, const float* X, float* Y, int nvec, int rows, int cols,
                       size_t row_bytes, hipStream_t s);
+int gemv_mx_max_nv(int cols);
+bool launch_gemv_mx_q4k(const void* w, const float* X, float* Y, int nvec, int rows, int cols, size_t row_bytes,
+                        hipStream_t s);
 bool launch_fill_synthetic(void* w, uint32_t t, size_t nblk, uint64_t seed, float mul, hipStream_t s);
 void launch_fill_normal_f32(float* x, size_t n, uint64_t seed, float mul, hipStream_t s);
 void launch_fill_normal_f16(uint16_t* x, size_t n, uint64_t seed, float mul, hipStream_t s);
@@ -71,9 +74,19 @@ int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int
   if (!w || !X) return QVX_E_NULL;
   const size_t row_bytes = (size_t)(cols / (int)ti->block) * ti->bytes;
   const bool fast = type != T_F32 && aligned16(w) && aligned16(X) && row_bytes % 16 == 0;
-  // The fast kernel takes any number of vectors (a few per launch, each vector's arithmetic the same
-  // in every launch, so batches stay bit-identical to single vectors); shapes it does not cover go
-  // to the generic kernel.
+  // The fast kernels take any number of vectors, a few per launch; each vector's arithmetic is the
+  // same in every launch, so batches stay bit-identical to single vectors.  Q4_K runs on the matrix
+  // cores (up to gemv_mx_max_nv vectors per launch), the other formats on the VALU kernel; shapes
+  // neither covers go to the generic kernel.
+  const int mx = (fast && type == T_Q4_K) ? gemv_mx_max_nv(cols) : 0;
+  if (mx > 0) {
+    for (int v0 = 0; v0 < nvec; v0 += mx) {
+      const int nv = nvec - v0 < mx ? nvec - v0 : mx;
+      if (!launch_gemv_mx_q4k(w, X + (size_t)v0 * cols, out + (size_t)v0 * rows, nv, rows, cols, row_bytes, s))
+        return QVX_E_TYPE;
+    }
+    return hip_status();
+  }
   if (fast && launch_gemv_fast(type, w, X, out, nvec, rows, cols, row_bytes, s)) return hip_status();
   for (int v0 = 0; v0 < nvec; v0 += 16) {
     const int nv = nvec - v0 < 16 ? nvec - v0 : 16;

@@ -369,7 +369,7 @@ __device__ inline void read_xq(const uint32_t* xs, XQ<R>& x) {
     const uint4 m = p[4];
     x.q[0] = (int)m.x;
     x.q[1] = (int)m.y;
-    x.sx = __builtin_bit_cast(float, m.z);
+    x.sx = __uint_as_float(m.z);
   } else {
     const uint4 m = p[8];
     x.q[0] = (int)m.x;
@@ -428,6 +428,7 @@ __global__ __launch_bounds__(1024) void k_gemv(const uint8_t* __restrict__ W, co
   typename L::Raw raw[PF];
 #pragma unroll
   for (int i = 0; i < PF; ++i) L::load(wb + (uint32_t)min(g + G * i, cnt - 1) * geo.row_bytes, sig, raw[i]);
+  __builtin_amdgcn_sched_barrier(0);  // keep the loads here: the scheduler would sink them to their uses
 
   // 3. fixed-point activations into LDS
 #pragma unroll
@@ -448,6 +449,7 @@ __global__ __launch_bounds__(1024) void k_gemv(const uint8_t* __restrict__ W, co
 #pragma unroll
     for (int v = 0; v < NV; ++v) p[i][v] = L::row(raw[i % PF], sig, x[v]) * (x[v].sx * keep);
     if (i + PF < RMAX) L::load(wb + (uint32_t)min(g + G * (i + PF), cnt - 1) * geo.row_bytes, sig, raw[i % PF]);
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   // 5. reduction over the group's S' lanes (fixed order)
