@@ -1,32 +1,93 @@
 // qvx_gemm.hip -- prefill GEMM (M >= 128) over raw GGUF Q4_K blocks on gfx950 matrix cores.
 //
-// out[m, r] = sum_k X[m, k] * dequant(W)[r, k],  X fp16 [M, K], W Q4_K [N rows, K], out fp32 [M, N].
+// out[m, r] = sum_k X[m, k] * dequant(W)[r, k],  X [M, K] 16-bit, W Q4_K [N rows, K], out fp32 [M, N].
 // No reference counterpart (the reference prefills token by token); the semantics are qmatmulN's
 // (runtime/src/qmatmul.cpp:64-115) with X converted fp16 -> fp32 exactly.
 //
-// Tiling (256 threads = 4 waves, v_mfma_f32_32x32x16_{bf16,f16}):
-//  * A workgroup computes a BM x (4*32*NT) output tile; wave w owns NT 32-row strips of W and
-//    all BM tokens, so every weight element is dequantised exactly once per workgroup.
-//  * K advances in slices of 64 elements = one 64-element group c of a Q4_K super-block.  Each
-//    lane (n = lane%32, g = lane/32) loads the 16 quant bytes 32c+16g..+15 of its weight row and
-//    the 16-byte super-block header straight into registers (aligned 16-byte loads), dequantises
-//    them exactly in fp32 (d*sc*n - dmin*m, one rounding, the reference's dequant value), rounds to
-//    bf16 / fp16 and uses them as the B operand of four K16 steps: low nibbles 0-7, 8-15, then high
-//    nibbles 0-7, 8-15.  The A operand (X) is read from LDS in exactly that element order.
-//  * The X slice (BM x 64 halves) is staged in a double-buffered LDS tile (row pitch padded by 16
-//    bytes) with one barrier per slice; loads of slice k+1 are in flight during slice k's MFMAs.
-//  * Small grids split K across workgroups and accumulate with fp32 atomics into a zeroed output.
+// Workgroup = 256 threads (4 waves) computing a BM x 256 output tile (BM tokens x 256 weight rows);
+// wave w owns weight rows 64w..64w+63 of the tile (two 32-row MFMA columns) and all BM tokens, so
+// every weight element is dequantised once per workgroup.  v_mfma_f32_32x32x16_{bf16,f16}.
+//
+// K advances in slices of 64 elements = one 64-element group c of a Q4_K super-block:
+//  * X slice (BM x 64 16-bit values, 128 bytes a row) and W slice (256 super-block headers of 16
+//    bytes + 256 x 32 quant bytes of group c) are copied global -> LDS with buffer_load_dwordx4 ...
+//    lds (no registers, no VALU), three stages deep: X two slices ahead, W three.  The main loop
+//    issues no other vector-memory operation, so s_waitcnt vmcnt with a static count tracks the
+//    copies, and one barrier per slice publishes them.
+//  * X rows sit 128 bytes apart with the 16-byte chunk kc of row r at slot kc ^ swz(r),
+//    swz(r) = (r ^ (r >> 3 & 3)) & 7: the A-fragment reads (rows r..r+15, one chunk each) hit
+//    distinct banks for 32- and 64-bank LDS alike.
+//  * B operands: lane (n = lane % 32, g = lane / 32) reads the header and quant bytes 16g..16g+15
+//    of group c of its weight row from LDS and dequantises them exactly in fp32 (d*sc*q - dmin*m,
+//    one rounding: the reference's dequant value) before rounding to bf16 / fp16; K16 steps 0-3
+//    take low nibbles 0-7, 8-15, then high nibbles 0-7, 8-15, and the A operand (X) is read in
+//    exactly that element order.  Slice k+1 is dequantised while the MFMAs of slice k run.
+//  * The loop reads LDS through inline asm (lds_read16) with explicit lgkmcnt waits: the compiler
+//    would otherwise wait for every copy in flight before each LDS read.
+// Grids smaller than the chip split K across workgroups and accumulate with fp32 atomics into a
+// zero-filled output.
+//
+// The bf16 variant first rounds X to bf16 (RNE) in a prepass into a stream-ordered temporary; the
+// fp16 variant reads X as is.
+// qvx_common.hpp (hip_runtime.h) must come first: a standard header included before it stops the
+// host stubs of template kernels from being emitted.
 #include "qvx_common.hpp"
 
+#include <mutex>
+
 namespace qvx {
+
+namespace gemm {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
-typedef int i32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+#define QVX_LDS __attribute__((address_space(3)))
 
 enum { VAR_BF16 = 0, VAR_I8 = 1, VAR_F16 = 2 };
+
+constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit data (gfx9)
+constexpr int kBN = 256;                      // weight rows per workgroup tile
+constexpr int kWStage = kBN * 48;             // LDS bytes of one W slice: headers + quant bytes
+
+// s_waitcnt vmcnt(N), other counters untouched (gfx9 encoding).
+template <int N>
+__device__ inline void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+template <int OFF = 0>
+__device__ inline u32x4 lds_read16(uint32_t addr) {
+  u32x4 r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF) : "memory");
+  return r;
+}
+// Waits for the LDS reads in flight; the results are operands, so no use moves above the wait.
+template <int N>
+__device__ inline void lds_wait(u32x4 (&r)[N]) {
+  static_assert(N == 8 || N == 4, "lds_wait arity");
+  if constexpr (N == 4) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3])::"memory");
+  } else {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7])::"memory");
+  }
+}
+__device__ inline void lds_wait(u32x4 (&a)[4], u32x4 (&b)[4]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3])::"memory");
+}
+__device__ inline void lds_wait(u32x4 (&a)[8], u32x4 (&b)[4]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]), "+v"(a[6]), "+v"(a[7]),
+                 "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3])::"memory");
+}
+
+__device__ inline uint32_t xswz(uint32_t r) { return (r ^ ((r >> 3) & 3u)) & 7u; }
+__device__ inline uint32_t qswz(uint32_t r) { return ((r >> 2) ^ (r >> 3)) & 1u; }
 
 // Two fp32 -> one dword of two 16-bit values (round to nearest even).
 template <int VAR> __device__ inline uint32_t pack2(float a, float b);
@@ -40,29 +101,62 @@ template <> __device__ inline uint32_t pack2<VAR_F16>(float a, float b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// 6-bit (scale, min) of sub-blocks 2c, 2c+1 from a Q4_K header, as byte pairs (c uniform).
-__device__ inline void q4k_pairs(const uint4& h, int c, uint32_t& scp, uint32_t& mp) {
-  if (c < 2) {
-    const uint32_t sh = 16u * (uint32_t)c;
-    scp = (h.y >> sh) & 0x3F3Fu;
-    mp = (h.z >> sh) & 0x3F3Fu;
-  } else {
-    const uint32_t sh = 16u * (uint32_t)(c - 2);
-    scp = ((h.w >> sh) & 0x0F0Fu) | ((h.y >> (sh + 2)) & 0x3030u);
-    mp = ((h.w >> (sh + 4)) & 0x0F0Fu) | ((h.z >> (sh + 2)) & 0x3030u);
-  }
-}
+__device__ inline float ub(uint32_t w, int k) { return (float)((w >> (8 * k)) & 0xFFu); }
 
-// Dequantises 8 nibbles (4 bytes of two dwords, low or high nibbles) to one MFMA operand.
+// 8 values ds * byte + dm of two dwords of masked codes (one MFMA operand).
 template <int VAR>
-__device__ inline i32x4_t deq8(uint32_t w0, uint32_t w1, float ds, float mdm) {
+__device__ inline i32x4_t deq8(uint32_t w0, uint32_t w1, float ds, float dm) {
   i32x4_t o;
-  o[0] = (int)pack2<VAR>(__builtin_fmaf(ds, (float)(w0 & 15u), mdm), __builtin_fmaf(ds, (float)((w0 >> 8) & 15u), mdm));
-  o[1] = (int)pack2<VAR>(__builtin_fmaf(ds, (float)((w0 >> 16) & 15u), mdm), __builtin_fmaf(ds, (float)(w0 >> 24 & 15u), mdm));
-  o[2] = (int)pack2<VAR>(__builtin_fmaf(ds, (float)(w1 & 15u), mdm), __builtin_fmaf(ds, (float)((w1 >> 8) & 15u), mdm));
-  o[3] = (int)pack2<VAR>(__builtin_fmaf(ds, (float)((w1 >> 16) & 15u), mdm), __builtin_fmaf(ds, (float)(w1 >> 24 & 15u), mdm));
+  o[0] = (int)pack2<VAR>(__builtin_fmaf(ds, ub(w0, 0), dm), __builtin_fmaf(ds, ub(w0, 1), dm));
+  o[1] = (int)pack2<VAR>(__builtin_fmaf(ds, ub(w0, 2), dm), __builtin_fmaf(ds, ub(w0, 3), dm));
+  o[2] = (int)pack2<VAR>(__builtin_fmaf(ds, ub(w1, 0), dm), __builtin_fmaf(ds, ub(w1, 1), dm));
+  o[3] = (int)pack2<VAR>(__builtin_fmaf(ds, ub(w1, 2), dm), __builtin_fmaf(ds, ub(w1, 3), dm));
   return o;
 }
+
+// a & mask as an opaque instruction: keeps the masked dword whole, so each byte converts with one
+// v_cvt_f32_ubyteN instead of being re-extracted per element.
+template <uint32_t MASK>
+__device__ inline uint32_t and_mask(uint32_t a) {
+  uint32_t r;
+  asm("v_and_b32 %0, %1, %2" : "=v"(r) : "i"(MASK), "v"(a));
+  return r;
+}
+
+// B operands of one weight row for one slice: header h, quant bytes q (16g..16g+15 of group c).
+// Low nibbles: ds0 * n - dmin*m0.  High nibbles are kept in place (16 n) and scaled by ds1 / 16,
+// an exact power-of-two step, so the fma rounds d*sc*n - dmin*m exactly once.
+// Shift / mask set that extracts the 6-bit (scale, min) pairs of sub-blocks 2c, 2c+1 from a Q4_K
+// header without branches: pair = ((word_a >> sa) & ma) | ((h.w >> sb) & mb), word_a = h.y for the
+// scales, h.z for the mins (the min nibbles sit 4 bits higher in h.w).  c is uniform: scalar math.
+struct ScaleSel {
+  uint32_t sa, ma, sb, mb;
+};
+__device__ inline ScaleSel scale_sel(int c) {
+  const bool hi = c >= 2;
+  const uint32_t base = 16u * (uint32_t)(c & 1);
+  return ScaleSel{hi ? base + 2u : base, hi ? 0x3030u : 0x3F3Fu, base, hi ? 0x0F0Fu : 0u};
+}
+
+// B operands of one weight row for one slice: header h, quant bytes q (16g..16g+15 of group c).
+// Low nibbles: ds0 * n - dmin*m0.  High nibbles are kept in place (16 n) and scaled by ds1 / 16,
+// an exact power-of-two step, so the fma rounds d*sc*n - dmin*m exactly once.
+template <int VAR>
+__device__ inline void dequant_row(const u32x4& h, const u32x4& q, const ScaleSel& sel, i32x4_t (&b)[4]) {
+  const uint32_t scp = ((h.y >> sel.sa) & sel.ma) | ((h.w >> sel.sb) & sel.mb);
+  const uint32_t mp = ((h.z >> sel.sa) & sel.ma) | ((h.w >> (sel.sb + 4u)) & sel.mb);
+  const float d = f16lo(h.x), dmin = f16hi(h.x);
+  const float ds0 = d * ub(scp, 0), ds1 = d * ub(scp, 1) * 0.0625f;
+  const float dm0 = -(dmin * ub(mp, 0)), dm1 = -(dmin * ub(mp, 1));
+  b[0] = deq8<VAR>(and_mask<0x0F0F0F0Fu>(q.x), and_mask<0x0F0F0F0Fu>(q.y), ds0, dm0);
+  b[1] = deq8<VAR>(and_mask<0x0F0F0F0Fu>(q.z), and_mask<0x0F0F0F0Fu>(q.w), ds0, dm0);
+  b[2] = deq8<VAR>(and_mask<0xF0F0F0F0u>(q.x), and_mask<0xF0F0F0F0u>(q.y), ds1, dm1);
+  b[3] = deq8<VAR>(and_mask<0xF0F0F0F0u>(q.z), and_mask<0xF0F0F0F0u>(q.w), ds1, dm1);
+}
+
+// Empty asm that claims to modify v: the value is materialised here, so the compiler cannot sink
+// its computation past this point (into the next slice's block).
+__device__ inline void pin(i32x4_t& v) { asm volatile("" : "+v"(v)); }
 
 template <int VAR>
 __device__ inline f32x16_t mfma32(i32x4_t a, i32x4_t b, f32x16_t c) {
@@ -74,143 +168,235 @@ __device__ inline f32x16_t mfma32(i32x4_t a, i32x4_t b, f32x16_t c) {
                                                   0, 0);
 }
 
-// X (fp16) -> the variant's 16-bit type, 8 values.
-template <int VAR>
-__device__ inline uint4 cvt_x8(uint4 v) {
-  if constexpr (VAR == VAR_F16) {
-    return v;
-  } else {
-    uint4 o;
-    const uint32_t in[4] = {v.x, v.y, v.z, v.w};
-    uint32_t r[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = pack2<VAR_BF16>(f16lo(in[i]), f16hi(in[i]));
-    o.x = r[0];
-    o.y = r[1];
-    o.z = r[2];
-    o.w = r[3];
-    return o;
-  }
-}
+// Shared geometry of one launch.
+struct GemmGeo {
+  int M, N, K;
+  uint32_t row_bytes;  // bytes of one weight row
+  int per_split;       // K slices per workgroup along grid z
+  int atomic_out;      // 1: accumulate into a zeroed output (split K)
+};
 
-template <int VAR, int BM, int NT>
+}  // namespace gemm
+
+using namespace gemm;
+
+template <int VAR, int BM>
 __global__ __launch_bounds__(256) void k_qgemm_q4k(const uint8_t* __restrict__ W, const uint16_t* __restrict__ X,
-                                                   float* __restrict__ Y, int M, int N, int K, size_t row_bytes,
-                                                   int slices_per_split, int atomic_out) {
-  constexpr int MT = BM / 32;
-  constexpr int BN = 4 * 32 * NT;
-  constexpr int XS = 64 + 8;               // LDS row pitch in halves (144 bytes)
-  constexpr int XCH = BM * 8;              // 16-byte chunks of one X slice
-  constexpr int XLD = (XCH + 255) / 256;   // per thread
-  __shared__ __attribute__((aligned(16))) uint16_t xl[2][BM * XS];
+                                                   float* __restrict__ Y, GemmGeo geo) {
+  constexpr int MT = BM / 32;         // 32-token A tiles (per wave: all BM tokens)
+  constexpr int XI = BM / 32;         // X copies per wave per slice (BM*128 bytes / 4 waves / 1 KB)
+  constexpr int WI = 3;               // W copies per wave per slice (1 KB headers + 2 KB quant bytes)
+  constexpr int XSTAGE = BM * 128;    // bytes of one X slice
+  static_assert(MT <= 8 && XI <= 8, "tile too large");
+  __shared__ __attribute__((aligned(1024))) uint8_t xs[3 * XSTAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t ws[3 * kWStage];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int M = geo.M, N = geo.N, K = geo.K;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ln = lane & 31, g = lane >> 5;
-  const int m0 = blockIdx.y * BM;
-  const int nw = blockIdx.x * BN + wave * 32 * NT;  // first weight row of this wave
+  const int n0 = blockIdx.x * kBN, m0 = blockIdx.y * BM;
   const int nsl = K / 64;
-  const int kb0 = blockIdx.z * slices_per_split;
-  const int kb1 = min(nsl, kb0 + slices_per_split);
+  const int kb0 = blockIdx.z * geo.per_split;
+  const int kb1 = min(nsl, kb0 + geo.per_split);
   if (kb0 >= kb1) return;
 
-  f32x16_t acc[MT][NT];
+  // Copy descriptors: rows past M or N read as zeros (buffer range check).
+  const uint32_t xrow_bytes = (uint32_t)K * 2u;
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(X + (size_t)m0 * K), (short)0, (int)((uint32_t)min(BM, M - m0) * xrow_bytes), (int)kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(W + (size_t)n0 * geo.row_bytes), (short)0, (int)((uint32_t)min(kBN, N - n0) * geo.row_bytes),
+      (int)kRsrcWord3);
+  // X copy i of this wave: chunk q = (wave*XI + i)*64 + lane -> row q/8, LDS slot q%8 holds global
+  // chunk slot ^ swz(row).
+  // (arrays captured by the lambdas below have a fixed size: clang drops the host stub of a kernel
+  // template whose lambdas capture an array sized by a template parameter)
+  uint32_t xoff[8];
+#pragma unroll
+  for (int i = 0; i < XI; ++i) {
+    const uint32_t q = (uint32_t)((wave * XI + i) * 64 + lane), r = q >> 3, p = q & 7u;
+    xoff[i] = r * xrow_bytes + 16u * (p ^ xswz(r));
+  }
+  // W copies of this wave (its own rows 64w..64w+63): headers (row = 64w + lane), then two quant
+  // copies (row = 64w + 32i + lane/2, LDS slot lane%2 holds global chunk slot ^ qswz(row)).
+  const uint32_t woff_h = (uint32_t)(64 * wave + lane) * geo.row_bytes;
+  uint32_t woff_q[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const uint32_t r = (uint32_t)(64 * wave + 32 * i + (lane >> 1)), p = (uint32_t)lane & 1u;
+    woff_q[i] = r * geo.row_bytes + 16u + 16u * (p ^ qswz(r));
+  }
+  QVX_LDS uint8_t* xs_l = (QVX_LDS uint8_t*)xs;
+  QVX_LDS uint8_t* ws_l = (QVX_LDS uint8_t*)ws;
+
+  auto issue_x = [&](int kb) {
+    QVX_LDS uint8_t* dst = xs_l + (kb % 3) * XSTAGE + wave * XI * 1024;
+#pragma unroll
+    for (int i = 0; i < XI; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, dst + i * 1024, 16, xoff[i], (uint32_t)kb * 128u, 0, 0);
+  };
+  auto issue_w = [&](int kb) {
+    const uint32_t sbo = (uint32_t)(kb >> 2) * 144u;
+    QVX_LDS uint8_t* st = ws_l + (kb % 3) * kWStage;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, st + wave * 1024, 16, woff_h, sbo, 0, 0);
+    const uint32_t qo = sbo + 32u * (uint32_t)(kb & 3);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, st + 4096 + (2 * wave + i) * 1024, 16, woff_q[i], qo, 0, 0);
+  };
+
+  // LDS read addresses.  A: row ln of each 32-token tile i (+4096 i), chunk kc_s ^ swz(ln).
+  const uint32_t xs_base = (uint32_t)(uintptr_t)xs_l;
+  const uint32_t ws_base = (uint32_t)(uintptr_t)ws_l;
+  const uint32_t sw = xswz((uint32_t)ln);
+  uint32_t a_rel[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const uint32_t kc = 4u * (uint32_t)(s >> 1) + 2u * (uint32_t)g + (uint32_t)(s & 1);
+    a_rel[s] = (uint32_t)ln * 128u + 16u * (kc ^ sw);
+  }
+  // B: this lane's weight rows 64w + 32j + ln: header, quant bytes 16g..16g+15.
+  uint32_t h_rel[2], q_rel[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const uint32_t r = (uint32_t)(64 * wave + 32 * j + ln);
+    h_rel[j] = 16u * r;
+    q_rel[j] = 4096u + 32u * r + 16u * ((uint32_t)g ^ qswz(r));
+  }
+
+  f32x16_t acc[8][2];  // rows >= MT unused
 #pragma unroll
   for (int i = 0; i < MT; ++i)
 #pragma unroll
-    for (int j = 0; j < NT; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-  uint4 xr[XLD];
-  uint4 wq[NT], wh[NT];
-
-  auto load_x = [&](int kb) {
-#pragma unroll
-    for (int j = 0; j < XLD; ++j) {
-      const int q = tid + 256 * j;
-      const int row = q >> 3, part = q & 7;
-      uint4 v = {0u, 0u, 0u, 0u};
-      if (q < XCH && m0 + row < M)
-        v = *reinterpret_cast<const uint4*>(X + (size_t)(m0 + row) * K + (size_t)kb * 64 + 8 * part);
-      xr[j] = v;
-    }
-  };
-  auto store_x = [&](int buf) {
-#pragma unroll
-    for (int j = 0; j < XLD; ++j) {
-      const int q = tid + 256 * j;
-      const int row = q >> 3, part = q & 7;
-      if (q < XCH) *reinterpret_cast<uint4*>(&xl[buf][row * XS + 8 * part]) = cvt_x8<VAR>(xr[j]);
-    }
-  };
-  auto load_w = [&](int kb) {
-    const int sb = kb >> 2, c = kb & 3;
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      const int n = nw + 32 * j + ln;
-      uint4 q = {0u, 0u, 0u, 0u}, h = {0u, 0u, 0u, 0u};
-      if (n < N) {
-        const uint8_t* blk = W + (size_t)n * row_bytes + (size_t)sb * 144;
-        h = *reinterpret_cast<const uint4*>(blk);
-        q = *reinterpret_cast<const uint4*>(blk + 16 + 32 * c + 16 * g);
-      }
-      wq[j] = q;
-      wh[j] = h;
-    }
+  // W reads of slice kb (this lane's two rows: header, quant bytes) into r.
+  auto read_w = [&](int kb, u32x4 (&r)[4]) {
+    const uint32_t st = ws_base + (uint32_t)(kb % 3) * kWStage;
+    r[0] = lds_read16(st + h_rel[0]);
+    r[1] = lds_read16(st + q_rel[0]);
+    r[2] = lds_read16(st + h_rel[1]);
+    r[3] = lds_read16(st + q_rel[1]);
   };
 
-  load_x(kb0);
-  load_w(kb0);
-  store_x(0);
-  for (int kb = kb0; kb < kb1; ++kb) {
-    const int buf = (kb - kb0) & 1;
-    __syncthreads();
-    // B operands of this slice from the registers loaded one slice ago.
-    i32x4_t bfrag[NT][4];
-    const int c = kb & 3;
+  // Wait for the copies of slice kb and publish them: X(kb) and W(kb+1) were issued two slices
+  // earlier, the copies issued one slice earlier may still fly.
+  auto sync_slice = [&](int kb) {
+    if (kb + 2 < kb1)
+      wait_vm<XI + WI>();
+    else if (kb + 1 < kb1)
+      wait_vm<XI>();
+    else
+      wait_vm<0>();
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS reads are done
+    __builtin_amdgcn_s_barrier();
+  };
+
+  // One slice: MFMAs of slice kb with B operands bc, dequantisation of slice kb+1 into bn (on the
+  // last slice it reads a stale stage and the result is unused).  One basic block, so the VALU work
+  // interleaves with the MFMAs.
+  auto slice = [&](int kb, const i32x4_t (&bc)[2][4], i32x4_t (&bn)[2][4]) {
+    const uint32_t xb = xs_base + (uint32_t)(kb % 3) * XSTAGE;
+    u32x4 a[2][MT], wq[4];
 #pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      uint32_t scp, mp;
-      q4k_pairs(wh[j], c, scp, mp);
-      const float d = f16lo(wh[j].x), dmin = f16hi(wh[j].x);
-      const float ds0 = d * (float)(scp & 0xFFu), ds1 = d * (float)(scp >> 8);
-      const float dm0 = -(dmin * (float)(mp & 0xFFu)), dm1 = -(dmin * (float)(mp >> 8));
-      const uint32_t q0 = wq[j].x, q1 = wq[j].y, q2 = wq[j].z, q3 = wq[j].w;
-      bfrag[j][0] = deq8<VAR>(q0, q1, ds0, dm0);
-      bfrag[j][1] = deq8<VAR>(q2, q3, ds0, dm0);
-      bfrag[j][2] = deq8<VAR>(q0 >> 4, q1 >> 4, ds1, dm1);
-      bfrag[j][3] = deq8<VAR>(q2 >> 4, q3 >> 4, ds1, dm1);
-    }
-    if (kb + 1 < kb1) {
-      load_x(kb + 1);
-      load_w(kb + 1);
-    }
+    for (int i = 0; i < MT; ++i) a[0][i] = lds_read16(xb + a_rel[0] + 4096u * i);
+    read_w(kb + 1, wq);
+    lds_wait(a[0], wq);
+#pragma unroll
+    for (int i = 0; i < MT; ++i) a[1][i] = lds_read16(xb + a_rel[1] + 4096u * i);
+    const ScaleSel sel = scale_sel((kb + 1) & 3);
+    dequant_row<VAR>(wq[0], wq[1], sel, bn[0]);
+    dequant_row<VAR>(wq[2], wq[3], sel, bn[1]);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const int kof = 32 * (s >> 1) + 16 * g + 8 * (s & 1);
 #pragma unroll
-      for (int i = 0; i < MT; ++i) {
-        const i32x4_t a = *reinterpret_cast<const i32x4_t*>(&xl[buf][(32 * i + ln) * XS + kof]);
+      for (int i = 0; i < MT; ++i)
 #pragma unroll
-        for (int j = 0; j < NT; ++j) acc[i][j] = mfma32<VAR>(a, bfrag[j][s], acc[i][j]);
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = mfma32<VAR>(__builtin_bit_cast(i32x4_t, a[s & 1][i]), bc[j][s], acc[i][j]);
+      if (s < 3) {
+        lds_wait(a[(s + 1) & 1]);
+        if (s < 2) {
+#pragma unroll
+          for (int i = 0; i < MT; ++i) a[s & 1][i] = lds_read16(xb + a_rel[s + 2] + 4096u * i);
+        }
       }
     }
-    if (kb + 1 < kb1) store_x(buf ^ 1);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) pin(bn[j][s]);
+    // 4*MT*2 MFMAs of 8 passes each; spread the ~200 VALU of the dequantisation between them.
+#pragma unroll
+    for (int k = 0; k < 8 * MT; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 200 / (8 * MT) + 1, 0);
+    }
+  };
+
+  // Prologue: group A = W(kb0), X(kb0), W(kb0+1); group B = X(kb0+1), W(kb0+2).
+  issue_w(kb0);
+  issue_x(kb0);
+  if (kb0 + 1 < kb1) issue_w(kb0 + 1);
+  if (kb0 + 1 < kb1) issue_x(kb0 + 1);
+  if (kb0 + 2 < kb1) issue_w(kb0 + 2);
+  if (kb0 + 2 < kb1)
+    wait_vm<XI + WI>();
+  else if (kb0 + 1 < kb1)
+    wait_vm<XI>();
+  else
+    wait_vm<0>();
+  __builtin_amdgcn_s_barrier();
+
+  i32x4_t b0[2][4], b1[2][4];
+  {
+    u32x4 wq[4];
+    read_w(kb0, wq);
+    lds_wait(wq);
+    const ScaleSel sel = scale_sel(kb0 & 3);
+    dequant_row<VAR>(wq[0], wq[1], sel, b0[0]);
+    dequant_row<VAR>(wq[2], wq[3], sel, b0[1]);
+  }
+
+  // Stages (kb+2)%3 (X) and kb%3 (W) are free once every wave is past slice kb-1.
+  auto issue_next = [&](int kb) {
+    if (kb + 2 < kb1) issue_x(kb + 2);
+    if (kb + 3 < kb1) issue_w(kb + 3);
+  };
+  int kb = kb0;
+  issue_next(kb);
+  slice(kb, b0, b1);
+  ++kb;
+  for (; kb + 1 < kb1; kb += 2) {
+    sync_slice(kb);
+    issue_next(kb);
+    slice(kb, b1, b0);
+    sync_slice(kb + 1);
+    issue_next(kb + 1);
+    slice(kb + 1, b0, b1);
+  }
+  if (kb < kb1) {
+    sync_slice(kb);
+    issue_next(kb);
+    slice(kb, b1, b0);
   }
 
   // C layout of v_mfma_f32_32x32x*: element e of lane l is row 8*(e/4) + 4*(l/32) + e%4, col l%32.
 #pragma unroll
   for (int i = 0; i < MT; ++i)
 #pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      const int n = nw + 32 * j + ln;
+    for (int j = 0; j < 2; ++j) {
+      const int n = n0 + 64 * wave + 32 * j + ln;
       if (n >= N) continue;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int m = m0 + 32 * i + 8 * (e >> 2) + 4 * g + (e & 3);
         if (m < M) {
           float* dst = Y + (size_t)m * N + n;
-          if (atomic_out)
+          if (geo.atomic_out)
             unsafeAtomicAdd(dst, acc[i][j][e]);
           else
             *dst = acc[i][j][e];
@@ -219,18 +405,66 @@ __global__ __launch_bounds__(256) void k_qgemm_q4k(const uint8_t* __restrict__ W
     }
 }
 
+// fp16 -> bf16 (round to nearest even), 8 values a thread.
+__global__ __launch_bounds__(256) void k_f16_to_bf16(const uint4* __restrict__ x, uint4* __restrict__ y, size_t n8) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n8) return;
+  const uint4 v = x[i];
+  y[i] = make_uint4(pack2<VAR_BF16>(f16lo(v.x), f16hi(v.x)), pack2<VAR_BF16>(f16lo(v.y), f16hi(v.y)),
+                    pack2<VAR_BF16>(f16lo(v.z), f16hi(v.z)), pack2<VAR_BF16>(f16lo(v.w), f16hi(v.w)));
+}
+
 __global__ __launch_bounds__(256) void k_zero_f32(float* __restrict__ p, size_t n) {
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (i < n) p[i] = 0.0f;
 }
+
+namespace {
+
+// One stream-ordered memory pool per device for the GEMM temporaries, created on first use and
+// kept for the life of the process; freed blocks stay in the pool for the next call.
+std::mutex g_pool_mu;
+hipMemPool_t g_pool[64];
+
+hipMemPool_t device_pool() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lk(g_pool_mu);
+  if (!g_pool[dev]) {
+    hipMemPoolProps props{};
+    props.allocType = hipMemAllocationTypePinned;
+    props.location.type = hipMemLocationTypeDevice;
+    props.location.id = dev;
+    hipMemPool_t p = nullptr;
+    if (hipMemPoolCreate(&p, &props) != hipSuccess) return nullptr;
+    uint64_t keep = ~0ull;
+    (void)hipMemPoolSetAttribute(p, hipMemPoolAttrReleaseThreshold, &keep);
+    g_pool[dev] = p;
+  }
+  return g_pool[dev];
+}
+
+}  // namespace
 
 // Zero fill by kernel (no memset nodes, so callers may capture it in a HIP graph).
 void launch_zero(float* p, size_t n, hipStream_t s) {
   if (n) k_zero_f32<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(p, n);
 }
 
+// Stream-ordered temporary from the library's pool (nullptr on failure) and its release.
+void* gemm_temp_alloc(size_t bytes, hipStream_t s) {
+  hipMemPool_t pool = device_pool();
+  if (!pool) return nullptr;
+  void* p = nullptr;
+  if (hipMallocFromPoolAsync(&p, bytes, pool, s) != hipSuccess) return nullptr;
+  return p;
+}
+void gemm_temp_free(void* p, hipStream_t s) {
+  if (p) (void)hipFreeAsync(p, s);
+}
+
 // ---- per-32 Q8 activation quantiser --------------------------------------------------------------
-// One wave per (row, 64 blocks): lane = block of 32 values; fp32 math as the oracle states it.
+// One thread per block of 32 values; fp32 math as the oracle states it.
 __global__ __launch_bounds__(256) void k_quant_q8(const uint16_t* __restrict__ X, int M, int K, int8_t* __restrict__ q,
                                                   float* __restrict__ scale, int32_t* __restrict__ qsum) {
   const int nb = K / 32;
@@ -282,34 +516,53 @@ int launch_quantize_act_q8(const uint16_t* X, int M, int K, int8_t* q, float* sc
   return 0;
 }
 
-template <int VAR, int BM, int NT>
-static void launch_q4k(float* out, const void* w, const uint16_t* X, int M, int N, int K, hipStream_t s) {
-  constexpr int BN = 4 * 32 * NT;
-  const size_t row_bytes = (size_t)(K / 256) * 144;
+namespace {
+
+template <int VAR, int BM>
+void launch_q4k(float* out, const void* w, const uint16_t* X, int M, int N, int K, hipStream_t s) {
   const int nsl = K / 64;
-  const int tiles = ((N + BN - 1) / BN) * ((M + BM - 1) / BM);
-  // Split K until the grid covers the 256 CUs about twice; each split keeps >= 8 slices.
+  const int tiles = ((N + kBN - 1) / kBN) * ((M + BM - 1) / BM);
+  // Split K until the grid covers the 256 CUs; each split keeps >= 8 slices.
   int splits = 1;
-  while (tiles * splits < 512 && nsl / (splits * 2) >= 8) splits *= 2;
+  while (tiles * splits < 256 && nsl / (splits * 2) >= 8) splits *= 2;
   const int per = (nsl + splits - 1) / splits;
   splits = (nsl + per - 1) / per;
   if (splits > 1) launch_zero(out, (size_t)M * N, s);
-  dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM, splits);
-  k_qgemm_q4k<VAR, BM, NT><<<grid, 256, 0, s>>>(static_cast<const uint8_t*>(w), X, out, M, N, K, row_bytes, per,
-                                                 splits > 1 ? 1 : 0);
+  GemmGeo geo{M, N, K, (uint32_t)(K / 256) * 144u, per, splits > 1 ? 1 : 0};
+  dim3 grid((N + kBN - 1) / kBN, (M + BM - 1) / BM, splits);
+  k_qgemm_q4k<VAR, BM><<<grid, 256, 0, s>>>(static_cast<const uint8_t*>(w), X, out, geo);
 }
 
-// Returns a QVX status (0 ok, -1 type, -7 range).
+template <int VAR>
+void launch_var(float* out, const void* w, const uint16_t* X, int M, int N, int K, hipStream_t s) {
+  if (M > 128)
+    launch_q4k<VAR, 256>(out, w, X, M, N, K, s);
+  else
+    launch_q4k<VAR, 128>(out, w, X, M, N, K, s);
+}
+
+}  // namespace
+
+// Returns a QVX status (0 ok, -1 type, -5 HIP, -7 range).
 int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M, int rows, int cols, int variant,
                  hipStream_t s) {
   if (t != T_Q4_K) return -1;
   if ((reinterpret_cast<uintptr_t>(w) & 15u) || (reinterpret_cast<uintptr_t>(X) & 15u)) return -7;
+  // Buffer offsets are 32-bit: a tile's rows must span less than 2 GiB.
+  if ((size_t)256 * (size_t)cols * 2u >= (1u << 31) || (size_t)kBN * (size_t)(cols / 256) * 144u >= (1u << 31))
+    return -7;
   if (variant == VAR_BF16) {
-    launch_q4k<VAR_BF16, 128, 2>(out, w, X, M, rows, cols, s);
+    const size_t n = (size_t)M * (size_t)cols;
+    void* xb = gemm_temp_alloc(n * 2u, s);
+    if (!xb) return -5;
+    k_f16_to_bf16<<<(unsigned)((n / 8 + 255) / 256), 256, 0, s>>>(reinterpret_cast<const uint4*>(X),
+                                                                    static_cast<uint4*>(xb), n / 8);
+    launch_var<VAR_BF16>(out, w, static_cast<const uint16_t*>(xb), M, rows, cols, s);
+    gemm_temp_free(xb, s);
     return 0;
   }
   if (variant == VAR_F16) {
-    launch_q4k<VAR_F16, 128, 2>(out, w, X, M, rows, cols, s);
+    launch_var<VAR_F16>(out, w, X, M, rows, cols, s);
     return 0;
   }
   return -1;  // the int8 variant is not built yet
