@@ -34,6 +34,7 @@
 #include "qvx_common.hpp"
 
 #include <mutex>
+#include <utility>
 
 namespace qvx {
 
@@ -50,7 +51,8 @@ enum { VAR_BF16 = 0, VAR_I8 = 1, VAR_F16 = 2 };
 
 constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit data (gfx9)
 constexpr int kBN = 256;                      // weight rows per workgroup tile
-constexpr int kWStage = kBN * 48;             // LDS bytes of one W slice: headers + quant bytes
+constexpr int kWStage = kBN * 80;             // LDS bytes of one W stage: 256 rows x half a super-block
+constexpr int kWQs = kBN * 16;                // ... of which the headers come first, the quant bytes after
 
 // s_waitcnt vmcnt(N), other counters untouched (gfx9 encoding).
 template <int N>
@@ -65,9 +67,10 @@ __device__ inline u32x4 lds_read16(uint32_t addr) {
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF) : "memory");
   return r;
 }
-// Waits for the LDS reads in flight; the results are operands, so no use moves above the wait.
+// Waits for the LDS reads in flight; the results (the first N of r, then the 4 of w) are operands,
+// so no use moves above the wait.
 template <int N>
-__device__ inline void lds_wait(u32x4 (&r)[N]) {
+__device__ inline void lds_wait(u32x4* r) {
   static_assert(N == 8 || N == 4, "lds_wait arity");
   if constexpr (N == 4) {
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3])::"memory");
@@ -76,18 +79,23 @@ __device__ inline void lds_wait(u32x4 (&r)[N]) {
                  : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7])::"memory");
   }
 }
-__device__ inline void lds_wait(u32x4 (&a)[4], u32x4 (&b)[4]) {
-  asm volatile("s_waitcnt lgkmcnt(0)"
-               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3])::"memory");
-}
-__device__ inline void lds_wait(u32x4 (&a)[8], u32x4 (&b)[4]) {
-  asm volatile("s_waitcnt lgkmcnt(0)"
-               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]), "+v"(a[6]), "+v"(a[7]),
-                 "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3])::"memory");
+template <int N>
+__device__ inline void lds_wait(u32x4* r, u32x4* w) {
+  static_assert(N == 8 || N == 4, "lds_wait arity");
+  if constexpr (N == 4) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3])::"memory");
+  } else {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]),
+                   "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3])::"memory");
+  }
 }
 
 __device__ inline uint32_t xswz(uint32_t r) { return (r ^ ((r >> 3) & 3u)) & 7u; }
-__device__ inline uint32_t qswz(uint32_t r) { return ((r >> 2) ^ (r >> 3)) & 1u; }
+// Quant-byte rows of a W stage are 64 bytes apart; 16-byte chunk p of row r sits at slot p ^ qswz(r),
+// which keeps the reads of 16 consecutive rows (one chunk each) on distinct banks.
+__device__ inline uint32_t qswz(uint32_t r) { return ((r >> 1) ^ (r >> 3)) & 3u; }
 
 // Two fp32 -> one dword of two 16-bit values (round to nearest even).
 template <int VAR> __device__ inline uint32_t pack2(float a, float b);
@@ -114,18 +122,6 @@ __device__ inline i32x4_t deq8(uint32_t w0, uint32_t w1, float ds, float dm) {
   return o;
 }
 
-// a & mask as an opaque instruction: keeps the masked dword whole, so each byte converts with one
-// v_cvt_f32_ubyteN instead of being re-extracted per element.
-template <uint32_t MASK>
-__device__ inline uint32_t and_mask(uint32_t a) {
-  uint32_t r;
-  asm("v_and_b32 %0, %1, %2" : "=v"(r) : "i"(MASK), "v"(a));
-  return r;
-}
-
-// B operands of one weight row for one slice: header h, quant bytes q (16g..16g+15 of group c).
-// Low nibbles: ds0 * n - dmin*m0.  High nibbles are kept in place (16 n) and scaled by ds1 / 16,
-// an exact power-of-two step, so the fma rounds d*sc*n - dmin*m exactly once.
 // Shift / mask set that extracts the 6-bit (scale, min) pairs of sub-blocks 2c, 2c+1 from a Q4_K
 // header without branches: pair = ((word_a >> sa) & ma) | ((h.w >> sb) & mb), word_a = h.y for the
 // scales, h.z for the mins (the min nibbles sit 4 bits higher in h.w).  c is uniform: scalar math.
@@ -142,16 +138,17 @@ __device__ inline ScaleSel scale_sel(int c) {
 // Low nibbles: ds0 * n - dmin*m0.  High nibbles are kept in place (16 n) and scaled by ds1 / 16,
 // an exact power-of-two step, so the fma rounds d*sc*n - dmin*m exactly once.
 template <int VAR>
-__device__ inline void dequant_row(const u32x4& h, const u32x4& q, const ScaleSel& sel, i32x4_t (&b)[4]) {
+__device__ inline void dequant_row(const u32x4& h, const u32x4& q, const ScaleSel& sel, uint32_t mlo, uint32_t mhi,
+                                   i32x4_t (&b)[4]) {
   const uint32_t scp = ((h.y >> sel.sa) & sel.ma) | ((h.w >> sel.sb) & sel.mb);
   const uint32_t mp = ((h.z >> sel.sa) & sel.ma) | ((h.w >> (sel.sb + 4u)) & sel.mb);
   const float d = f16lo(h.x), dmin = f16hi(h.x);
   const float ds0 = d * ub(scp, 0), ds1 = d * ub(scp, 1) * 0.0625f;
   const float dm0 = -(dmin * ub(mp, 0)), dm1 = -(dmin * ub(mp, 1));
-  b[0] = deq8<VAR>(and_mask<0x0F0F0F0Fu>(q.x), and_mask<0x0F0F0F0Fu>(q.y), ds0, dm0);
-  b[1] = deq8<VAR>(and_mask<0x0F0F0F0Fu>(q.z), and_mask<0x0F0F0F0Fu>(q.w), ds0, dm0);
-  b[2] = deq8<VAR>(and_mask<0xF0F0F0F0u>(q.x), and_mask<0xF0F0F0F0u>(q.y), ds1, dm1);
-  b[3] = deq8<VAR>(and_mask<0xF0F0F0F0u>(q.z), and_mask<0xF0F0F0F0u>(q.w), ds1, dm1);
+  b[0] = deq8<VAR>(q.x & mlo, q.y & mlo, ds0, dm0);
+  b[1] = deq8<VAR>(q.z & mlo, q.w & mlo, ds0, dm0);
+  b[2] = deq8<VAR>(q.x & mhi, q.y & mhi, ds1, dm1);
+  b[3] = deq8<VAR>(q.z & mhi, q.w & mhi, ds1, dm1);
 }
 
 // Empty asm that claims to modify v: the value is materialised here, so the compiler cannot sink
@@ -174,20 +171,30 @@ struct GemmGeo {
   uint32_t row_bytes;  // bytes of one weight row
   int per_split;       // K slices per workgroup along grid z
   int atomic_out;      // 1: accumulate into a zeroed output (split K)
+  uint32_t mask_lo;    // 0x0F0F0F0F and 0xF0F0F0F0, passed at run time: with compile-time masks the
+  uint32_t mask_hi;    // compiler re-extracts every nibble (bfe) instead of one AND per dword
+  uint32_t m_b0;       // 0x000F000F: bits 0-3 of each 16-bit half (fp16 mantissa bits 0-3)
+  uint32_t m_b4;       // 0x00F000F0: bits 4-7 of each 16-bit half (fp16 mantissa bits 4-7)
 };
 
 }  // namespace gemm
 
 using namespace gemm;
 
+// Reads A fragments i = 0..MT-1 (32-token tiles 4096 bytes apart) with immediate offsets.
+template <int... I>
+__device__ inline void read_frags(uint32_t addr, u32x4* a, std::integer_sequence<int, I...>) {
+  ((a[I] = lds_read16<4096 * I>(addr)), ...);
+}
+
 template <int VAR, int BM>
 __global__ __launch_bounds__(256) void k_qgemm_q4k(const uint8_t* __restrict__ W, const uint16_t* __restrict__ X,
                                                    float* __restrict__ Y, GemmGeo geo) {
   constexpr int MT = BM / 32;         // 32-token A tiles (per wave: all BM tokens)
   constexpr int XI = BM / 32;         // X copies per wave per slice (BM*128 bytes / 4 waves / 1 KB)
-  constexpr int WI = 3;               // W copies per wave per slice (1 KB headers + 2 KB quant bytes)
+  constexpr int WI = 5;               // W copies per wave per half super-block (1 KB headers, 4 KB quants)
   constexpr int XSTAGE = BM * 128;    // bytes of one X slice
-  static_assert(MT <= 8 && XI <= 8, "tile too large");
+  static_assert(MT <= 8, "tile too large");
   __shared__ __attribute__((aligned(1024))) uint8_t xs[3 * XSTAGE];
   __shared__ __attribute__((aligned(1024))) uint8_t ws[3 * kWStage];
 
@@ -197,7 +204,7 @@ __global__ __launch_bounds__(256) void k_qgemm_q4k(const uint8_t* __restrict__ W
   const int ln = lane & 31, g = lane >> 5;
   const int n0 = blockIdx.x * kBN, m0 = blockIdx.y * BM;
   const int nsl = K / 64;
-  const int kb0 = blockIdx.z * geo.per_split;
+  const int kb0 = blockIdx.z * geo.per_split;  // per_split is a multiple of 4: splits start a super-block
   const int kb1 = min(nsl, kb0 + geo.per_split);
   if (kb0 >= kb1) return;
 
@@ -208,42 +215,46 @@ __global__ __launch_bounds__(256) void k_qgemm_q4k(const uint8_t* __restrict__ W
   const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(W + (size_t)n0 * geo.row_bytes), (short)0, (int)((uint32_t)min(kBN, N - n0) * geo.row_bytes),
       (int)kRsrcWord3);
-  // X copy i of this wave: chunk q = (wave*XI + i)*64 + lane -> row q/8, LDS slot q%8 holds global
-  // chunk slot ^ swz(row).
   // (arrays captured by the lambdas below have a fixed size: clang drops the host stub of a kernel
   // template whose lambdas capture an array sized by a template parameter)
+  // X copy i of this wave: chunk q = (wave*XI + i)*64 + lane -> row q/8, LDS slot q%8 holds global
+  // chunk slot ^ swz(row).
   uint32_t xoff[8];
 #pragma unroll
   for (int i = 0; i < XI; ++i) {
     const uint32_t q = (uint32_t)((wave * XI + i) * 64 + lane), r = q >> 3, p = q & 7u;
     xoff[i] = r * xrow_bytes + 16u * (p ^ xswz(r));
   }
-  // W copies of this wave (its own rows 64w..64w+63): headers (row = 64w + lane), then two quant
-  // copies (row = 64w + 32i + lane/2, LDS slot lane%2 holds global chunk slot ^ qswz(row)).
+  // W copies of this wave's rows 64w..64w+63 for half super-block hb (quant bytes 64h..64h+63 of
+  // super-block hb/2, h = hb%2): one header copy (row 64w + lane, LDS 16 r), then four quant copies
+  // (row 64w + 16i + lane/4, LDS slot lane%4 of the row's 64 bytes holds chunk slot ^ qswz(row)).
   const uint32_t woff_h = (uint32_t)(64 * wave + lane) * geo.row_bytes;
-  uint32_t woff_q[2];
+  uint32_t woff[4];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const uint32_t r = (uint32_t)(64 * wave + 32 * i + (lane >> 1)), p = (uint32_t)lane & 1u;
-    woff_q[i] = r * geo.row_bytes + 16u + 16u * (p ^ qswz(r));
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t r = (uint32_t)(64 * wave + 16 * i + (lane >> 2)), slot = (uint32_t)lane & 3u;
+    woff[i] = r * geo.row_bytes + 16u + 16u * (slot ^ qswz(r));
   }
   QVX_LDS uint8_t* xs_l = (QVX_LDS uint8_t*)xs;
   QVX_LDS uint8_t* ws_l = (QVX_LDS uint8_t*)ws;
 
-  auto issue_x = [&](int kb) {
+  // Copy i of X(kb) (one 1 KB instruction).
+  auto issue_x1 = [&](int kb, int i) {
     QVX_LDS uint8_t* dst = xs_l + (kb % 3) * XSTAGE + wave * XI * 1024;
-#pragma unroll
-    for (int i = 0; i < XI; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, dst + i * 1024, 16, xoff[i], (uint32_t)kb * 128u, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, dst + i * 1024, 16, xoff[i], (uint32_t)kb * 128u, 0, 0);
   };
-  auto issue_w = [&](int kb) {
-    const uint32_t sbo = (uint32_t)(kb >> 2) * 144u;
-    QVX_LDS uint8_t* st = ws_l + (kb % 3) * kWStage;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, st + wave * 1024, 16, woff_h, sbo, 0, 0);
-    const uint32_t qo = sbo + 32u * (uint32_t)(kb & 3);
+  auto issue_x = [&](int kb) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, st + 4096 + (2 * wave + i) * 1024, 16, woff_q[i], qo, 0, 0);
+    for (int i = 0; i < XI; ++i) issue_x1(kb, i);
+  };
+  auto issue_w = [&](int hb) {
+    QVX_LDS uint8_t* st = ws_l + (hb % 3) * kWStage;
+    const uint32_t sbo = (uint32_t)(hb >> 1) * 144u;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, st + wave * 1024, 16, woff_h, sbo, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, st + kWQs + (4 * wave + i) * 1024, 16, woff[i],
+                                               sbo + 64u * (uint32_t)(hb & 1), 0, 0);
   };
 
   // LDS read addresses.  A: row ln of each 32-token tile i (+4096 i), chunk kc_s ^ swz(ln).
@@ -256,13 +267,15 @@ __global__ __launch_bounds__(256) void k_qgemm_q4k(const uint8_t* __restrict__ W
     const uint32_t kc = 4u * (uint32_t)(s >> 1) + 2u * (uint32_t)g + (uint32_t)(s & 1);
     a_rel[s] = (uint32_t)ln * 128u + 16u * (kc ^ sw);
   }
-  // B: this lane's weight rows 64w + 32j + ln: header, quant bytes 16g..16g+15.
-  uint32_t h_rel[2], q_rel[2];
+  // B: this lane's weight rows r = 64w + 32j + ln: header at 16 r; quant bytes 16g..16g+15 of
+  // group c (chunk 2(c%2) + g of the half super-block) at kWQs + 64 r + 16 (chunk ^ qswz(r)).
+  uint32_t h_rel[2], q_rel[2][2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const uint32_t r = (uint32_t)(64 * wave + 32 * j + ln);
     h_rel[j] = 16u * r;
-    q_rel[j] = 4096u + 32u * r + 16u * ((uint32_t)g ^ qswz(r));
+#pragma unroll
+    for (int c = 0; c < 2; ++c) q_rel[j][c] = (uint32_t)kWQs + 64u * r + 16u * ((2u * c + (uint32_t)g) ^ qswz(r));
   }
 
   f32x16_t acc[8][2];  // rows >= MT unused
@@ -275,114 +288,181 @@ __global__ __launch_bounds__(256) void k_qgemm_q4k(const uint8_t* __restrict__ W
 
   // W reads of slice kb (this lane's two rows: header, quant bytes) into r.
   auto read_w = [&](int kb, u32x4 (&r)[4]) {
-    const uint32_t st = ws_base + (uint32_t)(kb % 3) * kWStage;
+    const uint32_t st = ws_base + (uint32_t)((kb >> 1) % 3) * kWStage;
+    const int c = kb & 1;
     r[0] = lds_read16(st + h_rel[0]);
-    r[1] = lds_read16(st + q_rel[0]);
+    r[1] = lds_read16(st + (c ? q_rel[0][1] : q_rel[0][0]));
     r[2] = lds_read16(st + h_rel[1]);
-    r[3] = lds_read16(st + q_rel[1]);
+    r[3] = lds_read16(st + (c ? q_rel[1][1] : q_rel[1][0]));
   };
 
-  // Wait for the copies of slice kb and publish them: X(kb) and W(kb+1) were issued two slices
-  // earlier, the copies issued one slice earlier may still fly.
-  auto sync_slice = [&](int kb) {
-    if (kb + 2 < kb1)
-      wait_vm<XI + WI>();
-    else if (kb + 1 < kb1)
-      wait_vm<XI>();
-    else
-      wait_vm<0>();
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS reads are done
-    __builtin_amdgcn_s_barrier();
+  // MFMA pair i of K16 step s: token tile i times both weight tiles.
+  auto mfma_pair = [&](int i, int s, const u32x4& a, const i32x4_t (&b)[2][4]) {
+    acc[i][0] = mfma32<VAR>(__builtin_bit_cast(i32x4_t, a), b[0][s], acc[i][0]);
+    acc[i][1] = mfma32<VAR>(__builtin_bit_cast(i32x4_t, a), b[1][s], acc[i][1]);
   };
 
-  // One slice: MFMAs of slice kb with B operands bc, dequantisation of slice kb+1 into bn (on the
-  // last slice it reads a stale stage and the result is unused).  One basic block, so the VALU work
-  // interleaves with the MFMAs.
-  auto slice = [&](int kb, const i32x4_t (&bc)[2][4], i32x4_t (&bn)[2][4]) {
+  // Dequantisation of the next slice in 18 pieces of ~9 VALU, placed between MFMA pairs by hand:
+  // piece 9j = scales of row j, pieces 9j+1+u = dwords 2h, 2h+1 of bn[j][u/2] (h = u%2), converted
+  // from quant dword (u/2 % 2)*2 + h, low nibbles for u < 4, high nibbles after.
+  // A nibble n is dropped into the mantissa of the fp16 1024 (bits 0x6400) at bit b = 0 or 4 (one
+  // bitop3 for the two nibbles of a 16-bit half pair, after a shift for the odd bytes): the half is
+  // exactly 1024 + 2^b n, and v_fma_mix_f32 evaluates (ds / 2^b) * (1024 + 2^b n) +
+  // (dm - 1024 ds / 2^b) = ds * n + dm with one rounding (the bias itself rounds once, ~2^-14 ds:
+  // far below the bf16 / fp16 rounding that follows).  Byte k of a quant dword:
+  //   low nibble,  k even: (w      & 0x000F000F) -> n       low nibble,  k odd: (w >> 4 & 0x00F000F0) -> 16 n
+  //   high nibble, k even: (w      & 0x00F000F0) -> 16 n    high nibble, k odd: (w >> 8 & 0x00F000F0) -> 16 n
+  struct DeqState {
+    u32x4 h[2], q[2];
+    float s[2][3], b[2][3];  // scale, bias per row: low even, low odd, high
+    ScaleSel sel;
+  };
+  const uint32_t k1024 = 0x64006400u;  // two fp16 1024.0
+  auto piece = [&](int p, DeqState& st, i32x4_t (&bn)[2][4]) {
+    const int j = p / 9, r = p % 9;
+    if (r == 0) {
+      const u32x4& h = st.h[j];
+      const uint32_t scp = ((h.y >> st.sel.sa) & st.sel.ma) | ((h.w >> st.sel.sb) & st.sel.mb);
+      const uint32_t mp = ((h.z >> st.sel.sa) & st.sel.ma) | ((h.w >> (st.sel.sb + 4u)) & st.sel.mb);
+      const float d = f16lo(h.x), dmin = f16hi(h.x);
+      const float ds0 = d * ub(scp, 0), ds1 = d * ub(scp, 1);
+      const float dm0 = -(dmin * ub(mp, 0)), dm1 = -(dmin * ub(mp, 1));
+      st.s[j][0] = ds0;
+      st.s[j][1] = ds0 * 0.0625f;
+      st.s[j][2] = ds1 * 0.0625f;
+      st.b[j][0] = __builtin_fmaf(-1024.0f, ds0, dm0);
+      st.b[j][1] = __builtin_fmaf(-64.0f, ds0, dm0);
+      st.b[j][2] = __builtin_fmaf(-64.0f, ds1, dm1);
+    } else {
+      const int u = r - 1, sp = u >> 1, hh = u & 1, w = (sp & 1) * 2 + hh;
+      const uint32_t src = w == 0 ? st.q[j].x : w == 1 ? st.q[j].y : w == 2 ? st.q[j].z : st.q[j].w;
+      const bool lo = sp < 2;
+      const int ke = lo ? 0 : 2, ko = lo ? 1 : 2;
+      const uint32_t e = __builtin_amdgcn_bitop3_b32(src, lo ? geo.m_b0 : geo.m_b4, k1024, 0xEA);
+      const uint32_t o = __builtin_amdgcn_bitop3_b32(src >> (lo ? 4 : 8), geo.m_b4, k1024, 0xEA);
+      const half2_t he = __builtin_bit_cast(half2_t, e), ho = __builtin_bit_cast(half2_t, o);
+      bn[j][sp][2 * hh] = (int)pack2<VAR>(__builtin_fmaf((float)he.x, st.s[j][ke], st.b[j][ke]),
+                                          __builtin_fmaf((float)ho.x, st.s[j][ko], st.b[j][ko]));
+      bn[j][sp][2 * hh + 1] = (int)pack2<VAR>(__builtin_fmaf((float)he.y, st.s[j][ke], st.b[j][ke]),
+                                              __builtin_fmaf((float)ho.y, st.s[j][ko], st.b[j][ko]));
+      pin(bn[j][sp]);  // computed here, not sunk towards its use in the next slice
+    }
+  };
+
+  // One slice: MFMAs of slice kb with B operands bc and step-0 A fragments a[0] (read during the
+  // previous slice); dequantisation of slice kb+1 into bn (on the last slice it reads a stale stage
+  // and the result is unused) spread over steps 1-3.  After step 2 the wave holds every A fragment
+  // of slice kb, so the barrier that publishes X(kb+1) and frees stage kb%3 sits there, and the
+  // step-0 fragments of slice kb+1 are read while the step-3 MFMAs run.  Copies run ahead: the
+  // sync of slice kb issues W(kb/2+2) (even kb), step 0 of slice kb copies X(kb+2).
+  // sched_barrier(0) after every MFMA pair keeps this order exactly.
+  auto slice = [&](int kb, const i32x4_t (&bc)[2][4], i32x4_t (&bn)[2][4], u32x4 (&a)[2][8]) {
     const uint32_t xb = xs_base + (uint32_t)(kb % 3) * XSTAGE;
-    u32x4 a[2][MT], wq[4];
-#pragma unroll
-    for (int i = 0; i < MT; ++i) a[0][i] = lds_read16(xb + a_rel[0] + 4096u * i);
-    read_w(kb + 1, wq);
-    lds_wait(a[0], wq);
-#pragma unroll
-    for (int i = 0; i < MT; ++i) a[1][i] = lds_read16(xb + a_rel[1] + 4096u * i);
-    const ScaleSel sel = scale_sel((kb + 1) & 3);
-    dequant_row<VAR>(wq[0], wq[1], sel, bn[0]);
-    dequant_row<VAR>(wq[2], wq[3], sel, bn[1]);
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-#pragma unroll
-      for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = mfma32<VAR>(__builtin_bit_cast(i32x4_t, a[s & 1][i]), bc[j][s], acc[i][j]);
-      if (s < 3) {
-        lds_wait(a[(s + 1) & 1]);
-        if (s < 2) {
-#pragma unroll
-          for (int i = 0; i < MT; ++i) a[s & 1][i] = lds_read16(xb + a_rel[s + 2] + 4096u * i);
-        }
-      }
+    DeqState st;
+    st.sel = scale_sel((kb + 1) & 3);
+    lds_wait<MT>(a[0]);
+    read_frags(xb + a_rel[1], a[1], std::make_integer_sequence<int, MT>{});
+    {
+      u32x4 w4[4];
+      read_w(kb + 1, w4);
+      st.h[0] = w4[0];
+      st.q[0] = w4[1];
+      st.h[1] = w4[2];
+      st.q[1] = w4[3];
     }
+    __builtin_amdgcn_sched_barrier(0);
+    // X(kb+2), one copy after each MFMA pair (the vector memory path takes a steady trickle; a
+    // burst of copies stalls the issuing wave).  Past the last slice the index is clamped: the copy
+    // repeats X(kb1-1) into a stage no slice reads again.
+    const int kx = min(kb + 2, kb1 - 1);
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int i = 0; i < MT; ++i) {
+      mfma_pair(i, 0, a[0][i], bc);
+      if (i < XI) issue_x1(kx, i);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    {
+      u32x4 w4[4] = {st.h[0], st.q[0], st.h[1], st.q[1]};
+      lds_wait<MT>(a[1], w4);
+      st.h[0] = w4[0];
+      st.q[0] = w4[1];
+      st.h[1] = w4[2];
+      st.q[1] = w4[3];
+    }
+    read_frags(xb + a_rel[2], a[0], std::make_integer_sequence<int, MT>{});
+    constexpr int NP = 18;
+    constexpr int PER = (NP + 3 * MT - 1) / (3 * MT);  // pieces per MFMA pair over steps 1-3
 #pragma unroll
-      for (int s = 0; s < 4; ++s) pin(bn[j][s]);
-    // 4*MT*2 MFMAs of 8 passes each; spread the ~200 VALU of the dequantisation between them.
+    for (int i = 0; i < MT; ++i) {
+      mfma_pair(i, 1, a[1][i], bc);
 #pragma unroll
-    for (int k = 0; k < 8 * MT; ++k) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 200 / (8 * MT) + 1, 0);
+      for (int k = 0; k < PER; ++k)
+        if (i * PER + k < NP) piece(i * PER + k, st, bn);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    lds_wait<MT>(a[0]);
+    read_frags(xb + a_rel[3], a[1], std::make_integer_sequence<int, MT>{});
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      mfma_pair(i, 2, a[0][i], bc);
+#pragma unroll
+      for (int k = 0; k < PER; ++k)
+        if ((MT + i) * PER + k < NP) piece((MT + i) * PER + k, st, bn);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    lds_wait<MT>(a[1]);
+    if (kb + 1 < kb1) {
+      // X(kb+1) was copied during step 0 of slice kb-1; younger copies, which may still fly: W
+      // of the sync of slice kb-1 (odd kb) and X(kb+2) (step 0 of this slice).
+      if ((kb & 1) && kb + 3 < kb1)
+        wait_vm<WI + XI>();
+      else
+        wait_vm<XI>();
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+      __builtin_amdgcn_s_barrier();
+      // W stage (kb/2+2)%3 last fed the dequantisation of slice kb-1 (read during slice kb-2).
+      if (!(kb & 1) && kb + 4 < kb1) issue_w((kb >> 1) + 2);
+      read_frags(xs_base + (uint32_t)((kb + 1) % 3) * XSTAGE + a_rel[0], a[0], std::make_integer_sequence<int, MT>{});
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      mfma_pair(i, 3, a[1][i], bc);
+#pragma unroll
+      for (int k = 0; k < PER; ++k)
+        if ((2 * MT + i) * PER + k < NP) piece((2 * MT + i) * PER + k, st, bn);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  // Prologue: group A = W(kb0), X(kb0), W(kb0+1); group B = X(kb0+1), W(kb0+2).
-  issue_w(kb0);
+  // Prologue: half super-block kb0/2 and X(kb0) land; then the copies slice kb0-1 would have made:
+  // W(kb0/2+1) and X(kb0+1).
+  issue_w(kb0 >> 1);
   issue_x(kb0);
-  if (kb0 + 1 < kb1) issue_w(kb0 + 1);
-  if (kb0 + 1 < kb1) issue_x(kb0 + 1);
-  if (kb0 + 2 < kb1) issue_w(kb0 + 2);
-  if (kb0 + 2 < kb1)
-    wait_vm<XI + WI>();
-  else if (kb0 + 1 < kb1)
-    wait_vm<XI>();
-  else
-    wait_vm<0>();
+  wait_vm<0>();
   __builtin_amdgcn_s_barrier();
+  if (kb0 + 2 < kb1) issue_w((kb0 >> 1) + 1);
+  issue_x(min(kb0 + 1, kb1 - 1));
 
+  u32x4 a[2][8];
+  read_frags(xs_base + (uint32_t)(kb0 % 3) * XSTAGE + a_rel[0], a[0], std::make_integer_sequence<int, MT>{});
   i32x4_t b0[2][4], b1[2][4];
   {
     u32x4 wq[4];
     read_w(kb0, wq);
-    lds_wait(wq);
+    lds_wait<4>(wq);
     const ScaleSel sel = scale_sel(kb0 & 3);
-    dequant_row<VAR>(wq[0], wq[1], sel, b0[0]);
-    dequant_row<VAR>(wq[2], wq[3], sel, b0[1]);
+    dequant_row<VAR>(wq[0], wq[1], sel, geo.mask_lo, geo.mask_hi, b0[0]);
+    dequant_row<VAR>(wq[2], wq[3], sel, geo.mask_lo, geo.mask_hi, b0[1]);
   }
 
-  // Stages (kb+2)%3 (X) and kb%3 (W) are free once every wave is past slice kb-1.
-  auto issue_next = [&](int kb) {
-    if (kb + 2 < kb1) issue_x(kb + 2);
-    if (kb + 3 < kb1) issue_w(kb + 3);
-  };
   int kb = kb0;
-  issue_next(kb);
-  slice(kb, b0, b1);
-  ++kb;
   for (; kb + 1 < kb1; kb += 2) {
-    sync_slice(kb);
-    issue_next(kb);
-    slice(kb, b1, b0);
-    sync_slice(kb + 1);
-    issue_next(kb + 1);
-    slice(kb + 1, b0, b1);
+    slice(kb, b0, b1, a);
+    slice(kb + 1, b1, b0, a);
   }
-  if (kb < kb1) {
-    sync_slice(kb);
-    issue_next(kb);
-    slice(kb, b1, b0);
-  }
+  if (kb < kb1) slice(kb, b0, b1, a);
+  wait_vm<0>();  // the clamped copies of the last slices
 
   // C layout of v_mfma_f32_32x32x*: element e of lane l is row 8*(e/4) + 4*(l/32) + e%4, col l%32.
 #pragma unroll
@@ -525,10 +605,11 @@ void launch_q4k(float* out, const void* w, const uint16_t* X, int M, int N, int 
   // Split K until the grid covers the 256 CUs; each split keeps >= 8 slices.
   int splits = 1;
   while (tiles * splits < 256 && nsl / (splits * 2) >= 8) splits *= 2;
-  const int per = (nsl + splits - 1) / splits;
+  const int per = ((nsl + splits - 1) / splits + 3) & ~3;  // whole super-blocks per split
   splits = (nsl + per - 1) / per;
   if (splits > 1) launch_zero(out, (size_t)M * N, s);
-  GemmGeo geo{M, N, K, (uint32_t)(K / 256) * 144u, per, splits > 1 ? 1 : 0};
+  GemmGeo geo{M,           N,           K,           (uint32_t)(K / 256) * 144u, per, splits > 1 ? 1 : 0,
+              0x0F0F0F0Fu, 0xF0F0F0F0u, 0x000F000Fu, 0x00F000F0u};
   dim3 grid((N + kBN - 1) / kBN, (M + BM - 1) / BM, splits);
   k_qgemm_q4k<VAR, BM><<<grid, 256, 0, s>>>(static_cast<const uint8_t*>(w), X, out, geo);
 }
