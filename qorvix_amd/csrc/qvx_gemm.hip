@@ -92,6 +92,12 @@ __device__ inline void lds_wait(u32x4* r, u32x4* w) {
   }
 }
 
+__device__ inline void lds_wait8_1(u32x4* r, u32x4* w) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]),
+                 "+v"(w[0])::"memory");
+}
+
 __device__ inline uint32_t xswz(uint32_t r) { return (r ^ ((r >> 3) & 3u)) & 7u; }
 // Quant-byte rows of a W stage are 64 bytes apart; 16-byte chunk p of row r sits at slot p ^ qswz(r),
 // which keeps the reads of 16 consecutive rows (one chunk each) on distinct banks.
@@ -485,6 +491,248 @@ __global__ __launch_bounds__(256) void k_qgemm_q4k(const uint8_t* __restrict__ W
     }
 }
 
+// ---- int8 variant --------------------------------------------------------------------------------
+// X is quantised per 32 values to int8 (scale sx = amax/127, the public quantiser's arithmetic) by a
+// prepass; the weight nibbles are int8 operands as they are.  Per 32-element block b (one Q4_K
+// sub-block) one v_mfma_i32_32x32x32_i8 gives the exact integer dot I = sum q * n, folded as
+//   out += sx * (ds * I - dm * qsum) = I * (sx * ds) - (sx * qsum) * dm
+// (ds = d*sc, dm = dmin*m of the sub-block).  The fold is 4 VALU per output per block, against one
+// MFMA per 1024 outputs: this variant is bound by the fold, not by the matrix cores.
+//
+// Workgroup = 256 threads, tile 128 tokens x 256 weight rows; wave w owns rows 64w..64w+63 and all
+// 128 tokens (fp32 accumulators in VGPRs, as the fold updates them).  Per 64-column slice: int8 X
+// (128 x 64 bytes), the tile's scales (4 x 128 floats: sx of both blocks, sx*qsum of both) and the
+// weight headers + group-c quant bytes are copied into LDS (two stages, one slice ahead).
+constexpr int kI8BM = 128;
+
+// Quantiser prepass: one thread per 32-value block of the (tile-padded) M x K activations.  Writes
+// q int8 [M, K] and, for slice kb and token tile t, SC[((kb * ntile + t) * 4 + a) * 128 + m % 128]
+// with a = 0, 1: scale of block 2kb + a; a = 2, 3: scale * qsum of block 2kb + a - 2 (zeros for
+// padding rows).
+__global__ __launch_bounds__(256) void k_quant_q8_gemm(const uint16_t* __restrict__ X, int M, int K, int Mpad,
+                                                       int8_t* __restrict__ q, float* __restrict__ sc) {
+  const int nb = K / 32;
+  const size_t blk = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (blk >= (size_t)Mpad * nb) return;
+  const int m = (int)(blk / nb), j = (int)(blk % nb);
+  const int kb = j >> 1, h = j & 1, ntile = Mpad / kI8BM;
+  float* base = sc + ((size_t)kb * ntile + m / kI8BM) * 4 * kI8BM + (m % kI8BM);
+  if (m >= M) {
+    base[h * kI8BM] = 0.0f;
+    base[(2 + h) * kI8BM] = 0.0f;
+    return;
+  }
+  const uint16_t* x = X + (size_t)m * K + 32 * j;
+  float v[32];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint4 u = reinterpret_cast<const uint4*>(x)[i];
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      v[8 * i + 2 * k] = f16lo(w[k]);
+      v[8 * i + 2 * k + 1] = f16hi(w[k]);
+    }
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  const float s = amax / 127.0f;
+  const float inv = amax > 0.0f ? 127.0f / amax : 0.0f;
+  int sum = 0;
+  uint32_t packed[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float r = roundf(v[4 * i + k] * inv);
+      r = fminf(fmaxf(r, -127.0f), 127.0f);
+      const int qi = (int)r;
+      sum += qi;
+      word |= ((uint32_t)(qi & 0xFF)) << (8 * k);
+    }
+    packed[i] = word;
+  }
+  uint4* dst = reinterpret_cast<uint4*>(q + (size_t)m * K + 32 * j);
+  dst[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+  dst[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+  base[h * kI8BM] = s;
+  base[(2 + h) * kI8BM] = s * (float)sum;
+}
+
+namespace gemm {
+typedef int i32x16_t __attribute__((ext_vector_type(16)));
+// 32-byte rows (one Q4_K group of quant bytes): chunk g of row r at slot g ^ qswz1(r).
+__device__ inline uint32_t qswz1(uint32_t r) { return ((r >> 2) ^ (r >> 3)) & 1u; }
+}  // namespace gemm
+
+__global__ __launch_bounds__(256) void k_qgemm_q4k_i8(const uint8_t* __restrict__ W, const int8_t* __restrict__ Q,
+                                                      const float* __restrict__ SC, float* __restrict__ Y,
+                                                      GemmGeo geo) {
+  constexpr int BM = kI8BM, MT = BM / 32;
+  constexpr int XS = BM * 64;          // int8 X slice
+  constexpr int SS = 4 * BM * 4;       // scales of a slice
+  constexpr int WST = kBN * 48;        // headers (4 KB) + group quant bytes (8 KB)
+  __shared__ __attribute__((aligned(1024))) uint8_t xs[2 * XS];
+  __shared__ __attribute__((aligned(1024))) uint8_t ss[2 * SS];
+  __shared__ __attribute__((aligned(1024))) uint8_t ws[2 * WST];
+
+  const int M = geo.M, N = geo.N, K = geo.K;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ln = lane & 31, g = lane >> 5;
+  const int n0 = blockIdx.x * kBN, tile = blockIdx.y, m0 = tile * BM, ntile = gridDim.y;
+  const int nsl = K / 64;
+  const int kb0 = blockIdx.z * geo.per_split;
+  const int kb1 = min(nsl, kb0 + geo.per_split);
+  if (kb0 >= kb1) return;
+
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(Q + (size_t)m0 * K), (short)0, (int)((uint32_t)min(BM, M - m0) * (uint32_t)K), (int)kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)SC, (short)0, (int)((uint32_t)nsl * (uint32_t)ntile * (uint32_t)SS), (int)kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(W + (size_t)n0 * geo.row_bytes), (short)0, (int)((uint32_t)min(kBN, N - n0) * geo.row_bytes),
+      (int)kRsrcWord3);
+  // X copy i (of 2) of this wave: rows 16(2w+i) + lane/4, LDS slot lane%4 of the row's 64 bytes
+  // holds chunk slot ^ qswz(row).
+  uint32_t xoff[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const uint32_t r = (uint32_t)(16 * (2 * wave + i) + (lane >> 2)), slot = (uint32_t)lane & 3u;
+    xoff[i] = r * (uint32_t)K + 16u * (slot ^ qswz(r));
+  }
+  const uint32_t soff = (uint32_t)(wave * 64 + lane) * 16u;  // waves 0, 1: the two halves of the scales
+  const uint32_t woff_h = (uint32_t)(64 * wave + lane) * geo.row_bytes;
+  uint32_t woff_q[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const uint32_t r = (uint32_t)(64 * wave + 32 * i + (lane >> 1)), p = (uint32_t)lane & 1u;
+    woff_q[i] = r * geo.row_bytes + 16u + 16u * (p ^ qswz1(r));
+  }
+  QVX_LDS uint8_t* xs_l = (QVX_LDS uint8_t*)xs;
+  QVX_LDS uint8_t* ss_l = (QVX_LDS uint8_t*)ss;
+  QVX_LDS uint8_t* ws_l = (QVX_LDS uint8_t*)ws;
+  auto issue = [&](int kb) {
+    const int st = kb & 1;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, xs_l + st * XS + (2 * wave + i) * 1024, 16, xoff[i],
+                                               (uint32_t)kb * 64u, 0, 0);
+    if (wave < 2)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, ss_l + st * SS + wave * 1024, 16, soff,
+                                               (uint32_t)(kb * ntile + tile) * (uint32_t)SS, 0, 0);
+    const uint32_t sbo = (uint32_t)(kb >> 2) * 144u;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, ws_l + st * WST + wave * 1024, 16, woff_h, sbo, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, ws_l + st * WST + 4096 + (2 * wave + i) * 1024, 16, woff_q[i],
+                                               sbo + 32u * (uint32_t)(kb & 3), 0, 0);
+  };
+
+  const uint32_t xs_base = (uint32_t)(uintptr_t)xs_l, ss_base = (uint32_t)(uintptr_t)ss_l,
+                 ws_base = (uint32_t)(uintptr_t)ws_l;
+  // A: row 32i + ln, chunk 2h + g.  B rows r_j = 64w + 32j + ln.
+  uint32_t a_rel[2];
+  const uint32_t sw = qswz((uint32_t)ln);  // qswz(32i + ln) == qswz(ln)
+#pragma unroll
+  for (int h = 0; h < 2; ++h) a_rel[h] = 64u * (uint32_t)ln + 16u * ((2u * h + (uint32_t)g) ^ sw);
+  uint32_t h_rel[2], q_rel[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const uint32_t r = (uint32_t)(64 * wave + 32 * j + ln);
+    h_rel[j] = 16u * r;
+    q_rel[j] = 4096u + 32u * r + 16u * ((uint32_t)g ^ qswz1(r));
+  }
+  const uint32_t s_rel = 4u * (uint32_t)(4 * g);  // token 8q + 4g + t of a 32-token tile
+
+  float acc[MT][2][16];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  issue(kb0);
+  wait_vm<0>();
+  __builtin_amdgcn_s_barrier();
+  for (int kb = kb0; kb < kb1; ++kb) {
+    if (kb + 1 < kb1) issue(kb + 1);  // stage (kb+1)&1 held slice kb-1: every wave is past it
+    const int st = kb & 1, c = kb & 3;
+    const uint32_t xb = xs_base + (uint32_t)st * XS, sb = ss_base + (uint32_t)st * SS,
+                   wb = ws_base + (uint32_t)st * WST;
+    u32x4 wv[4] = {lds_read16(wb + h_rel[0]), lds_read16(wb + q_rel[0]), lds_read16(wb + h_rel[1]),
+                   lds_read16(wb + q_rel[1])};
+    lds_wait<4>(wv);
+    const ScaleSel sel = scale_sel(c);
+    float ds[2][2], dm[2][2];  // [h][j]
+    i32x4_t bq[2][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const u32x4 hd = wv[2 * j], qq = wv[2 * j + 1];
+      const uint32_t scp = ((hd.y >> sel.sa) & sel.ma) | ((hd.w >> sel.sb) & sel.mb);
+      const uint32_t mp = ((hd.z >> sel.sa) & sel.ma) | ((hd.w >> (sel.sb + 4u)) & sel.mb);
+      const float d = f16lo(hd.x), dmin = f16hi(hd.x);
+      ds[0][j] = d * ub(scp, 0);
+      ds[1][j] = d * ub(scp, 1);
+      dm[0][j] = dmin * ub(mp, 0);
+      dm[1][j] = dmin * ub(mp, 1);
+      bq[0][j] = i32x4_t{(int)(qq.x & geo.mask_lo), (int)(qq.y & geo.mask_lo), (int)(qq.z & geo.mask_lo),
+                         (int)(qq.w & geo.mask_lo)};
+      bq[1][j] = i32x4_t{(int)((qq.x >> 4) & geo.mask_lo), (int)((qq.y >> 4) & geo.mask_lo),
+                         (int)((qq.z >> 4) & geo.mask_lo), (int)((qq.w >> 4) & geo.mask_lo)};
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        u32x4 av[1] = {lds_read16(xb + a_rel[h] + 2048u * i)};
+        u32x4 sv[8];
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          sv[q4] = lds_read16(sb + 4u * (uint32_t)(h * BM + 32 * i + 8 * q4) + s_rel);
+          sv[4 + q4] = lds_read16(sb + 4u * (uint32_t)((2 + h) * BM + 32 * i + 8 * q4) + s_rel);
+        }
+        lds_wait8_1(sv, av);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const i32x16_t I = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4_t, av[0]), bq[h][j],
+                                                                   i32x16_t{}, 0, 0, 0);
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const float sx = __uint_as_float(sv[e >> 2][e & 3]), sq = __uint_as_float(sv[4 + (e >> 2)][e & 3]);
+            acc[i][j][e] = __builtin_fmaf((float)I[e], sx * ds[h][j], __builtin_fmaf(-sq, dm[h][j], acc[i][j][e]));
+          }
+        }
+      }
+    }
+    wait_vm<0>();
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+  }
+
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n = n0 + 64 * wave + 32 * j + ln;
+      if (n >= N) continue;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = m0 + 32 * i + 8 * (e >> 2) + 4 * g + (e & 3);
+        if (m < M) {
+          float* dst = Y + (size_t)m * N + n;
+          if (geo.atomic_out)
+            unsafeAtomicAdd(dst, acc[i][j][e]);
+          else
+            *dst = acc[i][j][e];
+        }
+      }
+    }
+}
+
 // fp16 -> bf16 (round to nearest even), 8 values a thread.
 __global__ __launch_bounds__(256) void k_f16_to_bf16(const uint4* __restrict__ x, uint4* __restrict__ y, size_t n8) {
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
@@ -646,7 +894,31 @@ int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M
     launch_var<VAR_F16>(out, w, X, M, rows, cols, s);
     return 0;
   }
-  return -1;  // the int8 variant is not built yet
+  if (variant == VAR_I8) {
+    const int ntile = (M + kI8BM - 1) / kI8BM, Mpad = ntile * kI8BM, nsl = cols / 64;
+    const size_t qbytes = ((size_t)M * cols + 255) & ~(size_t)255;
+    const size_t sbytes = (size_t)nsl * ntile * 4 * kI8BM * 4;
+    if ((size_t)nsl * ntile * 4 * kI8BM * 4 >= (1u << 31)) return -7;
+    uint8_t* ws = static_cast<uint8_t*>(gemm_temp_alloc(qbytes + sbytes, s));
+    if (!ws) return -5;
+    int8_t* q = reinterpret_cast<int8_t*>(ws);
+    float* sc = reinterpret_cast<float*>(ws + qbytes);
+    const size_t nblk = (size_t)Mpad * (cols / 32);
+    k_quant_q8_gemm<<<(unsigned)((nblk + 255) / 256), 256, 0, s>>>(X, M, cols, Mpad, q, sc);
+    const int tiles = ((rows + kBN - 1) / kBN) * ntile;
+    int splits = 1;
+    while (tiles * splits < 256 && nsl / (splits * 2) >= 8) splits *= 2;
+    const int per = ((nsl + splits - 1) / splits + 3) & ~3;
+    splits = (nsl + per - 1) / per;
+    if (splits > 1) launch_zero(out, (size_t)M * rows, s);
+    GemmGeo geo{M, rows, cols, (uint32_t)(cols / 256) * 144u, per, splits > 1 ? 1 : 0,
+                0x0F0F0F0Fu, 0xF0F0F0F0u, 0x000F000Fu, 0x00F000F0u};
+    dim3 grid((rows + kBN - 1) / kBN, ntile, splits);
+    k_qgemm_q4k_i8<<<grid, 256, 0, s>>>(static_cast<const uint8_t*>(w), q, sc, out, geo);
+    gemm_temp_free(ws, s);
+    return 0;
+  }
+  return -1;
 }
 
 }  // namespace qvx

@@ -246,7 +246,7 @@ def test_host_pointer_entry_points(cuda):
 
 # ---- GEMM ----------------------------------------------------------------------------------------
 
-@pytest.mark.parametrize("variant", [qvx.GEMM_BF16, qvx.GEMM_F16])
+@pytest.mark.parametrize("variant", [qvx.GEMM_BF16, qvx.GEMM_F16, qvx.GEMM_I8])
 @pytest.mark.parametrize("M,rows,cols", [(128, 512, 1024), (200, 300, 768), (512, 1024, 4096), (37, 256, 256)])
 def test_gemm_q4k_parity(cuda, variant, M, rows, cols):
     rng = np.random.default_rng(M + rows + cols + variant)
@@ -268,12 +268,30 @@ def test_gemm_q4k_config4_shape(cuda):
     qvx.fill_synthetic_t(W, t, rows, cols, seed=31, scale_mul=1e-3)
     X = cuda.empty((M, cols), dtype=cuda.float16, device="cuda")
     qvx.fill_normal_t(X, seed=32, mul=0.5)
-    for variant in (qvx.GEMM_BF16, qvx.GEMM_F16):
+    for variant in (qvx.GEMM_BF16, qvx.GEMM_F16, qvx.GEMM_I8):
         out = qvx.qgemm_t(W, t, X, rows, cols, variant)
         cuda.cuda.synchronize()
         w = W.cpu().numpy()
         ref = oracle.matmul_f64(w, t, X.cpu().numpy().astype(np.float32), M, rows, cols)
         assert max_rel(out.cpu().numpy(), ref) <= GEMM_TOL
+
+
+@pytest.mark.parametrize("M,rows,cols", [(128, 512, 1024), (200, 300, 768), (37, 256, 256), (640, 768, 2048)])
+def test_gemm_i8_matches_quantized_oracle(cuda, M, rows, cols):
+    """The int8 variant computes sum_b sx_b * sum_k q_k * w_k exactly up to fp32 rounding: compare with
+    the oracle's Q8 quantiser and bit-exact dequant, multiplied in fp64 (tolerance 1e-4)."""
+    rng = np.random.default_rng(M * 7 + rows + cols)
+    t = qvx.Q4_K
+    w = random_weight(t, rows, cols, rng, scale=0.002)
+    X16 = (rng.standard_normal((M, cols)) * 0.5).astype(np.float16)
+    X16[1, 32:64] = 0  # an all-zero block: scale 0
+    out = qvx.qgemm_t(dev(cuda, w), t, dev(cuda, X16.view(np.uint16)), rows, cols, qvx.GEMM_I8)
+    cuda.cuda.synchronize()
+    q, s, _ = oracle.quantize_q8_act(X16.astype(np.float32))
+    Xq = q.astype(np.float64) * np.repeat(s.astype(np.float64), 32, axis=1)
+    Wd = oracle.dequantize(t, w, rows * cols).reshape(rows, cols).astype(np.float64)
+    ref = Xq @ Wd.T
+    assert max_rel(out.cpu().numpy(), ref) <= 1e-4
 
 
 def test_quantize_act_q8_matches_oracle(cuda):
