@@ -6,9 +6,12 @@ A step is one Q4_K GEMV 4096 -> 14336 at M=1 (gate/up shape
 `--copies` distinct seeded weight copies (>= 1 GiB in total, so every timed read comes from HBM
 rather than the 256 MB Infinity Cache).  `value` is algorithmic bytes per step (weights +
 activation + output) / time per step, with inputs resident in HBM.  The prefill GEMM
-(Q4_K 4096 -> 14336, fp16 X, M = 2048, bf16 MFMA) is reported beside it.
-`cpu_baseline` times the reference's own CPU qmatmul (oracle/_ref, built from the reference's
-sources) on the same weights on this host's cores.
+(Q4_K 4096 -> 14336, fp16 X, M in {2048, 512, 128}; bf16 MFMA, fp16 MFMA and
+int8 MFMA variants) is reported beside it.  `cpu_baseline` times the reference's own CPU qmatmul
+(oracle/_ref, built from the reference's sources) on the same weights on this host's cores.
+`roofline.traffic` comes from the committed rocprofv3 PMC summary of this same GEMV
+(profiles/q4k_gemv_4096x14336_m1.traffic.json: FETCH_SIZE / WRITE_SIZE per dispatch, each scaled
+by the counter's reading for a plain device copy of known size), or is null when that file is absent.
 
 Prints exactly one JSON line on stdout; diagnostics go to stderr.
 """
@@ -28,6 +31,9 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 / fp16 MFMA
 ROWS, COLS = 14336, 4096       # Q4_K gate/up projection of Llama-3-8B
 Q4K_ROW_BYTES = COLS // 256 * 144
+GEMV_KERNEL = "qvx::k_gemv_mx<1, 3, 1>"      # matrix-core Q4_K GEMV, one vector per launch
+GEMM_KERNEL = "qvx::k_qgemm_q4k<0, 256>"    # bf16 variant, 256-token tiles
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4k_gemv_4096x14336_m1.traffic.json")
 
 
 def log(*a):
@@ -174,7 +180,7 @@ def main():
             X = torch.empty((M, COLS), dtype=torch.float16, device=dev)
             qvx.fill_normal_t(X, seed=11, mul=0.5)
             Y = torch.empty((M, ROWS), dtype=torch.float32, device=dev)
-            for name, var in (("bf16", qvx.GEMM_BF16), ("f16", qvx.GEMM_F16)):
+            for name, var in (("bf16", qvx.GEMM_BF16), ("f16", qvx.GEMM_F16), ("i8", qvx.GEMM_I8)):
                 def g(i):
                     rc = lib.qvx_qgemm_f16(Y.data_ptr(), wps[i % len(wps)], t, X.data_ptr(), M, ROWS, COLS, var, sh)
                     if rc != 0:
@@ -209,6 +215,10 @@ def main():
 
     achieved = nbytes / (ms_per_step * 1e-3) / 1e9
     g2048 = gemm.get("bf16_M2048", {})
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
     result = {
         "metric": "Q4_K GEMV HBM GB/s (% of peak) at M=1; Q4_K prefill GEMM TFLOPS (% MFMA)",
         "value": round(gbs, 1),
@@ -234,14 +244,25 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "qvx::k_gemv<12, 1, RL>",
+            "traffic": traffic,
+            "kernel": GEMV_KERNEL,
             "per_launch_event_pair_us": round(pair_med, 3),
         },
         "gemm": {
             "workload": "Q4_K 4096->14336 GEMM, X fp16 [M,4096], fp32 out (BASELINE configs[3])",
             "tflops_bf16_M2048": g2048.get("tflops"),
             "percent_of_bf16_peak_M2048": round(100 * g2048["frac_of_bf16_peak"], 2) if g2048 else None,
+            "roofline": {
+                "bound": "mfma",
+                "achieved": g2048.get("tflops"),
+                "peak": BF16_PEAK_TFLOPS,
+                "unit": "TFLOP/s",
+                "frac": g2048.get("frac_of_bf16_peak"),
+                "traffic": None,
+                "kernel": GEMM_KERNEL,
+                "note": "one call = fp16->bf16 prepass + GEMM kernel, timed together; i8 rows count "
+                        "2*M*N*K ops per call against the same bf16 peak",
+            },
             "runs": gemm,
         },
         "cpu_baseline": cpu,

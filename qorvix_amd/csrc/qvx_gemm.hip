@@ -847,12 +847,8 @@ int launch_quantize_act_q8(const uint16_t* X, int M, int K, int8_t* q, float* sc
 namespace {
 
 template <int VAR, int BM>
-void launch_q4k(float* out, const void* w, const uint16_t* X, int M, int N, int K, hipStream_t s) {
+void launch_q4k(float* out, const void* w, const uint16_t* X, int M, int N, int K, int splits, hipStream_t s) {
   const int nsl = K / 64;
-  const int tiles = ((N + kBN - 1) / kBN) * ((M + BM - 1) / BM);
-  // Split K until the grid covers the 256 CUs; each split keeps >= 8 slices.
-  int splits = 1;
-  while (tiles * splits < 256 && nsl / (splits * 2) >= 8) splits *= 2;
   const int per = ((nsl + splits - 1) / splits + 3) & ~3;  // whole super-blocks per split
   splits = (nsl + per - 1) / per;
   if (splits > 1) launch_zero(out, (size_t)M * N, s);
@@ -862,12 +858,20 @@ void launch_q4k(float* out, const void* w, const uint16_t* X, int M, int N, int 
   k_qgemm_q4k<VAR, BM><<<grid, 256, 0, s>>>(static_cast<const uint8_t*>(w), X, out, geo);
 }
 
+// Tile choice: 256-token tiles when they alone give ~one workgroup per CU; else 128-token tiles,
+// splitting K (fp32 atomics into a zeroed output, M*N adds per split) only while the grid is
+// smaller than that.
 template <int VAR>
 void launch_var(float* out, const void* w, const uint16_t* X, int M, int N, int K, hipStream_t s) {
-  if (M > 128)
-    launch_q4k<VAR, 256>(out, w, X, M, N, K, s);
-  else
-    launch_q4k<VAR, 128>(out, w, X, M, N, K, s);
+  const int nt = (N + kBN - 1) / kBN, nsl = K / 64;
+  if (nt * ((M + 255) / 256) >= 224) {
+    launch_q4k<VAR, 256>(out, w, X, M, N, K, 1, s);
+    return;
+  }
+  const int tiles = nt * ((M + 127) / 128);
+  int splits = 1;
+  while (tiles * splits < 200 && nsl / (splits * 2) >= 8) splits *= 2;
+  launch_q4k<VAR, 128>(out, w, X, M, N, K, splits, s);
 }
 
 }  // namespace
@@ -905,9 +909,10 @@ int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M
     float* sc = reinterpret_cast<float*>(ws + qbytes);
     const size_t nblk = (size_t)Mpad * (cols / 32);
     k_quant_q8_gemm<<<(unsigned)((nblk + 255) / 256), 256, 0, s>>>(X, M, cols, Mpad, q, sc);
+    // two int8 workgroups fit a CU (44 KB LDS, <= 256 registers): aim for ~two per CU
     const int tiles = ((rows + kBN - 1) / kBN) * ntile;
     int splits = 1;
-    while (tiles * splits < 256 && nsl / (splits * 2) >= 8) splits *= 2;
+    while (tiles * splits < 448 && nsl / (splits * 2) >= 8) splits *= 2;
     const int per = ((nsl + splits - 1) / splits + 3) & ~3;
     splits = (nsl + per - 1) / per;
     if (splits > 1) launch_zero(out, (size_t)M * rows, s);
