@@ -18,11 +18,12 @@
  *  - Device entry points take device pointers and a hipStream_t passed as `void*` (NULL = the
  *    null stream).  They are asynchronous and stream-ordered, like the CUDA backend's matmulS
  *    launch (cuda/src/cuda_backend.cu:1534-1542).  They allocate no device memory, except
- *    qvx_qgemm_f16 with QVX_GEMM_I8, which keeps a per-device workspace that grows on demand.
+ *    qvx_qgemm_f16 with QVX_GEMM_BF16 / QVX_GEMM_I8, which takes a stream-ordered temporary for the
+ *    converted activations from a memory pool the library owns per device.
  *  - Entry points ending in _host take host pointers and are synchronous: the exact calling
  *    convention of the reference's CPU operator, for a CPU-side drop-in.
  *  - Calls that overlap on one device are safe for distinct outputs; the library holds no
- *    mutable per-call state except the I8 workspace (serialised by a mutex).
+ *    mutable per-call state (the GEMM temporaries are per call and stream-ordered).
  */
 #ifndef QVX_H
 #define QVX_H
@@ -44,9 +45,9 @@ extern "C" {
 #define QVX_E_RANGE (-7)   /* row index out of range, n not a whole number of blocks, size overflow */
 
 /* GEMM variants for qvx_qgemm_f16 */
-#define QVX_GEMM_BF16 0 /* weights dequantised to bf16 tiles in LDS, X rounded to bf16, bf16 MFMA */
+#define QVX_GEMM_BF16 0 /* X rounded to bf16; raw weight blocks staged in LDS, dequantised to bf16; bf16 MFMA */
 #define QVX_GEMM_I8 1   /* X quantised per 32 to int8 (Q8), weight quants as int8, int8 MFMA */
-#define QVX_GEMM_F16 2  /* weights dequantised to fp16 tiles, X kept fp16, fp16 MFMA */
+#define QVX_GEMM_F16 2  /* X kept fp16; raw weight blocks staged in LDS, dequantised to fp16; fp16 MFMA */
 
 /* Version string of the engine, e.g. "qvx 0.1 gfx950". */
 const char* qvx_version(void);
@@ -91,7 +92,7 @@ int qvx_dequant_row(const void* d_w, uint32_t type, int cols, int row, float* d_
 /* Prefill GEMM: out[m * rows + r] = sum_k X[m, k] * dequant(W)[r, k] for m < M, X fp16 [M, cols].
  * No reference counterpart (the reference prefills token by token); semantics are qmatmulN's
  * with X converted fp16 -> fp32 exactly.  variant = QVX_GEMM_BF16 | QVX_GEMM_F16 | QVX_GEMM_I8;
- * tolerance 2e-2 max-relative against the exact sum.  type: Q4_K, Q4_0, Q8_0, Q6_K. */
+ * tolerance 2e-2 max-relative against the exact sum.  type: Q4_K (other types: QVX_E_TYPE). */
 int qvx_qgemm_f16(float* d_out, const void* d_w, uint32_t type, const uint16_t* d_X, int M,
                   int rows, int cols, int variant, void* stream);
 
