@@ -226,6 +226,40 @@ def test_gemv_linearity_full_size(cuda, t):
     assert max_rel(out, oracle.matmul_f64(w, t, X, 3, rows, cols)) <= GEMV_TOL
 
 
+# Every GEMV shape the BASELINE configs name, with their types and vector counts, on seeded device
+# blocks (scales |N(0,1)| * mul as the configs state), against the fp64 oracle.
+#   Q8_0 4096x4096 M=1             configs[1]: Q4_0 4096->11008, 11008->4096, M=1
+#   Q4_K 4096->14336 / 14336->4096, Q6_K 4096->128256 (lm_head), M in {1, 4, 16}
+#   Llama-3-8B Q4_K_M layer (q/o 4096->4096, k/v 4096->1024, gate/up, down; attn_v and
+#               ffn_down in Q6_K) and the Q6_K lm_head, M in {1, 8}
+BASELINE_GEMV = [
+    ("c1 q8_0", qvx.Q8_0, 4096, 4096, (1,), 0.01),
+    ("c2 q4_0 up", qvx.Q4_0, 11008, 4096, (1,), 0.02),
+    ("c2 q4_0 down", qvx.Q4_0, 4096, 11008, (1,), 0.02),
+    ("c3 q4_k gate", qvx.Q4_K, 14336, 4096, (1, 4, 16), 1e-3),
+    ("c3 q4_k down", qvx.Q4_K, 4096, 14336, (1, 4, 16), 1e-3),
+    ("c3 q6_k lm_head", qvx.Q6_K, 128256, 4096, (1, 4), 1e-3),
+    ("c5 q", qvx.Q4_K, 4096, 4096, (1, 8), 1e-3),
+    ("c5 k", qvx.Q4_K, 1024, 4096, (1, 8), 1e-3),
+    ("c5 v", qvx.Q6_K, 1024, 4096, (1, 8), 1e-3),
+    ("c5 down", qvx.Q6_K, 4096, 14336, (1, 8), 1e-3),
+]
+
+
+@pytest.mark.parametrize("name,t,rows,cols,ms,mul", BASELINE_GEMV, ids=[c[0] for c in BASELINE_GEMV])
+def test_gemv_baseline_config_shapes(cuda, name, t, rows, cols, ms, mul):
+    W = qvx.empty_weight(t, rows, cols)
+    qvx.fill_synthetic_t(W, t, rows, cols, seed=rows + cols + t, scale_mul=mul)
+    w = W.cpu().numpy()
+    for m in ms:
+        X = cuda.empty((m, cols), dtype=cuda.float32, device="cuda")
+        qvx.fill_normal_t(X, seed=m * 31 + t)
+        out = qvx.qmatmul_t(W, t, X, rows, cols)
+        cuda.cuda.synchronize()
+        ref = oracle.matmul_f64(w, t, X.cpu().numpy(), m, rows, cols)
+        assert max_rel(out.cpu().numpy(), ref) <= GEMV_TOL, (name, m)
+
+
 def test_host_pointer_entry_points(cuda):
     rng = np.random.default_rng(12)
     lib = qvx.lib()
