@@ -14,20 +14,29 @@
 //  * A (16 rows = (group c, part p), row 4c + p): lane (4c + p, g) is nonzero only for g == c and
 //    holds, at the same K positions, qh (p = 0) or ql (p = 1) of the low-nibble elements with zeros
 //    at the high-nibble positions, or zeros and qh (p = 2) / ql (p = 3) of the high-nibble elements.
-//    These 16-byte fragments are built once per workgroup in LDS, in MFMA order.
+//    Only the nonzero halves are built, once per workgroup, in LDS: 8 bytes per (group, part, m),
+//    512 bytes per (vector, super-block); the lane reads its part's 32 bytes (all four m) and makes
+//    the zero half of each operand, and the whole operand of a lane with g != c, with masks.
 //  * After the 4 MFMAs the accumulator of lane (j, c) holds rows 4c..4c+3 of column j, i.e. the
 //    four partial sums (lo.qh, lo.ql, hi.qh, hi.ql) of row j over group c: the lane applies the
 //    group's scale/min fold exactly as the VALU kernel does.  K positions are matched between A
 //    and B lane by lane and register by register, so the product does not depend on how the
 //    instruction orders K inside a lane group.
 //
-// Data movement: each wave owns a ring of NB LDS stages.  A tile's 2304 bytes (16 rows x 144) are
-// copied with three buffer_load_dwordx4 ... lds (chunk q = 64k + lane -> row q/9, 16-byte chunk
-// q%9, LDS offset 16q: rows 144 bytes apart, conflict-free for the 16-lane quarter reads; the
-// super-block offset is the scalar soffset), NB-1 tiles ahead of use; the wave waits for a tile with
-// s_waitcnt vmcnt (the copies are its only vector memory operations in the loop) and reads it back
-// in MFMA order.  The loop reads LDS through inline asm (see lds_read16).
-//
+// Data movement: each wave owns a ring of NB = 2 LDS stages.  A tile's 2304 bytes (16 rows x 144,
+// rows 144 bytes apart in LDS: conflict-free for the 16-lane quarter reads) are copied by three
+// buffer_load ... lds with all 64 lanes active: two 16-byte copies (lane l of copy k fills LDS
+// bytes 1024k + 16l..+15, i.e. row q/9, 16-byte chunk q%9 for q = 64k + l) and one 4-byte copy
+// for the last 256 bytes (lane l fills byte p = 2048 + 4l: row p/144, column p%144).  With no lane
+// condition on any copy there is no branch for the compiler to wait across.  (A 12-byte copy would
+// not do: it places each lane's 12 bytes at a 16-byte pitch in LDS.)  The super-block offset is
+// the scalar soffset.  The prologue fills both stages; a stage is refilled with the tile two
+// super-blocks on as soon as its contents are in registers, so two tiles are in flight while one
+// is folded.  The wave waits for a tile with s_waitcnt vmcnt (the copies are its only vector
+// memory operations in the loop) and reads it back in MFMA order, through inline asm (see
+// lds_read16).  Waves with activation conversion tasks load and convert before their first copy;
+// the others copy at once.
+
 // Work: workgroup b owns rows [rb, rb + cnt) (cnt <= 16 TQ); wave w = kq * TQ + tq takes tile tq
 // and super-blocks [kq nsb / KQ, (kq + 1) nsb / KQ).  Per-lane partials are summed over the four
 // groups with permlane swaps and over the KQ waves of a tile in wave order through LDS, so every
@@ -48,7 +57,7 @@ typedef short short2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kSB = 144;          // Q4_K super-block bytes
 constexpr int kTileBytes = 2304;  // 16 rows x one super-block
-constexpr int kFragBytes = 1024;  // A fragments of one (vector, super-block): [group][part][m] x 16 bytes
+constexpr int kFragBytes = 512;  // A fragment halves of one (vector, super-block): [group][part][m] x 8 bytes
 constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit data (gfx9)
 
 struct MxGeo {
@@ -58,11 +67,11 @@ struct MxGeo {
   uint32_t row_bytes;
 };
 
-// LDS: dynamic [fragments: NV*nsb*1024][meta: NV*nsb*4 groups*16][zero: 64] and a static tile ring
+// LDS: dynamic [fragments: NV*nsb*512][meta: NV*nsb*4 groups*16] and a static tile ring
 // [16 waves][NB][2304].
 __host__ __device__ inline size_t mx_frag_bytes(int nv, int nsb) { return (size_t)nv * nsb * kFragBytes; }
 __host__ __device__ inline size_t mx_meta_bytes(int nv, int nsb) { return (size_t)nv * nsb * 4 * 16; }
-__host__ __device__ inline size_t mx_dyn_bytes(int nv, int nsb) { return mx_frag_bytes(nv, nsb) + mx_meta_bytes(nv, nsb) + 64; }
+__host__ __device__ inline size_t mx_dyn_bytes(int nv, int nsb) { return mx_frag_bytes(nv, nsb) + mx_meta_bytes(nv, nsb); }
 __host__ __device__ inline size_t mx_lds_bytes(int nv, int nsb, int nb) {
   return mx_dyn_bytes(nv, nsb) + (size_t)16 * nb * kTileBytes;
 }
@@ -102,6 +111,19 @@ __device__ inline void lds_wait(u32x4& a, u32x4& b, u32x4& c) {
 }
 __device__ inline void lds_wait(u32x4& a, u32x4& b, u32x4& c, u32x4& d, u32x4& e) {
   asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e)::"memory");
+}
+
+// LDS write the compiler does not track, for the same reason: were a copy of this wave in flight
+// it would wait for all of them (vmcnt(0)) before an LDS store it emits, so the fragment stores do
+// not depend on the code order.  They never overlap the copy ring, and the lgkmcnt(0) before the
+// barrier that follows them orders them for the readers.
+__device__ inline uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(QVX_LDS const uint8_t*)p;
+}
+__device__ inline void lds_write8(uint32_t addr, uint32_t lo, uint32_t hi) {
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 v = {lo, hi};
+  asm volatile("ds_write_b64 %0, %1" ::"v"(addr), "v"(v) : "memory");
 }
 
 // ---- activations -> A fragments ---------------------------------------------------------------
@@ -151,35 +173,27 @@ __device__ inline void mx_convert(const float4 x0, const float4 x1, int v, int s
     const uint32_t h0 = __builtin_amdgcn_perm(hs[1], hs[0], 0x06040200u), h1 = __builtin_amdgcn_perm(hs[3], hs[2], 0x06040200u);
     const uint32_t l0 = __builtin_amdgcn_perm(ls[1], ls[0], 0x06040200u), l1 = __builtin_amdgcn_perm(ls[3], ls[2], 0x06040200u);
     const int g = sg & 3, s = sg >> 2, hi = part >> 2, m = part & 3;
-    uint8_t* f = frag + (size_t)(v * nsb + s) * kFragBytes + g * 256 + 2 * hi * 64 + m * 16;  // parts 2hi, 2hi+1
-    const uint4 fh = hi ? make_uint4(0u, 0u, h0, h1) : make_uint4(h0, h1, 0u, 0u);
-    const uint4 fl = hi ? make_uint4(0u, 0u, l0, l1) : make_uint4(l0, l1, 0u, 0u);
-    *reinterpret_cast<uint4*>(f) = fh;
-    *reinterpret_cast<uint4*>(f + 64) = fl;
-    float* mt = meta + ((size_t)(v * nsb + s) * 4 + g) * 4;  // [sx, Qa, Qb, 128 Qb as int]
-    if (part == 0) {
-      mt[0] = a * (1.0f / 16383.0f) + z;
-      mt[1] = (float)sq;
-    }
-    if (part == 4) {
-      mt[2] = (float)sq;
-      mt[3] = __builtin_bit_cast(float, 128 * sq);
-    }
+    const uint32_t f = lds_addr(frag) + (uint32_t)((v * nsb + s) * kFragBytes + g * 128 + 2 * hi * 32 + m * 8);
+    lds_write8(f, h0, h1);       // part 2hi: qh
+    lds_write8(f + 32, l0, l1);  // part 2hi + 1: ql
+    const uint32_t mt = lds_addr(meta) + (uint32_t)(((v * nsb + s) * 4 + g) * 16);  // [sx, Qa, Qb, 128 Qb as int]
+    if (part == 0) lds_write8(mt, __builtin_bit_cast(uint32_t, a * (1.0f / 16383.0f) + z), __builtin_bit_cast(uint32_t, (float)sq));
+    if (part == 4) lds_write8(mt + 8, __builtin_bit_cast(uint32_t, (float)sq), (uint32_t)(128 * sq));
   }
 }
 
-// Copy a tile (16 rows of this wave, super-block s) into an LDS stage: chunk q = 64k + lane.
-__device__ inline void mx_issue(__amdgpu_buffer_rsrc_t rsrc, const uint32_t (&off)[3], int s, QVX_LDS uint8_t* st,
-                                int lane) {
+// Copy a tile (16 rows of this wave, super-block s) into an LDS stage: 2 x 1024 + 256 bytes.
+__device__ inline void mx_issue(__amdgpu_buffer_rsrc_t rsrc, const uint32_t (&off)[3], int s, QVX_LDS uint8_t* st) {
   const uint32_t so = (uint32_t)s * kSB;
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, st, 16, off[0], so, 0, 0);
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, st + 1024, 16, off[1], so, 0, 0);
-  if (lane < 16) __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, st + 2048, 16, off[2], so, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, st + 2048, 4, off[2], so, 0, 0);
 }
 
 template <int NV, int NB, int TPT>
 __global__ __launch_bounds__(1024) void k_gemv_mx(const uint8_t* __restrict__ W, const float* __restrict__ X,
                                                   float* __restrict__ Y, int rows, int cols, MxGeo geo) {
+  static_assert(NB >= 2 && NB <= 4, "the tile wait below covers up to 3 tiles ahead");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   __shared__ __attribute__((aligned(16))) uint8_t ring[16 * NB * kTileBytes];
   const int nsb = geo.nsb, TQ = geo.TQ, KQ = geo.KQ;
@@ -187,7 +201,6 @@ __global__ __launch_bounds__(1024) void k_gemv_mx(const uint8_t* __restrict__ W,
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar offsets, M0
   uint8_t* frag = lds;
   float* meta = reinterpret_cast<float*>(lds + mx_frag_bytes(NV, nsb));
-  uint8_t* zero = lds + mx_frag_bytes(NV, nsb) + mx_meta_bytes(NV, nsb);
   QVX_LDS uint8_t* stage = (QVX_LDS uint8_t*)(ring + wave * NB * kTileBytes);
 
   const int b = blockIdx.x;
@@ -195,39 +208,36 @@ __global__ __launch_bounds__(1024) void k_gemv_mx(const uint8_t* __restrict__ W,
   const int tq = wave % TQ, kq = wave / TQ;
   const int s0 = kq * nsb / KQ, s1 = (kq + 1) * nsb / KQ, nu = s1 - s0;
 
-  // 1. this thread's activations (requested first: vector loads complete in order)
+  // 1. activations -> A fragments, by the waves that hold conversion tasks.  This comes before any
+  // copy: a wave's vector memory instructions stall at issue once the CU's queue of outstanding
+  // requests is full, and the CU returns data in request order, so activation loads issued behind
+  // tile copies would wait out the HBM latency and hold the fragment barrier back.  Waves without
+  // tasks go straight to their copies.
   const int per = nsb * 32, ntask = NV * per;
-  float4 xr[TPT][2];
-#pragma unroll
-  for (int k = 0; k < TPT; ++k) {
-    const int t = min(tid + 1024 * k, ntask - 1), v = task_vec<NV>(t, per), r = t - v * per;
-    const float4* src = reinterpret_cast<const float4*>(X + (size_t)v * cols + 8 * r);
-    xr[k][0] = src[0];
-    xr[k][1] = src[1];
-  }
-
-  // 2. A fragments into LDS (waves without tasks skip)
 #pragma unroll
   for (int k = 0; k < TPT; ++k) {
     if (1024 * k + 64 * wave < ntask) {
       const int t0 = tid + 1024 * k, t = min(t0, ntask - 1), v = task_vec<NV>(t, per), r = t - v * per;
-      mx_convert(xr[k][0], xr[k][1], v, r >> 3, r & 7, t0 < ntask, frag, meta, nsb);
+      const float4* src = reinterpret_cast<const float4*>(X + (size_t)v * cols + 8 * r);
+      mx_convert(src[0], src[1], v, r >> 3, r & 7, t0 < ntask, frag, meta, nsb);
     }
   }
-  if (tid < 16) reinterpret_cast<uint32_t*>(zero)[tid] = 0u;
 
-  // 3. prologue copies (tiles of the first NB-1 super-blocks; rows past cnt read as zeros), issued
-  // after the activations are consumed so no compiler-inserted wait covers them
+  // 2. prologue copies into all NB stages (tiles of super-blocks s0.., repeating the wave's last one
+  // when it has fewer than NB, so the count is fixed; rows past cnt read as zeros)
   const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(W + (size_t)rb * geo.row_bytes), (short)0, (int)((uint32_t)cnt * geo.row_bytes), (int)kRsrcWord3);
   uint32_t off[3];
 #pragma unroll
   for (int k = 0; k < 3; ++k) {
-    const uint32_t q = (uint32_t)min(64 * k + lane, 143), r = q / 9u, c9 = q - 9u * r;
-    off[k] = __umul24(16u * (uint32_t)tq + r, geo.row_bytes) + 16u * c9;
+    // LDS byte of this lane's chunk in the tile, then its row and column (chunks never cross rows).
+    const uint32_t p = k < 2 ? (uint32_t)(1024 * k + 16 * lane) : (uint32_t)(2048 + 4 * lane);
+    const uint32_t r = p / (uint32_t)kSB, c = p - (uint32_t)kSB * r;
+    off[k] = __umul24(16u * (uint32_t)tq + r, geo.row_bytes) + c;
   }
+  const int s_last = max(s0, s1 - 1);  // < nsb: s0 < nsb for every wave
 #pragma unroll
-  for (int u = 0; u < NB - 1; ++u) mx_issue(rsrc, off, min(s0 + u, nsb - 1), stage + u * kTileBytes, lane);
+  for (int u = 0; u < NB; ++u) mx_issue(rsrc, off, min(s0 + u, s_last), stage + u * kTileBytes);
 
   // Barrier for the fragments only: wait for this wave's LDS writes, not for the tile copies in
   // flight (__syncthreads would wait for those too).
@@ -238,10 +248,12 @@ __global__ __launch_bounds__(1024) void k_gemv_mx(const uint8_t* __restrict__ W,
   const int j = lane & 15, g = lane >> 4;  // B column (tile row) / K block = group; A row = j
   const uint32_t b_hd = kSB * j, b_q = kSB * j + 16 + 32 * g;
   const bool aon = (j >> 2) == g;
-  const uint32_t a_rel = (uint32_t)(g * 256 + (j & 3) * 64);
+  // A operand: this lane's part p = j & 3 of group g (32 bytes, m = 0..3), in the low half of the
+  // operand for p < 2 and the high half for p >= 2, all zero unless g == j / 4
+  const uint32_t a_rel = (uint32_t)(g * 128 + (j & 3) * 32);
+  const uint32_t mlo = aon && (j & 3) < 2 ? ~0u : 0u, mhi = aon && (j & 3) >= 2 ? ~0u : 0u;
   const uint32_t frag_base = (uint32_t)(uintptr_t)(QVX_LDS uint8_t*)frag;
   const uint32_t meta_base = (uint32_t)(uintptr_t)(QVX_LDS uint8_t*)meta + 16u * g;
-  const uint32_t zero_base = (uint32_t)(uintptr_t)(QVX_LDS uint8_t*)zero;
   const uint32_t stage_base = (uint32_t)(uintptr_t)stage;
   // fold constants of group g (the VALU kernel's Q4_K scale unpacking)
   const uint32_t jj = 2u * (uint32_t)(g & 1);
@@ -255,19 +267,21 @@ __global__ __launch_bounds__(1024) void k_gemv_mx(const uint8_t* __restrict__ W,
   for (int v = 0; v < NV; ++v) acc[v] = 0.0f;
 
   int slot = 0;
+  const int nlast = max(nu, NB) - 1;
   for (int u = 0; u < nu; ++u) {
-    if (u + NB - 1 < nu) {
-      const int ns = slot + NB - 1 >= NB ? slot - 1 : slot + NB - 1;  // (slot + NB - 1) % NB
-      mx_issue(rsrc, off, s0 + u + NB - 1, stage + ns * kTileBytes, lane);
-      wait_vm<3 * (NB - 1)>();
-    } else {
-      wait_vm<0>();
-    }
+    // copies issued after tile u: the prologue's NB-1-u, then one per earlier refill
+    const int ahead = min(NB - 1, nlast - u);
+    if (ahead >= 3) wait_vm<9>();
+    else if (ahead == 2) wait_vm<6>();
+    else if (ahead == 1) wait_vm<3>();
+    else wait_vm<0>();
     const int s = s0 + u;
     const uint32_t st = stage_base + (uint32_t)slot * kTileBytes;
-    slot = slot + 1 == NB ? 0 : slot + 1;
     u32x4 hd = lds_read16(st + b_hd), q0 = lds_read16(st + b_q), q1 = lds_read16<16>(st + b_q);
     lds_wait(hd, q0, q1);
+    // the stage is in registers: refill it with the tile NB super-blocks on
+    if (u + NB < nu) mx_issue(rsrc, off, s + NB, stage + slot * kTileBytes);
+    slot = slot + 1 == NB ? 0 : slot + 1;
     v4i bm[4];
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
@@ -285,10 +299,13 @@ __global__ __launch_bounds__(1024) void k_gemv_mx(const uint8_t* __restrict__ W,
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       const uint32_t vs = (uint32_t)(v * nsb + s);
-      const uint32_t aa = aon ? frag_base + vs * kFragBytes + a_rel : zero_base;
-      u32x4 a0 = lds_read16<0>(aa), a1 = lds_read16<16>(aa), a2 = lds_read16<32>(aa), a3 = lds_read16<48>(aa);
-      u32x4 mt = lds_read16(meta_base + vs * 64u);
-      lds_wait(a0, a1, a2, a3, mt);
+      const uint32_t aa = frag_base + vs * kFragBytes + a_rel;
+      u32x4 r0 = lds_read16<0>(aa), r1 = lds_read16<16>(aa), mt = lds_read16(meta_base + vs * 64u);
+      lds_wait(r0, r1, mt);
+      const u32x4 a0 = {r0.x & mlo, r0.y & mlo, r0.x & mhi, r0.y & mhi};
+      const u32x4 a1 = {r0.z & mlo, r0.w & mlo, r0.z & mhi, r0.w & mhi};
+      const u32x4 a2 = {r1.x & mlo, r1.y & mlo, r1.x & mhi, r1.y & mhi};
+      const u32x4 a3 = {r1.z & mlo, r1.w & mlo, r1.z & mhi, r1.w & mhi};
       v4i c = {0, 0, 0, 0};
       c = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, a0), bm[0], c, 0, 0, 0);
       c = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(v4i, a1), bm[1], c, 0, 0, 0);
@@ -303,6 +320,8 @@ __global__ __launch_bounds__(1024) void k_gemv_mx(const uint8_t* __restrict__ W,
       acc[v] = __builtin_fmaf(__builtin_fmaf(d, t, -dmin * w), __uint_as_float(mt.x), acc[v]);
     }
   }
+
+  wait_vm<0>();  // repeated prologue tiles may still be in flight; the ring is reused below
 
   // 5. sum over the four groups (lanes j, j+16, j+32, j+48), then over the KQ waves of the tile
 #pragma unroll
@@ -343,15 +362,16 @@ static void launch_mx(const void* w, const float* X, float* Y, int rows, int col
   kern<<<(unsigned)nwg, 1024u, lds, s>>>(static_cast<const uint8_t*>(w), X, Y, rows, cols, geo);
 }
 
-// NB = 3 stages when they fit; TPT = activation conversion tasks per thread.
+// Two stages per wave (two tiles in flight behind the one being folded).  Deeper rings only
+// lengthen each wave's copy issue before the fragment barrier, as issue stalls once the CU's
+// request queue is full.  TPT = activation conversion tasks per thread.
 template <int NV>
 static void launch_mx_nv(const void* w, const float* X, float* Y, int rows, int cols, const MxGeo& geo, int nwg,
                          hipStream_t s) {
-  const bool nb3 = mx_lds_bytes(NV, geo.nsb, 3) <= kLdsMax;
   const int tpt = (NV * geo.nsb * 32 + 1023) / 1024;
-  if (tpt <= 1) return nb3 ? launch_mx<NV, 3, 1>(w, X, Y, rows, cols, geo, nwg, s) : launch_mx<NV, 2, 1>(w, X, Y, rows, cols, geo, nwg, s);
-  if (tpt <= 2) return nb3 ? launch_mx<NV, 3, 2>(w, X, Y, rows, cols, geo, nwg, s) : launch_mx<NV, 2, 2>(w, X, Y, rows, cols, geo, nwg, s);
-  return nb3 ? launch_mx<NV, 3, 4>(w, X, Y, rows, cols, geo, nwg, s) : launch_mx<NV, 2, 4>(w, X, Y, rows, cols, geo, nwg, s);
+  if (tpt <= 1) return launch_mx<NV, 2, 1>(w, X, Y, rows, cols, geo, nwg, s);
+  if (tpt <= 2) return launch_mx<NV, 2, 2>(w, X, Y, rows, cols, geo, nwg, s);
+  return launch_mx<NV, 2, 4>(w, X, Y, rows, cols, geo, nwg, s);
 }
 
 }  // namespace
