@@ -31,7 +31,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 / fp16 MFMA
 ROWS, COLS = 14336, 4096       # Q4_K gate/up projection of Llama-3-8B
 Q4K_ROW_BYTES = COLS // 256 * 144
-GEMV_KERNEL = "qvx::k_gemv_mx<1, 3, 1>"      # matrix-core Q4_K GEMV, one vector per launch
+GEMV_KERNEL = "qvx::k_gemv_mx<1, 2, 1>"      # matrix-core Q4_K GEMV, one vector per launch
 GEMM_KERNEL = "qvx::k_qgemm_q4k<0, 256>"    # bf16 variant, 256-token tiles
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4k_gemv_4096x14336_m1.traffic.json")
 
@@ -81,6 +81,41 @@ def cpu_baseline(w_host, x_host, rows, cols, budget_s=5.0):
     }
 
 
+def decode_sweep(torch, stream, steps):
+    """Config 5: the 225 GEMVs of one Llama-3-8B Q4_K_M token (32 layers x q, k, v, o, gate, up,
+    down + the Q6_K LM head, 4.54 GiB of weights, cold in HBM every token) replayed as one HIP
+    graph, at M = 1 and M = 8.  Rate = algorithmic bytes per token / time per token."""
+    from qorvix_amd import decode
+    model = decode.Model.synthetic(n_layers=decode.N_LAYERS, lm_head=True, seed=5)
+    torch.cuda.synchronize()
+    sh = stream.cuda_stream
+    out = {"workload": "Llama-3-8B Q4_K_M decode weight sweep (BASELINE configs[4]): 32 x 7 projections "
+                       "+ Q6_K lm_head = 225 GEMVs per token, one HIP graph per token",
+           "weight_bytes_per_token": model.nbytes}
+    for m in (1, 8):
+        st = decode.DecodeStep(model, m)
+        for _ in range(3):
+            st.replay(sh)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            st.replay(sh)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        _, ab = decode.sweep_bytes(m)
+        gbs = ab / (ms * 1e-3) / 1e9
+        out[f"M{m}"] = {"ms_per_token": round(ms, 4), "algorithmic_bytes_per_token": ab, "gb_s": round(gbs, 1),
+                        "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "tokens_timed": steps}
+        log(f"[bench] sweep M={m}: {ms:.3f} ms/token, {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak)")
+        st.plan.close()
+        del st
+    del model
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -90,6 +125,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--gemm-steps", type=int, default=20)
     ap.add_argument("--gemv-only", action="store_true", help="only the GEMV leg (for profiler passes)")
+    ap.add_argument("--sweep-steps", type=int, default=20, help="timed tokens of the config-5 decode sweep")
+    ap.add_argument("--sweep-only", action="store_true", help="only the config-5 decode sweep (profiler passes)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MiB",
                     help="also run one plain device copy of this many MiB (PMC byte-counter calibration)")
     args = ap.parse_args()
@@ -107,6 +144,9 @@ def main():
     qvx.lib()  # fails loudly if libqvx.so was not built
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream()
+    if args.sweep_only:  # profiler pass over the decode sweep alone
+        print(json.dumps({"sweep": decode_sweep(torch, stream, args.sweep_steps)}), flush=True)
+        return
     t = qvx.Q4_K
     wbytes = qvx.weight_bytes(t, ROWS, COLS)
 
@@ -205,6 +245,15 @@ def main():
         gemm["error"] = str(e)
         log(f"[bench] GEMM failed: {e}")
 
+    # ---- full-model decode weight sweep ----------------------------------
+    sweep = {}
+    if not args.gemv_only:
+        try:
+            sweep = decode_sweep(torch, stream, args.sweep_steps)
+        except RuntimeError as e:  # report, never hide
+            sweep = {"error": str(e)}
+            log(f"[bench] sweep failed: {e}")
+
     # ---- CPU baseline (reference CPU operator on this host) ------------------------------------
     cpu = None
     if not args.no_cpu and not args.gemv_only:
@@ -265,6 +314,7 @@ def main():
             },
             "runs": gemm,
         },
+        "sweep": sweep,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

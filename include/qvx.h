@@ -43,6 +43,7 @@ extern "C" {
 #define QVX_E_HIP (-5)     /* the HIP runtime reported an error (launch, copy, allocation) */
 #define QVX_E_VARIANT (-6) /* unknown GEMM variant */
 #define QVX_E_RANGE (-7)   /* row index out of range, n not a whole number of blocks, size overflow */
+#define QVX_E_STATE (-8)   /* a plan launched before qvx_plan_instantiate, or changed after it */
 
 /* GEMM variants for qvx_qgemm_f16 */
 #define QVX_GEMM_BF16 0 /* X rounded to bf16; raw weight blocks staged in LDS, dequantised to bf16; bf16 MFMA */
@@ -113,6 +114,28 @@ int qvx_fill_synthetic(void* d_w, uint32_t type, int rows, int cols, uint64_t se
 int qvx_fill_normal_f32(float* d_x, size_t n, uint64_t seed, float mul, void* stream);
 int qvx_fill_normal_f16(uint16_t* d_x, size_t n, uint64_t seed, float mul, void* stream);
 
+/* ---- plans: a recorded sequence of GEMV calls replayed as one HIP graph ------------------- */
+/* The form in which the reference's CUDA backend runs a decode step: the same type-switched
+ * matmul launches (cuda/src/cuda_backend.cu:1523-1542, matmul / matmulS) issued on one stream and
+ * captured into a graph, so a token's projections replay with one launch.  A plan holds device
+ * pointers only; the buffers must outlive it.  Plans are not thread-safe; distinct plans are. */
+typedef struct qvx_plan qvx_plan;
+/* New empty plan bound to the current device. */
+int qvx_plan_create(qvx_plan** plan);
+/* Append out = W X (the arguments and checks of qvx_qmatmul_n; nothing runs).  A call with
+ * rows <= 0 is accepted and records nothing.  Appending to an instantiated plan -> QVX_E_STATE. */
+int qvx_plan_add_qmatmul_n(qvx_plan* plan, float* d_out, const void* d_w, uint32_t type,
+                           const float* d_X, int n_vec, int rows, int cols);
+/* Number of recorded calls. */
+int qvx_plan_size(const qvx_plan* plan);
+/* Capture the recorded calls into a HIP graph on the plan's device and instantiate it. */
+int qvx_plan_instantiate(qvx_plan* plan);
+/* Replay the graph on `stream` (stream-ordered, asynchronous).  Not instantiated -> QVX_E_STATE. */
+int qvx_plan_launch(qvx_plan* plan, void* stream);
+/* Issue the recorded calls one by one on `stream` (no graph): the same kernels and arguments. */
+int qvx_plan_run_eager(const qvx_plan* plan, void* stream);
+/* Free the plan and its graph (NULL is a no-op). */
+void qvx_plan_destroy(qvx_plan* plan);
 /* ---- host entry points (host pointers, synchronous) --------------------------------------- */
 /* The reference's CPU signatures (qmatmul.hpp:14-36, dequant.hpp:12-21) over the GPU kernels:
  * weight, x and out live in host memory; the call uploads, computes on the current device and

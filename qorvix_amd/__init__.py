@@ -29,7 +29,7 @@ TYPE_NAMES = {0: "F32", 1: "F16", 2: "Q4_0", 3: "Q4_1", 6: "Q5_0", 7: "Q5_1", 8:
               12: "Q4_K", 13: "Q5_K", 14: "Q6_K", 30: "BF16"}
 
 # status codes (include/qvx.h)
-OK, E_TYPE, E_SHAPE, E_NVEC, E_NULL, E_HIP, E_VARIANT, E_RANGE = 0, -1, -2, -3, -4, -5, -6, -7
+OK, E_TYPE, E_SHAPE, E_NVEC, E_NULL, E_HIP, E_VARIANT, E_RANGE, E_STATE = 0, -1, -2, -3, -4, -5, -6, -7, -8
 # GEMM variants
 GEMM_BF16, GEMM_I8, GEMM_F16 = 0, 1, 2
 
@@ -51,6 +51,13 @@ SIGNATURES = {
     "qvx_fill_synthetic": ([_vp, _u32, _i32, _i32, _u64, _f32, _vp], _i32),
     "qvx_fill_normal_f32": ([_vp, _sz, _u64, _f32, _vp], _i32),
     "qvx_fill_normal_f16": ([_vp, _sz, _u64, _f32, _vp], _i32),
+    "qvx_plan_create": ([C.POINTER(_vp)], _i32),
+    "qvx_plan_add_qmatmul_n": ([_vp, _vp, _vp, _u32, _vp, _i32, _i32, _i32], _i32),
+    "qvx_plan_size": ([_vp], _i32),
+    "qvx_plan_instantiate": ([_vp], _i32),
+    "qvx_plan_launch": ([_vp, _vp], _i32),
+    "qvx_plan_run_eager": ([_vp, _vp], _i32),
+    "qvx_plan_destroy": ([_vp], None),
     "qvx_qmatmul_host": ([_vp, _vp, _u32, _vp, _i32, _i32], _i32),
     "qvx_qmatmul_n_host": ([_vp, _vp, _u32, _vp, _i32, _i32, _i32], _i32),
     "qvx_dequantize_host": ([_u32, _vp, _vp, _sz], _i32),

@@ -9,6 +9,7 @@
 #include <cstdio>
 #include <cstring>
 #include <mutex>
+#include <new>
 #include <vector>
 
 #include "../../include/qvx.h"
@@ -34,6 +35,21 @@ void launch_zero(float* p, size_t n, hipStream_t s);
 }  // namespace qvx
 
 using namespace qvx;
+
+// A recorded GEMV sequence (include/qvx.h, qvx_plan_*).
+struct qvx_plan {
+  struct Call {
+    float* out;
+    const void* w;
+    uint32_t type;
+    const float* X;
+    int nvec, rows, cols;
+  };
+  std::vector<Call> calls;
+  int device = 0;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+};
 
 namespace {
 
@@ -96,6 +112,20 @@ int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int
   return hip_status();
 }
 
+// Makes `dev` current for a scope and restores the caller's device.
+struct DeviceGuard {
+  int prev = -1;
+  bool ok = false;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) return;
+    ok = prev == dev || hipSetDevice(dev) == hipSuccess;
+  }
+  ~DeviceGuard() {
+    int cur = -1;
+    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+  }
+};
+
 // Device buffer reused by the synchronous host-pointer entry points (one per calling thread).
 struct HostStage {
   void* p = nullptr;
@@ -134,6 +164,7 @@ const char* qvx_strerror(int code) {
     case QVX_E_HIP: return "HIP runtime error";
     case QVX_E_VARIANT: return "unknown GEMM variant";
     case QVX_E_RANGE: return "index or size out of range";
+    case QVX_E_STATE: return "plan not instantiated, or changed after instantiation";
     default: return "unknown qvx status";
   }
 }
@@ -232,6 +263,92 @@ int qvx_fill_normal_f16(uint16_t* d_x, size_t n, uint64_t seed, float mul, void*
   if (n && !d_x) return QVX_E_NULL;
   launch_fill_normal_f16(d_x, n, seed, mul, as_stream(stream));
   return hip_status();
+}
+
+// ---- plans ---------------------------------------------------------------------------------------
+
+int qvx_plan_create(qvx_plan** plan) {
+  if (!plan) return QVX_E_NULL;
+  *plan = nullptr;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return QVX_E_HIP;
+  auto* p = new (std::nothrow) qvx_plan;
+  if (!p) return QVX_E_HIP;
+  p->device = dev;
+  *plan = p;
+  return QVX_OK;
+}
+
+int qvx_plan_add_qmatmul_n(qvx_plan* plan, float* d_out, const void* d_w, uint32_t type, const float* d_X,
+                           int n_vec, int rows, int cols) {
+  if (!plan) return QVX_E_NULL;
+  if (plan->exec) return QVX_E_STATE;
+  const TypeInfo* ti = nullptr;
+  if (n_vec <= 0) return QVX_E_NVEC;
+  if (int rc = check_matmul(type, cols, &ti); rc != QVX_OK) return rc;
+  if (rows <= 0) return QVX_OK;
+  if (!d_out || (cols > 0 && (!d_w || !d_X))) return QVX_E_NULL;
+  plan->calls.push_back({d_out, d_w, type, d_X, n_vec, rows, cols});
+  return QVX_OK;
+}
+
+int qvx_plan_size(const qvx_plan* plan) { return plan ? (int)plan->calls.size() : 0; }
+
+int qvx_plan_run_eager(const qvx_plan* plan, void* stream) {
+  if (!plan) return QVX_E_NULL;
+  for (const auto& c : plan->calls)
+    if (int rc = gemv(c.out, c.w, c.type, c.X, c.nvec, c.rows, c.cols, as_stream(stream)); rc != QVX_OK) return rc;
+  return QVX_OK;
+}
+
+int qvx_plan_instantiate(qvx_plan* plan) {
+  if (!plan) return QVX_E_NULL;
+  if (plan->exec) return QVX_OK;
+  DeviceGuard guard(plan->device);
+  if (!guard.ok) return QVX_E_HIP;
+  // Capture on a stream of the plan's own (default priority), in thread-local mode: the GEMV
+  // launches make no calls that capture forbids.
+  hipStream_t cs = nullptr;
+  if (hipStreamCreateWithFlags(&cs, hipStreamNonBlocking) != hipSuccess) return QVX_E_HIP;
+  int rc = QVX_OK;
+  hipGraph_t graph = nullptr;
+  if (hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+    rc = QVX_E_HIP;
+  } else {
+    for (const auto& c : plan->calls) {
+      rc = gemv(c.out, c.w, c.type, c.X, c.nvec, c.rows, c.cols, cs);
+      if (rc != QVX_OK) break;
+    }
+    if (hipStreamEndCapture(cs, &graph) != hipSuccess && rc == QVX_OK) rc = QVX_E_HIP;
+  }
+  hipGraphExec_t exec = nullptr;
+  if (rc == QVX_OK && hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) != hipSuccess) rc = QVX_E_HIP;
+  (void)hipStreamDestroy(cs);
+  if (rc != QVX_OK) {
+    if (graph) (void)hipGraphDestroy(graph);
+    (void)hipGetLastError();
+    return rc;
+  }
+  plan->graph = graph;
+  plan->exec = exec;
+  return QVX_OK;
+}
+
+int qvx_plan_launch(qvx_plan* plan, void* stream) {
+  if (!plan) return QVX_E_NULL;
+  if (!plan->exec) return QVX_E_STATE;
+  if (hipGraphLaunch(plan->exec, as_stream(stream)) != hipSuccess) return QVX_E_HIP;
+  return QVX_OK;
+}
+
+void qvx_plan_destroy(qvx_plan* plan) {
+  if (!plan) return;
+  {
+    DeviceGuard guard(plan->device);
+    if (plan->exec) (void)hipGraphExecDestroy(plan->exec);
+    if (plan->graph) (void)hipGraphDestroy(plan->graph);
+  }
+  delete plan;
 }
 
 // ---- synchronous host-pointer forms --------------------------------------------------------------

@@ -1,0 +1,183 @@
+"""Decode-step caller of the quantized matmul: the weight side of one Llama token.
+
+Mirrors the reference's decoder (``runtime/src/text_model.cpp:146-173``): per layer, ``wmatmul`` of
+wq, wk, wv on the normed hidden state, wo on the attention output, ffn_gate and ffn_up on the normed
+state, ffn_down on the SwiGLU activation, then the LM head (``:176-177``).  ``wmatmul`` dispatches
+on the weight's ggml type (``runtime/include/qorvix/runtime/weights.hpp:49-56``; on the GPU, the
+type switch of ``cuda/src/cuda_backend.cu:1523-1542``), which here is ``qvx_qmatmul_n``: the
+engine's kernels pick the format.  A token's projections are recorded into a ``Plan`` (one HIP
+graph, ``qvx_plan_*`` in ``include/qvx.h``) and replayed with one launch, as the CUDA backend
+replays its captured decode step.
+
+Only the matmuls are issued: RMSNorm, RoPE, attention and SwiGLU are not part of this engine, so
+their outputs are stand-in activation buffers (seeded N(0,1)) of the right shapes.  This is the
+"full-model decode weight sweep" workload: 32 layers x 7 projections + the LM head = 225 GEMVs and
+4,875,853,824 weight bytes per token for Llama-3-8B Q4_K_M.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, field
+
+from . import OK, Q4_K, Q6_K, QvxError, lib, weight_bytes, fill_synthetic_t, fill_normal_t, empty_weight
+
+
+@dataclass
+class DevWeight:
+    """A device-resident GGUF weight [rows, cols] of one ggml type (``cuda_backend.cu:1257-1262``,
+    ``DevWeight``; the quantized case of ``WeightMat``, ``weights.hpp:22-46``)."""
+    data: object          # torch.uint8 tensor on the device, raw GGUF blocks row-major
+    type: int
+    rows: int
+    cols: int
+
+    @property
+    def nbytes(self) -> int:
+        return weight_bytes(self.type, self.rows, self.cols)
+
+
+def wmatmul_n(out, w: DevWeight, X, nvec: int, stream: int) -> None:
+    """out[nvec, rows] = X[nvec, cols] W^T (``weights.hpp:68-87``, ``wmatmulN`` without bias)."""
+    rc = lib().qvx_qmatmul_n(out.data_ptr(), w.data.data_ptr(), w.type, X.data_ptr(), nvec, w.rows, w.cols,
+                             stream)
+    if rc != OK:
+        raise QvxError(rc, "qvx_qmatmul_n")
+
+
+# Llama-3-8B projection shapes (rows = out features, cols = in features) and the Q4_K_M type mix:
+# attn_v and ffn_down in Q6_K, the rest Q4_K.
+D_MODEL, D_FF, D_KV, VOCAB, N_LAYERS = 4096, 14336, 1024, 128256, 32
+LAYER_SPECS = (  # (name, rows, cols, type, input buffer)
+    ("wq", D_MODEL, D_MODEL, Q4_K, "xn"),
+    ("wk", D_KV, D_MODEL, Q4_K, "xn"),
+    ("wv", D_KV, D_MODEL, Q6_K, "xn"),
+    ("wo", D_MODEL, D_MODEL, Q4_K, "attn"),
+    ("ffn_gate", D_FF, D_MODEL, Q4_K, "xn"),
+    ("ffn_up", D_FF, D_MODEL, Q4_K, "xn"),
+    ("ffn_down", D_MODEL, D_FF, Q6_K, "act"),
+)
+LM_HEAD = ("lm_head", VOCAB, D_MODEL, Q6_K, "xn")
+
+
+def sweep_specs(n_layers: int = N_LAYERS, lm_head: bool = True):
+    """The (layer, name, rows, cols, type, input) list of one token, in the reference's call order."""
+    out = [(l, *spec) for l in range(n_layers) for spec in LAYER_SPECS]
+    if lm_head:
+        out.append((n_layers, *LM_HEAD))
+    return out
+
+
+def sweep_bytes(m: int, n_layers: int = N_LAYERS, lm_head: bool = True):
+    """(weight bytes, algorithmic bytes) per token at M vectors: weights + 4 M (rows + cols) per GEMV."""
+    wb = ab = 0
+    for _, _, rows, cols, t, _ in sweep_specs(n_layers, lm_head):
+        w = weight_bytes(t, rows, cols)
+        wb += w
+        ab += w + 4 * m * (rows + cols)
+    return wb, ab
+
+
+@dataclass
+class Model:
+    """Synthetic Llama-3-8B Q4_K_M weights on the device (``layers[l][name]``, ``lm_head``)."""
+    layers: list = field(default_factory=list)
+    lm_head: DevWeight | None = None
+
+    @staticmethod
+    def synthetic(n_layers: int = N_LAYERS, lm_head: bool = True, seed: int = 5, device="cuda") -> "Model":
+        """Fresh seed per (layer, tensor); scales fp16(|N(0,1)| * 1e-3) as the configs specify."""
+        m = Model()
+        for l, name, rows, cols, t, _ in sweep_specs(n_layers, lm_head):
+            w = DevWeight(empty_weight(t, rows, cols, device), t, rows, cols)
+            fill_synthetic_t(w.data, t, rows, cols, seed=_tensor_seed(seed, l, name), scale_mul=1e-3)
+            if l < n_layers:
+                while len(m.layers) <= l:
+                    m.layers.append({})
+                m.layers[l][name] = w
+            else:
+                m.lm_head = w
+        return m
+
+    @property
+    def nbytes(self) -> int:
+        n = sum(w.nbytes for layer in self.layers for w in layer.values())
+        return n + (self.lm_head.nbytes if self.lm_head else 0)
+
+
+def _tensor_seed(seed: int, layer: int, name: str) -> int:
+    names = [s[0] for s in LAYER_SPECS] + [LM_HEAD[0]]
+    return (seed << 20) + (layer << 4) + names.index(name)
+
+
+class Plan:
+    """A recorded GEMV sequence replayed as one HIP graph (``qvx_plan_*``)."""
+
+    def __init__(self):
+        h = C.c_void_p()
+        rc = lib().qvx_plan_create(C.byref(h))
+        if rc != OK:
+            raise QvxError(rc, "qvx_plan_create")
+        self._h = h
+
+    def add(self, out, w: DevWeight, X, nvec: int) -> None:
+        rc = lib().qvx_plan_add_qmatmul_n(self._h, out.data_ptr(), w.data.data_ptr(), w.type, X.data_ptr(), nvec,
+                                          w.rows, w.cols)
+        if rc != OK:
+            raise QvxError(rc, "qvx_plan_add_qmatmul_n")
+
+    def __len__(self) -> int:
+        return lib().qvx_plan_size(self._h)
+
+    def instantiate(self) -> None:
+        rc = lib().qvx_plan_instantiate(self._h)
+        if rc != OK:
+            raise QvxError(rc, "qvx_plan_instantiate")
+
+    def launch(self, stream: int) -> None:
+        rc = lib().qvx_plan_launch(self._h, stream)
+        if rc != OK:
+            raise QvxError(rc, "qvx_plan_launch")
+
+    def run_eager(self, stream: int) -> None:
+        rc = lib().qvx_plan_run_eager(self._h, stream)
+        if rc != OK:
+            raise QvxError(rc, "qvx_plan_run_eager")
+
+    def close(self) -> None:
+        if self._h:
+            lib().qvx_plan_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class DecodeStep:
+    """The weight side of one decode step at M vectors: activation stand-ins, per-projection
+    outputs, and the plan of 7 GEMVs per layer + the LM head in the reference's order."""
+
+    def __init__(self, model: Model, m: int, seed: int = 9, device="cuda"):
+        import torch
+        self.model, self.m = model, m
+        f32 = dict(dtype=torch.float32, device=device)
+        self.inputs = {"xn": torch.empty((m, D_MODEL), **f32), "attn": torch.empty((m, D_MODEL), **f32),
+                       "act": torch.empty((m, D_FF), **f32)}
+        for i, k in enumerate(("xn", "attn", "act")):
+            fill_normal_t(self.inputs[k], seed=seed + i)
+        self.outputs = []
+        self.plan = Plan()
+        for l, name, rows, cols, t, src in sweep_specs(len(model.layers), model.lm_head is not None):
+            w = model.layers[l][name] if l < len(model.layers) else model.lm_head
+            y = torch.empty((m, rows), **f32)
+            self.outputs.append((l, name, y))
+            self.plan.add(y, w, self.inputs[src], m)
+        self.plan.instantiate()
+
+    def replay(self, stream: int) -> None:
+        self.plan.launch(stream)
+
+    def run_eager(self, stream: int) -> None:
+        self.plan.run_eager(stream)

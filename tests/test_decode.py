@@ -1,0 +1,54 @@
+"""CPU tests of the decode-step caller (qorvix_amd/decode.py): the token's GEMV list mirrors the
+reference's decoder call order and type mix, its byte accounting is the GGUF arithmetic, and the
+plan entry points reject bad handles before touching a device."""
+from __future__ import annotations
+
+import qorvix_amd as qvx
+from qorvix_amd import decode
+
+
+def test_layer_call_order_mirrors_reference_decoder():
+    # runtime/src/text_model.cpp:146-173: wq, wk, wv, (attention), wo, ffn_gate, ffn_up, ffn_down
+    assert [s[0] for s in decode.LAYER_SPECS] == ["wq", "wk", "wv", "wo", "ffn_gate", "ffn_up", "ffn_down"]
+    specs = decode.sweep_specs()
+    assert len(specs) == 32 * 7 + 1 and specs[-1][1] == "lm_head"
+    assert [s[1] for s in specs[:7]] == [s[0] for s in decode.LAYER_SPECS]
+    # inputs: q/k/v/gate/up read the normed state, wo the attention output, ffn_down the SwiGLU output
+    assert {s[0]: s[4] for s in decode.LAYER_SPECS} == {
+        "wq": "xn", "wk": "xn", "wv": "xn", "wo": "attn", "ffn_gate": "xn", "ffn_up": "xn", "ffn_down": "act"}
+
+
+def test_q4_k_m_type_mix():
+    types = {s[0]: s[3] for s in decode.LAYER_SPECS}
+    assert types["wv"] == qvx.Q6_K and types["ffn_down"] == qvx.Q6_K and decode.LM_HEAD[3] == qvx.Q6_K
+    assert all(types[n] == qvx.Q4_K for n in ("wq", "wk", "wo", "ffn_gate", "ffn_up"))
+
+
+def test_sweep_byte_accounting():
+    # per-tensor bytes from the block formats: rows * (cols / 256) * {144 (Q4_K), 210 (Q6_K)}
+    per = {"wq": 4096 * 16 * 144, "wk": 1024 * 16 * 144, "wv": 1024 * 16 * 210, "wo": 4096 * 16 * 144,
+           "ffn_gate": 14336 * 16 * 144, "ffn_up": 14336 * 16 * 144, "ffn_down": 4096 * 56 * 210}
+    assert per == {"wq": 9437184, "wk": 2359296, "wv": 3440640, "wo": 9437184, "ffn_gate": 33030144,
+                   "ffn_up": 33030144, "ffn_down": 48168960}
+    layer = sum(per.values())
+    assert layer == 138903552
+    lm = 128256 * 16 * 210
+    wb, ab1 = decode.sweep_bytes(1)
+    _, ab8 = decode.sweep_bytes(8)
+    assert wb == 32 * layer + lm == 4875853824
+    # activations in + outputs out, 4 bytes each, per GEMV and vector
+    io = sum(rows + cols for _, _, rows, cols, _, _ in decode.sweep_specs()) * 4
+    assert ab1 == wb + io == 4886868992
+    assert ab8 == wb + 8 * io == 4963975168
+
+
+def test_plan_entry_points_reject_null_handles():
+    lib = qvx.lib()
+    assert lib.qvx_plan_size(None) == 0
+    assert lib.qvx_plan_launch(None, None) == qvx.E_NULL
+    assert lib.qvx_plan_run_eager(None, None) == qvx.E_NULL
+    assert lib.qvx_plan_instantiate(None) == qvx.E_NULL
+    assert lib.qvx_plan_add_qmatmul_n(None, None, None, qvx.Q4_K, None, 1, 16, 256) == qvx.E_NULL
+    assert lib.qvx_plan_create(None) == qvx.E_NULL
+    lib.qvx_plan_destroy(None)
+    assert qvx.strerror(qvx.E_STATE).startswith("plan not instantiated")

@@ -1,0 +1,81 @@
+"""GPU tests of the decode-step plan: a token's GEMVs captured into one HIP graph replay to the same
+bits as the eager calls (several replays, with other work and synchronisations between them), and
+their outputs agree with the oracle."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+import qorvix_amd as qvx
+from conftest import max_rel
+from qorvix_amd import decode
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def small_model(cuda):
+    # two Llama-3-8B layers + the LM head: every projection shape and type of the full sweep
+    return decode.Model.synthetic(n_layers=2, lm_head=True, seed=7)
+
+
+@pytest.mark.parametrize("m", [1, 8])
+def test_plan_replays_match_eager(cuda, small_model, m):
+    torch = cuda
+    step = decode.DecodeStep(small_model, m, seed=m)
+    assert len(step.plan) == 2 * 7 + 1
+    s = torch.cuda.current_stream().cuda_stream
+    step.run_eager(s)
+    torch.cuda.synchronize()
+    ref = [y.clone() for _, _, y in step.outputs]
+    for rep in range(3):
+        for _, _, y in step.outputs:
+            y.fill_(float("nan"))
+        noise = torch.randn(1 << 20, device="cuda")  # eager work between replays
+        float(noise.sum())
+        step.replay(s)
+        torch.cuda.synchronize()
+        for (l, name, y), r in zip(step.outputs, ref):
+            assert torch.equal(y.view(torch.int32), r.view(torch.int32)), (rep, l, name)
+    step.plan.close()
+
+
+def test_plan_outputs_match_oracle(cuda, small_model):
+    torch = cuda
+    step = decode.DecodeStep(small_model, 2, seed=3)
+    step.replay(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    X = {k: v.cpu().numpy() for k, v in step.inputs.items()}
+    for (l, name, y), (_, _, rows, cols, t, src) in zip(step.outputs, decode.sweep_specs(2, True)):
+        w = small_model.layers[l][name] if l < 2 else small_model.lm_head
+        rb = qvx.row_bytes(t, cols)
+        r0 = (rows // 3) & ~15
+        nr = 48
+        wrows = w.data[r0 * rb:(r0 + nr) * rb].cpu().numpy()
+        ref = oracle.matmul_f64(wrows, t, X[src], 2, nr, cols)
+        assert max_rel(y[:, r0:r0 + nr].cpu().numpy(), ref) <= 1e-3, (l, name)
+    step.plan.close()
+
+
+def test_plan_state_and_argument_errors(cuda):
+    torch = cuda
+    p = decode.Plan()
+    W = qvx.empty_weight(qvx.Q4_K, 16, 256)
+    x = torch.zeros(256, device="cuda")
+    y = torch.zeros(16, device="cuda")
+    with pytest.raises(qvx.QvxError) as e:
+        p.launch(0)
+    assert e.value.code == qvx.E_STATE
+    lib = qvx.lib()
+    assert lib.qvx_plan_add_qmatmul_n(p._h, y.data_ptr(), W.data_ptr(), 99, x.data_ptr(), 1, 16, 256) == qvx.E_TYPE
+    assert lib.qvx_plan_add_qmatmul_n(p._h, y.data_ptr(), W.data_ptr(), qvx.Q4_K, x.data_ptr(), 1, 16, 200) == qvx.E_SHAPE
+    assert lib.qvx_plan_add_qmatmul_n(p._h, y.data_ptr(), W.data_ptr(), qvx.Q4_K, x.data_ptr(), 0, 16, 256) == qvx.E_NVEC
+    assert lib.qvx_plan_add_qmatmul_n(p._h, y.data_ptr(), W.data_ptr(), qvx.Q4_K, x.data_ptr(), 1, 0, 256) == qvx.OK
+    assert len(p) == 0
+    p.add(y, decode.DevWeight(W, qvx.Q4_K, 16, 256), x, 1)
+    p.instantiate()
+    assert lib.qvx_plan_add_qmatmul_n(p._h, y.data_ptr(), W.data_ptr(), qvx.Q4_K, x.data_ptr(), 1, 16, 256) == qvx.E_STATE
+    p.launch(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    p.close()
