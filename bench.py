@@ -90,10 +90,10 @@ def decode_sweep(torch, stream, steps):
     torch.cuda.synchronize()
     sh = stream.cuda_stream
     out = {"workload": "Llama-3-8B Q4_K_M decode weight sweep (BASELINE configs[4]): 32 x 7 projections "
-                       "+ Q6_K lm_head = 225 GEMVs per token, one HIP graph per token",
+                       "+ Q6_K lm_head = 225 GEMVs per token, one HIP graph per token, GEMVs in call order",
            "weight_bytes_per_token": model.nbytes}
-    for m in (1, 8):
-        st = decode.DecodeStep(model, m)
+    def time_step(m, concurrent):
+        st = decode.DecodeStep(model, m, concurrent=concurrent)
         for _ in range(3):
             st.replay(sh)
         torch.cuda.synchronize()
@@ -103,14 +103,19 @@ def decode_sweep(torch, stream, steps):
             st.replay(sh)
         e1.record(stream)
         torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / steps
+        st.plan.close()
+        return e0.elapsed_time(e1) / steps
+
+    for m in (1, 8):
+        ms = time_step(m, False)
+        ms_br = time_step(m, True)
         _, ab = decode.sweep_bytes(m)
         gbs = ab / (ms * 1e-3) / 1e9
         out[f"M{m}"] = {"ms_per_token": round(ms, 4), "algorithmic_bytes_per_token": ab, "gb_s": round(gbs, 1),
-                        "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "tokens_timed": steps}
-        log(f"[bench] sweep M={m}: {ms:.3f} ms/token, {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak)")
-        st.plan.close()
-        del st
+                        "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "tokens_timed": steps,
+                        "ms_per_token_qkv_gateup_branches": round(ms_br, 4)}
+        log(f"[bench] sweep M={m}: {ms:.3f} ms/token, {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak); "
+            f"{ms_br:.3f} ms/token with q/k/v and gate/up as concurrent graph branches")
     del model
     torch.cuda.empty_cache()
     return out

@@ -126,9 +126,17 @@ int qvx_plan_create(qvx_plan** plan);
  * rows <= 0 is accepted and records nothing.  Appending to an instantiated plan -> QVX_E_STATE. */
 int qvx_plan_add_qmatmul_n(qvx_plan* plan, float* d_out, const void* d_w, uint32_t type,
                            const float* d_X, int n_vec, int rows, int cols);
+/* Calls added between qvx_plan_fork and qvx_plan_join are independent of each other (the graph
+ * gets one branch per call, so their kernels may overlap on the device); all of them follow every
+ * call before the fork and precede every call after the join -- as the decoder's q/k/v
+ * projections all read the normed state (text_model.cpp:147-150).  Forking twice, or joining
+ * without a fork, -> QVX_E_STATE. */
+int qvx_plan_fork(qvx_plan* plan);
+int qvx_plan_join(qvx_plan* plan);
 /* Number of recorded calls. */
 int qvx_plan_size(const qvx_plan* plan);
-/* Capture the recorded calls into a HIP graph on the plan's device and instantiate it. */
+/* Capture the recorded calls into a HIP graph on the plan's device and instantiate it (an open
+ * fork is joined first). */
 int qvx_plan_instantiate(qvx_plan* plan);
 /* Replay the graph on `stream` (stream-ordered, asynchronous).  Not instantiated -> QVX_E_STATE. */
 int qvx_plan_launch(qvx_plan* plan, void* stream);

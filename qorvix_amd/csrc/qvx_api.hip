@@ -44,9 +44,12 @@ struct qvx_plan {
     uint32_t type;
     const float* X;
     int nvec, rows, cols;
+    int group;  // calls sharing a group >= 0 are independent of each other (one fork); -1: in order
   };
   std::vector<Call> calls;
   int device = 0;
+  int open_group = -1;  // the fork being recorded, -1 if none
+  int groups = 0;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
 };
@@ -288,7 +291,21 @@ int qvx_plan_add_qmatmul_n(qvx_plan* plan, float* d_out, const void* d_w, uint32
   if (int rc = check_matmul(type, cols, &ti); rc != QVX_OK) return rc;
   if (rows <= 0) return QVX_OK;
   if (!d_out || (cols > 0 && (!d_w || !d_X))) return QVX_E_NULL;
-  plan->calls.push_back({d_out, d_w, type, d_X, n_vec, rows, cols});
+  plan->calls.push_back({d_out, d_w, type, d_X, n_vec, rows, cols, plan->open_group});
+  return QVX_OK;
+}
+
+int qvx_plan_fork(qvx_plan* plan) {
+  if (!plan) return QVX_E_NULL;
+  if (plan->exec || plan->open_group >= 0) return QVX_E_STATE;
+  plan->open_group = plan->groups++;
+  return QVX_OK;
+}
+
+int qvx_plan_join(qvx_plan* plan) {
+  if (!plan) return QVX_E_NULL;
+  if (plan->exec || plan->open_group < 0) return QVX_E_STATE;
+  plan->open_group = -1;
   return QVX_OK;
 }
 
@@ -301,28 +318,75 @@ int qvx_plan_run_eager(const qvx_plan* plan, void* stream) {
   return QVX_OK;
 }
 
+// Records the plan's calls on `cs` (which is capturing).  A group of n independent calls gets
+// n branches: the first on `cs`, the others on side streams that wait for the fork point and are
+// joined back into `cs` after the group.
+static int plan_record(const qvx_plan* plan, hipStream_t cs, std::vector<hipStream_t>& side,
+                       std::vector<hipEvent_t>& events) {
+  const auto& calls = plan->calls;
+  auto event = [&](hipEvent_t* e) {
+    if (hipEventCreateWithFlags(e, hipEventDisableTiming) != hipSuccess) return false;
+    events.push_back(*e);
+    return true;
+  };
+  for (size_t i = 0; i < calls.size();) {
+    const int g = calls[i].group;
+    size_t n = 1;
+    while (g >= 0 && i + n < calls.size() && calls[i + n].group == g) ++n;
+    if (n == 1) {
+      const auto& c = calls[i];
+      if (int rc = gemv(c.out, c.w, c.type, c.X, c.nvec, c.rows, c.cols, cs); rc != QVX_OK) return rc;
+      ++i;
+      continue;
+    }
+    while (side.size() < n - 1) {
+      hipStream_t st = nullptr;
+      if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess) return QVX_E_HIP;
+      side.push_back(st);
+    }
+    hipEvent_t fork = nullptr;
+    if (!event(&fork) || hipEventRecord(fork, cs) != hipSuccess) return QVX_E_HIP;
+    for (size_t k = 0; k < n; ++k) {
+      const auto& c = calls[i + k];
+      hipStream_t st = k == 0 ? cs : side[k - 1];
+      if (k > 0 && hipStreamWaitEvent(st, fork, 0) != hipSuccess) return QVX_E_HIP;
+      if (int rc = gemv(c.out, c.w, c.type, c.X, c.nvec, c.rows, c.cols, st); rc != QVX_OK) return rc;
+    }
+    for (size_t k = 1; k < n; ++k) {
+      hipEvent_t done = nullptr;
+      if (!event(&done) || hipEventRecord(done, side[k - 1]) != hipSuccess ||
+          hipStreamWaitEvent(cs, done, 0) != hipSuccess)
+        return QVX_E_HIP;
+    }
+    i += n;
+  }
+  return QVX_OK;
+}
+
 int qvx_plan_instantiate(qvx_plan* plan) {
   if (!plan) return QVX_E_NULL;
   if (plan->exec) return QVX_OK;
+  plan->open_group = -1;
   DeviceGuard guard(plan->device);
   if (!guard.ok) return QVX_E_HIP;
-  // Capture on a stream of the plan's own (default priority), in thread-local mode: the GEMV
+  // Capture on streams of the plan's own (default priority), in thread-local mode: the GEMV
   // launches make no calls that capture forbids.
   hipStream_t cs = nullptr;
   if (hipStreamCreateWithFlags(&cs, hipStreamNonBlocking) != hipSuccess) return QVX_E_HIP;
+  std::vector<hipStream_t> side;
+  std::vector<hipEvent_t> events;
   int rc = QVX_OK;
   hipGraph_t graph = nullptr;
   if (hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal) != hipSuccess) {
     rc = QVX_E_HIP;
   } else {
-    for (const auto& c : plan->calls) {
-      rc = gemv(c.out, c.w, c.type, c.X, c.nvec, c.rows, c.cols, cs);
-      if (rc != QVX_OK) break;
-    }
+    rc = plan_record(plan, cs, side, events);
     if (hipStreamEndCapture(cs, &graph) != hipSuccess && rc == QVX_OK) rc = QVX_E_HIP;
   }
   hipGraphExec_t exec = nullptr;
   if (rc == QVX_OK && hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) != hipSuccess) rc = QVX_E_HIP;
+  for (hipEvent_t e : events) (void)hipEventDestroy(e);
+  for (hipStream_t st : side) (void)hipStreamDestroy(st);
   (void)hipStreamDestroy(cs);
   if (rc != QVX_OK) {
     if (graph) (void)hipGraphDestroy(graph);

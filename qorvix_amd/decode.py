@@ -125,6 +125,16 @@ class Plan:
         if rc != OK:
             raise QvxError(rc, "qvx_plan_add_qmatmul_n")
 
+    def fork(self) -> None:
+        rc = lib().qvx_plan_fork(self._h)
+        if rc != OK:
+            raise QvxError(rc, "qvx_plan_fork")
+
+    def join(self) -> None:
+        rc = lib().qvx_plan_join(self._h)
+        if rc != OK:
+            raise QvxError(rc, "qvx_plan_join")
+
     def __len__(self) -> int:
         return lib().qvx_plan_size(self._h)
 
@@ -159,7 +169,7 @@ class DecodeStep:
     """The weight side of one decode step at M vectors: activation stand-ins, per-projection
     outputs, and the plan of 7 GEMVs per layer + the LM head in the reference's order."""
 
-    def __init__(self, model: Model, m: int, seed: int = 9, device="cuda"):
+    def __init__(self, model: Model, m: int, seed: int = 9, device="cuda", concurrent: bool = False):
         import torch
         self.model, self.m = model, m
         f32 = dict(dtype=torch.float32, device=device)
@@ -173,7 +183,13 @@ class DecodeStep:
             w = model.layers[l][name] if l < len(model.layers) else model.lm_head
             y = torch.empty((m, rows), **f32)
             self.outputs.append((l, name, y))
+            # q/k/v read the same normed state, and so do gate/up: independent branches when asked
+            # (measured slower on MI355X: the graph's cross-branch joins cost more than the overlap)
+            if concurrent and name in ("wq", "ffn_gate"):
+                self.plan.fork()
             self.plan.add(y, w, self.inputs[src], m)
+            if concurrent and name in ("wv", "ffn_up"):
+                self.plan.join()
         self.plan.instantiate()
 
     def replay(self, stream: int) -> None:

@@ -20,10 +20,10 @@ def small_model(cuda):
     return decode.Model.synthetic(n_layers=2, lm_head=True, seed=7)
 
 
-@pytest.mark.parametrize("m", [1, 8])
-def test_plan_replays_match_eager(cuda, small_model, m):
+@pytest.mark.parametrize("m,concurrent", [(1, True), (8, True), (1, False)])
+def test_plan_replays_match_eager(cuda, small_model, m, concurrent):
     torch = cuda
-    step = decode.DecodeStep(small_model, m, seed=m)
+    step = decode.DecodeStep(small_model, m, seed=m, concurrent=concurrent)
     assert len(step.plan) == 2 * 7 + 1
     s = torch.cuda.current_stream().cuda_stream
     step.run_eager(s)
@@ -68,6 +68,10 @@ def test_plan_state_and_argument_errors(cuda):
         p.launch(0)
     assert e.value.code == qvx.E_STATE
     lib = qvx.lib()
+    assert lib.qvx_plan_join(p._h) == qvx.E_STATE
+    assert lib.qvx_plan_fork(p._h) == qvx.OK
+    assert lib.qvx_plan_fork(p._h) == qvx.E_STATE
+    assert lib.qvx_plan_join(p._h) == qvx.OK
     assert lib.qvx_plan_add_qmatmul_n(p._h, y.data_ptr(), W.data_ptr(), 99, x.data_ptr(), 1, 16, 256) == qvx.E_TYPE
     assert lib.qvx_plan_add_qmatmul_n(p._h, y.data_ptr(), W.data_ptr(), qvx.Q4_K, x.data_ptr(), 1, 16, 200) == qvx.E_SHAPE
     assert lib.qvx_plan_add_qmatmul_n(p._h, y.data_ptr(), W.data_ptr(), qvx.Q4_K, x.data_ptr(), 0, 16, 256) == qvx.E_NVEC
@@ -76,6 +80,7 @@ def test_plan_state_and_argument_errors(cuda):
     p.add(y, decode.DevWeight(W, qvx.Q4_K, 16, 256), x, 1)
     p.instantiate()
     assert lib.qvx_plan_add_qmatmul_n(p._h, y.data_ptr(), W.data_ptr(), qvx.Q4_K, x.data_ptr(), 1, 16, 256) == qvx.E_STATE
+    assert lib.qvx_plan_fork(p._h) == qvx.E_STATE
     p.launch(torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     p.close()
