@@ -303,10 +303,10 @@ __device__ inline float span_sum(float s, int width) {
 template <uint32_t T, int NV>
 __device__ inline const float* task_x(const float* X, int cols, int S, int t) {
   using L = Lane<T>;
-  static_assert(NV == 1 || NV == 2, "one or two vectors per launch");
+  static_assert(NV >= 1 && NV <= 4, "one to four vectors per launch");
   constexpr int R = L::kR;
   const int vs = t / (2 * R), part = t % (2 * R);
-  const int v = (NV == 2 && vs >= S) ? 1 : 0, s = vs - v * S;
+  const int v = NV == 1 ? 0 : vs / S, s = vs - v * S;
   return X + (size_t)v * cols + L::xoff(s, part >> 1) + 8 * (part & 1);
 }
 
@@ -557,13 +557,28 @@ static void launch_nv(const void* w, const float* X, float* Y, int rows, int col
 template <uint32_t T>
 static void launch_type(const void* w, const float* X, float* Y, int nvec, int rows, int cols, const Geo& geo,
                         hipStream_t s) {
-  for (int v0 = 0; v0 < nvec; v0 += 2) {
+  // Q6_K takes four vectors a launch when their activations fit in LDS (its 4-vector kernels
+  // stay within the register file; the other formats' would spill), so the weights are streamed
+  // once per four vectors instead of once per two.
+  const bool nv4 = T == T_Q6_K && gemv_lds_bytes<T>(4, geo.S) <= 150 * 1024;
+  for (int v0 = 0; v0 < nvec;) {
     const float* Xv = X + (size_t)v0 * cols;
     float* Yv = Y + (size_t)v0 * rows;
-    if (nvec - v0 >= 2)
+    const int left = nvec - v0;
+    if constexpr (T == T_Q6_K) {
+      if (nv4 && left >= 4) {
+        launch_nv<T, 4>(w, Xv, Yv, rows, cols, geo, s);
+        v0 += 4;
+        continue;
+      }
+    }
+    if (left >= 2) {
       launch_nv<T, 2>(w, Xv, Yv, rows, cols, geo, s);
-    else
+      v0 += 2;
+    } else {
       launch_nv<T, 1>(w, Xv, Yv, rows, cols, geo, s);
+      v0 += 1;
+    }
   }
 }
 
