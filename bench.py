@@ -5,9 +5,12 @@
 A step is one Q4_K GEMV 4096 -> 14336 at M=1 (gate/up shape) over one of
 `--copies` distinct seeded weight copies (>= 1 GiB in total, so every timed read comes from HBM
 rather than the 256 MB Infinity Cache).  `value` is algorithmic bytes per step (weights +
-activation + output) / time per step, with inputs resident in HBM.  The prefill GEMM
+activation + output) / time per step, with inputs resident in HBM; the K steps are recorded once
+into one HIP graph (a qvx_plan) and replayed, so the time is the device's, not the host's per-call
+launch cost (the eager launch loop is timed too and reported beside it).  The prefill GEMM
 (Q4_K 4096 -> 14336, fp16 X, M in {2048, 512, 128}; bf16 MFMA, fp16 MFMA and
-int8 MFMA variants) is reported beside it.  `cpu_baseline` times the reference's own CPU qmatmul
+int8 MFMA variants) is reported beside it, and so are every GEMV point of configs[0..2] and the
+config-5 decode sweep.  `cpu_baseline` times the reference's own CPU qmatmul
 (oracle/_ref, built from the reference's sources) on the same weights on this host's cores.
 `roofline.traffic` comes from the committed rocprofv3 PMC summary of this same GEMV
 (profiles/q4k_gemv_4096x14336_m1.traffic.json: FETCH_SIZE / WRITE_SIZE per dispatch, each scaled
@@ -81,6 +84,62 @@ def cpu_baseline(w_host, x_host, rows, cols, budget_s=5.0):
     }
 
 
+# BASELINE configs[0..2] GEMV points: (name, ggml type, rows, cols, M values, scale multiplier)
+CONFIG_GEMVS = (
+    ("C1 Q8_0 4096x4096", 8, 4096, 4096, (1,), 0.01),
+    ("C2 Q4_0 up 4096->11008", 2, 11008, 4096, (1,), 0.02),
+    ("C2 Q4_0 down 11008->4096", 2, 4096, 11008, (1,), 0.02),
+    ("C3 Q4_K gate/up 4096->14336", 12, 14336, 4096, (1, 4, 16), 1e-3),
+    ("C3 Q4_K down 14336->4096", 12, 4096, 14336, (1, 4, 16), 1e-3),
+    ("C3 Q6_K lm_head 4096->128256", 14, 128256, 4096, (1, 4, 16), 1e-3),
+)
+
+
+def config_gemvs(torch, stream, steps):
+    """Every GEMV point of BASELINE configs[0..2]: enough seeded weight copies (>= 1 GiB) cycled so
+    each launch reads HBM; n qmatmul_n calls recorded into one HIP graph (a qvx_plan), replayed,
+    and timed with HIP events (the device's time per call, not the host's per-call cost)."""
+    import qorvix_amd as qvx
+    from qorvix_amd import decode
+    sh = stream.cuda_stream
+    out = []
+    for name, t, rows, cols, ms, mul in CONFIG_GEMVS:
+        wb = qvx.weight_bytes(t, rows, cols)
+        ncopy = max(2, -(-(1 << 30) // wb))
+        ws = [decode.DevWeight(qvx.empty_weight(t, rows, cols), t, rows, cols) for _ in range(ncopy)]
+        for i, w in enumerate(ws):
+            qvx.fill_synthetic_t(w.data, t, rows, cols, seed=1000 + 17 * i + t, scale_mul=mul)
+        for m in ms:
+            X = torch.empty((m, cols), dtype=torch.float32, device="cuda")
+            qvx.fill_normal_t(X, seed=77 + m)
+            Y = torch.empty((m, rows), dtype=torch.float32, device="cuda")
+            n = max(2 * ncopy, min(steps, int(2e-3 / max(wb / 4e12, 1e-6))))  # ~2 ms of work per point
+            plan = decode.Plan()
+            for i in range(n):
+                plan.add(Y, ws[i % ncopy], X, m)
+            plan.instantiate()
+            plan.launch(sh)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            plan.launch(sh)
+            plan.launch(sh)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            plan.close()
+            us = e0.elapsed_time(e1) / (2 * n) * 1e3
+            ab = algorithmic_bytes(rows, cols, m, wb)
+            gbs = ab / (us * 1e-6) / 1e9
+            out.append({"config": name, "M": m, "us": round(us, 2), "algorithmic_bytes": ab, "gb_s": round(gbs, 1),
+                        "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "calls_timed": 2 * n,
+                        "weight_copies": ncopy})
+            log(f"[bench] {name} M={m}: {us:.2f} us, {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak)")
+            del X, Y
+        del ws
+        torch.cuda.empty_cache()
+    return out
+
+
 def decode_sweep(torch, stream, steps):
     """Config 5: the 225 GEMVs of one Llama-3-8B Q4_K_M token (32 layers x q, k, v, o, gate, up,
     down + the Q6_K LM head, 4.54 GiB of weights, cold in HBM every token) replayed as one HIP
@@ -132,6 +191,7 @@ def main():
     ap.add_argument("--gemv-only", action="store_true", help="only the GEMV leg (for profiler passes)")
     ap.add_argument("--sweep-steps", type=int, default=20, help="timed tokens of the config-5 decode sweep")
     ap.add_argument("--sweep-only", action="store_true", help="only the config-5 decode sweep (profiler passes)")
+    ap.add_argument("--configs-only", action="store_true", help="only the configs[0..2] GEMV points (profiler passes)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MiB",
                     help="also run one plain device copy of this many MiB (PMC byte-counter calibration)")
     args = ap.parse_args()
@@ -151,6 +211,9 @@ def main():
     stream = torch.cuda.current_stream()
     if args.sweep_only:  # profiler pass over the decode sweep alone
         print(json.dumps({"sweep": decode_sweep(torch, stream, args.sweep_steps)}), flush=True)
+        return
+    if args.configs_only:  # profiler pass over the configs[0..2] GEMV points alone
+        print(json.dumps({"config_gemvs": config_gemvs(torch, stream, 200)}), flush=True)
         return
     t = qvx.Q4_K
     wbytes = qvx.weight_bytes(t, ROWS, COLS)
@@ -190,11 +253,31 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_total = ev0.elapsed_time(ev1)
-    ms_per_step = ms_total / args.steps
+    ms_eager = ms_total / args.steps
     nbytes = algorithmic_bytes(ROWS, COLS, 1, wbytes)
+    log(f"[bench] GEMV eager: {args.steps} steps in {ms_total:.3f} ms (wall {wall * 1e3:.1f} ms): "
+        f"{ms_eager * 1e3:.2f} us/step, {nbytes / (ms_eager * 1e-3) / 1e9:.0f} GB/s")
+
+    # The same K steps recorded once into a qvx_plan (one HIP graph) and replayed: the device runs
+    # the launches back to back whatever the host's per-call cost, which the eager loop above
+    # includes when a launch takes longer to issue than the kernel takes to run.
+    from qorvix_amd import decode
+    plan = decode.Plan()
+    for i in range(args.steps):
+        plan.add(out, decode.DevWeight(copies[i % len(copies)], t, ROWS, COLS), x, 1)
+    plan.instantiate()
+    plan.launch(sh)
+    torch.cuda.synchronize()
+    reps = 3
+    ev0.record(stream)
+    for _ in range(reps):
+        plan.launch(sh)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    plan.close()
+    ms_per_step = ev0.elapsed_time(ev1) / (reps * args.steps)
     gbs = nbytes / (ms_per_step * 1e-3) / 1e9
-    log(f"[bench] GEMV: {args.steps} steps in {ms_total:.3f} ms (wall {wall * 1e3:.1f} ms): "
-        f"{ms_per_step * 1e3:.2f} us/step, {gbs:.0f} GB/s")
+    log(f"[bench] GEMV graph: {reps} x {args.steps} steps: {ms_per_step * 1e3:.2f} us/step, {gbs:.0f} GB/s")
 
     # per-launch event pairs (kernel duration incl. event overhead), for the roofline line
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(64)]
@@ -250,6 +333,15 @@ def main():
         gemm["error"] = str(e)
         log(f"[bench] GEMM failed: {e}")
 
+    # ---- every GEMV point of BASELINE configs[0..2] ----------------------------------------------
+    cfgs = []
+    if not args.gemv_only:
+        try:
+            cfgs = config_gemvs(torch, stream, 200)
+        except RuntimeError as e:  # report, never hide
+            cfgs = [{"error": str(e)}]
+            log(f"[bench] config GEMVs failed: {e}")
+
     # ---- full-model decode weight sweep ----------------------------------
     sweep = {}
     if not args.gemv_only:
@@ -281,6 +373,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 6),
+        "ms_per_step_eager_loop": round(ms_eager, 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -319,6 +412,7 @@ def main():
             },
             "runs": gemm,
         },
+        "config_gemvs": cfgs,
         "sweep": sweep,
         "cpu_baseline": cpu,
     }

@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstddef>
 #include <cstdint>
 
@@ -108,6 +109,23 @@ __device__ inline float f16hi(uint32_t w) {
 // ((hi:lo) >> 8*s)[31:0] for s in 0..3: realigns a byte stream read as aligned dwords.
 __device__ inline uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32_t s) {
   return __builtin_amdgcn_alignbyte(hi, lo, s);
+}
+
+// Raises a kernel's dynamic-LDS limit to at least `bytes` on the current device.  The attribute
+// persists, so hipFuncSetAttribute runs only when the limit has to grow (have[] holds the limit set
+// per device; one array per kernel): a decode loop does not pay for it on every launch.
+constexpr int kMaxDevices = 64;
+inline void ensure_dyn_lds(const void* kern, std::atomic<int>* have, int bytes) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    return;
+  }
+  int cur = have[dev].load(std::memory_order_relaxed);
+  if (cur >= bytes) return;
+  if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess) return;
+  while (cur < bytes && !have[dev].compare_exchange_weak(cur, bytes, std::memory_order_relaxed)) {
+  }
 }
 
 // SplitMix64 finaliser (Steele, Lea, Flood 2014): a counter-based 64-bit hash for seeded data.

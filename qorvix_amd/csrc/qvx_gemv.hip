@@ -506,9 +506,10 @@ static void launch_t(const void* w, const float* X, float* Y, int rows, int cols
   constexpr int PF = prefetch_rows<T>() < RMAX ? prefetch_rows<T>() : RMAX;
   auto kern = &k_gemv<T, NV, RMAX, TPT, PF>;
   const size_t lds = gemv_lds_bytes<T>(NV, geo.S);
-  if (lds > 64 * 1024)
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)lds);
+  if (lds > 64 * 1024) {
+    static std::atomic<int> have[kMaxDevices];
+    ensure_dyn_lds(reinterpret_cast<const void*>(kern), have, (int)lds);
+  }
   kern<<<(unsigned)nwg, dim3((unsigned)geo.Sp, (unsigned)geo.G), lds, s>>>(static_cast<const uint8_t*>(w), X, Y,
                                                                            rows, cols, geo);
 }

@@ -358,7 +358,8 @@ static void launch_mx(const void* w, const float* X, float* Y, int rows, int col
                       hipStream_t s) {
   auto kern = &k_gemv_mx<NV, NB, TPT>;
   const size_t lds = mx_dyn_bytes(NV, geo.nsb);
-  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  static std::atomic<int> have[kMaxDevices];
+  ensure_dyn_lds(reinterpret_cast<const void*>(kern), have, (int)lds);
   kern<<<(unsigned)nwg, 1024u, lds, s>>>(static_cast<const uint8_t*>(w), X, Y, rows, cols, geo);
 }
 
