@@ -24,6 +24,9 @@ bool launch_gemv_fast(uint32_t t, const void* w, const float* X, float* Y, int n
 int gemv_mx_max_nv(int cols);
 bool launch_gemv_mx_q4k(const void* w, const float* X, float* Y, int nvec, int rows, int cols, size_t row_bytes,
                         hipStream_t s);
+int gemv_mxb_supported(int cols);
+bool launch_gemv_mxb_q4k(const void* w, const float* X, float* Y, int nvec, int rows, int cols, size_t row_bytes,
+                         hipStream_t s);
 bool launch_fill_synthetic(void* w, uint32_t t, size_t nblk, uint64_t seed, float mul, hipStream_t s);
 void launch_fill_normal_f32(float* x, size_t n, uint64_t seed, float mul, hipStream_t s);
 void launch_fill_normal_f16(uint16_t* x, size_t n, uint64_t seed, float mul, hipStream_t s);
@@ -97,6 +100,19 @@ int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int
   // same in every launch, so batches stay bit-identical to single vectors.  Q4_K runs on the matrix
   // cores (up to gemv_mx_max_nv vectors per launch), the other formats on the VALU kernel; shapes
   // neither covers go to the generic kernel.
+  // Q4_K batches of two or more vectors take the batched matrix-core form (8 vectors a launch,
+  // bit-identical to the one-vector form) where its fragments fit in LDS.
+  if (fast && type == T_Q4_K && nvec >= 2 && gemv_mxb_supported(cols)) {
+    for (int v0 = 0; v0 < nvec; v0 += 8) {
+      const int nv = nvec - v0 < 8 ? nvec - v0 : 8;
+      const bool ok = nv == 1 ? launch_gemv_mx_q4k(w, X + (size_t)v0 * cols, out + (size_t)v0 * rows, 1, rows, cols,
+                                                   row_bytes, s)
+                              : launch_gemv_mxb_q4k(w, X + (size_t)v0 * cols, out + (size_t)v0 * rows, nv, rows,
+                                                    cols, row_bytes, s);
+      if (!ok) return QVX_E_TYPE;
+    }
+    return hip_status();
+  }
   const int mx = (fast && type == T_Q4_K) ? gemv_mx_max_nv(cols) : 0;
   if (mx > 0) {
     for (int v0 = 0; v0 < nvec; v0 += mx) {

@@ -137,8 +137,16 @@ __device__ inline int task_vec(int t, int per) {
   return v;
 }
 
-__device__ inline void mx_convert(const float4 x0, const float4 x1, int v, int sg, int part, bool store,
-                                  uint8_t* frag, float* meta, int nsb) {
+// The 15-bit fixed-point form of one task's 8 activations: qh / ql bytes (elements 0..3 in h0 / l0,
+// 4..7 in h1 / l1), the group's step sx (NaN when the group holds a non-finite value) and the sum
+// of q over the task's half of the group.  Every lane of the wave calls it (DPP across the 8 tasks
+// of a group).  Both GEMV layouts convert through this one function, so their arithmetic agrees.
+struct XQ8 {
+  uint32_t h0, h1, l0, l1;
+  float sx;
+  int sq;
+};
+__device__ inline XQ8 mx_quantize(const float4 x0, const float4 x1) {
   float a = fmaxf(fmaxf(fmaxf(fabsf(x0.x), fabsf(x0.y)), fmaxf(fabsf(x0.z), fabsf(x0.w))),
                   fmaxf(fmaxf(fabsf(x1.x), fabsf(x1.y)), fmaxf(fabsf(x1.z), fabsf(x1.w))));
   // 0 when the eight elements are finite, NaN otherwise (x * 0 is NaN for +-Inf and NaN)
@@ -169,16 +177,27 @@ __device__ inline void mx_convert(const float4 x0, const float4 x1, int v, int s
   for (int i = 0; i < 4; ++i) sq = __builtin_amdgcn_sdot2(__builtin_bit_cast(short2_t, p[i]), ones, sq, false);
   sq += dppi<kXor1>(sq);
   sq += dppi<kXor2>(sq);  // sum of q over the 32 elements of this task's half of the group
+  XQ8 r;
+  r.h0 = __builtin_amdgcn_perm(hs[1], hs[0], 0x06040200u);
+  r.h1 = __builtin_amdgcn_perm(hs[3], hs[2], 0x06040200u);
+  r.l0 = __builtin_amdgcn_perm(ls[1], ls[0], 0x06040200u);
+  r.l1 = __builtin_amdgcn_perm(ls[3], ls[2], 0x06040200u);
+  r.sx = a * (1.0f / 16383.0f) + z;
+  r.sq = sq;
+  return r;
+}
+
+__device__ inline void mx_convert(const float4 x0, const float4 x1, int v, int sg, int part, bool store,
+                                  uint8_t* frag, float* meta, int nsb) {
+  const XQ8 q = mx_quantize(x0, x1);
   if (store) {
-    const uint32_t h0 = __builtin_amdgcn_perm(hs[1], hs[0], 0x06040200u), h1 = __builtin_amdgcn_perm(hs[3], hs[2], 0x06040200u);
-    const uint32_t l0 = __builtin_amdgcn_perm(ls[1], ls[0], 0x06040200u), l1 = __builtin_amdgcn_perm(ls[3], ls[2], 0x06040200u);
     const int g = sg & 3, s = sg >> 2, hi = part >> 2, m = part & 3;
     const uint32_t f = lds_addr(frag) + (uint32_t)((v * nsb + s) * kFragBytes + g * 128 + 2 * hi * 32 + m * 8);
-    lds_write8(f, h0, h1);       // part 2hi: qh
-    lds_write8(f + 32, l0, l1);  // part 2hi + 1: ql
+    lds_write8(f, q.h0, q.h1);       // part 2hi: qh
+    lds_write8(f + 32, q.l0, q.l1);  // part 2hi + 1: ql
     const uint32_t mt = lds_addr(meta) + (uint32_t)(((v * nsb + s) * 4 + g) * 16);  // [sx, Qa, Qb, 128 Qb as int]
-    if (part == 0) lds_write8(mt, __builtin_bit_cast(uint32_t, a * (1.0f / 16383.0f) + z), __builtin_bit_cast(uint32_t, (float)sq));
-    if (part == 4) lds_write8(mt + 8, __builtin_bit_cast(uint32_t, (float)sq), (uint32_t)(128 * sq));
+    if (part == 0) lds_write8(mt, __builtin_bit_cast(uint32_t, q.sx), __builtin_bit_cast(uint32_t, (float)q.sq));
+    if (part == 4) lds_write8(mt + 8, __builtin_bit_cast(uint32_t, (float)q.sq), (uint32_t)(128 * q.sq));
   }
 }
 
@@ -350,6 +369,209 @@ __global__ __launch_bounds__(1024) void k_gemv_mx(const uint8_t* __restrict__ W,
   }
 }
 
+// ---- batched form: 2..8 vectors a launch ------------------------------------------------------
+// One v_mfma_i32_16x16x32_i8 per 32-element sub-block of the tile serves 8 vectors:
+//  * B (16 columns = weight rows j, K = 32): lane (j, kg) supplies the codes of elements
+//    8kg..8kg+7 of sub-block sb: low nibbles (even sb) or high nibbles (odd sb) of qs bytes
+//    32(sb/2) + 8kg..8kg+7 of row j, as bytes 0..15 (no offset).
+//  * A (16 rows = (vector u, part p), row 2u + p): lane (2u + p, kg) holds qh (p = 0) or ql
+//    (p = 1) of vector u at the same elements.  The fragments of one sub-block are 512 bytes,
+//    [kg][row] x 8 bytes, so a wave reads them with one conflict-free ds_read_b64.
+//  * D: lane (j, r) holds rows 4r..4r+3 = (vector 2r: qh, ql), (vector 2r+1: qh, ql) of column j:
+//    the integers sum n*q of sub-block sb for two vectors.
+// The lane keeps one accumulator per (vector, group), folds each group exactly as the one-vector
+// kernel does (the same integers ta = sum n q of sub-block 2c and tb = 16 sum n q of sub-block
+// 2c+1, the same float expression, the same order over super-blocks), combines the groups as
+// (g0 + g2) + (g1 + g3) -- the order of that kernel's permlane sums -- and the K-split waves in
+// wave order with the same geometry.  So every output is bit-identical to the one-vector kernel's,
+// which keeps qvx_qmatmul_n bit-identical to qvx_qmatmul per vector.
+
+constexpr int kSubBytes = 512;  // A fragments of one sub-block for 8 vectors
+
+// LDS: dynamic [fragments: nsb*8*512][meta: nsb*4 groups*8 vectors*16] and a static tile ring
+// [16 waves][2][2304].
+__host__ __device__ inline size_t mxb_frag_bytes(int nsb) { return (size_t)nsb * 8 * kSubBytes; }
+__host__ __device__ inline size_t mxb_meta_bytes(int nsb) { return (size_t)nsb * 4 * 8 * 16; }
+__host__ __device__ inline size_t mxb_dyn_bytes(int nsb) { return mxb_frag_bytes(nsb) + mxb_meta_bytes(nsb); }
+__host__ __device__ inline size_t mxb_lds_bytes(int nsb) { return mxb_dyn_bytes(nsb) + (size_t)16 * 2 * kTileBytes; }
+
+__device__ inline void mxb_convert(const float4 x0, const float4 x1, int v, int sg, int part, bool store,
+                                   uint8_t* frag, float* meta) {
+  const XQ8 q = mx_quantize(x0, x1);
+  if (store) {
+    const int g = sg & 3, s = sg >> 2, sb = 2 * g + (part >> 2), kg = part & 3;
+    const uint32_t f = lds_addr(frag) + (uint32_t)((s * 8 + sb) * kSubBytes + (kg * 16 + 2 * v) * 8);
+    lds_write8(f, q.h0, q.h1);      // row 2v: qh
+    lds_write8(f + 8, q.l0, q.l1);  // row 2v + 1: ql
+    const uint32_t mt = lds_addr(meta) + (uint32_t)(((s * 4 + g) * 8 + v) * 16);  // [sx, Qa, Qb, 128 Qb as int]
+    if (part == 0) lds_write8(mt, __builtin_bit_cast(uint32_t, q.sx), __builtin_bit_cast(uint32_t, (float)q.sq));
+    if (part == 4) lds_write8(mt + 8, __builtin_bit_cast(uint32_t, (float)q.sq), (uint32_t)(128 * q.sq));
+  }
+}
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+__device__ inline u32x2 lds_read8(uint32_t addr) {
+  u32x2 r;
+  asm volatile("ds_read_b64 %0, %1" : "=v"(r) : "v"(addr) : "memory");
+  return r;
+}
+__device__ inline void lds_wait5(u32x4& a, u32x2& b, u32x2& c, u32x2& d, u32x2& e) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e)::"memory");
+}
+__device__ inline void lds_wait16(u32x2 (&a)[8], u32x4 (&m)[8]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]), "+v"(a[6]), "+v"(a[7]),
+                 "+v"(m[0]), "+v"(m[1]), "+v"(m[2]), "+v"(m[3]), "+v"(m[4]), "+v"(m[5]), "+v"(m[6]), "+v"(m[7])::"memory");
+}
+
+// Scale / min of sub-blocks 2c, 2c+1 of a Q4_K header (the 6-bit fields, as the one-vector kernel
+// unpacks them for its lane group c).
+__device__ inline void q4k_group_scales(const u32x4& hd, int c, float& sca, float& scb16, float& mna, float& mnb) {
+  const uint32_t jj = 2u * (uint32_t)(c & 1);
+  const uint32_t sel1 = jj | (jj + 1) << 8 | (jj + 4) << 16 | (jj + 5) << 24;
+  const uint32_t sel2 = jj | (jj + 1) << 8 | jj << 16 | (jj + 1) << 24;
+  const bool up = c >= 2;
+  const uint32_t m1 = up ? 0u : 0x3F3F3F3Fu, m2 = up ? 0x30303030u : 0u, m3 = up ? 0x00000F0Fu : 0u,
+                 m4 = up ? 0x0F0F0000u : 0u;
+  const uint32_t p1 = __builtin_amdgcn_perm(hd.z, hd.y, sel1), p2 = __builtin_amdgcn_perm(hd.w, hd.w, sel2);
+  const uint32_t sm = (p1 & m1) | ((p1 >> 2) & m2) | (p2 & m3) | ((p2 >> 4) & m4);
+  sca = (float)(sm & 0xFFu);
+  scb16 = (float)((sm >> 8) & 0xFFu) * 0.0625f;
+  mna = (float)((sm >> 16) & 0xFFu);
+  mnb = (float)(sm >> 24);
+}
+
+template <int TPT>
+__global__ __launch_bounds__(1024) void k_gemv_mxb(const uint8_t* __restrict__ W, const float* __restrict__ X,
+                                                   float* __restrict__ Y, int rows, int cols, int nv, MxGeo geo) {
+  constexpr int NB = 2;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  __shared__ __attribute__((aligned(16))) uint8_t ring[16 * NB * kTileBytes];
+  const int nsb = geo.nsb, TQ = geo.TQ, KQ = geo.KQ;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  uint8_t* frag = lds;
+  float* meta = reinterpret_cast<float*>(lds + mxb_frag_bytes(nsb));
+  QVX_LDS uint8_t* stage = (QVX_LDS uint8_t*)(ring + wave * NB * kTileBytes);
+
+  const int b = blockIdx.x;
+  const int rb = b * geo.base + min(b, geo.rem), cnt = geo.base + (b < geo.rem ? 1 : 0);
+  const int tq = wave % TQ, kq = wave / TQ;
+  const int s0 = kq * nsb / KQ, s1 = (kq + 1) * nsb / KQ, nu = s1 - s0;
+
+  // 1. activations -> A fragments (waves with conversion tasks), before any copy
+  const int per = nsb * 32, ntask = nv * per;
+#pragma unroll
+  for (int k = 0; k < TPT; ++k) {
+    if (1024 * k + 64 * wave < ntask) {
+      const int t0 = tid + 1024 * k, t = min(t0, ntask - 1), v = t / per, r = t - v * per;
+      const float4* src = reinterpret_cast<const float4*>(X + (size_t)v * cols + 8 * r);
+      mxb_convert(src[0], src[1], v, r >> 3, r & 7, t0 < ntask, frag, meta);
+    }
+  }
+
+  // 2. prologue copies (as the one-vector kernel)
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(W + (size_t)rb * geo.row_bytes), (short)0, (int)((uint32_t)cnt * geo.row_bytes), (int)kRsrcWord3);
+  uint32_t off[3];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    const uint32_t p = k < 2 ? (uint32_t)(1024 * k + 16 * lane) : (uint32_t)(2048 + 4 * lane);
+    const uint32_t r = p / (uint32_t)kSB, c = p - (uint32_t)kSB * r;
+    off[k] = __umul24(16u * (uint32_t)tq + r, geo.row_bytes) + c;
+  }
+  const int s_last = max(s0, s1 - 1);
+#pragma unroll
+  for (int u = 0; u < NB; ++u) mx_issue(rsrc, off, min(s0 + u, s_last), stage + u * kTileBytes);
+
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's fragment stores
+  __builtin_amdgcn_s_barrier();
+
+  // 3. tiles
+  const int j = lane & 15, r4 = lane >> 4;  // B column (tile row) and K block; D rows 4 r4..4 r4+3
+  const uint32_t b_hd = kSB * j, b_q = kSB * j + 16 + 8 * r4;
+  const uint32_t frag_base = lds_addr(frag) + 8u * (uint32_t)lane;
+  const uint32_t meta_base = lds_addr(meta) + 32u * (uint32_t)r4;  // vectors 2 r4, 2 r4 + 1
+  const uint32_t stage_base = (uint32_t)(uintptr_t)stage;
+  float acc[2][4];
+#pragma unroll
+  for (int e = 0; e < 2; ++e)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[e][c] = 0.0f;
+
+  int slot = 0;
+  const int nlast = max(nu, NB) - 1;
+  for (int u = 0; u < nu; ++u) {
+    if (min(NB - 1, nlast - u) >= 1) wait_vm<3>();
+    else wait_vm<0>();
+    const int s = s0 + u;
+    const uint32_t st = stage_base + (uint32_t)slot * kTileBytes;
+    u32x4 hd = lds_read16(st + b_hd);
+    u32x2 q0 = lds_read8(st + b_q), q1 = lds_read8(st + b_q + 32), q2 = lds_read8(st + b_q + 64),
+          q3 = lds_read8(st + b_q + 96);
+    lds_wait5(hd, q0, q1, q2, q3);
+    if (u + NB < nu) mx_issue(rsrc, off, s + NB, stage + slot * kTileBytes);
+    slot = slot + 1 == NB ? 0 : slot + 1;
+    const float d = f16lo(hd.x), dmin = f16hi(hd.x);
+    const u32x2 qq[4] = {q0, q1, q2, q3};
+    // every A fragment and activation record of the tile in one round trip
+    u32x2 af[8];
+    u32x4 mf[8];
+    const uint32_t fa = frag_base + (uint32_t)(s * 8) * kSubBytes;
+    const uint32_t ma = meta_base + (uint32_t)(s * 4 * 8) * 16u;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) af[k] = lds_read8(fa + (uint32_t)k * kSubBytes);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      mf[2 * c] = lds_read16(ma + (uint32_t)c * 128u);
+      mf[2 * c + 1] = lds_read16<16>(ma + (uint32_t)c * 128u);
+    }
+    lds_wait16(af, mf);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const u32x2 bl = {qq[c].x & 0x0F0F0F0Fu, qq[c].y & 0x0F0F0F0Fu};
+      const u32x2 bh = {(qq[c].x >> 4) & 0x0F0F0F0Fu, (qq[c].y >> 4) & 0x0F0F0F0Fu};
+      const v4i zero = {0, 0, 0, 0};
+      const v4i da = __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, af[2 * c]),
+                                                           __builtin_bit_cast(long, bl), zero, 0, 0, 0);
+      const v4i db = __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, af[2 * c + 1]),
+                                                           __builtin_bit_cast(long, bh), zero, 0, 0, 0);
+      float sca, scb16, mna, mnb;
+      q4k_group_scales(hd, c, sca, scb16, mna, mnb);
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const u32x4 mt = mf[2 * c + e];  // [sx, Qa, Qb, 128 Qb]
+        const int ta = (int)((uint32_t)da[2 * e] << 7) + da[2 * e + 1];                      // sum n q, sub-block 2c
+        const int tb = (int)((((uint32_t)db[2 * e] << 7) + (uint32_t)db[2 * e + 1]) << 4);  // 16 sum n q, 2c+1
+        const float t = __builtin_fmaf((float)tb, scb16, (float)ta * sca);
+        const float w = __builtin_fmaf(__uint_as_float(mt.z), mnb, __uint_as_float(mt.y) * mna);
+        acc[e][c] = __builtin_fmaf(__builtin_fmaf(d, t, -dmin * w), __uint_as_float(mt.x), acc[e][c]);
+      }
+    }
+  }
+
+  wait_vm<0>();
+
+  // 4. groups as (g0 + g2) + (g1 + g3), then the KQ waves of the tile in wave order
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(ring);  // [tq][kq][v][16]
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int v = 2 * r4 + e;
+    if (v < nv) red[((tq * KQ + kq) * nv + v) * 16 + j] = (acc[e][0] + acc[e][2]) + (acc[e][1] + acc[e][3]);
+  }
+  __syncthreads();
+  for (int o = tid; o < TQ * nv * 16; o += 1024) {
+    const int t = o / (nv * 16), v = (o >> 4) % nv, r = o & 15;
+    const int row = 16 * t + r;
+    if (row < cnt) {
+      float sum = 0.0f;
+      for (int k = 0; k < KQ; ++k) sum += red[((t * KQ + k) * nv + v) * 16 + r];
+      Y[(size_t)v * rows + rb + row] = sum;
+    }
+  }
+}
+
 constexpr int kCUs = 256;
 constexpr size_t kLdsMax = 160 * 1024;
 
@@ -375,7 +597,55 @@ static void launch_mx_nv(const void* w, const float* X, float* Y, int rows, int 
   return launch_mx<NV, 2, 4>(w, X, Y, rows, cols, geo, nwg, s);
 }
 
+// Launch geometry shared by both forms (the batched form's bit-identity rests on it): one
+// workgroup of 16 waves per CU; tiles of 16 rows; TQ tiles x KQ K-splits per workgroup.
+static int mx_geometry(int rows, int cols, size_t row_bytes, MxGeo& geo) {
+  geo.nsb = cols / 256;
+  geo.row_bytes = (uint32_t)row_bytes;
+  int64_t nwg = std::min<int64_t>(kCUs, ((int64_t)rows + 15) / 16);
+  nwg = std::max<int64_t>(nwg, ((int64_t)rows + 255) / 256);
+  geo.base = (int)(rows / nwg);
+  geo.rem = (int)(rows % nwg);
+  const int per = geo.base + (geo.rem ? 1 : 0);
+  int tq = 1;
+  while (16 * tq < per) tq <<= 1;
+  geo.TQ = tq;
+  geo.KQ = 16 / tq;
+  return (int)nwg;
+}
+
+template <int TPT>
+static void launch_mxb(const void* w, const float* X, float* Y, int nv, int rows, int cols, const MxGeo& geo, int nwg,
+                       hipStream_t s) {
+  auto kern = &k_gemv_mxb<TPT>;
+  const size_t lds = mxb_dyn_bytes(geo.nsb);
+  static std::atomic<int> have[kMaxDevices];
+  ensure_dyn_lds(reinterpret_cast<const void*>(kern), have, (int)lds);
+  kern<<<(unsigned)nwg, 1024u, lds, s>>>(static_cast<const uint8_t*>(w), X, Y, rows, cols, nv, geo);
+}
+
 }  // namespace
+
+// 1 if the batched form takes `cols` (its 8-vector fragments fit in LDS with the tile ring).
+int gemv_mxb_supported(int cols) {
+  if (cols <= 0 || cols % 256 != 0) return 0;
+  const int nsb = cols / 256;
+  return mxb_lds_bytes(nsb) <= kLdsMax && (8 * nsb * 32 + 1023) / 1024 <= 4 ? 1 : 0;
+}
+
+// Q4_K GEMV on the matrix cores, 1 <= nvec <= 8 vectors, batched form.  Returns false, having
+// launched nothing, when the shape is not handled here.
+bool launch_gemv_mxb_q4k(const void* w, const float* X, float* Y, int nvec, int rows, int cols, size_t row_bytes,
+                         hipStream_t s) {
+  if (!gemv_mxb_supported(cols) || nvec < 1 || nvec > 8 || row_bytes >= (1u << 24)) return false;
+  MxGeo geo{};
+  const int nwg = mx_geometry(rows, cols, row_bytes, geo);
+  const int tpt = (nvec * geo.nsb * 32 + 1023) / 1024;
+  if (tpt <= 1) launch_mxb<1>(w, X, Y, nvec, rows, cols, geo, nwg, s);
+  else if (tpt <= 2) launch_mxb<2>(w, X, Y, nvec, rows, cols, geo, nwg, s);
+  else launch_mxb<4>(w, X, Y, nvec, rows, cols, geo, nwg, s);
+  return true;
+}
 
 // Largest vector count one launch takes for a row of `cols` columns (LDS budget), 0 if the shape
 // is not handled here.
@@ -394,27 +664,16 @@ bool launch_gemv_mx_q4k(const void* w, const float* X, float* Y, int nvec, int r
   const int maxnv = gemv_mx_max_nv(cols);
   if (maxnv == 0 || nvec < 1 || nvec > maxnv || row_bytes >= (1u << 24)) return false;
   MxGeo geo{};
-  geo.nsb = cols / 256;
-  geo.row_bytes = (uint32_t)row_bytes;
-  // one workgroup of 16 waves per CU; tiles of 16 rows; TQ tiles x KQ K-splits per workgroup
-  int64_t nwg = std::min<int64_t>(kCUs, ((int64_t)rows + 15) / 16);
-  nwg = std::max<int64_t>(nwg, ((int64_t)rows + 255) / 256);
-  geo.base = (int)(rows / nwg);
-  geo.rem = (int)(rows % nwg);
-  const int per = geo.base + (geo.rem ? 1 : 0);
-  int tq = 1;
-  while (16 * tq < per) tq <<= 1;
-  geo.TQ = tq;
-  geo.KQ = 16 / tq;
+  const int nwg = mx_geometry(rows, cols, row_bytes, geo);
   switch (nvec) {
-    case 1: launch_mx_nv<1>(w, X, Y, rows, cols, geo, (int)nwg, s); break;
-    case 2: launch_mx_nv<2>(w, X, Y, rows, cols, geo, (int)nwg, s); break;
-    case 3: launch_mx_nv<3>(w, X, Y, rows, cols, geo, (int)nwg, s); break;
-    case 4: launch_mx_nv<4>(w, X, Y, rows, cols, geo, (int)nwg, s); break;
-    case 5: launch_mx_nv<5>(w, X, Y, rows, cols, geo, (int)nwg, s); break;
-    case 6: launch_mx_nv<6>(w, X, Y, rows, cols, geo, (int)nwg, s); break;
-    case 7: launch_mx_nv<7>(w, X, Y, rows, cols, geo, (int)nwg, s); break;
-    default: launch_mx_nv<8>(w, X, Y, rows, cols, geo, (int)nwg, s); break;
+    case 1: launch_mx_nv<1>(w, X, Y, rows, cols, geo, nwg, s); break;
+    case 2: launch_mx_nv<2>(w, X, Y, rows, cols, geo, nwg, s); break;
+    case 3: launch_mx_nv<3>(w, X, Y, rows, cols, geo, nwg, s); break;
+    case 4: launch_mx_nv<4>(w, X, Y, rows, cols, geo, nwg, s); break;
+    case 5: launch_mx_nv<5>(w, X, Y, rows, cols, geo, nwg, s); break;
+    case 6: launch_mx_nv<6>(w, X, Y, rows, cols, geo, nwg, s); break;
+    case 7: launch_mx_nv<7>(w, X, Y, rows, cols, geo, nwg, s); break;
+    default: launch_mx_nv<8>(w, X, Y, rows, cols, geo, nwg, s); break;
   }
   return true;
 }

@@ -182,6 +182,22 @@ def test_gemv_batched_parity_and_bit_identity(cuda, t, nvec):
         np.testing.assert_array_equal(f32bits(got[v]), f32bits(single[0]))
 
 
+@pytest.mark.parametrize("rows,cols,nvec", [(14336, 4096, 8), (1024, 4096, 5), (17, 2048, 3), (64, 2304, 8),
+                                             (4096, 4096, 16)])
+def test_gemv_q4k_batched_form_bit_identical(cuda, rows, cols, nvec):
+    """The batched matrix-core form (2..8 vectors a launch) across the launch geometries (TQ x KQ
+    splits, ragged rows): within tolerance of the oracle and bit-identical to one-vector calls."""
+    t = qvx.Q4_K
+    rng = np.random.default_rng(rows + 3 * cols + nvec)
+    w = random_weight(t, rows, cols, rng)
+    X = rng.standard_normal((nvec, cols)).astype(np.float32)
+    got = run_gemv(cuda, w, t, X, rows, cols)
+    assert max_rel(got, oracle.matmul_f64(w, t, X, nvec, rows, cols)) <= GEMV_TOL
+    for v in range(nvec):
+        single = run_gemv(cuda, w, t, X[v:v + 1], rows, cols)
+        np.testing.assert_array_equal(f32bits(got[v]), f32bits(single[0]))
+
+
 @pytest.mark.parametrize("t", GEMV_TYPES)
 def test_gemv_unaligned_weight_uses_generic_path(cuda, t):
     rng = np.random.default_rng(77 + t)
