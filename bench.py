@@ -84,6 +84,38 @@ def cpu_baseline(w_host, x_host, rows, cols, budget_s=5.0):
     }
 
 
+def cpu_operator():
+    """(kind, qmatmul_n function, dot kernel name, threads): the reference's own CPU qmatmulN
+    (oracle/_ref, built from the reference's sources), else the C restatement."""
+    import oracle
+    so = oracle.ref_lib()
+    if so is not None:
+        kind, fn, dot = "reference", so.qvxr_qmatmul_n, so.qvxr_dot_kernel().decode()
+    else:
+        so = oracle.lib()
+        kind, fn, dot = "port", so.qvxo_qmatmul_n, so.qvxo_dot_kernel().decode()
+    cores = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or len(os.sched_getaffinity(0))
+    return kind, fn, dot, cores
+
+
+def cpu_time(fn, w_host, t, X_host, m, rows, cols, budget_s=0.6):
+    """Median seconds of the CPU operator over >= 5 runs after one warm-up (steady clock), up to
+    about budget_s of work."""
+    import numpy as np
+    out = np.zeros((m, rows), np.float32)
+    wp = w_host.ctypes.data
+    X = np.ascontiguousarray(X_host, np.float32)
+    if not fn(out, wp, t, X, m, rows, cols):
+        raise RuntimeError(f"CPU qmatmulN refused type {t}")
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 200):
+        t0 = time.perf_counter()
+        fn(out, wp, t, X, m, rows, cols)
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
 # BASELINE configs[0..2] GEMV points: (name, ggml type, rows, cols, M values, scale multiplier)
 CONFIG_GEMVS = (
     ("C1 Q8_0 4096x4096", 8, 4096, 4096, (1,), 0.01),
@@ -95,7 +127,7 @@ CONFIG_GEMVS = (
 )
 
 
-def config_gemvs(torch, stream, steps):
+def config_gemvs(torch, stream, steps, cpu=True):
     """Every GEMV point of BASELINE configs[0..2]: enough seeded weight copies (>= 1 GiB) cycled so
     each launch reads HBM; n qmatmul_n calls recorded into one HIP graph (a qvx_plan), replayed,
     and timed with HIP events (the device's time per call, not the host's per-call cost)."""
@@ -130,17 +162,25 @@ def config_gemvs(torch, stream, steps):
             us = e0.elapsed_time(e1) / (2 * n) * 1e3
             ab = algorithmic_bytes(rows, cols, m, wb)
             gbs = ab / (us * 1e-6) / 1e9
-            out.append({"config": name, "M": m, "us": round(us, 2), "algorithmic_bytes": ab, "gb_s": round(gbs, 1),
-                        "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "calls_timed": 2 * n,
-                        "weight_copies": ncopy})
-            log(f"[bench] {name} M={m}: {us:.2f} us, {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak)")
+            rec = {"config": name, "M": m, "us": round(us, 2), "algorithmic_bytes": ab, "gb_s": round(gbs, 1),
+                   "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "calls_timed": 2 * n, "weight_copies": ncopy}
+            cpu_note = ""
+            if cpu:  # the reference CPU operator on the same blocks and activations, this host's cores
+                kind, fn, dot, cores = cpu_operator()
+                sec, runs = cpu_time(fn, ws[0].data.cpu().numpy(), t, X.cpu().numpy(), m, rows, cols)
+                rec["cpu"] = {"kind": kind, "us": round(sec * 1e6, 1), "gb_s": round(ab / sec / 1e9, 2), "runs": runs,
+                              "threads": cores, "dot_kernel": dot}
+                cpu_note = f"; CPU {kind} {sec * 1e3:.2f} ms ({ab / sec / 1e9:.1f} GB/s)"
+            out.append(rec)
+            log(f"[bench] {name} M={m}: {us:.2f} us, {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak)"
+                + cpu_note)
             del X, Y
         del ws
         torch.cuda.empty_cache()
     return out
 
 
-def decode_sweep(torch, stream, steps):
+def decode_sweep(torch, stream, steps, cpu=True):
     """Config 5: the 225 GEMVs of one Llama-3-8B Q4_K_M token (32 layers x q, k, v, o, gate, up,
     down + the Q6_K LM head, 4.54 GiB of weights, cold in HBM every token) replayed as one HIP
     graph, at M = 1 and M = 8.  Rate = algorithmic bytes per token / time per token."""
@@ -175,6 +215,26 @@ def decode_sweep(torch, stream, steps):
                         "ms_per_token_qkv_gateup_branches": round(ms_br, 4)}
         log(f"[bench] sweep M={m}: {ms:.3f} ms/token, {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak); "
             f"{ms_br:.3f} ms/token with q/k/v and gate/up as concurrent graph branches")
+        if cpu:
+            # the reference CPU operator on layer 0's seven projections and the LM head (same blocks,
+            # seeded activations); per token = 32 x layer + LM head
+            import numpy as np
+            kind, fn, dot, cores = cpu_operator()
+            rng = np.random.default_rng(5 + m)
+            layer_s = 0.0
+            for name, rows, cols, t, _ in decode.LAYER_SPECS:
+                w = model.layers[0][name]
+                sec, _ = cpu_time(fn, w.data.cpu().numpy(), t, rng.standard_normal((m, cols)), m, rows, cols, 0.2)
+                layer_s += sec
+            lm = model.lm_head
+            lm_s, _ = cpu_time(fn, lm.data.cpu().numpy(), lm.type, rng.standard_normal((m, lm.cols)), m, lm.rows,
+                               lm.cols, 0.2)
+            cpu_ms = (decode.N_LAYERS * layer_s + lm_s) * 1e3
+            out[f"M{m}"]["cpu"] = {"kind": kind, "ms_per_token": round(cpu_ms, 2),
+                                   "gb_s": round(ab / (cpu_ms * 1e-3) / 1e9, 2), "threads": cores, "dot_kernel": dot,
+                                   "sample": "layer 0's 7 projections and the LM head, median of >= 5 runs each; "
+                                             "per token = 32 x layer + LM head"}
+            log(f"[bench] sweep M={m} CPU {kind}: {cpu_ms:.1f} ms/token ({ab / (cpu_ms * 1e-3) / 1e9:.1f} GB/s)")
     del model
     torch.cuda.empty_cache()
     return out
@@ -210,10 +270,10 @@ def main():
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream()
     if args.sweep_only:  # profiler pass over the decode sweep alone
-        print(json.dumps({"sweep": decode_sweep(torch, stream, args.sweep_steps)}), flush=True)
+        print(json.dumps({"sweep": decode_sweep(torch, stream, args.sweep_steps, cpu=not args.no_cpu)}), flush=True)
         return
     if args.configs_only:  # profiler pass over the configs[0..2] GEMV points alone
-        print(json.dumps({"config_gemvs": config_gemvs(torch, stream, 200)}), flush=True)
+        print(json.dumps({"config_gemvs": config_gemvs(torch, stream, 200, cpu=not args.no_cpu)}), flush=True)
         return
     t = qvx.Q4_K
     wbytes = qvx.weight_bytes(t, ROWS, COLS)
@@ -328,6 +388,19 @@ def main():
                                         "frac_of_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4)}
                 log(f"[bench] GEMM {name} M={M}: {ms * 1e3:.1f} us, {tflops:.1f} TFLOP/s "
                     f"({100 * tflops / BF16_PEAK_TFLOPS:.1f}% of bf16 peak)")
+            if not args.no_cpu:
+                # the reference CPU qmatmulN on the first 64 tokens of X (fp16 -> fp32 exactly; 64 is
+                # the operator's own vector tile), same blocks; GFLOP/s extrapolates per token
+                kind, fn, dot, cores = cpu_operator()
+                ms_tok = 64
+                Xs = X[:ms_tok].float().cpu().numpy()
+                sec, runs = cpu_time(fn, copies[0].cpu().numpy(), t, Xs, ms_tok, ROWS, COLS)
+                gf = 2.0 * ms_tok * ROWS * COLS / sec / 1e9
+                gemm[f"cpu_M{M}"] = {"kind": kind, "gflops": round(gf, 1), "ms_for_sample": round(sec * 1e3, 2),
+                                     "ms_extrapolated": round(sec * 1e3 * M / ms_tok, 1), "runs": runs,
+                                     "threads": cores, "dot_kernel": dot,
+                                     "sample": f"first {ms_tok} of the {M} tokens (qmatmulN, X converted fp16->fp32)"}
+                log(f"[bench] GEMM M={M} CPU {kind}: {gf:.1f} GFLOP/s on a {ms_tok}-token sample")
             del X, Y
     except RuntimeError as e:  # report, never hide: the JSON carries the error
         gemm["error"] = str(e)
@@ -337,7 +410,7 @@ def main():
     cfgs = []
     if not args.gemv_only:
         try:
-            cfgs = config_gemvs(torch, stream, 200)
+            cfgs = config_gemvs(torch, stream, 200, cpu=not args.no_cpu)
         except RuntimeError as e:  # report, never hide
             cfgs = [{"error": str(e)}]
             log(f"[bench] config GEMVs failed: {e}")
@@ -346,7 +419,7 @@ def main():
     sweep = {}
     if not args.gemv_only:
         try:
-            sweep = decode_sweep(torch, stream, args.sweep_steps)
+            sweep = decode_sweep(torch, stream, args.sweep_steps, cpu=not args.no_cpu)
         except RuntimeError as e:  # report, never hide
             sweep = {"error": str(e)}
             log(f"[bench] sweep failed: {e}")
