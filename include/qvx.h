@@ -44,6 +44,8 @@ extern "C" {
 #define QVX_E_VARIANT (-6) /* unknown GEMM variant */
 #define QVX_E_RANGE (-7)   /* row index out of range, n not a whole number of blocks, size overflow */
 #define QVX_E_STATE (-8)   /* a plan launched before qvx_plan_instantiate, or changed after it */
+#define QVX_E_FORMAT (-9)  /* malformed GGUF data (qvx_gguf_last_error() says what) */
+#define QVX_E_IO (-10)     /* a file could not be opened or mapped */
 
 /* GEMM variants for qvx_qgemm_f16 */
 #define QVX_GEMM_BF16 0 /* X rounded to bf16; raw weight blocks staged in LDS, dequantised to bf16; bf16 MFMA */
@@ -144,6 +146,52 @@ int qvx_plan_launch(qvx_plan* plan, void* stream);
 int qvx_plan_run_eager(const qvx_plan* plan, void* stream);
 /* Free the plan and its graph (NULL is a no-op). */
 void qvx_plan_destroy(qvx_plan* plan);
+/* ---- GGUF files: parse, locate tensors, upload ------------------------------------------- */
+/* The reference's GgufFile (gguf/include/qorvix/gguf/gguf_file.hpp:47-105): GGUF versions 1-3,
+ * with the checks of its parse (gguf/src/gguf_file.cpp:95-180); where it throws GgufParseError
+ * these return QVX_E_FORMAT and keep the message for qvx_gguf_last_error (per thread).  Tensor
+ * dimensions are in ggml order (dims[0] is the row length, `cols`; dims[1] the row count, `rows`);
+ * offsets are relative to the data section (qvx_gguf_data_offset); n_bytes is the on-disk size
+ * from the type's block traits, 0 for a type id without traits. */
+typedef struct qvx_gguf qvx_gguf;
+/* Memory-map `path` read-only and parse it (GgufFile::open, gguf_file.hpp:54-55). */
+int qvx_gguf_open(const char* path, qvx_gguf** out);
+/* Parse a caller's buffer, which must outlive the handle (GgufFile::parse, gguf_file.hpp:51-52). */
+int qvx_gguf_parse(const void* data, size_t size, qvx_gguf** out);
+void qvx_gguf_close(qvx_gguf* f);
+/* Message of the last failed open / parse on this thread ("" after a success). */
+const char* qvx_gguf_last_error(void);
+uint32_t qvx_gguf_version(const qvx_gguf* f);
+uint32_t qvx_gguf_alignment(const qvx_gguf* f);   /* general.alignment, default 32 */
+uint64_t qvx_gguf_data_offset(const qvx_gguf* f); /* dataOffset(), gguf_file.hpp:62 */
+int64_t qvx_gguf_tensor_count(const qvx_gguf* f);
+int64_t qvx_gguf_meta_count(const qvx_gguf* f);
+/* Index of the tensor named `name`, -1 if absent (tensor(), gguf_file.hpp:65). */
+int64_t qvx_gguf_find_tensor(const qvx_gguf* f, const char* name);
+/* Tensor i (GgufTensor, gguf_file.hpp:27-35): any output may be NULL; dims receives 8 values
+ * (zeros past n_dims).  i out of range -> QVX_E_RANGE. */
+int qvx_gguf_tensor_info(const qvx_gguf* f, int64_t i, const char** name, uint32_t* type, uint32_t* n_dims,
+                         uint64_t* dims, uint64_t* offset, uint64_t* n_elements, uint64_t* n_bytes);
+/* Host address of tensor i's bytes in the mapping / buffer, NULL when it does not carry them. */
+const void* qvx_gguf_tensor_data(const qvx_gguf* f, int64_t i);
+/* Copy tensor i's raw blocks to device memory (stream-ordered; the GPU weight upload of
+ * cuda_backend.cu:1300-1309 with weightBytes, :1246-1255).  dst_bytes < n_bytes -> QVX_E_RANGE;
+ * a type without traits -> QVX_E_TYPE.  The GEMV / GEMM entry points take the blocks as they are. */
+int qvx_gguf_upload(const qvx_gguf* f, int64_t i, void* d_dst, size_t dst_bytes, void* stream);
+/* Metadata key i in file order, NULL past the end (metadata(), gguf_file.hpp:68-70). */
+const char* qvx_gguf_meta_key(const qvx_gguf* f, int64_t i);
+/* Value type tag of `key` (0..12 as on disk), its element type for an array (else the same tag),
+ * and its element count (1 for a scalar).  Absent -> QVX_E_RANGE. */
+int qvx_gguf_meta_type(const qvx_gguf* f, const char* key, uint32_t* type, uint32_t* elem_type, uint64_t* count);
+/* Element `index` of `key` (0 for a scalar), widened as the reference's getU64 / getF64 / getBool /
+ * getString do (gguf_file.hpp:74-78; gguf_types.cpp:82-120): integers and bools as u64 / i64,
+ * numbers other than bools as f64.  Absent or index past the end -> QVX_E_RANGE; wrong category ->
+ * QVX_E_TYPE.  A string is not NUL-terminated; *len holds its length. */
+int qvx_gguf_meta_u64(const qvx_gguf* f, const char* key, uint64_t index, uint64_t* out);
+int qvx_gguf_meta_i64(const qvx_gguf* f, const char* key, uint64_t index, int64_t* out);
+int qvx_gguf_meta_f64(const qvx_gguf* f, const char* key, uint64_t index, double* out);
+int qvx_gguf_meta_bool(const qvx_gguf* f, const char* key, uint64_t index, int* out);
+int qvx_gguf_meta_string(const qvx_gguf* f, const char* key, uint64_t index, const char** out, size_t* len);
 /* ---- host entry points (host pointers, synchronous) --------------------------------------- */
 /* The reference's CPU signatures (qmatmul.hpp:14-36, dequant.hpp:12-21) over the GPU kernels:
  * weight, x and out live in host memory; the call uploads, computes on the current device and

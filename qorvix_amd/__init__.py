@@ -30,6 +30,7 @@ TYPE_NAMES = {0: "F32", 1: "F16", 2: "Q4_0", 3: "Q4_1", 6: "Q5_0", 7: "Q5_1", 8:
 
 # status codes (include/qvx.h)
 OK, E_TYPE, E_SHAPE, E_NVEC, E_NULL, E_HIP, E_VARIANT, E_RANGE, E_STATE = 0, -1, -2, -3, -4, -5, -6, -7, -8
+E_FORMAT, E_IO = -9, -10
 # GEMM variants
 GEMM_BF16, GEMM_I8, GEMM_F16 = 0, 1, 2
 
@@ -60,6 +61,27 @@ SIGNATURES = {
     "qvx_plan_launch": ([_vp, _vp], _i32),
     "qvx_plan_run_eager": ([_vp, _vp], _i32),
     "qvx_plan_destroy": ([_vp], None),
+    "qvx_gguf_open": ([C.c_char_p, C.POINTER(_vp)], _i32),
+    "qvx_gguf_parse": ([_vp, _sz, C.POINTER(_vp)], _i32),
+    "qvx_gguf_close": ([_vp], None),
+    "qvx_gguf_last_error": ([], C.c_char_p),
+    "qvx_gguf_version": ([_vp], _u32),
+    "qvx_gguf_alignment": ([_vp], _u32),
+    "qvx_gguf_data_offset": ([_vp], _u64),
+    "qvx_gguf_tensor_count": ([_vp], C.c_int64),
+    "qvx_gguf_meta_count": ([_vp], C.c_int64),
+    "qvx_gguf_find_tensor": ([_vp, C.c_char_p], C.c_int64),
+    "qvx_gguf_tensor_info": ([_vp, C.c_int64, C.POINTER(C.c_char_p), C.POINTER(_u32), C.POINTER(_u32),
+                              C.POINTER(_u64), C.POINTER(_u64), C.POINTER(_u64), C.POINTER(_u64)], _i32),
+    "qvx_gguf_tensor_data": ([_vp, C.c_int64], _vp),
+    "qvx_gguf_upload": ([_vp, C.c_int64, _vp, _sz, _vp], _i32),
+    "qvx_gguf_meta_key": ([_vp, C.c_int64], C.c_char_p),
+    "qvx_gguf_meta_type": ([_vp, C.c_char_p, C.POINTER(_u32), C.POINTER(_u32), C.POINTER(_u64)], _i32),
+    "qvx_gguf_meta_u64": ([_vp, C.c_char_p, _u64, C.POINTER(_u64)], _i32),
+    "qvx_gguf_meta_i64": ([_vp, C.c_char_p, _u64, C.POINTER(C.c_int64)], _i32),
+    "qvx_gguf_meta_f64": ([_vp, C.c_char_p, _u64, C.POINTER(C.c_double)], _i32),
+    "qvx_gguf_meta_bool": ([_vp, C.c_char_p, _u64, C.POINTER(_i32)], _i32),
+    "qvx_gguf_meta_string": ([_vp, C.c_char_p, _u64, C.POINTER(C.c_void_p), C.POINTER(_sz)], _i32),
     "qvx_qmatmul_host": ([_vp, _vp, _u32, _vp, _i32, _i32], _i32),
     "qvx_qmatmul_n_host": ([_vp, _vp, _u32, _vp, _i32, _i32, _i32], _i32),
     "qvx_dequantize_host": ([_u32, _vp, _vp, _sz], _i32),

@@ -184,6 +184,8 @@ const char* qvx_strerror(int code) {
     case QVX_E_VARIANT: return "unknown GEMM variant";
     case QVX_E_RANGE: return "index or size out of range";
     case QVX_E_STATE: return "plan not instantiated, or changed after instantiation";
+    case QVX_E_FORMAT: return "malformed GGUF data";
+    case QVX_E_IO: return "file could not be opened or mapped";
     default: return "unknown qvx status";
   }
 }

@@ -109,9 +109,6 @@ __device__ inline u32x4 lds_read16(uint32_t addr) {
 __device__ inline void lds_wait(u32x4& a, u32x4& b, u32x4& c) {
   asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c)::"memory");
 }
-__device__ inline void lds_wait(u32x4& a, u32x4& b, u32x4& c, u32x4& d, u32x4& e) {
-  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e)::"memory");
-}
 
 // LDS write the compiler does not track, for the same reason: were a copy of this wave in flight
 // it would wait for all of them (vmcnt(0)) before an LDS store it emits, so the fragment stores do

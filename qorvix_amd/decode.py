@@ -98,6 +98,48 @@ class Model:
                 m.lm_head = w
         return m
 
+    @staticmethod
+    def from_gguf(file, device="cuda") -> "Model":
+        """A Llama-family model's matmul weights from a GGUF file (a path or a gguf.GgufFile), by
+        the reference's tensor names and checks (runtime/src/weights.cpp:20-50; loadMat,
+        runtime/include/qorvix/runtime/tensor_load.hpp:51-63): each projection must exist, hold
+        rows x cols elements and have a type the engine computes; the LM head is output.weight, or
+        token_embd.weight when the file ties them (weights.hpp:119, lmHead()).  The raw blocks are
+        uploaded once and kept quantized."""
+        from . import supports
+        from .gguf import GgufFile
+        f = file if isinstance(file, GgufFile) else GgufFile.open(file)
+        n_layers = f.arch_u64("block_count")
+        if n_layers is None:
+            raise ValueError(f"GGUF file has no {f.architecture or '<arch>'}.block_count")
+        d = f.arch_u64("embedding_length")
+        ffn = f.arch_u64("feed_forward_length")
+        heads, kv_heads = f.arch_u64("attention.head_count"), f.arch_u64("attention.head_count_kv")
+        kv = d * (kv_heads or heads) // heads if d and heads else None
+
+        def load(name, rows, cols):
+            t = f.tensor(name)
+            if t is None:
+                raise ValueError(f"missing tensor '{name}'")
+            rows = t.rows if rows is None else rows
+            cols = t.cols if cols is None else cols
+            if t.n_elements != rows * cols:
+                raise ValueError(f"tensor '{name}' has {t.n_elements} elements, expected {rows} x {cols}")
+            if not supports(t.type_raw):
+                raise ValueError(f"tensor '{name}' uses unsupported type {t.type_name()}")
+            return f.upload(name, device)
+
+        m = Model()
+        shapes = {"wq": (d, d), "wk": (kv, d), "wv": (kv, d), "wo": (d, d), "ffn_gate": (ffn, d),
+                  "ffn_up": (ffn, d), "ffn_down": (d, ffn)}
+        names = {"wq": "attn_q", "wk": "attn_k", "wv": "attn_v", "wo": "attn_output", "ffn_gate": "ffn_gate",
+                 "ffn_up": "ffn_up", "ffn_down": "ffn_down"}
+        for layer in range(n_layers):
+            m.layers.append({k: load(f"blk.{layer}.{names[k]}.weight", *shapes[k]) for k, *_ in LAYER_SPECS})
+        head = "output.weight" if f.tensor("output.weight") is not None else "token_embd.weight"
+        m.lm_head = load(head, None, d)
+        return m
+
     @property
     def nbytes(self) -> int:
         n = sum(w.nbytes for layer in self.layers for w in layer.values())
@@ -173,15 +215,16 @@ class DecodeStep:
         import torch
         self.model, self.m = model, m
         f32 = dict(dtype=torch.float32, device=device)
-        self.inputs = {"xn": torch.empty((m, D_MODEL), **f32), "attn": torch.empty((m, D_MODEL), **f32),
-                       "act": torch.empty((m, D_FF), **f32)}
+        l0 = model.layers[0]
+        self.inputs = {"xn": torch.empty((m, l0["wq"].cols), **f32), "attn": torch.empty((m, l0["wo"].cols), **f32),
+                       "act": torch.empty((m, l0["ffn_down"].cols), **f32)}
         for i, k in enumerate(("xn", "attn", "act")):
             fill_normal_t(self.inputs[k], seed=seed + i)
         self.outputs = []
         self.plan = Plan()
-        for l, name, rows, cols, t, src in sweep_specs(len(model.layers), model.lm_head is not None):
+        for l, name, _, _, _, src in sweep_specs(len(model.layers), model.lm_head is not None):
             w = model.layers[l][name] if l < len(model.layers) else model.lm_head
-            y = torch.empty((m, rows), **f32)
+            y = torch.empty((m, w.rows), **f32)
             self.outputs.append((l, name, y))
             # q/k/v read the same normed state, and so do gate/up: independent branches when asked
             # (measured slower on MI355X: the graph's cross-branch joins cost more than the overlap)
