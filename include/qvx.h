@@ -58,9 +58,10 @@ const char* qvx_version(void);
 /* Message of a QVX_E_* code. */
 const char* qvx_strerror(int code);
 
-/* 1 if the GEMV / GEMM kernels compute `type` (qmatmul.cpp:24-26, qmatmulSupports).
- * Types the reference also dequantises (F16, BF16, Q4_1, Q5_0, Q5_1, Q8_1, Q5_K) return 0 here:
- * a caller falls back for them, and qvx_dequantize still handles them bit-exactly. */
+/* 1 if qvx_qmatmul / qvx_qmatmul_n compute `type` (qmatmul.cpp:24-26, qmatmulSupports): every
+ * type the reference dequantises (F32, F16, BF16, Q8_0, Q8_1, Q4_0, Q4_1, Q5_0, Q5_1, Q4_K, Q5_K,
+ * Q6_K).  Q8_0 / Q4_0 / Q4_K / Q6_K run on the fast kernels, the others on a generic kernel;
+ * qvx_qgemm_f16 computes Q4_K only. */
 int qvx_supports(uint32_t type);
 
 /* 1 if qvx_dequantize handles `type` (dequant.cpp:257-275, canDequantize). */

@@ -56,9 +56,10 @@ inline bool can_dequantize(uint32_t t) {
 }
 
 // Types the GEMV / GEMM kernels compute.
-inline bool gemv_supports(uint32_t t) {
-  return t == T_Q8_0 || t == T_Q4_0 || t == T_Q4_K || t == T_Q6_K || t == T_F32;
-}
+// Every type the reference's qmatmul accepts (qmatmulSupports = canDequantize && traits,
+// runtime/src/qmatmul.cpp:24-26): Q8_0 / Q4_0 / Q4_K / Q6_K on the fast kernels, the others on the
+// generic kernel.
+inline bool gemv_supports(uint32_t t) { return can_dequantize(t); }
 
 // Block geometry of the four GEMV formats.  A "panel" is PB consecutive blocks of a row: 2048
 // elements, PB*BB bytes, always a multiple of 16 so panels of 16-byte-aligned rows stay aligned.

@@ -168,6 +168,13 @@ bool launch_gemv_generic(uint32_t t, const void* w, const float* X, float* Y, in
     case T_Q4_0: k_gemv_generic<T_Q4_0, 32, 18><<<grid, 256, 0, s>>>(b, X, Y, rows, cols, nvec, row_bytes); return true;
     case T_Q4_K: k_gemv_generic<T_Q4_K, 256, 144><<<grid, 256, 0, s>>>(b, X, Y, rows, cols, nvec, row_bytes); return true;
     case T_Q6_K: k_gemv_generic<T_Q6_K, 256, 210><<<grid, 256, 0, s>>>(b, X, Y, rows, cols, nvec, row_bytes); return true;
+    case T_F16: k_gemv_generic<T_F16, 1, 2><<<grid, 256, 0, s>>>(b, X, Y, rows, cols, nvec, row_bytes); return true;
+    case T_BF16: k_gemv_generic<T_BF16, 1, 2><<<grid, 256, 0, s>>>(b, X, Y, rows, cols, nvec, row_bytes); return true;
+    case T_Q8_1: k_gemv_generic<T_Q8_1, 32, 36><<<grid, 256, 0, s>>>(b, X, Y, rows, cols, nvec, row_bytes); return true;
+    case T_Q4_1: k_gemv_generic<T_Q4_1, 32, 20><<<grid, 256, 0, s>>>(b, X, Y, rows, cols, nvec, row_bytes); return true;
+    case T_Q5_0: k_gemv_generic<T_Q5_0, 32, 22><<<grid, 256, 0, s>>>(b, X, Y, rows, cols, nvec, row_bytes); return true;
+    case T_Q5_1: k_gemv_generic<T_Q5_1, 32, 24><<<grid, 256, 0, s>>>(b, X, Y, rows, cols, nvec, row_bytes); return true;
+    case T_Q5_K: k_gemv_generic<T_Q5_K, 256, 176><<<grid, 256, 0, s>>>(b, X, Y, rows, cols, nvec, row_bytes); return true;
     default: return false;
   }
 }

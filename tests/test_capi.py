@@ -51,9 +51,11 @@ def test_type_table_matches_gguf():
     assert qvx.type_traits(qvx.Q8_0) == (32, 34)
     assert qvx.type_traits(qvx.Q4_0) == (32, 18)
     assert qvx.type_traits(4) is None
-    for t in (qvx.Q8_0, qvx.Q4_0, qvx.Q4_K, qvx.Q6_K, qvx.F32):
+    # every type the reference's qmatmulSupports accepts (canDequantize && traits)
+    for t in (qvx.Q8_0, qvx.Q4_0, qvx.Q4_K, qvx.Q6_K, qvx.F32, qvx.F16, qvx.BF16, qvx.Q4_1, qvx.Q5_0, qvx.Q5_1,
+              qvx.Q8_1, qvx.Q5_K):
         assert qvx.supports(t)
-    for t in (qvx.F16, qvx.BF16, qvx.Q4_1, qvx.Q5_0, qvx.Q5_1, qvx.Q8_1, qvx.Q5_K, 10, 16, 99):
+    for t in (10, 11, 15, 16, 99):
         assert not qvx.supports(t)
     for t in (0, 1, 2, 3, 6, 7, 8, 9, 12, 13, 14, 30):
         assert qvx.can_dequantize(t)
@@ -77,7 +79,9 @@ def test_qmatmul_rejections():
     assert lib.qvx_qmatmul(FAKE, FAKE, qvx.Q4_K, FAKE, 1, 300, None) == qvx.E_SHAPE  # cols % 256
     assert lib.qvx_qmatmul(FAKE, FAKE, 10, FAKE, 1, 256, None) == qvx.E_TYPE  # Q2_K
     assert lib.qvx_qmatmul(FAKE, FAKE, 4, FAKE, 1, 256, None) == qvx.E_TYPE  # retired id
-    assert lib.qvx_qmatmul(FAKE, FAKE, qvx.F16, FAKE, 1, 256, None) == qvx.E_TYPE  # host-only type
+    assert lib.qvx_qmatmul(FAKE, FAKE, 11, FAKE, 1, 256, None) == qvx.E_TYPE  # Q3_K: not dequantisable
+    assert lib.qvx_qmatmul(FAKE, FAKE, qvx.Q5_K, FAKE, 1, 128, None) == qvx.E_SHAPE  # cols % 256
+    assert lib.qvx_qgemm_f16(FAKE, FAKE, qvx.F16, FAKE, 128, 256, 256, 0, None) == qvx.E_TYPE  # GEMM: Q4_K only
     assert lib.qvx_qmatmul_n(FAKE, FAKE, qvx.Q8_0, FAKE, 0, 1, 32, None) == qvx.E_NVEC
     assert lib.qvx_qmatmul_n(FAKE, FAKE, qvx.Q8_0, FAKE, -3, 1, 32, None) == qvx.E_NVEC
     # nVec is checked first, as in the reference (qmatmulN returns false before the type check)

@@ -198,6 +198,23 @@ def test_gemv_q4k_batched_form_bit_identical(cuda, rows, cols, nvec):
         np.testing.assert_array_equal(f32bits(got[v]), f32bits(single[0]))
 
 
+OTHER_TYPES = [qvx.F16, qvx.BF16, qvx.Q4_1, qvx.Q5_0, qvx.Q5_1, qvx.Q8_1, qvx.Q5_K]
+
+
+@pytest.mark.parametrize("t", OTHER_TYPES)
+@pytest.mark.parametrize("rows,cols,nvec", [(37, 256, 1), (300, 2048, 3), (1024, 4096, 2)])
+def test_gemv_other_dequantizable_types(cuda, t, rows, cols, nvec):
+    """Types the reference's qmatmul accepts beyond the four tuned formats run on the generic kernel:
+    within tolerance of the oracle, batched calls bit-identical to single ones."""
+    rng = np.random.default_rng(rows + cols + 13 * t + nvec)
+    w = random_weight(t, rows, cols, rng)
+    X = rng.standard_normal((nvec, cols)).astype(np.float32)
+    got = run_gemv(cuda, w, t, X, rows, cols)
+    assert max_rel(got, oracle.matmul_f64(w, t, X, nvec, rows, cols)) <= GEMV_TOL
+    for v in range(nvec):
+        np.testing.assert_array_equal(f32bits(got[v]), f32bits(run_gemv(cuda, w, t, X[v:v + 1], rows, cols)[0]))
+
+
 @pytest.mark.parametrize("t", GEMV_TYPES)
 def test_gemv_unaligned_weight_uses_generic_path(cuda, t):
     rng = np.random.default_rng(77 + t)
