@@ -60,7 +60,7 @@ const char* qvx_strerror(int code);
 
 /* 1 if qvx_qmatmul / qvx_qmatmul_n compute `type` (qmatmul.cpp:24-26, qmatmulSupports): every
  * type the reference dequantises (F32, F16, BF16, Q8_0, Q8_1, Q4_0, Q4_1, Q5_0, Q5_1, Q4_K, Q5_K,
- * Q6_K).  Q8_0 / Q4_0 / Q4_K / Q6_K run on the fast kernels, the others on a generic kernel;
+ * Q6_K).  Q8_0 / Q4_0 / Q4_K / Q5_K / Q6_K run on the fast kernels, the others on a generic kernel;
  * qvx_qgemm_f16 computes Q4_K only. */
 int qvx_supports(uint32_t type);
 
@@ -107,7 +107,8 @@ int qvx_quantize_act_q8(const uint16_t* d_X, int M, int K, int8_t* d_q, float* d
                         int32_t* d_qsum, void* stream);
 
 /* Fill a [rows, cols] weight of `type` with seeded synthetic blocks on the device (benchmark and
- * test data; no reference counterpart).  Scales are fp16(|N(0,1)| * scale_mul) (Q4_K: d and dmin;
+ * test data; no reference counterpart), for Q8_0, Q4_0, Q4_K, Q5_K and Q6_K.  Scales are
+ * fp16(|N(0,1)| * scale_mul) (Q4_K / Q5_K: d and dmin;
  * Q6_K: d), quant bytes uniform, Q6_K int8 sub-scales uniform over [-128, 127].  Deterministic in
  * (seed, byte position). */
 int qvx_fill_synthetic(void* d_w, uint32_t type, int rows, int cols, uint64_t seed, float scale_mul,

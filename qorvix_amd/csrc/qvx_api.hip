@@ -266,7 +266,8 @@ int qvx_quantize_act_q8(const uint16_t* d_X, int M, int K, int8_t* d_q, float* d
 
 int qvx_fill_synthetic(void* d_w, uint32_t type, int rows, int cols, uint64_t seed, float scale_mul, void* stream) {
   const TypeInfo* t = type_info(type);
-  if (!t || (type != T_Q8_0 && type != T_Q4_0 && type != T_Q4_K && type != T_Q6_K)) return QVX_E_TYPE;
+  if (!t || (type != T_Q8_0 && type != T_Q4_0 && type != T_Q4_K && type != T_Q5_K &&
+              type != T_Q6_K)) return QVX_E_TYPE;
   if (rows < 0 || cols < 0 || cols % (int)t->block != 0) return QVX_E_SHAPE;
   if (!d_w) return QVX_E_NULL;
   const size_t nblk = (size_t)rows * (size_t)(cols / (int)t->block);

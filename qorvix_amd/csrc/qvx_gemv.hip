@@ -145,6 +145,56 @@ template <> struct Lane<T_Q4_K> {
   }
 };
 
+// Q5_K (176-byte super-blocks: d, dmin, the Q4_K scale packing, qh[32], qs[128]): slot sig = scale
+// group c = sig%4 of super-block b = sig/4, as for Q4_K, with qs at byte 48.  Element l of the
+// group's low sub-block 2c is (qs[32c + l] & 15) + 16 * bit 2c of qh[l], of the high sub-block 2c+1
+// (qs[32c + l] >> 4) + 16 * bit 2c+1 of qh[l] (public K-quant layout).  The 5-bit codes 0..31 are
+// multiplied as they are, so no offset correction enters the fold.
+template <> struct Lane<T_Q5_K> {
+  static constexpr int kR = 4;
+  static constexpr int kSlotElems = 64;
+  struct Raw {
+    uint4 h, qh0, qh1, q0, q1;
+  };
+  static __device__ inline int xoff(int sig, int run) { return 256 * (sig >> 2) + 64 * (sig & 3) + 16 * run; }
+  static __device__ inline void load(const uint8_t* row, int sig, Raw& r) {
+    const uint8_t* blk = row + 176 * (sig >> 2);
+    r.h = ldg16(blk);
+    r.qh0 = ldg16(blk + 16);
+    r.qh1 = ldg16(blk + 32);
+    r.q0 = ldg16(blk + 48 + 32 * (sig & 3));
+    r.q1 = ldg16(blk + 64 + 32 * (sig & 3));
+  }
+  static __device__ inline float row(const Raw& r, int sig, const XQ<4>& x) {
+    const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+    const uint32_t qh[8] = {r.qh0.x, r.qh0.y, r.qh0.z, r.qh0.w, r.qh1.x, r.qh1.y, r.qh1.z, r.qh1.w};
+    const int c = sig & 3;
+    const uint32_t sa = 2u * (uint32_t)c;  // bit of qh for the low sub-block; sa + 1 for the high
+    uint32_t lo[8], hi[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t ba = ((qh[j] >> sa) << 4) & 0x10101010u, bb = ((qh[j] >> (sa + 1u)) << 4) & 0x10101010u;
+      lo[j] = __builtin_amdgcn_bitop3_b32(q[j], 0x0F0F0F0Fu, ba, 0xEA);          // (q & 15) | 16 h
+      hi[j] = __builtin_amdgcn_bitop3_b32(q[j] >> 4, 0x0F0F0F0Fu, bb, 0xEA);
+    }
+    const int qa = x.q[0] + x.q[1], qb = x.q[2] + x.q[3];
+    const int ta = dotq<8>(lo, x.h, x.l);          // sum n q over sub-block 2c
+    const int tb = dotq<8>(hi, x.h + 8, x.l + 8);  // sum n q over sub-block 2c+1
+    // scale / min of sub-blocks 2c, 2c+1: the Q4_K packing (see Lane<T_Q4_K>)
+    const uint32_t j = 2u * (uint32_t)(c & 1);
+    const uint32_t p1 = __builtin_amdgcn_perm(r.h.z, r.h.y, j | (j + 1) << 8 | (j + 4) << 16 | (j + 5) << 24);
+    const uint32_t p2 = __builtin_amdgcn_perm(r.h.w, r.h.w, j | (j + 1) << 8 | j << 16 | (j + 1) << 24);
+    const bool up = c >= 2;
+    const uint32_t sm = (p1 & (up ? 0u : 0x3F3F3F3Fu)) | ((p1 >> 2) & (up ? 0x30303030u : 0u)) |
+                        (p2 & (up ? 0x00000F0Fu : 0u)) | ((p2 >> 4) & (up ? 0x0F0F0000u : 0u));
+    const float sca = (float)(sm & 0xFFu), scb = (float)((sm >> 8) & 0xFFu);
+    const float mna = (float)((sm >> 16) & 0xFFu), mnb = (float)(sm >> 24);
+    const float t = __builtin_fmaf((float)tb, scb, (float)ta * sca);
+    const float u = __builtin_fmaf((float)qb, mnb, (float)qa * mna);
+    return __builtin_fmaf(f16lo(r.h.x), t, -f16hi(r.h.x) * u);
+  }
+};
+
 // Q6_K: slot = super-block b = sig/8, u = sig%8 -> half h = u/4, l-group t = (u/2)%2, e = u%2.
 // Run 0 is quarter e (low nibbles of ql[64h + 32e + 16t ..+16]), run 1 quarter e+2 (their high
 // nibbles), with 2-bit high parts from qh[32h + 16t ..+16], bits (2e, 2e+1) and (2e+4, 2e+5);
@@ -497,7 +547,7 @@ constexpr int kCUs = 256;  // MI355X compute units
 // formats, with the most registers per row, do best with one).
 template <uint32_t T>
 constexpr int prefetch_rows() {
-  return T == T_Q6_K ? 1 : 2;
+  return T == T_Q6_K || T == T_Q5_K ? 1 : 2;
 }
 
 template <uint32_t T, int NV, int RMAX, int TPT>
@@ -615,13 +665,14 @@ static bool launch_fast_t(const void* w, const float* X, float* Y, int nvec, int
   return true;
 }
 
-// Fast-path GEMV for nvec >= 1 on 16-byte-aligned rows of Q8_0 / Q4_0 / Q4_K / Q6_K.  Returns
+// Fast-path GEMV for nvec >= 1 on 16-byte-aligned rows of Q8_0 / Q4_0 / Q4_K / Q5_K / Q6_K.  Returns
 // false, having launched nothing, when the shape needs the generic kernel.
 bool launch_gemv_fast(uint32_t t, const void* w, const float* X, float* Y, int nvec, int rows, int cols,
                       size_t row_bytes, hipStream_t s) {
   switch (t) {
     case T_Q4_K: return launch_fast_t<T_Q4_K>(w, X, Y, nvec, rows, cols, row_bytes, s);
     case T_Q6_K: return launch_fast_t<T_Q6_K>(w, X, Y, nvec, rows, cols, row_bytes, s);
+    case T_Q5_K: return launch_fast_t<T_Q5_K>(w, X, Y, nvec, rows, cols, row_bytes, s);
     case T_Q4_0: return launch_fast_t<T_Q4_0>(w, X, Y, nvec, rows, cols, row_bytes, s);
     case T_Q8_0: return launch_fast_t<T_Q8_0>(w, X, Y, nvec, rows, cols, row_bytes, s);
     default: return false;

@@ -4,7 +4,7 @@
 // function of (seed, position) through the SplitMix64 finaliser, so a weight of any size is
 // reproducible, generated at HBM speed, and needs no host staging.  Distributions follow the
 // benchmark configurations: fp16 scales |N(0,1)| * mul, uniform quant bytes (which makes the
-// Q4_K 6-bit scale/min fields and the Q6_K 6-bit quants exactly uniform), Q8_0 quants uniform in
+// Q4_K / Q5_K 6-bit scale/min fields and the Q6_K 6-bit quants exactly uniform), Q8_0 quants uniform in
 // [-127, 127], Q6_K int8 sub-scales uniform in [-128, 127].
 #include "qvx_common.hpp"
 
@@ -47,10 +47,10 @@ __global__ __launch_bounds__(256) void k_fill_blocks(uint8_t* __restrict__ w, si
   } else if constexpr (T == T_Q4_0) {
     put16(0, f16_bits(fabsf(normal_at(s, 2 * blk)) * mul));
     for (int i = 0; i < 16; ++i) p[2 + i] = byte_at(i);
-  } else if constexpr (T == T_Q4_K) {
+  } else if constexpr (T == T_Q4_K || T == T_Q5_K) {
     put16(0, f16_bits(fabsf(normal_at(s, 2 * blk)) * mul));
     put16(2, f16_bits(fabsf(normal_at(s, 2 * blk + 1)) * mul));
-    for (int i = 4; i < 144; ++i) p[i] = byte_at(i);
+    for (int i = 4; i < BB; ++i) p[i] = byte_at(i);
   } else if constexpr (T == T_Q6_K) {
     for (int i = 0; i < 208; ++i) p[i] = byte_at(i);  // ql, qh, and int8 scales uniform
     put16(208, f16_bits(fabsf(normal_at(s, 2 * blk)) * mul));
@@ -75,6 +75,7 @@ bool launch_fill_synthetic(void* w, uint32_t t, size_t nblk, uint64_t seed, floa
     case T_Q8_0: k_fill_blocks<T_Q8_0, 34><<<grid, 256, 0, s>>>(p, nblk, seed, mul); return true;
     case T_Q4_0: k_fill_blocks<T_Q4_0, 18><<<grid, 256, 0, s>>>(p, nblk, seed, mul); return true;
     case T_Q4_K: k_fill_blocks<T_Q4_K, 144><<<grid, 256, 0, s>>>(p, nblk, seed, mul); return true;
+    case T_Q5_K: k_fill_blocks<T_Q5_K, 176><<<grid, 256, 0, s>>>(p, nblk, seed, mul); return true;
     case T_Q6_K: k_fill_blocks<T_Q6_K, 210><<<grid, 256, 0, s>>>(p, nblk, seed, mul); return true;
     default: return false;
   }

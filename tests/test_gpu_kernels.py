@@ -22,7 +22,7 @@ BLOCK = {qvx.Q4_0: (32, 18), qvx.Q4_1: (32, 20), qvx.Q5_0: (32, 22), qvx.Q5_1: (
          qvx.F16: (1, 2), qvx.BF16: (1, 2), qvx.F32: (1, 4)}
 HALF_OFFS = {qvx.Q4_0: [0], qvx.Q4_1: [0, 2], qvx.Q5_0: [0], qvx.Q5_1: [0, 2], qvx.Q8_0: [0], qvx.Q8_1: [0, 2],
              qvx.Q4_K: [0, 2], qvx.Q5_K: [0, 2], qvx.Q6_K: [208]}
-GEMV_TYPES = [qvx.Q8_0, qvx.Q4_0, qvx.Q4_K, qvx.Q6_K]
+GEMV_TYPES = [qvx.Q8_0, qvx.Q4_0, qvx.Q4_K, qvx.Q5_K, qvx.Q6_K]
 
 
 def f32bits(a):
@@ -198,13 +198,13 @@ def test_gemv_q4k_batched_form_bit_identical(cuda, rows, cols, nvec):
         np.testing.assert_array_equal(f32bits(got[v]), f32bits(single[0]))
 
 
-OTHER_TYPES = [qvx.F16, qvx.BF16, qvx.Q4_1, qvx.Q5_0, qvx.Q5_1, qvx.Q8_1, qvx.Q5_K]
+OTHER_TYPES = [qvx.F16, qvx.BF16, qvx.Q4_1, qvx.Q5_0, qvx.Q5_1, qvx.Q8_1]
 
 
 @pytest.mark.parametrize("t", OTHER_TYPES)
 @pytest.mark.parametrize("rows,cols,nvec", [(37, 256, 1), (300, 2048, 3), (1024, 4096, 2)])
 def test_gemv_other_dequantizable_types(cuda, t, rows, cols, nvec):
-    """Types the reference's qmatmul accepts beyond the four tuned formats run on the generic kernel:
+    """Types the reference's qmatmul accepts beyond the tuned formats run on the generic kernel:
     within tolerance of the oracle, batched calls bit-identical to single ones."""
     rng = np.random.default_rng(rows + cols + 13 * t + nvec)
     w = random_weight(t, rows, cols, rng)
@@ -383,7 +383,7 @@ def test_quantize_act_q8_matches_oracle(cuda):
 # ---- synthetic data generator ---------------------------------------------------------------------
 
 def test_synthetic_blocks_are_well_formed(cuda):
-    for t, mul in ((qvx.Q8_0, 0.01), (qvx.Q4_0, 0.02), (qvx.Q4_K, 1e-3), (qvx.Q6_K, 1e-3)):
+    for t, mul in ((qvx.Q8_0, 0.01), (qvx.Q4_0, 0.02), (qvx.Q4_K, 1e-3), (qvx.Q5_K, 1e-3), (qvx.Q6_K, 1e-3)):
         rows, cols = 64, 4096
         W = qvx.empty_weight(t, rows, cols)
         qvx.fill_synthetic_t(W, t, rows, cols, seed=5, scale_mul=mul)
