@@ -22,6 +22,9 @@ bool launch_gemv_generic(uint32_t t, const void* w, const float* X, float* Y, in
 bool launch_gemv_fast(uint32_t t, const void* w, const float* X, float* Y, int nvec, int rows, int cols,
                       size_t row_bytes, hipStream_t s);
 int gemv_mx_max_nv(int cols);
+int gemv_mxj_supported(int cols);
+bool launch_gemv_mxj_q4k(const void* w, const float* X, float* Y, int nvec, int rows, int cols, size_t row_bytes,
+                         hipStream_t s);
 bool launch_gemv_mx_q4k(const void* w, const float* X, float* Y, int nvec, int rows, int cols, size_t row_bytes,
                         hipStream_t s);
 int gemv_mxb_supported(int cols);
@@ -100,15 +103,18 @@ int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int
   // same in every launch, so batches stay bit-identical to single vectors.  Q4_K runs on the matrix
   // cores (up to gemv_mx_max_nv vectors per launch), the other formats on the VALU kernel; shapes
   // neither covers go to the generic kernel.
-  // Q4_K batches of two or more vectors take the batched matrix-core form (8 vectors a launch,
-  // bit-identical to the one-vector form) where its fragments fit in LDS.
-  if (fast && type == T_Q4_K && nvec >= 2 && gemv_mxb_supported(cols)) {
+  // Q4_K batches of two or more vectors take a batched matrix-core form (8 vectors a launch,
+  // bit-identical to the one-vector form): the one that stages a whole row's activation fragments
+  // in LDS where they fit, else the long-row one that converts them per super-block.
+  if (fast && type == T_Q4_K && nvec >= 2 && (gemv_mxb_supported(cols) || gemv_mxj_supported(cols))) {
+    const bool whole = gemv_mxb_supported(cols) != 0;
     for (int v0 = 0; v0 < nvec; v0 += 8) {
       const int nv = nvec - v0 < 8 ? nvec - v0 : 8;
-      const bool ok = nv == 1 ? launch_gemv_mx_q4k(w, X + (size_t)v0 * cols, out + (size_t)v0 * rows, 1, rows, cols,
-                                                   row_bytes, s)
-                              : launch_gemv_mxb_q4k(w, X + (size_t)v0 * cols, out + (size_t)v0 * rows, nv, rows,
-                                                    cols, row_bytes, s);
+      const float* Xv = X + (size_t)v0 * cols;
+      float* Yv = out + (size_t)v0 * rows;
+      const bool ok = nv == 1  ? launch_gemv_mx_q4k(w, Xv, Yv, 1, rows, cols, row_bytes, s)
+                      : whole ? launch_gemv_mxb_q4k(w, Xv, Yv, nv, rows, cols, row_bytes, s)
+                              : launch_gemv_mxj_q4k(w, Xv, Yv, nv, rows, cols, row_bytes, s);
       if (!ok) return QVX_E_TYPE;
     }
     return hip_status();

@@ -438,6 +438,42 @@ __device__ inline void q4k_group_scales(const u32x4& hd, int c, float& sca, floa
   mnb = (float)(sm >> 24);
 }
 
+// One tile's MFMAs and fold: header hd and codes qq (this lane's row j = lane%16, K block
+// r4 = lane/16), A fragments af[sb] of the super-block's eight sub-blocks, activation records
+// mf[2c + e] of group c for vectors 2 r4 + e.  acc[e][c] += the group's term, for both vectors.
+// Group c of the tile: A fragments a0 / a1 of sub-blocks 2c / 2c+1, records m0 / m1 of vectors
+// 2 r4 / 2 r4 + 1 ([sx, Qa, Qb, ...]).
+template <typename MT>
+__device__ inline void mxb_fold_group(int c, const u32x4& hd, const u32x2& q, const u32x2& a0, const u32x2& a1,
+                                      const MT& m0, const MT& m1, float (&acc)[2][4]) {
+  const float d = f16lo(hd.x), dmin = f16hi(hd.x);
+  const u32x2 bl = {q.x & 0x0F0F0F0Fu, q.y & 0x0F0F0F0Fu};
+  const u32x2 bh = {(q.x >> 4) & 0x0F0F0F0Fu, (q.y >> 4) & 0x0F0F0F0Fu};
+  const v4i zero = {0, 0, 0, 0};
+  const v4i da =
+      __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, a0), __builtin_bit_cast(long, bl), zero, 0, 0, 0);
+  const v4i db =
+      __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, a1), __builtin_bit_cast(long, bh), zero, 0, 0, 0);
+  float sca, scb16, mna, mnb;
+  q4k_group_scales(hd, c, sca, scb16, mna, mnb);
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const MT mt = e == 0 ? m0 : m1;
+    const int ta = (int)((uint32_t)da[2 * e] << 7) + da[2 * e + 1];                      // sum n q, sub-block 2c
+    const int tb = (int)((((uint32_t)db[2 * e] << 7) + (uint32_t)db[2 * e + 1]) << 4);  // 16 sum n q, 2c+1
+    const float t = __builtin_fmaf((float)tb, scb16, (float)ta * sca);
+    const float w = __builtin_fmaf(__uint_as_float(mt.z), mnb, __uint_as_float(mt.y) * mna);
+    acc[e][c] = __builtin_fmaf(__builtin_fmaf(d, t, -dmin * w), __uint_as_float(mt.x), acc[e][c]);
+  }
+}
+
+template <typename MT>
+__device__ inline void mxb_fold(const u32x4& hd, const u32x2 (&qq)[4], const u32x2 (&af)[8], const MT (&mf)[8],
+                                float (&acc)[2][4]) {
+#pragma unroll
+  for (int c = 0; c < 4; ++c) mxb_fold_group(c, hd, qq[c], af[2 * c], af[2 * c + 1], mf[2 * c], mf[2 * c + 1], acc);
+}
+
 template <int TPT>
 __global__ __launch_bounds__(1024) void k_gemv_mxb(const uint8_t* __restrict__ W, const float* __restrict__ X,
                                                    float* __restrict__ Y, int rows, int cols, int nv, MxGeo geo) {
@@ -509,7 +545,6 @@ __global__ __launch_bounds__(1024) void k_gemv_mxb(const uint8_t* __restrict__ W
     lds_wait5(hd, q0, q1, q2, q3);
     if (u + NB < nu) mx_issue(rsrc, off, s + NB, stage + slot * kTileBytes);
     slot = slot + 1 == NB ? 0 : slot + 1;
-    const float d = f16lo(hd.x), dmin = f16hi(hd.x);
     const u32x2 qq[4] = {q0, q1, q2, q3};
     // every A fragment and activation record of the tile in one round trip
     u32x2 af[8];
@@ -524,32 +559,182 @@ __global__ __launch_bounds__(1024) void k_gemv_mxb(const uint8_t* __restrict__ W
       mf[2 * c + 1] = lds_read16<16>(ma + (uint32_t)c * 128u);
     }
     lds_wait16(af, mf);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const u32x2 bl = {qq[c].x & 0x0F0F0F0Fu, qq[c].y & 0x0F0F0F0Fu};
-      const u32x2 bh = {(qq[c].x >> 4) & 0x0F0F0F0Fu, (qq[c].y >> 4) & 0x0F0F0F0Fu};
-      const v4i zero = {0, 0, 0, 0};
-      const v4i da = __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, af[2 * c]),
-                                                           __builtin_bit_cast(long, bl), zero, 0, 0, 0);
-      const v4i db = __builtin_amdgcn_mfma_i32_16x16x32_i8(__builtin_bit_cast(long, af[2 * c + 1]),
-                                                           __builtin_bit_cast(long, bh), zero, 0, 0, 0);
-      float sca, scb16, mna, mnb;
-      q4k_group_scales(hd, c, sca, scb16, mna, mnb);
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const u32x4 mt = mf[2 * c + e];  // [sx, Qa, Qb, 128 Qb]
-        const int ta = (int)((uint32_t)da[2 * e] << 7) + da[2 * e + 1];                      // sum n q, sub-block 2c
-        const int tb = (int)((((uint32_t)db[2 * e] << 7) + (uint32_t)db[2 * e + 1]) << 4);  // 16 sum n q, 2c+1
-        const float t = __builtin_fmaf((float)tb, scb16, (float)ta * sca);
-        const float w = __builtin_fmaf(__uint_as_float(mt.z), mnb, __uint_as_float(mt.y) * mna);
-        acc[e][c] = __builtin_fmaf(__builtin_fmaf(d, t, -dmin * w), __uint_as_float(mt.x), acc[e][c]);
-      }
-    }
+    mxb_fold(hd, qq, af, mf, acc);
   }
 
   wait_vm<0>();
 
   // 4. groups as (g0 + g2) + (g1 + g3), then the KQ waves of the tile in wave order
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(ring);  // [tq][kq][v][16]
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int v = 2 * r4 + e;
+    if (v < nv) red[((tq * KQ + kq) * nv + v) * 16 + j] = (acc[e][0] + acc[e][2]) + (acc[e][1] + acc[e][3]);
+  }
+  __syncthreads();
+  for (int o = tid; o < TQ * nv * 16; o += 1024) {
+    const int t = o / (nv * 16), v = (o >> 4) % nv, r = o & 15;
+    const int row = 16 * t + r;
+    if (row < cnt) {
+      float sum = 0.0f;
+      for (int k = 0; k < KQ; ++k) sum += red[((t * KQ + k) * nv + v) * 16 + r];
+      Y[(size_t)v * rows + rb + row] = sum;
+    }
+  }
+}
+
+// ---- batched form for long rows -----------------------------------------------------------------
+// Where the batched form's fragments for a whole row do not fit in LDS, each wave converts the
+// activations of one super-block just before it folds that super-block, into a private buffer with
+// the batched form's layout ([sb][kg][row] fragments, [g][v] records: 4.5 KB), so LDS use does not
+// depend on K.  The next super-block's activations are loaded into registers while the current
+// one is folded: issue order x(s0) c(s0) c(s0+1) | x(s0+1) c(s0+2) | ..., so at step u the wave
+// needs x(u) and c(u) and only c(u+1) may still be in flight (vmcnt 3); the last two steps are
+// peeled so that every wait is exact.  The geometry, the conversion (the same 8-lane task groups)
+// and the fold are the batched form's, so outputs stay bit-identical to the one-vector kernel's.
+// Waves whose tiles share super-blocks (TQ > 1) convert them again each: the form is meant for
+// the long-row shapes, where rows <= 16 * 256 and TQ = 1.
+
+constexpr int kJitBytes = 8 * kSubBytes + 4 * 8 * 16;  // one super-block: fragments + records
+
+// NVT conversion rounds per lane: task t = lane + 64 k = 8 elements (vector t/32, group (t%32)/8,
+// part t%8); the vector index is clamped for the loads, the stores skip vectors >= nv.
+template <int NVT>
+struct XRegs {
+  float4 a[NVT], b[NVT];
+};
+
+template <int NVT>
+__device__ inline void mxj_load(const float* __restrict__ X, int cols, int nv, int s, int lane, XRegs<NVT>& x) {
+#pragma unroll
+  for (int k = 0; k < NVT; ++k) {
+    const int t = lane + 64 * k, v = min(t >> 5, nv - 1), r = t & 31;
+    const float4* p = reinterpret_cast<const float4*>(X + (size_t)v * cols + 256 * s + 8 * r);
+    x.a[k] = p[0];
+    x.b[k] = p[1];
+  }
+}
+
+template <int NVT>
+__device__ inline void mxj_convert(const XRegs<NVT>& x, int nv, int lane, uint8_t* frag, float* meta) {
+#pragma unroll
+  for (int k = 0; k < NVT; ++k) {
+    const int t = lane + 64 * k, v = t >> 5, r = t & 31;
+    mxb_convert(x.a[k], x.b[k], v, r >> 3, r & 7, v < nv, frag, meta);
+  }
+}
+
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+template <int OFF = 0>
+__device__ inline u32x3 lds_read12(uint32_t addr) {
+  u32x3 r;
+  asm volatile("ds_read_b96 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF) : "memory");
+  return r;
+}
+
+__device__ inline void lds_wait13(u32x4& h, u32x2 (&q)[4], u32x2 (&a)[4], u32x3 (&m)[4]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(h), "+v"(q[0]), "+v"(q[1]), "+v"(q[2]), "+v"(q[3]), "+v"(a[0]), "+v"(a[1]), "+v"(a[2]),
+                 "+v"(a[3]), "+v"(m[0]), "+v"(m[1]), "+v"(m[2]), "+v"(m[3])::"memory");
+}
+__device__ inline void lds_wait8(u32x2 (&a)[4], u32x3 (&m)[4]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(m[0]), "+v"(m[1]), "+v"(m[2]), "+v"(m[3])::"memory");
+}
+
+// A fragments of sub-blocks 4h..4h+3 and the records of groups 2h, 2h+1 (this lane's two vectors).
+__device__ inline void mxj_read_half(int h, uint32_t fa, uint32_t ma, u32x2 (&a)[4], u32x3 (&m)[4]) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) a[k] = lds_read8(fa + (uint32_t)(4 * h + k) * kSubBytes);
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    m[2 * c] = lds_read12(ma + (uint32_t)(2 * h + c) * 128u);
+    m[2 * c + 1] = lds_read12<16>(ma + (uint32_t)(2 * h + c) * 128u);
+  }
+}
+
+template <int NVT>
+__global__ __launch_bounds__(1024) void k_gemv_mxj(const uint8_t* __restrict__ W, const float* __restrict__ X,
+                                                   float* __restrict__ Y, int rows, int cols, int nv, MxGeo geo) {
+  constexpr int NB = 2;
+  __shared__ __attribute__((aligned(16))) uint8_t ring[16 * NB * kTileBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t jit[16 * kJitBytes];
+  const int nsb = geo.nsb, TQ = geo.TQ, KQ = geo.KQ;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  uint8_t* frag = jit + wave * kJitBytes;
+  float* meta = reinterpret_cast<float*>(frag + 8 * kSubBytes);
+  QVX_LDS uint8_t* stage = (QVX_LDS uint8_t*)(ring + wave * NB * kTileBytes);
+
+  const int b = blockIdx.x;
+  const int rb = b * geo.base + min(b, geo.rem), cnt = geo.base + (b < geo.rem ? 1 : 0);
+  const int tq = wave % TQ, kq = wave / TQ;
+  const int s0 = kq * nsb / KQ, s1 = (kq + 1) * nsb / KQ, nu = s1 - s0;
+
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(W + (size_t)rb * geo.row_bytes), (short)0, (int)((uint32_t)cnt * geo.row_bytes), (int)kRsrcWord3);
+  uint32_t off[3];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    const uint32_t p = k < 2 ? (uint32_t)(1024 * k + 16 * lane) : (uint32_t)(2048 + 4 * lane);
+    const uint32_t r = p / (uint32_t)kSB, c = p - (uint32_t)kSB * r;
+    off[k] = __umul24(16u * (uint32_t)tq + r, geo.row_bytes) + c;
+  }
+
+  const int j = lane & 15, r4 = lane >> 4;  // B column (tile row) and K block; D rows 4 r4..4 r4+3
+  const uint32_t b_hd = kSB * j, b_q = kSB * j + 16 + 8 * r4;
+  const uint32_t fa = lds_addr(frag) + 8u * (uint32_t)lane;
+  const uint32_t ma = lds_addr(meta) + 32u * (uint32_t)r4;  // vectors 2 r4, 2 r4 + 1
+  const uint32_t stage_base = (uint32_t)(uintptr_t)stage;
+  float acc[2][4];
+#pragma unroll
+  for (int e = 0; e < 2; ++e)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[e][c] = 0.0f;
+  XRegs<NVT> x;
+
+  // step u: super-block s0 + u is in stage u & 1 and its activations in x
+#define QVX_MXJ_STEP(U, WAITN, NEXT_X, NEXT_COPY)                                                    \
+  {                                                                                                  \
+    wait_vm<WAITN>();                                                                                \
+    mxj_convert<NVT>(x, nv, lane, frag, meta);                                                       \
+    const uint32_t st = stage_base + (uint32_t)((U) & 1) * kTileBytes;                              \
+    u32x4 hd = lds_read16(st + b_hd);                                                                \
+    u32x2 qq[4];                                                                                     \
+    _Pragma("unroll") for (int c = 0; c < 4; ++c) qq[c] = lds_read8(st + b_q + 32u * (uint32_t)c);  \
+    u32x2 a0[4], a1[4];                                                                              \
+    u32x3 m0[4], m1[4];                                                                              \
+    mxj_read_half(0, fa, ma, a0, m0);                                                                \
+    lds_wait13(hd, qq, a0, m0);                                                                      \
+    if (NEXT_X) mxj_load<NVT>(X, cols, nv, s0 + (U) + 1, lane, x);                                   \
+    if (NEXT_COPY) mx_issue(rsrc, off, s0 + (U) + 2, stage + ((U) & 1) * kTileBytes);                \
+    mxj_read_half(1, fa, ma, a1, m1);                                                                \
+    mxb_fold_group(0, hd, qq[0], a0[0], a0[1], m0[0], m0[1], acc);                                   \
+    mxb_fold_group(1, hd, qq[1], a0[2], a0[3], m0[2], m0[3], acc);                                   \
+    lds_wait8(a1, m1);                                                                               \
+    mxb_fold_group(2, hd, qq[2], a1[0], a1[1], m1[0], m1[1], acc);                                   \
+    mxb_fold_group(3, hd, qq[3], a1[2], a1[3], m1[2], m1[3], acc);                                   \
+  }
+
+  if (nu >= 2) {
+    mxj_load<NVT>(X, cols, nv, s0, lane, x);
+    mx_issue(rsrc, off, s0, stage);
+    mx_issue(rsrc, off, s0 + 1, stage + kTileBytes);
+    int u = 0;
+    for (; u + 2 < nu; ++u) QVX_MXJ_STEP(u, 3, true, true)
+    QVX_MXJ_STEP(u, 3, true, false)
+    ++u;
+    QVX_MXJ_STEP(u, 0, false, false)
+  } else if (nu == 1) {
+    mxj_load<NVT>(X, cols, nv, s0, lane, x);
+    mx_issue(rsrc, off, s0, stage);
+    QVX_MXJ_STEP(0, 0, false, false)
+  }
+#undef QVX_MXJ_STEP
+  wait_vm<0>();
+
+  // groups as (g0 + g2) + (g1 + g3), then the KQ waves of the tile in wave order
   __syncthreads();
   float* red = reinterpret_cast<float*>(ring);  // [tq][kq][v][16]
 #pragma unroll
@@ -644,6 +829,28 @@ bool launch_gemv_mxb_q4k(const void* w, const float* X, float* Y, int nvec, int 
   return true;
 }
 
+// 1 if the long-row batched form takes `cols`: whole super-blocks, and the one-vector kernel takes
+// the same shape (the form's outputs are bit-identical to that kernel's, which single-vector calls
+// run).
+int gemv_mxj_supported(int cols);
+
+// Q4_K GEMV on the matrix cores, 1 <= nvec <= 8 vectors, long-row batched form (LDS use
+// independent of K).  Returns false, having launched nothing, when the shape is not handled here.
+bool launch_gemv_mxj_q4k(const void* w, const float* X, float* Y, int nvec, int rows, int cols, size_t row_bytes,
+                         hipStream_t s) {
+  if (!gemv_mxj_supported(cols) || nvec < 1 || nvec > 8 || row_bytes >= (1u << 24)) return false;
+  MxGeo geo{};
+  const int nwg = mx_geometry(rows, cols, row_bytes, geo);
+  auto* wp = static_cast<const uint8_t*>(w);
+  switch ((nvec + 1) / 2) {
+    case 1: k_gemv_mxj<1><<<(unsigned)nwg, 1024u, 0, s>>>(wp, X, Y, rows, cols, nvec, geo); break;
+    case 2: k_gemv_mxj<2><<<(unsigned)nwg, 1024u, 0, s>>>(wp, X, Y, rows, cols, nvec, geo); break;
+    case 3: k_gemv_mxj<3><<<(unsigned)nwg, 1024u, 0, s>>>(wp, X, Y, rows, cols, nvec, geo); break;
+    default: k_gemv_mxj<4><<<(unsigned)nwg, 1024u, 0, s>>>(wp, X, Y, rows, cols, nvec, geo); break;
+  }
+  return true;
+}
+
 // Largest vector count one launch takes for a row of `cols` columns (LDS budget), 0 if the shape
 // is not handled here.
 int gemv_mx_max_nv(int cols) {
@@ -673,6 +880,10 @@ bool launch_gemv_mx_q4k(const void* w, const float* X, float* Y, int nvec, int r
     default: launch_mx_nv<8>(w, X, Y, rows, cols, geo, nwg, s); break;
   }
   return true;
+}
+
+int gemv_mxj_supported(int cols) {
+  return cols > 0 && cols % 256 == 0 && gemv_mx_max_nv(cols) >= 1 ? 1 : 0;
 }
 
 }  // namespace qvx

@@ -198,6 +198,24 @@ def test_gemv_q4k_batched_form_bit_identical(cuda, rows, cols, nvec):
         np.testing.assert_array_equal(f32bits(got[v]), f32bits(single[0]))
 
 
+@pytest.mark.parametrize("rows,cols,nvec", [(4096, 14336, 16), (4096, 14336, 3), (300, 14336, 5), (4099, 14336, 8),
+                                             (17, 5120, 2), (64, 4352, 7), (1000, 28672, 8), (33, 4608, 6)])
+def test_gemv_q4k_long_row_batched_form_bit_identical(cuda, rows, cols, nvec):
+    """Rows too long for the batched form's whole-row fragments (K > 4096) take the long-row form
+    (activations converted per super-block by each wave): within tolerance of the oracle and
+    bit-identical to one-vector calls, across K splits where waves own one or two super-blocks,
+    ragged rows, and more than 16 rows per workgroup (tiles sharing super-blocks)."""
+    t = qvx.Q4_K
+    rng = np.random.default_rng(rows + 5 * cols + nvec)
+    w = random_weight(t, rows, cols, rng)
+    X = rng.standard_normal((nvec, cols)).astype(np.float32)
+    got = run_gemv(cuda, w, t, X, rows, cols)
+    assert max_rel(got, oracle.matmul_f64(w, t, X, nvec, rows, cols)) <= GEMV_TOL
+    for v in range(nvec):
+        single = run_gemv(cuda, w, t, X[v:v + 1], rows, cols)
+        np.testing.assert_array_equal(f32bits(got[v]), f32bits(single[0]))
+
+
 OTHER_TYPES = [qvx.F16, qvx.BF16, qvx.Q4_1, qvx.Q5_0, qvx.Q5_1, qvx.Q8_1]
 
 
