@@ -60,7 +60,8 @@ const char* qvx_strerror(int code);
 
 /* 1 if qvx_qmatmul / qvx_qmatmul_n compute `type` (qmatmul.cpp:24-26, qmatmulSupports): every
  * type the reference dequantises (F32, F16, BF16, Q8_0, Q8_1, Q4_0, Q4_1, Q5_0, Q5_1, Q4_K, Q5_K,
- * Q6_K).  Q8_0 / Q4_0 / Q4_K / Q5_K / Q6_K run on the fast kernels, the others on a generic kernel;
+ * Q6_K).  Q8_0 / Q4_0 / Q5_0 / Q4_K / Q5_K / Q6_K run on the integer fast kernels, F32 / F16 /
+ * BF16 on the float kernel, Q8_1 / Q4_1 / Q5_1 and unaligned weights on a generic kernel;
  * qvx_qgemm_f16 computes Q4_K only. */
 int qvx_supports(uint32_t type);
 

@@ -21,6 +21,8 @@ bool launch_gemv_generic(uint32_t t, const void* w, const float* X, float* Y, in
                          size_t row_bytes, hipStream_t s);
 bool launch_gemv_fast(uint32_t t, const void* w, const float* X, float* Y, int nvec, int rows, int cols,
                       size_t row_bytes, hipStream_t s);
+bool launch_gemv_float(uint32_t t, const void* w, const float* X, float* Y, int nvec, int rows, int cols,
+                       size_t row_bytes, hipStream_t s);
 int gemv_mx_max_nv(int cols);
 int gemv_mxj_supported(int cols);
 bool launch_gemv_mxj_q4k(const void* w, const float* X, float* Y, int nvec, int rows, int cols, size_t row_bytes,
@@ -98,7 +100,11 @@ int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int
   }
   if (!w || !X) return QVX_E_NULL;
   const size_t row_bytes = (size_t)(cols / (int)ti->block) * ti->bytes;
-  const bool fast = type != T_F32 && aligned16(w) && aligned16(X) && row_bytes % 16 == 0;
+  const bool fast = aligned16(w) && aligned16(X) && row_bytes % 16 == 0;
+  // Unquantised weights stream through the float kernel.
+  if (fast && (type == T_F32 || type == T_F16 || type == T_BF16) &&
+      launch_gemv_float(type, w, X, out, nvec, rows, cols, row_bytes, s))
+    return hip_status();
   // The fast kernels take any number of vectors, a few per launch; each vector's arithmetic is the
   // same in every launch, so batches stay bit-identical to single vectors.  Q4_K runs on the matrix
   // cores (up to gemv_mx_max_nv vectors per launch), the other formats on the VALU kernel; shapes

@@ -286,6 +286,52 @@ template <> struct Lane<T_Q4_0> {
   }
 };
 
+// Q5_0: slot sig = blocks 2 sig, 2 sig + 1 (44 bytes at 44 sig, dword aligned): block k holds its
+// fp16 scale at bytes 22k..22k+1, the fifth bits qh (bit i for element i) at 22k+2..22k+5 and qs at
+// 22k+6..22k+21; element i < 16 is (qs[i] & 15) + 16 * bit i, element 16 + i is (qs[i] >> 4) +
+// 16 * bit (16 + i), value d * (code - 16) (dequant.cpp:75-91).  Runs as for Q4_0.  Codes 0..31
+// are multiplied as they are and 16 * sum q subtracted per block.
+template <> struct Lane<T_Q5_0> {
+  static constexpr int kR = 4;
+  static constexpr int kSlotElems = 64;
+  struct Raw {
+    u32x4a4_t a, b;
+    uint32_t c0, c1, c2;
+  };
+  static __device__ inline int xoff(int sig, int run) { return 64 * sig + 16 * run; }
+  static __device__ inline void load(const uint8_t* row, int sig, Raw& r) {
+    const uint8_t* p = row + 44 * sig;
+    r.a = ldg16a4(p);
+    r.b = ldg16a4(p + 16);
+    r.c0 = ldg4(p + 32);
+    r.c1 = ldg4(p + 36);
+    r.c2 = ldg4(p + 40);
+  }
+  // byte k of the result = 16 * bit k of the low four bits of n
+  static __device__ inline uint32_t spread4(uint32_t n) { return (__umul24(n & 15u, 0x00204081u) & 0x01010101u) << 4; }
+  // sum((code - 16) q) over one block: quant dwords qs, fifth bits qh
+  static __device__ inline int block(const uint32_t (&qs)[4], uint32_t qh, const uint32_t* h, const uint32_t* l,
+                                     int q_lo, int q_hi) {
+    uint32_t lo[4], hi[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      lo[j] = (qs[j] & 0x0F0F0F0Fu) | spread4(qh >> (4 * j));
+      hi[j] = ((qs[j] >> 4) & 0x0F0F0F0Fu) | spread4(qh >> (16 + 4 * j));
+    }
+    return dotq<4>(lo, h, l) + dotq<4>(hi, h + 4, l + 4) - 16 * (q_lo + q_hi);
+  }
+  static __device__ inline float row(const Raw& r, int, const XQ<4>& x) {
+    const uint32_t w[11] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w, r.c0, r.c1, r.c2};
+    const uint32_t qh0 = align_bytes(w[1], w[0], 2);  // bytes 2..5
+    const uint32_t q0[4] = {align_bytes(w[2], w[1], 2), align_bytes(w[3], w[2], 2), align_bytes(w[4], w[3], 2),
+                            align_bytes(w[5], w[4], 2)};  // bytes 6..21
+    const uint32_t q1[4] = {w[7], w[8], w[9], w[10]};   // bytes 28..43
+    const int v0 = block(q0, qh0, x.h, x.l, x.q[0], x.q[1]);
+    const int v1 = block(q1, w[6], x.h + 8, x.l + 8, x.q[2], x.q[3]);
+    return __builtin_fmaf(f16hi(w[5]), (float)v1, f16lo(w[0]) * (float)v0);
+  }
+};
+
 // Q8_0: slot sig = blocks 2 sig, 2 sig + 1 (68 bytes at 68 sig, dword aligned): block k holds its
 // fp16 scale at bytes 34k..34k+1 and 32 signed codes at 34k+2..34k+33.  Runs 0, 1 = block 0.
 template <> struct Lane<T_Q8_0> {
@@ -665,7 +711,7 @@ static bool launch_fast_t(const void* w, const float* X, float* Y, int nvec, int
   return true;
 }
 
-// Fast-path GEMV for nvec >= 1 on 16-byte-aligned rows of Q8_0 / Q4_0 / Q4_K / Q5_K / Q6_K.  Returns
+// Fast-path GEMV for nvec >= 1 on 16-byte-aligned rows of Q8_0 / Q4_0 / Q5_0 / Q4_K / Q5_K / Q6_K.  Returns
 // false, having launched nothing, when the shape needs the generic kernel.
 bool launch_gemv_fast(uint32_t t, const void* w, const float* X, float* Y, int nvec, int rows, int cols,
                       size_t row_bytes, hipStream_t s) {
@@ -674,6 +720,7 @@ bool launch_gemv_fast(uint32_t t, const void* w, const float* X, float* Y, int n
     case T_Q6_K: return launch_fast_t<T_Q6_K>(w, X, Y, nvec, rows, cols, row_bytes, s);
     case T_Q5_K: return launch_fast_t<T_Q5_K>(w, X, Y, nvec, rows, cols, row_bytes, s);
     case T_Q4_0: return launch_fast_t<T_Q4_0>(w, X, Y, nvec, rows, cols, row_bytes, s);
+    case T_Q5_0: return launch_fast_t<T_Q5_0>(w, X, Y, nvec, rows, cols, row_bytes, s);
     case T_Q8_0: return launch_fast_t<T_Q8_0>(w, X, Y, nvec, rows, cols, row_bytes, s);
     default: return false;
   }

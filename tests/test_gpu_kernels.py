@@ -22,7 +22,7 @@ BLOCK = {qvx.Q4_0: (32, 18), qvx.Q4_1: (32, 20), qvx.Q5_0: (32, 22), qvx.Q5_1: (
          qvx.F16: (1, 2), qvx.BF16: (1, 2), qvx.F32: (1, 4)}
 HALF_OFFS = {qvx.Q4_0: [0], qvx.Q4_1: [0, 2], qvx.Q5_0: [0], qvx.Q5_1: [0, 2], qvx.Q8_0: [0], qvx.Q8_1: [0, 2],
              qvx.Q4_K: [0, 2], qvx.Q5_K: [0, 2], qvx.Q6_K: [208]}
-GEMV_TYPES = [qvx.Q8_0, qvx.Q4_0, qvx.Q4_K, qvx.Q5_K, qvx.Q6_K]
+GEMV_TYPES = [qvx.Q8_0, qvx.Q4_0, qvx.Q5_0, qvx.Q4_K, qvx.Q5_K, qvx.Q6_K]
 
 
 def f32bits(a):
@@ -216,13 +216,14 @@ def test_gemv_q4k_long_row_batched_form_bit_identical(cuda, rows, cols, nvec):
         np.testing.assert_array_equal(f32bits(got[v]), f32bits(single[0]))
 
 
-OTHER_TYPES = [qvx.F16, qvx.BF16, qvx.Q4_1, qvx.Q5_0, qvx.Q5_1, qvx.Q8_1]
+OTHER_TYPES = [qvx.F16, qvx.BF16, qvx.Q4_1, qvx.Q5_1, qvx.Q8_1]
 
 
 @pytest.mark.parametrize("t", OTHER_TYPES)
 @pytest.mark.parametrize("rows,cols,nvec", [(37, 256, 1), (300, 2048, 3), (1024, 4096, 2)])
 def test_gemv_other_dequantizable_types(cuda, t, rows, cols, nvec):
-    """Types the reference's qmatmul accepts beyond the tuned formats run on the generic kernel:
+    """Types the reference's qmatmul accepts beyond the integer fast kernels (the float kernel for
+    F16 / BF16, the generic kernel for the rest):
     within tolerance of the oracle, batched calls bit-identical to single ones."""
     rng = np.random.default_rng(rows + cols + 13 * t + nvec)
     w = random_weight(t, rows, cols, rng)
@@ -244,6 +245,26 @@ def test_gemv_unaligned_weight_uses_generic_path(cuda, t):
     for off in (0, 2, 6):
         got = run_gemv(cuda, w, t, X, rows, cols, offset=off)
         assert max_rel(got, ref) <= GEMV_TOL
+
+
+FLOAT_TYPES = [qvx.F32, qvx.F16, qvx.BF16]
+
+
+@pytest.mark.parametrize("t", FLOAT_TYPES)
+@pytest.mark.parametrize("rows,cols,nvec", [(4096, 4096, 9), (33, 520, 3), (300, 14336, 5), (17, 32768, 2),
+                                             (5, 33280, 2), (1, 8, 1)])
+def test_gemv_float_weights(cuda, t, rows, cols, nvec):
+    """Unquantised weights on the float kernel: within tolerance of the oracle (fp32 dequant + f64
+    dot) and batched calls bit-identical to single ones, across rows that end inside a block of
+    chunks, K where the activation budget takes 4, 2 or 1 vectors a launch, and K past it (the
+    generic kernel)."""
+    rng = np.random.default_rng(rows + cols + 7 * t + nvec)
+    w = random_weight(t, rows, cols, rng)
+    X = rng.standard_normal((nvec, cols)).astype(np.float32)
+    got = run_gemv(cuda, w, t, X, rows, cols)
+    assert max_rel(got, oracle.matmul_f64(w, t, X, nvec, rows, cols)) <= GEMV_TOL
+    for v in range(nvec):
+        np.testing.assert_array_equal(f32bits(got[v]), f32bits(run_gemv(cuda, w, t, X[v:v + 1], rows, cols)[0]))
 
 
 def test_gemv_f32_weight(cuda):
