@@ -490,12 +490,14 @@ struct Geo {
   uint32_t row_bytes;
 };
 
-// One workgroup: G groups of Sp lanes; group g computes rows rb + g + G*i (i < RMAX, g + G*i < cnt).
+// One workgroup: G groups of Sp lanes; group g computes rows rb + g + G*i (g + G*i < cnt), RMAX rows
+// a chunk, so one workgroup per CU can stream any number of rows after converting the activations
+// once.
 // TPT = conversion tasks per thread (NV * S * 2R <= TPT * blockDim).  Every global load is issued
 // unconditionally (rows past the workgroup's last are clamped to it and their results dropped):
 // activations first, then the first PF rows, and each later row PF rows ahead of its use, so a
 // row's arithmetic waits only for its own bytes while the next ones are arriving.
-template <uint32_t T, int NV, int RMAX, int TPT, int PF>
+template <uint32_t T, int NV, int RMAX, int TPT, int PF, bool CH>
 __global__ __launch_bounds__(1024) void k_gemv(const uint8_t* __restrict__ W, const float* __restrict__ X,
                                                float* __restrict__ Y, int rows, int cols, Geo geo) {
   using L = Lane<T>;
@@ -534,53 +536,65 @@ __global__ __launch_bounds__(1024) void k_gemv(const uint8_t* __restrict__ W, co
   }
   __syncthreads();
 
-  // 4. rows in arrival order
+  // 4. rows in arrival order, RMAX at a time; each chunk is reduced and written before the next.
+  // CH (several chunks): the loads run PF rows ahead across chunk boundaries (RMAX is a multiple of
+  // PF, so row i always lands in raw[i % PF]); like every row load they are unconditional, the last
+  // chunk's PF look-ahead loads re-reading the last row.  Without CH there is one chunk and no
+  // load past it.
   XQ<R> x[NV];
 #pragma unroll
   for (int v = 0; v < NV; ++v) read_xq<R>(xs + ((size_t)v * S + sig) * xq_words<R>(), x[v]);
   const float keep = sig0 < S ? 1.0f : 0.0f;
-  float p[RMAX][NV];
-#pragma unroll
-  for (int i = 0; i < RMAX; ++i) {
-#pragma unroll
-    for (int v = 0; v < NV; ++v) p[i][v] = L::row(raw[i % PF], sig, x[v]) * (x[v].sx * keep);
-    if (i + PF < RMAX) L::load(wb + (uint32_t)min(g + G * (i + PF), cnt - 1) * geo.row_bytes, sig, raw[i % PF]);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-
-  // 5. reduction over the group's S' lanes (fixed order)
-  if (Sp <= 64) {
+  static_assert(!CH || RMAX % PF == 0, "chunks keep the prefetch ring aligned");
+  const int nchunk = CH ? ((cnt + G - 1) / G + RMAX - 1) / RMAX : 1;  // the same for every group
+  for (int c = 0; c < nchunk; ++c) {
+    const int i0 = c * RMAX;
+    float p[RMAX][NV];
 #pragma unroll
     for (int i = 0; i < RMAX; ++i) {
 #pragma unroll
-      for (int v = 0; v < NV; ++v) {
-        const float s = span_sum(p[i][v], Sp);
-        if (sig0 == 0 && g + G * i < cnt) Y[(size_t)v * rows + rb + g + G * i] = s;
-      }
+      for (int v = 0; v < NV; ++v) p[i][v] = L::row(raw[i % PF], sig, x[v]) * (x[v].sx * keep);
+      if (CH || i + PF < RMAX)
+        L::load(wb + (uint32_t)min(g + G * (i0 + i + PF), cnt - 1) * geo.row_bytes, sig, raw[i % PF]);
+      __builtin_amdgcn_sched_barrier(0);
     }
-  } else {
-    const int wig = sig0 >> 6, nw = Sp >> 6;  // wave index within the group, waves per group
-    // outputs in chunks of 16 so the LDS table stays small for any RMAX * NV
-    constexpr int NO = RMAX * NV;
+
+    // 5. reduction over the group's S' lanes (fixed order)
+    if (Sp <= 64) {
 #pragma unroll
-    for (int o0 = 0; o0 < NO; o0 += 16) {
+      for (int i = 0; i < RMAX; ++i) {
+        const int r = g + G * (i0 + i);
 #pragma unroll
-      for (int o = o0; o < NO && o < o0 + 16; ++o) {
-        const float s = span_sum(p[o / NV][o % NV], 64);
-        if ((sig0 & 63) == 0) red[o - o0][g * nw + wig] = s;
-      }
-      __syncthreads();
-      // one thread per (group, output): sum the group's wave partials in wave order
-      const int gg = tid >> 4, oo = tid & 15;
-      if (gg < G && o0 + oo < NO) {
-        const int i = (o0 + oo) / NV, v = (o0 + oo) % NV;
-        if (gg + G * i < cnt) {
-          float s = 0.0f;
-          for (int w = 0; w < nw; ++w) s += red[oo][gg * nw + w];
-          Y[(size_t)v * rows + rb + gg + G * i] = s;
+        for (int v = 0; v < NV; ++v) {
+          const float s = span_sum(p[i][v], Sp);
+          if (sig0 == 0 && r < cnt) Y[(size_t)v * rows + rb + r] = s;
         }
       }
-      __syncthreads();
+    } else {
+      const int wig = sig0 >> 6, nw = Sp >> 6;  // wave index within the group, waves per group
+      // outputs in chunks of 16 so the LDS table stays small for any RMAX * NV
+      constexpr int NO = RMAX * NV;
+#pragma unroll
+      for (int o0 = 0; o0 < NO; o0 += 16) {
+#pragma unroll
+        for (int o = o0; o < NO && o < o0 + 16; ++o) {
+          const float s = span_sum(p[o / NV][o % NV], 64);
+          if ((sig0 & 63) == 0) red[o - o0][g * nw + wig] = s;
+        }
+        __syncthreads();
+        // one thread per (group, output): sum the group's wave partials in wave order
+        const int gg = tid >> 4, oo = tid & 15;
+        if (gg < G && o0 + oo < NO) {
+          const int i = (o0 + oo) / NV, v = (o0 + oo) % NV;
+          const int r = gg + G * (i0 + i);
+          if (r < cnt) {
+            float s = 0.0f;
+            for (int w = 0; w < nw; ++w) s += red[oo][gg * nw + w];
+            Y[(size_t)v * rows + rb + r] = s;
+          }
+        }
+        __syncthreads();
+      }
     }
   }
 }
@@ -596,11 +610,11 @@ constexpr int prefetch_rows() {
   return T == T_Q6_K || T == T_Q5_K ? 1 : 2;
 }
 
-template <uint32_t T, int NV, int RMAX, int TPT>
+template <uint32_t T, int NV, int RMAX, int TPT, bool CH>
 static void launch_t(const void* w, const float* X, float* Y, int rows, int cols, const Geo& geo, int nwg,
                      hipStream_t s) {
   constexpr int PF = prefetch_rows<T>() < RMAX ? prefetch_rows<T>() : RMAX;
-  auto kern = &k_gemv<T, NV, RMAX, TPT, PF>;
+  auto kern = &k_gemv<T, NV, RMAX, TPT, PF, CH>;
   const size_t lds = gemv_lds_bytes<T>(NV, geo.S);
   if (lds > 64 * 1024) {
     static std::atomic<int> have[kMaxDevices];
@@ -617,7 +631,7 @@ static void launch_r(int rmax, const void* w, const float* X, float* Y, int rows
   if constexpr (RM > 1) {
     if (rmax < RM) return launch_r<T, NV, TPT, RM - 1>(rmax, w, X, Y, rows, cols, geo, nwg, s);
   }
-  launch_t<T, NV, RM, TPT>(w, X, Y, rows, cols, geo, nwg, s);
+  launch_t<T, NV, RM, TPT, false>(w, X, Y, rows, cols, geo, nwg, s);
 }
 
 // Most rows a group takes (its partial sums stay in registers until the end).
@@ -629,16 +643,17 @@ constexpr int max_rows() {
 template <uint32_t T, int NV, int TPT>
 static void launch_tpt(const void* w, const float* X, float* Y, int rows, int cols, Geo geo, hipStream_t s) {
   constexpr int rm = max_rows<NV, TPT>();
+  static_assert(rm % prefetch_rows<T>() == 0, "chunks of rm rows keep the prefetch ring aligned");
   const int G = geo.G, waves = geo.Sp * G / 64;
   // one pass of workgroups over the chip (16 waves per CU), at least one row per group on
-  // average, and never more than rm rows per group
+  // average; a group with more than rm rows walks them in chunks of rm
   int64_t nwg = (int64_t)kCUs * (waves >= 16 ? 1 : 16 / waves);
   nwg = std::min<int64_t>(nwg, ((int64_t)rows + G - 1) / G);
-  nwg = std::max<int64_t>(nwg, ((int64_t)rows + (int64_t)G * rm - 1) / ((int64_t)G * rm));
   geo.base = (int)(rows / nwg);
   geo.rem = (int)(rows % nwg);
-  const int rmax = (geo.base + (geo.rem ? 1 : 0) + G - 1) / G;
-  launch_r<T, NV, TPT, rm>(rmax, w, X, Y, rows, cols, geo, (int)nwg, s);
+  const int per_group = (geo.base + (geo.rem ? 1 : 0) + G - 1) / G;
+  if (per_group <= rm) return launch_r<T, NV, TPT, rm>(per_group, w, X, Y, rows, cols, geo, (int)nwg, s);
+  launch_t<T, NV, rm, TPT, true>(w, X, Y, rows, cols, geo, (int)nwg, s);
 }
 
 template <uint32_t T, int NV>
