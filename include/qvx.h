@@ -18,8 +18,9 @@
  *  - Device entry points take device pointers and a hipStream_t passed as `void*` (NULL = the
  *    null stream).  They are asynchronous and stream-ordered, like the CUDA backend's matmulS
  *    launch (cuda/src/cuda_backend.cu:1534-1542).  They allocate no device memory, except
- *    qvx_qgemm_f16 with QVX_GEMM_BF16 / QVX_GEMM_I8, which takes a stream-ordered temporary for the
- *    converted activations from a memory pool the library owns per device.
+ *    qvx_qgemm_f16 with QVX_GEMM_BF16 / QVX_GEMM_I8 or a weight type other than Q4_K, which takes a
+ *    stream-ordered temporary for the converted activations (or the dequantised weight) from a
+ *    memory pool the library owns per device.
  *  - Entry points ending in _host take host pointers and are synchronous: the exact calling
  *    convention of the reference's CPU operator, for a CPU-side drop-in.
  *  - Calls that overlap on one device are safe for distinct outputs; the library holds no
@@ -46,6 +47,7 @@ extern "C" {
 #define QVX_E_STATE (-8)   /* a plan launched before qvx_plan_instantiate, or changed after it */
 #define QVX_E_FORMAT (-9)  /* malformed GGUF data (qvx_gguf_last_error() says what) */
 #define QVX_E_IO (-10)     /* a file could not be opened or mapped */
+#define QVX_E_LIB (-11)    /* a runtime library the call needs (rocBLAS) is missing or failed */
 
 /* GEMM variants for qvx_qgemm_f16 */
 #define QVX_GEMM_BF16 0 /* X rounded to bf16; raw weight blocks staged in LDS, dequantised to bf16; bf16 MFMA */
@@ -61,8 +63,8 @@ const char* qvx_strerror(int code);
 /* 1 if qvx_qmatmul / qvx_qmatmul_n compute `type` (qmatmul.cpp:24-26, qmatmulSupports): every
  * type the reference dequantises (F32, F16, BF16, Q8_0, Q8_1, Q4_0, Q4_1, Q5_0, Q5_1, Q4_K, Q5_K,
  * Q6_K).  Q8_0 / Q4_0 / Q5_0 / Q4_K / Q5_K / Q6_K run on the integer fast kernels, F32 / F16 /
- * BF16 on the float kernel, Q8_1 / Q4_1 / Q5_1 and unaligned weights on a generic kernel;
- * qvx_qgemm_f16 computes Q4_K only. */
+ * BF16 on the float kernel, Q8_1 / Q4_1 / Q5_1 and unaligned weights on a generic kernel.
+ * qvx_qgemm_f16 computes the same types. */
 int qvx_supports(uint32_t type);
 
 /* 1 if qvx_dequantize handles `type` (dequant.cpp:257-275, canDequantize). */
@@ -97,7 +99,12 @@ int qvx_dequant_row(const void* d_w, uint32_t type, int cols, int row, float* d_
 /* Prefill GEMM: out[m * rows + r] = sum_k X[m, k] * dequant(W)[r, k] for m < M, X fp16 [M, cols].
  * No reference counterpart (the reference prefills token by token); semantics are qmatmulN's
  * with X converted fp16 -> fp32 exactly.  variant = QVX_GEMM_BF16 | QVX_GEMM_F16 | QVX_GEMM_I8;
- * tolerance 2e-2 max-relative against the exact sum.  type: Q4_K (other types: QVX_E_TYPE). */
+ * tolerance 2e-2 max-relative against the exact sum.  type: every type qvx_qmatmul takes.  Q4_K
+ * runs on the engine's MFMA kernels; the other types are dequantised into a stream-ordered 16-bit
+ * temporary (fp16, bf16 for QVX_GEMM_BF16) and multiplied by one rocBLAS gemm_ex (fp32 accumulate),
+ * rocBLAS being loaded on first use (QVX_E_LIB when it is missing or fails; these calls create a
+ * rocBLAS handle per host thread and device on first use, so they are not for graph capture).
+ * QVX_GEMM_I8 takes Q4_K only (other types: QVX_E_TYPE). */
 int qvx_qgemm_f16(float* d_out, const void* d_w, uint32_t type, const uint16_t* d_X, int M,
                   int rows, int cols, int variant, void* stream);
 

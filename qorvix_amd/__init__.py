@@ -30,7 +30,7 @@ TYPE_NAMES = {0: "F32", 1: "F16", 2: "Q4_0", 3: "Q4_1", 6: "Q5_0", 7: "Q5_1", 8:
 
 # status codes (include/qvx.h)
 OK, E_TYPE, E_SHAPE, E_NVEC, E_NULL, E_HIP, E_VARIANT, E_RANGE, E_STATE = 0, -1, -2, -3, -4, -5, -6, -7, -8
-E_FORMAT, E_IO = -9, -10
+E_FORMAT, E_IO, E_LIB = -9, -10, -11
 # GEMM variants
 GEMM_BF16, GEMM_I8, GEMM_F16 = 0, 1, 2
 

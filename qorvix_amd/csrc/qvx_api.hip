@@ -198,6 +198,7 @@ const char* qvx_strerror(int code) {
     case QVX_E_STATE: return "plan not instantiated, or changed after instantiation";
     case QVX_E_FORMAT: return "malformed GGUF data";
     case QVX_E_IO: return "file could not be opened or mapped";
+    case QVX_E_LIB: return "a runtime library the call needs (rocBLAS) is missing or failed";
     default: return "unknown qvx status";
   }
 }
@@ -254,7 +255,7 @@ int qvx_qgemm_f16(float* d_out, const void* d_w, uint32_t type, const uint16_t* 
   if (M <= 0) return QVX_E_NVEC;
   if (variant != QVX_GEMM_BF16 && variant != QVX_GEMM_I8 && variant != QVX_GEMM_F16) return QVX_E_VARIANT;
   if (int rc = check_matmul(type, cols, &ti); rc != QVX_OK) return rc;
-  if (type == T_F32) return QVX_E_TYPE;
+  if (variant == QVX_GEMM_I8 && type != T_Q4_K) return QVX_E_TYPE;
   if (rows <= 0) return QVX_OK;
   if (!d_out) return QVX_E_NULL;
   if (cols <= 0) {

@@ -129,6 +129,56 @@ bool launch_dequant(uint32_t t, const void* src, float* dst, size_t n, hipStream
   }
 }
 
+// ---- dequantisation to 16-bit (prefill GEMM operands) ----------------------------------------------
+// The fp32 value above, rounded once to nearest-even fp16 or bf16 (NaN stays NaN, quiet).
+__device__ inline uint16_t to_bf16(float f) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x0040u);
+  return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+template <uint32_t T, int QK, int BB, bool BF>
+__global__ __launch_bounds__(256) void k_dequant16(const uint8_t* __restrict__ src, uint16_t* __restrict__ dst,
+                                                   size_t n) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  float v;
+  if constexpr (T == T_F32) {
+    v = reinterpret_cast<const float*>(src)[i];
+  } else {
+    const size_t blk = i / QK;
+    v = deq_elem<T>(src + blk * BB, (int)(i - blk * QK));
+  }
+  dst[i] = BF ? to_bf16(v) : __builtin_bit_cast(uint16_t, (_Float16)v);
+}
+
+template <bool BF>
+bool launch_dequant16_t(uint32_t t, const void* src, uint16_t* dst, size_t n, hipStream_t s) {
+  const size_t grid = (n + 255) / 256;
+  if (n == 0) return true;
+  const auto* b = static_cast<const uint8_t*>(src);
+  switch (t) {
+    case T_F32: k_dequant16<T_F32, 1, 4, BF><<<grid, 256, 0, s>>>(b, dst, n); return true;
+    case T_F16: k_dequant16<T_F16, 1, 2, BF><<<grid, 256, 0, s>>>(b, dst, n); return true;
+    case T_BF16: k_dequant16<T_BF16, 1, 2, BF><<<grid, 256, 0, s>>>(b, dst, n); return true;
+    case T_Q8_0: k_dequant16<T_Q8_0, 32, 34, BF><<<grid, 256, 0, s>>>(b, dst, n); return true;
+    case T_Q8_1: k_dequant16<T_Q8_1, 32, 36, BF><<<grid, 256, 0, s>>>(b, dst, n); return true;
+    case T_Q4_0: k_dequant16<T_Q4_0, 32, 18, BF><<<grid, 256, 0, s>>>(b, dst, n); return true;
+    case T_Q4_1: k_dequant16<T_Q4_1, 32, 20, BF><<<grid, 256, 0, s>>>(b, dst, n); return true;
+    case T_Q5_0: k_dequant16<T_Q5_0, 32, 22, BF><<<grid, 256, 0, s>>>(b, dst, n); return true;
+    case T_Q5_1: k_dequant16<T_Q5_1, 32, 24, BF><<<grid, 256, 0, s>>>(b, dst, n); return true;
+    case T_Q4_K: k_dequant16<T_Q4_K, 256, 144, BF><<<grid, 256, 0, s>>>(b, dst, n); return true;
+    case T_Q5_K: k_dequant16<T_Q5_K, 256, 176, BF><<<grid, 256, 0, s>>>(b, dst, n); return true;
+    case T_Q6_K: k_dequant16<T_Q6_K, 256, 210, BF><<<grid, 256, 0, s>>>(b, dst, n); return true;
+    default: return false;
+  }
+}
+
+// dst[i] = 16-bit rounding of dequant(src)[i] (bf16 when `bf16`, else fp16), i < n.
+bool launch_dequant16(uint32_t t, const void* src, uint16_t* dst, size_t n, bool bf16, hipStream_t s) {
+  return bf16 ? launch_dequant16_t<true>(t, src, dst, n, s) : launch_dequant16_t<false>(t, src, dst, n, s);
+}
+
 // ---- generic GEMV: any alignment, any supported type ---------------------------------------------
 // One wave per (row, vector); lane-strided elements dequantised with deq_elem; used only when a
 // weight's base or row pitch is not 16-byte aligned (the fast kernels in qvx_gemv.hip need both).

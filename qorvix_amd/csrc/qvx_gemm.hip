@@ -877,9 +877,17 @@ void launch_var(float* out, const void* w, const uint16_t* X, int M, int N, int 
 }  // namespace
 
 // Returns a QVX status (0 ok, -1 type, -5 HIP, -7 range).
+int launch_qgemm_dequant(float* out, const void* w, uint32_t t, const uint16_t* X, int M, int rows, int cols,
+                         bool bf16, hipStream_t s);
+
 int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M, int rows, int cols, int variant,
                  hipStream_t s) {
-  if (t != T_Q4_K) return -1;
+  // Weight types without a GEMM kernel of their own: dequantise to 16 bits, then a library GEMM.
+  if (t != T_Q4_K) {
+    if (variant == VAR_I8) return -1;
+    if ((size_t)rows * (size_t)cols >= (1ull << 31) || (size_t)M * (size_t)cols >= (1ull << 31)) return -7;
+    return launch_qgemm_dequant(out, w, t, X, M, rows, cols, variant == VAR_BF16, s);
+  }
   if ((reinterpret_cast<uintptr_t>(w) & 15u) || (reinterpret_cast<uintptr_t>(X) & 15u)) return -7;
   // Buffer offsets are 32-bit: a tile's rows must span less than 2 GiB.
   if ((size_t)256 * (size_t)cols * 2u >= (1u << 31) || (size_t)kBN * (size_t)(cols / 256) * 144u >= (1u << 31))

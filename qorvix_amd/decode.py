@@ -19,7 +19,8 @@ from __future__ import annotations
 import ctypes as C
 from dataclasses import dataclass, field
 
-from . import OK, Q4_K, Q6_K, QvxError, lib, weight_bytes, fill_synthetic_t, fill_normal_t, empty_weight
+from . import (GEMM_F16, OK, Q4_K, Q6_K, QvxError, empty_weight, fill_normal_t, fill_synthetic_t, lib,
+               weight_bytes)
 
 
 @dataclass
@@ -240,3 +241,53 @@ class DecodeStep:
 
     def run_eager(self, stream: int) -> None:
         self.plan.run_eager(stream)
+
+
+def wgemm(out, w: DevWeight, X16, m: int, stream: int, variant: int = GEMM_F16) -> None:
+    """out[m, rows] = X16[m, cols] W^T with X in fp16: the prefill GEMM (``qvx_qgemm_f16``)."""
+    rc = lib().qvx_qgemm_f16(out.data_ptr(), w.data.data_ptr(), w.type, X16.data_ptr(), m, w.rows, w.cols, variant,
+                             stream)
+    if rc != OK:
+        raise QvxError(rc, "qvx_qgemm_f16")
+
+
+class PrefillStep:
+    """The weight side of a prompt prefill of M positions, batched.  The reference prefills token
+    by token, one ``forward`` per prompt position (``runtime/src/generator.cpp:24-28``), each
+    running the decoder's seven projections per layer; here every projection of a layer takes all M
+    positions at once as one GEMM (``qvx_qgemm_f16``: Q4_K on the engine's MFMA kernels, the Q6_K
+    tensors dequantised to fp16 for a library GEMM), and the LM head runs on the last position only,
+    as the reference keeps only the logits after the last prompt token.  Activations are seeded fp16
+    stand-ins (norms, RoPE, attention and SwiGLU are outside the engine); one output buffer per
+    projection name is reused across layers.  Calls are issued eagerly: the library GEMM path creates
+    its handle on first use and is not for graph capture."""
+
+    def __init__(self, model: Model, m: int, seed: int = 11, device="cuda", variant: int = GEMM_F16):
+        import torch
+        self.model, self.m, self.variant = model, m, variant
+        f16 = dict(dtype=torch.float16, device=device)
+        f32 = dict(dtype=torch.float32, device=device)
+        l0 = model.layers[0]
+        self.inputs = {"xn": torch.empty((m, l0["wq"].cols), **f16), "attn": torch.empty((m, l0["wo"].cols), **f16),
+                       "act": torch.empty((m, l0["ffn_down"].cols), **f16)}
+        for i, k in enumerate(("xn", "attn", "act")):
+            fill_normal_t(self.inputs[k], seed=seed + i, mul=0.5)
+        self.outputs = {name: torch.empty((m, l0[name].rows), **f32) for name, *_ in LAYER_SPECS}
+        self.last = torch.empty((1, l0["wq"].cols), **f32)  # the last position's normed state
+        fill_normal_t(self.last, seed=seed + 3)
+        self.logits = torch.empty((1, model.lm_head.rows), **f32) if model.lm_head is not None else None
+
+    def flops(self) -> int:
+        """2 * rows * cols per position per layer projection, and once for the LM head."""
+        n = sum(2 * self.m * w.rows * w.cols for layer in self.model.layers for w in layer.values())
+        if self.model.lm_head is not None:
+            n += 2 * self.model.lm_head.rows * self.model.lm_head.cols
+        return n
+
+    def run(self, stream: int) -> None:
+        for layer in self.model.layers:
+            for name, _, _, _, src in LAYER_SPECS:
+                wgemm(self.outputs[name], layer[name], self.inputs[src], self.m, stream, self.variant)
+        if self.model.lm_head is not None:
+            wmatmul_n(self.logits, self.model.lm_head, self.last, 1, stream)
+

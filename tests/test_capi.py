@@ -43,6 +43,7 @@ def test_version_and_errors():
     assert "gfx950" in qvx.version()
     assert qvx.strerror(qvx.E_TYPE).startswith("unsupported")
     assert qvx.strerror(qvx.OK) == "ok"
+    assert "rocBLAS" in qvx.strerror(qvx.E_LIB)
 
 
 def test_type_table_matches_gguf():
@@ -81,7 +82,8 @@ def test_qmatmul_rejections():
     assert lib.qvx_qmatmul(FAKE, FAKE, 4, FAKE, 1, 256, None) == qvx.E_TYPE  # retired id
     assert lib.qvx_qmatmul(FAKE, FAKE, 11, FAKE, 1, 256, None) == qvx.E_TYPE  # Q3_K: not dequantisable
     assert lib.qvx_qmatmul(FAKE, FAKE, qvx.Q5_K, FAKE, 1, 128, None) == qvx.E_SHAPE  # cols % 256
-    assert lib.qvx_qgemm_f16(FAKE, FAKE, qvx.F16, FAKE, 128, 256, 256, 0, None) == qvx.E_TYPE  # GEMM: Q4_K only
+    assert lib.qvx_qgemm_f16(FAKE, FAKE, qvx.F16, FAKE, 128, 256, 256, qvx.GEMM_I8, None) == qvx.E_TYPE  # int8: Q4_K only
+    assert lib.qvx_qgemm_f16(FAKE, FAKE, 11, FAKE, 128, 256, 256, qvx.GEMM_F16, None) == qvx.E_TYPE  # Q3_K
     assert lib.qvx_qmatmul_n(FAKE, FAKE, qvx.Q8_0, FAKE, 0, 1, 32, None) == qvx.E_NVEC
     assert lib.qvx_qmatmul_n(FAKE, FAKE, qvx.Q8_0, FAKE, -3, 1, 32, None) == qvx.E_NVEC
     # nVec is checked first, as in the reference (qmatmulN returns false before the type check)
@@ -100,7 +102,10 @@ def test_gemm_and_dequant_rejections():
     assert lib.qvx_qgemm_f16(FAKE, FAKE, qvx.Q4_K, FAKE, 128, 256, 256, 7, None) == qvx.E_VARIANT
     assert lib.qvx_qgemm_f16(FAKE, FAKE, qvx.Q4_K, FAKE, 0, 256, 256, 0, None) == qvx.E_NVEC
     assert lib.qvx_qgemm_f16(FAKE, FAKE, qvx.Q4_K, FAKE, 128, 256, 300, 0, None) == qvx.E_SHAPE
-    assert lib.qvx_qgemm_f16(FAKE, FAKE, qvx.F32, FAKE, 128, 256, 256, 0, None) == qvx.E_TYPE
+    assert lib.qvx_qgemm_f16(FAKE, FAKE, qvx.Q6_K, FAKE, 128, 256, 256, qvx.GEMM_I8, None) == qvx.E_TYPE
+    assert lib.qvx_qgemm_f16(FAKE, FAKE, qvx.Q6_K, FAKE, 128, 256, 300, qvx.GEMM_F16, None) == qvx.E_SHAPE
+    assert lib.qvx_qgemm_f16(FAKE, FAKE, qvx.Q6_K, FAKE, 128, 0, 256, qvx.GEMM_F16, None) == qvx.OK  # no rows
+    assert lib.qvx_qgemm_f16(None, FAKE, qvx.Q6_K, FAKE, 128, 4, 256, qvx.GEMM_F16, None) == qvx.E_NULL
     assert lib.qvx_dequantize(qvx.Q4_K, FAKE, FAKE, 100, None) == qvx.E_RANGE
     assert lib.qvx_dequantize(10, FAKE, FAKE, 256, None) == qvx.E_TYPE
     assert lib.qvx_dequantize(qvx.Q4_K, FAKE, FAKE, 0, None) == qvx.OK

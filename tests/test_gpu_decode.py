@@ -84,3 +84,33 @@ def test_plan_state_and_argument_errors(cuda):
     p.launch(torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     p.close()
+
+
+@pytest.mark.parametrize("m", [16, 130])
+def test_prefill_outputs_match_oracle(cuda, small_model, m):
+    """The batched prefill: every projection of the last layer (the outputs are reused across layers)
+    within the GEMM tolerance of the oracle on a slice of rows, the Q4_K ones on the MFMA kernel and
+    the Q6_K ones through the dequantising library GEMM; the LM head on the last position within the
+    GEMV tolerance."""
+    torch = cuda
+    step = decode.PrefillStep(small_model, m, seed=m)
+    step.run(torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    X = {k: v.cpu().numpy().astype(np.float32) for k, v in step.inputs.items()}
+    last = small_model.layers[-1]
+    for name, rows, cols, t, src in decode.LAYER_SPECS:
+        w = last[name]
+        assert w.type == t
+        rb = qvx.row_bytes(t, cols)
+        r0 = (rows // 3) & ~15
+        nr = 48
+        wrows = w.data[r0 * rb:(r0 + nr) * rb].cpu().numpy()
+        ref = oracle.matmul_f64(wrows, t, X[src], m, nr, cols)
+        assert max_rel(step.outputs[name][:, r0:r0 + nr].cpu().numpy(), ref) <= 2e-2, name
+    head = small_model.lm_head
+    rb = qvx.row_bytes(head.type, head.cols)
+    wrows = head.data[:64 * rb].cpu().numpy()
+    ref = oracle.matmul_f64(wrows, head.type, step.last.cpu().numpy(), 1, 64, head.cols)
+    assert max_rel(step.logits[:, :64].cpu().numpy(), ref) <= 1e-3
+    assert step.flops() == 2 * m * sum(w.rows * w.cols for l in small_model.layers for w in l.values()) + \
+        2 * head.rows * head.cols

@@ -366,6 +366,42 @@ def test_gemm_q4k_parity(cuda, variant, M, rows, cols):
     assert max_rel(out.cpu().numpy(), ref) <= GEMM_TOL
 
 
+DEQUANT_GEMM_TYPES = [qvx.Q6_K, qvx.Q8_0, qvx.Q4_0, qvx.Q5_0, qvx.Q5_K, qvx.Q4_1, qvx.Q5_1, qvx.Q8_1,
+                      qvx.F16, qvx.BF16, qvx.F32]
+
+
+@pytest.mark.parametrize("t", DEQUANT_GEMM_TYPES)
+@pytest.mark.parametrize("variant", [qvx.GEMM_BF16, qvx.GEMM_F16])
+@pytest.mark.parametrize("M,rows,cols", [(128, 512, 1024), (37, 300, 256)])
+def test_gemm_other_types_parity(cuda, t, variant, M, rows, cols):
+    """Weight types without a GEMM kernel of their own (dequantised to 16 bits, then a library GEMM):
+    within the GEMM tolerance of the fp64 oracle."""
+    rng = np.random.default_rng(M + rows + cols + 3 * t + variant)
+    w = random_weight(t, rows, cols, rng, scale=0.002)
+    X16 = (rng.standard_normal((M, cols)) * 0.5).astype(np.float16)
+    out = qvx.qgemm_t(dev(cuda, w), t, dev(cuda, X16.view(np.uint16)), rows, cols, variant)
+    cuda.cuda.synchronize()
+    ref = oracle.matmul_f64(w, t, X16.astype(np.float32), M, rows, cols)
+    assert max_rel(out.cpu().numpy(), ref) <= GEMM_TOL
+
+
+def test_gemm_q6k_ffn_down_shape(cuda):
+    """The Q4_K_M model's Q6_K ffn_down (14336 -> 4096) at M = 64 through the dequantising path, and
+    the int8 variant refused for it."""
+    t, M, rows, cols = qvx.Q6_K, 64, 4096, 14336
+    W = qvx.empty_weight(t, rows, cols)
+    qvx.fill_synthetic_t(W, t, rows, cols, seed=41, scale_mul=1e-3)
+    X = cuda.empty((M, cols), dtype=cuda.float16, device="cuda")
+    qvx.fill_normal_t(X, seed=42, mul=0.5)
+    ref = oracle.matmul_f64(W.cpu().numpy(), t, X.cpu().numpy().astype(np.float32), M, rows, cols)
+    for variant in (qvx.GEMM_BF16, qvx.GEMM_F16):
+        out = qvx.qgemm_t(W, t, X, rows, cols, variant)
+        cuda.cuda.synchronize()
+        assert max_rel(out.cpu().numpy(), ref) <= GEMM_TOL
+    with pytest.raises(qvx.QvxError):
+        qvx.qgemm_t(W, t, X, rows, cols, qvx.GEMM_I8)
+
+
 def test_gemm_q4k_config4_shape(cuda):
     """BASELINE config 4 (Q4_K 4096 -> 14336, M = 128) against the fp64 oracle."""
     rng = np.random.default_rng(2024)
