@@ -235,6 +235,33 @@ def decode_sweep(torch, stream, steps, cpu=True):
                                    "sample": "layer 0's 7 projections and the LM head, median of >= 5 runs each; "
                                              "per token = 32 x layer + LM head"}
             log(f"[bench] sweep M={m} CPU {kind}: {cpu_ms:.1f} ms/token ({ab / (cpu_ms * 1e-3) / 1e9:.1f} GB/s)")
+    # Prefill: M prompt positions through every projection as one GEMM each (qvx_qgemm_f16, fp16 X;
+    # Q4_K on the MFMA kernels, the Q6_K tensors through the dequantising library GEMM) and the LM head
+    # on the last position.  The reference prefills token by token (generator.cpp:24-28), one decode
+    # step per position: its equivalent here is M x the M = 1 sweep time.
+    pre = {}
+    for mp in (512, 2048):
+        st = decode.PrefillStep(model, mp)
+        st.run(sh)
+        torch.cuda.synchronize()
+        reps = 3
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            st.run(sh)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        tf = st.flops() / (ms * 1e-3) / 1e12
+        tbt = mp * out["M1"]["ms_per_token"]
+        pre[f"M{mp}"] = {"ms": round(ms, 3), "tokens_per_s": round(mp / (ms * 1e-3), 1), "tflops": round(tf, 1),
+                         "frac_of_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4), "runs_timed": reps,
+                         "token_by_token_ms": round(tbt, 2), "speedup_vs_token_by_token": round(tbt / ms, 1)}
+        log(f"[bench] prefill M={mp}: {ms:.2f} ms ({mp / (ms * 1e-3):.0f} tokens/s, {tf:.0f} TFLOP/s); token by token "
+            f"{tbt:.1f} ms")
+        del st
+    out["prefill"] = {"workload": "Llama-3-8B Q4_K_M prompt prefill: 32 x 7 projections as GEMMs over M positions "
+                                  "(fp16 activations) + the Q6_K LM head on the last position", **pre}
     del model
     torch.cuda.empty_cache()
     return out
