@@ -152,11 +152,74 @@ __global__ __launch_bounds__(256) void k_dequant16(const uint8_t* __restrict__ s
   dst[i] = BF ? to_bf16(v) : __builtin_bit_cast(uint16_t, (_Float16)v);
 }
 
+// Eight consecutive elements per thread (always inside one block: every block size is a multiple
+// of 8), so the block header is read once for the eight and the result leaves as one 16-byte store.
+template <uint32_t T, int QK, int BB, bool BF>
+__global__ __launch_bounds__(256) void k_dequant16x8(const uint8_t* __restrict__ src, uint4* __restrict__ dst,
+                                                     size_t n8) {
+  const size_t g = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (g >= n8) return;
+  const size_t i = 8 * g;
+  float v[8];
+  if constexpr (T == T_F32) {
+    const float4* p = reinterpret_cast<const float4*>(src) + 2 * g;
+    const float4 a = p[0], c = p[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = c.x; v[5] = c.y; v[6] = c.z; v[7] = c.w;
+  } else {
+    const size_t blk = i / QK;
+    const int e = (int)(i - blk * QK);
+    const uint8_t* b = src + blk * BB;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = deq_elem<T>(b, e + k);
+  }
+  uint32_t w[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t lo = BF ? to_bf16(v[2 * j]) : __builtin_bit_cast(uint16_t, (_Float16)v[2 * j]);
+    const uint32_t hi = BF ? to_bf16(v[2 * j + 1]) : __builtin_bit_cast(uint16_t, (_Float16)v[2 * j + 1]);
+    w[j] = lo | (hi << 16);
+  }
+  dst[g] = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 template <bool BF>
 bool launch_dequant16_t(uint32_t t, const void* src, uint16_t* dst, size_t n, hipStream_t s) {
-  const size_t grid = (n + 255) / 256;
   if (n == 0) return true;
   const auto* b = static_cast<const uint8_t*>(src);
+  // whole groups of 8 on the vector kernel (dst 16-byte aligned; F32 sources too), the rest scalar
+  const bool vec = (reinterpret_cast<uintptr_t>(dst) & 15u) == 0 &&
+                   (t != T_F32 || (reinterpret_cast<uintptr_t>(src) & 15u) == 0);
+  const size_t n8 = vec ? n / 8 : 0;
+  if (n8) {
+    const size_t grid8 = (n8 + 255) / 256;
+    auto* d8 = reinterpret_cast<uint4*>(dst);
+    switch (t) {
+      case T_F32: k_dequant16x8<T_F32, 1, 4, BF><<<grid8, 256, 0, s>>>(b, d8, n8); break;
+      case T_F16: k_dequant16x8<T_F16, 1, 2, BF><<<grid8, 256, 0, s>>>(b, d8, n8); break;
+      case T_BF16: k_dequant16x8<T_BF16, 1, 2, BF><<<grid8, 256, 0, s>>>(b, d8, n8); break;
+      case T_Q8_0: k_dequant16x8<T_Q8_0, 32, 34, BF><<<grid8, 256, 0, s>>>(b, d8, n8); break;
+      case T_Q8_1: k_dequant16x8<T_Q8_1, 32, 36, BF><<<grid8, 256, 0, s>>>(b, d8, n8); break;
+      case T_Q4_0: k_dequant16x8<T_Q4_0, 32, 18, BF><<<grid8, 256, 0, s>>>(b, d8, n8); break;
+      case T_Q4_1: k_dequant16x8<T_Q4_1, 32, 20, BF><<<grid8, 256, 0, s>>>(b, d8, n8); break;
+      case T_Q5_0: k_dequant16x8<T_Q5_0, 32, 22, BF><<<grid8, 256, 0, s>>>(b, d8, n8); break;
+      case T_Q5_1: k_dequant16x8<T_Q5_1, 32, 24, BF><<<grid8, 256, 0, s>>>(b, d8, n8); break;
+      case T_Q4_K: k_dequant16x8<T_Q4_K, 256, 144, BF><<<grid8, 256, 0, s>>>(b, d8, n8); break;
+      case T_Q5_K: k_dequant16x8<T_Q5_K, 256, 176, BF><<<grid8, 256, 0, s>>>(b, d8, n8); break;
+      case T_Q6_K: k_dequant16x8<T_Q6_K, 256, 210, BF><<<grid8, 256, 0, s>>>(b, d8, n8); break;
+      default: return false;
+    }
+  }
+  const size_t done = 8 * n8;
+  if (done == n) return true;
+  // the tail: whole blocks for the quantised types (n is a whole number of blocks), so the scalar
+  // kernel indexes from a block boundary; F32 / F16 / BF16 have one-element blocks
+  const TypeInfo* ti = type_info(t);
+  if (!ti) return false;
+  b += done / ti->block * ti->bytes;
+  dst += done;
+  n -= done;
+  const size_t grid = (n + 255) / 256;
   switch (t) {
     case T_F32: k_dequant16<T_F32, 1, 4, BF><<<grid, 256, 0, s>>>(b, dst, n); return true;
     case T_F16: k_dequant16<T_F16, 1, 2, BF><<<grid, 256, 0, s>>>(b, dst, n); return true;

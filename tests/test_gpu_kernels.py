@@ -385,6 +385,21 @@ def test_gemm_other_types_parity(cuda, t, variant, M, rows, cols):
     assert max_rel(out.cpu().numpy(), ref) <= GEMM_TOL
 
 
+@pytest.mark.parametrize("t", [qvx.F16, qvx.BF16, qvx.F32])
+def test_gemm_float_weights_ragged_tail(cuda, t):
+    """rows * cols not a multiple of 8: the dequantiser's vector kernel takes the whole groups of 8
+    and the scalar kernel the tail."""
+    rng = np.random.default_rng(5 + t)
+    M, rows, cols = 5, 3, 260
+    w = random_weight(t, rows, cols, rng, scale=0.002)
+    X16 = (rng.standard_normal((M, cols)) * 0.5).astype(np.float16)
+    ref = oracle.matmul_f64(w, t, X16.astype(np.float32), M, rows, cols)
+    for variant in (qvx.GEMM_BF16, qvx.GEMM_F16):
+        out = qvx.qgemm_t(dev(cuda, w), t, dev(cuda, X16.view(np.uint16)), rows, cols, variant)
+        cuda.cuda.synchronize()
+        assert max_rel(out.cpu().numpy(), ref) <= GEMM_TOL
+
+
 def test_gemm_q6k_ffn_down_shape(cuda):
     """The Q4_K_M model's Q6_K ffn_down (14336 -> 4096) at M = 64 through the dequantising path, and
     the int8 variant refused for it."""
