@@ -191,8 +191,8 @@ def decode_sweep(torch, stream, steps, cpu=True):
     out = {"workload": "Llama-3-8B Q4_K_M decode weight sweep (BASELINE configs[4]): 32 x 7 projections "
                        "+ Q6_K lm_head = 225 GEMVs per token, one HIP graph per token, GEMVs in call order",
            "weight_bytes_per_token": model.nbytes}
-    def time_step(m, concurrent):
-        st = decode.DecodeStep(model, m, concurrent=concurrent)
+    def time_step(mdl, m, concurrent):
+        st = decode.DecodeStep(mdl, m, concurrent=concurrent)
         for _ in range(3):
             st.replay(sh)
         torch.cuda.synchronize()
@@ -205,16 +205,21 @@ def decode_sweep(torch, stream, steps, cpu=True):
         st.plan.close()
         return e0.elapsed_time(e1) / steps
 
+    fused = model.fused()  # q|k and gate|up stacked: 5 GEMVs a layer
     for m in (1, 8):
-        ms = time_step(m, False)
-        ms_br = time_step(m, True)
+        ms = time_step(model, m, False)
+        ms_br = time_step(model, m, True)
+        ms_fu = time_step(fused, m, False)
         _, ab = decode.sweep_bytes(m)
         gbs = ab / (ms * 1e-3) / 1e9
         out[f"M{m}"] = {"ms_per_token": round(ms, 4), "algorithmic_bytes_per_token": ab, "gb_s": round(gbs, 1),
                         "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "tokens_timed": steps,
-                        "ms_per_token_qkv_gateup_branches": round(ms_br, 4)}
+                        "ms_per_token_qkv_gateup_branches": round(ms_br, 4),
+                        "ms_per_token_fused_qk_gateup": round(ms_fu, 4),
+                        "gb_s_fused_qk_gateup": round(ab / (ms_fu * 1e-3) / 1e9, 1)}
         log(f"[bench] sweep M={m}: {ms:.3f} ms/token, {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak); "
-            f"{ms_br:.3f} ms/token with q/k/v and gate/up as concurrent graph branches")
+            f"{ms_br:.3f} ms/token with q/k/v and gate/up as concurrent graph branches; {ms_fu:.3f} ms/token with "
+            f"q|k and gate|up stacked (5 GEMVs a layer)")
         if cpu:
             # the reference CPU operator on layer 0's seven projections and the LM head (same blocks,
             # seeded activations); per token = 32 x layer + LM head
@@ -262,7 +267,7 @@ def decode_sweep(torch, stream, steps, cpu=True):
         del st
     out["prefill"] = {"workload": "Llama-3-8B Q4_K_M prompt prefill: 32 x 7 projections as GEMMs over M positions "
                                   "(fp16 activations) + the Q6_K LM head on the last position", **pre}
-    del model
+    del model, fused
     torch.cuda.empty_cache()
     return out
 

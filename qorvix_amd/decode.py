@@ -58,6 +58,12 @@ LAYER_SPECS = (  # (name, rows, cols, type, input buffer)
     ("ffn_down", D_MODEL, D_FF, Q6_K, "act"),
 )
 LM_HEAD = ("lm_head", VOCAB, D_MODEL, Q6_K, "xn")
+INPUTS = {spec[0]: spec[4] for spec in LAYER_SPECS}
+
+# Projections of one type and row length that read the same input, stacked row-wise into one weight
+# so that one GEMV computes both (rows are independent, so each row's arithmetic is a one-weight
+# call's under the stacked launch geometry): q with k (attn_v is Q6_K in Q4_K_M files), gate with up.
+FUSED = (("wqk", ("wq", "wk")), ("ffn_gateup", ("ffn_gate", "ffn_up")))
 
 
 def sweep_specs(n_layers: int = N_LAYERS, lm_head: bool = True):
@@ -83,6 +89,40 @@ class Model:
     """Synthetic Llama-3-8B Q4_K_M weights on the device (``layers[l][name]``, ``lm_head``)."""
     layers: list = field(default_factory=list)
     lm_head: DevWeight | None = None
+    # name of a stacked weight -> ((part name, rows), ...) in row order (see FUSED)
+    parts: dict = field(default_factory=dict)
+
+    def fused(self) -> "Model":
+        """The same weights with each FUSED pair of a layer stacked into one device weight when the
+        two share type and row length (the other projections are shared, not copied)."""
+        import torch
+        m = Model(lm_head=self.lm_head)
+        for layer in self.layers:
+            out, used = {}, set()
+            for name, (a, b) in FUSED:
+                wa, wb = layer.get(a), layer.get(b)
+                if wa is None or wb is None or wa.type != wb.type or wa.cols != wb.cols:
+                    continue
+                out[name] = DevWeight(torch.cat([wa.data, wb.data]), wa.type, wa.rows + wb.rows, wa.cols)
+                m.parts[name] = ((a, wa.rows), (b, wb.rows))
+                used.update((a, b))
+            out.update({k: w for k, w in layer.items() if k not in used})
+            m.layers.append(out)
+        return m
+
+    def calls(self):
+        """(layer, name, weight, input) per GEMV of one token: the reference's order
+        (text_model.cpp:146-177), a stacked weight taking the place of its first part."""
+        for l, layer in enumerate(self.layers):
+            first = {parts[0][0]: name for name, parts in self.parts.items() if name in layer}
+            skip = {p[0] for name, parts in self.parts.items() if name in layer for p in parts[1:]}
+            for name, *_ in LAYER_SPECS:
+                if name in skip:
+                    continue
+                key = first.get(name, name)
+                yield l, key, layer[key], INPUTS[name]
+        if self.lm_head is not None:
+            yield len(self.layers), LM_HEAD[0], self.lm_head, LM_HEAD[4]
 
     @staticmethod
     def synthetic(n_layers: int = N_LAYERS, lm_head: bool = True, seed: int = 5, device="cuda") -> "Model":
@@ -145,6 +185,11 @@ class Model:
     def nbytes(self) -> int:
         n = sum(w.nbytes for layer in self.layers for w in layer.values())
         return n + (self.lm_head.nbytes if self.lm_head else 0)
+
+
+def _input_widths(model: Model) -> dict:
+    """Row length of each activation buffer (xn, attn, act), from the first layer's calls."""
+    return {src: w.cols for l, _, w, src in model.calls() if l == 0}
 
 
 def _tensor_seed(seed: int, layer: int, name: str) -> int:
@@ -214,17 +259,16 @@ class DecodeStep:
 
     def __init__(self, model: Model, m: int, seed: int = 9, device="cuda", concurrent: bool = False):
         import torch
+        if concurrent and model.parts:
+            raise ValueError("concurrent q/k/v and gate/up branches are for the unfused model")
         self.model, self.m = model, m
         f32 = dict(dtype=torch.float32, device=device)
-        l0 = model.layers[0]
-        self.inputs = {"xn": torch.empty((m, l0["wq"].cols), **f32), "attn": torch.empty((m, l0["wo"].cols), **f32),
-                       "act": torch.empty((m, l0["ffn_down"].cols), **f32)}
+        self.inputs = {k: torch.empty((m, c), **f32) for k, c in _input_widths(model).items()}
         for i, k in enumerate(("xn", "attn", "act")):
             fill_normal_t(self.inputs[k], seed=seed + i)
         self.outputs = []
         self.plan = Plan()
-        for l, name, _, _, _, src in sweep_specs(len(model.layers), model.lm_head is not None):
-            w = model.layers[l][name] if l < len(model.layers) else model.lm_head
+        for l, name, w, src in model.calls():
             y = torch.empty((m, w.rows), **f32)
             self.outputs.append((l, name, y))
             # q/k/v read the same normed state, and so do gate/up: independent branches when asked
@@ -267,13 +311,13 @@ class PrefillStep:
         self.model, self.m, self.variant = model, m, variant
         f16 = dict(dtype=torch.float16, device=device)
         f32 = dict(dtype=torch.float32, device=device)
-        l0 = model.layers[0]
-        self.inputs = {"xn": torch.empty((m, l0["wq"].cols), **f16), "attn": torch.empty((m, l0["wo"].cols), **f16),
-                       "act": torch.empty((m, l0["ffn_down"].cols), **f16)}
+        widths = _input_widths(model)
+        self.inputs = {k: torch.empty((m, c), **f16) for k, c in widths.items()}
         for i, k in enumerate(("xn", "attn", "act")):
             fill_normal_t(self.inputs[k], seed=seed + i, mul=0.5)
-        self.outputs = {name: torch.empty((m, l0[name].rows), **f32) for name, *_ in LAYER_SPECS}
-        self.last = torch.empty((1, l0["wq"].cols), **f32)  # the last position's normed state
+        self.calls = [c for c in model.calls() if c[0] < len(model.layers)]
+        self.outputs = {name: torch.empty((m, w.rows), **f32) for l, name, w, _ in self.calls if l == 0}
+        self.last = torch.empty((1, widths["xn"]), **f32)  # the last position's normed state
         fill_normal_t(self.last, seed=seed + 3)
         self.logits = torch.empty((1, model.lm_head.rows), **f32) if model.lm_head is not None else None
 
@@ -285,9 +329,8 @@ class PrefillStep:
         return n
 
     def run(self, stream: int) -> None:
-        for layer in self.model.layers:
-            for name, _, _, _, src in LAYER_SPECS:
-                wgemm(self.outputs[name], layer[name], self.inputs[src], self.m, stream, self.variant)
+        for _, name, w, src in self.calls:
+            wgemm(self.outputs[name], w, self.inputs[src], self.m, stream, self.variant)
         if self.model.lm_head is not None:
             wmatmul_n(self.logits, self.model.lm_head, self.last, 1, stream)
 

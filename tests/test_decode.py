@@ -52,3 +52,34 @@ def test_plan_entry_points_reject_null_handles():
     assert lib.qvx_plan_create(None) == qvx.E_NULL
     lib.qvx_plan_destroy(None)
     assert qvx.strerror(qvx.E_STATE).startswith("plan not instantiated")
+
+
+def test_fused_model_stacks_same_input_pairs():
+    """Model.fused stacks q with k and gate with up (same type and row length) row-wise; calls()
+    then yields 5 GEMVs per layer in the reference's order, each stacked weight in place of its
+    first part, and the bytes of each part sit where its rows do."""
+    import torch
+    from qorvix_amd import decode
+    m = decode.Model()
+    for l in range(2):
+        layer = {}
+        for i, (name, rows, cols, t, _) in enumerate(decode.LAYER_SPECS):
+            rows, cols = rows // 256, cols // 16  # small stand-ins keeping the type mix and ratios
+            nb = qvx.weight_bytes(t, rows, cols)
+            layer[name] = decode.DevWeight(torch.full((nb,), 16 * l + i, dtype=torch.uint8), t, rows, cols)
+        m.layers.append(layer)
+    m.lm_head = decode.DevWeight(torch.zeros(qvx.weight_bytes(qvx.Q6_K, 8, 256), dtype=torch.uint8), qvx.Q6_K, 8, 256)
+    f = m.fused()
+    names = [(l, n, src) for l, n, _, src in f.calls()]
+    per_layer = [("wqk", "xn"), ("wv", "xn"), ("wo", "attn"), ("ffn_gateup", "xn"), ("ffn_down", "act")]
+    assert names == [(l, n, s) for l in range(2) for n, s in per_layer] + [(2, "lm_head", "xn")]
+    for l in range(2):
+        qk, gu = f.layers[l]["wqk"], f.layers[l]["ffn_gateup"]
+        q, k = m.layers[l]["wq"], m.layers[l]["wk"]
+        assert (qk.rows, qk.cols, qk.type) == (q.rows + k.rows, q.cols, q.type)
+        assert torch.equal(qk.data[:q.data.numel()], q.data) and torch.equal(qk.data[q.data.numel():], k.data)
+        assert gu.rows == m.layers[l]["ffn_gate"].rows + m.layers[l]["ffn_up"].rows
+        assert f.layers[l]["wv"] is m.layers[l]["wv"]  # Q6_K: not stacked with q/k, shared
+    assert f.parts["wqk"] == (("wq", 16), ("wk", 4))
+    # the unfused model keeps the reference's 7 calls per layer
+    assert [n for l, n, _, _ in m.calls() if l == 0] == [s[0] for s in decode.LAYER_SPECS]
