@@ -229,13 +229,23 @@ __global__ __launch_bounds__(1024) void k_gemv_mx(const uint8_t* __restrict__ W,
   // requests is full, and the CU returns data in request order, so activation loads issued behind
   // tile copies would wait out the HBM latency and hold the fragment barrier back.  Waves without
   // tasks go straight to their copies.
+  // Every round's loads go out before the first conversion (see the batched form).
   const int per = nsb * 32, ntask = NV * per;
+  float4 xa[TPT], xb[TPT];
+#pragma unroll
+  for (int k = 0; k < TPT; ++k) {
+    if (1024 * k + 64 * wave < ntask) {
+      const int t = min(tid + 1024 * k, ntask - 1), v = task_vec<NV>(t, per), r = t - v * per;
+      const float4* src = reinterpret_cast<const float4*>(X + (size_t)v * cols + 8 * r);
+      xa[k] = src[0];
+      xb[k] = src[1];
+    }
+  }
 #pragma unroll
   for (int k = 0; k < TPT; ++k) {
     if (1024 * k + 64 * wave < ntask) {
       const int t0 = tid + 1024 * k, t = min(t0, ntask - 1), v = task_vec<NV>(t, per), r = t - v * per;
-      const float4* src = reinterpret_cast<const float4*>(X + (size_t)v * cols + 8 * r);
-      mx_convert(src[0], src[1], v, r >> 3, r & 7, t0 < ntask, frag, meta, nsb);
+      mx_convert(xa[k], xb[k], v, r >> 3, r & 7, t0 < ntask, frag, meta, nsb);
     }
   }
 
@@ -492,14 +502,26 @@ __global__ __launch_bounds__(1024) void k_gemv_mxb(const uint8_t* __restrict__ W
   const int tq = wave % TQ, kq = wave / TQ;
   const int s0 = kq * nsb / KQ, s1 = (kq + 1) * nsb / KQ, nu = s1 - s0;
 
-  // 1. activations -> A fragments (waves with conversion tasks), before any copy
+  // 1. activations -> A fragments (waves with conversion tasks), before any copy.  Every round's
+  // loads are issued before the first conversion: the fragment stores (inline asm with a memory
+  // clobber) would otherwise keep each round's loads behind the previous round's stores, one memory
+  // latency per round.
   const int per = nsb * 32, ntask = nv * per;
+  float4 xa[TPT], xb[TPT];
+#pragma unroll
+  for (int k = 0; k < TPT; ++k) {
+    if (1024 * k + 64 * wave < ntask) {
+      const int t = min(tid + 1024 * k, ntask - 1), v = t / per, r = t - v * per;
+      const float4* src = reinterpret_cast<const float4*>(X + (size_t)v * cols + 8 * r);
+      xa[k] = src[0];
+      xb[k] = src[1];
+    }
+  }
 #pragma unroll
   for (int k = 0; k < TPT; ++k) {
     if (1024 * k + 64 * wave < ntask) {
       const int t0 = tid + 1024 * k, t = min(t0, ntask - 1), v = t / per, r = t - v * per;
-      const float4* src = reinterpret_cast<const float4*>(X + (size_t)v * cols + 8 * r);
-      mxb_convert(src[0], src[1], v, r >> 3, r & 7, t0 < ntask, frag, meta);
+      mxb_convert(xa[k], xb[k], v, r >> 3, r & 7, t0 < ntask, frag, meta);
     }
   }
 
