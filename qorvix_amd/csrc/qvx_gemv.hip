@@ -604,16 +604,17 @@ __global__ __launch_bounds__(1024) void k_gemv(const uint8_t* __restrict__ W, co
 constexpr int kCUs = 256;  // MI355X compute units
 
 // Rows a group keeps in flight ahead of the one being computed (measured per type: the 6-bit
-// formats, with the most registers per row, do best with one).
-template <uint32_t T>
+// formats, with the most registers per row, do best with one, Q6_K two when a launch takes one
+// vector; deeper rings spill with more vectors).
+template <uint32_t T, int NV>
 constexpr int prefetch_rows() {
-  return T == T_Q6_K || T == T_Q5_K ? 1 : 2;
+  return T == T_Q6_K ? (NV == 1 ? 2 : 1) : T == T_Q5_K ? 1 : 2;
 }
 
 template <uint32_t T, int NV, int RMAX, int TPT, bool CH>
 static void launch_t(const void* w, const float* X, float* Y, int rows, int cols, const Geo& geo, int nwg,
                      hipStream_t s) {
-  constexpr int PF = prefetch_rows<T>() < RMAX ? prefetch_rows<T>() : RMAX;
+  constexpr int PF = prefetch_rows<T, NV>() < RMAX ? prefetch_rows<T, NV>() : RMAX;
   auto kern = &k_gemv<T, NV, RMAX, TPT, PF, CH>;
   const size_t lds = gemv_lds_bytes<T>(NV, geo.S);
   if (lds > 64 * 1024) {
@@ -643,7 +644,7 @@ constexpr int max_rows() {
 template <uint32_t T, int NV, int TPT>
 static void launch_tpt(const void* w, const float* X, float* Y, int rows, int cols, Geo geo, hipStream_t s) {
   constexpr int rm = max_rows<NV, TPT>();
-  static_assert(rm % prefetch_rows<T>() == 0, "chunks of rm rows keep the prefetch ring aligned");
+  static_assert(rm % prefetch_rows<T, NV>() == 0, "chunks of rm rows keep the prefetch ring aligned");
   const int G = geo.G, waves = geo.Sp * G / 64;
   // one pass of workgroups over the chip (16 waves per CU), at least one row per group on
   // average; a group with more than rm rows walks them in chunks of rm
