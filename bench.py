@@ -244,27 +244,31 @@ def decode_sweep(torch, stream, steps, cpu=True):
     # Q4_K on the MFMA kernels, the Q6_K tensors through the dequantising library GEMM) and the LM head
     # on the last position.  The reference prefills token by token (generator.cpp:24-28), one decode
     # step per position: its equivalent here is M x the M = 1 sweep time.
-    pre = {}
-    for mp in (512, 2048):
-        st = decode.PrefillStep(model, mp)
+    def time_prefill(mdl, mp, reps=3):
+        st = decode.PrefillStep(mdl, mp)
         st.run(sh)
         torch.cuda.synchronize()
-        reps = 3
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
         for _ in range(reps):
             st.run(sh)
         e1.record(stream)
         torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / reps
-        tf = st.flops() / (ms * 1e-3) / 1e12
+        return e0.elapsed_time(e1) / reps, st.flops()
+
+    pre = {}
+    for mp in (512, 2048):
+        ms, flops = time_prefill(model, mp)
+        ms_fu, _ = time_prefill(fused, mp)
+        tf = flops / (ms * 1e-3) / 1e12
         tbt = mp * out["M1"]["ms_per_token"]
         pre[f"M{mp}"] = {"ms": round(ms, 3), "tokens_per_s": round(mp / (ms * 1e-3), 1), "tflops": round(tf, 1),
-                         "frac_of_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4), "runs_timed": reps,
-                         "token_by_token_ms": round(tbt, 2), "speedup_vs_token_by_token": round(tbt / ms, 1)}
+                         "frac_of_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4), "runs_timed": 3,
+                         "token_by_token_ms": round(tbt, 2), "speedup_vs_token_by_token": round(tbt / ms, 1),
+                         "ms_fused_qk_gateup": round(ms_fu, 3),
+                         "tokens_per_s_fused_qk_gateup": round(mp / (ms_fu * 1e-3), 1)}
         log(f"[bench] prefill M={mp}: {ms:.2f} ms ({mp / (ms * 1e-3):.0f} tokens/s, {tf:.0f} TFLOP/s); token by token "
-            f"{tbt:.1f} ms")
-        del st
+            f"{tbt:.1f} ms; {ms_fu:.2f} ms with q|k and gate|up stacked")
     out["prefill"] = {"workload": "Llama-3-8B Q4_K_M prompt prefill: 32 x 7 projections as GEMMs over M positions "
                                   "(fp16 activations) + the Q6_K LM head on the last position", **pre}
     del model, fused

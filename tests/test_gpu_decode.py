@@ -142,3 +142,24 @@ def test_fused_plan_matches_unfused(cuda, small_model, m):
             assert torch.equal(y.view(torch.int32), ya[(l, n)].view(torch.int32)), (l, n)
     a.plan.close()
     b.plan.close()
+
+
+def test_fused_prefill_matches_unfused(cuda, small_model):
+    """Prefill over the stacked q|k and gate|up weights: each part of a stacked output within the GEMM
+    tolerance of the separate projection's output, the other projections identical."""
+    torch = cuda
+    fused = small_model.fused()
+    a = decode.PrefillStep(small_model, 64, seed=5)
+    b = decode.PrefillStep(fused, 64, seed=5)
+    s = torch.cuda.current_stream().cuda_stream
+    a.run(s)
+    b.run(s)
+    torch.cuda.synchronize()
+    for name, y in b.outputs.items():
+        if name in fused.parts:
+            r0 = 0
+            for part, rows in fused.parts[name]:
+                assert max_rel(y[:, r0:r0 + rows].cpu().numpy(), a.outputs[part].cpu().numpy()) <= 2e-2, (name, part)
+                r0 += rows
+        else:
+            assert max_rel(y.cpu().numpy(), a.outputs[name].cpu().numpy()) <= 1e-6, name
