@@ -49,11 +49,11 @@ const Blas& blas() {
   return b;
 }
 
-// This thread's handle for the current device (nullptr when it cannot be created).
-rocblas_handle thread_handle(const Blas& b) {
+// This thread's handle for device `dev` (nullptr when it cannot be created).  Handles are kept for
+// the life of the process: destroying them from thread-exit destructors would race the HIP
+// runtime's own teardown at process exit.
+rocblas_handle thread_handle(const Blas& b, int dev) {
   thread_local rocblas_handle handles[kMaxDevices] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
   if (!handles[dev] && b.create(&handles[dev]) != rocblas_status_success) handles[dev] = nullptr;
   return handles[dev];
 }
@@ -74,9 +74,11 @@ __global__ __launch_bounds__(256) void k_f16_to_bf16_any(const uint16_t* __restr
 // 32-bit dimensions), -11 (rocBLAS missing or failing).  bf16: the bf16 variant.
 int launch_qgemm_dequant(float* out, const void* w, uint32_t t, const uint16_t* X, int M, int rows, int cols,
                          bool bf16, hipStream_t s) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return -5;
   const Blas& b = blas();
   if (!b.ok) return -11;
-  rocblas_handle h = thread_handle(b);
+  rocblas_handle h = thread_handle(b, dev);
   if (!h) return -11;
   const size_t nw = (size_t)rows * (size_t)cols, nx = (size_t)M * (size_t)cols;
   uint16_t* wd = static_cast<uint16_t*>(gemm_temp_alloc(nw * 2u + (bf16 ? nx * 2u : 0u), s));
