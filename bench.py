@@ -276,6 +276,74 @@ def decode_sweep(torch, stream, steps, cpu=True):
     return out
 
 
+def hbm_context(torch, stream, copies):
+    """Measured HBM rates beside the assumed peak, for context: the engine's bare streaming read
+    (qvx_bench_read, one 16-byte load per thread) over the GEMV's own weight copies (same bytes, same
+    cycling past the Infinity Cache, replayed as one graph like the GEMV leg) -- the most one launch
+    of that size reads -- and over 1 GiB; and a 512 MiB device-to-device copy (read + write bytes)."""
+    import qorvix_amd as qvx
+    so = qvx.lib()
+    sh = stream.cuda_stream
+    flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+
+    def read(buf, nbytes):
+        qvx._check(so.qvx_bench_read(buf.data_ptr(), nbytes, flag.data_ptr(), torch.cuda.current_stream().cuda_stream),
+                   "qvx_bench_read")
+
+    nb = copies[0].numel()
+    for c in copies:
+        read(c, nb)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for c in copies:
+            read(c, nb)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 5
+    e0.record(stream)
+    for _ in range(reps):
+        g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us_small = e0.elapsed_time(e1) * 1e3 / (reps * len(copies))
+    del g
+
+    def timed(fn, n=5):
+        fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(n):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            fn()
+            b.record(stream)
+            torch.cuda.synchronize()
+            ts.append(a.elapsed_time(b) * 1e-3)
+        return sorted(ts)[len(ts) // 2]
+    big = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    big.fill_(7)
+    with torch.cuda.stream(stream):
+        t_big = timed(lambda: read(big, 1 << 30))
+    del big
+    src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    src.fill_(1)
+    with torch.cuda.stream(stream):
+        t_copy = timed(lambda: dst.copy_(src))
+    del src, dst
+    torch.cuda.empty_cache()
+    assert int(flag.item()) == 0  # no word matched the pattern: nothing was stored
+    return {"read_us_gemv_weight_bytes": round(us_small, 2), "read_gbs_gemv_weight_bytes": round(nb / us_small / 1e3, 1),
+            "read_gbs_1gib": round((1 << 30) / t_big / 1e9, 1),
+            "copy_gbs_512mib": round(2 * (512 << 20) / t_copy / 1e9, 1),
+            "peak_assumed_gbs": HBM_PEAK_GBS,
+            "note": "qvx_bench_read (one 16-byte load per thread) over the GEMV's weight bytes cycled over its "
+                    "weight copies (graph-timed), and over 1 GiB; device copy of 512 MiB counts read + write "
+                    "bytes; context for the GEMV's HBM fraction, not part of the metric"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -468,6 +536,12 @@ def main():
         cpu = cpu_baseline(w_host, x_host, ROWS, COLS)
         log(f"[bench] CPU baseline ({cpu['kind']}): {cpu['value']} GB/s, {cpu['ms_per_gemv']} ms/GEMV")
 
+    hbm_ctx = hbm_context(torch, stream, copies)
+    log(f"[bench] HBM context: bare read of the GEMV's {copies[0].numel()} weight bytes "
+        f"{hbm_ctx['read_us_gemv_weight_bytes']} us ({hbm_ctx['read_gbs_gemv_weight_bytes']} GB/s), of 1 GiB "
+        f"{hbm_ctx['read_gbs_1gib']} GB/s; device copy {hbm_ctx['copy_gbs_512mib']} GB/s (peak assumed "
+        f"{HBM_PEAK_GBS:.0f} GB/s)")
+
     achieved = nbytes / (ms_per_step * 1e-3) / 1e9
     g2048 = gemm.get("bf16_M2048", {})
     traffic = None
@@ -524,6 +598,7 @@ def main():
         "config_gemvs": cfgs,
         "sweep": sweep,
         "cpu_baseline": cpu,
+        "hbm_context": hbm_ctx,
     }
     print(json.dumps(result), flush=True)
 

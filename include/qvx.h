@@ -126,6 +126,12 @@ int qvx_fill_synthetic(void* d_w, uint32_t type, int rows, int cols, uint64_t se
 int qvx_fill_normal_f32(float* d_x, size_t n, uint64_t seed, float mul, void* stream);
 int qvx_fill_normal_f16(uint16_t* d_x, size_t n, uint64_t seed, float mul, void* stream);
 
+/* Bare streaming read of n bytes (benchmark only, no reference counterpart): the HBM read rate a
+ * single launch reaches, beside which the GEMV's rate is judged.  One 16-byte load per thread; *d_flag
+ * is written (1) only if a 16-byte word of the data equals the fixed pattern 0x5A17C0DE x 4, so for
+ * other data nothing is stored.  n % 16 == 0 and d_src 16-byte aligned, else QVX_E_RANGE. */
+int qvx_bench_read(const void* d_src, size_t n, uint32_t* d_flag, void* stream);
+
 /* ---- plans: a recorded sequence of GEMV calls replayed as one HIP graph ------------------- */
 /* The form in which the reference's CUDA backend runs a decode step: the same type-switched
  * matmul launches (cuda/src/cuda_backend.cu:1523-1542, matmul / matmulS) issued on one stream and

@@ -52,6 +52,7 @@ SIGNATURES = {
     "qvx_fill_synthetic": ([_vp, _u32, _i32, _i32, _u64, _f32, _vp], _i32),
     "qvx_fill_normal_f32": ([_vp, _sz, _u64, _f32, _vp], _i32),
     "qvx_fill_normal_f16": ([_vp, _sz, _u64, _f32, _vp], _i32),
+    "qvx_bench_read": ([_vp, _sz, _vp, _vp], _i32),
     "qvx_plan_create": ([C.POINTER(_vp)], _i32),
     "qvx_plan_add_qmatmul_n": ([_vp, _vp, _vp, _u32, _vp, _i32, _i32, _i32], _i32),
     "qvx_plan_fork": ([_vp], _i32),

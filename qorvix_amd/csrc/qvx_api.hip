@@ -35,6 +35,7 @@ bool launch_gemv_mxb_q4k(const void* w, const float* X, float* Y, int nvec, int 
 bool launch_fill_synthetic(void* w, uint32_t t, size_t nblk, uint64_t seed, float mul, hipStream_t s);
 void launch_fill_normal_f32(float* x, size_t n, uint64_t seed, float mul, hipStream_t s);
 void launch_fill_normal_f16(uint16_t* x, size_t n, uint64_t seed, float mul, hipStream_t s);
+void launch_read16(const void* src, size_t n16, uint32_t* flag, hipStream_t s);
 int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M, int rows, int cols,
                  int variant, hipStream_t s);
 int launch_quantize_act_q8(const uint16_t* X, int M, int K, int8_t* q, float* scale, int32_t* qsum,
@@ -297,6 +298,14 @@ int qvx_fill_normal_f32(float* d_x, size_t n, uint64_t seed, float mul, void* st
 int qvx_fill_normal_f16(uint16_t* d_x, size_t n, uint64_t seed, float mul, void* stream) {
   if (n && !d_x) return QVX_E_NULL;
   launch_fill_normal_f16(d_x, n, seed, mul, as_stream(stream));
+  return hip_status();
+}
+
+int qvx_bench_read(const void* d_src, size_t n, uint32_t* d_flag, void* stream) {
+  if (n % 16 != 0) return QVX_E_RANGE;
+  if (n && (!d_src || !d_flag)) return QVX_E_NULL;
+  if (reinterpret_cast<uintptr_t>(d_src) & 15u) return QVX_E_RANGE;
+  launch_read16(d_src, n / 16, d_flag, as_stream(stream));
   return hip_status();
 }
 

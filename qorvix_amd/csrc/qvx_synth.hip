@@ -89,4 +89,19 @@ void launch_fill_normal_f16(uint16_t* x, size_t n, uint64_t seed, float mul, hip
   if (n) k_fill_normal_f16<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(x, n, seed, mul);
 }
 
+// Bare streaming read (benchmark only): one 16-byte load per thread, the fastest pattern measured for
+// a single launch on this part.  The loaded words are kept live by a comparison that holds only for
+// a fixed pattern (all four words equal to 0x5A17C0DE), in which case the thread stores 1 to *flag;
+// any other data writes nothing.
+__global__ __launch_bounds__(1024) void k_read16(const uint4* __restrict__ src, size_t n16, uint32_t* __restrict__ flag) {
+  const size_t i = (size_t)blockIdx.x * 1024 + threadIdx.x;
+  if (i >= n16) return;
+  const uint4 v = src[i];
+  if ((v.x & v.y & v.z & v.w) == 0x5A17C0DEu && (v.x | v.y | v.z | v.w) == 0x5A17C0DEu) *flag = 1u;
+}
+
+void launch_read16(const void* src, size_t n16, uint32_t* flag, hipStream_t s) {
+  if (n16) k_read16<<<(unsigned)((n16 + 1023) / 1024), 1024, 0, s>>>(static_cast<const uint4*>(src), n16, flag);
+}
+
 }  // namespace qvx

@@ -146,3 +146,11 @@ def test_product_never_imports_oracle():
             if f.endswith((".py", ".hip", ".hpp", ".cpp", ".h")):
                 text = open(os.path.join(dirpath, f)).read()
                 assert "import oracle" not in text and "liboracle" not in text and "qvxo_" not in text, f
+
+
+def test_bench_read_rejections():
+    lib = qvx.lib()
+    assert lib.qvx_bench_read(FAKE, 100, FAKE, None) == qvx.E_RANGE  # not whole 16-byte words
+    assert lib.qvx_bench_read(None, 256, FAKE, None) == qvx.E_NULL
+    assert lib.qvx_bench_read(FAKE, 256, None, None) == qvx.E_NULL
+    assert lib.qvx_bench_read(FAKE + 4, 256, FAKE, None) == qvx.E_RANGE  # source not 16-byte aligned

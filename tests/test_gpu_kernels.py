@@ -492,3 +492,17 @@ def test_synthetic_blocks_are_well_formed(cuda):
         if t == qvx.Q8_0:
             q = blk[:, 2:].view(np.int8)
             assert q.min() == -127 and q.max() == 127
+
+
+def test_bench_read_stores_only_on_the_pattern(cuda):
+    """The bare-read helper stores nothing for ordinary data and 1 when a word holds the pattern."""
+    buf = cuda.zeros(1 << 20, dtype=cuda.uint8, device="cuda")
+    flag = cuda.zeros(1, dtype=cuda.int32, device="cuda")
+    s = cuda.cuda.current_stream().cuda_stream
+    assert qvx.lib().qvx_bench_read(buf.data_ptr(), buf.numel(), flag.data_ptr(), s) == qvx.OK
+    cuda.cuda.synchronize()
+    assert int(flag.item()) == 0
+    buf.view(cuda.int32)[4096:4100] = 0x5A17C0DE
+    assert qvx.lib().qvx_bench_read(buf.data_ptr(), buf.numel(), flag.data_ptr(), s) == qvx.OK
+    cuda.cuda.synchronize()
+    assert int(flag.item()) == 1
