@@ -224,12 +224,14 @@ __global__ __launch_bounds__(1024) void k_gemv_mx(const uint8_t* __restrict__ W,
   const int tq = wave % TQ, kq = wave / TQ;
   const int s0 = kq * nsb / KQ, s1 = (kq + 1) * nsb / KQ, nu = s1 - s0;
 
-  // 1. activations -> A fragments, by the waves that hold conversion tasks.  This comes before any
-  // copy: a wave's vector memory instructions stall at issue once the CU's queue of outstanding
-  // requests is full, and the CU returns data in request order, so activation loads issued behind
-  // tile copies would wait out the HBM latency and hold the fragment barrier back.  Waves without
-  // tasks go straight to their copies.
-  // Every round's loads go out before the first conversion (see the batched form).
+  // 1. activation loads (waves that hold conversion tasks), then 2. the prologue tile copies, then
+  // 3. the conversion into A fragments.  The activation loads go first: a wave's vector memory
+  // instructions stall at issue once the CU's queue of outstanding requests is full, and the CU
+  // returns data in request order, so activation loads behind tile copies would wait out the HBM
+  // latency and hold the fragment barrier back.  The copies go before the conversion so that the
+  // tiles are in flight while it runs (one launch of 4096 -> 14336 3 % faster, of 4096 -> 4096 9 %).
+  // Waves without tasks go straight to their copies.  Every round's loads go out before the first
+  // conversion (see the batched form).
   const int per = nsb * 32, ntask = NV * per;
   float4 xa[TPT], xb[TPT];
 #pragma unroll
@@ -241,14 +243,6 @@ __global__ __launch_bounds__(1024) void k_gemv_mx(const uint8_t* __restrict__ W,
       xb[k] = src[1];
     }
   }
-#pragma unroll
-  for (int k = 0; k < TPT; ++k) {
-    if (1024 * k + 64 * wave < ntask) {
-      const int t0 = tid + 1024 * k, t = min(t0, ntask - 1), v = task_vec<NV>(t, per), r = t - v * per;
-      mx_convert(xa[k], xb[k], v, r >> 3, r & 7, t0 < ntask, frag, meta, nsb);
-    }
-  }
-
   // 2. prologue copies into all NB stages (tiles of super-blocks s0.., repeating the wave's last one
   // when it has fewer than NB, so the count is fixed; rows past cnt read as zeros)
   const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -264,6 +258,14 @@ __global__ __launch_bounds__(1024) void k_gemv_mx(const uint8_t* __restrict__ W,
   const int s_last = max(s0, s1 - 1);  // < nsb: s0 < nsb for every wave
 #pragma unroll
   for (int u = 0; u < NB; ++u) mx_issue(rsrc, off, min(s0 + u, s_last), stage + u * kTileBytes);
+
+#pragma unroll
+  for (int k = 0; k < TPT; ++k) {
+    if (1024 * k + 64 * wave < ntask) {
+      const int t0 = tid + 1024 * k, t = min(t0, ntask - 1), v = task_vec<NV>(t, per), r = t - v * per;
+      mx_convert(xa[k], xb[k], v, r >> 3, r & 7, t0 < ntask, frag, meta, nsb);
+    }
+  }
 
   // Barrier for the fragments only: wait for this wave's LDS writes, not for the tile copies in
   // flight (__syncthreads would wait for those too).
