@@ -67,13 +67,13 @@ struct MxGeo {
   uint32_t row_bytes;
 };
 
-// LDS: dynamic [fragments: NV*nsb*512][meta: NV*nsb*4 groups*16] and a static tile ring
-// [16 waves][NB][2304].
+// LDS: dynamic [fragments: NV*nsb*512][meta: NV*nsb*4 groups*16], a static tile ring
+// [16 waves][NB][2304] and the partial sums [16 waves][NV][16] floats.
 __host__ __device__ inline size_t mx_frag_bytes(int nv, int nsb) { return (size_t)nv * nsb * kFragBytes; }
 __host__ __device__ inline size_t mx_meta_bytes(int nv, int nsb) { return (size_t)nv * nsb * 4 * 16; }
 __host__ __device__ inline size_t mx_dyn_bytes(int nv, int nsb) { return mx_frag_bytes(nv, nsb) + mx_meta_bytes(nv, nsb); }
 __host__ __device__ inline size_t mx_lds_bytes(int nv, int nsb, int nb) {
-  return mx_dyn_bytes(nv, nsb) + (size_t)16 * nb * kTileBytes;
+  return mx_dyn_bytes(nv, nsb) + (size_t)16 * nb * kTileBytes + (size_t)16 * nv * 16 * 4;
 }
 
 template <int CTRL>
@@ -212,6 +212,7 @@ __global__ __launch_bounds__(1024) void k_gemv_mx(const uint8_t* __restrict__ W,
   static_assert(NB >= 2 && NB <= 4, "the tile wait below covers up to 3 tiles ahead");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   __shared__ __attribute__((aligned(16))) uint8_t ring[16 * NB * kTileBytes];
+  __shared__ float red[16 * NV * 16];  // per-wave partial sums [tq][kq][v][16]
   const int nsb = geo.nsb, TQ = geo.TQ, KQ = geo.KQ;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar offsets, M0
@@ -349,7 +350,7 @@ __global__ __launch_bounds__(1024) void k_gemv_mx(const uint8_t* __restrict__ W,
     }
   }
 
-  wait_vm<0>();  // repeated prologue tiles may still be in flight; the ring is reused below
+  wait_vm<0>();  // repeated prologue tiles may still be in flight: none may land after the wave ends
 
   // 5. sum over the four groups (lanes j, j+16, j+32, j+48), then over the KQ waves of the tile
 #pragma unroll
@@ -360,8 +361,6 @@ __global__ __launch_bounds__(1024) void k_gemv_mx(const uint8_t* __restrict__ W,
     const auto a16 = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, sv), __builtin_bit_cast(int, sv), false, false);
     acc[v] = __builtin_bit_cast(float, (int)a16[0]) + __builtin_bit_cast(float, (int)a16[1]);
   }
-  __syncthreads();  // every wave is done with its stages: reuse the ring for the sums
-  float* red = reinterpret_cast<float*>(ring);  // [tq][kq][v][16]
   if (lane < 16) {
 #pragma unroll
     for (int v = 0; v < NV; ++v) red[((tq * KQ + kq) * NV + v) * 16 + lane] = acc[v];
