@@ -15,6 +15,8 @@
 #include "../../include/qvx.h"
 #include "qvx_common.hpp"
 
+#include <algorithm>
+
 namespace qvx {
 bool launch_dequant(uint32_t t, const void* src, float* dst, size_t n, hipStream_t s);
 bool launch_gemv_generic(uint32_t t, const void* w, const float* X, float* Y, int rows, int cols, int nvec,
@@ -110,18 +112,21 @@ int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int
   // same in every launch, so batches stay bit-identical to single vectors.  Q4_K runs on the matrix
   // cores (up to gemv_mx_max_nv vectors per launch), the other formats on the VALU kernel; shapes
   // neither covers go to the generic kernel.
-  // Q4_K batches of two or more vectors take a batched matrix-core form (8 vectors a launch,
-  // bit-identical to the one-vector form): the one that stages a whole row's activation fragments
-  // in LDS where they fit, else the long-row one that converts them per super-block.
+  // Q4_K batches of two or more vectors, 8 at a time: a chunk of up to 3 vectors (2 on long rows)
+  // runs on the one-vector kernel, several vectors a launch (measured faster there); larger chunks
+  // take a batched matrix-core form: the one that stages a whole row's activation fragments in LDS
+  // where they fit, else the long-row one that converts them per super-block.  All three forms are
+  // bit-identical per vector.
   if (fast && type == T_Q4_K && nvec >= 2 && (gemv_mxb_supported(cols) || gemv_mxj_supported(cols))) {
     const bool whole = gemv_mxb_supported(cols) != 0;
+    const int small = std::min(whole ? 3 : 2, gemv_mx_max_nv(cols));
     for (int v0 = 0; v0 < nvec; v0 += 8) {
       const int nv = nvec - v0 < 8 ? nvec - v0 : 8;
       const float* Xv = X + (size_t)v0 * cols;
       float* Yv = out + (size_t)v0 * rows;
-      const bool ok = nv == 1  ? launch_gemv_mx_q4k(w, Xv, Yv, 1, rows, cols, row_bytes, s)
-                      : whole ? launch_gemv_mxb_q4k(w, Xv, Yv, nv, rows, cols, row_bytes, s)
-                              : launch_gemv_mxj_q4k(w, Xv, Yv, nv, rows, cols, row_bytes, s);
+      const bool ok = nv <= small ? launch_gemv_mx_q4k(w, Xv, Yv, nv, rows, cols, row_bytes, s)
+                      : whole     ? launch_gemv_mxb_q4k(w, Xv, Yv, nv, rows, cols, row_bytes, s)
+                                  : launch_gemv_mxj_q4k(w, Xv, Yv, nv, rows, cols, row_bytes, s);
       if (!ok) return QVX_E_TYPE;
     }
     return hip_status();
