@@ -344,6 +344,58 @@ def hbm_context(torch, stream, copies):
                     "bytes; context for the GEMV's HBM fraction, not part of the metric"}
 
 
+def gemm_leg(torch, stream, t, wps, copies, steps, cpu):
+    """Q4_K 4096 -> 14336 prefill GEMM at M = 2048, 512, 128 in the bf16, fp16 and
+    int8 variants, each call timed whole (prepass + GEMM) with HIP events on the launch stream, and the
+    reference CPU qmatmulN beside it on a 64-token sample."""
+    import qorvix_amd as qvx
+    lib, sh, dev = qvx.lib(), stream.cuda_stream, stream.device
+    gemm = {}
+    try:
+        for M in (2048, 512, 128):
+            X = torch.empty((M, COLS), dtype=torch.float16, device=dev)
+            qvx.fill_normal_t(X, seed=11, mul=0.5)
+            Y = torch.empty((M, ROWS), dtype=torch.float32, device=dev)
+            for name, var in (("bf16", qvx.GEMM_BF16), ("f16", qvx.GEMM_F16), ("i8", qvx.GEMM_I8)):
+                def g(i):
+                    rc = lib.qvx_qgemm_f16(Y.data_ptr(), wps[i % len(wps)], t, X.data_ptr(), M, ROWS, COLS, var, sh)
+                    if rc != 0:
+                        raise RuntimeError(f"qvx_qgemm_f16 failed: {qvx.strerror(rc)}")
+                for i in range(3):
+                    g(i)
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for i in range(steps):
+                    g(i)
+                e1.record(stream)
+                torch.cuda.synchronize()
+                ms = e0.elapsed_time(e1) / steps
+                tflops = 2.0 * M * ROWS * COLS / (ms * 1e-3) / 1e12
+                gemm[f"{name}_M{M}"] = {"ms": round(ms, 4), "tflops": round(tflops, 1),
+                                        "frac_of_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4)}
+                log(f"[bench] GEMM {name} M={M}: {ms * 1e3:.1f} us, {tflops:.1f} TFLOP/s "
+                    f"({100 * tflops / BF16_PEAK_TFLOPS:.1f}% of bf16 peak)")
+            if cpu:
+                # the reference CPU qmatmulN on the first 64 tokens of X (fp16 -> fp32 exactly; 64 is
+                # the operator's own vector tile), same blocks; GFLOP/s extrapolates per token
+                kind, fn, dot, cores = cpu_operator()
+                ms_tok = 64
+                Xs = X[:ms_tok].float().cpu().numpy()
+                sec, runs = cpu_time(fn, copies[0].cpu().numpy(), t, Xs, ms_tok, ROWS, COLS)
+                gf = 2.0 * ms_tok * ROWS * COLS / sec / 1e9
+                gemm[f"cpu_M{M}"] = {"kind": kind, "gflops": round(gf, 1), "ms_for_sample": round(sec * 1e3, 2),
+                                     "ms_extrapolated": round(sec * 1e3 * M / ms_tok, 1), "runs": runs,
+                                     "threads": cores, "dot_kernel": dot,
+                                     "sample": f"first {ms_tok} of the {M} tokens (qmatmulN, X converted fp16->fp32)"}
+                log(f"[bench] GEMM M={M} CPU {kind}: {gf:.1f} GFLOP/s on a {ms_tok}-token sample")
+            del X, Y
+    except RuntimeError as e:  # report, never hide: the JSON carries the error
+        gemm["error"] = str(e)
+        log(f"[bench] GEMM failed: {e}")
+    return gemm
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -356,6 +408,7 @@ def main():
     ap.add_argument("--sweep-steps", type=int, default=20, help="timed tokens of the config-5 decode sweep")
     ap.add_argument("--sweep-only", action="store_true", help="only the config-5 decode sweep (profiler passes)")
     ap.add_argument("--configs-only", action="store_true", help="only the configs[0..2] GEMV points (profiler passes)")
+    ap.add_argument("--gemm-only", action="store_true", help="only the prefill GEMM leg (profiler passes)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MiB",
                     help="also run one plain device copy of this many MiB (PMC byte-counter calibration)")
     args = ap.parse_args()
@@ -390,6 +443,11 @@ def main():
     qvx.fill_normal_t(x, seed=7)
     out = torch.empty(ROWS, dtype=torch.float32, device=dev)
     torch.cuda.synchronize()
+    if args.gemm_only:  # profiler pass over the prefill GEMM leg alone
+        wps = [w.data_ptr() for w in copies]
+        print(json.dumps({"gemm": gemm_leg(torch, stream, t, wps, copies, args.gemm_steps, cpu=not args.no_cpu)}),
+              flush=True)
+        return
     log(f"[bench] {args.copies} Q4_K copies x {wbytes / 2**20:.1f} MiB = {args.copies * wbytes / 2**30:.2f} GiB")
 
     lib = qvx.lib()
@@ -466,49 +524,7 @@ def main():
         del a, b
 
     # ---- prefill GEMM ----------------------------------------------------
-    gemm = {}
-    try:
-        for M in ((2048, 512, 128) if not args.gemv_only else ()):
-            X = torch.empty((M, COLS), dtype=torch.float16, device=dev)
-            qvx.fill_normal_t(X, seed=11, mul=0.5)
-            Y = torch.empty((M, ROWS), dtype=torch.float32, device=dev)
-            for name, var in (("bf16", qvx.GEMM_BF16), ("f16", qvx.GEMM_F16), ("i8", qvx.GEMM_I8)):
-                def g(i):
-                    rc = lib.qvx_qgemm_f16(Y.data_ptr(), wps[i % len(wps)], t, X.data_ptr(), M, ROWS, COLS, var, sh)
-                    if rc != 0:
-                        raise RuntimeError(f"qvx_qgemm_f16 failed: {qvx.strerror(rc)}")
-                for i in range(3):
-                    g(i)
-                torch.cuda.synchronize()
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record(stream)
-                for i in range(args.gemm_steps):
-                    g(i)
-                e1.record(stream)
-                torch.cuda.synchronize()
-                ms = e0.elapsed_time(e1) / args.gemm_steps
-                tflops = 2.0 * M * ROWS * COLS / (ms * 1e-3) / 1e12
-                gemm[f"{name}_M{M}"] = {"ms": round(ms, 4), "tflops": round(tflops, 1),
-                                        "frac_of_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4)}
-                log(f"[bench] GEMM {name} M={M}: {ms * 1e3:.1f} us, {tflops:.1f} TFLOP/s "
-                    f"({100 * tflops / BF16_PEAK_TFLOPS:.1f}% of bf16 peak)")
-            if not args.no_cpu:
-                # the reference CPU qmatmulN on the first 64 tokens of X (fp16 -> fp32 exactly; 64 is
-                # the operator's own vector tile), same blocks; GFLOP/s extrapolates per token
-                kind, fn, dot, cores = cpu_operator()
-                ms_tok = 64
-                Xs = X[:ms_tok].float().cpu().numpy()
-                sec, runs = cpu_time(fn, copies[0].cpu().numpy(), t, Xs, ms_tok, ROWS, COLS)
-                gf = 2.0 * ms_tok * ROWS * COLS / sec / 1e9
-                gemm[f"cpu_M{M}"] = {"kind": kind, "gflops": round(gf, 1), "ms_for_sample": round(sec * 1e3, 2),
-                                     "ms_extrapolated": round(sec * 1e3 * M / ms_tok, 1), "runs": runs,
-                                     "threads": cores, "dot_kernel": dot,
-                                     "sample": f"first {ms_tok} of the {M} tokens (qmatmulN, X converted fp16->fp32)"}
-                log(f"[bench] GEMM M={M} CPU {kind}: {gf:.1f} GFLOP/s on a {ms_tok}-token sample")
-            del X, Y
-    except RuntimeError as e:  # report, never hide: the JSON carries the error
-        gemm["error"] = str(e)
-        log(f"[bench] GEMM failed: {e}")
+    gemm = {} if args.gemv_only else gemm_leg(torch, stream, t, wps, copies, args.gemm_steps, cpu=not args.no_cpu)
 
     # ---- every GEMV point of BASELINE configs[0..2] ----------------------------------------------
     cfgs = []
