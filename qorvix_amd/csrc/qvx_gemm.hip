@@ -33,6 +33,7 @@
 // host stubs of template kernels from being emitted.
 #include "qvx_common.hpp"
 
+#include <algorithm>
 #include <mutex>
 #include <utility>
 
@@ -733,18 +734,26 @@ __global__ __launch_bounds__(256) void k_qgemm_q4k_i8(const uint8_t* __restrict_
     }
 }
 
-// fp16 -> bf16 (round to nearest even), 8 values a thread.
-__global__ __launch_bounds__(256) void k_f16_to_bf16(const uint4* __restrict__ x, uint4* __restrict__ y, size_t n8) {
+// fp16 -> bf16 (round to nearest even), 8 values a thread; the same launch also zeroes z4[0, nz4)
+// (the output of a K-split GEMM, 16-byte aligned) with a grid-stride loop.
+__global__ __launch_bounds__(256) void k_f16_to_bf16(const uint4* __restrict__ x, uint4* __restrict__ y, size_t n8,
+                                                     float4* __restrict__ z4, size_t nz4) {
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  for (size_t k = i; k < nz4; k += (size_t)gridDim.x * 256) z4[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   if (i >= n8) return;
   const uint4 v = x[i];
   y[i] = make_uint4(pack2<VAR_BF16>(f16lo(v.x), f16hi(v.x)), pack2<VAR_BF16>(f16lo(v.y), f16hi(v.y)),
                     pack2<VAR_BF16>(f16lo(v.z), f16hi(v.z)), pack2<VAR_BF16>(f16lo(v.w), f16hi(v.w)));
 }
 
-__global__ __launch_bounds__(256) void k_zero_f32(float* __restrict__ p, size_t n) {
+// Zero fill: four floats a thread from the first 16-byte boundary, single floats before it and in
+// the tail.
+__global__ __launch_bounds__(256) void k_zero_f32(float* __restrict__ p, size_t head, size_t n4, size_t n) {
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (i < n) p[i] = 0.0f;
+  if (i < n4) reinterpret_cast<float4*>(p + head)[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (i < head) p[i] = 0.0f;
+  const size_t t = head + 4 * n4 + i;
+  if (t < n && i < 4) p[t] = 0.0f;
 }
 
 namespace {
@@ -776,7 +785,11 @@ hipMemPool_t device_pool() {
 
 // Zero fill by kernel (no memset nodes, so callers may capture it in a HIP graph).
 void launch_zero(float* p, size_t n, hipStream_t s) {
-  if (n) k_zero_f32<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(p, n);
+  if (!n) return;
+  const size_t mis = (reinterpret_cast<uintptr_t>(p) >> 2) & 3u;  // p is 4-byte aligned
+  const size_t head = std::min(n, mis ? 4 - mis : (size_t)0), n4 = (n - head) / 4;
+  const size_t threads = std::max<size_t>(n4, 4);
+  k_zero_f32<<<(unsigned)((threads + 255) / 256), 256, 0, s>>>(p, head, n4, n);
 }
 
 // Stream-ordered temporary from the library's pool (nullptr on failure) and its release.
@@ -846,12 +859,16 @@ int launch_quantize_act_q8(const uint16_t* X, int M, int K, int8_t* q, float* sc
 
 namespace {
 
+// Whole super-blocks of K per split, and the split count that results.
+inline int split_per(int nsl, int splits) { return ((nsl + splits - 1) / splits + 3) & ~3; }
+
 template <int VAR, int BM>
-void launch_q4k(float* out, const void* w, const uint16_t* X, int M, int N, int K, int splits, hipStream_t s) {
+void launch_q4k(float* out, const void* w, const uint16_t* X, int M, int N, int K, int splits, bool zeroed,
+                hipStream_t s) {
   const int nsl = K / 64;
-  const int per = ((nsl + splits - 1) / splits + 3) & ~3;  // whole super-blocks per split
+  const int per = split_per(nsl, splits);
   splits = (nsl + per - 1) / per;
-  if (splits > 1) launch_zero(out, (size_t)M * N, s);
+  if (splits > 1 && !zeroed) launch_zero(out, (size_t)M * N, s);
   GemmGeo geo{M,           N,           K,           (uint32_t)(K / 256) * 144u, per, splits > 1 ? 1 : 0,
               0x0F0F0F0Fu, 0xF0F0F0F0u, 0x000F000Fu, 0x00F000F0u};
   dim3 grid((N + kBN - 1) / kBN, (M + BM - 1) / BM, splits);
@@ -861,17 +878,30 @@ void launch_q4k(float* out, const void* w, const uint16_t* X, int M, int N, int 
 // Tile choice: 256-token tiles when they alone give ~one workgroup per CU; else 128-token tiles,
 // splitting K (fp32 atomics into a zeroed output, M*N adds per split) only while the grid is
 // smaller than that.
-template <int VAR>
-void launch_var(float* out, const void* w, const uint16_t* X, int M, int N, int K, hipStream_t s) {
+// Tile rows (256 or 128) and K splits for an M x N x K launch.
+inline void q4k_plan(int M, int N, int K, int& bm, int& splits) {
   const int nt = (N + kBN - 1) / kBN, nsl = K / 64;
+  splits = 1;
   if (nt * ((M + 255) / 256) >= 224) {
-    launch_q4k<VAR, 256>(out, w, X, M, N, K, 1, s);
+    bm = 256;
     return;
   }
+  bm = 128;
   const int tiles = nt * ((M + 127) / 128);
-  int splits = 1;
   while (tiles * splits < 200 && nsl / (splits * 2) >= 8) splits *= 2;
-  launch_q4k<VAR, 128>(out, w, X, M, N, K, splits, s);
+  const int per = split_per(nsl, splits);
+  splits = (nsl + per - 1) / per;
+}
+
+// zeroed: the caller has already zeroed the output of a K-split launch.
+template <int VAR>
+void launch_var(float* out, const void* w, const uint16_t* X, int M, int N, int K, bool zeroed, hipStream_t s) {
+  int bm, splits;
+  q4k_plan(M, N, K, bm, splits);
+  if (bm == 256)
+    launch_q4k<VAR, 256>(out, w, X, M, N, K, splits, zeroed, s);
+  else
+    launch_q4k<VAR, 128>(out, w, X, M, N, K, splits, zeroed, s);
 }
 
 }  // namespace
@@ -896,14 +926,20 @@ int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M
     const size_t n = (size_t)M * (size_t)cols;
     void* xb = gemm_temp_alloc(n * 2u, s);
     if (!xb) return -5;
-    k_f16_to_bf16<<<(unsigned)((n / 8 + 255) / 256), 256, 0, s>>>(reinterpret_cast<const uint4*>(X),
-                                                                    static_cast<uint4*>(xb), n / 8);
-    launch_var<VAR_BF16>(out, w, static_cast<const uint16_t*>(xb), M, rows, cols, s);
+    // a K-split launch accumulates into a zeroed output: zero it in the prepass when it is aligned
+    int bm, splits;
+    q4k_plan(M, rows, cols, bm, splits);
+    const size_t nout = (size_t)M * (size_t)rows;
+    const bool fuse = splits > 1 && !(reinterpret_cast<uintptr_t>(out) & 15u) && nout % 4 == 0;
+    k_f16_to_bf16<<<(unsigned)((n / 8 + 255) / 256), 256, 0, s>>>(
+        reinterpret_cast<const uint4*>(X), static_cast<uint4*>(xb), n / 8, reinterpret_cast<float4*>(out),
+        fuse ? nout / 4 : 0);
+    launch_var<VAR_BF16>(out, w, static_cast<const uint16_t*>(xb), M, rows, cols, fuse, s);
     gemm_temp_free(xb, s);
     return 0;
   }
   if (variant == VAR_F16) {
-    launch_var<VAR_F16>(out, w, X, M, rows, cols, s);
+    launch_var<VAR_F16>(out, w, X, M, rows, cols, false, s);
     return 0;
   }
   if (variant == VAR_I8) {

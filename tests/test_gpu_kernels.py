@@ -284,6 +284,20 @@ def test_gemv_zero_cols_writes_zeros(cuda):
     assert np.all(out.cpu().numpy() == 0)
 
 
+@pytest.mark.parametrize("offset,n", [(0, 5), (1, 7), (3, 9), (2, 1), (1, 4099)])
+def test_zero_fill_head_and_tail(cuda, offset, n):
+    """cols == 0 zero-fills through the library's zero kernel: vector stores from the first 16-byte
+    boundary, single floats before it and after the last whole vector; nothing outside is touched."""
+    buf = cuda.full((n + 8,), 3.0, dtype=cuda.float32, device="cuda")
+    out = buf[offset:offset + n]
+    rc = qvx.qmatmul(out.data_ptr(), 0, qvx.Q4_K, 0, n, 0, cuda.cuda.current_stream().cuda_stream)
+    assert rc == qvx.OK
+    cuda.cuda.synchronize()
+    got = buf.cpu().numpy()
+    assert np.all(got[offset:offset + n] == 0)
+    assert np.all(got[:offset] == 3.0) and np.all(got[offset + n:] == 3.0)
+
+
 @pytest.mark.parametrize("t", GEMV_TYPES)
 def test_gemv_linearity_full_size(cuda, t):
     """Size-independent property at a BASELINE shape: W(a x + b y) = a Wx + b Wy (fp32 tolerance)."""
@@ -364,6 +378,30 @@ def test_gemm_q4k_parity(cuda, variant, M, rows, cols):
     cuda.cuda.synchronize()
     ref = oracle.matmul_f64(w, t, X16.astype(np.float32), M, rows, cols)
     assert max_rel(out.cpu().numpy(), ref) <= GEMM_TOL
+
+
+@pytest.mark.parametrize("variant", [qvx.GEMM_BF16, qvx.GEMM_F16, qvx.GEMM_I8])
+@pytest.mark.parametrize("offset", [0, 1, 3])
+def test_gemm_split_k_overwrites_stale_output(cuda, variant, offset):
+    """M = 128 splits K across workgroups that accumulate into an output zeroed first (in the bf16
+    prepass when the output is 16-byte aligned, by the zero kernel otherwise): NaN left in the output
+    buffer never leaks into the result, at any float offset, and nothing outside it is written."""
+    rng = np.random.default_rng(77 + 10 * variant + offset)
+    t, M, rows, cols = qvx.Q4_K, 128, 512, 1024
+    w = random_weight(t, rows, cols, rng, scale=0.002)
+    X16 = (rng.standard_normal((M, cols)) * 0.5).astype(np.float16)
+    X, W = dev(cuda, X16.view(np.uint16)), dev(cuda, w)
+    buf = cuda.full((M * rows + 8,), float("nan"), dtype=cuda.float32, device="cuda")
+    out = buf[offset:offset + M * rows]
+    rc = qvx.lib().qvx_qgemm_f16(out.data_ptr(), W.data_ptr(), t, X.data_ptr(), M, rows, cols, variant,
+                                 cuda.cuda.current_stream().cuda_stream)
+    assert rc == qvx.OK
+    cuda.cuda.synchronize()
+    got = buf.cpu().numpy()
+    ref = oracle.matmul_f64(w, t, X16.astype(np.float32), M, rows, cols)
+    assert np.isfinite(got[offset:offset + M * rows]).all()
+    assert max_rel(got[offset:offset + M * rows].reshape(M, rows), ref) <= GEMM_TOL
+    assert np.isnan(got[:offset]).all() and np.isnan(got[offset + M * rows:]).all()
 
 
 DEQUANT_GEMM_TYPES = [qvx.Q6_K, qvx.Q8_0, qvx.Q4_0, qvx.Q5_0, qvx.Q5_K, qvx.Q4_1, qvx.Q5_1, qvx.Q8_1,
