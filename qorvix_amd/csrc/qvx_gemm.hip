@@ -509,11 +509,13 @@ constexpr int kI8BM = 128;
 // Quantiser prepass: one thread per 32-value block of the (tile-padded) M x K activations.  Writes
 // q int8 [M, K] and, for slice kb and token tile t, SC[((kb * ntile + t) * 4 + a) * 128 + m % 128]
 // with a = 0, 1: scale of block 2kb + a; a = 2, 3: scale * qsum of block 2kb + a - 2 (zeros for
-// padding rows).
+// padding rows).  The same launch zeroes z4[0, nz4) (the output of a K-split GEMM, 16-byte aligned).
 __global__ __launch_bounds__(256) void k_quant_q8_gemm(const uint16_t* __restrict__ X, int M, int K, int Mpad,
-                                                       int8_t* __restrict__ q, float* __restrict__ sc) {
+                                                       int8_t* __restrict__ q, float* __restrict__ sc,
+                                                       float4* __restrict__ z4, size_t nz4) {
   const int nb = K / 32;
   const size_t blk = (size_t)blockIdx.x * 256 + threadIdx.x;
+  for (size_t k = blk; k < nz4; k += (size_t)gridDim.x * 256) z4[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   if (blk >= (size_t)Mpad * nb) return;
   const int m = (int)(blk / nb), j = (int)(blk % nb);
   const int kb = j >> 1, h = j & 1, ntile = Mpad / kI8BM;
@@ -951,15 +953,19 @@ int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M
     if (!ws) return -5;
     int8_t* q = reinterpret_cast<int8_t*>(ws);
     float* sc = reinterpret_cast<float*>(ws + qbytes);
-    const size_t nblk = (size_t)Mpad * (cols / 32);
-    k_quant_q8_gemm<<<(unsigned)((nblk + 255) / 256), 256, 0, s>>>(X, M, cols, Mpad, q, sc);
     // two int8 workgroups fit a CU (44 KB LDS, <= 256 registers): aim for ~two per CU
     const int tiles = ((rows + kBN - 1) / kBN) * ntile;
     int splits = 1;
     while (tiles * splits < 448 && nsl / (splits * 2) >= 8) splits *= 2;
-    const int per = ((nsl + splits - 1) / splits + 3) & ~3;
+    const int per = split_per(nsl, splits);
     splits = (nsl + per - 1) / per;
-    if (splits > 1) launch_zero(out, (size_t)M * rows, s);
+    // a K-split launch accumulates into a zeroed output: zero it in the prepass when it is aligned
+    const size_t nout = (size_t)M * (size_t)rows;
+    const bool fuse = splits > 1 && !(reinterpret_cast<uintptr_t>(out) & 15u) && nout % 4 == 0;
+    const size_t nblk = (size_t)Mpad * (cols / 32);
+    k_quant_q8_gemm<<<(unsigned)((nblk + 255) / 256), 256, 0, s>>>(X, M, cols, Mpad, q, sc,
+                                                                    reinterpret_cast<float4*>(out), fuse ? nout / 4 : 0);
+    if (splits > 1 && !fuse) launch_zero(out, nout, s);
     GemmGeo geo{M, rows, cols, (uint32_t)(cols / 256) * 144u, per, splits > 1 ? 1 : 0,
                 0x0F0F0F0Fu, 0xF0F0F0F0u, 0x000F000Fu, 0x00F000F0u};
     dim3 grid((rows + kBN - 1) / kBN, ntile, splits);
