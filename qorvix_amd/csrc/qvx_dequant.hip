@@ -183,10 +183,68 @@ __global__ __launch_bounds__(256) void k_dequant16x8(const uint8_t* __restrict__
   dst[g] = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+// Block types, staged: a workgroup's 2048 elements are whole blocks (2048 / QK of them, a multiple
+// of 4 bytes in every format), copied from a 4-byte-aligned source into LDS with coalesced dword
+// loads (the last partial dword of the tensor byte by byte), then each thread dequantises eight
+// consecutive elements from LDS as above.  n is a whole number of blocks.
+template <uint32_t T, int QK, int BB, bool BF>
+__global__ __launch_bounds__(256) void k_dequant16_lds(const uint8_t* __restrict__ src, uint4* __restrict__ dst,
+                                                       size_t n) {
+  constexpr int kElems = 2048, kBytes = kElems / QK * BB;
+  static_assert(kElems % QK == 0 && kBytes % 4 == 0, "workgroup span must be whole blocks and dwords");
+  __shared__ uint32_t sm[kBytes / 4];
+  const int tid = threadIdx.x;
+  const size_t e0 = (size_t)blockIdx.x * kElems, b0 = e0 / QK * BB;
+  const size_t avail = min((size_t)kBytes, n / QK * BB - b0);
+  const uint32_t* g4 = reinterpret_cast<const uint32_t*>(src + b0);
+  for (int k = tid; k < (int)(avail / 4); k += 256) sm[k] = g4[k];
+  const int full = (int)(avail & ~(size_t)3);
+  if (tid < (int)(avail & 3)) reinterpret_cast<uint8_t*>(sm)[full + tid] = src[b0 + full + tid];
+  __syncthreads();
+  const size_t i = e0 + 8 * (size_t)tid;
+  if (i >= n) return;
+  const int lb = (8 * tid) / QK, e = (8 * tid) % QK;
+  const uint8_t* b = reinterpret_cast<const uint8_t*>(sm) + lb * BB;
+  float v[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) v[k] = deq_elem<T>(b, e + k);
+  uint32_t w[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t lo = BF ? to_bf16(v[2 * j]) : __builtin_bit_cast(uint16_t, (_Float16)v[2 * j]);
+    const uint32_t hi = BF ? to_bf16(v[2 * j + 1]) : __builtin_bit_cast(uint16_t, (_Float16)v[2 * j + 1]);
+    w[j] = lo | (hi << 16);
+  }
+  dst[i / 8] = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+template <bool BF>
+bool launch_dequant16_lds(uint32_t t, const uint8_t* b, uint4* d8, size_t n, hipStream_t s) {
+  const unsigned grid = (unsigned)((n + 2047) / 2048);
+  switch (t) {
+    case T_Q8_0: k_dequant16_lds<T_Q8_0, 32, 34, BF><<<grid, 256, 0, s>>>(b, d8, n); return true;
+    case T_Q8_1: k_dequant16_lds<T_Q8_1, 32, 36, BF><<<grid, 256, 0, s>>>(b, d8, n); return true;
+    case T_Q4_0: k_dequant16_lds<T_Q4_0, 32, 18, BF><<<grid, 256, 0, s>>>(b, d8, n); return true;
+    case T_Q4_1: k_dequant16_lds<T_Q4_1, 32, 20, BF><<<grid, 256, 0, s>>>(b, d8, n); return true;
+    case T_Q5_0: k_dequant16_lds<T_Q5_0, 32, 22, BF><<<grid, 256, 0, s>>>(b, d8, n); return true;
+    case T_Q5_1: k_dequant16_lds<T_Q5_1, 32, 24, BF><<<grid, 256, 0, s>>>(b, d8, n); return true;
+    case T_Q4_K: k_dequant16_lds<T_Q4_K, 256, 144, BF><<<grid, 256, 0, s>>>(b, d8, n); return true;
+    case T_Q5_K: k_dequant16_lds<T_Q5_K, 256, 176, BF><<<grid, 256, 0, s>>>(b, d8, n); return true;
+    case T_Q6_K: k_dequant16_lds<T_Q6_K, 256, 210, BF><<<grid, 256, 0, s>>>(b, d8, n); return true;
+    default: return false;
+  }
+}
+
 template <bool BF>
 bool launch_dequant16_t(uint32_t t, const void* src, uint16_t* dst, size_t n, hipStream_t s) {
   if (n == 0) return true;
   const auto* b = static_cast<const uint8_t*>(src);
+  // block types over whole blocks: the LDS-staged kernel (source 4-byte, destination 16-byte aligned)
+  const size_t qk = (t == T_Q4_K || t == T_Q5_K || t == T_Q6_K) ? 256 : 32;
+  if (t != T_F32 && t != T_F16 && t != T_BF16 && n % qk == 0 && (reinterpret_cast<uintptr_t>(src) & 3u) == 0 &&
+      (reinterpret_cast<uintptr_t>(dst) & 15u) == 0 &&
+      launch_dequant16_lds<BF>(t, b, reinterpret_cast<uint4*>(dst), n, s))
+    return true;
   // whole groups of 8 on the vector kernel (dst 16-byte aligned; F32 sources too), the rest scalar
   const bool vec = (reinterpret_cast<uintptr_t>(dst) & 15u) == 0 &&
                    (t != T_F32 || (reinterpret_cast<uintptr_t>(src) & 15u) == 0);

@@ -423,6 +423,44 @@ def test_gemm_other_types_parity(cuda, t, variant, M, rows, cols):
     assert max_rel(out.cpu().numpy(), ref) <= GEMM_TOL
 
 
+def _round16(v32, bf16):
+    """fp32 -> fp16 or bf16 bits, round to nearest even (finite inputs)."""
+    if not bf16:
+        return v32.astype(np.float16).view(np.uint16)
+    u = v32.view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+@pytest.mark.parametrize("t", DEQUANT_GEMM_TYPES)
+@pytest.mark.parametrize("variant", [qvx.GEMM_BF16, qvx.GEMM_F16])
+@pytest.mark.parametrize("src_offset", [0, 2])
+def test_gemm_dequant16_bit_exact(cuda, t, variant, src_offset):
+    """The 16-bit weight operand of the dequantise-and-library GEMM, read back exactly: with X the
+    identity (M = cols), out[m, r] = W16[r, m] (one nonzero product per sum, exact in fp32), which must
+    equal the oracle's dequantised fp32 value rounded once to fp16 / bf16.  src_offset 2 moves the
+    blocks off 4-byte alignment (the unstaged kernel), 0 takes the LDS-staged one for block types.
+    Zeros are compared without their sign."""
+    if t == qvx.F32 and src_offset:
+        pytest.skip("fp32 weights are 4-byte values: a 2-byte offset is not a layout they come in")
+    rng = np.random.default_rng(5 * t + variant + src_offset)
+    rows, cols = 300, 512
+    w = random_weight(t, rows, cols, rng, scale=0.002)
+    raw = cuda.zeros(w.size + 16, dtype=cuda.uint8, device="cuda")
+    raw[src_offset:src_offset + w.size].copy_(cuda.from_numpy(w))
+    X = dev(cuda, np.eye(cols, dtype=np.float16).view(np.uint16))
+    out = cuda.empty((cols, rows), dtype=cuda.float32, device="cuda")
+    rc = qvx.lib().qvx_qgemm_f16(out.data_ptr(), raw.data_ptr() + src_offset, t, X.data_ptr(), cols, rows, cols,
+                                 variant, cuda.cuda.current_stream().cuda_stream)
+    assert rc == qvx.OK
+    cuda.cuda.synchronize()
+    got = out.cpu().numpy().T.copy()  # [rows, cols]
+    want16 = _round16(oracle.dequantize(t, w, rows * cols).astype(np.float32), variant == qvx.GEMM_BF16)
+    want = (want16.astype(np.uint32) << 16).view(np.float32) if variant == qvx.GEMM_BF16 else \
+        want16.view(np.float16).astype(np.float32)
+    # + 0.0: a sum that holds one -0 product and +0 products is +0, so zeros compare without sign
+    np.testing.assert_array_equal(f32bits(got.reshape(-1) + np.float32(0)), f32bits(want.reshape(-1) + np.float32(0)))
+
+
 @pytest.mark.parametrize("t", [qvx.F16, qvx.BF16, qvx.F32])
 def test_gemm_float_weights_ragged_tail(cuda, t):
     """rows * cols not a multiple of 8: the dequantiser's vector kernel takes the whole groups of 8
