@@ -344,6 +344,38 @@ def hbm_context(torch, stream, copies):
                     "bytes; context for the GEMV's HBM fraction, not part of the metric"}
 
 
+def dequant_leg(torch, stream, t, copies, reps=20):
+    """qvx_dequantize (the reference's dequantize) of one Q4_K 4096 -> 14336 weight to fp32, cycling
+    the weight copies, HIP events on the launch stream; bytes = block bytes read + 4 B written per
+    element."""
+    import qorvix_amd as qvx
+    lib, sh = qvx.lib(), stream.cuda_stream
+    n = ROWS * COLS
+    out = torch.empty(n, dtype=torch.float32, device=stream.device)
+
+    def d(i):
+        rc = lib.qvx_dequantize(t, copies[i % len(copies)].data_ptr(), out.data_ptr(), n, sh)
+        if rc != 0:
+            raise RuntimeError(f"qvx_dequantize failed: {qvx.strerror(rc)}")
+    for i in range(3):
+        d(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(reps):
+        d(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    nbytes = copies[0].numel() + 4 * n
+    gbs = nbytes / (us * 1e-6) / 1e9
+    log(f"[bench] dequantize Q4_K {ROWS}x{COLS} -> fp32: {us:.1f} us, {gbs:.0f} GB/s "
+        f"({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak)")
+    del out
+    return {"workload": f"qvx_dequantize Q4_K {ROWS}x{COLS} -> fp32", "us": round(us, 2), "bytes": nbytes,
+            "gbs": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def gemm_leg(torch, stream, t, wps, copies, steps, cpu):
     """Q4_K 4096 -> 14336 prefill GEMM at M = 2048, 512, 128 in the bf16, fp16 and
     int8 variants, each call timed whole (prepass + GEMM) with HIP events on the launch stream, and the
@@ -525,6 +557,13 @@ def main():
 
     # ---- prefill GEMM ----------------------------------------------------
     gemm = {} if args.gemv_only else gemm_leg(torch, stream, t, wps, copies, args.gemm_steps, cpu=not args.no_cpu)
+    deq = {}
+    if not args.gemv_only:
+        try:
+            deq = dequant_leg(torch, stream, t, copies)
+        except RuntimeError as e:  # report, never hide
+            deq = {"error": str(e)}
+            log(f"[bench] dequantize failed: {e}")
 
     # ---- every GEMV point of BASELINE configs[0..2] ----------------------------------------------
     cfgs = []
@@ -614,6 +653,7 @@ def main():
         "config_gemvs": cfgs,
         "sweep": sweep,
         "cpu_baseline": cpu,
+        "dequant": deq,
         "hbm_context": hbm_ctx,
     }
     print(json.dumps(result), flush=True)

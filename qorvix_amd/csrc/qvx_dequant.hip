@@ -1,8 +1,10 @@
 // qvx_dequant.hip -- GGUF block dequantisation to fp32 on gfx950, bit-exact with the reference.
 //
-// One thread per output element: each thread decodes its element from its block's bytes (block
-// headers are re-read by neighbouring threads and served from L1), so the fp32 stores of a wave
-// are one contiguous 256-byte run.  Every formula is the public ggml block definition as the
+// Whole blocks from a 4-byte-aligned source into a 16-byte-aligned output: each workgroup copies its
+// 2048 elements' blocks into LDS with coalesced dword loads, then each thread decodes eight
+// consecutive elements from LDS and stores them as 16-byte vectors.  Otherwise one thread per output
+// element decodes its element from its block's bytes in global memory (block headers re-read by
+// neighbouring threads and served from L1).  Every formula is the public ggml block definition as the
 // reference states it in runtime/src/dequant.cpp:38-210; the products are exact in fp32, so the
 // single rounding (Q4_K / Q5_K subtract, Q4_1 / Q5_1 add) gives the same value in any order.
 #include "qvx_common.hpp"
@@ -107,11 +109,67 @@ __global__ __launch_bounds__(256) void k_copy_f32(const uint32_t* __restrict__ s
   if (i < n) dst[i] = src[i];
 }
 
+constexpr int kStageElems = 2048;  // elements per workgroup of the LDS-staged kernels
+
+// Copies workgroup blockIdx.x's blocks (elements [2048 x, 2048 x + 2048) of n, whole blocks) into sm
+// with dword loads, the tensor's last partial dword byte by byte; ends with a barrier.
+template <int QK, int BB>
+__device__ inline void stage_blocks(const uint8_t* __restrict__ src, size_t n, uint32_t* sm) {
+  constexpr int kBytes = kStageElems / QK * BB;
+  static_assert(kStageElems % QK == 0 && kBytes % 4 == 0, "workgroup span must be whole blocks and dwords");
+  const int tid = threadIdx.x;
+  const size_t b0 = (size_t)blockIdx.x * kStageElems / QK * BB;
+  const size_t avail = min((size_t)kBytes, n / QK * BB - b0);
+  const uint32_t* g4 = reinterpret_cast<const uint32_t*>(src + b0);
+  for (int k = tid; k < (int)(avail / 4); k += 256) sm[k] = g4[k];
+  const int full = (int)(avail & ~(size_t)3);
+  if (tid < (int)(avail & 3)) reinterpret_cast<uint8_t*>(sm)[full + tid] = src[b0 + full + tid];
+  __syncthreads();
+}
+
+// fp32 output: dst[i] = dequant(src)[i], eight elements a thread from the staged blocks, two 16-byte
+// stores (dst 16-byte aligned).
+template <uint32_t T, int QK, int BB>
+__global__ __launch_bounds__(256) void k_dequant_lds(const uint8_t* __restrict__ src, float4* __restrict__ dst,
+                                                     size_t n) {
+  __shared__ uint32_t sm[kStageElems / QK * BB / 4];
+  stage_blocks<QK, BB>(src, n, sm);
+  const int tid = threadIdx.x;
+  const size_t i = (size_t)blockIdx.x * kStageElems + 8 * (size_t)tid;
+  if (i >= n) return;
+  const uint8_t* b = reinterpret_cast<const uint8_t*>(sm) + (8 * tid) / QK * BB;
+  const int e = (8 * tid) % QK;
+  float v[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) v[k] = deq_elem<T>(b, e + k);
+  dst[i / 4] = make_float4(v[0], v[1], v[2], v[3]);
+  dst[i / 4 + 1] = make_float4(v[4], v[5], v[6], v[7]);
+}
+
 // Host launcher: returns false for a type outside the dequantisable set.
 bool launch_dequant(uint32_t t, const void* src, float* dst, size_t n, hipStream_t s) {
   const size_t grid = (n + 255) / 256;
   if (n == 0) return true;
   const auto* b = static_cast<const uint8_t*>(src);
+  // block types over whole blocks, source 4-byte and destination 16-byte aligned: staged through LDS
+  const size_t qk = (t == T_Q4_K || t == T_Q5_K || t == T_Q6_K) ? 256 : 32;
+  if (t != T_F32 && t != T_F16 && t != T_BF16 && n % qk == 0 && (reinterpret_cast<uintptr_t>(src) & 3u) == 0 &&
+      (reinterpret_cast<uintptr_t>(dst) & 15u) == 0) {
+    const unsigned g = (unsigned)((n + kStageElems - 1) / kStageElems);
+    auto* d4 = reinterpret_cast<float4*>(dst);
+    switch (t) {
+      case T_Q8_0: k_dequant_lds<T_Q8_0, 32, 34><<<g, 256, 0, s>>>(b, d4, n); return true;
+      case T_Q8_1: k_dequant_lds<T_Q8_1, 32, 36><<<g, 256, 0, s>>>(b, d4, n); return true;
+      case T_Q4_0: k_dequant_lds<T_Q4_0, 32, 18><<<g, 256, 0, s>>>(b, d4, n); return true;
+      case T_Q4_1: k_dequant_lds<T_Q4_1, 32, 20><<<g, 256, 0, s>>>(b, d4, n); return true;
+      case T_Q5_0: k_dequant_lds<T_Q5_0, 32, 22><<<g, 256, 0, s>>>(b, d4, n); return true;
+      case T_Q5_1: k_dequant_lds<T_Q5_1, 32, 24><<<g, 256, 0, s>>>(b, d4, n); return true;
+      case T_Q4_K: k_dequant_lds<T_Q4_K, 256, 144><<<g, 256, 0, s>>>(b, d4, n); return true;
+      case T_Q5_K: k_dequant_lds<T_Q5_K, 256, 176><<<g, 256, 0, s>>>(b, d4, n); return true;
+      case T_Q6_K: k_dequant_lds<T_Q6_K, 256, 210><<<g, 256, 0, s>>>(b, d4, n); return true;
+      default: return false;
+    }
+  }
   switch (t) {
     case T_F32: k_copy_f32<<<grid, 256, 0, s>>>((const uint32_t*)src, (uint32_t*)dst, n); return true;
     case T_F16: k_dequant<T_F16, 1, 2><<<grid, 256, 0, s>>>(b, dst, n); return true;
@@ -190,21 +248,13 @@ __global__ __launch_bounds__(256) void k_dequant16x8(const uint8_t* __restrict__
 template <uint32_t T, int QK, int BB, bool BF>
 __global__ __launch_bounds__(256) void k_dequant16_lds(const uint8_t* __restrict__ src, uint4* __restrict__ dst,
                                                        size_t n) {
-  constexpr int kElems = 2048, kBytes = kElems / QK * BB;
-  static_assert(kElems % QK == 0 && kBytes % 4 == 0, "workgroup span must be whole blocks and dwords");
-  __shared__ uint32_t sm[kBytes / 4];
+  __shared__ uint32_t sm[kStageElems / QK * BB / 4];
+  stage_blocks<QK, BB>(src, n, sm);
   const int tid = threadIdx.x;
-  const size_t e0 = (size_t)blockIdx.x * kElems, b0 = e0 / QK * BB;
-  const size_t avail = min((size_t)kBytes, n / QK * BB - b0);
-  const uint32_t* g4 = reinterpret_cast<const uint32_t*>(src + b0);
-  for (int k = tid; k < (int)(avail / 4); k += 256) sm[k] = g4[k];
-  const int full = (int)(avail & ~(size_t)3);
-  if (tid < (int)(avail & 3)) reinterpret_cast<uint8_t*>(sm)[full + tid] = src[b0 + full + tid];
-  __syncthreads();
-  const size_t i = e0 + 8 * (size_t)tid;
+  const size_t i = (size_t)blockIdx.x * kStageElems + 8 * (size_t)tid;
   if (i >= n) return;
-  const int lb = (8 * tid) / QK, e = (8 * tid) % QK;
-  const uint8_t* b = reinterpret_cast<const uint8_t*>(sm) + lb * BB;
+  const uint8_t* b = reinterpret_cast<const uint8_t*>(sm) + (8 * tid) / QK * BB;
+  const int e = (8 * tid) % QK;
   float v[8];
 #pragma unroll
   for (int k = 0; k < 8; ++k) v[k] = deq_elem<T>(b, e + k);
@@ -220,7 +270,7 @@ __global__ __launch_bounds__(256) void k_dequant16_lds(const uint8_t* __restrict
 
 template <bool BF>
 bool launch_dequant16_lds(uint32_t t, const uint8_t* b, uint4* d8, size_t n, hipStream_t s) {
-  const unsigned grid = (unsigned)((n + 2047) / 2048);
+  const unsigned grid = (unsigned)((n + kStageElems - 1) / kStageElems);
   switch (t) {
     case T_Q8_0: k_dequant16_lds<T_Q8_0, 32, 34, BF><<<grid, 256, 0, s>>>(b, d8, n); return true;
     case T_Q8_1: k_dequant16_lds<T_Q8_1, 32, 36, BF><<<grid, 256, 0, s>>>(b, d8, n); return true;

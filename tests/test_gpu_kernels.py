@@ -82,6 +82,30 @@ def test_dequant_bit_exact(cuda, t):
     np.testing.assert_array_equal(f32bits(got.cpu().numpy()), f32bits(want))
 
 
+@pytest.mark.parametrize("t", [qvx.Q8_0, qvx.Q4_0, qvx.Q4_K, qvx.Q5_K, qvx.Q6_K, qvx.Q5_1])
+def test_dequant_unaligned_buffers(cuda, t):
+    """Blocks 2 bytes off 4-byte alignment and an output 4 bytes off 16-byte alignment take the
+    unstaged kernel; aligned ones the LDS-staged kernel, whose last workgroup is partial here.  Both
+    are bit-exact, and the unstaged one writes nothing outside its output."""
+    rng = np.random.default_rng(60 + t)
+    rows, cols = 9, 768
+    w = random_weight(t, rows, cols, rng)
+    n = rows * cols
+    want = f32bits(oracle.dequantize(t, w, n))
+    raw = cuda.zeros(w.size + 16, dtype=cuda.uint8, device="cuda")
+    raw[2:2 + w.size].copy_(cuda.from_numpy(w))
+    buf = cuda.full((n + 8,), 7.0, dtype=cuda.float32, device="cuda")
+    st = cuda.cuda.current_stream().cuda_stream
+    assert qvx.lib().qvx_dequantize(t, raw.data_ptr() + 2, buf.data_ptr() + 4, n, st) == qvx.OK
+    cuda.cuda.synchronize()
+    got = buf.cpu().numpy()
+    np.testing.assert_array_equal(f32bits(got[1:1 + n]), want)
+    assert got[0] == 7.0 and np.all(got[1 + n:] == 7.0)
+    aligned = qvx.dequantize_t(dev(cuda, w), t, n)
+    cuda.cuda.synchronize()
+    np.testing.assert_array_equal(f32bits(aligned.cpu().numpy()), want)
+
+
 def test_dequant_fp16_scale_edge_values(cuda):
     """Scales at fp16 extremes: subnormal, smallest normal, max, negative, zero; quants at 0/15/63."""
     t = qvx.Q4_K
