@@ -378,8 +378,85 @@ __global__ __launch_bounds__(256) void k_gemv_generic(const uint8_t* __restrict_
   if (lane == 0) Y[(size_t)v * rows + r] = acc;
 }
 
+// Runs of eight: one wave per row, up to NV vectors a pass; lane l takes the runs of eight
+// consecutive elements l, l + 64, ... (a run never crosses a block: every block size is 1 or a
+// multiple of 8), decodes each weight element once for all NV vectors, and keeps one fp32 sum per
+// vector, runs in order and elements in order within a run, then the same xor tree.  A vector's
+// arithmetic does not depend on NV or on the other vectors, so batched calls stay bit-identical to
+// single ones.  Needs cols % 8 == 0 and 16-byte-aligned activations.
+template <uint32_t T, int QK, int BB, int NV>
+__global__ __launch_bounds__(256) void k_gemv_generic8(const uint8_t* __restrict__ W, const float* __restrict__ X,
+                                                       float* __restrict__ Y, int rows, int cols, int nvec,
+                                                       size_t row_bytes) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + wave;
+  if (r >= rows) return;
+  const uint8_t* rp = W + (size_t)r * row_bytes;
+  const int nrun = cols / 8;
+  for (int v0 = 0; v0 < nvec; v0 += NV) {
+    const int nv = min(NV, nvec - v0);
+    float acc[NV];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) acc[v] = 0.0f;
+    for (int g = lane; g < nrun; g += 64) {
+      const int k = 8 * g;
+      float w[8];
+      if constexpr (T == T_F32) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) w[e] = reinterpret_cast<const float*>(rp)[k + e];
+      } else {
+        const int blk = k / QK;
+        const uint8_t* bp = rp + (size_t)blk * BB;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) w[e] = deq_elem<T>(bp + (QK == 1 ? 2 * e : 0), QK == 1 ? 0 : k - blk * QK + e);
+      }
+#pragma unroll
+      for (int v = 0; v < NV; ++v) {
+        if (v < nv) {
+          const float4* xp = reinterpret_cast<const float4*>(X + (size_t)(v0 + v) * cols + k);
+          const float4 x0 = xp[0], x1 = xp[1];
+          const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[v] = __builtin_fmaf(w[e], xs[e], acc[v]);
+        }
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      float a = acc[v];
+      for (int off = 32; off > 0; off >>= 1) a += __shfl_xor(a, off, 64);
+      if (v < nv && lane == 0) Y[(size_t)(v0 + v) * rows + r] = a;
+    }
+  }
+}
+
+template <uint32_t T, int QK, int BB>
+void launch_generic8(const uint8_t* b, const float* X, float* Y, int rows, int cols, int nvec, size_t row_bytes,
+                     hipStream_t s) {
+  k_gemv_generic8<T, QK, BB, 4><<<(unsigned)((rows + 3) / 4), 256, 0, s>>>(b, X, Y, rows, cols, nvec, row_bytes);
+}
+
 bool launch_gemv_generic(uint32_t t, const void* w, const float* X, float* Y, int rows, int cols, int nvec,
                          size_t row_bytes, hipStream_t s) {
+  const auto* b8 = static_cast<const uint8_t*>(w);
+  if (cols % 8 == 0 && (reinterpret_cast<uintptr_t>(X) & 15u) == 0 &&
+      (t != T_F32 || (reinterpret_cast<uintptr_t>(w) & 3u) == 0)) {
+    switch (t) {
+      case T_F32: launch_generic8<T_F32, 1, 4>(b8, X, Y, rows, cols, nvec, row_bytes, s); return true;
+      case T_F16: launch_generic8<T_F16, 1, 2>(b8, X, Y, rows, cols, nvec, row_bytes, s); return true;
+      case T_BF16: launch_generic8<T_BF16, 1, 2>(b8, X, Y, rows, cols, nvec, row_bytes, s); return true;
+      case T_Q8_0: launch_generic8<T_Q8_0, 32, 34>(b8, X, Y, rows, cols, nvec, row_bytes, s); return true;
+      case T_Q8_1: launch_generic8<T_Q8_1, 32, 36>(b8, X, Y, rows, cols, nvec, row_bytes, s); return true;
+      case T_Q4_0: launch_generic8<T_Q4_0, 32, 18>(b8, X, Y, rows, cols, nvec, row_bytes, s); return true;
+      case T_Q4_1: launch_generic8<T_Q4_1, 32, 20>(b8, X, Y, rows, cols, nvec, row_bytes, s); return true;
+      case T_Q5_0: launch_generic8<T_Q5_0, 32, 22>(b8, X, Y, rows, cols, nvec, row_bytes, s); return true;
+      case T_Q5_1: launch_generic8<T_Q5_1, 32, 24>(b8, X, Y, rows, cols, nvec, row_bytes, s); return true;
+      case T_Q4_K: launch_generic8<T_Q4_K, 256, 144>(b8, X, Y, rows, cols, nvec, row_bytes, s); return true;
+      case T_Q5_K: launch_generic8<T_Q5_K, 256, 176>(b8, X, Y, rows, cols, nvec, row_bytes, s); return true;
+      case T_Q6_K: launch_generic8<T_Q6_K, 256, 210>(b8, X, Y, rows, cols, nvec, row_bytes, s); return true;
+      default: return false;
+    }
+  }
   const long tasks = (long)rows * nvec;
   const unsigned grid = (unsigned)((tasks + 3) / 4);
   const auto* b = static_cast<const uint8_t*>(w);
