@@ -47,7 +47,7 @@ def algorithmic_bytes(rows, cols, m, wbytes):
     return wbytes + 4 * m * cols + 4 * m * rows
 
 
-def cpu_baseline(w_host, x_host, rows, cols, budget_s=5.0):
+def cpu_baseline(w_host, x_host, rows, cols, budget_s=10.0):
     """The reference's CPU qmatmul (oracle/_ref, else the C restatement) on this host's cores."""
     import numpy as np
     import oracle
@@ -66,7 +66,7 @@ def cpu_baseline(w_host, x_host, rows, cols, budget_s=5.0):
     fn(out, wp, 12, x_host, rows, cols)  # warm-up
     times = []
     t_end = time.perf_counter() + budget_s
-    while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 2000):
+    while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 50000):
         t0 = time.perf_counter()
         fn(out, wp, 12, x_host, rows, cols)
         times.append(time.perf_counter() - t0)
