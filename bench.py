@@ -615,7 +615,10 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "i8 MFMA, i32 accumulate, f32 fold",
+        "arithmetic": "x rounded to 15-bit fixed point per 64-element group and split into two signed bytes; "
+                      "Q4_K codes as int8; exact i32 dot products on v_mfma_i32_16x16x64_i8; each group's "
+                      "scale/min fold and the sum over groups in fp32 (max-rel error vs exact <= 1e-3)",
         "data": "synthetic (seeded Q4_K blocks: fp16 d, dmin = |N(0,1)|*1e-3, uniform scale/quant bytes; x ~ N(0,1))",
         "config": {
             "workload": "Q4_K GEMV 4096->14336, M=1 (BASELINE configs[2]); one step = one GEMV",
@@ -632,6 +635,13 @@ def main():
             "traffic": traffic,
             "kernel": GEMV_KERNEL,
             "per_launch_event_pair_us": round(pair_med, 3),
+        },
+        "isolated_call": {
+            "note": "one GEMV between its own pair of events (launch ramp and drain not overlapped with a "
+                    "neighbouring launch), median of 64",
+            "us": round(pair_med, 3),
+            "GB/s": round(nbytes / (pair_med * 1e-6) / 1e9, 1),
+            "frac": round(nbytes / (pair_med * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         },
         "gemm": {
             "workload": "Q4_K 4096->14336 GEMM, X fp16 [M,4096], fp32 out (BASELINE configs[3])",

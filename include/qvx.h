@@ -76,6 +76,10 @@ int qvx_type_traits(uint32_t type, uint32_t* block_size, uint32_t* type_size);
 /* Exact IEEE half -> single (dequant.cpp:222-248, fp16ToFloat).  Host function. */
 float qvx_fp16_to_float(uint16_t h);
 
+/* bfloat16 -> single: the 16 bits become the high half of the fp32 word (dequant.cpp:250-255,
+ * bf16ToFloat; runtime/include/qorvix/runtime/dequant.hpp:51).  Host function. */
+float qvx_bf16_to_float(uint16_t b);
+
 /* ---- device entry points (device pointers, stream-ordered) --------------------------------- */
 
 /* out[r] = dot(dequant(row r of W), x), r < rows.  Replaces qmatmul (qmatmul.cpp:28-62).
@@ -88,8 +92,9 @@ int qvx_qmatmul(float* d_out, const void* d_w, uint32_t type, const float* d_x, 
 int qvx_qmatmul_n(float* d_out, const void* d_w, uint32_t type, const float* d_X, int n_vec,
                   int rows, int cols, void* stream);
 
-/* Dequantise n elements (n a whole number of blocks) of `type` to fp32, bit-exact with the
- * reference's dequantize (dequant.cpp:277-296) for every value but NaN payloads. */
+/* Dequantise the first n / blockSize whole blocks of `type` to fp32, bit-exact with the reference's
+ * dequantize (dequant.cpp:277-296) for every value but NaN payloads.  As there, n is not required
+ * to be a whole number of blocks: the last n % blockSize outputs are left untouched. */
 int qvx_dequantize(uint32_t type, const void* d_src, float* d_dst, size_t n, void* stream);
 
 /* Dequantise row `row` (cols elements) of W.  Replaces dequantRow (qmatmul.cpp:117-126); as

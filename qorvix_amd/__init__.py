@@ -43,6 +43,7 @@ SIGNATURES = {
     "qvx_can_dequantize": ([_u32], _i32),
     "qvx_type_traits": ([_u32, C.POINTER(_u32), C.POINTER(_u32)], _i32),
     "qvx_fp16_to_float": ([C.c_uint16], _f32),
+    "qvx_bf16_to_float": ([C.c_uint16], _f32),
     "qvx_qmatmul": ([_vp, _vp, _u32, _vp, _i32, _i32, _vp], _i32),
     "qvx_qmatmul_n": ([_vp, _vp, _u32, _vp, _i32, _i32, _i32, _vp], _i32),
     "qvx_dequantize": ([_u32, _vp, _vp, _sz, _vp], _i32),
@@ -158,6 +159,11 @@ def type_traits(ggml_type: int):
 def fp16_to_float(h: int) -> float:
     """fp16ToFloat (runtime/src/dequant.cpp:222-248)."""
     return lib().qvx_fp16_to_float(h)
+
+
+def bf16_to_float(b: int) -> float:
+    """bf16ToFloat (runtime/src/dequant.cpp:250-255)."""
+    return lib().qvx_bf16_to_float(b)
 
 
 def row_bytes(ggml_type: int, cols: int) -> int:

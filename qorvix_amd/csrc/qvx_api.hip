@@ -80,6 +80,15 @@ inline int hip_status() {
   return QVX_OK;
 }
 
+// A kernel launcher declined a call that passed the argument checks: its launch could not be
+// configured (the kernel's LDS limit could not be raised, or its LDS plan would exceed the CU's
+// 160 KiB).  That is a runtime failure, not a property of the type.
+inline int refused() {
+  (void)hipGetLastError();
+  std::fprintf(stderr, "qvx: no kernel launch could be configured for this call\n");
+  return QVX_E_HIP;
+}
+
 // Shape checks shared by qmatmul / qmatmul_n / qgemm: the reference's order of tests.
 inline int check_matmul(uint32_t type, int cols, const TypeInfo** ti) {
   const TypeInfo* t = type_info(type);
@@ -127,7 +136,7 @@ int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int
       const bool ok = nv <= small ? launch_gemv_mx_q4k(w, Xv, Yv, nv, rows, cols, row_bytes, s)
                       : whole     ? launch_gemv_mxb_q4k(w, Xv, Yv, nv, rows, cols, row_bytes, s)
                                   : launch_gemv_mxj_q4k(w, Xv, Yv, nv, rows, cols, row_bytes, s);
-      if (!ok) return QVX_E_TYPE;
+      if (!ok) return refused();
     }
     return hip_status();
   }
@@ -136,7 +145,7 @@ int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int
     for (int v0 = 0; v0 < nvec; v0 += mx) {
       const int nv = nvec - v0 < mx ? nvec - v0 : mx;
       if (!launch_gemv_mx_q4k(w, X + (size_t)v0 * cols, out + (size_t)v0 * rows, nv, rows, cols, row_bytes, s))
-        return QVX_E_TYPE;
+        return refused();
     }
     return hip_status();
   }
@@ -144,7 +153,7 @@ int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int
   for (int v0 = 0; v0 < nvec; v0 += 16) {
     const int nv = nvec - v0 < 16 ? nvec - v0 : 16;
     if (!launch_gemv_generic(type, w, X + (size_t)v0 * cols, out + (size_t)v0 * rows, rows, cols, nv, row_bytes, s))
-      return QVX_E_TYPE;
+      return refused();
   }
   return hip_status();
 }
@@ -223,6 +232,8 @@ int qvx_type_traits(uint32_t type, uint32_t* block_size, uint32_t* type_size) {
 
 float qvx_fp16_to_float(uint16_t h) { return f16_bits_to_f32(h); }
 
+float qvx_bf16_to_float(uint16_t b) { return __builtin_bit_cast(float, (uint32_t)b << 16); }
+
 int qvx_qmatmul(float* d_out, const void* d_w, uint32_t type, const float* d_x, int rows, int cols, void* stream) {
   return gemv(d_out, d_w, type, d_x, 1, rows, cols, as_stream(stream));
 }
@@ -235,10 +246,12 @@ int qvx_qmatmul_n(float* d_out, const void* d_w, uint32_t type, const float* d_X
 int qvx_dequantize(uint32_t type, const void* d_src, float* d_dst, size_t n, void* stream) {
   const TypeInfo* t = type_info(type);
   if (!t || !can_dequantize(type)) return QVX_E_TYPE;
-  if (n % t->block != 0) return QVX_E_RANGE;  // the reference floors silently; this engine refuses
+  // The reference converts n / blockSize whole blocks and leaves dst[n - n % blockSize, n) as it was
+  // (dequant.cpp:38-210: every block loop runs to n / QK); the same here.
+  n -= n % t->block;
   if (n == 0) return QVX_OK;
   if (!d_src || !d_dst) return QVX_E_NULL;
-  if (!launch_dequant(type, d_src, d_dst, n, as_stream(stream))) return QVX_E_TYPE;
+  if (!launch_dequant(type, d_src, d_dst, n, as_stream(stream))) return QVX_E_HIP;
   return hip_status();
 }
 
@@ -251,7 +264,7 @@ int qvx_dequant_row(const void* d_w, uint32_t type, int cols, int row, float* d_
   if (!d_w || !d_dst) return QVX_E_NULL;
   const size_t row_bytes = (size_t)(cols / (int)t->block) * t->bytes;
   const auto* src = static_cast<const uint8_t*>(d_w) + (size_t)row * row_bytes;
-  if (!launch_dequant(type, src, d_dst, (size_t)cols, as_stream(stream))) return QVX_E_TYPE;
+  if (!launch_dequant(type, src, d_dst, (size_t)cols, as_stream(stream))) return QVX_E_HIP;
   return hip_status();
 }
 
@@ -497,7 +510,7 @@ int qvx_qmatmul_host(float* out, const void* w, uint32_t type, const float* x, i
 int qvx_dequantize_host(uint32_t type, const void* src, float* dst, size_t n) {
   const TypeInfo* t = type_info(type);
   if (!t || !can_dequantize(type)) return QVX_E_TYPE;
-  if (n % t->block != 0) return QVX_E_RANGE;
+  n -= n % t->block;  // whole blocks only, as qvx_dequantize
   if (n == 0) return QVX_OK;
   if (!src || !dst) return QVX_E_NULL;
   const size_t sb = n / t->block * t->bytes, db = n * sizeof(float);
@@ -505,7 +518,7 @@ int qvx_dequantize_host(uint32_t type, const void* src, float* dst, size_t n) {
   if (!base) return QVX_E_HIP;
   auto* ddst = reinterpret_cast<float*>(base + align_up(sb));
   if (hipMemcpy(base, src, sb, hipMemcpyHostToDevice) != hipSuccess) return hip_status();
-  if (!launch_dequant(type, base, ddst, n, nullptr)) return QVX_E_TYPE;
+  if (!launch_dequant(type, base, ddst, n, nullptr)) return QVX_E_HIP;
   if (int rc = hip_status(); rc != QVX_OK) return rc;
   if (hipMemcpy(dst, ddst, db, hipMemcpyDeviceToHost) != hipSuccess) return hip_status();
   return QVX_OK;

@@ -112,21 +112,41 @@ __device__ inline uint32_t align_bytes(uint32_t hi, uint32_t lo, uint32_t s) {
   return __builtin_amdgcn_alignbyte(hi, lo, s);
 }
 
-// Raises a kernel's dynamic-LDS limit to at least `bytes` on the current device.  The attribute
-// persists, so hipFuncSetAttribute runs only when the limit has to grow (have[] holds the limit set
-// per device; one array per kernel): a decode loop does not pay for it on every launch.
+// LDS per compute unit on gfx950: a workgroup's static plus dynamic LDS must fit in it, or the
+// dispatch fails at run time (HSA_STATUS_ERROR_INVALID_ALLOCATION) instead of at the launch call.
 constexpr int kMaxDevices = 64;
-inline void ensure_dyn_lds(const void* kern, std::atomic<int>* have, int bytes) {
+constexpr size_t kLdsPerCU = 160 * 1024;
+constexpr size_t kLdsDefaultDyn = 64 * 1024;  // dynamic LDS a kernel may take without raising its limit
+
+// Per-kernel launch state: the kernel's static LDS (read once from its code object) and the
+// dynamic-LDS limit already set on each device (the attribute persists, so hipFuncSetAttribute runs
+// only when the limit has to grow: a decode loop does not pay for it on every launch).
+struct LdsLimit {
+  std::atomic<long> stat{-1};
+  std::atomic<int> have[kMaxDevices] = {};
+};
+
+// Readies a launch of `kern` with `dyn` bytes of dynamic LDS on the current device.  Returns false,
+// and the caller launches nothing, when static + dynamic LDS would exceed the CU's 160 KiB or the
+// runtime refuses to report the kernel's attributes or to raise its dynamic limit.
+inline bool lds_ready(const void* kern, LdsLimit& lim, size_t dyn) {
+  long st = lim.stat.load(std::memory_order_relaxed);
+  if (st < 0) {
+    hipFuncAttributes a{};
+    if (hipFuncGetAttributes(&a, kern) != hipSuccess) return false;
+    st = (long)a.sharedSizeBytes;
+    lim.stat.store(st, std::memory_order_relaxed);
+  }
+  if ((size_t)st + dyn > kLdsPerCU) return false;
+  if (dyn <= kLdsDefaultDyn) return true;
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
-    (void)hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-    return;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+  int cur = lim.have[dev].load(std::memory_order_relaxed);
+  if (cur >= (int)dyn) return true;
+  if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn) != hipSuccess) return false;
+  while (cur < (int)dyn && !lim.have[dev].compare_exchange_weak(cur, (int)dyn, std::memory_order_relaxed)) {
   }
-  int cur = have[dev].load(std::memory_order_relaxed);
-  if (cur >= bytes) return;
-  if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess) return;
-  while (cur < bytes && !have[dev].compare_exchange_weak(cur, bytes, std::memory_order_relaxed)) {
-  }
+  return true;
 }
 
 // SplitMix64 finaliser (Steele, Lea, Flood 2014): a counter-based 64-bit hash for seeded data.

@@ -865,8 +865,10 @@ namespace {
 inline int split_per(int nsl, int splits) { return ((nsl + splits - 1) / splits + 3) & ~3; }
 
 template <int VAR, int BM>
-void launch_q4k(float* out, const void* w, const uint16_t* X, int M, int N, int K, int splits, bool zeroed,
+bool launch_q4k(float* out, const void* w, const uint16_t* X, int M, int N, int K, int splits, bool zeroed,
                 hipStream_t s) {
+  static LdsLimit lim;
+  if (!lds_ready(reinterpret_cast<const void*>(&k_qgemm_q4k<VAR, BM>), lim, 0)) return false;
   const int nsl = K / 64;
   const int per = split_per(nsl, splits);
   splits = (nsl + per - 1) / per;
@@ -875,6 +877,7 @@ void launch_q4k(float* out, const void* w, const uint16_t* X, int M, int N, int 
               0x0F0F0F0Fu, 0xF0F0F0F0u, 0x000F000Fu, 0x00F000F0u};
   dim3 grid((N + kBN - 1) / kBN, (M + BM - 1) / BM, splits);
   k_qgemm_q4k<VAR, BM><<<grid, 256, 0, s>>>(static_cast<const uint8_t*>(w), X, out, geo);
+  return true;
 }
 
 // Tile choice: 256-token tiles when they alone give ~one workgroup per CU; else 128-token tiles,
@@ -897,13 +900,11 @@ inline void q4k_plan(int M, int N, int K, int& bm, int& splits) {
 
 // zeroed: the caller has already zeroed the output of a K-split launch.
 template <int VAR>
-void launch_var(float* out, const void* w, const uint16_t* X, int M, int N, int K, bool zeroed, hipStream_t s) {
+bool launch_var(float* out, const void* w, const uint16_t* X, int M, int N, int K, bool zeroed, hipStream_t s) {
   int bm, splits;
   q4k_plan(M, N, K, bm, splits);
-  if (bm == 256)
-    launch_q4k<VAR, 256>(out, w, X, M, N, K, splits, zeroed, s);
-  else
-    launch_q4k<VAR, 128>(out, w, X, M, N, K, splits, zeroed, s);
+  if (bm == 256) return launch_q4k<VAR, 256>(out, w, X, M, N, K, splits, zeroed, s);
+  return launch_q4k<VAR, 128>(out, w, X, M, N, K, splits, zeroed, s);
 }
 
 }  // namespace
@@ -936,15 +937,14 @@ int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M
     k_f16_to_bf16<<<(unsigned)((n / 8 + 255) / 256), 256, 0, s>>>(
         reinterpret_cast<const uint4*>(X), static_cast<uint4*>(xb), n / 8, reinterpret_cast<float4*>(out),
         fuse ? nout / 4 : 0);
-    launch_var<VAR_BF16>(out, w, static_cast<const uint16_t*>(xb), M, rows, cols, fuse, s);
+    const bool ok = launch_var<VAR_BF16>(out, w, static_cast<const uint16_t*>(xb), M, rows, cols, fuse, s);
     gemm_temp_free(xb, s);
-    return 0;
+    return ok ? 0 : -5;
   }
-  if (variant == VAR_F16) {
-    launch_var<VAR_F16>(out, w, X, M, rows, cols, false, s);
-    return 0;
-  }
+  if (variant == VAR_F16) return launch_var<VAR_F16>(out, w, X, M, rows, cols, false, s) ? 0 : -5;
   if (variant == VAR_I8) {
+    static LdsLimit lim;
+    if (!lds_ready(reinterpret_cast<const void*>(&k_qgemm_q4k_i8), lim, 0)) return -5;
     const int ntile = (M + kI8BM - 1) / kI8BM, Mpad = ntile * kI8BM, nsl = cols / 64;
     const size_t qbytes = ((size_t)M * cols + 255) & ~(size_t)255;
     const size_t sbytes = (size_t)nsl * ntile * 4 * kI8BM * 4;

@@ -612,27 +612,26 @@ constexpr int prefetch_rows() {
 }
 
 template <uint32_t T, int NV, int RMAX, int TPT, bool CH>
-static void launch_t(const void* w, const float* X, float* Y, int rows, int cols, const Geo& geo, int nwg,
+static bool launch_t(const void* w, const float* X, float* Y, int rows, int cols, const Geo& geo, int nwg,
                      hipStream_t s) {
   constexpr int PF = prefetch_rows<T, NV>() < RMAX ? prefetch_rows<T, NV>() : RMAX;
   auto kern = &k_gemv<T, NV, RMAX, TPT, PF, CH>;
   const size_t lds = gemv_lds_bytes<T>(NV, geo.S);
-  if (lds > 64 * 1024) {
-    static std::atomic<int> have[kMaxDevices];
-    ensure_dyn_lds(reinterpret_cast<const void*>(kern), have, (int)lds);
-  }
+  static LdsLimit lim;
+  if (!lds_ready(reinterpret_cast<const void*>(kern), lim, lds)) return false;
   kern<<<(unsigned)nwg, dim3((unsigned)geo.Sp, (unsigned)geo.G), lds, s>>>(static_cast<const uint8_t*>(w), X, Y,
                                                                            rows, cols, geo);
+  return true;
 }
 
 // Rows per group RMAX (1..RM), rounded up to an instantiated value.
 template <uint32_t T, int NV, int TPT, int RM>
-static void launch_r(int rmax, const void* w, const float* X, float* Y, int rows, int cols, const Geo& geo, int nwg,
+static bool launch_r(int rmax, const void* w, const float* X, float* Y, int rows, int cols, const Geo& geo, int nwg,
                      hipStream_t s) {
   if constexpr (RM > 1) {
     if (rmax < RM) return launch_r<T, NV, TPT, RM - 1>(rmax, w, X, Y, rows, cols, geo, nwg, s);
   }
-  launch_t<T, NV, RM, TPT, false>(w, X, Y, rows, cols, geo, nwg, s);
+  return launch_t<T, NV, RM, TPT, false>(w, X, Y, rows, cols, geo, nwg, s);
 }
 
 // Most rows a group takes (its partial sums stay in registers until the end).
@@ -642,7 +641,7 @@ constexpr int max_rows() {
 }
 
 template <uint32_t T, int NV, int TPT>
-static void launch_tpt(const void* w, const float* X, float* Y, int rows, int cols, Geo geo, hipStream_t s) {
+static bool launch_tpt(const void* w, const float* X, float* Y, int rows, int cols, Geo geo, hipStream_t s) {
   constexpr int rm = max_rows<NV, TPT>();
   static_assert(rm % prefetch_rows<T, NV>() == 0, "chunks of rm rows keep the prefetch ring aligned");
   const int G = geo.G, waves = geo.Sp * G / 64;
@@ -654,11 +653,11 @@ static void launch_tpt(const void* w, const float* X, float* Y, int rows, int co
   geo.rem = (int)(rows % nwg);
   const int per_group = (geo.base + (geo.rem ? 1 : 0) + G - 1) / G;
   if (per_group <= rm) return launch_r<T, NV, TPT, rm>(per_group, w, X, Y, rows, cols, geo, (int)nwg, s);
-  launch_t<T, NV, rm, TPT, true>(w, X, Y, rows, cols, geo, (int)nwg, s);
+  return launch_t<T, NV, rm, TPT, true>(w, X, Y, rows, cols, geo, (int)nwg, s);
 }
 
 template <uint32_t T, int NV>
-static void launch_nv(const void* w, const float* X, float* Y, int rows, int cols, const Geo& geo, hipStream_t s) {
+static bool launch_nv(const void* w, const float* X, float* Y, int rows, int cols, const Geo& geo, hipStream_t s) {
   const int threads = geo.G * geo.Sp;
   const int tpt = (NV * geo.S * 2 * Lane<T>::kR + threads - 1) / threads;
   if (tpt <= 1) return launch_tpt<T, NV, 1>(w, X, Y, rows, cols, geo, s);
@@ -668,7 +667,7 @@ static void launch_nv(const void* w, const float* X, float* Y, int rows, int col
 }
 
 template <uint32_t T>
-static void launch_type(const void* w, const float* X, float* Y, int nvec, int rows, int cols, const Geo& geo,
+static bool launch_type(const void* w, const float* X, float* Y, int nvec, int rows, int cols, const Geo& geo,
                         hipStream_t s) {
   // Q6_K takes four vectors a launch when their activations fit in LDS (its 4-vector kernels
   // stay within the register file; the other formats' would spill), so the weights are streamed
@@ -680,19 +679,20 @@ static void launch_type(const void* w, const float* X, float* Y, int nvec, int r
     const int left = nvec - v0;
     if constexpr (T == T_Q6_K) {
       if (nv4 && left >= 4) {
-        launch_nv<T, 4>(w, Xv, Yv, rows, cols, geo, s);
+        if (!launch_nv<T, 4>(w, Xv, Yv, rows, cols, geo, s)) return false;
         v0 += 4;
         continue;
       }
     }
     if (left >= 2) {
-      launch_nv<T, 2>(w, Xv, Yv, rows, cols, geo, s);
+      if (!launch_nv<T, 2>(w, Xv, Yv, rows, cols, geo, s)) return false;
       v0 += 2;
     } else {
-      launch_nv<T, 1>(w, Xv, Yv, rows, cols, geo, s);
+      if (!launch_nv<T, 1>(w, Xv, Yv, rows, cols, geo, s)) return false;
       v0 += 1;
     }
   }
+  return true;
 }
 
 // Slot geometry of a row: S slots, padded group width Sp, groups per workgroup G.  Returns false
@@ -723,8 +723,7 @@ static bool launch_fast_t(const void* w, const float* X, float* Y, int nvec, int
                           hipStream_t s) {
   Geo geo{};
   if (!geometry<T>(cols, row_bytes, geo)) return false;
-  launch_type<T>(w, X, Y, nvec, rows, cols, geo, s);
-  return true;
+  return launch_type<T>(w, X, Y, nvec, rows, cols, geo, s);
 }
 
 // Fast-path GEMV for nvec >= 1 on 16-byte-aligned rows of Q8_0 / Q4_0 / Q5_0 / Q4_K / Q5_K / Q6_K.  Returns

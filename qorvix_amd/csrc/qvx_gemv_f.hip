@@ -108,15 +108,14 @@ __global__ __launch_bounds__(1024) void k_gemv_float(const uint8_t* __restrict__
 }
 
 template <uint32_t T, int NV>
-void launch_nv(const uint8_t* w, const float* X, float* Y, int rows, int cols, size_t row_bytes, hipStream_t s) {
+bool launch_nv(const uint8_t* w, const float* X, float* Y, int rows, int cols, size_t row_bytes, hipStream_t s) {
   auto kern = &k_gemv_float<T, NV>;
   const size_t lds = (size_t)NV * cols * 4;
-  if (lds > 64 * 1024) {
-    static std::atomic<int> have[kMaxDevices];
-    ensure_dyn_lds(reinterpret_cast<const void*>(kern), have, (int)lds);
-  }
+  static LdsLimit lim;
+  if (!lds_ready(reinterpret_cast<const void*>(kern), lim, lds)) return false;
   const int nwg = (int)std::min<int64_t>(kCUs, ((int64_t)rows + 15) / 16);
   kern<<<(unsigned)nwg, 1024u, lds, s>>>(w, X, Y, rows, cols, row_bytes);
+  return true;
 }
 
 template <uint32_t T>
@@ -131,13 +130,13 @@ bool launch_t(const void* w, const float* X, float* Y, int nvec, int rows, int c
     const float* Xv = X + (size_t)v0 * cols;
     float* Yv = Y + (size_t)v0 * rows;
     if (nvmax >= 4 && left >= 4) {
-      launch_nv<T, 4>(wb, Xv, Yv, rows, cols, row_bytes, s);
+      if (!launch_nv<T, 4>(wb, Xv, Yv, rows, cols, row_bytes, s)) return false;
       v0 += 4;
     } else if (nvmax >= 2 && left >= 2) {
-      launch_nv<T, 2>(wb, Xv, Yv, rows, cols, row_bytes, s);
+      if (!launch_nv<T, 2>(wb, Xv, Yv, rows, cols, row_bytes, s)) return false;
       v0 += 2;
     } else {
-      launch_nv<T, 1>(wb, Xv, Yv, rows, cols, row_bytes, s);
+      if (!launch_nv<T, 1>(wb, Xv, Yv, rows, cols, row_bytes, s)) return false;
       v0 += 1;
     }
   }

@@ -778,23 +778,24 @@ __global__ __launch_bounds__(1024) void k_gemv_mxj(const uint8_t* __restrict__ W
 }
 
 constexpr int kCUs = 256;
-constexpr size_t kLdsMax = 160 * 1024;
+constexpr size_t kLdsMax = kLdsPerCU;
 
 template <int NV, int NB, int TPT>
-static void launch_mx(const void* w, const float* X, float* Y, int rows, int cols, const MxGeo& geo, int nwg,
+static bool launch_mx(const void* w, const float* X, float* Y, int rows, int cols, const MxGeo& geo, int nwg,
                       hipStream_t s) {
   auto kern = &k_gemv_mx<NV, NB, TPT>;
   const size_t lds = mx_dyn_bytes(NV, geo.nsb);
-  static std::atomic<int> have[kMaxDevices];
-  ensure_dyn_lds(reinterpret_cast<const void*>(kern), have, (int)lds);
+  static LdsLimit lim;
+  if (!lds_ready(reinterpret_cast<const void*>(kern), lim, lds)) return false;
   kern<<<(unsigned)nwg, 1024u, lds, s>>>(static_cast<const uint8_t*>(w), X, Y, rows, cols, geo);
+  return true;
 }
 
 // Two stages per wave (two tiles in flight behind the one being folded).  Deeper rings only
 // lengthen each wave's copy issue before the fragment barrier, as issue stalls once the CU's
 // request queue is full.  TPT = activation conversion tasks per thread.
 template <int NV>
-static void launch_mx_nv(const void* w, const float* X, float* Y, int rows, int cols, const MxGeo& geo, int nwg,
+static bool launch_mx_nv(const void* w, const float* X, float* Y, int rows, int cols, const MxGeo& geo, int nwg,
                          hipStream_t s) {
   const int tpt = (NV * geo.nsb * 32 + 1023) / 1024;
   if (tpt <= 1) return launch_mx<NV, 2, 1>(w, X, Y, rows, cols, geo, nwg, s);
@@ -820,13 +821,24 @@ static int mx_geometry(int rows, int cols, size_t row_bytes, MxGeo& geo) {
 }
 
 template <int TPT>
-static void launch_mxb(const void* w, const float* X, float* Y, int nv, int rows, int cols, const MxGeo& geo, int nwg,
+static bool launch_mxb(const void* w, const float* X, float* Y, int nv, int rows, int cols, const MxGeo& geo, int nwg,
                        hipStream_t s) {
   auto kern = &k_gemv_mxb<TPT>;
   const size_t lds = mxb_dyn_bytes(geo.nsb);
-  static std::atomic<int> have[kMaxDevices];
-  ensure_dyn_lds(reinterpret_cast<const void*>(kern), have, (int)lds);
+  static LdsLimit lim;
+  if (!lds_ready(reinterpret_cast<const void*>(kern), lim, lds)) return false;
   kern<<<(unsigned)nwg, 1024u, lds, s>>>(static_cast<const uint8_t*>(w), X, Y, rows, cols, nv, geo);
+  return true;
+}
+
+template <int NVT>
+static bool launch_mxj(const uint8_t* w, const float* X, float* Y, int nv, int rows, int cols, const MxGeo& geo,
+                       int nwg, hipStream_t s) {
+  auto kern = &k_gemv_mxj<NVT>;
+  static LdsLimit lim;
+  if (!lds_ready(reinterpret_cast<const void*>(kern), lim, 0)) return false;
+  kern<<<(unsigned)nwg, 1024u, 0, s>>>(w, X, Y, rows, cols, nv, geo);
+  return true;
 }
 
 }  // namespace
@@ -846,10 +858,9 @@ bool launch_gemv_mxb_q4k(const void* w, const float* X, float* Y, int nvec, int 
   MxGeo geo{};
   const int nwg = mx_geometry(rows, cols, row_bytes, geo);
   const int tpt = (nvec * geo.nsb * 32 + 1023) / 1024;
-  if (tpt <= 1) launch_mxb<1>(w, X, Y, nvec, rows, cols, geo, nwg, s);
-  else if (tpt <= 2) launch_mxb<2>(w, X, Y, nvec, rows, cols, geo, nwg, s);
-  else launch_mxb<4>(w, X, Y, nvec, rows, cols, geo, nwg, s);
-  return true;
+  if (tpt <= 1) return launch_mxb<1>(w, X, Y, nvec, rows, cols, geo, nwg, s);
+  if (tpt <= 2) return launch_mxb<2>(w, X, Y, nvec, rows, cols, geo, nwg, s);
+  return launch_mxb<4>(w, X, Y, nvec, rows, cols, geo, nwg, s);
 }
 
 // 1 if the long-row batched form takes `cols`: whole super-blocks, and the one-vector kernel takes
@@ -866,12 +877,11 @@ bool launch_gemv_mxj_q4k(const void* w, const float* X, float* Y, int nvec, int 
   const int nwg = mx_geometry(rows, cols, row_bytes, geo);
   auto* wp = static_cast<const uint8_t*>(w);
   switch ((nvec + 1) / 2) {
-    case 1: k_gemv_mxj<1><<<(unsigned)nwg, 1024u, 0, s>>>(wp, X, Y, rows, cols, nvec, geo); break;
-    case 2: k_gemv_mxj<2><<<(unsigned)nwg, 1024u, 0, s>>>(wp, X, Y, rows, cols, nvec, geo); break;
-    case 3: k_gemv_mxj<3><<<(unsigned)nwg, 1024u, 0, s>>>(wp, X, Y, rows, cols, nvec, geo); break;
-    default: k_gemv_mxj<4><<<(unsigned)nwg, 1024u, 0, s>>>(wp, X, Y, rows, cols, nvec, geo); break;
+    case 1: return launch_mxj<1>(wp, X, Y, nvec, rows, cols, geo, nwg, s);
+    case 2: return launch_mxj<2>(wp, X, Y, nvec, rows, cols, geo, nwg, s);
+    case 3: return launch_mxj<3>(wp, X, Y, nvec, rows, cols, geo, nwg, s);
+    default: return launch_mxj<4>(wp, X, Y, nvec, rows, cols, geo, nwg, s);
   }
-  return true;
 }
 
 // Largest vector count one launch takes for a row of `cols` columns (LDS budget), 0 if the shape
@@ -893,16 +903,15 @@ bool launch_gemv_mx_q4k(const void* w, const float* X, float* Y, int nvec, int r
   MxGeo geo{};
   const int nwg = mx_geometry(rows, cols, row_bytes, geo);
   switch (nvec) {
-    case 1: launch_mx_nv<1>(w, X, Y, rows, cols, geo, nwg, s); break;
-    case 2: launch_mx_nv<2>(w, X, Y, rows, cols, geo, nwg, s); break;
-    case 3: launch_mx_nv<3>(w, X, Y, rows, cols, geo, nwg, s); break;
-    case 4: launch_mx_nv<4>(w, X, Y, rows, cols, geo, nwg, s); break;
-    case 5: launch_mx_nv<5>(w, X, Y, rows, cols, geo, nwg, s); break;
-    case 6: launch_mx_nv<6>(w, X, Y, rows, cols, geo, nwg, s); break;
-    case 7: launch_mx_nv<7>(w, X, Y, rows, cols, geo, nwg, s); break;
-    default: launch_mx_nv<8>(w, X, Y, rows, cols, geo, nwg, s); break;
+    case 1: return launch_mx_nv<1>(w, X, Y, rows, cols, geo, nwg, s);
+    case 2: return launch_mx_nv<2>(w, X, Y, rows, cols, geo, nwg, s);
+    case 3: return launch_mx_nv<3>(w, X, Y, rows, cols, geo, nwg, s);
+    case 4: return launch_mx_nv<4>(w, X, Y, rows, cols, geo, nwg, s);
+    case 5: return launch_mx_nv<5>(w, X, Y, rows, cols, geo, nwg, s);
+    case 6: return launch_mx_nv<6>(w, X, Y, rows, cols, geo, nwg, s);
+    case 7: return launch_mx_nv<7>(w, X, Y, rows, cols, geo, nwg, s);
+    default: return launch_mx_nv<8>(w, X, Y, rows, cols, geo, nwg, s);
   }
-  return true;
 }
 
 int gemv_mxj_supported(int cols) {

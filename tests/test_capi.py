@@ -106,7 +106,9 @@ def test_gemm_and_dequant_rejections():
     assert lib.qvx_qgemm_f16(FAKE, FAKE, qvx.Q6_K, FAKE, 128, 256, 300, qvx.GEMM_F16, None) == qvx.E_SHAPE
     assert lib.qvx_qgemm_f16(FAKE, FAKE, qvx.Q6_K, FAKE, 128, 0, 256, qvx.GEMM_F16, None) == qvx.OK  # no rows
     assert lib.qvx_qgemm_f16(None, FAKE, qvx.Q6_K, FAKE, 128, 4, 256, qvx.GEMM_F16, None) == qvx.E_NULL
-    assert lib.qvx_dequantize(qvx.Q4_K, FAKE, FAKE, 100, None) == qvx.E_RANGE
+    # fewer elements than one block: no whole block to convert, a successful no-op (dequant.cpp:124)
+    assert lib.qvx_dequantize(qvx.Q4_K, FAKE, FAKE, 100, None) == qvx.OK
+    assert lib.qvx_dequantize(qvx.Q4_K, None, FAKE, 300, None) == qvx.E_NULL  # one whole block
     assert lib.qvx_dequantize(10, FAKE, FAKE, 256, None) == qvx.E_TYPE
     assert lib.qvx_dequantize(qvx.Q4_K, FAKE, FAKE, 0, None) == qvx.OK
     assert lib.qvx_dequant_row(FAKE, qvx.Q8_0, 32, -1, FAKE, None) == qvx.E_RANGE
@@ -128,7 +130,22 @@ def test_host_entry_points_reject_like_reference():
     out[:] = 7
     assert lib.qvx_qmatmul_host(p(out), p(w), qvx.Q8_0, p(x), 4, 0) == qvx.OK
     assert np.all(out == 0)
-    assert lib.qvx_dequantize_host(qvx.Q4_K, p(w), p(out), 3) == qvx.E_RANGE
+    out[:] = 7  # n below one block: nothing converted, nothing written (the reference's floor)
+    assert lib.qvx_dequantize_host(qvx.Q4_K, p(w), p(out), 3) == qvx.OK
+    assert np.all(out == 7)
+    assert qvx.bf16_to_float(0x3F80) == 1.0 and qvx.bf16_to_float(0xC040) == -3.0
+
+
+def test_bf16_to_float_all_encodings():
+    """bf16ToFloat (dequant.cpp:250-255) for all 65536 encodings: the bits shifted into the high half.
+    NaN encodings only as NaN (ctypes widens the float return to a Python double, which quiets
+    signalling NaNs)."""
+    lib = qvx.lib()
+    got = np.array([lib.qvx_bf16_to_float(b) for b in range(65536)], np.float32)
+    want = (np.arange(65536, dtype=np.uint32) << 16).view(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    np.testing.assert_array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
 
 
 def test_product_has_no_cpu_fallback(monkeypatch):

@@ -106,6 +106,27 @@ def test_dequant_unaligned_buffers(cuda, t):
     np.testing.assert_array_equal(f32bits(aligned.cpu().numpy()), want)
 
 
+@pytest.mark.parametrize("t", [qvx.Q8_0, qvx.Q4_K, qvx.Q6_K])
+def test_dequant_floors_to_whole_blocks(cuda, t):
+    """n not a whole number of blocks: the reference converts n / blockSize blocks and leaves the rest
+    of dst as it was (dequant.cpp:38-210); so does qvx_dequantize, on both host and device forms."""
+    rng = np.random.default_rng(70 + t)
+    bs, _ = BLOCK[t]
+    w = random_weight(t, 3, 2 * bs, rng)
+    n = 5 * bs + bs // 2 + 1  # five whole blocks and part of a sixth
+    want = oracle.dequantize(t, w, 6 * bs)
+    buf = cuda.full((6 * bs,), 7.0, dtype=cuda.float32, device="cuda")
+    assert qvx.dequantize(t, dev(cuda, w).data_ptr(), buf.data_ptr(), n,
+                          cuda.cuda.current_stream().cuda_stream) == qvx.OK
+    cuda.cuda.synchronize()
+    got = buf.cpu().numpy()
+    np.testing.assert_array_equal(f32bits(got[:5 * bs]), f32bits(want[:5 * bs]))
+    assert np.all(got[5 * bs:] == 7.0)
+    host = np.full(6 * bs, 7.0, np.float32)
+    assert qvx.lib().qvx_dequantize_host(t, w.ctypes.data, host.ctypes.data, n) == qvx.OK
+    np.testing.assert_array_equal(f32bits(host), f32bits(got))
+
+
 def test_dequant_fp16_scale_edge_values(cuda):
     """Scales at fp16 extremes: subnormal, smallest normal, max, negative, zero; quants at 0/15/63."""
     t = qvx.Q4_K
