@@ -113,6 +113,21 @@ int qvx_dequant_row(const void* d_w, uint32_t type, int cols, int row, float* d_
 int qvx_qgemm_f16(float* d_out, const void* d_w, uint32_t type, const uint16_t* d_X, int M,
                   int rows, int cols, int variant, void* stream);
 
+/* The prefill GEMM without any device allocation: the arguments, checks, kernels and results of
+ * qvx_qgemm_f16 for the engine's own GEMM kernels, for callers that cannot allocate (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  No reference counterpart.
+ * Its temporaries (the bf16 or Q8 copy of X) live in one fixed scratch array per device, of
+ * QVX_NOALLOC_SCRATCH_BYTES, held from the first call on a device until the process ends; no call
+ * makes hipMalloc, hipFree or an allocating library call.  Limits: the weight type must be Q4_K
+ * (other types: QVX_E_TYPE, as their GEMM goes through a library that allocates); a call whose
+ * temporaries exceed the scratch -> QVX_E_RANGE (QVX_GEMM_BF16 needs 2*M*cols bytes, QVX_GEMM_I8
+ * about 1.25*M*cols; QVX_GEMM_F16 needs none).  Every call on a device shares that device's scratch:
+ * calls that overlap on one device (different streams, or host threads) race and must be ordered by
+ * the caller. */
+#define QVX_NOALLOC_SCRATCH_BYTES (64u << 20)
+int qvx_qgemm_f16_noalloc(float* d_out, const void* d_w, uint32_t type, const uint16_t* d_X, int M,
+                          int rows, int cols, int variant, void* stream);
+
 /* Per-32 Q8 activation quantiser used by QVX_GEMM_I8 (no reference counterpart): for row m and
  * block j, scale = amax/127, q = round-half-away(x * 127/amax) clamped to +-127, qsum = sum q.
  * d_q int8 [M, K], d_scale fp32 [M, K/32], d_qsum int32 [M, K/32]; K % 32 == 0. */

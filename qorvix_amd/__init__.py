@@ -49,6 +49,7 @@ SIGNATURES = {
     "qvx_dequantize": ([_u32, _vp, _vp, _sz, _vp], _i32),
     "qvx_dequant_row": ([_vp, _u32, _i32, _i32, _vp, _vp], _i32),
     "qvx_qgemm_f16": ([_vp, _vp, _u32, _vp, _i32, _i32, _i32, _i32, _vp], _i32),
+    "qvx_qgemm_f16_noalloc": ([_vp, _vp, _u32, _vp, _i32, _i32, _i32, _i32, _vp], _i32),
     "qvx_quantize_act_q8": ([_vp, _i32, _i32, _vp, _vp, _vp, _vp], _i32),
     "qvx_fill_synthetic": ([_vp, _u32, _i32, _i32, _u64, _f32, _vp], _i32),
     "qvx_fill_normal_f32": ([_vp, _sz, _u64, _f32, _vp], _i32),

@@ -39,13 +39,21 @@ void launch_fill_normal_f32(float* x, size_t n, uint64_t seed, float mul, hipStr
 void launch_fill_normal_f16(uint16_t* x, size_t n, uint64_t seed, float mul, hipStream_t s);
 void launch_read16(const void* src, size_t n16, uint32_t* flag, hipStream_t s);
 int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M, int rows, int cols,
-                 int variant, hipStream_t s);
+                 int variant, hipStream_t s, void* ws, size_t ws_cap);
 int launch_quantize_act_q8(const uint16_t* X, int M, int K, int8_t* q, float* scale, int32_t* qsum,
                            hipStream_t s);
 void launch_zero(float* p, size_t n, hipStream_t s);
 }  // namespace qvx
 
 using namespace qvx;
+
+// Scratch of qvx_qgemm_f16_noalloc: one fixed array per device, held from the library's first use
+// on that device until the process ends.  In host code `scratch` names a host-side stand-in, not the
+// device array, so kernels receive its device address, resolved once per device with
+// hipGetSymbolAddress (each device holds its own copy at its own address) and used everywhere
+// host code hands the array's memory to the device.
+constexpr size_t kScratchBytes = (size_t)QVX_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
 // A recorded GEMV sequence (include/qvx.h, qvx_plan_*).
 struct qvx_plan {
@@ -193,6 +201,26 @@ thread_local HostStage g_stage;
 
 inline size_t align_up(size_t n) { return (n + 255) & ~size_t(255); }
 
+// Device address of this device's copy of `scratch` (below), resolved once per device.
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices];
+
+// Device address of this device's scratch (the device current at the call), null on failure.
+void* scratch_ptr() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    g_scratch[dev] = p;
+  }
+  return g_scratch[dev];
+}
+
 }  // namespace
 
 #pragma GCC visibility push(default)
@@ -282,7 +310,28 @@ int qvx_qgemm_f16(float* d_out, const void* d_w, uint32_t type, const uint16_t* 
     return hip_status();
   }
   if (!d_w || !d_X) return QVX_E_NULL;
-  const int rc = launch_qgemm(d_out, d_w, type, d_X, M, rows, cols, variant, as_stream(stream));
+  const int rc = launch_qgemm(d_out, d_w, type, d_X, M, rows, cols, variant, as_stream(stream), nullptr, 0);
+  if (rc != QVX_OK) return rc;
+  return hip_status();
+}
+
+int qvx_qgemm_f16_noalloc(float* d_out, const void* d_w, uint32_t type, const uint16_t* d_X, int M, int rows,
+                          int cols, int variant, void* stream) {
+  const TypeInfo* ti = nullptr;
+  if (M <= 0) return QVX_E_NVEC;
+  if (variant != QVX_GEMM_BF16 && variant != QVX_GEMM_I8 && variant != QVX_GEMM_F16) return QVX_E_VARIANT;
+  if (int rc = check_matmul(type, cols, &ti); rc != QVX_OK) return rc;
+  if (type != T_Q4_K) return QVX_E_TYPE;  // only the engine's own GEMM kernels run without allocating
+  if (rows <= 0) return QVX_OK;
+  if (!d_out) return QVX_E_NULL;
+  if (cols <= 0) {
+    launch_zero(d_out, (size_t)rows * (size_t)M, as_stream(stream));
+    return hip_status();
+  }
+  if (!d_w || !d_X) return QVX_E_NULL;
+  void* ws = scratch_ptr();
+  if (!ws) return QVX_E_HIP;
+  const int rc = launch_qgemm(d_out, d_w, type, d_X, M, rows, cols, variant, as_stream(stream), ws, kScratchBytes);
   if (rc != QVX_OK) return rc;
   return hip_status();
 }

@@ -913,11 +913,24 @@ bool launch_var(float* out, const void* w, const uint16_t* X, int M, int N, int 
 int launch_qgemm_dequant(float* out, const void* w, uint32_t t, const uint16_t* X, int M, int rows, int cols,
                          bool bf16, hipStream_t s);
 
+// Device memory for the call's temporaries: from the library's pool when ws is null, else the
+// caller's region [ws, ws + ws_cap) (the no-allocation entry point's scratch; -7 when the call needs
+// more).  Returns the region, or null.
+static void* gemm_ws(size_t need, void* ws, size_t ws_cap, hipStream_t s) {
+  if (ws) return need <= ws_cap ? ws : nullptr;
+  return gemm_temp_alloc(need, s);
+}
+static void gemm_ws_release(void* p, void* ws, hipStream_t s) {
+  if (!ws) gemm_temp_free(p, s);
+}
+
 int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M, int rows, int cols, int variant,
-                 hipStream_t s) {
+                 hipStream_t s, void* ws, size_t ws_cap) {
+  const int no_mem = ws ? -7 : -5;  // a caller's region too small for the call / pool allocation failed
   // Weight types without a GEMM kernel of their own: dequantise to 16 bits, then a library GEMM.
   if (t != T_Q4_K) {
     if (variant == VAR_I8) return -1;
+    if (ws) return -1;  // the library GEMM allocates (its handle, the 16-bit weight): not without allocation
     if ((size_t)rows * (size_t)cols >= (1ull << 31) || (size_t)M * (size_t)cols >= (1ull << 31)) return -7;
     return launch_qgemm_dequant(out, w, t, X, M, rows, cols, variant == VAR_BF16, s);
   }
@@ -927,8 +940,8 @@ int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M
     return -7;
   if (variant == VAR_BF16) {
     const size_t n = (size_t)M * (size_t)cols;
-    void* xb = gemm_temp_alloc(n * 2u, s);
-    if (!xb) return -5;
+    void* xb = gemm_ws(n * 2u, ws, ws_cap, s);
+    if (!xb) return no_mem;
     // a K-split launch accumulates into a zeroed output: zero it in the prepass when it is aligned
     int bm, splits;
     q4k_plan(M, rows, cols, bm, splits);
@@ -938,7 +951,7 @@ int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M
         reinterpret_cast<const uint4*>(X), static_cast<uint4*>(xb), n / 8, reinterpret_cast<float4*>(out),
         fuse ? nout / 4 : 0);
     const bool ok = launch_var<VAR_BF16>(out, w, static_cast<const uint16_t*>(xb), M, rows, cols, fuse, s);
-    gemm_temp_free(xb, s);
+    gemm_ws_release(xb, ws, s);
     return ok ? 0 : -5;
   }
   if (variant == VAR_F16) return launch_var<VAR_F16>(out, w, X, M, rows, cols, false, s) ? 0 : -5;
@@ -949,10 +962,10 @@ int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M
     const size_t qbytes = ((size_t)M * cols + 255) & ~(size_t)255;
     const size_t sbytes = (size_t)nsl * ntile * 4 * kI8BM * 4;
     if ((size_t)nsl * ntile * 4 * kI8BM * 4 >= (1u << 31)) return -7;
-    uint8_t* ws = static_cast<uint8_t*>(gemm_temp_alloc(qbytes + sbytes, s));
-    if (!ws) return -5;
-    int8_t* q = reinterpret_cast<int8_t*>(ws);
-    float* sc = reinterpret_cast<float*>(ws + qbytes);
+    uint8_t* qb = static_cast<uint8_t*>(gemm_ws(qbytes + sbytes, ws, ws_cap, s));
+    if (!qb) return no_mem;
+    int8_t* q = reinterpret_cast<int8_t*>(qb);
+    float* sc = reinterpret_cast<float*>(qb + qbytes);
     // two int8 workgroups fit a CU (44 KB LDS, <= 256 registers): aim for ~two per CU
     const int tiles = ((rows + kBN - 1) / kBN) * ntile;
     int splits = 1;
@@ -970,7 +983,7 @@ int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M
                 0x0F0F0F0Fu, 0xF0F0F0F0u, 0x000F000Fu, 0x00F000F0u};
     dim3 grid((rows + kBN - 1) / kBN, ntile, splits);
     k_qgemm_q4k_i8<<<grid, 256, 0, s>>>(static_cast<const uint8_t*>(w), q, sc, out, geo);
-    gemm_temp_free(ws, s);
+    gemm_ws_release(qb, ws, s);
     return 0;
   }
   return -1;

@@ -111,6 +111,14 @@ def test_gemm_and_dequant_rejections():
     assert lib.qvx_dequantize(qvx.Q4_K, None, FAKE, 300, None) == qvx.E_NULL  # one whole block
     assert lib.qvx_dequantize(10, FAKE, FAKE, 256, None) == qvx.E_TYPE
     assert lib.qvx_dequantize(qvx.Q4_K, FAKE, FAKE, 0, None) == qvx.OK
+    # the no-allocation GEMM: the same checks, and weight types whose GEMM would allocate refused
+    assert lib.qvx_qgemm_f16_noalloc(FAKE, FAKE, qvx.Q4_K, FAKE, 128, 256, 256, 7, None) == qvx.E_VARIANT
+    assert lib.qvx_qgemm_f16_noalloc(FAKE, FAKE, qvx.Q4_K, FAKE, 0, 256, 256, 0, None) == qvx.E_NVEC
+    assert lib.qvx_qgemm_f16_noalloc(FAKE, FAKE, qvx.Q4_K, FAKE, 128, 256, 300, 0, None) == qvx.E_SHAPE
+    assert lib.qvx_qgemm_f16_noalloc(FAKE, FAKE, qvx.Q6_K, FAKE, 128, 256, 256, qvx.GEMM_F16, None) == qvx.E_TYPE
+    assert lib.qvx_qgemm_f16_noalloc(FAKE, FAKE, 10, FAKE, 128, 256, 256, qvx.GEMM_F16, None) == qvx.E_TYPE
+    assert lib.qvx_qgemm_f16_noalloc(FAKE, FAKE, qvx.Q4_K, FAKE, 128, 0, 256, qvx.GEMM_F16, None) == qvx.OK
+    assert lib.qvx_qgemm_f16_noalloc(None, FAKE, qvx.Q4_K, FAKE, 128, 4, 256, qvx.GEMM_F16, None) == qvx.E_NULL
     assert lib.qvx_dequant_row(FAKE, qvx.Q8_0, 32, -1, FAKE, None) == qvx.E_RANGE
     assert lib.qvx_dequant_row(FAKE, qvx.Q8_0, 33, 0, FAKE, None) == qvx.E_SHAPE
     assert lib.qvx_quantize_act_q8(FAKE, 4, 33, FAKE, FAKE, FAKE, None) == qvx.E_SHAPE
