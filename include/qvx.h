@@ -183,12 +183,19 @@ int qvx_plan_run_eager(const qvx_plan* plan, void* stream);
 /* Free the plan and its graph (NULL is a no-op). */
 void qvx_plan_destroy(qvx_plan* plan);
 /* ---- GGUF files: parse, locate tensors, upload ------------------------------------------- */
-/* The reference's GgufFile (gguf/include/qorvix/gguf/gguf_file.hpp:47-105): GGUF versions 1-3,
- * with the checks of its parse (gguf/src/gguf_file.cpp:95-180); where it throws GgufParseError
- * these return QVX_E_FORMAT and keep the message for qvx_gguf_last_error (per thread).  Tensor
- * dimensions are in ggml order (dims[0] is the row length, `cols`; dims[1] the row count, `rows`);
- * offsets are relative to the data section (qvx_gguf_data_offset); n_bytes is the on-disk size
- * from the type's block traits, 0 for a type id without traits. */
+/* GGUF files, in place of the reference's GgufFile (gguf/include/qorvix/gguf/gguf_file.hpp:47-105):
+ * a reader of the public GGUF container, versions 1-3, little-endian.  Malformed data returns
+ * QVX_E_FORMAT and keeps a message for qvx_gguf_last_error (per thread); a file is refused when a
+ * read would pass its end, a value type is not one of the format's 13, a tensor has more than 4
+ * dimensions, a block-quantised tensor's rows are not whole blocks, a tensor offset is not a
+ * multiple of the alignment (general.alignment, a u32 power of two, default 32), a key or tensor
+ * name appears twice, sizes overflow 64 bits, or a tensor's bytes lie outside the data section.
+ * Arrays of arrays parse (the format allows them) but their elements are not exposed.  Nothing is
+ * copied: the handle indexes the mapping (qvx_gguf_open) or the caller's buffer (qvx_gguf_parse),
+ * and values are decoded when asked for.  Tensor dimensions are in ggml order (dims[0] is the row
+ * length, `cols`; dims[1] the row count, `rows`); offsets are relative to the data section
+ * (qvx_gguf_data_offset); n_bytes is the on-disk size from the type's block traits, 0 for a type id
+ * without traits. */
 typedef struct qvx_gguf qvx_gguf;
 /* Memory-map `path` read-only and parse it (GgufFile::open, gguf_file.hpp:54-55). */
 int qvx_gguf_open(const char* path, qvx_gguf** out);
@@ -205,7 +212,7 @@ int64_t qvx_gguf_meta_count(const qvx_gguf* f);
 /* Index of the tensor named `name`, -1 if absent (tensor(), gguf_file.hpp:65). */
 int64_t qvx_gguf_find_tensor(const qvx_gguf* f, const char* name);
 /* Tensor i (GgufTensor, gguf_file.hpp:27-35): any output may be NULL; dims receives 8 values
- * (zeros past n_dims).  i out of range -> QVX_E_RANGE. */
+ * (zeros past n_dims, which is at most 4).  i out of range -> QVX_E_RANGE. */
 int qvx_gguf_tensor_info(const qvx_gguf* f, int64_t i, const char** name, uint32_t* type, uint32_t* n_dims,
                          uint64_t* dims, uint64_t* offset, uint64_t* n_elements, uint64_t* n_bytes);
 /* Host address of tensor i's bytes in the mapping / buffer, NULL when it does not carry them. */
@@ -219,10 +226,11 @@ const char* qvx_gguf_meta_key(const qvx_gguf* f, int64_t i);
 /* Value type tag of `key` (0..12 as on disk), its element type for an array (else the same tag),
  * and its element count (1 for a scalar).  Absent -> QVX_E_RANGE. */
 int qvx_gguf_meta_type(const qvx_gguf* f, const char* key, uint32_t* type, uint32_t* elem_type, uint64_t* count);
-/* Element `index` of `key` (0 for a scalar), widened as the reference's getU64 / getF64 / getBool /
- * getString do (gguf_file.hpp:74-78; gguf_types.cpp:82-120): integers and bools as u64 / i64,
- * numbers other than bools as f64.  Absent or index past the end -> QVX_E_RANGE; wrong category ->
- * QVX_E_TYPE.  A string is not NUL-terminated; *len holds its length. */
+/* Element `index` of `key` (0 for a scalar), in the categories of the reference's getU64 / getF64 /
+ * getBool / getString (gguf_file.hpp:74-78): integers and bools as u64 / i64, numbers other than
+ * bools as f64.  Absent or index past the end -> QVX_E_RANGE; wrong category (or an element of an
+ * array of arrays) -> QVX_E_TYPE.  A string points into the file and is not NUL-terminated; *len
+ * holds its length. */
 int qvx_gguf_meta_u64(const qvx_gguf* f, const char* key, uint64_t index, uint64_t* out);
 int qvx_gguf_meta_i64(const qvx_gguf* f, const char* key, uint64_t index, int64_t* out);
 int qvx_gguf_meta_f64(const qvx_gguf* f, const char* key, uint64_t index, double* out);

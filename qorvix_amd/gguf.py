@@ -167,6 +167,8 @@ class GgufFile:
 
     def _element(self, k: bytes, tag: int, i: int):
         so = lib()
+        if tag == M_ARR:  # an element of an array of arrays: the format allows them, the engine reads none
+            return None
         if tag == M_STR:
             p, n = C.c_void_p(), C.c_size_t()
             _check(so.qvx_gguf_meta_string(self._h, k, i, C.byref(p), C.byref(n)), "qvx_gguf_meta_string")

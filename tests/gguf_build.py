@@ -64,18 +64,18 @@ class GgufBuilder:
     def _scalar(self, tag, v):
         return self._string(v) if tag == STR else struct.pack(_FMT[tag], v)
 
+    def _value(self, tag, v):
+        """A value of `tag`; an array value is (element tag, items), nested arrays included."""
+        if tag != ARR:
+            return self._scalar(tag, v)
+        elem, items = v
+        return struct.pack("<I", elem) + self._len(len(items)) + b"".join(self._value(elem, it) for it in items)
+
     def header_and_tables(self):
         out = bytearray(struct.pack("<II", MAGIC, self.version))
         out += self._len(len(self.tensors)) + self._len(len(self.meta))
         for key, tag, v in self.meta:
-            out += self._string(key) + struct.pack("<I", tag)
-            if tag == ARR:
-                elem, items = v
-                out += struct.pack("<I", elem) + self._len(len(items))
-                for it in items:
-                    out += self._scalar(elem, it)
-            else:
-                out += self._scalar(tag, v)
+            out += self._string(key) + struct.pack("<I", tag) + self._value(tag, v)
         for name, dims, t, off in self.tensors:
             out += self._string(name) + struct.pack("<I", len(dims))
             for d in dims:

@@ -1,9 +1,10 @@
-"""CPU tests of the GGUF reader (qvx_gguf_*, qorvix_amd/gguf.py), mirroring the reference's own
-cases (tests/gguf_file_test.cpp): header, metadata and typed accessors, arrays, the tensor table
-with computed sizes and data offset, v1/v2 files, and every rejection -- plus file mapping and the
-data-extent check.  No GPU is touched."""
+"""CPU tests of the GGUF reader (qvx_gguf_*, qorvix_amd/gguf.py): header, metadata and typed
+accessors, arrays (nested ones included), the tensor table with computed sizes and data offset,
+v1/v2 files, file mapping, and every rejection the public format implies (the cases of the
+reference's tests/gguf_file_test.cpp among them).  No GPU is touched."""
 from __future__ import annotations
 
+import ctypes as C
 import struct
 
 import pytest
@@ -72,44 +73,85 @@ def test_older_versions_parse_identically(version):
 
 
 def test_rejects_bad_magic():
-    with pytest.raises(GgufParseError, match="bad magic"):
+    with pytest.raises(GgufParseError, match="no GGUF magic"):
         GgufFile.parse(bytes(16))
+    with pytest.raises(GgufParseError, match="big-endian"):
+        GgufFile.parse(b"FUGG" + bytes(12))
+    with pytest.raises(GgufParseError, match="no GGUF magic"):
+        GgufFile.parse(b"GG")
 
 
 def test_rejects_unsupported_version():
-    with pytest.raises(GgufParseError, match="unsupported GGUF version 99"):
+    with pytest.raises(GgufParseError, match="version 99 is not one of 1, 2, 3"):
         GgufFile.parse(GgufBuilder(99).build())
 
 
 def test_rejects_truncation_mid_metadata():
-    with pytest.raises(GgufParseError, match="truncated"):
-        GgufFile.parse(sample_model()[:40])
+    with pytest.raises(GgufParseError, match="file ends inside"):
+        GgufFile.parse(sample_model()[:150])
+    # every cut inside the header and tables is refused, never read past
+    full = sample_model()
+    for cut in range(0, 200, 7):
+        with pytest.raises(GgufParseError):
+            GgufFile.parse(full[:cut])
 
 
 def test_rejects_misaligned_tensor_offset():
     b = GgufBuilder(3).str("general.architecture", "llama").u32("general.alignment", 32)
     b.tensor("bad.weight", [32], qvx.F32, 7)
-    with pytest.raises(GgufParseError, match="not aligned"):
+    with pytest.raises(GgufParseError, match="not a multiple of the alignment"):
         GgufFile.parse(b.build())
 
 
 def test_rejects_block_size_mismatch():
     b = GgufBuilder(3).str("general.architecture", "llama")
     b.tensor("bad.weight", [100], qvx.Q4_K, 0)
-    with pytest.raises(GgufParseError, match="not a multiple of block size"):
+    with pytest.raises(GgufParseError, match="not whole blocks of 256"):
         GgufFile.parse(b.build())
+    # whole blocks in total but not per row: 100 x 256 elements with rows of 100
+    b = GgufBuilder(3)
+    b.tensor("bad.weight", [100, 256], qvx.Q4_K, 0)
+    with pytest.raises(GgufParseError, match="rows of 100 elements"):
+        GgufFile.parse(b.build(32, data_bytes=100 * 144))
 
 
-def test_rejects_nested_arrays_unknown_types_and_impossible_lengths():
-    b = GgufBuilder(3).array("a", ARR, [])
-    with pytest.raises(GgufParseError, match="nested arrays"):
-        GgufFile.parse(b.build())
-    with pytest.raises(GgufParseError, match="unknown metadata value type"):
+def test_nested_arrays_parse_and_are_skipped():
+    """The format allows arrays of arrays: they are walked (what follows them parses), reported as
+    arrays, and their elements are not exposed as scalars."""
+    b = (GgufBuilder(3).array("a", ARR, [(MU32, [1, 2, 3]), (STR, ["x", "yz"])]).array("e", ARR, [])
+         .u32("after", 7))
+    f = GgufFile.parse(b.build())
+    assert f.get_u64("after") == 7
+    assert f.find("a") == [None, None] and f.find("e") == []
+    lib = qvx.lib()
+    out = C.c_uint64()
+    assert lib.qvx_gguf_meta_u64(f._h, b"a", 0, C.byref(out)) == qvx.E_TYPE
+
+
+def test_rejects_unknown_types_and_impossible_lengths():
+    with pytest.raises(GgufParseError, match="value type 77 is not defined"):
         GgufFile.parse(_raw_kv_type(77))
     # an array that claims more elements than the buffer could hold
     head = struct.pack("<IIQQ", 0x46554747, 3, 0, 1) + struct.pack("<Q", 1) + b"k" + struct.pack("<IIQ", ARR, MU32, 1 << 40)
-    with pytest.raises(GgufParseError, match="exceeds remaining buffer"):
+    with pytest.raises(GgufParseError, match="runs past the end of the file"):
         GgufFile.parse(head)
+    head = struct.pack("<IIQQ", 0x46554747, 3, 0, 1) + struct.pack("<Q", 1) + b"k" + struct.pack("<IIQ", ARR, STR, 1 << 40)
+    with pytest.raises(GgufParseError, match="runs past the end of the file"):
+        GgufFile.parse(head)
+    # counts that cannot fit are refused before anything is reserved
+    with pytest.raises(GgufParseError, match="metadata count"):
+        GgufFile.parse(struct.pack("<IIQQ", 0x46554747, 3, 0, 1 << 60))
+    with pytest.raises(GgufParseError, match="tensor count"):
+        GgufFile.parse(struct.pack("<IIQQ", 0x46554747, 3, 1 << 60, 0))
+
+
+def test_rejects_duplicate_keys_and_tensor_names():
+    with pytest.raises(GgufParseError, match="key 'k' appears twice"):
+        GgufFile.parse(GgufBuilder(3).u32("k", 1).u32("k", 2).build())
+    b = GgufBuilder(3)
+    b.tensor("t", [32], qvx.F32, 0).tensor("t", [32], qvx.F32, 128)
+    with pytest.raises(GgufParseError, match="tensor name 't' appears twice"):
+        GgufFile.parse(b.build(32, data_bytes=256))
 
 
 def _raw_kv_type(tag):
@@ -118,25 +160,42 @@ def _raw_kv_type(tag):
 
 def test_rejects_rank_overflow_and_data_extent():
     b = GgufBuilder(3)
-    b.tensor("t", [2] * 9, qvx.F32, 0)
-    with pytest.raises(GgufParseError, match="implausible rank"):
+    b.tensor("t", [2] * 5, qvx.F32, 0)
+    with pytest.raises(GgufParseError, match="5 dimensions"):
         GgufFile.parse(b.build())
     b = GgufBuilder(3)
+    b.tensor("t", [2] * 4, qvx.F32, 0)  # four is the format's maximum
+    assert GgufFile.parse(b.build(32, data_bytes=64)).tensor("t").n_elements == 16
+    b = GgufBuilder(3)
     b.tensor("t", [1 << 40, 1 << 40], qvx.F32, 0)
-    with pytest.raises(GgufParseError, match="overflows"):
+    with pytest.raises(GgufParseError, match="does not fit in 64 bits"):
+        GgufFile.parse(b.build())
+    b = GgufBuilder(3)
+    b.tensor("t", [1 << 62, 2], qvx.F32, 0)  # elements fit, bytes do not
+    with pytest.raises(GgufParseError, match="does not fit in 64 bits"):
         GgufFile.parse(b.build())
     b = GgufBuilder(3)
     b.tensor("t", [256], qvx.F32, 0)  # 1024 bytes, but the file carries 100
-    with pytest.raises(GgufParseError, match="exceeds the tensor-data section"):
+    with pytest.raises(GgufParseError, match="outside the file's data section"):
         GgufFile.parse(b.build(32, data_bytes=100))
 
 
-def test_header_only_buffer_is_accepted():
-    # the reference checks extents only when the buffer carries a data section
+def test_data_must_be_in_the_file():
+    """A buffer that stops after the tables (or whose tensor offset points past its end) is not a
+    GGUF file: a tensor's bytes must lie in the data section."""
     b = GgufBuilder(3)
     b.tensor("t", [256], qvx.Q4_K, 0)
-    f = GgufFile.parse(b.header_and_tables())
-    assert f.tensor("t").n_bytes == 144
+    with pytest.raises(GgufParseError, match="outside the file's data section"):
+        GgufFile.parse(b.header_and_tables())
+    b = GgufBuilder(3)
+    b.tensor("t", [256], qvx.Q4_K, (1 << 64) - 32)  # aligned offset near 2^64: no wrap-around
+    with pytest.raises(GgufParseError, match="outside the file's data section"):
+        GgufFile.parse(b.build(32, data_bytes=144))
+    # a tensor of an id without known block size occupies no known bytes and is only listed
+    b = GgufBuilder(3)
+    b.tensor("odd", [32], 4, 0)
+    f = GgufFile.parse(b.build())
+    assert f.tensor("odd").n_bytes == 0
 
 
 def test_alignment_key_and_default():
@@ -144,8 +203,12 @@ def test_alignment_key_and_default():
     b.tensor("t", [16], qvx.F32, 64)
     f = GgufFile.parse(b.build(64, data_bytes=128))
     assert f.alignment == 64 and f.data_offset % 64 == 0
-    b = GgufBuilder(3).u32("general.alignment", 0)  # 0 -> the default 32
-    assert GgufFile.parse(b.build()).alignment == 32
+    assert GgufFile.parse(GgufBuilder(3).build()).alignment == 32  # default
+    for bad in (0, 48):
+        with pytest.raises(GgufParseError, match="not a power of two"):
+            GgufFile.parse(GgufBuilder(3).u32("general.alignment", bad).build())
+    with pytest.raises(GgufParseError, match="must be a u32"):
+        GgufFile.parse(GgufBuilder(3).u64("general.alignment", 32).build())
 
 
 def test_open_maps_a_file(tmp_path):
