@@ -105,11 +105,13 @@ int qvx_dequant_row(const void* d_w, uint32_t type, int cols, int row, float* d_
  * No reference counterpart (the reference prefills token by token); semantics are qmatmulN's
  * with X converted fp16 -> fp32 exactly.  variant = QVX_GEMM_BF16 | QVX_GEMM_F16 | QVX_GEMM_I8;
  * tolerance 2e-2 max-relative against the exact sum.  type: every type qvx_qmatmul takes.  Q4_K
- * runs on the engine's MFMA kernels; the other types are dequantised into a stream-ordered 16-bit
- * temporary (fp16, bf16 for QVX_GEMM_BF16) and multiplied by one rocBLAS gemm_ex (fp32 accumulate),
- * rocBLAS being loaded on first use (QVX_E_LIB when it is missing or fails; these calls create a
- * rocBLAS handle per host thread and device on first use, so they are not for graph capture).
- * QVX_GEMM_I8 takes Q4_K only (other types: QVX_E_TYPE). */
+ * runs on the engine's raw-block MFMA kernels; Q6_K (cols a multiple of 64, X 16-byte and W 4-byte
+ * aligned) on its dequantising MFMA kernel, each weight element rounded once from its exact value
+ * to fp16 / bf16.  Other types, and Q6_K calls that kernel declines, are dequantised into a
+ * stream-ordered 16-bit temporary (fp16, bf16 for QVX_GEMM_BF16) and multiplied by one rocBLAS
+ * gemm_ex (fp32 accumulate), rocBLAS being loaded on first use (QVX_E_LIB when it is missing or
+ * fails; these calls create a rocBLAS handle per host thread and device on first use, so they are
+ * not for graph capture).  QVX_GEMM_I8 takes Q4_K only (other types: QVX_E_TYPE). */
 int qvx_qgemm_f16(float* d_out, const void* d_w, uint32_t type, const uint16_t* d_X, int M,
                   int rows, int cols, int variant, void* stream);
 
@@ -118,8 +120,9 @@ int qvx_qgemm_f16(float* d_out, const void* d_w, uint32_t type, const uint16_t* 
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  No reference counterpart.
  * Its temporaries (the bf16 or Q8 copy of X) live in one fixed scratch array per device, of
  * QVX_NOALLOC_SCRATCH_BYTES, held from the first call on a device until the process ends; no call
- * makes hipMalloc, hipFree or an allocating library call.  Limits: the weight type must be Q4_K
- * (other types: QVX_E_TYPE, as their GEMM goes through a library that allocates); a call whose
+ * makes hipMalloc, hipFree or an allocating library call.  Limits: the weight type must be Q4_K,
+ * or Q6_K with cols a multiple of 64, X 16-byte and W 4-byte aligned, and not QVX_GEMM_I8 (other
+ * calls: QVX_E_TYPE, as their GEMM goes through a library that allocates); a call whose
  * temporaries exceed the scratch -> QVX_E_RANGE (QVX_GEMM_BF16 needs 2*M*cols bytes, QVX_GEMM_I8
  * about 1.25*M*cols; QVX_GEMM_F16 needs none).  Every call on a device shares that device's scratch:
  * calls that overlap on one device (different streams, or host threads) race and must be ordered by

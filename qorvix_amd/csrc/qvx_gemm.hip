@@ -912,6 +912,11 @@ bool launch_var(float* out, const void* w, const uint16_t* X, int M, int N, int 
 // Returns a QVX status (0 ok, -1 type, -5 HIP, -7 range).
 int launch_qgemm_dequant(float* out, const void* w, uint32_t t, const uint16_t* X, int M, int rows, int cols,
                          bool bf16, hipStream_t s);
+// The dequantising MFMA GEMM of the other weight types (qvx_gemm_deq.hip).
+bool qgemm_deq_supported(uint32_t t, const void* w, const uint16_t* X, int K, size_t row_bytes);
+bool qgemm_deq_splits(int M, int N, int K);
+bool launch_qgemm_deq(uint32_t t, float* out, const void* w, const uint16_t* X, int M, int N, int K, size_t row_bytes,
+                      bool bf16, bool zeroed, hipStream_t s);
 
 // Device memory for the call's temporaries: from the library's pool when ws is null, else the
 // caller's region [ws, ws + ws_cap) (the no-allocation entry point's scratch; -7 when the call needs
@@ -927,10 +932,32 @@ static void gemm_ws_release(void* p, void* ws, hipStream_t s) {
 int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M, int rows, int cols, int variant,
                  hipStream_t s, void* ws, size_t ws_cap) {
   const int no_mem = ws ? -7 : -5;  // a caller's region too small for the call / pool allocation failed
-  // Weight types without a GEMM kernel of their own: dequantise to 16 bits, then a library GEMM.
   if (t != T_Q4_K) {
     if (variant == VAR_I8) return -1;
-    if (ws) return -1;  // the library GEMM allocates (its handle, the 16-bit weight): not without allocation
+    const TypeInfo* ti = type_info(t);
+    if (!ti) return -1;
+    const size_t row_bytes = (size_t)(cols / (int)ti->block) * ti->bytes;
+    // The other weight types: their rows dequantised into the MFMA tiles (cols % 64 == 0, aligned
+    // operands) ...
+    if (qgemm_deq_supported(t, w, X, cols, row_bytes)) {
+      if (variant == VAR_F16)
+        return launch_qgemm_deq(t, out, w, X, M, rows, cols, row_bytes, false, false, s) ? 0 : -5;
+      const size_t n = (size_t)M * (size_t)cols;
+      void* xb = gemm_ws(n * 2u, ws, ws_cap, s);
+      if (!xb) return no_mem;
+      const size_t nout = (size_t)M * (size_t)rows;
+      const bool fuse = qgemm_deq_splits(M, rows, cols) && !(reinterpret_cast<uintptr_t>(out) & 15u) && nout % 4 == 0;
+      k_f16_to_bf16<<<(unsigned)((n / 8 + 255) / 256), 256, 0, s>>>(
+          reinterpret_cast<const uint4*>(X), static_cast<uint4*>(xb), n / 8, reinterpret_cast<float4*>(out),
+          fuse ? nout / 4 : 0);
+      const bool ok =
+          launch_qgemm_deq(t, out, w, static_cast<const uint16_t*>(xb), M, rows, cols, row_bytes, true, fuse, s);
+      gemm_ws_release(xb, ws, s);
+      return ok ? 0 : -5;
+    }
+    // ... else dequantised whole to 16 bits, then a library GEMM, which allocates (its handle, the
+    // 16-bit weight): not for the no-allocation entry point.
+    if (ws) return -1;
     if ((size_t)rows * (size_t)cols >= (1ull << 31) || (size_t)M * (size_t)cols >= (1ull << 31)) return -7;
     return launch_qgemm_dequant(out, w, t, X, M, rows, cols, variant == VAR_BF16, s);
   }

@@ -287,24 +287,27 @@ class DecodeStep:
         self.plan.run_eager(stream)
 
 
-def wgemm(out, w: DevWeight, X16, m: int, stream: int, variant: int = GEMM_F16) -> None:
-    """out[m, rows] = X16[m, cols] W^T with X in fp16: the prefill GEMM (``qvx_qgemm_f16``)."""
-    rc = lib().qvx_qgemm_f16(out.data_ptr(), w.data.data_ptr(), w.type, X16.data_ptr(), m, w.rows, w.cols, variant,
-                             stream)
+def wgemm(out, w: DevWeight, X16, m: int, stream: int, variant: int = GEMM_F16, noalloc: bool = False) -> None:
+    """out[m, rows] = X16[m, cols] W^T with X in fp16: the prefill GEMM (``qvx_qgemm_f16``, or
+    ``qvx_qgemm_f16_noalloc`` when ``noalloc``: no device allocation, for graph capture)."""
+    name = "qvx_qgemm_f16_noalloc" if noalloc else "qvx_qgemm_f16"
+    rc = getattr(lib(), name)(out.data_ptr(), w.data.data_ptr(), w.type, X16.data_ptr(), m, w.rows, w.cols, variant,
+                              stream)
     if rc != OK:
-        raise QvxError(rc, "qvx_qgemm_f16")
+        raise QvxError(rc, name)
 
 
 class PrefillStep:
     """The weight side of a prompt prefill of M positions, batched.  The reference prefills token
     by token, one ``forward`` per prompt position (``runtime/src/generator.cpp:24-28``), each
     running the decoder's seven projections per layer; here every projection of a layer takes all M
-    positions at once as one GEMM (``qvx_qgemm_f16``: Q4_K on the engine's MFMA kernels, the Q6_K
-    tensors dequantised to fp16 for a library GEMM), and the LM head runs on the last position only,
-    as the reference keeps only the logits after the last prompt token.  Activations are seeded fp16
-    stand-ins (norms, RoPE, attention and SwiGLU are outside the engine); one output buffer per
-    projection name is reused across layers.  Calls are issued eagerly: the library GEMM path creates
-    its handle on first use and is not for graph capture."""
+    positions at once as one GEMM (``qvx_qgemm_f16``: Q4_K on the engine's raw-block MFMA kernels,
+    the Q6_K tensors on its dequantising MFMA kernel), and the LM head runs on the last position
+    only, as the reference keeps only the logits after the last prompt token.  Activations are
+    seeded fp16 stand-ins (norms, RoPE, attention and SwiGLU are outside the engine); one output
+    buffer per projection name is reused across layers.  ``run`` issues the calls eagerly;
+    ``capture`` records them into one graph through the no-allocation entry point and ``replay``
+    launches it."""
 
     def __init__(self, model: Model, m: int, seed: int = 11, device="cuda", variant: int = GEMM_F16):
         import torch
@@ -328,9 +331,23 @@ class PrefillStep:
             n += 2 * self.model.lm_head.rows * self.model.lm_head.cols
         return n
 
-    def run(self, stream: int) -> None:
+    def run(self, stream: int, noalloc: bool = False) -> None:
         for _, name, w, src in self.calls:
-            wgemm(self.outputs[name], w, self.inputs[src], self.m, stream, self.variant)
+            wgemm(self.outputs[name], w, self.inputs[src], self.m, stream, self.variant, noalloc)
         if self.model.lm_head is not None:
             wmatmul_n(self.logits, self.model.lm_head, self.last, 1, stream)
+
+    def capture(self) -> None:
+        """Record the step into a graph (``torch.cuda.CUDAGraph``), every GEMM through
+        ``qvx_qgemm_f16_noalloc``.  One eager run first sets up the kernels' launch configuration
+        and the device's scratch array outside the capture."""
+        import torch
+        self.run(torch.cuda.current_stream().cuda_stream, noalloc=True)
+        torch.cuda.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.run(torch.cuda.current_stream().cuda_stream, noalloc=True)
+
+    def replay(self) -> None:
+        self.graph.replay()
 

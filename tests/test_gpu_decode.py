@@ -89,9 +89,9 @@ def test_plan_state_and_argument_errors(cuda):
 @pytest.mark.parametrize("m", [16, 130])
 def test_prefill_outputs_match_oracle(cuda, small_model, m):
     """The batched prefill: every projection of the last layer (the outputs are reused across layers)
-    within the GEMM tolerance of the oracle on a slice of rows, the Q4_K ones on the MFMA kernel and
-    the Q6_K ones through the dequantising library GEMM; the LM head on the last position within the
-    GEMV tolerance."""
+    within the GEMM tolerance of the oracle on a slice of rows, the Q4_K ones on the raw-block MFMA
+    kernel and the Q6_K ones on the dequantising MFMA kernel; the LM head on the last position within
+    the GEMV tolerance."""
     torch = cuda
     step = decode.PrefillStep(small_model, m, seed=m)
     step.run(torch.cuda.current_stream().cuda_stream)
@@ -114,6 +114,33 @@ def test_prefill_outputs_match_oracle(cuda, small_model, m):
     assert max_rel(step.logits[:, :64].cpu().numpy(), ref) <= 1e-3
     assert step.flops() == 2 * m * sum(w.rows * w.cols for l in small_model.layers for w in l.values()) + \
         2 * head.rows * head.cols
+
+
+@pytest.mark.parametrize("variant", [qvx.GEMM_F16, qvx.GEMM_BF16])
+def test_prefill_graph_replays_match_eager(cuda, small_model, variant):
+    """The whole prefill step (Q4_K and Q6_K GEMMs, the LM head GEMV) captured into one graph:
+    every replay, with other work and synchronisations between them, agrees with the eager run.
+    Split-K launches add their partial sums with fp32 atomics in whatever order they land, so the
+    bar is 1e-5 relative, not bit identity (a dropped or doubled split moves outputs by ~10%)."""
+    torch = cuda
+    step = decode.PrefillStep(small_model, 130, seed=17, variant=variant)
+    s = torch.cuda.current_stream().cuda_stream
+    step.run(s)
+    torch.cuda.synchronize()
+    ref = {k: v.clone() for k, v in step.outputs.items()}
+    ref_logits = step.logits.clone()
+    step.capture()
+    for rep in range(3):
+        for v in step.outputs.values():
+            v.fill_(float("nan"))
+        step.logits.fill_(float("nan"))
+        noise = torch.randn(1 << 20, device="cuda")  # eager work between replays
+        float(noise.sum())
+        step.replay()
+        torch.cuda.synchronize()
+        for k, v in step.outputs.items():
+            assert max_rel(v.cpu().numpy(), ref[k].cpu().numpy()) <= 1e-5, (rep, k)
+        assert torch.equal(step.logits.view(torch.int32), ref_logits.view(torch.int32)), rep
 
 
 @pytest.mark.parametrize("m", [1, 8])

@@ -455,10 +455,13 @@ DEQUANT_GEMM_TYPES = [qvx.Q6_K, qvx.Q8_0, qvx.Q4_0, qvx.Q5_0, qvx.Q5_K, qvx.Q4_1
 
 @pytest.mark.parametrize("t", DEQUANT_GEMM_TYPES)
 @pytest.mark.parametrize("variant", [qvx.GEMM_BF16, qvx.GEMM_F16])
-@pytest.mark.parametrize("M,rows,cols", [(128, 512, 1024), (37, 300, 256)])
+@pytest.mark.parametrize("M,rows,cols", [(128, 512, 1024), (37, 300, 256), (37, 300, 2304)])
 def test_gemm_other_types_parity(cuda, t, variant, M, rows, cols):
-    """Weight types without a GEMM kernel of their own (dequantised to 16 bits, then a library GEMM):
-    within the GEMM tolerance of the fp64 oracle."""
+    """The weight types other than Q4_K (Q6_K on the dequantising MFMA GEMM, the rest dequantised to
+    16 bits for the library GEMM), within the GEMM tolerance of the fp64 oracle: 128 x 512 x 1024
+    takes two K splits of 8 slices, 37 x 300 x 256 one range of 4 slices with a ragged tile in both M
+    and N, and 37 x 300 x 2304 four splits of 9 slices (an odd range: its last slice runs outside
+    the MFMA kernel's two-slice loop)."""
     rng = np.random.default_rng(M + rows + cols + 3 * t + variant)
     w = random_weight(t, rows, cols, rng, scale=0.002)
     X16 = (rng.standard_normal((M, cols)) * 0.5).astype(np.float16)
@@ -466,6 +469,21 @@ def test_gemm_other_types_parity(cuda, t, variant, M, rows, cols):
     cuda.cuda.synchronize()
     ref = oracle.matmul_f64(w, t, X16.astype(np.float32), M, rows, cols)
     assert max_rel(out.cpu().numpy(), ref) <= GEMM_TOL
+
+
+@pytest.mark.parametrize("t", [qvx.Q8_0, qvx.Q4_0, qvx.Q5_1])
+def test_gemm_32_blocks_odd_slices(cuda, t):
+    """32-element block types at cols = 320 and cols = 96 (not a multiple of 64), against the
+    oracle."""
+    rng = np.random.default_rng(70 + t)
+    for M, rows, cols in ((45, 260, 320), (9, 40, 96)):
+        w = random_weight(t, rows, cols, rng, scale=0.002)
+        X16 = (rng.standard_normal((M, cols)) * 0.5).astype(np.float16)
+        ref = oracle.matmul_f64(w, t, X16.astype(np.float32), M, rows, cols)
+        for variant in (qvx.GEMM_BF16, qvx.GEMM_F16):
+            out = qvx.qgemm_t(dev(cuda, w), t, dev(cuda, X16.view(np.uint16)), rows, cols, variant)
+            cuda.cuda.synchronize()
+            assert max_rel(out.cpu().numpy(), ref) <= GEMM_TOL, (M, rows, cols, variant)
 
 
 def _round16(v32, bf16):
@@ -480,11 +498,13 @@ def _round16(v32, bf16):
 @pytest.mark.parametrize("variant", [qvx.GEMM_BF16, qvx.GEMM_F16])
 @pytest.mark.parametrize("src_offset", [0, 2])
 def test_gemm_dequant16_bit_exact(cuda, t, variant, src_offset):
-    """The 16-bit weight operand of the dequantise-and-library GEMM, read back exactly: with X the
-    identity (M = cols), out[m, r] = W16[r, m] (one nonzero product per sum, exact in fp32), which must
-    equal the oracle's dequantised fp32 value rounded once to fp16 / bf16.  src_offset 2 moves the
-    blocks off 4-byte alignment (the unstaged kernel), 0 takes the LDS-staged one for block types.
-    Zeros are compared without their sign."""
+    """The 16-bit weight operand of the GEMM, read back exactly: with X the identity (M = cols),
+    out[m, r] = W16[r, m] (one nonzero product per sum, exact in fp32), which must equal the oracle's
+    dequantised fp32 value rounded once to fp16 / bf16.  src_offset 0 runs the dequantising MFMA
+    kernel (every weight element of the 300 x 512 matrix passes through its LDS B tile); 2 moves the
+    blocks off 4-byte alignment, which that kernel declines, so the dequantise-and-library fallback
+    (its unstaged dequantiser) runs; the other types always take that fallback.  Zeros are compared
+    without their sign."""
     if t == qvx.F32 and src_offset:
         pytest.skip("fp32 weights are 4-byte values: a 2-byte offset is not a layout they come in")
     rng = np.random.default_rng(5 * t + variant + src_offset)
@@ -522,8 +542,8 @@ def test_gemm_float_weights_ragged_tail(cuda, t):
 
 
 def test_gemm_q6k_ffn_down_shape(cuda):
-    """The Q4_K_M model's Q6_K ffn_down (14336 -> 4096) at M = 64 through the dequantising path, and
-    the int8 variant refused for it."""
+    """The Q4_K_M model's Q6_K ffn_down (14336 -> 4096) at M = 64 (16 K splits of 14 slices) on the
+    dequantising MFMA kernel, and the int8 variant refused for it."""
     t, M, rows, cols = qvx.Q6_K, 64, 4096, 14336
     W = qvx.empty_weight(t, rows, cols)
     qvx.fill_synthetic_t(W, t, rows, cols, seed=41, scale_mul=1e-3)
