@@ -38,7 +38,7 @@ bool launch_fill_synthetic(void* w, uint32_t t, size_t nblk, uint64_t seed, floa
 void launch_fill_normal_f32(float* x, size_t n, uint64_t seed, float mul, hipStream_t s);
 void launch_fill_normal_f16(uint16_t* x, size_t n, uint64_t seed, float mul, hipStream_t s);
 void launch_read16(const void* src, size_t n16, uint32_t* flag, hipStream_t s);
-bool qgemm_deq_supported(uint32_t t, const void* w, const uint16_t* X, int K, size_t row_bytes);
+bool qgemm_deq_supported(uint32_t t, const void* w, const uint16_t* X, int K, int N, size_t row_bytes);
 int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M, int rows, int cols,
                  int variant, hipStream_t s, void* ws, size_t ws_cap);
 int launch_quantize_act_q8(const uint16_t* X, int M, int K, int8_t* q, float* scale, int32_t* qsum,
@@ -333,7 +333,7 @@ int qvx_qgemm_f16_noalloc(float* d_out, const void* d_w, uint32_t type, const ui
   // the other weight types run without allocating only on the dequantising MFMA kernel (cols a
   // multiple of 64, X 16-byte and W 4-byte aligned); their fallback GEMM allocates
   if (type != T_Q4_K &&
-      !qgemm_deq_supported(type, d_w, d_X, cols, (size_t)(cols / (int)ti->block) * ti->bytes))
+      !qgemm_deq_supported(type, d_w, d_X, cols, rows, (size_t)(cols / (int)ti->block) * ti->bytes))
     return QVX_E_TYPE;
   void* ws = scratch_ptr();
   if (!ws) return QVX_E_HIP;

@@ -913,7 +913,7 @@ bool launch_var(float* out, const void* w, const uint16_t* X, int M, int N, int 
 int launch_qgemm_dequant(float* out, const void* w, uint32_t t, const uint16_t* X, int M, int rows, int cols,
                          bool bf16, hipStream_t s);
 // The dequantising MFMA GEMM of the other weight types (qvx_gemm_deq.hip).
-bool qgemm_deq_supported(uint32_t t, const void* w, const uint16_t* X, int K, size_t row_bytes);
+bool qgemm_deq_supported(uint32_t t, const void* w, const uint16_t* X, int K, int N, size_t row_bytes);
 bool qgemm_deq_splits(int M, int N, int K);
 bool launch_qgemm_deq(uint32_t t, float* out, const void* w, const uint16_t* X, int M, int N, int K, size_t row_bytes,
                       bool bf16, bool zeroed, hipStream_t s);
@@ -939,7 +939,7 @@ int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M
     const size_t row_bytes = (size_t)(cols / (int)ti->block) * ti->bytes;
     // The other weight types: their rows dequantised into the MFMA tiles (cols % 64 == 0, aligned
     // operands) ...
-    if (qgemm_deq_supported(t, w, X, cols, row_bytes)) {
+    if (qgemm_deq_supported(t, w, X, cols, rows, row_bytes)) {
       if (variant == VAR_F16)
         return launch_qgemm_deq(t, out, w, X, M, rows, cols, row_bytes, false, false, s) ? 0 : -5;
       const size_t n = (size_t)M * (size_t)cols;
