@@ -166,9 +166,7 @@ __device__ inline void q6k_prepare(const u32x4 (&rw)[8], uint32_t s, Q6Row& q) {
   const uint32_t scw = E ? align_bytes(q.w[28], q.w[27], s) : align_bytes(q.w[27], q.w[26], s);
   // d by the hardware conversion (exact for every finite fp16; a NaN d stays NaN)
   const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)((q.w[29] >> (8u * s)) & 0xFFFFu));
-  // the signed sub-scales through their unsigned bytes (exact): hipcc for gfx950 folds a
-  // sign-extended byte converted to float into v_cvt_f32_u32 with an SDWA sext source, which turns
-  // every negative scale into ~4.3e9
+  // the signed sub-scales through their unsigned bytes (exact; v_cvt_f32_ubyte<k>)
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const float sb = (float)((scw >> (8u * (uint32_t)k)) & 0xFFu);
