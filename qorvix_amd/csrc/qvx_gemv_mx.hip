@@ -198,6 +198,19 @@ __device__ inline void mx_convert(const float4 x0, const float4 x1, int v, int s
   }
 }
 
+// Step u of a K-split wave -> super-block.  Even waves of a split walk their range backwards, odd
+// waves forwards: a 128-byte line that straddles two waves' ranges (super-blocks are 144 bytes, so
+// most split points fall inside a line) is then requested by both waves at the same moment -- at
+// the start of both walks or at the end of both -- and fetched from HBM once, instead of once at
+// the start of one walk and again, long evicted from L2, at the end of the other.  All three forms
+// (one-vector, batched, long-row batched) walk the same order, so their folds stay identical.
+struct SbOrder {
+  int base, step;
+  __device__ SbOrder(int kq, int KQ, int s0, int s1)
+      : base(KQ > 1 && !(kq & 1) ? s1 - 1 : s0), step(KQ > 1 && !(kq & 1) ? -1 : 1) {}
+  __device__ int operator()(int u) const { return base + step * u; }
+};
+
 // Copy a tile (16 rows of this wave, super-block s) into an LDS stage: 2 x 1024 + 256 bytes.
 __device__ inline void mx_issue(__amdgpu_buffer_rsrc_t rsrc, const uint32_t (&off)[3], int s, QVX_LDS uint8_t* st) {
   const uint32_t so = (uint32_t)s * kSB;
@@ -224,6 +237,7 @@ __global__ __launch_bounds__(1024) void k_gemv_mx(const uint8_t* __restrict__ W,
   const int rb = b * geo.base + min(b, geo.rem), cnt = geo.base + (b < geo.rem ? 1 : 0);
   const int tq = wave % TQ, kq = wave / TQ;
   const int s0 = kq * nsb / KQ, s1 = (kq + 1) * nsb / KQ, nu = s1 - s0;
+  const SbOrder order(kq, KQ, s0, s1);
 
   // 1. activation loads (waves that hold conversion tasks), then 2. the prologue tile copies, then
   // 3. the conversion into A fragments.  The activation loads go first: a wave's vector memory
@@ -256,9 +270,8 @@ __global__ __launch_bounds__(1024) void k_gemv_mx(const uint8_t* __restrict__ W,
     const uint32_t r = p / (uint32_t)kSB, c = p - (uint32_t)kSB * r;
     off[k] = __umul24(16u * (uint32_t)tq + r, geo.row_bytes) + c;
   }
-  const int s_last = max(s0, s1 - 1);  // < nsb: s0 < nsb for every wave
 #pragma unroll
-  for (int u = 0; u < NB; ++u) mx_issue(rsrc, off, min(s0 + u, s_last), stage + u * kTileBytes);
+  for (int u = 0; u < NB; ++u) mx_issue(rsrc, off, nu > 0 ? order(min(u, nu - 1)) : s0, stage + u * kTileBytes);
 
 #pragma unroll
   for (int k = 0; k < TPT; ++k) {
@@ -304,12 +317,12 @@ __global__ __launch_bounds__(1024) void k_gemv_mx(const uint8_t* __restrict__ W,
     else if (ahead == 2) wait_vm<6>();
     else if (ahead == 1) wait_vm<3>();
     else wait_vm<0>();
-    const int s = s0 + u;
+    const int s = order(u);
     const uint32_t st = stage_base + (uint32_t)slot * kTileBytes;
     u32x4 hd = lds_read16(st + b_hd), q0 = lds_read16(st + b_q), q1 = lds_read16<16>(st + b_q);
     lds_wait(hd, q0, q1);
     // the stage is in registers: refill it with the tile NB super-blocks on
-    if (u + NB < nu) mx_issue(rsrc, off, s + NB, stage + slot * kTileBytes);
+    if (u + NB < nu) mx_issue(rsrc, off, order(u + NB), stage + slot * kTileBytes);
     slot = slot + 1 == NB ? 0 : slot + 1;
     v4i bm[4];
 #pragma unroll
@@ -502,6 +515,7 @@ __global__ __launch_bounds__(1024) void k_gemv_mxb(const uint8_t* __restrict__ W
   const int rb = b * geo.base + min(b, geo.rem), cnt = geo.base + (b < geo.rem ? 1 : 0);
   const int tq = wave % TQ, kq = wave / TQ;
   const int s0 = kq * nsb / KQ, s1 = (kq + 1) * nsb / KQ, nu = s1 - s0;
+  const SbOrder order(kq, KQ, s0, s1);
 
   // 1. activations -> A fragments (waves with conversion tasks), before any copy.  Every round's
   // loads are issued before the first conversion: the fragment stores (inline asm with a memory
@@ -536,9 +550,8 @@ __global__ __launch_bounds__(1024) void k_gemv_mxb(const uint8_t* __restrict__ W
     const uint32_t r = p / (uint32_t)kSB, c = p - (uint32_t)kSB * r;
     off[k] = __umul24(16u * (uint32_t)tq + r, geo.row_bytes) + c;
   }
-  const int s_last = max(s0, s1 - 1);
 #pragma unroll
-  for (int u = 0; u < NB; ++u) mx_issue(rsrc, off, min(s0 + u, s_last), stage + u * kTileBytes);
+  for (int u = 0; u < NB; ++u) mx_issue(rsrc, off, nu > 0 ? order(min(u, nu - 1)) : s0, stage + u * kTileBytes);
 
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's fragment stores
   __builtin_amdgcn_s_barrier();
@@ -560,13 +573,13 @@ __global__ __launch_bounds__(1024) void k_gemv_mxb(const uint8_t* __restrict__ W
   for (int u = 0; u < nu; ++u) {
     if (min(NB - 1, nlast - u) >= 1) wait_vm<3>();
     else wait_vm<0>();
-    const int s = s0 + u;
+    const int s = order(u);
     const uint32_t st = stage_base + (uint32_t)slot * kTileBytes;
     u32x4 hd = lds_read16(st + b_hd);
     u32x2 q0 = lds_read8(st + b_q), q1 = lds_read8(st + b_q + 32), q2 = lds_read8(st + b_q + 64),
           q3 = lds_read8(st + b_q + 96);
     lds_wait5(hd, q0, q1, q2, q3);
-    if (u + NB < nu) mx_issue(rsrc, off, s + NB, stage + slot * kTileBytes);
+    if (u + NB < nu) mx_issue(rsrc, off, order(u + NB), stage + slot * kTileBytes);
     slot = slot + 1 == NB ? 0 : slot + 1;
     const u32x2 qq[4] = {q0, q1, q2, q3};
     // every A fragment and activation record of the tile in one round trip
@@ -694,6 +707,7 @@ __global__ __launch_bounds__(1024) void k_gemv_mxj(const uint8_t* __restrict__ W
   const int rb = b * geo.base + min(b, geo.rem), cnt = geo.base + (b < geo.rem ? 1 : 0);
   const int tq = wave % TQ, kq = wave / TQ;
   const int s0 = kq * nsb / KQ, s1 = (kq + 1) * nsb / KQ, nu = s1 - s0;
+  const SbOrder order(kq, KQ, s0, s1);
 
   const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(W + (size_t)rb * geo.row_bytes), (short)0, (int)((uint32_t)cnt * geo.row_bytes), (int)kRsrcWord3);
@@ -717,7 +731,7 @@ __global__ __launch_bounds__(1024) void k_gemv_mxj(const uint8_t* __restrict__ W
     for (int c = 0; c < 4; ++c) acc[e][c] = 0.0f;
   XRegs<NVT> x;
 
-  // step u: super-block s0 + u is in stage u & 1 and its activations in x
+  // step u: super-block order(u) is in stage u & 1 and its activations in x
 #define QVX_MXJ_STEP(U, WAITN, NEXT_X, NEXT_COPY)                                                    \
   {                                                                                                  \
     wait_vm<WAITN>();                                                                                \
@@ -730,8 +744,8 @@ __global__ __launch_bounds__(1024) void k_gemv_mxj(const uint8_t* __restrict__ W
     u32x3 m0[4], m1[4];                                                                              \
     mxj_read_half(0, fa, ma, a0, m0);                                                                \
     lds_wait13(hd, qq, a0, m0);                                                                      \
-    if (NEXT_X) mxj_load<NVT>(X, cols, nv, s0 + (U) + 1, lane, x);                                   \
-    if (NEXT_COPY) mx_issue(rsrc, off, s0 + (U) + 2, stage + ((U) & 1) * kTileBytes);                \
+    if (NEXT_X) mxj_load<NVT>(X, cols, nv, order((U) + 1), lane, x);                                 \
+    if (NEXT_COPY) mx_issue(rsrc, off, order((U) + 2), stage + ((U) & 1) * kTileBytes);              \
     mxj_read_half(1, fa, ma, a1, m1);                                                                \
     mxb_fold_group(0, hd, qq[0], a0[0], a0[1], m0[0], m0[1], acc);                                   \
     mxb_fold_group(1, hd, qq[1], a0[2], a0[3], m0[2], m0[3], acc);                                   \
@@ -741,9 +755,9 @@ __global__ __launch_bounds__(1024) void k_gemv_mxj(const uint8_t* __restrict__ W
   }
 
   if (nu >= 2) {
-    mxj_load<NVT>(X, cols, nv, s0, lane, x);
-    mx_issue(rsrc, off, s0, stage);
-    mx_issue(rsrc, off, s0 + 1, stage + kTileBytes);
+    mxj_load<NVT>(X, cols, nv, order(0), lane, x);
+    mx_issue(rsrc, off, order(0), stage);
+    mx_issue(rsrc, off, order(1), stage + kTileBytes);
     int u = 0;
     for (; u + 2 < nu; ++u) QVX_MXJ_STEP(u, 3, true, true)
     QVX_MXJ_STEP(u, 3, true, false)
