@@ -191,35 +191,56 @@ def decode_sweep(torch, stream, steps, cpu=True):
     out = {"workload": "Llama-3-8B Q4_K_M decode weight sweep (BASELINE configs[4]): 32 x 7 projections "
                        "+ Q6_K lm_head = 225 GEMVs per token, one HIP graph per token, GEMVs in call order",
            "weight_bytes_per_token": model.nbytes}
-    def time_step(mdl, m, concurrent):
-        st = decode.DecodeStep(mdl, m, concurrent=concurrent)
-        for _ in range(3):
-            st.replay(sh)
+    def time_step(mdl, m, concurrent, ops=None):
+        if ops == "fused":
+            st = decode.FusedDecodeStep(mdl, m)
+        elif ops == "separate":
+            st = decode.OpsDecodeStep(mdl, m)
+            with torch.cuda.stream(stream):
+                st.capture()
+        else:
+            st = decode.DecodeStep(mdl, m, concurrent=concurrent)
+        with torch.cuda.stream(stream):
+            for _ in range(3):
+                st.replay(sh)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(steps):
+                st.replay(sh)
+            e1.record(stream)
         torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(steps):
-            st.replay(sh)
-        e1.record(stream)
-        torch.cuda.synchronize()
-        st.plan.close()
+        if ops != "separate":
+            st.plan.close()
         return e0.elapsed_time(e1) / steps
 
     fused = model.fused()  # q|k and gate|up stacked: 5 GEMVs a layer
+    fops = model.fused_ops()  # ... and the RMSNorms and the SwiGLU folded in (gate|up interleaved)
     for m in (1, 8):
         ms = time_step(model, m, False)
         ms_br = time_step(model, m, True)
         ms_fu = time_step(fused, m, False)
+        ms_ops = time_step(fops, m, False, ops="fused")
+        ms_sep = time_step(model, m, False, ops="separate")
         _, ab = decode.sweep_bytes(m)
         gbs = ab / (ms * 1e-3) / 1e9
         out[f"M{m}"] = {"ms_per_token": round(ms, 4), "algorithmic_bytes_per_token": ab, "gb_s": round(gbs, 1),
                         "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "tokens_timed": steps,
                         "ms_per_token_qkv_gateup_branches": round(ms_br, 4),
                         "ms_per_token_fused_qk_gateup": round(ms_fu, 4),
-                        "gb_s_fused_qk_gateup": round(ab / (ms_fu * 1e-3) / 1e9, 1)}
+                        "gb_s_fused_qk_gateup": round(ab / (ms_fu * 1e-3) / 1e9, 1),
+                        "ms_per_token_fused_ops": round(ms_ops, 4),
+                        "gb_s_fused_ops": round(ab / (ms_ops * 1e-3) / 1e9, 1),
+                        "ms_per_token_separate_ops": round(ms_sep, 4),
+                        "fused_ops_note": "q|k and v with the attention RMSNorm folded in, o, gate|up with the FFN "
+                                          "RMSNorm and the SwiGLU epilogue, down on that SwiGLU output, LM head with "
+                                          "the output norm: 5 launches a layer + 1 (161 a token); separate_ops: the "
+                                          "reference's op sequence, one launch per op (2 RMSNorms, 7 GEMVs, 1 SwiGLU a "
+                                          "layer + norm and LM head = 322 a token), one graph"}
         log(f"[bench] sweep M={m}: {ms:.3f} ms/token, {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak); "
             f"{ms_br:.3f} ms/token with q/k/v and gate/up as concurrent graph branches; {ms_fu:.3f} ms/token with "
-            f"q|k and gate|up stacked (5 GEMVs a layer)")
+            f"q|k and gate|up stacked (5 GEMVs a layer); {ms_ops:.3f} ms/token with the norms and SwiGLU folded in "
+            f"(the same ops as separate launches: {ms_sep:.3f})")
         if cpu:
             # the reference CPU operator on layer 0's seven projections and the LM head (same blocks,
             # seeded activations); per token = 32 x layer + LM head
@@ -271,7 +292,7 @@ def decode_sweep(torch, stream, steps, cpu=True):
             f"{tbt:.1f} ms; {ms_fu:.2f} ms with q|k and gate|up stacked")
     out["prefill"] = {"workload": "Llama-3-8B Q4_K_M prompt prefill: 32 x 7 projections as GEMMs over M positions "
                                   "(fp16 activations) + the Q6_K LM head on the last position", **pre}
-    del model, fused
+    del model, fused, fops
     torch.cuda.empty_cache()
     return out
 

@@ -101,6 +101,42 @@ int qvx_dequantize(uint32_t type, const void* d_src, float* d_dst, size_t n, voi
  * there, the caller guarantees the row exists.  row < 0 -> QVX_E_RANGE. */
 int qvx_dequant_row(const void* d_w, uint32_t type, int cols, int row, float* d_dst, void* stream);
 
+/* ---- the decoder's ops on either side of the operator ----------------------------------- */
+/* The reference's ops::rmsnorm (runtime/src/ops.cpp:8-13) on n_vec rows of n: out = x * scale * w,
+ * scale = 1 / sqrt(sum x^2 / n + eps) formed in double.  The sum of squares is taken in the engine's
+ * one canonical order (512-element chunks, 8-element runs, a fixed tree; the reference sums in
+ * double element by element, so the scale may differ from it in the last bit), the order every
+ * fused call below uses too, so normed inputs agree bit for bit across all routes.  n < 0 or
+ * n > 16384 -> QVX_E_RANGE. */
+int qvx_rmsnorm(float* d_out, const float* d_x, const float* d_w, float eps, int n_vec, int n, void* stream);
+/* The reference's ops::swiglu (runtime/src/ops.cpp:96-100): out[i] = silu(gate[i]) * up[i],
+ * silu(z) = z / (1 + exp(-z)), in fp32. */
+int qvx_swiglu(float* d_out, const float* d_gate, const float* d_up, size_t n, void* stream);
+
+/* y[v] = W . rmsnorm(x[v], norm_w, eps): the reference decoder's ops::rmsnorm followed by wmatmul
+ * (runtime/src/text_model.cpp:146-149, 161-163, 171-172) in one call; the arguments and checks of
+ * qvx_qmatmul_n plus d_norm_w [cols] (NULL -> QVX_E_NULL; cols > 16384 -> QVX_E_RANGE).  Where the GEMV kernel takes the shape
+ * (Q4_K and the integer-dot formats, cols a multiple of 512 up to 16384, aligned operands) the norm
+ * is folded into the kernel's activation conversion: one launch, no temporary; the per-vector
+ * arithmetic does not depend on n_vec, so batches are bit-identical to single vectors.  Otherwise a
+ * standalone norm into a stream-ordered temporary, then qvx_qmatmul_n. */
+int qvx_qmatmul_n_rmsnorm(float* d_out, const void* d_w, uint32_t type, const float* d_X,
+                          const float* d_norm_w, float eps, int n_vec, int rows, int cols, void* stream);
+/* out[v, i] = silu(g[v, i]) * u[v, i], g = W_gate . xn[v], u = W_up . xn[v], xn = rmsnorm(x[v])
+ * when d_norm_w is non-NULL, else x[v]: the reference's gate / up wmatmuls and ops::swiglu
+ * (text_model.cpp:161-165) in one call.  d_w_gu holds both weights interleaved in 16-row groups
+ * (rows 32k .. 32k+15 = gate rows 16k .., rows 32k+16 .. 32k+31 = up rows 16k ..; build it with
+ * qvx_interleave_rows16), 2 * ffn rows; out [n_vec, ffn].  ffn % 16 != 0 -> QVX_E_SHAPE.  Q4_K with
+ * ffn % 16 == 0 and aligned operands runs fused (the gate and up tiles of a workgroup meet in its
+ * epilogue); other calls run the product into a temporary and a standalone SwiGLU. */
+int qvx_qmatmul_swiglu(float* d_out, const void* d_w_gu, uint32_t type, const float* d_X,
+                       const float* d_norm_w, float eps, int n_vec, int ffn, int cols, void* stream);
+/* Interleave two [rows, cols] weights of `type` in 16-row groups into d_dst (2 rows x cols), the
+ * layout qvx_qmatmul_swiglu reads: a load-time repack of raw blocks (no reference counterpart;
+ * the reference keeps gate and up apart, weights.hpp:22-97).  rows % 16 != 0 -> QVX_E_SHAPE. */
+int qvx_interleave_rows16(void* d_dst, const void* d_a, const void* d_b, uint32_t type, int rows, int cols,
+                          void* stream);
+
 /* Prefill GEMM: out[m * rows + r] = sum_k X[m, k] * dequant(W)[r, k] for m < M, X fp16 [M, cols].
  * No reference counterpart (the reference prefills token by token); semantics are qmatmulN's
  * with X converted fp16 -> fp32 exactly.  variant = QVX_GEMM_BF16 | QVX_GEMM_F16 | QVX_GEMM_I8;
@@ -167,6 +203,15 @@ int qvx_plan_create(qvx_plan** plan);
  * rows <= 0 is accepted and records nothing.  Appending to an instantiated plan -> QVX_E_STATE. */
 int qvx_plan_add_qmatmul_n(qvx_plan* plan, float* d_out, const void* d_w, uint32_t type,
                            const float* d_X, int n_vec, int rows, int cols);
+/* Append a fused call (the arguments and checks of qvx_qmatmul_n_rmsnorm / qvx_qmatmul_swiglu).  A
+ * replay allocates nothing, so only calls a kernel folds the norm / SwiGLU into are accepted
+ * (others -> QVX_E_SHAPE). */
+int qvx_plan_add_qmatmul_n_rmsnorm(qvx_plan* plan, float* d_out, const void* d_w, uint32_t type,
+                                   const float* d_X, const float* d_norm_w, float eps, int n_vec,
+                                   int rows, int cols);
+int qvx_plan_add_qmatmul_swiglu(qvx_plan* plan, float* d_out, const void* d_w_gu, uint32_t type,
+                                const float* d_X, const float* d_norm_w, float eps, int n_vec,
+                                int ffn, int cols);
 /* Calls added between qvx_plan_fork and qvx_plan_join are independent of each other (the graph
  * gets one branch per call, so their kernels may overlap on the device); all of them follow every
  * call before the fork and precede every call after the join -- as the decoder's q/k/v

@@ -57,6 +57,15 @@ def _bind(so, prefix):
         fn.restype = restype
 
 
+def _bind_ops(so, prefix):
+    f = getattr(so, prefix + "rmsnorm")
+    f.argtypes = [_f32p, _f32p, _f32p, C.c_int, C.c_float]
+    f.restype = None
+    f = getattr(so, prefix + "swiglu")
+    f.argtypes = [_f32p, _f32p, _f32p, C.c_int]
+    f.restype = None
+
+
 def lib():
     """The C restatement (liboracle.so), built on first use if missing."""
     global _lib
@@ -77,6 +86,7 @@ def lib():
         so.qvxo_matmul_f64.restype = C.c_int
         so.qvxo_quantize_q8_act.argtypes = [_f32p, C.c_int, C.c_int, _i8p, _f32p, _i32p]
         so.qvxo_quantize_q8_act.restype = None
+        _bind_ops(so, "qvxo_")
         _lib = so
     return _lib
 
@@ -87,6 +97,7 @@ def ref_lib():
     if _ref is None and os.path.exists(REF_SO):
         so = C.CDLL(REF_SO)
         _bind(so, "qvxr_")
+        _bind_ops(so, "qvxr_")
         _ref = so
     return _ref
 
@@ -155,3 +166,28 @@ def dequant_row(w: np.ndarray, t: int, cols: int, row: int, use_ref: bool = Fals
     fn = so.qvxr_dequant_row if use_ref else so.qvxo_dequant_row
     ok = fn(_ptr(np.ascontiguousarray(w)), t, cols, row, out)
     return out if ok else None
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float, use_ref: bool = False) -> np.ndarray:
+    """The reference's ops::rmsnorm over each row of x (restated, or the reference build)."""
+    x = np.ascontiguousarray(np.atleast_2d(x), np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    so = ref_lib() if use_ref else lib()
+    fn = so.qvxr_rmsnorm if use_ref else so.qvxo_rmsnorm
+    out = np.empty_like(x)
+    for v in range(x.shape[0]):
+        row = np.empty(x.shape[1], np.float32)
+        fn(row, np.ascontiguousarray(x[v]), w, x.shape[1], eps)
+        out[v] = row
+    return out
+
+
+def swiglu(gate: np.ndarray, up: np.ndarray, use_ref: bool = False) -> np.ndarray:
+    """The reference's ops::swiglu, elementwise over equal-shaped arrays."""
+    g = np.ascontiguousarray(gate, np.float32).ravel()
+    u = np.ascontiguousarray(up, np.float32).ravel()
+    so = ref_lib() if use_ref else lib()
+    fn = so.qvxr_swiglu if use_ref else so.qvxo_swiglu
+    out = np.empty_like(g)
+    fn(out, g, u, g.size)
+    return out.reshape(np.shape(gate))

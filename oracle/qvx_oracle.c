@@ -19,6 +19,9 @@
  *   qvxo_qmatmul_n        runtime/src/qmatmul.cpp:64-115   (row dequantised once, vectors tiled by 64)
  *   qvxo_dequant_row      runtime/src/qmatmul.cpp:117-126
  *   qvxo_supports         runtime/src/qmatmul.cpp:24-26
+ *   qvxo_rmsnorm          runtime/src/ops.cpp:8-13         (sum of squares in double, scale in
+ *                         float, out = x * scale * w)
+ *   qvxo_swiglu           runtime/src/ops.cpp:96-100       (silu(g) * u, silu(z) = z / (1 + exp(-z)))
  * and the build-defined parts that have no reference counterpart:
  *   qvxo_matmul_f64       exact dequant values x f32 activations, summed in double
  *                         (the tolerance oracle for every GEMV/GEMM)
@@ -34,7 +37,11 @@
  *     their double references, bit-identity batched vs unbatched, and bit-identity with
  *     oracle/_ref on random blocks;
  *   - fp16 decode: all 65536 encodings against numpy's float16;
- *   - qvxo_matmul_f64: brute-force Fraction sums on tiny inputs.
+ *   - qvxo_matmul_f64: brute-force Fraction sums on tiny inputs;
+ *   - rmsnorm / swiglu: bit-identity with oracle/_ref (the reference's own ops.cpp built from
+ *     its sources), and what the mathematics fixes: the output's mean square is 1 for eps = 0 and
+ *     unit weights, rmsnorm is invariant under x -> a x, silu(0) = 0 and silu(z) -> z, 0 at the
+ *     tails, swiglu is linear in up.
  */
 #include <math.h>
 #include <stdint.h>
@@ -490,5 +497,25 @@ QVXO_EXPORT void qvxo_quantize_q8_act(const float* X, int M, int K, int8_t* q, f
       scale[(size_t)m * nb + j] = s;
       qsum[(size_t)m * nb + j] = sum;
     }
+  }
+}
+
+/* ---- decoder elementwise ops on the path's inputs and outputs ------------------------------- */
+
+/* The reference's ops::rmsnorm (runtime/src/ops.cpp:8-13): the sum of squares in double, the scale
+ * 1 / sqrt(sum / n + eps) in double rounded to float, then x * scale * w in float, left to right. */
+QVXO_EXPORT void qvxo_rmsnorm(float* out, const float* x, const float* w, int n, float eps) {
+  double ss = 0.0;
+  for (int i = 0; i < n; ++i) ss += (double)x[i] * (double)x[i];
+  const float scale = (float)(1.0 / sqrt(ss / n + (double)eps));
+  for (int i = 0; i < n; ++i) out[i] = x[i] * scale * w[i];
+}
+
+/* The reference's ops::swiglu (runtime/src/ops.cpp:96-100): out = silu(g) * u in float, with
+ * silu(z) = z / (1 + exp(-z)) (float exp). */
+QVXO_EXPORT void qvxo_swiglu(float* out, const float* gate, const float* up, int n) {
+  for (int i = 0; i < n; ++i) {
+    const float z = gate[i];
+    out[i] = z / (1.0f + expf(-z)) * up[i];
   }
 }

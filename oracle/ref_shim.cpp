@@ -1,7 +1,7 @@
 // ref_shim.cpp -- C entry points onto the reference's own CPU operator, for ctypes.
 //
 // TEST INFRASTRUCTURE ONLY (see qvx_oracle.c).  Linked with the reference's unmodified sources
-// runtime/src/{dequant,qmatmul,cpu_features}.cpp and gguf/src/gguf_types.cpp, compiled where they
+// runtime/src/{dequant,qmatmul,cpu_features,ops}.cpp and gguf/src/gguf_types.cpp, compiled where they
 // lie under /root/reference by oracle/Makefile into oracle/_ref/.  Nothing here restates the
 // reference; each function forwards to the declaration cited beside it.
 #include <cstddef>
@@ -9,6 +9,7 @@
 
 #include "qorvix/runtime/cpu_features.hpp"  // runtime/include/qorvix/runtime/cpu_features.hpp:38-45
 #include "qorvix/runtime/dequant.hpp"       // runtime/include/qorvix/runtime/dequant.hpp:12-21
+#include "qorvix/runtime/ops.hpp"           // runtime/include/qorvix/runtime/ops.hpp:11,35-38
 #include "qorvix/runtime/qmatmul.hpp"       // runtime/include/qorvix/runtime/qmatmul.hpp:14-36
 
 namespace rt = qorvix::runtime;
@@ -34,4 +35,11 @@ __attribute__((visibility("default"))) int qvxr_dequant_row(const void* w, std::
   return rt::dequantRow(w, t, cols, row, dst);
 }
 __attribute__((visibility("default"))) const char* qvxr_dot_kernel() { return rt::cpu::activeDotKernel(); }
+__attribute__((visibility("default"))) void qvxr_rmsnorm(float* out, const float* x, const float* w, int n,
+                                                         float eps) {
+  rt::ops::rmsnorm(out, x, w, n, eps);
+}
+__attribute__((visibility("default"))) void qvxr_swiglu(float* out, const float* gate, const float* up, int n) {
+  rt::ops::swiglu(out, gate, up, n);
+}
 }

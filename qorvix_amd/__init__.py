@@ -46,6 +46,11 @@ SIGNATURES = {
     "qvx_bf16_to_float": ([C.c_uint16], _f32),
     "qvx_qmatmul": ([_vp, _vp, _u32, _vp, _i32, _i32, _vp], _i32),
     "qvx_qmatmul_n": ([_vp, _vp, _u32, _vp, _i32, _i32, _i32, _vp], _i32),
+    "qvx_qmatmul_n_rmsnorm": ([_vp, _vp, _u32, _vp, _vp, _f32, _i32, _i32, _i32, _vp], _i32),
+    "qvx_qmatmul_swiglu": ([_vp, _vp, _u32, _vp, _vp, _f32, _i32, _i32, _i32, _vp], _i32),
+    "qvx_interleave_rows16": ([_vp, _vp, _vp, _u32, _i32, _i32, _vp], _i32),
+    "qvx_rmsnorm": ([_vp, _vp, _vp, _f32, _i32, _i32, _vp], _i32),
+    "qvx_swiglu": ([_vp, _vp, _vp, _sz, _vp], _i32),
     "qvx_dequantize": ([_u32, _vp, _vp, _sz, _vp], _i32),
     "qvx_dequant_row": ([_vp, _u32, _i32, _i32, _vp, _vp], _i32),
     "qvx_qgemm_f16": ([_vp, _vp, _u32, _vp, _i32, _i32, _i32, _i32, _vp], _i32),
@@ -57,6 +62,8 @@ SIGNATURES = {
     "qvx_bench_read": ([_vp, _sz, _vp, _vp], _i32),
     "qvx_plan_create": ([C.POINTER(_vp)], _i32),
     "qvx_plan_add_qmatmul_n": ([_vp, _vp, _vp, _u32, _vp, _i32, _i32, _i32], _i32),
+    "qvx_plan_add_qmatmul_n_rmsnorm": ([_vp, _vp, _vp, _u32, _vp, _vp, _f32, _i32, _i32, _i32], _i32),
+    "qvx_plan_add_qmatmul_swiglu": ([_vp, _vp, _vp, _u32, _vp, _vp, _f32, _i32, _i32, _i32], _i32),
     "qvx_plan_fork": ([_vp], _i32),
     "qvx_plan_join": ([_vp], _i32),
     "qvx_plan_size": ([_vp], _i32),
@@ -187,6 +194,30 @@ def qmatmul_n(out: int, weight: int, ggml_type: int, X: int, nvec: int, rows: in
     return lib().qvx_qmatmul_n(out, weight, ggml_type, X, nvec, rows, cols, stream)
 
 
+def qmatmul_n_rmsnorm(out: int, weight: int, ggml_type: int, X: int, norm_w: int, eps: float, nvec: int, rows: int,
+                      cols: int, stream: int = 0) -> int:
+    """out = W . rmsnorm(x) per vector: the decoder's ops::rmsnorm + wmatmul
+    (runtime/src/text_model.cpp:146-149, ops.cpp:8-13) in one call. Status."""
+    return lib().qvx_qmatmul_n_rmsnorm(out, weight, ggml_type, X, norm_w, eps, nvec, rows, cols, stream)
+
+
+def qmatmul_swiglu(out: int, weight_gu: int, ggml_type: int, X: int, norm_w: int, eps: float, nvec: int, ffn: int,
+                   cols: int, stream: int = 0) -> int:
+    """out = silu(W_gate . xn) * (W_up . xn), xn = rmsnorm(x) when norm_w (else x), over a gate|up weight
+    interleaved in 16-row groups (text_model.cpp:161-165, ops.cpp:96-100). Status."""
+    return lib().qvx_qmatmul_swiglu(out, weight_gu, ggml_type, X, norm_w or None, eps, nvec, ffn, cols, stream)
+
+
+def rmsnorm(out: int, x: int, w: int, eps: float, nvec: int, n: int, stream: int = 0) -> int:
+    """ops::rmsnorm (runtime/src/ops.cpp:8-13) over nvec rows of n on device pointers. Status."""
+    return lib().qvx_rmsnorm(out, x, w, eps, nvec, n, stream)
+
+
+def swiglu(out: int, gate: int, up: int, n: int, stream: int = 0) -> int:
+    """ops::swiglu (runtime/src/ops.cpp:96-100) on device pointers. Status."""
+    return lib().qvx_swiglu(out, gate, up, n, stream)
+
+
 def dequantize(ggml_type: int, src: int, dst: int, n: int, stream: int = 0) -> int:
     """dequantize (runtime/src/dequant.cpp:277-296) on device pointers. Status."""
     return lib().qvx_dequantize(ggml_type, src, dst, n, stream)
@@ -264,4 +295,55 @@ def qgemm_t(w, ggml_type: int, X, rows: int, cols: int, variant: int = GEMM_BF16
         out = torch.empty((M, rows), dtype=torch.float32, device=X.device)
     _check(lib().qvx_qgemm_f16(out.data_ptr(), w.data_ptr(), ggml_type, X.data_ptr(), M, rows, cols, variant,
                                _stream()), "qvx_qgemm_f16")
+    return out
+
+
+def rmsnorm_t(x, w, eps: float, out=None):
+    """rmsnorm over the last dimension of an fp32 device tensor ([n] or [nvec, n])."""
+    import torch
+    n = x.shape[-1]
+    nvec = x.numel() // n if n else 1
+    if out is None:
+        out = torch.empty_like(x)
+    _check(lib().qvx_rmsnorm(out.data_ptr(), x.data_ptr(), w.data_ptr(), eps, nvec, n, _stream()), "qvx_rmsnorm")
+    return out
+
+
+def swiglu_t(gate, up, out=None):
+    import torch
+    if out is None:
+        out = torch.empty_like(gate)
+    _check(lib().qvx_swiglu(out.data_ptr(), gate.data_ptr(), up.data_ptr(), gate.numel(), _stream()), "qvx_swiglu")
+    return out
+
+
+def qmatmul_rmsnorm_t(w, ggml_type: int, x, norm_w, eps: float, rows: int, cols: int, out=None):
+    """W . rmsnorm(x) for fp32 x [cols] or [n, cols] (one launch where the kernel folds the norm in)."""
+    import torch
+    nvec = 1 if x.dim() == 1 else x.shape[0]
+    if out is None:
+        out = torch.empty((nvec, rows) if x.dim() > 1 else (rows,), dtype=torch.float32, device=x.device)
+    _check(lib().qvx_qmatmul_n_rmsnorm(out.data_ptr(), w.data_ptr(), ggml_type, x.data_ptr(), norm_w.data_ptr(), eps,
+                                       nvec, rows, cols, _stream()), "qvx_qmatmul_n_rmsnorm")
+    return out
+
+
+def qmatmul_swiglu_t(w_gu, ggml_type: int, x, ffn: int, cols: int, norm_w=None, eps: float = 0.0, out=None):
+    """silu(W_gate . xn) * (W_up . xn) for an interleaved gate|up weight (interleave_rows16_t); [ffn] or [n, ffn]."""
+    import torch
+    nvec = 1 if x.dim() == 1 else x.shape[0]
+    if out is None:
+        out = torch.empty((nvec, ffn) if x.dim() > 1 else (ffn,), dtype=torch.float32, device=x.device)
+    nw = norm_w.data_ptr() if norm_w is not None else None
+    _check(lib().qvx_qmatmul_swiglu(out.data_ptr(), w_gu.data_ptr(), ggml_type, x.data_ptr(), nw, eps, nvec, ffn,
+                                    cols, _stream()), "qvx_qmatmul_swiglu")
+    return out
+
+
+def interleave_rows16_t(a, b, ggml_type: int, rows: int, cols: int):
+    """The gate|up weight qmatmul_swiglu reads: a and b ([rows, cols] raw blocks) in 16-row groups."""
+    import torch
+    out = torch.empty(2 * weight_bytes(ggml_type, rows, cols), dtype=torch.uint8, device=a.device)
+    _check(lib().qvx_interleave_rows16(out.data_ptr(), a.data_ptr(), b.data_ptr(), ggml_type, rows, cols, _stream()),
+           "qvx_interleave_rows16")
     return out

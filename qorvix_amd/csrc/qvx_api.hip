@@ -14,6 +14,7 @@
 
 #include "../../include/qvx.h"
 #include "qvx_common.hpp"
+#include "qvx_norm.hpp"
 
 #include <algorithm>
 
@@ -22,7 +23,14 @@ bool launch_dequant(uint32_t t, const void* src, float* dst, size_t n, hipStream
 bool launch_gemv_generic(uint32_t t, const void* w, const float* X, float* Y, int rows, int cols, int nvec,
                          size_t row_bytes, hipStream_t s);
 bool launch_gemv_fast(uint32_t t, const void* w, const float* X, float* Y, int nvec, int rows, int cols,
-                      size_t row_bytes, hipStream_t s);
+                      size_t row_bytes, const GemvEpi& epi, hipStream_t s);
+bool gemv_fast_fusable(uint32_t t, int cols, size_t row_bytes, const GemvEpi& epi);
+bool mx_epi_supported(const GemvEpi& epi, int rows, int cols);
+void launch_rmsnorm(float* out, const float* x, const float* w, float eps, int nvec, int n, hipStream_t s);
+void launch_swiglu(float* out, const float* g, const float* u, size_t n, hipStream_t s);
+void launch_swiglu_interleaved(float* out, const float* y, int nvec, int ffn, hipStream_t s);
+void* gemm_temp_alloc(size_t bytes, hipStream_t s);
+void gemm_temp_free(void* p, hipStream_t s);
 bool launch_gemv_float(uint32_t t, const void* w, const float* X, float* Y, int nvec, int rows, int cols,
                        size_t row_bytes, hipStream_t s);
 int gemv_mx_max_nv(int cols);
@@ -30,10 +38,10 @@ int gemv_mxj_supported(int cols);
 bool launch_gemv_mxj_q4k(const void* w, const float* X, float* Y, int nvec, int rows, int cols, size_t row_bytes,
                          hipStream_t s);
 bool launch_gemv_mx_q4k(const void* w, const float* X, float* Y, int nvec, int rows, int cols, size_t row_bytes,
-                        hipStream_t s);
+                        const GemvEpi& epi, hipStream_t s);
 int gemv_mxb_supported(int cols);
 bool launch_gemv_mxb_q4k(const void* w, const float* X, float* Y, int nvec, int rows, int cols, size_t row_bytes,
-                         hipStream_t s);
+                         const GemvEpi& epi, hipStream_t s);
 bool launch_fill_synthetic(void* w, uint32_t t, size_t nblk, uint64_t seed, float mul, hipStream_t s);
 void launch_fill_normal_f32(float* x, size_t n, uint64_t seed, float mul, hipStream_t s);
 void launch_fill_normal_f16(uint16_t* x, size_t n, uint64_t seed, float mul, hipStream_t s);
@@ -65,6 +73,7 @@ struct qvx_plan {
     const float* X;
     int nvec, rows, cols;
     int group;  // calls sharing a group >= 0 are independent of each other (one fork); -1: in order
+    GemvEpi epi;  // fused RMSNorm / SwiGLU (rows = the weight's rows: 2 ffn for SwiGLU)
   };
   std::vector<Call> calls;
   int device = 0;
@@ -109,19 +118,77 @@ inline int check_matmul(uint32_t type, int cols, const TypeInfo** ti) {
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int rows, int cols, hipStream_t s) {
+// Q4_K: the vector count a chunk may have on the one-vector matrix-core kernel before the batched
+// forms take over (measured faster there), and whether the whole-row batched form takes the row.
+inline int q4k_small(int cols) { return std::min(gemv_mxb_supported(cols) ? 3 : 2, gemv_mx_max_nv(cols)); }
+
+// 1 if the routing below sends every chunk of this call to a kernel that folds `epi` in.
+bool fused_route(uint32_t type, int nvec, int rows, int cols, size_t row_bytes, bool fast, const GemvEpi& epi) {
+  if (!fast) return false;
+  if (type == T_Q4_K && gemv_mx_max_nv(cols) > 0) {
+    if (!mx_epi_supported(epi, rows, cols)) return false;
+    return nvec == 1 || gemv_mxb_supported(cols) || nvec <= q4k_small(cols);
+  }
+  return gemv_fast_fusable(type, cols, row_bytes, epi);
+}
+
+int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int rows, int cols, hipStream_t s,
+         const GemvEpi& epi = {});
+
+// A fused call no kernel folds in: the standalone norm into a temporary, the plain product (into a
+// temporary for SwiGLU), then the de-interleaving SwiGLU.  Temporaries come from the library's
+// stream-ordered pool.
+int gemv_unfused(float* out, const void* w, uint32_t type, const float* X, int nvec, int rows, int cols,
+                 hipStream_t s, const GemvEpi& epi) {
+  const float* xin = X;
+  float* xn = nullptr;
+  float* y = nullptr;
+  if (epi.norm_w) {
+    if (cols > kNormChunk * kNormMaxChunks) return QVX_E_RANGE;
+    xn = static_cast<float*>(gemm_temp_alloc((size_t)nvec * (size_t)cols * sizeof(float), s));
+    if (!xn) return QVX_E_HIP;
+    launch_rmsnorm(xn, X, epi.norm_w, epi.eps, nvec, cols, s);
+    xin = xn;
+  }
+  float* dst = out;
+  if (epi.swiglu) {
+    y = static_cast<float*>(gemm_temp_alloc((size_t)nvec * (size_t)rows * sizeof(float), s));
+    if (!y) {
+      gemm_temp_free(xn, s);
+      return QVX_E_HIP;
+    }
+    dst = y;
+  }
+  int rc = gemv(dst, w, type, xin, nvec, rows, cols, s);
+  if (rc == QVX_OK && epi.swiglu) {
+    launch_swiglu_interleaved(out, y, nvec, rows / 2, s);
+    rc = hip_status();
+  }
+  gemm_temp_free(xn, s);
+  gemm_temp_free(y, s);
+  return rc;
+}
+
+// out = W . x per vector, optionally with the activations normalised (epi.norm_w) and / or the
+// interleaved gate|up rows gated (epi.swiglu: rows / 2 outputs a vector).  The argument checks are
+// the plain operator's.
+int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int rows, int cols, hipStream_t s,
+         const GemvEpi& epi) {
   const TypeInfo* ti = nullptr;
   if (nvec <= 0) return QVX_E_NVEC;
   if (int rc = check_matmul(type, cols, &ti); rc != QVX_OK) return rc;
   if (rows <= 0) return QVX_OK;
   if (!out) return QVX_E_NULL;
-  if (cols <= 0) {  // no columns: every dot product is empty (the reference writes 0.0f)
-    launch_zero(out, (size_t)rows * (size_t)nvec, s);
+  const int nout = epi.swiglu ? rows / 2 : rows;
+  if (cols <= 0) {  // no columns: every dot product is empty (the reference writes 0.0f; silu(0) * 0 = 0)
+    launch_zero(out, (size_t)nout * (size_t)nvec, s);
     return hip_status();
   }
   if (!w || !X) return QVX_E_NULL;
   const size_t row_bytes = (size_t)(cols / (int)ti->block) * ti->bytes;
   const bool fast = aligned16(w) && aligned16(X) && row_bytes % 16 == 0;
+  if (epi.flags() && !fused_route(type, nvec, rows, cols, row_bytes, fast, epi))
+    return gemv_unfused(out, w, type, X, nvec, rows, cols, s, epi);
   // Unquantised weights stream through the float kernel.
   if (fast && (type == T_F32 || type == T_F16 || type == T_BF16) &&
       launch_gemv_float(type, w, X, out, nvec, rows, cols, row_bytes, s))
@@ -137,13 +204,13 @@ int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int
   // bit-identical per vector.
   if (fast && type == T_Q4_K && nvec >= 2 && (gemv_mxb_supported(cols) || gemv_mxj_supported(cols))) {
     const bool whole = gemv_mxb_supported(cols) != 0;
-    const int small = std::min(whole ? 3 : 2, gemv_mx_max_nv(cols));
+    const int small = q4k_small(cols);
     for (int v0 = 0; v0 < nvec; v0 += 8) {
       const int nv = nvec - v0 < 8 ? nvec - v0 : 8;
       const float* Xv = X + (size_t)v0 * cols;
-      float* Yv = out + (size_t)v0 * rows;
-      const bool ok = nv <= small ? launch_gemv_mx_q4k(w, Xv, Yv, nv, rows, cols, row_bytes, s)
-                      : whole     ? launch_gemv_mxb_q4k(w, Xv, Yv, nv, rows, cols, row_bytes, s)
+      float* Yv = out + (size_t)v0 * nout;
+      const bool ok = nv <= small ? launch_gemv_mx_q4k(w, Xv, Yv, nv, rows, cols, row_bytes, epi, s)
+                      : whole     ? launch_gemv_mxb_q4k(w, Xv, Yv, nv, rows, cols, row_bytes, epi, s)
                                   : launch_gemv_mxj_q4k(w, Xv, Yv, nv, rows, cols, row_bytes, s);
       if (!ok) return refused();
     }
@@ -153,12 +220,13 @@ int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int
   if (mx > 0) {
     for (int v0 = 0; v0 < nvec; v0 += mx) {
       const int nv = nvec - v0 < mx ? nvec - v0 : mx;
-      if (!launch_gemv_mx_q4k(w, X + (size_t)v0 * cols, out + (size_t)v0 * rows, nv, rows, cols, row_bytes, s))
+      if (!launch_gemv_mx_q4k(w, X + (size_t)v0 * cols, out + (size_t)v0 * nout, nv, rows, cols, row_bytes, epi, s))
         return refused();
     }
     return hip_status();
   }
-  if (fast && launch_gemv_fast(type, w, X, out, nvec, rows, cols, row_bytes, s)) return hip_status();
+  if (fast && launch_gemv_fast(type, w, X, out, nvec, rows, cols, row_bytes, epi, s)) return hip_status();
+  if (epi.flags()) return refused();  // fused_route() promised a fused kernel
   for (int v0 = 0; v0 < nvec; v0 += 16) {
     const int nv = nvec - v0 < 16 ? nvec - v0 : 16;
     if (!launch_gemv_generic(type, w, X + (size_t)v0 * cols, out + (size_t)v0 * rows, rows, cols, nv, row_bytes, s))
@@ -224,6 +292,30 @@ void* scratch_ptr() {
 
 }  // namespace
 
+namespace {
+
+// A fused call in a plan: recorded only when a kernel folds the norm / SwiGLU in, since a replay
+// allocates nothing (the unfused route needs pool temporaries).
+int plan_add_fused(qvx_plan* plan, float* d_out, const void* d_w, uint32_t type, const float* d_X, int n_vec,
+                          int rows, int cols, const GemvEpi& epi) {
+  if (!plan) return QVX_E_NULL;
+  if (plan->exec) return QVX_E_STATE;
+  const TypeInfo* ti = nullptr;
+  if (n_vec <= 0) return QVX_E_NVEC;
+  if (int rc = check_matmul(type, cols, &ti); rc != QVX_OK) return rc;
+  if (rows <= 0) return QVX_OK;
+  if (!d_out || (cols > 0 && (!d_w || !d_X))) return QVX_E_NULL;
+  if (cols > 0) {
+    const size_t row_bytes = (size_t)(cols / (int)ti->block) * ti->bytes;
+    const bool fast = aligned16(d_w) && aligned16(d_X) && row_bytes % 16 == 0;
+    if (!fused_route(type, n_vec, rows, cols, row_bytes, fast, epi)) return QVX_E_SHAPE;
+  }
+  plan->calls.push_back({d_out, d_w, type, d_X, n_vec, rows, cols, plan->open_group, epi});
+  return QVX_OK;
+}
+
+}  // namespace
+
 #pragma GCC visibility push(default)
 extern "C" {
 
@@ -270,6 +362,66 @@ int qvx_qmatmul(float* d_out, const void* d_w, uint32_t type, const float* d_x, 
 int qvx_qmatmul_n(float* d_out, const void* d_w, uint32_t type, const float* d_X, int n_vec, int rows, int cols,
                   void* stream) {
   return gemv(d_out, d_w, type, d_X, n_vec, rows, cols, as_stream(stream));
+}
+
+int qvx_qmatmul_n_rmsnorm(float* d_out, const void* d_w, uint32_t type, const float* d_X, const float* d_norm_w,
+                          float eps, int n_vec, int rows, int cols, void* stream) {
+  const TypeInfo* ti = nullptr;
+  if (n_vec <= 0) return QVX_E_NVEC;
+  if (int rc = check_matmul(type, cols, &ti); rc != QVX_OK) return rc;
+  if (rows > 0 && cols > 0 && !d_norm_w) return QVX_E_NULL;
+  GemvEpi epi;
+  epi.norm_w = d_norm_w;
+  epi.eps = eps;
+  return gemv(d_out, d_w, type, d_X, n_vec, rows, cols, as_stream(stream), epi);
+}
+
+int qvx_qmatmul_swiglu(float* d_out, const void* d_w_gu, uint32_t type, const float* d_X, const float* d_norm_w,
+                       float eps, int n_vec, int ffn, int cols, void* stream) {
+  const TypeInfo* ti = nullptr;
+  if (n_vec <= 0) return QVX_E_NVEC;
+  if (int rc = check_matmul(type, cols, &ti); rc != QVX_OK) return rc;
+  if (ffn < 0 || ffn % 16 != 0) return QVX_E_SHAPE;
+  if (ffn > (1 << 30)) return QVX_E_RANGE;
+  GemvEpi epi;
+  epi.norm_w = d_norm_w;
+  epi.eps = eps;
+  epi.swiglu = true;
+  return gemv(d_out, d_w_gu, type, d_X, n_vec, 2 * ffn, cols, as_stream(stream), epi);
+}
+
+int qvx_rmsnorm(float* d_out, const float* d_x, const float* d_w, float eps, int n_vec, int n, void* stream) {
+  if (n_vec <= 0) return QVX_E_NVEC;
+  if (n < 0 || n > kNormChunk * kNormMaxChunks) return QVX_E_RANGE;
+  if (n == 0) return QVX_OK;
+  if (!d_out || !d_x || !d_w) return QVX_E_NULL;
+  launch_rmsnorm(d_out, d_x, d_w, eps, n_vec, n, as_stream(stream));
+  return hip_status();
+}
+
+int qvx_swiglu(float* d_out, const float* d_gate, const float* d_up, size_t n, void* stream) {
+  if (n == 0) return QVX_OK;
+  if (!d_out || !d_gate || !d_up) return QVX_E_NULL;
+  launch_swiglu(d_out, d_gate, d_up, n, as_stream(stream));
+  return hip_status();
+}
+
+int qvx_interleave_rows16(void* d_dst, const void* d_a, const void* d_b, uint32_t type, int rows, int cols,
+                          void* stream) {
+  const TypeInfo* t = type_info(type);
+  if (!t) return QVX_E_TYPE;
+  if (t->block == 0 || cols < 0 || cols % (int)t->block != 0 || rows < 0 || rows % 16 != 0) return QVX_E_SHAPE;
+  if (rows == 0 || cols == 0) return QVX_OK;
+  if (!d_dst || !d_a || !d_b) return QVX_E_NULL;
+  const size_t g = 16 * (size_t)(cols / (int)t->block) * t->bytes;  // bytes of 16 rows
+  const hipStream_t s = as_stream(stream);
+  auto* dst = static_cast<uint8_t*>(d_dst);
+  if (hipMemcpy2DAsync(dst, 2 * g, d_a, g, g, (size_t)rows / 16, hipMemcpyDeviceToDevice, s) != hipSuccess ||
+      hipMemcpy2DAsync(dst + g, 2 * g, d_b, g, g, (size_t)rows / 16, hipMemcpyDeviceToDevice, s) != hipSuccess) {
+    (void)hipGetLastError();
+    return QVX_E_HIP;
+  }
+  return hip_status();
 }
 
 int qvx_dequantize(uint32_t type, const void* d_src, float* d_dst, size_t n, void* stream) {
@@ -405,8 +557,28 @@ int qvx_plan_add_qmatmul_n(qvx_plan* plan, float* d_out, const void* d_w, uint32
   if (int rc = check_matmul(type, cols, &ti); rc != QVX_OK) return rc;
   if (rows <= 0) return QVX_OK;
   if (!d_out || (cols > 0 && (!d_w || !d_X))) return QVX_E_NULL;
-  plan->calls.push_back({d_out, d_w, type, d_X, n_vec, rows, cols, plan->open_group});
+  plan->calls.push_back({d_out, d_w, type, d_X, n_vec, rows, cols, plan->open_group, GemvEpi{}});
   return QVX_OK;
+}
+
+int qvx_plan_add_qmatmul_n_rmsnorm(qvx_plan* plan, float* d_out, const void* d_w, uint32_t type, const float* d_X,
+                                   const float* d_norm_w, float eps, int n_vec, int rows, int cols) {
+  if (plan && !d_norm_w && n_vec > 0 && rows > 0 && cols > 0) return QVX_E_NULL;
+  GemvEpi epi;
+  epi.norm_w = d_norm_w;
+  epi.eps = eps;
+  return plan_add_fused(plan, d_out, d_w, type, d_X, n_vec, rows, cols, epi);
+}
+
+int qvx_plan_add_qmatmul_swiglu(qvx_plan* plan, float* d_out, const void* d_w_gu, uint32_t type, const float* d_X,
+                                const float* d_norm_w, float eps, int n_vec, int ffn, int cols) {
+  if (ffn < 0 || ffn % 16 != 0) return QVX_E_SHAPE;
+  if (ffn > (1 << 30)) return QVX_E_RANGE;
+  GemvEpi epi;
+  epi.norm_w = d_norm_w;
+  epi.eps = eps;
+  epi.swiglu = true;
+  return plan_add_fused(plan, d_out, d_w_gu, type, d_X, n_vec, 2 * ffn, cols, epi);
 }
 
 int qvx_plan_fork(qvx_plan* plan) {
@@ -428,7 +600,7 @@ int qvx_plan_size(const qvx_plan* plan) { return plan ? (int)plan->calls.size() 
 int qvx_plan_run_eager(const qvx_plan* plan, void* stream) {
   if (!plan) return QVX_E_NULL;
   for (const auto& c : plan->calls)
-    if (int rc = gemv(c.out, c.w, c.type, c.X, c.nvec, c.rows, c.cols, as_stream(stream)); rc != QVX_OK) return rc;
+    if (int rc = gemv(c.out, c.w, c.type, c.X, c.nvec, c.rows, c.cols, as_stream(stream), c.epi); rc != QVX_OK) return rc;
   return QVX_OK;
 }
 
@@ -449,7 +621,7 @@ static int plan_record(const qvx_plan* plan, hipStream_t cs, std::vector<hipStre
     while (g >= 0 && i + n < calls.size() && calls[i + n].group == g) ++n;
     if (n == 1) {
       const auto& c = calls[i];
-      if (int rc = gemv(c.out, c.w, c.type, c.X, c.nvec, c.rows, c.cols, cs); rc != QVX_OK) return rc;
+      if (int rc = gemv(c.out, c.w, c.type, c.X, c.nvec, c.rows, c.cols, cs, c.epi); rc != QVX_OK) return rc;
       ++i;
       continue;
     }
@@ -464,7 +636,7 @@ static int plan_record(const qvx_plan* plan, hipStream_t cs, std::vector<hipStre
       const auto& c = calls[i + k];
       hipStream_t st = k == 0 ? cs : side[k - 1];
       if (k > 0 && hipStreamWaitEvent(st, fork, 0) != hipSuccess) return QVX_E_HIP;
-      if (int rc = gemv(c.out, c.w, c.type, c.X, c.nvec, c.rows, c.cols, st); rc != QVX_OK) return rc;
+      if (int rc = gemv(c.out, c.w, c.type, c.X, c.nvec, c.rows, c.cols, st, c.epi); rc != QVX_OK) return rc;
     }
     for (size_t k = 1; k < n; ++k) {
       hipEvent_t done = nullptr;

@@ -41,6 +41,7 @@
 #include <algorithm>
 
 #include "qvx_common.hpp"
+#include "qvx_norm.hpp"
 
 namespace qvx {
 
@@ -497,13 +498,16 @@ struct Geo {
 // unconditionally (rows past the workgroup's last are clamped to it and their results dropped):
 // activations first, then the first PF rows, and each later row PF rows ahead of its use, so a
 // row's arithmetic waits only for its own bytes while the next ones are arriving.
-template <uint32_t T, int NV, int RMAX, int TPT, int PF, bool CH>
+// NORM: the activations are rmsnorm(x, NW, eps), folded into the conversion (cols % 512 == 0).
+template <uint32_t T, int NV, int RMAX, int TPT, int PF, bool CH, bool NORM>
 __global__ __launch_bounds__(1024) void k_gemv(const uint8_t* __restrict__ W, const float* __restrict__ X,
-                                               float* __restrict__ Y, int rows, int cols, Geo geo) {
+                                               float* __restrict__ Y, int rows, int cols, Geo geo,
+                                               const float* __restrict__ NW, float eps) {
   using L = Lane<T>;
   constexpr int R = L::kR;
   extern __shared__ uint4 xs_lds[];
   __shared__ float red[16][16];  // [output of the group][wave of the group] for groups wider than a wave
+  __shared__ __attribute__((aligned(16))) float sqp[NORM ? NV * kNormMaxChunks : 4];  // chunk sums of squares
   uint32_t* xs = reinterpret_cast<uint32_t*>(xs_lds);
   const int S = geo.S, Sp = geo.Sp, G = geo.G;
   const int sig0 = threadIdx.x, g = threadIdx.y, tid = g * Sp + sig0, nthr = Sp * G;
@@ -513,13 +517,19 @@ __global__ __launch_bounds__(1024) void k_gemv(const uint8_t* __restrict__ W, co
   const uint8_t* wb = W + (size_t)rb * geo.row_bytes;
   const int ntask = NV * S * 2 * R;
 
-  // 1. activations of this thread's conversion tasks
-  float4 xr[TPT][2];
+  // 1. activations of this thread's conversion tasks (and, with NORM, the norm weights beside them)
+  float4 xr[TPT][2], wr[TPT][2];
 #pragma unroll
   for (int k = 0; k < TPT; ++k) {
-    const float4* p = reinterpret_cast<const float4*>(task_x<T, NV>(X, cols, S, min(tid + k * nthr, ntask - 1)));
+    const float* px = task_x<T, NV>(X, cols, S, min(tid + k * nthr, ntask - 1));
+    const float4* p = reinterpret_cast<const float4*>(px);
     xr[k][0] = p[0];
     xr[k][1] = p[1];
+    if constexpr (NORM) {
+      const float4* q = reinterpret_cast<const float4*>(NW + ((px - X) % cols));
+      wr[k][0] = q[0];
+      wr[k][1] = q[1];
+    }
   }
 
   // 2. the quant bytes of the first PF rows (row offsets within the workgroup fit 32 bits)
@@ -528,7 +538,29 @@ __global__ __launch_bounds__(1024) void k_gemv(const uint8_t* __restrict__ W, co
   for (int i = 0; i < PF; ++i) L::load(wb + (uint32_t)min(g + G * i, cnt - 1) * geo.row_bytes, sig, raw[i]);
   __builtin_amdgcn_sched_barrier(0);  // keep the loads here: the scheduler would sink them to their uses
 
-  // 3. fixed-point activations into LDS
+  // 3. (NORM) each vector's sum of squares in the engine's canonical order (512-element chunks,
+  // lane i of a chunk's wave summing elements 8i .. 8i+7; this kernel's conversion tasks are not in
+  // element order, so the chunks are read again, from L2), every task scaled by its vector's factor;
+  // then fixed-point activations into LDS
+  if constexpr (NORM) {
+    const int wave = tid >> 6, lane = tid & 63, nw = nthr >> 6, nch = cols / kNormChunk;
+    const uint32_t sq_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)sqp;
+    for (int q = wave; q < NV * nch; q += nw) {
+      const int v = q / nch, c = q - v * nch;
+      const float4* p = reinterpret_cast<const float4*>(X + (size_t)v * cols + kNormChunk * c + 8 * lane);
+      const float sq = wave_sum64(norm_sq8(p[0], p[1]));
+      if (lane == 0) norm_store(sq_base + 4u * (uint32_t)(v * kNormMaxChunks + c), sq);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    const int per = S * 2 * R;
+#pragma unroll
+    for (int k = 0; k < TPT; ++k) {
+      const int v = min(tid + k * nthr, ntask - 1) / per;
+      const float scale = norm_scale(sq_base + 4u * (uint32_t)(v * kNormMaxChunks), nch, cols, eps);
+      norm_apply(xr[k][0], xr[k][1], scale, wr[k][0], wr[k][1]);
+    }
+  }
 #pragma unroll
   for (int k = 0; k < TPT; ++k) {
     const int t = tid + k * nthr;
@@ -611,27 +643,27 @@ constexpr int prefetch_rows() {
   return T == T_Q6_K ? (NV == 1 ? 2 : 1) : T == T_Q5_K ? 1 : 2;
 }
 
-template <uint32_t T, int NV, int RMAX, int TPT, bool CH>
+template <uint32_t T, int NV, int RMAX, int TPT, bool CH, bool NORM>
 static bool launch_t(const void* w, const float* X, float* Y, int rows, int cols, const Geo& geo, int nwg,
-                     hipStream_t s) {
+                     const GemvEpi& epi, hipStream_t s) {
   constexpr int PF = prefetch_rows<T, NV>() < RMAX ? prefetch_rows<T, NV>() : RMAX;
-  auto kern = &k_gemv<T, NV, RMAX, TPT, PF, CH>;
+  auto kern = &k_gemv<T, NV, RMAX, TPT, PF, CH, NORM>;
   const size_t lds = gemv_lds_bytes<T>(NV, geo.S);
   static LdsLimit lim;
   if (!lds_ready(reinterpret_cast<const void*>(kern), lim, lds)) return false;
   kern<<<(unsigned)nwg, dim3((unsigned)geo.Sp, (unsigned)geo.G), lds, s>>>(static_cast<const uint8_t*>(w), X, Y,
-                                                                           rows, cols, geo);
+                                                                           rows, cols, geo, epi.norm_w, epi.eps);
   return true;
 }
 
 // Rows per group RMAX (1..RM), rounded up to an instantiated value.
-template <uint32_t T, int NV, int TPT, int RM>
+template <uint32_t T, int NV, int TPT, int RM, bool NORM>
 static bool launch_r(int rmax, const void* w, const float* X, float* Y, int rows, int cols, const Geo& geo, int nwg,
-                     hipStream_t s) {
+                     const GemvEpi& epi, hipStream_t s) {
   if constexpr (RM > 1) {
-    if (rmax < RM) return launch_r<T, NV, TPT, RM - 1>(rmax, w, X, Y, rows, cols, geo, nwg, s);
+    if (rmax < RM) return launch_r<T, NV, TPT, RM - 1, NORM>(rmax, w, X, Y, rows, cols, geo, nwg, epi, s);
   }
-  return launch_t<T, NV, RM, TPT, false>(w, X, Y, rows, cols, geo, nwg, s);
+  return launch_t<T, NV, RM, TPT, false, NORM>(w, X, Y, rows, cols, geo, nwg, epi, s);
 }
 
 // Most rows a group takes (its partial sums stay in registers until the end).
@@ -640,8 +672,9 @@ constexpr int max_rows() {
   return NV == 1 && TPT < 8 ? 8 : 4;
 }
 
-template <uint32_t T, int NV, int TPT>
-static bool launch_tpt(const void* w, const float* X, float* Y, int rows, int cols, Geo geo, hipStream_t s) {
+template <uint32_t T, int NV, int TPT, bool NORM>
+static bool launch_tpt(const void* w, const float* X, float* Y, int rows, int cols, Geo geo, const GemvEpi& epi,
+                       hipStream_t s) {
   constexpr int rm = max_rows<NV, TPT>();
   static_assert(rm % prefetch_rows<T, NV>() == 0, "chunks of rm rows keep the prefetch ring aligned");
   const int G = geo.G, waves = geo.Sp * G / 64;
@@ -652,23 +685,30 @@ static bool launch_tpt(const void* w, const float* X, float* Y, int rows, int co
   geo.base = (int)(rows / nwg);
   geo.rem = (int)(rows % nwg);
   const int per_group = (geo.base + (geo.rem ? 1 : 0) + G - 1) / G;
-  if (per_group <= rm) return launch_r<T, NV, TPT, rm>(per_group, w, X, Y, rows, cols, geo, (int)nwg, s);
-  return launch_t<T, NV, rm, TPT, true>(w, X, Y, rows, cols, geo, (int)nwg, s);
+  if (per_group <= rm) return launch_r<T, NV, TPT, rm, NORM>(per_group, w, X, Y, rows, cols, geo, (int)nwg, epi, s);
+  return launch_t<T, NV, rm, TPT, true, NORM>(w, X, Y, rows, cols, geo, (int)nwg, epi, s);
 }
 
-template <uint32_t T, int NV>
-static bool launch_nv(const void* w, const float* X, float* Y, int rows, int cols, const Geo& geo, hipStream_t s) {
+template <uint32_t T, int NV, bool NORM>
+static bool launch_nv2(const void* w, const float* X, float* Y, int rows, int cols, const Geo& geo,
+                       const GemvEpi& epi, hipStream_t s) {
   const int threads = geo.G * geo.Sp;
   const int tpt = (NV * geo.S * 2 * Lane<T>::kR + threads - 1) / threads;
-  if (tpt <= 1) return launch_tpt<T, NV, 1>(w, X, Y, rows, cols, geo, s);
-  if (tpt <= 2) return launch_tpt<T, NV, 2>(w, X, Y, rows, cols, geo, s);
-  if (tpt <= 4) return launch_tpt<T, NV, 4>(w, X, Y, rows, cols, geo, s);
-  return launch_tpt<T, NV, 8>(w, X, Y, rows, cols, geo, s);
+  if (tpt <= 1) return launch_tpt<T, NV, 1, NORM>(w, X, Y, rows, cols, geo, epi, s);
+  if (tpt <= 2) return launch_tpt<T, NV, 2, NORM>(w, X, Y, rows, cols, geo, epi, s);
+  if (tpt <= 4) return launch_tpt<T, NV, 4, NORM>(w, X, Y, rows, cols, geo, epi, s);
+  return launch_tpt<T, NV, 8, NORM>(w, X, Y, rows, cols, geo, epi, s);
+}
+template <uint32_t T, int NV>
+static bool launch_nv(const void* w, const float* X, float* Y, int rows, int cols, const Geo& geo,
+                      const GemvEpi& epi, hipStream_t s) {
+  return epi.norm_w ? launch_nv2<T, NV, true>(w, X, Y, rows, cols, geo, epi, s)
+                    : launch_nv2<T, NV, false>(w, X, Y, rows, cols, geo, epi, s);
 }
 
 template <uint32_t T>
 static bool launch_type(const void* w, const float* X, float* Y, int nvec, int rows, int cols, const Geo& geo,
-                        hipStream_t s) {
+                        const GemvEpi& epi, hipStream_t s) {
   // Q6_K takes four vectors a launch when their activations fit in LDS (its 4-vector kernels
   // stay within the register file; the other formats' would spill), so the weights are streamed
   // once per four vectors instead of once per two.
@@ -679,16 +719,16 @@ static bool launch_type(const void* w, const float* X, float* Y, int nvec, int r
     const int left = nvec - v0;
     if constexpr (T == T_Q6_K) {
       if (nv4 && left >= 4) {
-        if (!launch_nv<T, 4>(w, Xv, Yv, rows, cols, geo, s)) return false;
+        if (!launch_nv<T, 4>(w, Xv, Yv, rows, cols, geo, epi, s)) return false;
         v0 += 4;
         continue;
       }
     }
     if (left >= 2) {
-      if (!launch_nv<T, 2>(w, Xv, Yv, rows, cols, geo, s)) return false;
+      if (!launch_nv<T, 2>(w, Xv, Yv, rows, cols, geo, epi, s)) return false;
       v0 += 2;
     } else {
-      if (!launch_nv<T, 1>(w, Xv, Yv, rows, cols, geo, s)) return false;
+      if (!launch_nv<T, 1>(w, Xv, Yv, rows, cols, geo, epi, s)) return false;
       v0 += 1;
     }
   }
@@ -720,23 +760,42 @@ static bool geometry(int cols, size_t row_bytes, Geo& geo) {
 
 template <uint32_t T>
 static bool launch_fast_t(const void* w, const float* X, float* Y, int nvec, int rows, int cols, size_t row_bytes,
-                          hipStream_t s) {
+                          const GemvEpi& epi, hipStream_t s) {
   Geo geo{};
   if (!geometry<T>(cols, row_bytes, geo)) return false;
-  return launch_type<T>(w, X, Y, nvec, rows, cols, geo, s);
+  if (epi.swiglu) return false;
+  if (epi.norm_w && (cols % kNormChunk != 0 || cols / kNormChunk > kNormMaxChunks)) return false;
+  return launch_type<T>(w, X, Y, nvec, rows, cols, geo, epi, s);
+}
+
+// 1 if launch_gemv_fast takes this shape together with the fused prologue `epi` (RMSNorm only:
+// this kernel's outputs are plain rows), so a fused call can be routed here before anything runs.
+bool gemv_fast_fusable(uint32_t t, int cols, size_t row_bytes, const GemvEpi& epi) {
+  if (epi.swiglu) return false;
+  if (epi.norm_w && (cols % kNormChunk != 0 || cols / kNormChunk > kNormMaxChunks)) return false;
+  Geo geo{};
+  switch (t) {
+    case T_Q4_K: return geometry<T_Q4_K>(cols, row_bytes, geo);
+    case T_Q6_K: return geometry<T_Q6_K>(cols, row_bytes, geo);
+    case T_Q5_K: return geometry<T_Q5_K>(cols, row_bytes, geo);
+    case T_Q4_0: return geometry<T_Q4_0>(cols, row_bytes, geo);
+    case T_Q5_0: return geometry<T_Q5_0>(cols, row_bytes, geo);
+    case T_Q8_0: return geometry<T_Q8_0>(cols, row_bytes, geo);
+    default: return false;
+  }
 }
 
 // Fast-path GEMV for nvec >= 1 on 16-byte-aligned rows of Q8_0 / Q4_0 / Q5_0 / Q4_K / Q5_K / Q6_K.  Returns
 // false, having launched nothing, when the shape needs the generic kernel.
 bool launch_gemv_fast(uint32_t t, const void* w, const float* X, float* Y, int nvec, int rows, int cols,
-                      size_t row_bytes, hipStream_t s) {
+                      size_t row_bytes, const GemvEpi& epi, hipStream_t s) {
   switch (t) {
-    case T_Q4_K: return launch_fast_t<T_Q4_K>(w, X, Y, nvec, rows, cols, row_bytes, s);
-    case T_Q6_K: return launch_fast_t<T_Q6_K>(w, X, Y, nvec, rows, cols, row_bytes, s);
-    case T_Q5_K: return launch_fast_t<T_Q5_K>(w, X, Y, nvec, rows, cols, row_bytes, s);
-    case T_Q4_0: return launch_fast_t<T_Q4_0>(w, X, Y, nvec, rows, cols, row_bytes, s);
-    case T_Q5_0: return launch_fast_t<T_Q5_0>(w, X, Y, nvec, rows, cols, row_bytes, s);
-    case T_Q8_0: return launch_fast_t<T_Q8_0>(w, X, Y, nvec, rows, cols, row_bytes, s);
+    case T_Q4_K: return launch_fast_t<T_Q4_K>(w, X, Y, nvec, rows, cols, row_bytes, epi, s);
+    case T_Q6_K: return launch_fast_t<T_Q6_K>(w, X, Y, nvec, rows, cols, row_bytes, epi, s);
+    case T_Q5_K: return launch_fast_t<T_Q5_K>(w, X, Y, nvec, rows, cols, row_bytes, epi, s);
+    case T_Q4_0: return launch_fast_t<T_Q4_0>(w, X, Y, nvec, rows, cols, row_bytes, epi, s);
+    case T_Q5_0: return launch_fast_t<T_Q5_0>(w, X, Y, nvec, rows, cols, row_bytes, epi, s);
+    case T_Q8_0: return launch_fast_t<T_Q8_0>(w, X, Y, nvec, rows, cols, row_bytes, epi, s);
     default: return false;
   }
 }

@@ -45,6 +45,7 @@
 #include <algorithm>
 
 #include "qvx_common.hpp"
+#include "qvx_norm.hpp"
 
 namespace qvx {
 
@@ -62,7 +63,8 @@ constexpr uint32_t kRsrcWord3 = 0x00020000u;  // raw buffer, 32-bit data (gfx9)
 
 struct MxGeo {
   int nsb;        // super-blocks per row
-  int base, rem;  // workgroup b owns base + (b < rem) rows starting at b*base + min(b, rem)
+  int base, rem;  // workgroup b owns base + unit (b < rem) rows starting at b*base + unit min(b, rem)
+  int unit;       // rows come in whole units: 1, or 32 (a fused SwiGLU launch: 16 gate + 16 up rows)
   int TQ, KQ;     // tiles per workgroup, K splits; TQ * KQ = 16 waves
   uint32_t row_bytes;
 };
@@ -198,6 +200,69 @@ __device__ inline void mx_convert(const float4 x0, const float4 x1, int v, int s
   }
 }
 
+// RMSNorm folded into the conversion (the batched form shares it): each wave's 64 tasks of round k
+// are 512 consecutive elements of one vector (cols % 512 == 0); their sum of squares goes to LDS as
+// chunk (v, c), and after a barrier every task scales its 8 elements by its vector's factor.  Tasks
+// past ntask (clamped duplicates) add nothing.
+template <int TPT>
+__device__ inline void mx_norm(float4 (&xa)[TPT], float4 (&xb)[TPT], const float4 (&wa)[TPT],
+                               const float4 (&wb)[TPT], int tid, int per, int ntask, int cols, float eps,
+                               float* sqp) {
+  const int wave = tid >> 6, lane = tid & 63;
+  const uint32_t sq_base = lds_addr(sqp);
+#pragma unroll
+  for (int k = 0; k < TPT; ++k) {
+    const int tw = 1024 * k + 64 * wave;  // the wave's first task (uniform)
+    if (tw < ntask) {
+      const float s = wave_sum64(tid + 1024 * k < ntask ? norm_sq8(xa[k], xb[k]) : 0.0f);
+      const int v = tw / per, c = (tw - v * per) >> 6;
+      if (lane == 0) norm_store(sq_base + 4u * (uint32_t)(v * kNormMaxChunks + c), s);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+#pragma unroll
+  for (int k = 0; k < TPT; ++k) {
+    if (1024 * k + 64 * wave < ntask) {
+      const int t = min(tid + 1024 * k, ntask - 1), v = t / per;
+      const float scale = norm_scale(sq_base + 4u * (uint32_t)(v * kNormMaxChunks), per >> 6, cols, eps);
+      norm_apply(xa[k], xb[k], scale, wa[k], wb[k]);
+    }
+  }
+}
+
+// Final outputs from the per-wave partials red[tq][kq][v][16] (every K-split wave of a tile, in wave
+// order): plain rows, or with EPI_SWIGLU silu(gate) * up of each (gate tile 2p, up tile 2p + 1)
+// pair, written at output row (rb + 32 p) / 2 + r of the rows / 2 a vector has.
+template <int EPI>
+__device__ inline void mx_store(const float* red, float* Y, int nv, int rows, int rb, int cnt, int TQ, int KQ,
+                                int tid) {
+  if constexpr ((EPI & EPI_SWIGLU) != 0) {
+    const int half = rows >> 1;
+    for (int o = tid; o < (TQ >> 1) * nv * 16; o += 1024) {
+      const int p = o / (nv * 16), v = (o >> 4) % nv, r = o & 15;
+      if (32 * p < cnt) {
+        float g = 0.0f, u = 0.0f;
+        for (int k = 0; k < KQ; ++k) {
+          g += red[((2 * p * KQ + k) * nv + v) * 16 + r];
+          u += red[(((2 * p + 1) * KQ + k) * nv + v) * 16 + r];
+        }
+        Y[(size_t)v * half + (rb >> 1) + 16 * p + r] = silu_mul(g, u);
+      }
+    }
+  } else {
+    for (int o = tid; o < TQ * nv * 16; o += 1024) {
+      const int t = o / (nv * 16), v = (o >> 4) % nv, r = o & 15;
+      const int row = 16 * t + r;
+      if (row < cnt) {
+        float sum = 0.0f;
+        for (int k = 0; k < KQ; ++k) sum += red[((t * KQ + k) * nv + v) * 16 + r];
+        Y[(size_t)v * rows + rb + row] = sum;
+      }
+    }
+  }
+}
+
 // Step u of a K-split wave -> super-block.  Even waves of a split walk their range backwards, odd
 // waves forwards: a 128-byte line that straddles two waves' ranges (super-blocks are 144 bytes, so
 // most split points fall inside a line) is then requested by both waves at the same moment -- at
@@ -219,13 +284,18 @@ __device__ inline void mx_issue(__amdgpu_buffer_rsrc_t rsrc, const uint32_t (&of
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, st + 2048, 4, off[2], so, 0, 0);
 }
 
-template <int NV, int NB, int TPT>
+// EPI: EPI_NORM takes rmsnorm(x, NW, eps) as the activations (folded into the conversion: the
+// workgroup's tasks cover every element of its vectors); EPI_SWIGLU takes rows interleaved in
+// 16-row (gate, up) groups (geo.unit = 32) and writes silu(gate) * up, rows / 2 outputs a vector.
+template <int NV, int NB, int TPT, int EPI>
 __global__ __launch_bounds__(1024) void k_gemv_mx(const uint8_t* __restrict__ W, const float* __restrict__ X,
-                                                  float* __restrict__ Y, int rows, int cols, MxGeo geo) {
+                                                  float* __restrict__ Y, int rows, int cols, MxGeo geo,
+                                                  const float* __restrict__ NW, float eps) {
   static_assert(NB >= 2 && NB <= 4, "the tile wait below covers up to 3 tiles ahead");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   __shared__ __attribute__((aligned(16))) uint8_t ring[16 * NB * kTileBytes];
   __shared__ float red[16 * NV * 16];  // per-wave partial sums [tq][kq][v][16]
+  __shared__ __attribute__((aligned(16))) float sqp[(EPI & EPI_NORM) ? NV * kNormMaxChunks : 4];  // chunk sums
   const int nsb = geo.nsb, TQ = geo.TQ, KQ = geo.KQ;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar offsets, M0
@@ -234,7 +304,7 @@ __global__ __launch_bounds__(1024) void k_gemv_mx(const uint8_t* __restrict__ W,
   QVX_LDS uint8_t* stage = (QVX_LDS uint8_t*)(ring + wave * NB * kTileBytes);
 
   const int b = blockIdx.x;
-  const int rb = b * geo.base + min(b, geo.rem), cnt = geo.base + (b < geo.rem ? 1 : 0);
+  const int rb = b * geo.base + geo.unit * min(b, geo.rem), cnt = geo.base + (b < geo.rem ? geo.unit : 0);
   const int tq = wave % TQ, kq = wave / TQ;
   const int s0 = kq * nsb / KQ, s1 = (kq + 1) * nsb / KQ, nu = s1 - s0;
   const SbOrder order(kq, KQ, s0, s1);
@@ -248,7 +318,7 @@ __global__ __launch_bounds__(1024) void k_gemv_mx(const uint8_t* __restrict__ W,
   // Waves without tasks go straight to their copies.  Every round's loads go out before the first
   // conversion (see the batched form).
   const int per = nsb * 32, ntask = NV * per;
-  float4 xa[TPT], xb[TPT];
+  float4 xa[TPT], xb[TPT], wa[TPT], wb[TPT];
 #pragma unroll
   for (int k = 0; k < TPT; ++k) {
     if (1024 * k + 64 * wave < ntask) {
@@ -256,6 +326,10 @@ __global__ __launch_bounds__(1024) void k_gemv_mx(const uint8_t* __restrict__ W,
       const float4* src = reinterpret_cast<const float4*>(X + (size_t)v * cols + 8 * r);
       xa[k] = src[0];
       xb[k] = src[1];
+      if constexpr ((EPI & EPI_NORM) != 0) {
+        wa[k] = reinterpret_cast<const float4*>(NW + 8 * r)[0];
+        wb[k] = reinterpret_cast<const float4*>(NW + 8 * r)[1];
+      }
     }
   }
   // 2. prologue copies into all NB stages (tiles of super-blocks s0.., repeating the wave's last one
@@ -273,6 +347,7 @@ __global__ __launch_bounds__(1024) void k_gemv_mx(const uint8_t* __restrict__ W,
 #pragma unroll
   for (int u = 0; u < NB; ++u) mx_issue(rsrc, off, nu > 0 ? order(min(u, nu - 1)) : s0, stage + u * kTileBytes);
 
+  if constexpr ((EPI & EPI_NORM) != 0) mx_norm<TPT>(xa, xb, wa, wb, tid, per, ntask, cols, eps, sqp);
 #pragma unroll
   for (int k = 0; k < TPT; ++k) {
     if (1024 * k + 64 * wave < ntask) {
@@ -379,15 +454,7 @@ __global__ __launch_bounds__(1024) void k_gemv_mx(const uint8_t* __restrict__ W,
     for (int v = 0; v < NV; ++v) red[((tq * KQ + kq) * NV + v) * 16 + lane] = acc[v];
   }
   __syncthreads();
-  for (int o = tid; o < TQ * NV * 16; o += 1024) {
-    const int t = o / (NV * 16), v = (o >> 4) % NV, r = o & 15;
-    const int row = 16 * t + r;
-    if (row < cnt) {
-      float sum = 0.0f;
-      for (int k = 0; k < KQ; ++k) sum += red[((t * KQ + k) * NV + v) * 16 + r];
-      Y[(size_t)v * rows + rb + row] = sum;
-    }
-  }
+  mx_store<EPI>(red, Y, NV, rows, rb, cnt, TQ, KQ, tid);
 }
 
 // ---- batched form: 2..8 vectors a launch ------------------------------------------------------
@@ -498,12 +565,15 @@ __device__ inline void mxb_fold(const u32x4& hd, const u32x2 (&qq)[4], const u32
   for (int c = 0; c < 4; ++c) mxb_fold_group(c, hd, qq[c], af[2 * c], af[2 * c + 1], mf[2 * c], mf[2 * c + 1], acc);
 }
 
-template <int TPT>
+// EPI as for k_gemv_mx.
+template <int TPT, int EPI>
 __global__ __launch_bounds__(1024) void k_gemv_mxb(const uint8_t* __restrict__ W, const float* __restrict__ X,
-                                                   float* __restrict__ Y, int rows, int cols, int nv, MxGeo geo) {
+                                                   float* __restrict__ Y, int rows, int cols, int nv, MxGeo geo,
+                                                   const float* __restrict__ NW, float eps) {
   constexpr int NB = 2;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   __shared__ __attribute__((aligned(16))) uint8_t ring[16 * NB * kTileBytes];
+  __shared__ __attribute__((aligned(16))) float sqp[(EPI & EPI_NORM) ? 8 * kNormMaxChunks : 4];  // chunk sums
   const int nsb = geo.nsb, TQ = geo.TQ, KQ = geo.KQ;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -512,7 +582,7 @@ __global__ __launch_bounds__(1024) void k_gemv_mxb(const uint8_t* __restrict__ W
   QVX_LDS uint8_t* stage = (QVX_LDS uint8_t*)(ring + wave * NB * kTileBytes);
 
   const int b = blockIdx.x;
-  const int rb = b * geo.base + min(b, geo.rem), cnt = geo.base + (b < geo.rem ? 1 : 0);
+  const int rb = b * geo.base + geo.unit * min(b, geo.rem), cnt = geo.base + (b < geo.rem ? geo.unit : 0);
   const int tq = wave % TQ, kq = wave / TQ;
   const int s0 = kq * nsb / KQ, s1 = (kq + 1) * nsb / KQ, nu = s1 - s0;
   const SbOrder order(kq, KQ, s0, s1);
@@ -522,7 +592,7 @@ __global__ __launch_bounds__(1024) void k_gemv_mxb(const uint8_t* __restrict__ W
   // clobber) would otherwise keep each round's loads behind the previous round's stores, one memory
   // latency per round.
   const int per = nsb * 32, ntask = nv * per;
-  float4 xa[TPT], xb[TPT];
+  float4 xa[TPT], xb[TPT], wa[TPT], wb[TPT];
 #pragma unroll
   for (int k = 0; k < TPT; ++k) {
     if (1024 * k + 64 * wave < ntask) {
@@ -530,8 +600,13 @@ __global__ __launch_bounds__(1024) void k_gemv_mxb(const uint8_t* __restrict__ W
       const float4* src = reinterpret_cast<const float4*>(X + (size_t)v * cols + 8 * r);
       xa[k] = src[0];
       xb[k] = src[1];
+      if constexpr ((EPI & EPI_NORM) != 0) {
+        wa[k] = reinterpret_cast<const float4*>(NW + 8 * r)[0];
+        wb[k] = reinterpret_cast<const float4*>(NW + 8 * r)[1];
+      }
     }
   }
+  if constexpr ((EPI & EPI_NORM) != 0) mx_norm<TPT>(xa, xb, wa, wb, tid, per, ntask, cols, eps, sqp);
 #pragma unroll
   for (int k = 0; k < TPT; ++k) {
     if (1024 * k + 64 * wave < ntask) {
@@ -609,15 +684,7 @@ __global__ __launch_bounds__(1024) void k_gemv_mxb(const uint8_t* __restrict__ W
     if (v < nv) red[((tq * KQ + kq) * nv + v) * 16 + j] = (acc[e][0] + acc[e][2]) + (acc[e][1] + acc[e][3]);
   }
   __syncthreads();
-  for (int o = tid; o < TQ * nv * 16; o += 1024) {
-    const int t = o / (nv * 16), v = (o >> 4) % nv, r = o & 15;
-    const int row = 16 * t + r;
-    if (row < cnt) {
-      float sum = 0.0f;
-      for (int k = 0; k < KQ; ++k) sum += red[((t * KQ + k) * nv + v) * 16 + r];
-      Y[(size_t)v * rows + rb + row] = sum;
-    }
-  }
+  mx_store<EPI>(red, Y, nv, rows, rb, cnt, TQ, KQ, tid);
 }
 
 // ---- batched form for long rows -----------------------------------------------------------------
@@ -704,7 +771,7 @@ __global__ __launch_bounds__(1024) void k_gemv_mxj(const uint8_t* __restrict__ W
   QVX_LDS uint8_t* stage = (QVX_LDS uint8_t*)(ring + wave * NB * kTileBytes);
 
   const int b = blockIdx.x;
-  const int rb = b * geo.base + min(b, geo.rem), cnt = geo.base + (b < geo.rem ? 1 : 0);
+  const int rb = b * geo.base + geo.unit * min(b, geo.rem), cnt = geo.base + (b < geo.rem ? geo.unit : 0);
   const int tq = wave % TQ, kq = wave / TQ;
   const int s0 = kq * nsb / KQ, s1 = (kq + 1) * nsb / KQ, nu = s1 - s0;
   const SbOrder order(kq, KQ, s0, s1);
@@ -794,15 +861,26 @@ __global__ __launch_bounds__(1024) void k_gemv_mxj(const uint8_t* __restrict__ W
 constexpr int kCUs = 256;
 constexpr size_t kLdsMax = kLdsPerCU;
 
-template <int NV, int NB, int TPT>
+template <int NV, int NB, int TPT, int EPI>
 static bool launch_mx(const void* w, const float* X, float* Y, int rows, int cols, const MxGeo& geo, int nwg,
-                      hipStream_t s) {
-  auto kern = &k_gemv_mx<NV, NB, TPT>;
+                      const GemvEpi& epi, hipStream_t s) {
+  auto kern = &k_gemv_mx<NV, NB, TPT, EPI>;
   const size_t lds = mx_dyn_bytes(NV, geo.nsb);
   static LdsLimit lim;
   if (!lds_ready(reinterpret_cast<const void*>(kern), lim, lds)) return false;
-  kern<<<(unsigned)nwg, 1024u, lds, s>>>(static_cast<const uint8_t*>(w), X, Y, rows, cols, geo);
+  kern<<<(unsigned)nwg, 1024u, lds, s>>>(static_cast<const uint8_t*>(w), X, Y, rows, cols, geo, epi.norm_w, epi.eps);
   return true;
+}
+
+template <int NV, int NB, int TPT>
+static bool launch_mx_epi(const void* w, const float* X, float* Y, int rows, int cols, const MxGeo& geo, int nwg,
+                          const GemvEpi& epi, hipStream_t s) {
+  switch (epi.flags()) {
+    case 0: return launch_mx<NV, NB, TPT, 0>(w, X, Y, rows, cols, geo, nwg, epi, s);
+    case EPI_NORM: return launch_mx<NV, NB, TPT, EPI_NORM>(w, X, Y, rows, cols, geo, nwg, epi, s);
+    case EPI_SWIGLU: return launch_mx<NV, NB, TPT, EPI_SWIGLU>(w, X, Y, rows, cols, geo, nwg, epi, s);
+    default: return launch_mx<NV, NB, TPT, EPI_NORM | EPI_SWIGLU>(w, X, Y, rows, cols, geo, nwg, epi, s);
+  }
 }
 
 // Two stages per wave (two tiles in flight behind the one being folded).  Deeper rings only
@@ -810,23 +888,28 @@ static bool launch_mx(const void* w, const float* X, float* Y, int rows, int col
 // request queue is full.  TPT = activation conversion tasks per thread.
 template <int NV>
 static bool launch_mx_nv(const void* w, const float* X, float* Y, int rows, int cols, const MxGeo& geo, int nwg,
-                         hipStream_t s) {
+                         const GemvEpi& epi, hipStream_t s) {
   const int tpt = (NV * geo.nsb * 32 + 1023) / 1024;
-  if (tpt <= 1) return launch_mx<NV, 2, 1>(w, X, Y, rows, cols, geo, nwg, s);
-  if (tpt <= 2) return launch_mx<NV, 2, 2>(w, X, Y, rows, cols, geo, nwg, s);
-  return launch_mx<NV, 2, 4>(w, X, Y, rows, cols, geo, nwg, s);
+  if (tpt <= 1) return launch_mx_epi<NV, 2, 1>(w, X, Y, rows, cols, geo, nwg, epi, s);
+  if (tpt <= 2) return launch_mx_epi<NV, 2, 2>(w, X, Y, rows, cols, geo, nwg, epi, s);
+  return launch_mx_epi<NV, 2, 4>(w, X, Y, rows, cols, geo, nwg, epi, s);
 }
 
-// Launch geometry shared by both forms (the batched form's bit-identity rests on it): one
-// workgroup of 16 waves per CU; tiles of 16 rows; TQ tiles x KQ K-splits per workgroup.
-static int mx_geometry(int rows, int cols, size_t row_bytes, MxGeo& geo) {
+// Launch geometry shared by all three forms (the batched forms' bit-identity rests on it): one
+// workgroup of 16 waves per CU; tiles of 16 rows; TQ tiles x KQ K-splits per workgroup.  Rows are
+// dealt in whole units (unit = 32 for a fused SwiGLU launch, rows % 32 == 0, so every workgroup
+// holds whole (gate, up) tile pairs).
+static int mx_geometry(int rows, int cols, size_t row_bytes, MxGeo& geo, int unit = 1) {
   geo.nsb = cols / 256;
   geo.row_bytes = (uint32_t)row_bytes;
+  geo.unit = unit;
+  const int units = rows / unit;
   int64_t nwg = std::min<int64_t>(kCUs, ((int64_t)rows + 15) / 16);
   nwg = std::max<int64_t>(nwg, ((int64_t)rows + 255) / 256);
-  geo.base = (int)(rows / nwg);
-  geo.rem = (int)(rows % nwg);
-  const int per = geo.base + (geo.rem ? 1 : 0);
+  nwg = std::min<int64_t>(nwg, units);
+  geo.base = (int)(units / nwg) * unit;
+  geo.rem = (int)(units % nwg);
+  const int per = geo.base + (geo.rem ? unit : 0);
   int tq = 1;
   while (16 * tq < per) tq <<= 1;
   geo.TQ = tq;
@@ -834,15 +917,27 @@ static int mx_geometry(int rows, int cols, size_t row_bytes, MxGeo& geo) {
   return (int)nwg;
 }
 
-template <int TPT>
+template <int TPT, int EPI>
 static bool launch_mxb(const void* w, const float* X, float* Y, int nv, int rows, int cols, const MxGeo& geo, int nwg,
-                       hipStream_t s) {
-  auto kern = &k_gemv_mxb<TPT>;
+                       const GemvEpi& epi, hipStream_t s) {
+  auto kern = &k_gemv_mxb<TPT, EPI>;
   const size_t lds = mxb_dyn_bytes(geo.nsb);
   static LdsLimit lim;
   if (!lds_ready(reinterpret_cast<const void*>(kern), lim, lds)) return false;
-  kern<<<(unsigned)nwg, 1024u, lds, s>>>(static_cast<const uint8_t*>(w), X, Y, rows, cols, nv, geo);
+  kern<<<(unsigned)nwg, 1024u, lds, s>>>(static_cast<const uint8_t*>(w), X, Y, rows, cols, nv, geo, epi.norm_w,
+                                         epi.eps);
   return true;
+}
+
+template <int TPT>
+static bool launch_mxb_epi(const void* w, const float* X, float* Y, int nv, int rows, int cols, const MxGeo& geo,
+                           int nwg, const GemvEpi& epi, hipStream_t s) {
+  switch (epi.flags()) {
+    case 0: return launch_mxb<TPT, 0>(w, X, Y, nv, rows, cols, geo, nwg, epi, s);
+    case EPI_NORM: return launch_mxb<TPT, EPI_NORM>(w, X, Y, nv, rows, cols, geo, nwg, epi, s);
+    case EPI_SWIGLU: return launch_mxb<TPT, EPI_SWIGLU>(w, X, Y, nv, rows, cols, geo, nwg, epi, s);
+    default: return launch_mxb<TPT, EPI_NORM | EPI_SWIGLU>(w, X, Y, nv, rows, cols, geo, nwg, epi, s);
+  }
 }
 
 template <int NVT>
@@ -857,6 +952,14 @@ static bool launch_mxj(const uint8_t* w, const float* X, float* Y, int nv, int r
 
 }  // namespace
 
+// 1 if the fused prologue / epilogue can run on this shape: the norm needs whole 512-element
+// chunks (at most kNormMaxChunks), SwiGLU whole 32-row (gate, up) groups.
+bool mx_epi_supported(const GemvEpi& epi, int rows, int cols) {
+  if (epi.norm_w && (cols % kNormChunk != 0 || cols / kNormChunk > kNormMaxChunks)) return false;
+  if (epi.swiglu && rows % 32 != 0) return false;
+  return true;
+}
+
 // 1 if the batched form takes `cols` (its 8-vector fragments fit in LDS with the tile ring).
 int gemv_mxb_supported(int cols) {
   if (cols <= 0 || cols % 256 != 0) return 0;
@@ -867,14 +970,15 @@ int gemv_mxb_supported(int cols) {
 // Q4_K GEMV on the matrix cores, 1 <= nvec <= 8 vectors, batched form.  Returns false, having
 // launched nothing, when the shape is not handled here.
 bool launch_gemv_mxb_q4k(const void* w, const float* X, float* Y, int nvec, int rows, int cols, size_t row_bytes,
-                         hipStream_t s) {
+                         const GemvEpi& epi, hipStream_t s) {
   if (!gemv_mxb_supported(cols) || nvec < 1 || nvec > 8 || row_bytes >= (1u << 24)) return false;
+  if (!mx_epi_supported(epi, rows, cols)) return false;
   MxGeo geo{};
-  const int nwg = mx_geometry(rows, cols, row_bytes, geo);
+  const int nwg = mx_geometry(rows, cols, row_bytes, geo, epi.swiglu ? 32 : 1);
   const int tpt = (nvec * geo.nsb * 32 + 1023) / 1024;
-  if (tpt <= 1) return launch_mxb<1>(w, X, Y, nvec, rows, cols, geo, nwg, s);
-  if (tpt <= 2) return launch_mxb<2>(w, X, Y, nvec, rows, cols, geo, nwg, s);
-  return launch_mxb<4>(w, X, Y, nvec, rows, cols, geo, nwg, s);
+  if (tpt <= 1) return launch_mxb_epi<1>(w, X, Y, nvec, rows, cols, geo, nwg, epi, s);
+  if (tpt <= 2) return launch_mxb_epi<2>(w, X, Y, nvec, rows, cols, geo, nwg, epi, s);
+  return launch_mxb_epi<4>(w, X, Y, nvec, rows, cols, geo, nwg, epi, s);
 }
 
 // 1 if the long-row batched form takes `cols`: whole super-blocks, and the one-vector kernel takes
@@ -911,20 +1015,21 @@ int gemv_mx_max_nv(int cols) {
 // Q4_K GEMV on the matrix cores for 1 <= nvec <= gemv_mx_max_nv(cols).  Returns false, having
 // launched nothing, when the shape is not handled here.
 bool launch_gemv_mx_q4k(const void* w, const float* X, float* Y, int nvec, int rows, int cols, size_t row_bytes,
-                        hipStream_t s) {
+                        const GemvEpi& epi, hipStream_t s) {
   const int maxnv = gemv_mx_max_nv(cols);
   if (maxnv == 0 || nvec < 1 || nvec > maxnv || row_bytes >= (1u << 24)) return false;
+  if (!mx_epi_supported(epi, rows, cols)) return false;
   MxGeo geo{};
-  const int nwg = mx_geometry(rows, cols, row_bytes, geo);
+  const int nwg = mx_geometry(rows, cols, row_bytes, geo, epi.swiglu ? 32 : 1);
   switch (nvec) {
-    case 1: return launch_mx_nv<1>(w, X, Y, rows, cols, geo, nwg, s);
-    case 2: return launch_mx_nv<2>(w, X, Y, rows, cols, geo, nwg, s);
-    case 3: return launch_mx_nv<3>(w, X, Y, rows, cols, geo, nwg, s);
-    case 4: return launch_mx_nv<4>(w, X, Y, rows, cols, geo, nwg, s);
-    case 5: return launch_mx_nv<5>(w, X, Y, rows, cols, geo, nwg, s);
-    case 6: return launch_mx_nv<6>(w, X, Y, rows, cols, geo, nwg, s);
-    case 7: return launch_mx_nv<7>(w, X, Y, rows, cols, geo, nwg, s);
-    default: return launch_mx_nv<8>(w, X, Y, rows, cols, geo, nwg, s);
+    case 1: return launch_mx_nv<1>(w, X, Y, rows, cols, geo, nwg, epi, s);
+    case 2: return launch_mx_nv<2>(w, X, Y, rows, cols, geo, nwg, epi, s);
+    case 3: return launch_mx_nv<3>(w, X, Y, rows, cols, geo, nwg, epi, s);
+    case 4: return launch_mx_nv<4>(w, X, Y, rows, cols, geo, nwg, epi, s);
+    case 5: return launch_mx_nv<5>(w, X, Y, rows, cols, geo, nwg, epi, s);
+    case 6: return launch_mx_nv<6>(w, X, Y, rows, cols, geo, nwg, epi, s);
+    case 7: return launch_mx_nv<7>(w, X, Y, rows, cols, geo, nwg, epi, s);
+    default: return launch_mx_nv<8>(w, X, Y, rows, cols, geo, nwg, epi, s);
   }
 }
 

@@ -9,17 +9,24 @@ engine's kernels pick the format.  A token's projections are recorded into a ``P
 graph, ``qvx_plan_*`` in ``include/qvx.h``) and replayed with one launch, as the CUDA backend
 replays its captured decode step.
 
-Only the matmuls are issued: RMSNorm, RoPE, attention and SwiGLU are not part of this engine, so
-their outputs are stand-in activation buffers (seeded N(0,1)) of the right shapes.  This is the
+``DecodeStep`` issues only the matmuls: RMSNorm, RoPE, attention and SwiGLU are outside it, so their
+outputs are stand-in activation buffers (seeded N(0,1)) of the right shapes.  This is the
 "full-model decode weight sweep" workload: 32 layers x 7 projections + the LM head = 225 GEMVs and
 4,875,853,824 weight bytes per token for Llama-3-8B Q4_K_M.
+
+``FusedDecodeStep`` runs the same weights with the decoder ops the engine owns folded into the
+GEMVs (``qvx_qmatmul_n_rmsnorm``, ``qvx_qmatmul_swiglu``): per layer q|k and v on rmsnorm(x,
+attn_norm), o on the attention output, gate|up on rmsnorm(x, ffn_norm) with the SwiGLU epilogue,
+down on that SwiGLU output, and the LM head on rmsnorm(x, output_norm) -- 5 launches a layer.  RoPE,
+attention and the residual adds stay outside, so the hidden state x and the attention output are
+stand-ins; the FFN's SwiGLU activation is the engine's own.
 """
 from __future__ import annotations
 
 import ctypes as C
 from dataclasses import dataclass, field
 
-from . import (GEMM_F16, OK, Q4_K, Q6_K, QvxError, empty_weight, fill_normal_t, fill_synthetic_t, lib,
+from . import (F32, GEMM_F16, OK, Q4_K, Q6_K, QvxError, empty_weight, fill_normal_t, fill_synthetic_t, lib,
                weight_bytes)
 
 
@@ -84,19 +91,26 @@ def sweep_bytes(m: int, n_layers: int = N_LAYERS, lm_head: bool = True):
     return wb, ab
 
 
+NORM_EPS = 1e-5  # Llama-3 rms_norm_eps (the GGUF key llama.attention.layer_norm_rms_epsilon)
+
+
 @dataclass
 class Model:
-    """Synthetic Llama-3-8B Q4_K_M weights on the device (``layers[l][name]``, ``lm_head``)."""
+    """Synthetic Llama-3-8B Q4_K_M weights on the device (``layers[l][name]``, ``lm_head``) and the
+    RMSNorm weights (``norms[l]`` = {"attn_norm", "ffn_norm"} fp32 [d], ``output_norm``)."""
     layers: list = field(default_factory=list)
     lm_head: DevWeight | None = None
     # name of a stacked weight -> ((part name, rows), ...) in row order (see FUSED)
     parts: dict = field(default_factory=dict)
+    norms: list = field(default_factory=list)
+    output_norm: object = None
+    eps: float = NORM_EPS
 
     def fused(self) -> "Model":
         """The same weights with each FUSED pair of a layer stacked into one device weight when the
         two share type and row length (the other projections are shared, not copied)."""
         import torch
-        m = Model(lm_head=self.lm_head)
+        m = Model(lm_head=self.lm_head, norms=self.norms, output_norm=self.output_norm, eps=self.eps)
         for layer in self.layers:
             out, used = {}, set()
             for name, (a, b) in FUSED:
@@ -107,6 +121,27 @@ class Model:
                 m.parts[name] = ((a, wa.rows), (b, wb.rows))
                 used.update((a, b))
             out.update({k: w for k, w in layer.items() if k not in used})
+            m.layers.append(out)
+        return m
+
+    def fused_ops(self) -> "Model":
+        """The weights as FusedDecodeStep reads them: q and k stacked (as ``fused``), gate and up
+        interleaved in 16-row groups (``qvx_interleave_rows16``, the layout of the SwiGLU epilogue),
+        the rest shared."""
+        import torch
+        from . import interleave_rows16_t
+        m = Model(lm_head=self.lm_head, norms=self.norms, output_norm=self.output_norm, eps=self.eps)
+        for layer in self.layers:
+            out = {k: w for k, w in layer.items() if k not in ("wq", "wk", "ffn_gate", "ffn_up")}
+            wq, wk, wg, wu = layer["wq"], layer["wk"], layer["ffn_gate"], layer["ffn_up"]
+            if wq.type == wk.type and wq.cols == wk.cols:
+                out["wqk"] = DevWeight(torch.cat([wq.data, wk.data]), wq.type, wq.rows + wk.rows, wq.cols)
+            else:
+                out["wq"], out["wk"] = wq, wk
+            if wg.type != wu.type or wg.rows != wu.rows or wg.cols != wu.cols or wg.rows % 16:
+                raise ValueError("gate and up must share type and shape (rows a multiple of 16) to interleave")
+            out["ffn_gateup"] = DevWeight(interleave_rows16_t(wg.data, wu.data, wg.type, wg.rows, wg.cols), wg.type,
+                                          2 * wg.rows, wg.cols)
             m.layers.append(out)
         return m
 
@@ -127,7 +162,11 @@ class Model:
     @staticmethod
     def synthetic(n_layers: int = N_LAYERS, lm_head: bool = True, seed: int = 5, device="cuda") -> "Model":
         """Fresh seed per (layer, tensor); scales fp16(|N(0,1)| * 1e-3) as the configs specify."""
+        import torch
         m = Model()
+        for l in range(n_layers):
+            m.norms.append({k: _norm_weight(D_MODEL, _tensor_seed(seed, l, k), device) for k in ("attn_norm", "ffn_norm")})
+        m.output_norm = _norm_weight(D_MODEL, _tensor_seed(seed, n_layers, "output_norm"), device)
         for l, name, rows, cols, t, _ in sweep_specs(n_layers, lm_head):
             w = DevWeight(empty_weight(t, rows, cols, device), t, rows, cols)
             fill_synthetic_t(w.data, t, rows, cols, seed=_tensor_seed(seed, l, name), scale_mul=1e-3)
@@ -175,10 +214,24 @@ class Model:
                   "ffn_up": (ffn, d), "ffn_down": (d, ffn)}
         names = {"wq": "attn_q", "wk": "attn_k", "wv": "attn_v", "wo": "attn_output", "ffn_gate": "ffn_gate",
                  "ffn_up": "ffn_up", "ffn_down": "ffn_down"}
+        def load_norm(name):
+            t = f.tensor(name)
+            if t is None:
+                return None
+            if t.type_raw != F32 or t.n_elements != d:
+                raise ValueError(f"norm tensor '{name}' must be F32 with {d} elements")
+            import torch
+            return f.upload(name, device).data.view(torch.float32)
+
         for layer in range(n_layers):
             m.layers.append({k: load(f"blk.{layer}.{names[k]}.weight", *shapes[k]) for k, *_ in LAYER_SPECS})
+            m.norms.append({"attn_norm": load_norm(f"blk.{layer}.attn_norm.weight"),
+                            "ffn_norm": load_norm(f"blk.{layer}.ffn_norm.weight")})
         head = "output.weight" if f.tensor("output.weight") is not None else "token_embd.weight"
         m.lm_head = load(head, None, d)
+        m.output_norm = load_norm("output_norm.weight")
+        eps = f.get_f64(f"{f.architecture}.attention.layer_norm_rms_epsilon") if f.architecture else None
+        m.eps = float(eps) if eps is not None else NORM_EPS
         return m
 
     @property
@@ -193,8 +246,16 @@ def _input_widths(model: Model) -> dict:
 
 
 def _tensor_seed(seed: int, layer: int, name: str) -> int:
-    names = [s[0] for s in LAYER_SPECS] + [LM_HEAD[0]]
+    names = [s[0] for s in LAYER_SPECS] + [LM_HEAD[0], "attn_norm", "ffn_norm", "output_norm"]
     return (seed << 20) + (layer << 4) + names.index(name)
+
+
+def _norm_weight(n: int, seed: int, device):
+    """A synthetic RMSNorm weight: 1 + 0.1 N(0,1) (trained Llama norm weights sit around 1)."""
+    import torch
+    w = torch.empty(n, dtype=torch.float32, device=device)
+    fill_normal_t(w, seed=seed, mul=0.1)
+    return w.add_(1.0)
 
 
 class Plan:
@@ -212,6 +273,22 @@ class Plan:
                                           w.rows, w.cols)
         if rc != OK:
             raise QvxError(rc, "qvx_plan_add_qmatmul_n")
+
+    def add_rmsnorm(self, out, w: DevWeight, X, norm_w, eps: float, nvec: int) -> None:
+        """out = W . rmsnorm(X) (``qvx_plan_add_qmatmul_n_rmsnorm``)."""
+        rc = lib().qvx_plan_add_qmatmul_n_rmsnorm(self._h, out.data_ptr(), w.data.data_ptr(), w.type, X.data_ptr(),
+                                                  norm_w.data_ptr(), eps, nvec, w.rows, w.cols)
+        if rc != OK:
+            raise QvxError(rc, "qvx_plan_add_qmatmul_n_rmsnorm")
+
+    def add_swiglu(self, out, w_gu: DevWeight, X, norm_w, eps: float, nvec: int) -> None:
+        """out = silu(W_gate . xn) * (W_up . xn) over an interleaved gate|up weight
+        (``qvx_plan_add_qmatmul_swiglu``; xn = rmsnorm(X) when norm_w is given)."""
+        nw = norm_w.data_ptr() if norm_w is not None else None
+        rc = lib().qvx_plan_add_qmatmul_swiglu(self._h, out.data_ptr(), w_gu.data.data_ptr(), w_gu.type,
+                                               X.data_ptr(), nw, eps, nvec, w_gu.rows // 2, w_gu.cols)
+        if rc != OK:
+            raise QvxError(rc, "qvx_plan_add_qmatmul_swiglu")
 
     def fork(self) -> None:
         rc = lib().qvx_plan_fork(self._h)
@@ -285,6 +362,106 @@ class DecodeStep:
 
     def run_eager(self, stream: int) -> None:
         self.plan.run_eager(stream)
+
+
+class FusedDecodeStep:
+    """One decode step at M vectors with the engine's fused decoder ops (5 launches a layer + the LM
+    head), in the reference's order (text_model.cpp:146-177) on a ``Model.fused_ops()`` model:
+    per layer qk = Wqk . rmsnorm(x, attn_norm) and v = Wv . rmsnorm(x, attn_norm) (text_model.cpp:
+    146-149), o = Wo . attn (:158), h = swiglu(Wgate . xn, Wup . xn) with xn = rmsnorm(x, ffn_norm)
+    (:161-165), down = Wdown . h (:166); logits = Wlm . rmsnorm(x, output_norm) (:171-172).  x (the
+    residual stream) and attn (the attention output) are seeded stand-ins, h is the SwiGLU output
+    the step itself computes; one output buffer per projection, reused across layers."""
+
+    def __init__(self, model: Model, m: int, seed: int = 9, device="cuda"):
+        import torch
+        self.model, self.m = model, m
+        f32 = dict(dtype=torch.float32, device=device)
+        l0 = model.layers[0]
+        d = l0["wo"].rows
+        self.x = fill_normal_t(torch.empty((m, d), **f32), seed=seed)
+        self.attn = fill_normal_t(torch.empty((m, l0["wo"].cols), **f32), seed=seed + 1)
+        self.out = {k: torch.empty((m, w.rows), **f32) for k, w in l0.items() if k != "ffn_gateup"}
+        self.h = torch.empty((m, l0["ffn_gateup"].rows // 2), **f32)
+        self.logits = torch.empty((m, model.lm_head.rows), **f32) if model.lm_head is not None else None
+        self.plan = Plan()
+        eps = model.eps
+        for l, layer in enumerate(model.layers):
+            an, fn = model.norms[l]["attn_norm"], model.norms[l]["ffn_norm"]
+            for k in ("wqk", "wq", "wk", "wv"):
+                if k in layer:
+                    self.plan.add_rmsnorm(self.out[k], layer[k], self.x, an, eps, m)
+            self.plan.add(self.out["wo"], layer["wo"], self.attn, m)
+            self.plan.add_swiglu(self.h, layer["ffn_gateup"], self.x, fn, eps, m)
+            self.plan.add(self.out["ffn_down"], layer["ffn_down"], self.h, m)
+        if model.lm_head is not None:
+            self.plan.add_rmsnorm(self.logits, model.lm_head, self.x, model.output_norm, eps, m)
+        self.plan.instantiate()
+
+    def launches(self) -> int:
+        return len(self.plan)
+
+    def replay(self, stream: int) -> None:
+        self.plan.launch(stream)
+
+    def run_eager(self, stream: int) -> None:
+        self.plan.run_eager(stream)
+
+
+class OpsDecodeStep:
+    """The same decode step as FusedDecodeStep issued as the reference's op sequence, one launch per
+    op (text_model.cpp:146-177): per layer rmsnorm, wq, wk, wv, wo, rmsnorm, ffn_gate, ffn_up, swiglu,
+    ffn_down (10 launches) and rmsnorm + the LM head -- the engine's standalone qvx_rmsnorm /
+    qvx_swiglu beside the plain GEMVs, on a plain (unstacked) model.  ``capture`` records it into one
+    graph (torch.cuda.CUDAGraph; nothing allocates), the baseline the fused step is measured against."""
+
+    def __init__(self, model: Model, m: int, seed: int = 9, device="cuda"):
+        import torch
+        self.model, self.m = model, m
+        f32 = dict(dtype=torch.float32, device=device)
+        l0 = model.layers[0]
+        d = l0["wo"].rows
+        self.x = fill_normal_t(torch.empty((m, d), **f32), seed=seed)
+        self.attn = fill_normal_t(torch.empty((m, l0["wo"].cols), **f32), seed=seed + 1)
+        self.xn = torch.empty((m, d), **f32)
+        self.out = {k: torch.empty((m, w.rows), **f32) for k, w in l0.items()}
+        self.h = torch.empty((m, l0["ffn_gate"].rows), **f32)
+        self.logits = torch.empty((m, model.lm_head.rows), **f32) if model.lm_head is not None else None
+        self.graph = None
+
+    def run(self, stream: int) -> None:
+        from . import _check
+        so, m, eps = lib(), self.m, self.model.eps
+
+        def norm(w):
+            _check(so.qvx_rmsnorm(self.xn.data_ptr(), self.x.data_ptr(), w.data_ptr(), eps, m, self.x.shape[1],
+                                  stream), "qvx_rmsnorm")
+
+        for l, layer in enumerate(self.model.layers):
+            norm(self.model.norms[l]["attn_norm"])
+            for k in ("wq", "wk", "wv"):
+                wmatmul_n(self.out[k], layer[k], self.xn, m, stream)
+            wmatmul_n(self.out["wo"], layer["wo"], self.attn, m, stream)
+            norm(self.model.norms[l]["ffn_norm"])
+            wmatmul_n(self.out["ffn_gate"], layer["ffn_gate"], self.xn, m, stream)
+            wmatmul_n(self.out["ffn_up"], layer["ffn_up"], self.xn, m, stream)
+            _check(so.qvx_swiglu(self.h.data_ptr(), self.out["ffn_gate"].data_ptr(), self.out["ffn_up"].data_ptr(),
+                                 self.h.numel(), stream), "qvx_swiglu")
+            wmatmul_n(self.out["ffn_down"], layer["ffn_down"], self.h, m, stream)
+        if self.model.lm_head is not None:
+            norm(self.model.output_norm)
+            wmatmul_n(self.logits, self.model.lm_head, self.xn, m, stream)
+
+    def capture(self) -> None:
+        import torch
+        self.run(torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.run(torch.cuda.current_stream().cuda_stream)
+
+    def replay(self, stream: int = 0) -> None:
+        self.graph.replay()
 
 
 def wgemm(out, w: DevWeight, X16, m: int, stream: int, variant: int = GEMM_F16, noalloc: bool = False) -> None:

@@ -190,3 +190,85 @@ def test_fused_prefill_matches_unfused(cuda, small_model):
                 r0 += rows
         else:
             assert max_rel(y.cpu().numpy(), a.outputs[name].cpu().numpy()) <= 1e-6, name
+
+
+@pytest.mark.parametrize("m", [1, 8])
+def test_fused_ops_step(cuda, small_model, m):
+    """The decode step with the engine's fused ops (5 launches a layer + the LM head): graph replays
+    equal the eager run bit for bit, and the last layer's outputs agree with the oracle -- q|k and v
+    against the fp64 product of rmsnorm(x, attn_norm) (ops.cpp:8-13), the SwiGLU activation against
+    silu(g) * u of the fp64 gate / up products of rmsnorm(x, ffn_norm) on a slice of its features,
+    ffn_down against the fp64 product of that activation, the LM head against rmsnorm(x,
+    output_norm)."""
+    torch = cuda
+    fm = small_model.fused_ops()
+    step = decode.FusedDecodeStep(fm, m, seed=40 + m)
+    assert step.launches() == 2 * 5 + 1
+    s = torch.cuda.current_stream().cuda_stream
+    step.run_eager(s)
+    torch.cuda.synchronize()
+    bufs = lambda: [*step.out.values(), step.h, step.logits]
+    ref = [b.clone() for b in bufs()]
+    for rep in range(3):
+        for b in bufs():
+            b.fill_(float("nan"))
+        step.replay(s)
+        torch.cuda.synchronize()
+        for b, r in zip(bufs(), ref):
+            assert torch.equal(b.view(torch.int32), r.view(torch.int32)), rep
+    x = step.x.cpu().numpy()
+    eps = fm.eps
+    last = fm.layers[-1]
+    norms = fm.norms[-1]
+    xa = oracle.rmsnorm(x, norms["attn_norm"].cpu().numpy(), eps)
+    xf = oracle.rmsnorm(x, norms["ffn_norm"].cpu().numpy(), eps)
+
+    def rows_of(w, r0, nr):
+        rb = qvx.row_bytes(w.type, w.cols)
+        return w.data[r0 * rb:(r0 + nr) * rb].cpu().numpy()
+
+    for k, xin in (("wqk", xa), ("wv", xa)):
+        w = last[k]
+        r0 = (w.rows // 3) & ~15
+        got = step.out[k][:, r0:r0 + 48].cpu().numpy()
+        assert max_rel(got, oracle.matmul_f64(rows_of(w, r0, 48), w.type, xin, m, 48, w.cols)) <= 1e-3, k
+    gu = last["ffn_gateup"]
+    j0 = 16 * 37  # features 592 .. 623: gate rows 1184 .., up rows 1200 .. of the interleaved weight
+    g = oracle.matmul_f64(rows_of(gu, 2 * j0, 16), gu.type, xf, m, 16, gu.cols)
+    u = oracle.matmul_f64(rows_of(gu, 2 * j0 + 16, 16), gu.type, xf, m, 16, gu.cols)
+    h_ref = oracle.swiglu(g.astype(np.float32), u.astype(np.float32)).astype(np.float64)
+    h = step.h.cpu().numpy()
+    bound = 1e-3 * (1.1 * np.abs(g).max() * np.abs(u).max() + np.abs(g).max() * np.abs(u).max())
+    assert np.abs(h[:, j0:j0 + 16] - h_ref).max() <= bound
+    wd = last["ffn_down"]
+    assert max_rel(step.out["ffn_down"][:, :64].cpu().numpy(),
+                   oracle.matmul_f64(rows_of(wd, 0, 64), wd.type, h, m, 64, wd.cols)) <= 1e-3
+    lm = fm.lm_head
+    xo = oracle.rmsnorm(x, fm.output_norm.cpu().numpy(), eps)
+    r0 = 64000
+    assert max_rel(step.logits[:, r0:r0 + 48].cpu().numpy(),
+                   oracle.matmul_f64(rows_of(lm, r0, 48), lm.type, xo, m, 48, lm.cols)) <= 1e-3
+    step.plan.close()
+
+
+def test_separate_ops_step_matches_fused(cuda, small_model):
+    """The reference's op sequence as separate launches (OpsDecodeStep, captured into one graph) and
+    the fused step compute the same layer: the standalone norm and the fused prologue share one
+    canonical sum, so q (the first rows of q|k) and v agree to the GEMV bar, and so do the SwiGLU
+    activation and ffn_down."""
+    torch = cuda
+    m = 2
+    fused = decode.FusedDecodeStep(small_model.fused_ops(), m, seed=60)
+    ops = decode.OpsDecodeStep(small_model, m, seed=60)
+    s = torch.cuda.current_stream().cuda_stream
+    fused.run_eager(s)
+    ops.capture()
+    ops.replay()
+    torch.cuda.synchronize()
+    d = small_model.layers[0]["wq"].rows
+    pairs = [(fused.out["wqk"][:, :d], ops.out["wq"]), (fused.out["wqk"][:, d:], ops.out["wk"]),
+             (fused.out["wv"], ops.out["wv"]), (fused.h, ops.h), (fused.out["ffn_down"], ops.out["ffn_down"]),
+             (fused.logits, ops.logits)]
+    for i, (a, b) in enumerate(pairs):
+        assert max_rel(a.cpu().numpy(), b.cpu().numpy().astype(np.float64)) <= 2e-3, i
+    fused.plan.close()

@@ -349,3 +349,57 @@ def test_oracle_rejections_match_reference_build():
     x = np.ones(512, np.float32)
     for t, cols in [(Q8_0, 30), (Q4_K, 300), (2, 40), (10, 256), (16, 256)]:
         assert (oracle.qmatmul(w, t, x, 1, cols) is None) == (oracle.qmatmul(w, t, x, 1, cols, use_ref=True) is None)
+
+
+# ---- rmsnorm / swiglu (runtime/src/ops.cpp:8-13, 96-100) -----------------------------------------
+
+@needs_ref
+@pytest.mark.parametrize("n,eps", [(4096, 1e-5), (512, 1e-6), (7, 0.0), (14336, 1e-5)])
+def test_rmsnorm_matches_reference_build(n, eps):
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal((3, n)) * rng.uniform(0.01, 30.0)).astype(np.float32)
+    w = rng.standard_normal(n).astype(np.float32)
+    a, b = oracle.rmsnorm(x, w, eps), oracle.rmsnorm(x, w, eps, use_ref=True)
+    np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@needs_ref
+def test_swiglu_matches_reference_build():
+    rng = np.random.default_rng(5)
+    g = np.concatenate([rng.standard_normal(4000) * 6, [0.0, -0.0, 88.0, -88.0, 1e-30, -200.0, 200.0]]).astype(np.float32)
+    u = rng.standard_normal(g.size).astype(np.float32)
+    a, b = oracle.swiglu(g, u), oracle.swiglu(g, u, use_ref=True)
+    np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_rmsnorm_invariants():
+    """What the definition fixes: with unit weights and eps = 0 the output's mean square is 1 and the
+    output does not change when x is scaled by a power of two; a constant vector maps to +-1; the
+    weight multiplies elementwise; eps bounds the scale of a zero vector."""
+    rng = np.random.default_rng(11)
+    n = 4096
+    x = rng.standard_normal((2, n)).astype(np.float32)
+    ones = np.ones(n, np.float32)
+    y = oracle.rmsnorm(x, ones, 0.0).astype(np.float64)
+    assert abs(float(np.mean(y * y, axis=1).max()) - 1.0) < 1e-5
+    np.testing.assert_array_equal(oracle.rmsnorm(x * np.float32(8.0), ones, 0.0), oracle.rmsnorm(x, ones, 0.0))
+    c = np.full((1, 100), -3.5, np.float32)
+    np.testing.assert_allclose(oracle.rmsnorm(c, np.ones(100, np.float32), 0.0), -1.0, rtol=1e-6)
+    w = rng.standard_normal(n).astype(np.float32)
+    np.testing.assert_allclose(oracle.rmsnorm(x, w, 1e-5), oracle.rmsnorm(x, ones, 1e-5) * w, rtol=1e-6)
+    z = np.zeros((1, 64), np.float32)
+    np.testing.assert_array_equal(oracle.rmsnorm(z, np.ones(64, np.float32), 1e-5), z)
+
+
+def test_swiglu_invariants():
+    """silu(0) = 0; silu(z) -> z for large z and -> 0 for very negative z; silu(z) - silu(-z) = z;
+    swiglu is linear in up."""
+    z = np.array([0.0, 30.0, -30.0, 2.0, -2.0, 0.5], np.float32)
+    one = np.ones_like(z)
+    s = oracle.swiglu(z, one).astype(np.float64)
+    assert s[0] == 0.0
+    assert abs(s[1] - 30.0) < 1e-6 and abs(s[2]) < 1e-10
+    np.testing.assert_allclose(s[3] - s[4], 2.0, rtol=1e-6)
+    np.testing.assert_allclose(s[3], 2.0 / (1.0 + np.exp(-2.0)), rtol=1e-6)
+    u = np.linspace(-3, 3, z.size).astype(np.float32)
+    np.testing.assert_allclose(oracle.swiglu(z, 2 * u), 2 * oracle.swiglu(z, u), rtol=1e-6)
