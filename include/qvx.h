@@ -167,6 +167,15 @@ int qvx_qgemm_f16(float* d_out, const void* d_w, uint32_t type, const uint16_t* 
 int qvx_qgemm_f16_noalloc(float* d_out, const void* d_w, uint32_t type, const uint16_t* d_X, int M,
                           int rows, int cols, int variant, void* stream);
 
+/* Tile plan of the Q4_K bf16 / fp16 GEMM kernels behind qvx_qgemm_f16 for an M x rows x cols call
+ * on a device with `cus` compute units (cus <= 0: the current device's).  No reference
+ * counterpart: a host-only query for tests and for callers sizing concurrent work.  Writes up to
+ * `cap` launches of 8 ints each -- tile tokens BM, K splits, tiles, cols_a, mt_a, base_a, mt_b,
+ * base_b: weight-row columns 0..cols_a-1 (256 rows each) hold mt_a tiles of BM tokens from token
+ * base_a, the remaining columns mt_b tiles from token base_b -- and returns the number of launches
+ * (1 or 2), or QVX_E_SHAPE when M, rows or cols is not positive or cols % 256 != 0. */
+int qvx_qgemm_plan_q4k(int M, int rows, int cols, int cus, int* desc, int cap);
+
 /* Per-32 Q8 activation quantiser used by QVX_GEMM_I8 (no reference counterpart): for row m and
  * block j, scale = amax/127, q = round-half-away(x * 127/amax) clamped to +-127, qsum = sum q.
  * d_q int8 [M, K], d_scale fp32 [M, K/32], d_qsum int32 [M, K/32]; K % 32 == 0. */

@@ -55,6 +55,7 @@ SIGNATURES = {
     "qvx_dequant_row": ([_vp, _u32, _i32, _i32, _vp, _vp], _i32),
     "qvx_qgemm_f16": ([_vp, _vp, _u32, _vp, _i32, _i32, _i32, _i32, _vp], _i32),
     "qvx_qgemm_f16_noalloc": ([_vp, _vp, _u32, _vp, _i32, _i32, _i32, _i32, _vp], _i32),
+    "qvx_qgemm_plan_q4k": ([_i32, _i32, _i32, _i32, _vp, _i32], _i32),
     "qvx_quantize_act_q8": ([_vp, _i32, _i32, _vp, _vp, _vp, _vp], _i32),
     "qvx_fill_synthetic": ([_vp, _u32, _i32, _i32, _u64, _f32, _vp], _i32),
     "qvx_fill_normal_f32": ([_vp, _sz, _u64, _f32, _vp], _i32),
@@ -296,6 +297,16 @@ def qgemm_t(w, ggml_type: int, X, rows: int, cols: int, variant: int = GEMM_BF16
     _check(lib().qvx_qgemm_f16(out.data_ptr(), w.data_ptr(), ggml_type, X.data_ptr(), M, rows, cols, variant,
                                _stream()), "qvx_qgemm_f16")
     return out
+
+
+def qgemm_plan_q4k(M: int, rows: int, cols: int, cus: int = 0):
+    """Launches of the Q4_K bf16 / fp16 GEMM for an M x rows x cols call (qvx_qgemm_plan_q4k): a list
+    of dicts with bm, splits, tiles, cols_a, mt_a, base_a, mt_b, base_b.  Host only."""
+    desc = (C.c_int * 16)()
+    n = lib().qvx_qgemm_plan_q4k(M, rows, cols, cus, desc, 2)
+    _check(n if n < 0 else 0, "qvx_qgemm_plan_q4k")
+    keys = ("bm", "splits", "tiles", "cols_a", "mt_a", "base_a", "mt_b", "base_b")
+    return [dict(zip(keys, desc[8 * i:8 * i + 8])) for i in range(n)]
 
 
 def rmsnorm_t(x, w, eps: float, out=None):

@@ -47,6 +47,7 @@ void launch_fill_normal_f32(float* x, size_t n, uint64_t seed, float mul, hipStr
 void launch_fill_normal_f16(uint16_t* x, size_t n, uint64_t seed, float mul, hipStream_t s);
 void launch_read16(const void* src, size_t n16, uint32_t* flag, hipStream_t s);
 bool qgemm_deq_supported(uint32_t t, const void* w, const uint16_t* X, int K, int N, size_t row_bytes);
+int q4k_plan_desc(int M, int N, int K, int cus, int* desc, int cap);
 int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M, int rows, int cols,
                  int variant, hipStream_t s, void* ws, size_t ws_cap);
 int launch_quantize_act_q8(const uint16_t* X, int M, int K, int8_t* q, float* scale, int32_t* qsum,
@@ -466,6 +467,12 @@ int qvx_qgemm_f16(float* d_out, const void* d_w, uint32_t type, const uint16_t* 
   const int rc = launch_qgemm(d_out, d_w, type, d_X, M, rows, cols, variant, as_stream(stream), nullptr, 0);
   if (rc != QVX_OK) return rc;
   return hip_status();
+}
+
+int qvx_qgemm_plan_q4k(int M, int rows, int cols, int cus, int* desc, int cap) {
+  if (M <= 0 || rows <= 0 || cols <= 0 || cols % 256) return QVX_E_SHAPE;
+  if (!desc && cap > 0) return QVX_E_NULL;
+  return q4k_plan_desc(M, rows, cols, cus, desc, cap);
 }
 
 int qvx_qgemm_f16_noalloc(float* d_out, const void* d_w, uint32_t type, const uint16_t* d_X, int M, int rows,

@@ -4,9 +4,11 @@
 // No reference counterpart (the reference prefills token by token); the semantics are qmatmulN's
 // (runtime/src/qmatmul.cpp:64-115) with X converted fp16 -> fp32 exactly.
 //
-// Workgroup = 256 threads (4 waves) computing a BM x 256 output tile (BM tokens x 256 weight rows);
-// wave w owns weight rows 64w..64w+63 of the tile (two 32-row MFMA columns) and all BM tokens, so
-// every weight element is dequantised once per workgroup.  v_mfma_f32_32x32x16_{bf16,f16}.
+// Workgroup = 512 threads (8 waves, two per SIMD) computing a BM x 256 output tile (BM = 64..256
+// tokens x 256 weight rows); wave w owns weight rows 32w..32w+31 of the tile and all BM tokens, so
+// every weight element is dequantised once per workgroup, and on each SIMD one wave's
+// dequantisation VALU, copy issue and LDS waits run beside the other wave's MFMAs.
+// v_mfma_f32_32x32x16_{bf16,f16}.
 //
 // K advances in slices of 64 elements = one 64-element group c of a Q4_K super-block:
 //  * X slice (BM x 64 16-bit values, 128 bytes a row) and W slice (256 super-block headers of 16
@@ -24,8 +26,13 @@
 //    exactly that element order.  Slice k+1 is dequantised while the MFMAs of slice k run.
 //  * The loop reads LDS through inline asm (lds_read16) with explicit lgkmcnt waits: the compiler
 //    would otherwise wait for every copy in flight before each LDS read.
-// Grids smaller than the chip split K across workgroups and accumulate with fp32 atomics into a
-// zero-filled output.
+// Tiles are numbered in a 1-D grid, M-tile fastest within a column of 256 weight rows, and
+// consecutive numbers are placed on one XCD (the dispatcher deals workgroups round-robin over the 8
+// XCDs), so the concurrent tiles of an XCD share their columns' weights and their X rows in its L2.
+// A launch covers two kinds of columns with their own tile count and first token (TileMap), so the
+// host can cut M into one full round of 256-token tiles plus one of shorter tiles where a uniform
+// grid would leave the chip part-idle in its last round.  Grids smaller than the chip split K
+// across workgroups and accumulate with fp32 atomics into a zero-filled output.
 //
 // The bf16 variant first rounds X to bf16 (RNE) in a prepass into a stream-ordered temporary; the
 // fp16 variant reads X as is.
@@ -34,6 +41,7 @@
 #include "qvx_common.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 #include <utility>
 
@@ -70,27 +78,38 @@ __device__ inline u32x4 lds_read16(uint32_t addr) {
 }
 // Waits for the LDS reads in flight; the results (the first N of r, then the 4 of w) are operands,
 // so no use moves above the wait.
+#define QVX_R2(r, i) "+v"(r[i]), "+v"(r[i + 1])
 template <int N>
 __device__ inline void lds_wait(u32x4* r) {
-  static_assert(N == 8 || N == 4, "lds_wait arity");
-  if constexpr (N == 4) {
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3])::"memory");
-  } else {
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7])::"memory");
-  }
+  static_assert(N == 2 || N == 4 || N == 6 || N == 8, "lds_wait arity");
+  if constexpr (N == 2) asm volatile("s_waitcnt lgkmcnt(0)" : QVX_R2(r, 0)::"memory");
+  if constexpr (N == 4) asm volatile("s_waitcnt lgkmcnt(0)" : QVX_R2(r, 0), QVX_R2(r, 2)::"memory");
+  if constexpr (N == 6) asm volatile("s_waitcnt lgkmcnt(0)" : QVX_R2(r, 0), QVX_R2(r, 2), QVX_R2(r, 4)::"memory");
+  if constexpr (N == 8)
+    asm volatile("s_waitcnt lgkmcnt(0)" : QVX_R2(r, 0), QVX_R2(r, 2), QVX_R2(r, 4), QVX_R2(r, 6)::"memory");
 }
 template <int N>
 __device__ inline void lds_wait(u32x4* r, u32x4* w) {
-  static_assert(N == 8 || N == 4, "lds_wait arity");
-  if constexpr (N == 4) {
+  static_assert(N == 4 || N == 8, "lds_wait arity");
+  if constexpr (N == 4)
+    asm volatile("s_waitcnt lgkmcnt(0)" : QVX_R2(r, 0), QVX_R2(r, 2), QVX_R2(w, 0), QVX_R2(w, 2)::"memory");
+  if constexpr (N == 8)
     asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3])::"memory");
-  } else {
+                 : QVX_R2(r, 0), QVX_R2(r, 2), QVX_R2(r, 4), QVX_R2(r, 6), QVX_R2(w, 0), QVX_R2(w, 2)::"memory");
+}
+
+// Waits as above for the first N of r (N = 0, 2, 4, 6 or 8) and two more results w[0], w[1].
+template <int N>
+__device__ inline void lds_wait_w2(u32x4* r, u32x4* w) {
+  static_assert(N == 0 || N == 2 || N == 4 || N == 6 || N == 8, "lds_wait_w2 arity");
+  if constexpr (N == 0) asm volatile("s_waitcnt lgkmcnt(0)" : QVX_R2(w, 0)::"memory");
+  if constexpr (N == 2) asm volatile("s_waitcnt lgkmcnt(0)" : QVX_R2(r, 0), QVX_R2(w, 0)::"memory");
+  if constexpr (N == 4) asm volatile("s_waitcnt lgkmcnt(0)" : QVX_R2(r, 0), QVX_R2(r, 2), QVX_R2(w, 0)::"memory");
+  if constexpr (N == 6)
+    asm volatile("s_waitcnt lgkmcnt(0)" : QVX_R2(r, 0), QVX_R2(r, 2), QVX_R2(r, 4), QVX_R2(w, 0)::"memory");
+  if constexpr (N == 8)
     asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]),
-                   "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3])::"memory");
-  }
+                 : QVX_R2(r, 0), QVX_R2(r, 2), QVX_R2(r, 4), QVX_R2(r, 6), QVX_R2(w, 0)::"memory");
 }
 
 __device__ inline void lds_wait8_1(u32x4* r, u32x4* w) {
@@ -184,6 +203,12 @@ struct GemmGeo {
   uint32_t m_b4;       // 0x00F000F0: bits 4-7 of each 16-bit half (fp16 mantissa bits 4-7)
 };
 
+// Tile numbering of one launch: columns 0..cols_a-1 hold mt_a tiles from token base_a, columns
+// cols_a.. hold mt_b tiles from token base_b (BM tokens a tile, M-tile fastest).
+struct TileMap {
+  int cols_a, mt_a, base_a, mt_b, base_b;
+};
+
 }  // namespace gemm
 
 using namespace gemm;
@@ -195,13 +220,13 @@ __device__ inline void read_frags(uint32_t addr, u32x4* a, std::integer_sequence
 }
 
 template <int VAR, int BM>
-__global__ __launch_bounds__(256) void k_qgemm_q4k(const uint8_t* __restrict__ W, const uint16_t* __restrict__ X,
-                                                   float* __restrict__ Y, GemmGeo geo) {
+__global__ __launch_bounds__(512) void k_qgemm_q4k(const uint8_t* __restrict__ W, const uint16_t* __restrict__ X,
+                                                   float* __restrict__ Y, GemmGeo geo, TileMap tm) {
   constexpr int MT = BM / 32;         // 32-token A tiles (per wave: all BM tokens)
-  constexpr int XI = BM / 32;         // X copies per wave per slice (BM*128 bytes / 4 waves / 1 KB)
-  constexpr int WI = 5;               // W copies per wave per half super-block (1 KB headers, 4 KB quants)
+  constexpr int XI = BM / 64;         // X copies per wave per slice (BM*128 bytes / 8 waves / 1 KB)
+  constexpr int WI = 3;               // W copies per wave per half super-block (headers, 2 x quants)
   constexpr int XSTAGE = BM * 128;    // bytes of one X slice
-  static_assert(MT <= 8, "tile too large");
+  static_assert(BM % 64 == 0 && BM >= 64 && BM <= 256, "tile size");
   __shared__ __attribute__((aligned(1024))) uint8_t xs[3 * XSTAGE];
   __shared__ __attribute__((aligned(1024))) uint8_t ws[3 * kWStage];
 
@@ -209,11 +234,25 @@ __global__ __launch_bounds__(256) void k_qgemm_q4k(const uint8_t* __restrict__ W
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ln = lane & 31, g = lane >> 5;
-  const int n0 = blockIdx.x * kBN, m0 = blockIdx.y * BM;
+  int n0, m0;
+  {
+    const int nb = (int)gridDim.x;
+    int b = (int)blockIdx.x;
+    if ((nb & 7) == 0) b = (b & 7) * (nb >> 3) + (b >> 3);  // XCD b % 8 takes a contiguous range
+    const int na = tm.cols_a * tm.mt_a;
+    if (b < na) {
+      n0 = (b / tm.mt_a) * kBN;
+      m0 = tm.base_a + (b % tm.mt_a) * BM;
+    } else {
+      b -= na;
+      n0 = (tm.cols_a + b / tm.mt_b) * kBN;
+      m0 = tm.base_b + (b % tm.mt_b) * BM;
+    }
+  }
   const int nsl = K / 64;
   const int kb0 = blockIdx.z * geo.per_split;  // per_split is a multiple of 4: splits start a super-block
   const int kb1 = min(nsl, kb0 + geo.per_split);
-  if (kb0 >= kb1) return;
+  if (kb0 >= kb1 || m0 >= M || n0 >= N) return;
 
   // Copy descriptors: rows past M or N read as zeros (buffer range check).
   const uint32_t xrow_bytes = (uint32_t)K * 2u;
@@ -222,30 +261,27 @@ __global__ __launch_bounds__(256) void k_qgemm_q4k(const uint8_t* __restrict__ W
   const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(W + (size_t)n0 * geo.row_bytes), (short)0, (int)((uint32_t)min(kBN, N - n0) * geo.row_bytes),
       (int)kRsrcWord3);
-  // (arrays captured by the lambdas below have a fixed size: clang drops the host stub of a kernel
-  // template whose lambdas capture an array sized by a template parameter)
   // X copy i of this wave: chunk q = (wave*XI + i)*64 + lane -> row q/8, LDS slot q%8 holds global
   // chunk slot ^ swz(row).
-  uint32_t xoff[8];
+  uint32_t xoff[4];
 #pragma unroll
   for (int i = 0; i < XI; ++i) {
     const uint32_t q = (uint32_t)((wave * XI + i) * 64 + lane), r = q >> 3, p = q & 7u;
     xoff[i] = r * xrow_bytes + 16u * (p ^ xswz(r));
   }
-  // W copies of this wave's rows 64w..64w+63 for half super-block hb (quant bytes 64h..64h+63 of
-  // super-block hb/2, h = hb%2): one header copy (row 64w + lane, LDS 16 r), then four quant copies
-  // (row 64w + 16i + lane/4, LDS slot lane%4 of the row's 64 bytes holds chunk slot ^ qswz(row)).
-  const uint32_t woff_h = (uint32_t)(64 * wave + lane) * geo.row_bytes;
-  uint32_t woff[4];
+  // W copies of this wave's rows 32w..32w+31 for half super-block hb: the 32 headers (lanes 0..31,
+  // row 32w + lane, LDS 16 r), then two quant copies (row 32w + 16i + lane/4, LDS slot lane%4 of the
+  // row's 64 bytes holds chunk slot ^ qswz(row)).
+  const uint32_t woff_h = (uint32_t)(32 * wave + ln) * geo.row_bytes;
+  uint32_t woff[2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t r = (uint32_t)(64 * wave + 16 * i + (lane >> 2)), slot = (uint32_t)lane & 3u;
+  for (int i = 0; i < 2; ++i) {
+    const uint32_t r = (uint32_t)(32 * wave + 16 * i + (lane >> 2)), slot = (uint32_t)lane & 3u;
     woff[i] = r * geo.row_bytes + 16u + 16u * (slot ^ qswz(r));
   }
   QVX_LDS uint8_t* xs_l = (QVX_LDS uint8_t*)xs;
   QVX_LDS uint8_t* ws_l = (QVX_LDS uint8_t*)ws;
 
-  // Copy i of X(kb) (one 1 KB instruction).
   auto issue_x1 = [&](int kb, int i) {
     QVX_LDS uint8_t* dst = xs_l + (kb % 3) * XSTAGE + wave * XI * 1024;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, dst + i * 1024, 16, xoff[i], (uint32_t)kb * 128u, 0, 0);
@@ -257,14 +293,13 @@ __global__ __launch_bounds__(256) void k_qgemm_q4k(const uint8_t* __restrict__ W
   auto issue_w = [&](int hb) {
     QVX_LDS uint8_t* st = ws_l + (hb % 3) * kWStage;
     const uint32_t sbo = (uint32_t)(hb >> 1) * 144u;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, st + wave * 1024, 16, woff_h, sbo, 0, 0);
+    if (lane < 32) __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, st + wave * 512, 16, woff_h, sbo, 0, 0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, st + kWQs + (4 * wave + i) * 1024, 16, woff[i],
+    for (int i = 0; i < 2; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, st + kWQs + (2 * wave + i) * 1024, 16, woff[i],
                                                sbo + 64u * (uint32_t)(hb & 1), 0, 0);
   };
 
-  // LDS read addresses.  A: row ln of each 32-token tile i (+4096 i), chunk kc_s ^ swz(ln).
   const uint32_t xs_base = (uint32_t)(uintptr_t)xs_l;
   const uint32_t ws_base = (uint32_t)(uintptr_t)ws_l;
   const uint32_t sw = xswz((uint32_t)ln);
@@ -274,44 +309,27 @@ __global__ __launch_bounds__(256) void k_qgemm_q4k(const uint8_t* __restrict__ W
     const uint32_t kc = 4u * (uint32_t)(s >> 1) + 2u * (uint32_t)g + (uint32_t)(s & 1);
     a_rel[s] = (uint32_t)ln * 128u + 16u * (kc ^ sw);
   }
-  // B: this lane's weight rows r = 64w + 32j + ln: header at 16 r; quant bytes 16g..16g+15 of
-  // group c (chunk 2(c%2) + g of the half super-block) at kWQs + 64 r + 16 (chunk ^ qswz(r)).
-  uint32_t h_rel[2], q_rel[2][2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const uint32_t r = (uint32_t)(64 * wave + 32 * j + ln);
-    h_rel[j] = 16u * r;
-#pragma unroll
-    for (int c = 0; c < 2; ++c) q_rel[j][c] = (uint32_t)kWQs + 64u * r + 16u * ((2u * c + (uint32_t)g) ^ qswz(r));
-  }
+  // B: this lane's weight row r = 32w + ln.
+  const uint32_t rr = (uint32_t)(32 * wave + ln);
+  const uint32_t h_rel = 16u * rr;
+  const uint32_t q_rel0 = (uint32_t)kWQs + 64u * rr + 16u * ((uint32_t)g ^ qswz(rr));
+  const uint32_t q_rel1 = (uint32_t)kWQs + 64u * rr + 16u * ((2u + (uint32_t)g) ^ qswz(rr));
 
-  f32x16_t acc[8][2];  // rows >= MT unused
+  f32x16_t acc[8];  // rows >= MT unused
 #pragma unroll
   for (int i = 0; i < MT; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+    for (int e = 0; e < 16; ++e) acc[i][e] = 0.0f;
 
-  // W reads of slice kb (this lane's two rows: header, quant bytes) into r.
-  auto read_w = [&](int kb, u32x4 (&r)[4]) {
+  auto read_w = [&](int kb, u32x4 (&r)[2]) {
     const uint32_t st = ws_base + (uint32_t)((kb >> 1) % 3) * kWStage;
-    const int c = kb & 1;
-    r[0] = lds_read16(st + h_rel[0]);
-    r[1] = lds_read16(st + (c ? q_rel[0][1] : q_rel[0][0]));
-    r[2] = lds_read16(st + h_rel[1]);
-    r[3] = lds_read16(st + (c ? q_rel[1][1] : q_rel[1][0]));
+    r[0] = lds_read16(st + h_rel);
+    r[1] = lds_read16(st + ((kb & 1) ? q_rel1 : q_rel0));
   };
 
-  // MFMA pair i of K16 step s: token tile i times both weight tiles.
-  auto mfma_pair = [&](int i, int s, const u32x4& a, const i32x4_t (&b)[2][4]) {
-    acc[i][0] = mfma32<VAR>(__builtin_bit_cast(i32x4_t, a), b[0][s], acc[i][0]);
-    acc[i][1] = mfma32<VAR>(__builtin_bit_cast(i32x4_t, a), b[1][s], acc[i][1]);
-  };
-
-  // Dequantisation of the next slice in 18 pieces of ~9 VALU, placed between MFMA pairs by hand:
-  // piece 9j = scales of row j, pieces 9j+1+u = dwords 2h, 2h+1 of bn[j][u/2] (h = u%2), converted
-  // from quant dword (u/2 % 2)*2 + h, low nibbles for u < 4, high nibbles after.
+  // Dequantisation of the next slice in 9 pieces of ~9 VALU for this lane's row, placed between the
+  // MFMAs by hand: piece 0 = the row's scales, piece 1+u = dwords 2h, 2h+1 of bn[u/2] (h = u%2),
+  // converted from quant dword (u/2 % 2)*2 + h, low nibbles for u < 4, high nibbles after.
   // A nibble n is dropped into the mantissa of the fp16 1024 (bits 0x6400) at bit b = 0 or 4 (one
   // bitop3 for the two nibbles of a 16-bit half pair, after a shift for the odd bytes): the half is
   // exactly 1024 + 2^b n, and v_fma_mix_f32 evaluates (ds / 2^b) * (1024 + 2^b n) +
@@ -320,130 +338,115 @@ __global__ __launch_bounds__(256) void k_qgemm_q4k(const uint8_t* __restrict__ W
   //   low nibble,  k even: (w      & 0x000F000F) -> n       low nibble,  k odd: (w >> 4 & 0x00F000F0) -> 16 n
   //   high nibble, k even: (w      & 0x00F000F0) -> 16 n    high nibble, k odd: (w >> 8 & 0x00F000F0) -> 16 n
   struct DeqState {
-    u32x4 h[2], q[2];
-    float s[2][3], b[2][3];  // scale, bias per row: low even, low odd, high
+    u32x4 h, q;
+    float s[3], b[3];  // scale, bias: low even, low odd, high
     ScaleSel sel;
   };
   const uint32_t k1024 = 0x64006400u;  // two fp16 1024.0
-  auto piece = [&](int p, DeqState& st, i32x4_t (&bn)[2][4]) {
-    const int j = p / 9, r = p % 9;
-    if (r == 0) {
-      const u32x4& h = st.h[j];
+  auto piece = [&](int p, DeqState& st, i32x4_t (&bn)[4]) {
+    if (p == 0) {
+      const u32x4& h = st.h;
       const uint32_t scp = ((h.y >> st.sel.sa) & st.sel.ma) | ((h.w >> st.sel.sb) & st.sel.mb);
       const uint32_t mp = ((h.z >> st.sel.sa) & st.sel.ma) | ((h.w >> (st.sel.sb + 4u)) & st.sel.mb);
       const float d = f16lo(h.x), dmin = f16hi(h.x);
       const float ds0 = d * ub(scp, 0), ds1 = d * ub(scp, 1);
       const float dm0 = -(dmin * ub(mp, 0)), dm1 = -(dmin * ub(mp, 1));
-      st.s[j][0] = ds0;
-      st.s[j][1] = ds0 * 0.0625f;
-      st.s[j][2] = ds1 * 0.0625f;
-      st.b[j][0] = __builtin_fmaf(-1024.0f, ds0, dm0);
-      st.b[j][1] = __builtin_fmaf(-64.0f, ds0, dm0);
-      st.b[j][2] = __builtin_fmaf(-64.0f, ds1, dm1);
+      st.s[0] = ds0;
+      st.s[1] = ds0 * 0.0625f;
+      st.s[2] = ds1 * 0.0625f;
+      st.b[0] = __builtin_fmaf(-1024.0f, ds0, dm0);
+      st.b[1] = __builtin_fmaf(-64.0f, ds0, dm0);
+      st.b[2] = __builtin_fmaf(-64.0f, ds1, dm1);
     } else {
-      const int u = r - 1, sp = u >> 1, hh = u & 1, w = (sp & 1) * 2 + hh;
-      const uint32_t src = w == 0 ? st.q[j].x : w == 1 ? st.q[j].y : w == 2 ? st.q[j].z : st.q[j].w;
+      const int u = p - 1, sp = u >> 1, hh = u & 1, w = (sp & 1) * 2 + hh;
+      const uint32_t src = w == 0 ? st.q.x : w == 1 ? st.q.y : w == 2 ? st.q.z : st.q.w;
       const bool lo = sp < 2;
       const int ke = lo ? 0 : 2, ko = lo ? 1 : 2;
       const uint32_t e = __builtin_amdgcn_bitop3_b32(src, lo ? geo.m_b0 : geo.m_b4, k1024, 0xEA);
       const uint32_t o = __builtin_amdgcn_bitop3_b32(src >> (lo ? 4 : 8), geo.m_b4, k1024, 0xEA);
       const half2_t he = __builtin_bit_cast(half2_t, e), ho = __builtin_bit_cast(half2_t, o);
-      bn[j][sp][2 * hh] = (int)pack2<VAR>(__builtin_fmaf((float)he.x, st.s[j][ke], st.b[j][ke]),
-                                          __builtin_fmaf((float)ho.x, st.s[j][ko], st.b[j][ko]));
-      bn[j][sp][2 * hh + 1] = (int)pack2<VAR>(__builtin_fmaf((float)he.y, st.s[j][ke], st.b[j][ke]),
-                                              __builtin_fmaf((float)ho.y, st.s[j][ko], st.b[j][ko]));
-      pin(bn[j][sp]);  // computed here, not sunk towards its use in the next slice
+      bn[sp][2 * hh] = (int)pack2<VAR>(__builtin_fmaf((float)he.x, st.s[ke], st.b[ke]),
+                                       __builtin_fmaf((float)ho.x, st.s[ko], st.b[ko]));
+      bn[sp][2 * hh + 1] = (int)pack2<VAR>(__builtin_fmaf((float)he.y, st.s[ke], st.b[ke]),
+                                           __builtin_fmaf((float)ho.y, st.s[ko], st.b[ko]));
+      pin(bn[sp]);
     }
   };
 
-  // One slice: MFMAs of slice kb with B operands bc and step-0 A fragments a[0] (read during the
-  // previous slice); dequantisation of slice kb+1 into bn (on the last slice it reads a stale stage
-  // and the result is unused) spread over steps 1-3.  After step 2 the wave holds every A fragment
-  // of slice kb, so the barrier that publishes X(kb+1) and frees stage kb%3 sits there, and the
-  // step-0 fragments of slice kb+1 are read while the step-3 MFMAs run.  Copies run ahead: the
-  // sync of slice kb issues W(kb/2+2) (even kb), step 0 of slice kb copies X(kb+2).
-  // sched_barrier(0) after every MFMA pair keeps this order exactly.
-  auto slice = [&](int kb, const i32x4_t (&bc)[2][4], i32x4_t (&bn)[2][4], u32x4 (&a)[2][8]) {
+  // A fragments go through a ring of two groups of four 32-token tiles (NG groups per slice, group G
+  // = step G / (MT/4), tiles 4 (G % (MT/4)) ..+3); a group's reads are issued one group ahead, so four
+  // MFMAs (eight with the SIMD's other wave) cover their latency.
+  constexpr int GPS = MT / 4 > 0 ? MT / 4 : 1;  // groups per K16 step
+  constexpr int GT = MT / GPS;                  // tiles per group
+  constexpr int NG = 4 * GPS;                   // groups per slice
+  auto read_group = [&](uint32_t xb, int G, u32x4 (&r)[8]) {
+    const uint32_t base = xb + a_rel[G / GPS] + 4096u * (uint32_t)(GT * (G % GPS));
+    read_frags(base, r, std::make_integer_sequence<int, GT>{});
+  };
+  // Dequantisation pieces of slice kb+1 go after the MFMAs of groups 1..NG-1: piece p after slot
+  // p * NS / 9 of those NS = GT (NG - 1) slots.
+  constexpr int NS = GT * (NG - 1);
+
+  // One slice: group 0's fragments were read during the previous slice.  Group 0 also issues the
+  // X(kb+2) copies (one after each MFMA) and the LDS reads of this lane's W(kb+1) header and quant
+  // bytes; the barrier that publishes X(kb+1) and frees stage kb%3 comes once every fragment of
+  // slice kb is in registers (before the last group), and W(kb/2+2) is issued right after it on even
+  // slices.
+  auto slice = [&](int kb, const i32x4_t (&bc)[4], i32x4_t (&bn)[4], u32x4 (&a)[2][8]) {
     const uint32_t xb = xs_base + (uint32_t)(kb % 3) * XSTAGE;
     DeqState st;
     st.sel = scale_sel((kb + 1) & 3);
-    lds_wait<MT>(a[0]);
-    read_frags(xb + a_rel[1], a[1], std::make_integer_sequence<int, MT>{});
-    {
-      u32x4 w4[4];
-      read_w(kb + 1, w4);
-      st.h[0] = w4[0];
-      st.q[0] = w4[1];
-      st.h[1] = w4[2];
-      st.q[1] = w4[3];
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    // X(kb+2), one copy after each MFMA pair (the vector memory path takes a steady trickle; a
-    // burst of copies stalls the issuing wave).  Past the last slice the index is clamped: the copy
-    // repeats X(kb1-1) into a stage no slice reads again.
     const int kx = min(kb + 2, kb1 - 1);
 #pragma unroll
-    for (int i = 0; i < MT; ++i) {
-      mfma_pair(i, 0, a[0][i], bc);
-      if (i < XI) issue_x1(kx, i);
+    for (int G = 0; G < NG; ++G) {
+      u32x4(&cur)[8] = a[G & 1];
+      u32x4(&nxt)[8] = a[(G + 1) & 1];
+      if (G == 1) {
+        u32x4 w2[2] = {st.h, st.q};
+        lds_wait_w2<GT>(cur, w2);
+        st.h = w2[0];
+        st.q = w2[1];
+      } else {
+        lds_wait<GT>(cur);
+      }
+      if (G == NG - 1) {
+        if (kb + 1 < kb1) {
+          // X(kb+1) was copied during group 0 of slice kb-1; younger copies, which may still fly:
+          // W of the sync of slice kb-1 (odd kb) and X(kb+2) (group 0 of this slice).
+          if ((kb & 1) && kb + 3 < kb1)
+            wait_vm<WI + XI>();
+          else
+            wait_vm<XI>();
+          __builtin_amdgcn_s_barrier();
+          if (!(kb & 1) && kb + 4 < kb1) issue_w((kb >> 1) + 2);
+          read_group(xs_base + (uint32_t)((kb + 1) % 3) * XSTAGE, 0, nxt);
+        }
+      } else {
+        read_group(xb, G + 1, nxt);
+      }
+      if (G == 0) {
+        u32x4 w2[2];
+        read_w(kb + 1, w2);
+        st.h = w2[0];
+        st.q = w2[1];
+      }
       __builtin_amdgcn_sched_barrier(0);
-    }
-    {
-      u32x4 w4[4] = {st.h[0], st.q[0], st.h[1], st.q[1]};
-      lds_wait<MT>(a[1], w4);
-      st.h[0] = w4[0];
-      st.q[0] = w4[1];
-      st.h[1] = w4[2];
-      st.q[1] = w4[3];
-    }
-    read_frags(xb + a_rel[2], a[0], std::make_integer_sequence<int, MT>{});
-    constexpr int NP = 18;
-    constexpr int PER = (NP + 3 * MT - 1) / (3 * MT);  // pieces per MFMA pair over steps 1-3
+      const int s = G / GPS;
 #pragma unroll
-    for (int i = 0; i < MT; ++i) {
-      mfma_pair(i, 1, a[1][i], bc);
+      for (int t = 0; t < GT; ++t) {
+        acc[GT * (G % GPS) + t] = mfma32<VAR>(__builtin_bit_cast(i32x4_t, cur[t]), bc[s], acc[GT * (G % GPS) + t]);
+        if (G == 0 && t < XI) issue_x1(kx, t);
+        if (G > 0) {
+          const int slot = GT * (G - 1) + t;
 #pragma unroll
-      for (int k = 0; k < PER; ++k)
-        if (i * PER + k < NP) piece(i * PER + k, st, bn);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    lds_wait<MT>(a[0]);
-    read_frags(xb + a_rel[3], a[1], std::make_integer_sequence<int, MT>{});
-#pragma unroll
-    for (int i = 0; i < MT; ++i) {
-      mfma_pair(i, 2, a[0][i], bc);
-#pragma unroll
-      for (int k = 0; k < PER; ++k)
-        if ((MT + i) * PER + k < NP) piece((MT + i) * PER + k, st, bn);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    lds_wait<MT>(a[1]);
-    if (kb + 1 < kb1) {
-      // X(kb+1) was copied during step 0 of slice kb-1; younger copies, which may still fly: W
-      // of the sync of slice kb-1 (odd kb) and X(kb+2) (step 0 of this slice).
-      if ((kb & 1) && kb + 3 < kb1)
-        wait_vm<WI + XI>();
-      else
-        wait_vm<XI>();
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-      __builtin_amdgcn_s_barrier();
-      // W stage (kb/2+2)%3 last fed the dequantisation of slice kb-1 (read during slice kb-2).
-      if (!(kb & 1) && kb + 4 < kb1) issue_w((kb >> 1) + 2);
-      read_frags(xs_base + (uint32_t)((kb + 1) % 3) * XSTAGE + a_rel[0], a[0], std::make_integer_sequence<int, MT>{});
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < MT; ++i) {
-      mfma_pair(i, 3, a[1][i], bc);
-#pragma unroll
-      for (int k = 0; k < PER; ++k)
-        if ((2 * MT + i) * PER + k < NP) piece((2 * MT + i) * PER + k, st, bn);
-      __builtin_amdgcn_sched_barrier(0);
+          for (int p = 0; p < 9; ++p)
+            if (p * NS / 9 == slot) piece(p, st, bn);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
   };
 
-  // Prologue: half super-block kb0/2 and X(kb0) land; then the copies slice kb0-1 would have made:
-  // W(kb0/2+1) and X(kb0+1).
   issue_w(kb0 >> 1);
   issue_x(kb0);
   wait_vm<0>();
@@ -452,15 +455,13 @@ __global__ __launch_bounds__(256) void k_qgemm_q4k(const uint8_t* __restrict__ W
   issue_x(min(kb0 + 1, kb1 - 1));
 
   u32x4 a[2][8];
-  read_frags(xs_base + (uint32_t)(kb0 % 3) * XSTAGE + a_rel[0], a[0], std::make_integer_sequence<int, MT>{});
-  i32x4_t b0[2][4], b1[2][4];
+  read_group(xs_base + (uint32_t)(kb0 % 3) * XSTAGE, 0, a[0]);
+  i32x4_t b0[4], b1[4];
   {
-    u32x4 wq[4];
+    u32x4 wq[2];
     read_w(kb0, wq);
-    lds_wait<4>(wq);
-    const ScaleSel sel = scale_sel(kb0 & 3);
-    dequant_row<VAR>(wq[0], wq[1], sel, geo.mask_lo, geo.mask_hi, b0[0]);
-    dequant_row<VAR>(wq[2], wq[3], sel, geo.mask_lo, geo.mask_hi, b0[1]);
+    lds_wait_w2<0>(nullptr, wq);
+    dequant_row<VAR>(wq[0], wq[1], scale_sel(kb0 & 3), geo.mask_lo, geo.mask_hi, b0);
   }
 
   int kb = kb0;
@@ -469,27 +470,24 @@ __global__ __launch_bounds__(256) void k_qgemm_q4k(const uint8_t* __restrict__ W
     slice(kb + 1, b1, b0, a);
   }
   if (kb < kb1) slice(kb, b0, b1, a);
-  wait_vm<0>();  // the clamped copies of the last slices
+  wait_vm<0>();
 
-  // C layout of v_mfma_f32_32x32x*: element e of lane l is row 8*(e/4) + 4*(l/32) + e%4, col l%32.
 #pragma unroll
-  for (int i = 0; i < MT; ++i)
+  for (int i = 0; i < MT; ++i) {
+    const int n = n0 + 32 * wave + ln;
+    if (n >= N) continue;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int n = n0 + 64 * wave + 32 * j + ln;
-      if (n >= N) continue;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int m = m0 + 32 * i + 8 * (e >> 2) + 4 * g + (e & 3);
-        if (m < M) {
-          float* dst = Y + (size_t)m * N + n;
-          if (geo.atomic_out)
-            unsafeAtomicAdd(dst, acc[i][j][e]);
-          else
-            *dst = acc[i][j][e];
-        }
+    for (int e = 0; e < 16; ++e) {
+      const int m = m0 + 32 * i + 8 * (e >> 2) + 4 * g + (e & 3);
+      if (m < M) {
+        float* dst = Y + (size_t)m * N + n;
+        if (geo.atomic_out)
+          unsafeAtomicAdd(dst, acc[i][e]);
+        else
+          *dst = acc[i][e];
       }
     }
+  }
 }
 
 // ---- int8 variant --------------------------------------------------------------------------------
@@ -864,50 +862,133 @@ namespace {
 // Whole super-blocks of K per split, and the split count that results.
 inline int split_per(int nsl, int splits) { return ((nsl + splits - 1) / splits + 3) & ~3; }
 
+// One launch of the Q4_K GEMM: BM tokens a tile, K splits, the 1-D tile numbering.
+struct Q4kLaunch {
+  int bm, splits, ntiles;
+  TileMap tm;
+};
+struct Q4kPlan {
+  int n;
+  Q4kLaunch l[2];
+};
+
 template <int VAR, int BM>
-bool launch_q4k(float* out, const void* w, const uint16_t* X, int M, int N, int K, int splits, bool zeroed,
+bool launch_q4k(float* out, const void* w, const uint16_t* X, int M, int N, int K, const Q4kLaunch& L,
                 hipStream_t s) {
   static LdsLimit lim;
   if (!lds_ready(reinterpret_cast<const void*>(&k_qgemm_q4k<VAR, BM>), lim, 0)) return false;
-  const int nsl = K / 64;
-  const int per = split_per(nsl, splits);
-  splits = (nsl + per - 1) / per;
-  if (splits > 1 && !zeroed) launch_zero(out, (size_t)M * N, s);
-  GemmGeo geo{M,           N,           K,           (uint32_t)(K / 256) * 144u, per, splits > 1 ? 1 : 0,
+  const int per = split_per(K / 64, L.splits);
+  GemmGeo geo{M,           N,           K,           (uint32_t)(K / 256) * 144u, per, L.splits > 1 ? 1 : 0,
               0x0F0F0F0Fu, 0xF0F0F0F0u, 0x000F000Fu, 0x00F000F0u};
-  dim3 grid((N + kBN - 1) / kBN, (M + BM - 1) / BM, splits);
-  k_qgemm_q4k<VAR, BM><<<grid, 256, 0, s>>>(static_cast<const uint8_t*>(w), X, out, geo);
+  k_qgemm_q4k<VAR, BM><<<dim3(L.ntiles, 1, L.splits), 512, 0, s>>>(static_cast<const uint8_t*>(w), X, out, geo, L.tm);
   return true;
 }
 
-// Tile choice: 256-token tiles when they alone give ~one workgroup per CU; else 128-token tiles,
-// splitting K (fp32 atomics into a zeroed output, M*N adds per split) only while the grid is
-// smaller than that.
-// Tile rows (256 or 128) and K splits for an M x N x K launch.
-inline void q4k_plan(int M, int N, int K, int& bm, int& splits) {
-  const int nt = (N + kBN - 1) / kBN, nsl = K / 64;
-  splits = 1;
-  if (nt * ((M + 255) / 256) >= 224) {
-    bm = 256;
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static std::atomic<int> cache[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+inline int cdiv(int a, int b) { return (a + b - 1) / b; }
+
+// Tile plan for an M x N x K launch on `cus` compute units (one 512-thread workgroup fits a CU).
+//  * Grids smaller than the chip: 128-token tiles, splitting K (fp32 atomics into a zeroed output,
+//    M*N adds per split) only while the grid is below ~200 workgroups.
+//  * Otherwise the cheapest of: a uniform grid of 256-, 192- or 128-token tiles, or two launches,
+//    the first of 256-token tiles from token 0 and the second of 192- or 128-token tiles for the
+//    rest, with two kinds of columns (x columns with a1 + b1 tiles, the others with a2 + b2).  The
+//    cost of a launch is its rounds of workgroups times the tile time, BM / 256 plus a fixed part
+//    for the prologue and the output store.  For 2048 x 14336 on 256 CUs this gives 256 tiles of
+//    256 tokens (48 columns x 5 + 8 x 2) and 256 tiles of 192 (48 x 4 + 8 x 8): 1.75 rounds of
+//    256-token tile time where a uniform grid takes 2.
+void q4k_plan(int M, int N, int K, int cus, Q4kPlan& p) {
+  const int nt = cdiv(N, kBN), nsl = K / 64;
+  auto uniform = [&](int bm, int splits) {
+    Q4kLaunch L{bm, splits, nt * cdiv(M, bm), TileMap{nt, cdiv(M, bm), 0, 1, 0}};
+    return L;
+  };
+  p.n = 1;
+  if (nt * cdiv(M, 256) < 224 * cus / 256) {
+    int splits = 1;
+    const int tiles = nt * cdiv(M, 128);
+    while (tiles * splits < 200 * cus / 256 && nsl / (splits * 2) >= 8) splits *= 2;
+    const int per = split_per(nsl, splits);
+    p.l[0] = uniform(128, (nsl + per - 1) / per);
     return;
   }
-  bm = 128;
-  const int tiles = nt * ((M + 127) / 128);
-  while (tiles * splits < 200 && nsl / (splits * 2) >= 8) splits *= 2;
-  const int per = split_per(nsl, splits);
-  splits = (nsl + per - 1) / per;
+  auto cost = [&](int bm, int tiles) { return tiles ? cdiv(tiles, cus) * (bm / 256.0 + 0.05) : 0.0; };
+  double best = cost(256, nt * cdiv(M, 256));
+  p.l[0] = uniform(256, 1);
+  for (int bm : {192, 128}) {
+    const double c = cost(bm, nt * cdiv(M, bm));
+    if (c < best - 1e-9) {
+      best = c;
+      p.l[0] = uniform(bm, 1);
+    }
+  }
+  const int A = cdiv(M, 256);
+  for (int bmb : {192, 128})
+    for (int a1 = std::max(1, A - 8); a1 <= A; ++a1)
+      for (int a2 = std::max(0, A - 8); a2 <= a1; ++a2) {
+        const int b1 = M > 256 * a1 ? cdiv(M - 256 * a1, bmb) : 0;
+        const int b2 = M > 256 * a2 ? cdiv(M - 256 * a2, bmb) : 0;
+        for (int x = 1; x <= nt; ++x) {
+          const int ta = x * a1 + (nt - x) * a2, tb = x * b1 + (nt - x) * b2;
+          if (!tb) continue;
+          const double c = cost(256, ta) + cost(bmb, tb) + 0.02;
+          if (c < best - 1e-9) {
+            best = c;
+            p.n = 2;
+            p.l[0] = Q4kLaunch{256, 1, ta, TileMap{x, a1, 0, a2, 0}};
+            p.l[1] = Q4kLaunch{bmb, 1, tb, TileMap{x, b1, 256 * a1, b2, 256 * a2}};
+          }
+        }
+      }
+}
+
+template <int VAR>
+bool launch_one(float* out, const void* w, const uint16_t* X, int M, int N, int K, const Q4kLaunch& L,
+                hipStream_t s) {
+  switch (L.bm) {
+    case 256: return launch_q4k<VAR, 256>(out, w, X, M, N, K, L, s);
+    case 192: return launch_q4k<VAR, 192>(out, w, X, M, N, K, L, s);
+    case 128: return launch_q4k<VAR, 128>(out, w, X, M, N, K, L, s);
+    default: return false;
+  }
 }
 
 // zeroed: the caller has already zeroed the output of a K-split launch.
 template <int VAR>
 bool launch_var(float* out, const void* w, const uint16_t* X, int M, int N, int K, bool zeroed, hipStream_t s) {
-  int bm, splits;
-  q4k_plan(M, N, K, bm, splits);
-  if (bm == 256) return launch_q4k<VAR, 256>(out, w, X, M, N, K, splits, zeroed, s);
-  return launch_q4k<VAR, 128>(out, w, X, M, N, K, splits, zeroed, s);
+  Q4kPlan p;
+  q4k_plan(M, N, K, device_cus(), p);
+  if (p.l[0].splits > 1 && !zeroed) launch_zero(out, (size_t)M * N, s);
+  for (int i = 0; i < p.n; ++i)
+    if (!launch_one<VAR>(out, w, X, M, N, K, p.l[i], s)) return false;
+  return true;
 }
 
 }  // namespace
+
+// The Q4_K tile plan as 8 ints a launch (qvx_qgemm_plan_q4k); returns the launch count.
+int q4k_plan_desc(int M, int N, int K, int cus, int* desc, int cap) {
+  Q4kPlan p;
+  q4k_plan(M, N, K, cus > 0 ? cus : device_cus(), p);
+  for (int i = 0; i < p.n && i < cap; ++i) {
+    const Q4kLaunch& L = p.l[i];
+    const int v[8] = {L.bm, L.splits, L.ntiles, L.tm.cols_a, L.tm.mt_a, L.tm.base_a, L.tm.mt_b, L.tm.base_b};
+    for (int j = 0; j < 8; ++j) desc[8 * i + j] = v[j];
+  }
+  return p.n;
+}
 
 // Returns a QVX status (0 ok, -1 type, -5 HIP, -7 range).
 int launch_qgemm_dequant(float* out, const void* w, uint32_t t, const uint16_t* X, int M, int rows, int cols,
@@ -970,10 +1051,10 @@ int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M
     void* xb = gemm_ws(n * 2u, ws, ws_cap, s);
     if (!xb) return no_mem;
     // a K-split launch accumulates into a zeroed output: zero it in the prepass when it is aligned
-    int bm, splits;
-    q4k_plan(M, rows, cols, bm, splits);
+    Q4kPlan plan;
+    q4k_plan(M, rows, cols, device_cus(), plan);
     const size_t nout = (size_t)M * (size_t)rows;
-    const bool fuse = splits > 1 && !(reinterpret_cast<uintptr_t>(out) & 15u) && nout % 4 == 0;
+    const bool fuse = plan.l[0].splits > 1 && !(reinterpret_cast<uintptr_t>(out) & 15u) && nout % 4 == 0;
     k_f16_to_bf16<<<(unsigned)((n / 8 + 255) / 256), 256, 0, s>>>(
         reinterpret_cast<const uint4*>(X), static_cast<uint4*>(xb), n / 8, reinterpret_cast<float4*>(out),
         fuse ? nout / 4 : 0);
