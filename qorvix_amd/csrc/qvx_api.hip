@@ -48,6 +48,9 @@ void launch_fill_normal_f16(uint16_t* x, size_t n, uint64_t seed, float mul, hip
 void launch_read16(const void* src, size_t n16, uint32_t* flag, hipStream_t s);
 bool qgemm_deq_supported(uint32_t t, const void* w, const uint16_t* X, int K, int N, size_t row_bytes);
 int q4k_plan_desc(int M, int N, int K, int cus, int* desc, int cap);
+bool gemv_q6n_supported(int rows, int cols, size_t row_bytes);
+bool launch_gemv_q6n(const void* w, const float* X, float* Y, int nvec, int rows, int cols, size_t row_bytes,
+                     hipStream_t s);
 int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M, int rows, int cols,
                  int variant, hipStream_t s, void* ws, size_t ws_cap);
 int launch_quantize_act_q8(const uint16_t* X, int M, int K, int8_t* q, float* scale, int32_t* qsum,
@@ -87,6 +90,7 @@ struct qvx_plan {
 namespace {
 
 constexpr int kMaxBlock = 256;  // largest block the operator accepts (qmatmul.cpp:11)
+int kQ6nMin = 3;                 // smallest Q6_K batch on the matrix-core form
 
 inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
@@ -215,6 +219,13 @@ int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int
                                   : launch_gemv_mxj_q4k(w, Xv, Yv, nv, rows, cols, row_bytes, s);
       if (!ok) return refused();
     }
+    return hip_status();
+  }
+  // Q6_K batches of kQ6nMin or more vectors stream the weights once per 16 vectors on the
+  // matrix-core form (rows of 2048-element multiples), bit-identical per vector to the VALU kernel
+  // that takes single vectors.
+  if (fast && type == T_Q6_K && nvec >= kQ6nMin && !epi.flags() && gemv_q6n_supported(rows, cols, row_bytes)) {
+    if (!launch_gemv_q6n(w, X, out, nvec, rows, cols, row_bytes, s)) return refused();
     return hip_status();
   }
   const int mx = (fast && type == T_Q4_K) ? gemv_mx_max_nv(cols) : 0;

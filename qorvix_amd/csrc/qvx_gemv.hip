@@ -246,7 +246,12 @@ template <> struct Lane<T_Q6_K> {
     // type is unsigned: the (int) keeps the conversion signed.
     const float sa = (float)(int)__builtin_amdgcn_sbfe((int)r.s0, 8u * r.ssh, 8u);
     const float sb = (float)(int)__builtin_amdgcn_sbfe((int)r.s1, 8u * r.ssh, 8u);
-    return f16lo(r.dd) * __builtin_fmaf(sb, (float)tb, sa * (float)ta);
+    return fold(f16lo(r.dd), sa, sb, ta, tb);
+  }
+  // The slot's partial from its two exact run sums (sum (code - 32) q per run): shared with the
+  // batched matrix-core form, so both evaluate the same float operations.
+  static __device__ inline float fold(float d, float sa, float sb, int ta, int tb) {
+    return d * __builtin_fmaf(sb, (float)tb, sa * (float)ta);
   }
 };
 
@@ -408,7 +413,8 @@ __device__ inline const float* task_x(const float* X, int cols, int S, int t) {
 }
 
 template <int R>
-__device__ inline void convert_task(const float4 x0, const float4 x1, int t, bool store, uint32_t* xs) {
+__device__ inline void convert_task(const float4 x0, const float4 x1, int t, bool store, uint32_t* xs,
+                                    float* sx_out = nullptr) {
   const int vs = t / (2 * R), part = t % (2 * R), run = part >> 1, hf = part & 1;
   float a = fmaxf(fmaxf(fmaxf(fabsf(x0.x), fabsf(x0.y)), fmaxf(fabsf(x0.z), fabsf(x0.w))),
                   fmaxf(fmaxf(fabsf(x1.x), fabsf(x1.y)), fmaxf(fabsf(x1.z), fabsf(x1.w))));
@@ -450,6 +456,7 @@ __device__ inline void convert_task(const float4 x0, const float4 x1, int t, boo
     o[4 * R + w + 1] = __builtin_amdgcn_perm(ls[3], ls[2], 0x06040200u);
     if (hf == 0) o[8 * R + run] = (uint32_t)sq;
     if (part == 0) o[9 * R] = __builtin_bit_cast(uint32_t, a * (1.0f / 16383.0f) + z);
+    if (part == 0 && sx_out) *sx_out = a * (1.0f / 16383.0f) + z;
   }
 }
 
@@ -585,7 +592,12 @@ __global__ __launch_bounds__(1024) void k_gemv(const uint8_t* __restrict__ W, co
 #pragma unroll
     for (int i = 0; i < RMAX; ++i) {
 #pragma unroll
-      for (int v = 0; v < NV; ++v) p[i][v] = L::row(raw[i % PF], sig, x[v]) * (x[v].sx * keep);
+      for (int v = 0; v < NV; ++v) {
+        p[i][v] = L::row(raw[i % PF], sig, x[v]) * (x[v].sx * keep);
+        // the product is rounded before the lane sums add it (no fused multiply-add into them), the
+        // arithmetic the batched matrix-core form reproduces
+        asm volatile("" : "+v"(p[i][v]));
+      }
       if (CH || i + PF < RMAX)
         L::load(wb + (uint32_t)min(g + G * (i0 + i + PF), cnt - 1) * geo.row_bytes, sig, raw[i % PF]);
       __builtin_amdgcn_sched_barrier(0);
@@ -629,6 +641,466 @@ __global__ __launch_bounds__(1024) void k_gemv(const uint8_t* __restrict__ W, co
       }
     }
   }
+}
+
+// ---- batched Q6_K on the matrix cores ----------------------------------------------------------
+// qmatmul_n over Q6_K weights, NV (8 or 16) vectors a launch, each weight byte streamed once, and
+// bit-identical per vector to the one-vector VALU kernel above (k_gemv<T_Q6_K, ...>):
+//  * the same slots (32 elements: quarters e and e+2 of a 16-element column range of a
+//    128-element half, Lane<T_Q6_K>), the same activation conversion (convert_task<2>), the same
+//    exact integer run sums -- here sum (code - 32) q over a run, which equals the VALU kernel's
+//    dotq - 32 Q -- and the same float fold (Lane<T_Q6_K>::fold, times sx);
+//  * the same reduction.  The VALU kernel sums a row's slot partials over 64-lane spans with DPP and
+//    permlane swaps: a balanced pairwise tree over each 64 consecutive slots, then, for rows of
+//    more than 64 slots, those 64-slot sums in order from 0.  Here a lane adds the two slots of a
+//    pair (tree level 1), keeps a carry stack over the 8 pairs of a unit (16 slots, levels 2-4),
+//    and the combine step adds the four units of a 64-slot block (levels 5-6), then the blocks in
+//    the same order from 0.
+// MFMA (v_mfma_i32_32x32x16_i8, one per 16-element quarter of a slot pair): A = 32 rows (vector v,
+// part p: qh / ql) x the quarter's 16 fixed-point activation bytes; B = the quarter's 16 signed
+// codes (code - 32) of 32 weight rows.  Lane l supplies row / column l%32 and K elements
+// 8 (l/32)..+7 of both operands; its accumulator holds column l%32 (weight row) and rows
+// 8j + 4 (l/32) + i (i, j = 0..3): the qh and ql sums of vectors 4j + 2 (l/32) + {0, 1}.  The run
+// sum is T = (qh sum) * 128 + (ql sum), as dotq forms it.
+// Work: a unit is one 32-row tile x 16 slots (8 pairs, two super-blocks).  Workgroup b owns tpw
+// tiles and all upt = S/16 units of each; its 8 waves take units w, w+8, ...  Per pair a wave
+// converts the pair's activations for all vectors into a private LDS buffer (X read from L2),
+// reads its A fragments back, builds B from the raw blocks (loaded a super-block ahead as
+// dword-aligned windows and realigned, as the VALU kernel reads them), runs four MFMAs and folds.
+// Unit sums go to LDS; after a barrier the workgroup combines them per (tile, vector, row).
+struct Q6nGeo {
+  int S;      // slots per row (cols / 32), a multiple of 64
+  int ntile;  // 32-row tiles
+  int upt;    // 16-slot units per tile
+  int tpw;    // tiles per workgroup
+  uint32_t row_bytes;
+};
+typedef uint32_t u32x3a4_t __attribute__((ext_vector_type(3), aligned(4)));
+
+// Raw bytes of half h of one super-block of a lane's row (l%32) for its K half g = l/32: the ql
+// pieces (q&1, t) at 64h + 32(q&1) + 16t + 8g, the qh pieces t at 128 + 32h + 16t + 8g (8 bytes
+// each, read as dword-aligned 12-byte windows, never past the super-block), and the super-block's
+// 16 scale bytes (a 20-byte window ending at or before byte 210), d and byte misalignment.
+struct Q6Half {
+  u32x3a4_t ql[4], qh[2];
+  uint32_t sc[5], d, sh;
+};
+// Loads half h's pieces; the scales, d and misalignment with h = 0, from `first` (the same
+// super-block's half 0) with h = 1.
+__device__ __attribute__((always_inline)) inline void q6_load_half(const uint8_t* base, int g, int h,
+                                                                   const Q6Half& first, Q6Half& r) {
+  const uint32_t sh = (uint32_t)(uintptr_t)base & 3u;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int off = 64 * h + 32 * (k >> 1) + 16 * (k & 1) + 8 * g;
+    r.ql[k] = *reinterpret_cast<const u32x3a4_t*>(base + off - sh);
+  }
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int off = 128 + 32 * h + 16 * k + 8 * g;
+    r.qh[k] = *reinterpret_cast<const u32x3a4_t*>(base + off - sh);
+  }
+  if (h == 0) {
+    r.sh = sh;
+    const uint8_t* sw = base + 190 - ((sh + 2u) & 3u);  // [188, 208) or [190, 210) of the super-block
+#pragma unroll
+    for (int k = 0; k < 5; ++k) r.sc[k] = ldg4(sw + 4 * k);
+    r.d = ldg2(base + 208);
+  } else {
+    r.sh = first.sh;
+#pragma unroll
+    for (int k = 0; k < 5; ++k) r.sc[k] = first.sc[k];
+    r.d = first.d;
+  }
+}
+// 16 signed codes (code - 32) of quarter Q (elements 8g..8g+7 of it) of pair t as two dwords.
+template <int Q>
+__device__ __attribute__((always_inline)) inline void q6_codes(const Q6Half& r, int t, uint32_t (&c)[2]) {
+  const u32x3a4_t& l = r.ql[2 * (Q & 1) + t];
+  const u32x3a4_t& hh = r.qh[t];
+  const uint32_t ql[2] = {align_bytes(l.y, l.x, r.sh), align_bytes(l.z, l.y, r.sh)};
+  const uint32_t qh[2] = {align_bytes(hh.y, hh.x, r.sh), align_bytes(hh.z, hh.y, r.sh)};
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const uint32_t lo = (Q >> 1) ? (ql[i] >> 4) : ql[i];
+    const uint32_t hi = Q == 0 ? qh[i] << 4 : Q == 1 ? qh[i] << 2 : Q == 2 ? qh[i] : qh[i] >> 2;  // bits 2Q, 2Q+1 -> 4, 5
+    const uint32_t u = (lo & 0x0F0F0F0Fu) | (hi & 0x30303030u) | 0x80808080u;                  // code + 128 per byte
+    c[i] = (u - 0x20202020u) ^ 0x80808080u;                                                    // code - 32
+  }
+}
+
+// One slot pair (h, t) of a super-block half r for this lane's row (l%32): each vector's pair sum
+// p(slot 2p) + p(slot 2p+1), for the 8 (NV = 16) or 4 (NV = 8) vectors v = 4j + 2g + b this lane's
+// accumulators hold.  xrec: the pair's converted-activation records (record (v, e) at word
+// v*vstride + 20 e, the convert_task<2> layout); sxc: the pair's compact steps, sx of (e, g, 2j + b)
+// at e*NV + g*NV/2 + 2j + b.
+template <int NV>
+__device__ __attribute__((always_inline)) inline void q6_pair(const Q6Half& r, int h, int t, const uint32_t* xrec,
+                                                              int vstride, const float* sxc, int lane,
+                                                              float (&P)[NV / 2]) {
+  using L6 = Lane<T_Q6_K>;
+  constexpr int NJ = NV / 4;
+  const int ln = lane & 31, g = lane >> 5, av = ln >> 1, ap = ln & 1;
+  const float keep = 1.0f;
+  // 6-bit scales of slots e = 0, 1: sc[8h + t + 2e] and sc[8h + t + 2e + 4]
+  uint32_t s4[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s4[i] = r.sh ? align_bytes(r.sc[i + 1], r.sc[i], 2u) : r.sc[i + 1];
+  const float d = f16lo(r.d);
+  float4 sxv[2][NV / 8];
+#pragma unroll
+  for (int e = 0; e < 2; ++e)
+#pragma unroll
+    for (int k = 0; k < NV / 8; ++k) sxv[e][k] = reinterpret_cast<const float4*>(sxc + e * NV + g * (NV / 2))[k];
+  // A operand of quarter q = e + 2 run: vector av, part ap, elements 8g..8g+7 of the run; lanes past
+  // the launch's NV vectors hold zeros
+  uint64_t av4[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    av4[q] = av < NV ? *reinterpret_cast<const uint64_t*>(xrec + av * vstride + (q & 1) * 20 + ap * 8 + 4 * (q >> 1) + 2 * g)
+                     : 0ull;
+  float p0[NV / 2];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    uint32_t ca[2], cb[2];
+    if (e == 0) {
+      q6_codes<0>(r, t, ca);
+      q6_codes<2>(r, t, cb);
+    } else {
+      q6_codes<1>(r, t, ca);
+      q6_codes<3>(r, t, cb);
+    }
+    typedef int v16i __attribute__((ext_vector_type(16)));
+    const v16i zero = {};
+    const v16i Ca = __builtin_amdgcn_mfma_i32_32x32x16_i8((long)av4[e], (long)(((uint64_t)ca[1] << 32) | ca[0]), zero, 0, 0, 0);
+    const v16i Cb = __builtin_amdgcn_mfma_i32_32x32x16_i8((long)av4[e + 2], (long)(((uint64_t)cb[1] << 32) | cb[0]), zero, 0, 0, 0);
+    const float sa = (float)(int)__builtin_amdgcn_sbfe((int)s4[2 * h], 8u * (uint32_t)(t + 2 * e), 8u);
+    const float sb = (float)(int)__builtin_amdgcn_sbfe((int)s4[2 * h + 1], 8u * (uint32_t)(t + 2 * e), 8u);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const int ta = (int)(((uint32_t)Ca[4 * j + 2 * b] << 7) + (uint32_t)Ca[4 * j + 2 * b + 1]);
+        const int tb = (int)(((uint32_t)Cb[4 * j + 2 * b] << 7) + (uint32_t)Cb[4 * j + 2 * b + 1]);
+        const int k = 2 * j + b;
+        const float4 s4v = sxv[e][k >> 2];
+        const float sx = (k & 3) == 0 ? s4v.x : (k & 3) == 1 ? s4v.y : (k & 3) == 2 ? s4v.z : s4v.w;
+        float pe = L6::fold(d, sa, sb, ta, tb) * (sx * keep);
+        asm volatile("" : "+v"(pe));  // rounded before the pair add, as in the VALU kernel
+        if (e == 0)
+          p0[k] = pe;
+        else
+          P[k] = p0[k] + pe;
+      }
+  }
+}
+
+template <int NV>
+__global__ __launch_bounds__(512) void k_gemv_q6n(const uint8_t* __restrict__ W, const float* __restrict__ X,
+                                                  float* __restrict__ Y, int rows, int cols, int nv, Q6nGeo geo) {
+  static_assert(NV == 8 || NV == 16, "8 or 16 vectors a launch");
+  constexpr int XW = NV * 2 * 20;  // words of a wave's converted activations: (vector, slot e) records
+  constexpr int NJ = NV / 4;       // accumulator row groups j holding real vectors
+  __shared__ __attribute__((aligned(16))) uint32_t xq_all[8][XW];
+  __shared__ __attribute__((aligned(16))) float sxc_all[8][2][2][NV / 2];  // [wave][slot e][g][2j + b]
+  extern __shared__ __attribute__((aligned(16))) float res[];              // [unit][vector][32 rows]
+  using L6 = Lane<T_Q6_K>;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ln = lane & 31, g = lane >> 5;
+  uint32_t* xq = xq_all[wave];
+  const int upt = geo.upt, units = geo.tpw * upt, tile0 = blockIdx.x * geo.tpw;
+
+
+  // Conversion tasks of a pair: t = lane + 64 k (k < NV/8): record vs = t/4 = (vector, e), part t%4.
+  constexpr int KT = NV / 8;
+  auto task_ptr = [&](int pair, int k) {
+    const int t = lane + 64 * k, vs = t >> 2, part = t & 3, v = min(vs >> 1, nv - 1), e = vs & 1;
+    return X + (size_t)v * cols + L6::xoff(2 * pair + e, part >> 1) + 8 * (part & 1);
+  };
+  auto load_x = [&](int pair, float4 (&xr)[KT][2]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < KT; ++k) {
+      const float4* p = reinterpret_cast<const float4*>(task_ptr(pair, k));
+      xr[k][0] = p[0];
+      xr[k][1] = p[1];
+    }
+  };
+  auto convert = [&](const float4 (&xr)[KT][2]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < KT; ++k) {
+      const int t = lane + 64 * k, vs = t >> 2, v = vs >> 1, e = vs & 1;
+      float* so = &sxc_all[wave][e][(v >> 1) & 1][2 * (v >> 2) + (v & 1)];
+      convert_task<2>(xr[k][0], xr[k][1], t, v < nv, xq, so);
+    }
+  };
+  auto row_base = [&](int u) {
+    const int tile = tile0 + u / upt;
+    const int row = min(tile * 32 + ln, rows - 1);
+    return W + (size_t)row * geo.row_bytes + (size_t)(u % upt) * 2 * 210;
+  };
+
+  // The wave walks its steps: step i is half i%2 of super-block (i/2)%2 of unit w + 8 (i/4).  A
+  // step folds its two pairs into P0 + P1; a super-block's sum is (half 0) + (half 1), a unit's
+  // (super-block 0) + (super-block 1): the balanced tree over the unit's 8 pairs.  The next step's
+  // raw bytes are loaded at the start of a step, the next pair's activations at the start of a
+  // pair (activations first, so that a wait for them never waits for the blocks behind them).
+  Q6Half cur, nxt;
+  float4 xr[2][KT][2];
+  auto step_unit = [&](int i) { return wave + 8 * (i >> 2); };
+  auto step_base = [&](int i) { return row_base(step_unit(i)) + (size_t)((i >> 1) & 1) * 210; };
+  auto step_pair = [&](int i) { return (step_unit(i) % upt) * 8 + ((i >> 1) & 1) * 4 + (i & 1) * 2; };
+  if (wave < units) {
+    q6_load_half(step_base(0), g, 0, cur, cur);
+    load_x(step_pair(0), xr[0]);
+  }
+  float H0[NV / 2], S0[NV / 2];
+#pragma unroll 1
+  for (int i = 0; step_unit(i) < units; ++i) {
+    const bool more = step_unit(i + 1) < units;
+    const int pair0 = step_pair(i), h = i & 1;
+    float H[NV / 2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      if (t == 0)
+        load_x(pair0 + 1, xr[1]);
+      else if (more)
+        load_x(step_pair(i + 1), xr[0]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (t == 0 && more) q6_load_half(step_base(i + 1), g, (i + 1) & 1, cur, nxt);
+      __builtin_amdgcn_sched_barrier(0);
+      convert(xr[t]);
+      float P[NV / 2];
+      q6_pair<NV>(cur, h, t, xq, 40, &sxc_all[wave][0][0][0], lane, P);
+#pragma unroll
+      for (int k = 0; k < NV / 2; ++k) H[k] = t == 0 ? P[k] : H[k] + P[k];
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if ((i & 3) == 0 || (i & 3) == 2) {
+#pragma unroll
+      for (int k = 0; k < NV / 2; ++k) H0[k] = H[k];
+    } else if ((i & 3) == 1) {
+#pragma unroll
+      for (int k = 0; k < NV / 2; ++k) S0[k] = H0[k] + H[k];
+    } else {
+      const int u = step_unit(i);
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          const int kk = 2 * j + b;
+          res[((size_t)u * NV + 4 * j + 2 * g + b) * 32 + ln] = S0[kk] + (H0[kk] + H[kk]);
+        }
+    }
+    cur = nxt;
+  }
+  __syncthreads();
+
+  // Combine: units of a 64-slot block as ((U0 + U1) + (U2 + U3)), blocks in order from 0 (a row of
+  // one block takes its block sum as it is).
+  const int nb = geo.S / 64, per_tile = NV * 32;
+  for (int idx = tid; idx < geo.tpw * per_tile; idx += 512) {
+    const int tl = idx / per_tile, v = (idx % per_tile) >> 5, r = idx & 31;
+    const int row = (tile0 + tl) * 32 + r;
+    if (v >= nv || tile0 + tl >= geo.ntile || row >= rows) continue;
+    const float* U = res + ((size_t)tl * upt * NV + v) * 32 + r;
+    auto blk = [&](int k) {
+      const size_t st = (size_t)NV * 32;
+      return (U[(4 * k) * st] + U[(4 * k + 1) * st]) + (U[(4 * k + 2) * st] + U[(4 * k + 3) * st]);
+    };
+    float sum;
+    if (nb == 1) {
+      sum = blk(0);
+    } else {
+      sum = 0.0f;
+      for (int k = 0; k < nb; ++k) sum += blk(k);
+    }
+    Y[(size_t)v * rows + row] = sum;
+  }
+}
+
+// Wide form (tall weights: rows >= kQ6wRows): the same arithmetic with the activation conversion
+// shared by a workgroup.  Its 8 waves take 8 consecutive 32-row tiles and walk the super-blocks in
+// lockstep: while the waves fold super-block s from one LDS buffer, the workgroup converts s+1 into
+// the other (one conversion task a thread, X loaded a super-block ahead), and one barrier per
+// super-block swaps them.  Each wave keeps the whole row: super-block sums ((P0 + P1) + (P2 + P3)),
+// a carry stack over the 8 super-blocks of a 64-slot block, and the blocks summed in order from 0.
+template <int NV>
+__global__ __launch_bounds__(512) void k_gemv_q6w(const uint8_t* __restrict__ W, const float* __restrict__ X,
+                                                  float* __restrict__ Y, int rows, int cols, int nv,
+                                                  uint32_t row_bytes) {
+  static_assert(NV == 8 || NV == 16, "8 or 16 vectors a launch");
+  constexpr int NT = 32 * NV;  // conversion tasks of a super-block: (vector, slot of 8, part of 4)
+  __shared__ __attribute__((aligned(16))) uint32_t xq[2][NV * 8 * 20];        // records (v, slot) of a super-block
+  __shared__ __attribute__((aligned(16))) float sxc[2][4][2][2][NV / 2];     // [buf][pair][e][g][2j + b]
+  using L6 = Lane<T_Q6_K>;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ln = lane & 31, g = lane >> 5;
+  const int nsb = cols / 256, S = cols / 32;
+  const int tile = blockIdx.x * 8 + wave;
+  const uint8_t* rowp = W + (size_t)min(tile * 32 + ln, rows - 1) * row_bytes;
+
+  // conversion task t = tid: record vs = t/4 = (vector v, slot q of the super-block), part t%4
+  const int cv = min((tid >> 2) >> 3, nv - 1), cq = (tid >> 2) & 7, cpart = tid & 3;
+  const bool ctask = tid < NT;
+  auto load_x = [&](int sb, float4& x0, float4& x1) {
+    if (ctask) {
+      const float4* p = reinterpret_cast<const float4*>(X + (size_t)cv * cols + L6::xoff(8 * sb + cq, cpart >> 1) +
+                                                        8 * (cpart & 1));
+      x0 = p[0];
+      x1 = p[1];
+    }
+  };
+  auto convert = [&](int buf, const float4& x0, const float4& x1) {
+    if (ctask) {
+      const int v = (tid >> 2) >> 3;
+      float* so = &sxc[buf][cq >> 1][cq & 1][(v >> 1) & 1][2 * (v >> 2) + (v & 1)];
+      convert_task<2>(x0, x1, tid, v < nv, xq[buf], so);
+    }
+  };
+
+  float4 x0, x1;
+  load_x(0, x0, x1);
+  convert(0, x0, x1);
+  if (nsb > 1) load_x(1, x0, x1);
+  Q6Half cur, nxt;
+  q6_load_half(rowp, g, 0, cur, cur);
+  __syncthreads();
+
+  float st[3][NV / 2], run[NV / 2];
+#pragma unroll
+  for (int k = 0; k < NV / 2; ++k) run[k] = 0.0f;
+#pragma unroll 1
+  for (int sb = 0; sb < nsb; ++sb) {
+    const int buf = sb & 1;
+    if (sb + 1 < nsb) {
+      convert(buf ^ 1, x0, x1);
+      if (sb + 2 < nsb) load_x(sb + 2, x0, x1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float T[NV / 2], H[NV / 2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      // next half-step's raw bytes: half 1 of this super-block, or half 0 of the next
+      if (h == 0)
+        q6_load_half(rowp + (size_t)sb * 210, g, 1, cur, nxt);
+      else if (sb + 1 < nsb)
+        q6_load_half(rowp + (size_t)(sb + 1) * 210, g, 0, cur, nxt);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        float P[NV / 2];
+        const int pp = 2 * h + t;
+        q6_pair<NV>(cur, h, t, &xq[buf][2 * pp * 20], 8 * 20, &sxc[buf][pp][0][0][0], lane, P);
+#pragma unroll
+        for (int k = 0; k < NV / 2; ++k) H[k] = t == 0 ? P[k] : H[k] + P[k];
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int k = 0; k < NV / 2; ++k) T[k] = h == 0 ? H[k] : T[k] + H[k];
+      cur = nxt;
+    }
+    // carry stack over the 8 super-blocks of a 64-slot block, then the running sum of blocks
+    const int q = sb & 7;
+#pragma unroll
+    for (int k = 0; k < NV / 2; ++k) {
+      float c = T[k];
+      if (q & 1) {
+        c = st[0][k] + c;
+        if (q & 2) {
+          c = st[1][k] + c;
+          if (q & 4) {
+            c = st[2][k] + c;
+            run[k] = S == 64 ? c : run[k] + c;
+          } else {
+            st[2][k] = c;
+          }
+        } else {
+          st[1][k] = c;
+        }
+      } else {
+        st[0][k] = c;
+      }
+    }
+    __syncthreads();  // buffer `buf` is free for the conversion two super-blocks on; `buf ^ 1` is ready
+  }
+  const int row = tile * 32 + ln;
+  if (row < rows) {
+#pragma unroll
+    for (int j = 0; j < NV / 4; ++j)
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const int v = 4 * j + 2 * g + b;
+        if (v < nv) Y[(size_t)v * rows + row] = run[2 * j + b];
+      }
+  }
+}
+
+constexpr int kQ6wRows = 65536;  // rows from which the wide form (8 tiles a workgroup) fills the chip
+
+template <int NV>
+static bool launch_q6w_t(const void* w, const float* X, float* Y, int nv, int rows, int cols, size_t row_bytes,
+                         hipStream_t s) {
+  static LdsLimit lim;
+  if (!lds_ready(reinterpret_cast<const void*>(&k_gemv_q6w<NV>), lim, 0)) return false;
+  const int nwg = ((rows + 31) / 32 + 7) / 8;
+  k_gemv_q6w<NV><<<nwg, 512, 0, s>>>(static_cast<const uint8_t*>(w), X, Y, rows, cols, nv, (uint32_t)row_bytes);
+  return true;
+}
+
+// LDS bytes of the unit sums (dynamic) for a launch.
+inline size_t q6n_res_bytes(int nv_t, const Q6nGeo& geo) { return (size_t)geo.tpw * geo.upt * nv_t * 32 * 4; }
+
+template <int NV>
+static bool launch_q6n_t(const void* w, const float* X, float* Y, int nv, int rows, int cols, const Q6nGeo& geo,
+                         hipStream_t s) {
+  static LdsLimit lim;
+  const size_t dyn = q6n_res_bytes(NV, geo);
+  if (!lds_ready(reinterpret_cast<const void*>(&k_gemv_q6n<NV>), lim, dyn)) return false;
+  const int nwg = (geo.ntile + geo.tpw - 1) / geo.tpw;
+  k_gemv_q6n<NV><<<nwg, 512, dyn, s>>>(static_cast<const uint8_t*>(w), X, Y, rows, cols, nv, geo);
+  return true;
+}
+
+static bool q6n_geometry(int rows, int cols, size_t row_bytes, Q6nGeo& geo) {
+  if (cols % 2048 != 0 || rows <= 0 || row_bytes > 0xFFFFFFFFull) return false;
+  geo.S = cols / 32;
+  geo.ntile = (rows + 31) / 32;
+  geo.upt = geo.S / 16;
+  geo.tpw = std::max(1, 8 / geo.upt);
+  geo.row_bytes = (uint32_t)row_bytes;
+  return q6n_res_bytes(16, geo) <= 96 * 1024;
+}
+
+// 1 if the batched matrix-core Q6_K form takes this shape (cols a multiple of 2048, rows whose unit
+// sums fit in LDS).
+bool gemv_q6n_supported(int rows, int cols, size_t row_bytes) {
+  Q6nGeo geo;
+  return q6n_geometry(rows, cols, row_bytes, geo);
+}
+
+// qmatmul_n over Q6_K on the matrix-core form, 16 vectors a launch (the last launch 8 when at most
+// 8 remain).  Returns false, having launched nothing past the failing launch, when refused.
+bool launch_gemv_q6n(const void* w, const float* X, float* Y, int nvec, int rows, int cols, size_t row_bytes,
+                     hipStream_t s) {
+  Q6nGeo geo;
+  if (!q6n_geometry(rows, cols, row_bytes, geo)) return false;
+  const bool wide = rows >= kQ6wRows;
+  for (int v0 = 0; v0 < nvec; v0 += 16) {
+    const int nv = std::min(16, nvec - v0);
+    const float* Xv = X + (size_t)v0 * cols;
+    float* Yv = Y + (size_t)v0 * rows;
+    bool ok;
+    if (wide)
+      ok = nv <= 8 ? launch_q6w_t<8>(w, Xv, Yv, nv, rows, cols, row_bytes, s)
+                   : launch_q6w_t<16>(w, Xv, Yv, nv, rows, cols, row_bytes, s);
+    else
+      ok = nv <= 8 ? launch_q6n_t<8>(w, Xv, Yv, nv, rows, cols, geo, s)
+                   : launch_q6n_t<16>(w, Xv, Yv, nv, rows, cols, geo, s);
+    if (!ok) return false;
+  }
+  return true;
 }
 
 // ---- launch ---------------------------------------------------------------------------------

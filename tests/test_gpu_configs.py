@@ -134,6 +134,20 @@ def test_gemv_q6k_lm_head_m16(cuda):
         np.testing.assert_array_equal(single.cpu().numpy().view(np.uint32), out[v].cpu().numpy().view(np.uint32))
 
 
+@pytest.mark.parametrize("rows,cols,m", [(65573, 2048, 9), (70000, 6144, 16), (128256, 4096, 5)])
+def test_gemv_q6k_wide_form(cuda, rows, cols, m):
+    """The wide batched Q6_K form (weights of 65536 rows or more; the workgroup shares each
+    super-block's activation conversion across 8 tiles): ragged last tiles, a row of one 64-slot
+    block and of several, a 16 + 0 and a 9-vector launch; every vector bit-identical to a one-vector
+    call."""
+    t = qvx.Q6_K
+    W, X, out = _check_gemv_slice(cuda, t, rows, cols, m, seed=8150 + m, stride=101)
+    for v in range(m):
+        single = qvx.qmatmul_t(W, t, X[v], rows, cols)
+        cuda.cuda.synchronize()
+        np.testing.assert_array_equal(single.cpu().numpy().view(np.uint32), out[v].cpu().numpy().view(np.uint32))
+
+
 @pytest.mark.parametrize("rows,cols", [(14336, 4096), (4096, 14336)])
 def test_gemv_q4k_m512(cuda, rows, cols):
     """qmatmul_n over 512 vectors at config 3's Q4_K shapes (64 launches of 8 vectors)."""

@@ -243,6 +243,25 @@ def test_gemv_q4k_batched_form_bit_identical(cuda, rows, cols, nvec):
         np.testing.assert_array_equal(f32bits(got[v]), f32bits(single[0]))
 
 
+@pytest.mark.parametrize("rows,cols,nvec", [(300, 2048, 5), (17, 2048, 16), (1000, 14336, 8), (4099, 4096, 16),
+                                             (64, 6144, 9), (33, 4096, 3), (257, 4096, 20)])
+def test_gemv_q6k_batched_form_bit_identical(cuda, rows, cols, nvec):
+    """The batched matrix-core Q6_K form (8 or 16 vectors a launch, K a multiple of 2048): within
+    tolerance of the oracle and bit-identical to one-vector calls (the VALU kernel), for rows of one
+    64-slot block (no running sum) and of several, ragged 32-row tiles, and launches of 16 + 4
+    vectors; one vector is all zeros (the signs of zero sums must agree too)."""
+    t = qvx.Q6_K
+    rng = np.random.default_rng(rows + 7 * cols + nvec)
+    w = random_weight(t, rows, cols, rng)
+    X = rng.standard_normal((nvec, cols)).astype(np.float32)
+    X[1] = 0.0
+    got = run_gemv(cuda, w, t, X, rows, cols)
+    assert max_rel(got, oracle.matmul_f64(w, t, X, nvec, rows, cols)) <= GEMV_TOL
+    for v in range(nvec):
+        single = run_gemv(cuda, w, t, X[v:v + 1], rows, cols)
+        np.testing.assert_array_equal(f32bits(got[v]), f32bits(single[0]))
+
+
 @pytest.mark.parametrize("rows,cols,nvec", [(4096, 14336, 16), (4096, 14336, 3), (300, 14336, 5), (4099, 14336, 8),
                                              (17, 5120, 2), (64, 4352, 7), (1000, 28672, 8), (33, 4608, 6)])
 def test_gemv_q4k_long_row_batched_form_bit_identical(cuda, rows, cols, nvec):
