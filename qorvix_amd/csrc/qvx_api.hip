@@ -90,7 +90,14 @@ struct qvx_plan {
 namespace {
 
 constexpr int kMaxBlock = 256;  // largest block the operator accepts (qmatmul.cpp:11)
-int kQ6nMin = 3;                 // smallest Q6_K batch on the matrix-core form
+// Whether a Q6_K batch takes the matrix-core form (measured crossovers against the VALU kernel on
+// MI355X: 128256 rows from 3 vectors, 14336 from 5, 4096 from 8, fewer rows from 12).
+inline bool q6_batched(int nvec, int rows) {
+  if (rows >= 65536) return nvec >= 3;
+  if (rows >= 8192) return nvec >= 5;
+  if (rows >= 4096) return nvec >= 8;
+  return nvec >= 12;
+}
 
 inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
@@ -221,10 +228,11 @@ int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int
     }
     return hip_status();
   }
-  // Q6_K batches of kQ6nMin or more vectors stream the weights once per 16 vectors on the
-  // matrix-core form (rows of 2048-element multiples), bit-identical per vector to the VALU kernel
-  // that takes single vectors.
-  if (fast && type == T_Q6_K && nvec >= kQ6nMin && !epi.flags() && gemv_q6n_supported(rows, cols, row_bytes)) {
+  // Q6_K batches stream the weights once per 16 vectors on the matrix-core form (rows of
+  // 2048-element multiples), bit-identical per vector to the VALU kernel that takes single vectors.
+  // Below the measured crossovers (few rows leave that form's grid thin) the VALU kernel, four
+  // vectors a launch, is faster.
+  if (fast && type == T_Q6_K && q6_batched(nvec, rows) && !epi.flags() && gemv_q6n_supported(rows, cols, row_bytes)) {
     if (!launch_gemv_q6n(w, X, out, nvec, rows, cols, row_bytes, s)) return refused();
     return hip_status();
   }
