@@ -449,6 +449,19 @@ def gemm_leg(torch, stream, t, wps, copies, steps, cpu):
     return gemm
 
 
+def calibration_copy(torch, dev, mib):
+    """One plain device copy of `mib` MiB: the PMC byte counters' scale for a known transfer."""
+    n = mib << 20
+    a = torch.empty(n, dtype=torch.uint8, device=dev)
+    b = torch.empty(n, dtype=torch.uint8, device=dev)
+    a.fill_(1)
+    torch.cuda.synchronize()
+    b.copy_(a)
+    torch.cuda.synchronize()
+    log(f"[bench] calibration copy of {mib} MiB done")
+    del a, b
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -483,6 +496,8 @@ def main():
         print(json.dumps({"sweep": decode_sweep(torch, stream, args.sweep_steps, cpu=not args.no_cpu)}), flush=True)
         return
     if args.configs_only:  # profiler pass over the configs[0..2] GEMV points alone
+        if args.calibrate_copy:
+            calibration_copy(torch, dev, args.calibrate_copy)
         print(json.dumps({"config_gemvs": config_gemvs(torch, stream, 200, cpu=not args.no_cpu)}), flush=True)
         return
     t = qvx.Q4_K
@@ -566,15 +581,7 @@ def main():
     log(f"[bench] GEMV per-launch event pairs: median {pair_med:.2f} us, min {pair_us[0]:.2f} us")
 
     if args.calibrate_copy:
-        n = args.calibrate_copy << 20
-        a = torch.empty(n, dtype=torch.uint8, device=dev)
-        b = torch.empty(n, dtype=torch.uint8, device=dev)
-        a.fill_(1)
-        torch.cuda.synchronize()
-        b.copy_(a)
-        torch.cuda.synchronize()
-        log(f"[bench] calibration copy of {args.calibrate_copy} MiB done")
-        del a, b
+        calibration_copy(torch, dev, args.calibrate_copy)
 
     # ---- prefill GEMM ----------------------------------------------------
     gemm = {} if args.gemv_only else gemm_leg(torch, stream, t, wps, copies, args.gemm_steps, cpu=not args.no_cpu)
