@@ -506,8 +506,16 @@ struct Geo {
 // activations first, then the first PF rows, and each later row PF rows ahead of its use, so a
 // row's arithmetic waits only for its own bytes while the next ones are arriving.
 // NORM: the activations are rmsnorm(x, NW, eps), folded into the conversion (cols % 512 == 0).
+// Threads of a workgroup: 1024, or 512 for four vectors of the formats other than Q6_K, whose four
+// vectors' fixed-point activations need more registers than a wave may hold at 16 waves a CU.  The
+// per-vector arithmetic does not depend on how many groups a workgroup holds.
+template <uint32_t T, int NV>
+constexpr int gemv_threads() {
+  return NV == 4 && T != T_Q6_K ? 512 : 1024;
+}
+
 template <uint32_t T, int NV, int RMAX, int TPT, int PF, bool CH, bool NORM>
-__global__ __launch_bounds__(1024) void k_gemv(const uint8_t* __restrict__ W, const float* __restrict__ X,
+__global__ __launch_bounds__((gemv_threads<T, NV>())) void k_gemv(const uint8_t* __restrict__ W, const float* __restrict__ X,
                                                float* __restrict__ Y, int rows, int cols, Geo geo,
                                                const float* __restrict__ NW, float eps) {
   using L = Lane<T>;
@@ -1166,6 +1174,7 @@ static bool launch_nv2(const void* w, const float* X, float* Y, int rows, int co
                        const GemvEpi& epi, hipStream_t s) {
   const int threads = geo.G * geo.Sp;
   const int tpt = (NV * geo.S * 2 * Lane<T>::kR + threads - 1) / threads;
+  if (tpt > 8) return false;  // the kernel converts at most 8 tasks a thread
   if (tpt <= 1) return launch_tpt<T, NV, 1, NORM>(w, X, Y, rows, cols, geo, epi, s);
   if (tpt <= 2) return launch_tpt<T, NV, 2, NORM>(w, X, Y, rows, cols, geo, epi, s);
   if (tpt <= 4) return launch_tpt<T, NV, 4, NORM>(w, X, Y, rows, cols, geo, epi, s);
@@ -1174,27 +1183,29 @@ static bool launch_nv2(const void* w, const float* X, float* Y, int rows, int co
 template <uint32_t T, int NV>
 static bool launch_nv(const void* w, const float* X, float* Y, int rows, int cols, const Geo& geo,
                       const GemvEpi& epi, hipStream_t s) {
-  return epi.norm_w ? launch_nv2<T, NV, true>(w, X, Y, rows, cols, geo, epi, s)
-                    : launch_nv2<T, NV, false>(w, X, Y, rows, cols, geo, epi, s);
+  Geo g = geo;
+  g.G = gemv_threads<T, NV>() / geo.Sp;  // the caller checked Sp <= the workgroup's threads
+  return epi.norm_w ? launch_nv2<T, NV, true>(w, X, Y, rows, cols, g, epi, s)
+                    : launch_nv2<T, NV, false>(w, X, Y, rows, cols, g, epi, s);
 }
 
 template <uint32_t T>
 static bool launch_type(const void* w, const float* X, float* Y, int nvec, int rows, int cols, const Geo& geo,
                         const GemvEpi& epi, hipStream_t s) {
-  // Q6_K takes four vectors a launch when their activations fit in LDS (its 4-vector kernels
-  // stay within the register file; the other formats' would spill), so the weights are streamed
-  // once per four vectors instead of once per two.
-  const bool nv4 = T == T_Q6_K && gemv_lds_bytes<T>(4, geo.S) <= 150 * 1024;
+  // Four vectors a launch when their activations fit in LDS, so the weights are streamed once per
+  // four vectors instead of once per two: Q6_K at 1024 threads, the other formats at 512 (groups
+  // of up to 512 lanes).
+  constexpr int thr4 = gemv_threads<T, 4>();
+  const bool nv4 = gemv_lds_bytes<T>(4, geo.S) <= 150 * 1024 && geo.Sp <= thr4 &&
+                   4 * geo.S * 2 * Lane<T>::kR <= 8 * thr4;  // at most 8 conversion tasks a thread
   for (int v0 = 0; v0 < nvec;) {
     const float* Xv = X + (size_t)v0 * cols;
     float* Yv = Y + (size_t)v0 * rows;
     const int left = nvec - v0;
-    if constexpr (T == T_Q6_K) {
-      if (nv4 && left >= 4) {
-        if (!launch_nv<T, 4>(w, Xv, Yv, rows, cols, geo, epi, s)) return false;
-        v0 += 4;
-        continue;
-      }
+    if (nv4 && left >= 4) {
+      if (!launch_nv<T, 4>(w, Xv, Yv, rows, cols, geo, epi, s)) return false;
+      v0 += 4;
+      continue;
     }
     if (left >= 2) {
       if (!launch_nv<T, 2>(w, Xv, Yv, rows, cols, geo, epi, s)) return false;
