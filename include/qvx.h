@@ -18,9 +18,8 @@
  *  - Device entry points take device pointers and a hipStream_t passed as `void*` (NULL = the
  *    null stream).  They are asynchronous and stream-ordered, like the CUDA backend's matmulS
  *    launch (cuda/src/cuda_backend.cu:1534-1542).  They allocate no device memory, except
- *    qvx_qgemm_f16 with QVX_GEMM_BF16 / QVX_GEMM_I8 or a weight type other than Q4_K, which takes a
- *    stream-ordered temporary for the converted activations (or the dequantised weight) from a
- *    memory pool the library owns per device.
+ *    qvx_qgemm_f16, which takes stream-ordered temporaries (the converted activations, the partial
+ *    tiles of a K split, or the dequantised weight) from a memory pool the library owns per device.
  *  - Entry points ending in _host take host pointers and are synchronous: the exact calling
  *    convention of the reference's CPU operator, for a CPU-side drop-in.
  *  - Calls that overlap on one device are safe for distinct outputs; the library holds no
@@ -147,7 +146,9 @@ int qvx_interleave_rows16(void* d_dst, const void* d_a, const void* d_b, uint32_
  * stream-ordered 16-bit temporary (fp16, bf16 for QVX_GEMM_BF16) and multiplied by one rocBLAS
  * gemm_ex (fp32 accumulate), rocBLAS being loaded on first use (QVX_E_LIB when it is missing or
  * fails; these calls create a rocBLAS handle per host thread and device on first use, so they are
- * not for graph capture).  QVX_GEMM_I8 takes Q4_K only (other types: QVX_E_TYPE). */
+ * not for graph capture).  QVX_GEMM_I8 takes Q4_K only (other types: QVX_E_TYPE).  Grids smaller
+ * than the chip (small M) split K across workgroups; the last split of each output tile adds the
+ * partial tiles in split order, so every call returns the same bits for the same inputs. */
 int qvx_qgemm_f16(float* d_out, const void* d_w, uint32_t type, const uint16_t* d_X, int M,
                   int rows, int cols, int variant, void* stream);
 
@@ -160,7 +161,8 @@ int qvx_qgemm_f16(float* d_out, const void* d_w, uint32_t type, const uint16_t* 
  * or Q6_K with cols a multiple of 64, X 16-byte and W 4-byte aligned, and not QVX_GEMM_I8 (other
  * calls: QVX_E_TYPE, as their GEMM goes through a library that allocates); a call whose
  * temporaries exceed the scratch -> QVX_E_RANGE (QVX_GEMM_BF16 needs 2*M*cols bytes, QVX_GEMM_I8
- * about 1.25*M*cols; QVX_GEMM_F16 needs none).  Every call on a device shares that device's scratch:
+ * about 1.25*M*cols, QVX_GEMM_F16 none; plus, when a grid smaller than the chip splits K, 128 KiB
+ * of partial tile per tile and split -- qvx_qgemm_plan_q4k reports both for Q4_K).  Every call on a device shares that device's scratch:
  * calls that overlap on one device (different streams, or host threads) race and must be ordered by
  * the caller. */
 #define QVX_NOALLOC_SCRATCH_BYTES (64u << 20)

@@ -149,6 +149,54 @@ inline bool lds_ready(const void* kern, LdsLimit& lim, size_t dyn) {
   return true;
 }
 
+// Deterministic K-split epilogue of the GEMM kernels.  The S workgroups of one output tile (grid z =
+// split 0..S-1) each store their NA accumulators per thread to part[z][a][thread] (the tile's
+// S * NA * nthr floats); the one that arrives last at the tile's counter adds them in split order
+// 0, 1, ..., S-1 into acc and returns true: it stores the tile.  The others return false and exit.
+// No workgroup waits for another.  Every split must call this (an empty K range stores zeros), and
+// the counters start at zero.  `last` is one int of LDS that no wave still reads (a word of a
+// staging buffer once the K loop is over).
+// Visibility across the XCDs' separate L2 caches without flushing or invalidating them (a
+// device-scope fence writes back and drops the whole L2, which costs the tiles still running their
+// K loop far more than this epilogue): the partials are written and read with device-scope relaxed
+// atomic accesses, which the compiler issues coherent at device scope (sc1); every wave waits for
+// its partial stores to complete (vmcnt 0) before the barrier after which the counter is
+// incremented (a device-scope atomic), and the last split issues its loads only after that atomic
+// has returned.
+template <int NA, int NTHR>
+__device__ __forceinline__ bool split_k_last(float (&acc)[NA], float* __restrict__ part, uint32_t* cnt, int S,
+                                             int z, int tid, int* last) {
+  constexpr size_t kSplit = (size_t)NA * NTHR;
+  float* mine = part + (size_t)z * kSplit;  // uniform base: lane offsets stay 32-bit
+#pragma unroll
+  for (int a = 0; a < NA; ++a)
+    __hip_atomic_store(mine + (a * NTHR + tid), acc[a], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0)
+    *last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(S - 1);
+  __syncthreads();
+  if (!*last) return false;
+  // every partial (this split's too) is read back, so acc is free while the sums build up in it
+  static_assert(NA % 16 == 0, "accumulators come in 16s");
+  auto ld = [&](int zz, int a) {
+    return __hip_atomic_load(part + (size_t)zz * kSplit + (a * NTHR + tid), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+  };
+#pragma unroll
+  for (int a0 = 0; a0 < NA; a0 += 16) {
+    float sum[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) sum[j] = ld(0, a0 + j);
+    for (int zz = 1; zz < S; ++zz)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) sum[j] += ld(zz, a0 + j);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[a0 + j] = sum[j];
+  }
+  return true;
+}
+
 // SplitMix64 finaliser (Steele, Lea, Flood 2014): a counter-based 64-bit hash for seeded data.
 __host__ __device__ inline uint64_t splitmix64(uint64_t z) {
   z += 0x9E3779B97F4A7C15ull;

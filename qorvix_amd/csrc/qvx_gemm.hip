@@ -32,7 +32,8 @@
 // A launch covers two kinds of columns with their own tile count and first token (TileMap), so the
 // host can cut M into one full round of 256-token tiles plus one of shorter tiles where a uniform
 // grid would leave the chip part-idle in its last round.  Grids smaller than the chip split K
-// across workgroups and accumulate with fp32 atomics into a zero-filled output.
+// across workgroups: each split stores its partial tile, and the split that finishes a tile last
+// adds the partials in split order and stores the tile, so results do not vary between runs.
 //
 // The bf16 variant first rounds X to bf16 (RNE) in a prepass into a stream-ordered temporary; the
 // fp16 variant reads X as is.
@@ -196,11 +197,12 @@ struct GemmGeo {
   int M, N, K;
   uint32_t row_bytes;  // bytes of one weight row
   int per_split;       // K slices per workgroup along grid z
-  int atomic_out;      // 1: accumulate into a zeroed output (split K)
   uint32_t mask_lo;    // 0x0F0F0F0F and 0xF0F0F0F0, passed at run time: with compile-time masks the
   uint32_t mask_hi;    // compiler re-extracts every nibble (bfe) instead of one AND per dword
   uint32_t m_b0;       // 0x000F000F: bits 0-3 of each 16-bit half (fp16 mantissa bits 0-3)
   uint32_t m_b4;       // 0x00F000F0: bits 4-7 of each 16-bit half (fp16 mantissa bits 4-7)
+  float* part = nullptr;     // K-split launches: partial tiles [tile][split][BM * 256]
+  uint32_t* cnt = nullptr;   // ... and one arrival counter per tile, zero before the launch
 };
 
 // Tile numbering of one launch: columns 0..cols_a-1 hold mt_a tiles from token base_a, columns
@@ -234,11 +236,12 @@ __global__ __launch_bounds__(512) void k_qgemm_q4k(const uint8_t* __restrict__ W
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ln = lane & 31, g = lane >> 5;
-  int n0, m0;
+  int n0, m0, tile_id;
   {
     const int nb = (int)gridDim.x;
     int b = (int)blockIdx.x;
     if ((nb & 7) == 0) b = (b & 7) * (nb >> 3) + (b >> 3);  // XCD b % 8 takes a contiguous range
+    tile_id = b;
     const int na = tm.cols_a * tm.mt_a;
     if (b < na) {
       n0 = (b / tm.mt_a) * kBN;
@@ -472,6 +475,18 @@ __global__ __launch_bounds__(512) void k_qgemm_q4k(const uint8_t* __restrict__ W
   if (kb < kb1) slice(kb, b0, b1, a);
   wait_vm<0>();
 
+  // K split: the split that finishes a tile last sums the partials in split order and stores it.
+  if (gridDim.z > 1) {
+    float v[MT * 16];
+#pragma unroll
+    for (int a = 0; a < MT * 16; ++a) v[a] = acc[a >> 4][a & 15];
+    if (!split_k_last<MT * 16, 512>(v, geo.part + (size_t)tile_id * gridDim.z * (MT * 16 * 512), geo.cnt + tile_id,
+                                    (int)gridDim.z, (int)blockIdx.z, tid, reinterpret_cast<int*>(xs)))
+      return;
+#pragma unroll
+    for (int a = 0; a < MT * 16; ++a) acc[a >> 4][a & 15] = v[a];
+  }
+
 #pragma unroll
   for (int i = 0; i < MT; ++i) {
     const int n = n0 + 32 * wave + ln;
@@ -479,13 +494,7 @@ __global__ __launch_bounds__(512) void k_qgemm_q4k(const uint8_t* __restrict__ W
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int m = m0 + 32 * i + 8 * (e >> 2) + 4 * g + (e & 3);
-      if (m < M) {
-        float* dst = Y + (size_t)m * N + n;
-        if (geo.atomic_out)
-          unsafeAtomicAdd(dst, acc[i][e]);
-        else
-          *dst = acc[i][e];
-      }
+      if (m < M) Y[(size_t)m * N + n] = acc[i][e];
     }
   }
 }
@@ -507,7 +516,7 @@ constexpr int kI8BM = 128;
 // Quantiser prepass: one thread per 32-value block of the (tile-padded) M x K activations.  Writes
 // q int8 [M, K] and, for slice kb and token tile t, SC[((kb * ntile + t) * 4 + a) * 128 + m % 128]
 // with a = 0, 1: scale of block 2kb + a; a = 2, 3: scale * qsum of block 2kb + a - 2 (zeros for
-// padding rows).  The same launch zeroes z4[0, nz4) (the output of a K-split GEMM, 16-byte aligned).
+// padding rows).  The same launch zeroes z4[0, nz4) (the tile counters of a K-split GEMM).
 __global__ __launch_bounds__(256) void k_quant_q8_gemm(const uint16_t* __restrict__ X, int M, int K, int Mpad,
                                                        int8_t* __restrict__ q, float* __restrict__ sc,
                                                        float4* __restrict__ z4, size_t nz4) {
@@ -714,6 +723,18 @@ __global__ __launch_bounds__(256) void k_qgemm_q4k_i8(const uint8_t* __restrict_
     __builtin_amdgcn_s_barrier();
   }
 
+  if (gridDim.z > 1) {
+    const int t = (int)(blockIdx.y * gridDim.x + blockIdx.x);
+    float v[MT * 32];
+#pragma unroll
+    for (int a = 0; a < MT * 32; ++a) v[a] = acc[a >> 5][(a >> 4) & 1][a & 15];
+    if (!split_k_last<MT * 32, 256>(v, geo.part + (size_t)t * gridDim.z * (MT * 32 * 256), geo.cnt + t,
+                                    (int)gridDim.z, (int)blockIdx.z, tid, reinterpret_cast<int*>(xs)))
+      return;
+#pragma unroll
+    for (int a = 0; a < MT * 32; ++a) acc[a >> 5][(a >> 4) & 1][a & 15] = v[a];
+  }
+
 #pragma unroll
   for (int i = 0; i < MT; ++i)
 #pragma unroll
@@ -723,19 +744,13 @@ __global__ __launch_bounds__(256) void k_qgemm_q4k_i8(const uint8_t* __restrict_
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int m = m0 + 32 * i + 8 * (e >> 2) + 4 * g + (e & 3);
-        if (m < M) {
-          float* dst = Y + (size_t)m * N + n;
-          if (geo.atomic_out)
-            unsafeAtomicAdd(dst, acc[i][j][e]);
-          else
-            *dst = acc[i][j][e];
-        }
+        if (m < M) Y[(size_t)m * N + n] = acc[i][j][e];
       }
     }
 }
 
 // fp16 -> bf16 (round to nearest even), 8 values a thread; the same launch also zeroes z4[0, nz4)
-// (the output of a K-split GEMM, 16-byte aligned) with a grid-stride loop.
+// (the tile counters of a K-split GEMM) with a grid-stride loop.
 __global__ __launch_bounds__(256) void k_f16_to_bf16(const uint4* __restrict__ x, uint4* __restrict__ y, size_t n8,
                                                      float4* __restrict__ z4, size_t nz4) {
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
@@ -874,12 +889,12 @@ struct Q4kPlan {
 
 template <int VAR, int BM>
 bool launch_q4k(float* out, const void* w, const uint16_t* X, int M, int N, int K, const Q4kLaunch& L,
-                hipStream_t s) {
+                float* part, uint32_t* cnt, hipStream_t s) {
   static LdsLimit lim;
   if (!lds_ready(reinterpret_cast<const void*>(&k_qgemm_q4k<VAR, BM>), lim, 0)) return false;
+  if (L.splits > 1 && (!part || !cnt)) return false;
   const int per = split_per(K / 64, L.splits);
-  GemmGeo geo{M,           N,           K,           (uint32_t)(K / 256) * 144u, per, L.splits > 1 ? 1 : 0,
-              0x0F0F0F0Fu, 0xF0F0F0F0u, 0x000F000Fu, 0x00F000F0u};
+  GemmGeo geo{M, N, K, (uint32_t)(K / 256) * 144u, per, 0x0F0F0F0Fu, 0xF0F0F0F0u, 0x000F000Fu, 0x00F000F0u, part, cnt};
   k_qgemm_q4k<VAR, BM><<<dim3(L.ntiles, 1, L.splits), 512, 0, s>>>(static_cast<const uint8_t*>(w), X, out, geo, L.tm);
   return true;
 }
@@ -900,8 +915,9 @@ int device_cus() {
 inline int cdiv(int a, int b) { return (a + b - 1) / b; }
 
 // Tile plan for an M x N x K launch on `cus` compute units (one 512-thread workgroup fits a CU).
-//  * Grids smaller than the chip: 128-token tiles, splitting K (fp32 atomics into a zeroed output,
-//    M*N adds per split) only while the grid is below ~200 workgroups.
+//  * Grids smaller than the chip: 128-token tiles, splitting K (each split stores its partial tile;
+//    the last split of a tile sums them in split order) only while the grid is below ~200
+//    workgroups.
 //  * Otherwise the cheapest of: a uniform grid of 256-, 192- or 128-token tiles, or two launches,
 //    the first of 256-token tiles from token 0 and the second of 192- or 128-token tiles for the
 //    rest, with two kinds of columns (x columns with a1 + b1 tiles, the others with a2 + b2).  The
@@ -956,23 +972,35 @@ void q4k_plan(int M, int N, int K, int cus, Q4kPlan& p) {
 
 template <int VAR>
 bool launch_one(float* out, const void* w, const uint16_t* X, int M, int N, int K, const Q4kLaunch& L,
-                hipStream_t s) {
+                float* part, uint32_t* cnt, hipStream_t s) {
   switch (L.bm) {
-    case 256: return launch_q4k<VAR, 256>(out, w, X, M, N, K, L, s);
-    case 192: return launch_q4k<VAR, 192>(out, w, X, M, N, K, L, s);
-    case 128: return launch_q4k<VAR, 128>(out, w, X, M, N, K, L, s);
+    case 256: return launch_q4k<VAR, 256>(out, w, X, M, N, K, L, part, cnt, s);
+    case 192: return launch_q4k<VAR, 192>(out, w, X, M, N, K, L, part, cnt, s);
+    case 128: return launch_q4k<VAR, 128>(out, w, X, M, N, K, L, part, cnt, s);
     default: return false;
   }
 }
 
-// zeroed: the caller has already zeroed the output of a K-split launch.
+// Workspace of a K-split plan (partial tiles, then the tile counters, 256-byte aligned); 0 when
+// the plan does not split K (two-launch plans never do).
+size_t q4k_split_bytes(const Q4kPlan& p) {
+  const Q4kLaunch& L = p.l[0];
+  if (L.splits <= 1) return 0;
+  const size_t parts = (size_t)L.ntiles * L.splits * L.bm * kBN * 4;
+  return parts + (((size_t)L.ntiles * 4 + 255) & ~(size_t)255);
+}
+
+// ws: the workspace of q4k_split_bytes(p) bytes, its counters already zero.
 template <int VAR>
-bool launch_var(float* out, const void* w, const uint16_t* X, int M, int N, int K, bool zeroed, hipStream_t s) {
-  Q4kPlan p;
-  q4k_plan(M, N, K, device_cus(), p);
-  if (p.l[0].splits > 1 && !zeroed) launch_zero(out, (size_t)M * N, s);
+bool launch_var(float* out, const void* w, const uint16_t* X, int M, int N, int K, const Q4kPlan& p, void* ws,
+                hipStream_t s) {
+  const size_t sb = q4k_split_bytes(p);
+  float* part = sb ? static_cast<float*>(ws) : nullptr;
+  uint32_t* cnt = sb ? reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(ws) +
+                                                   (size_t)p.l[0].ntiles * p.l[0].splits * p.l[0].bm * kBN * 4)
+                     : nullptr;
   for (int i = 0; i < p.n; ++i)
-    if (!launch_one<VAR>(out, w, X, M, N, K, p.l[i], s)) return false;
+    if (!launch_one<VAR>(out, w, X, M, N, K, p.l[i], part, cnt, s)) return false;
   return true;
 }
 
@@ -995,9 +1023,9 @@ int launch_qgemm_dequant(float* out, const void* w, uint32_t t, const uint16_t* 
                          bool bf16, hipStream_t s);
 // The dequantising MFMA GEMM of the other weight types (qvx_gemm_deq.hip).
 bool qgemm_deq_supported(uint32_t t, const void* w, const uint16_t* X, int K, int N, size_t row_bytes);
-bool qgemm_deq_splits(int M, int N, int K);
+size_t qgemm_deq_split_bytes(int M, int N, int K, size_t* counters);
 bool launch_qgemm_deq(uint32_t t, float* out, const void* w, const uint16_t* X, int M, int N, int K, size_t row_bytes,
-                      bool bf16, bool zeroed, hipStream_t s);
+                      bool bf16, void* split_ws, hipStream_t s);
 
 // Device memory for the call's temporaries: from the library's pool when ws is null, else the
 // caller's region [ws, ws + ws_cap) (the no-allocation entry point's scratch; -7 when the call needs
@@ -1021,19 +1049,30 @@ int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M
     // The other weight types: their rows dequantised into the MFMA tiles (cols % 64 == 0, aligned
     // operands) ...
     if (qgemm_deq_supported(t, w, X, cols, rows, row_bytes)) {
-      if (variant == VAR_F16)
-        return launch_qgemm_deq(t, out, w, X, M, rows, cols, row_bytes, false, false, s) ? 0 : -5;
+      // Temporaries: the bf16 copy of X (bf16 variant), then a K split's partial tiles and tile
+      // counters, the counters cleared by the bf16 prepass or a zero kernel.
       const size_t n = (size_t)M * (size_t)cols;
-      void* xb = gemm_ws(n * 2u, ws, ws_cap, s);
-      if (!xb) return no_mem;
-      const size_t nout = (size_t)M * (size_t)rows;
-      const bool fuse = qgemm_deq_splits(M, rows, cols) && !(reinterpret_cast<uintptr_t>(out) & 15u) && nout % 4 == 0;
-      k_f16_to_bf16<<<(unsigned)((n / 8 + 255) / 256), 256, 0, s>>>(
-          reinterpret_cast<const uint4*>(X), static_cast<uint4*>(xb), n / 8, reinterpret_cast<float4*>(out),
-          fuse ? nout / 4 : 0);
-      const bool ok =
-          launch_qgemm_deq(t, out, w, static_cast<const uint16_t*>(xb), M, rows, cols, row_bytes, true, fuse, s);
-      gemm_ws_release(xb, ws, s);
+      const size_t xbytes = variant == VAR_BF16 ? (n * 2u + 255) & ~(size_t)255 : 0;
+      size_t cbytes = 0;
+      const size_t sbytes = qgemm_deq_split_bytes(M, rows, cols, &cbytes);
+      uint8_t* tmp = nullptr;
+      if (xbytes + sbytes) {
+        tmp = static_cast<uint8_t*>(gemm_ws(xbytes + sbytes, ws, ws_cap, s));
+        if (!tmp) return no_mem;
+      }
+      float* cnt = sbytes ? reinterpret_cast<float*>(tmp + xbytes + sbytes - cbytes) : nullptr;
+      const uint16_t* Xg = X;
+      if (variant == VAR_BF16) {
+        k_f16_to_bf16<<<(unsigned)((n / 8 + 255) / 256), 256, 0, s>>>(
+            reinterpret_cast<const uint4*>(X), reinterpret_cast<uint4*>(tmp), n / 8, reinterpret_cast<float4*>(cnt),
+            cbytes / 16);
+        Xg = reinterpret_cast<const uint16_t*>(tmp);
+      } else if (sbytes) {
+        launch_zero(cnt, cbytes / 4, s);
+      }
+      const bool ok = launch_qgemm_deq(t, out, w, Xg, M, rows, cols, row_bytes, variant == VAR_BF16,
+                                       sbytes ? tmp + xbytes : nullptr, s);
+      if (tmp) gemm_ws_release(tmp, ws, s);
       return ok ? 0 : -5;
     }
     // ... else dequantised whole to 16 bits, then a library GEMM, which allocates (its handle, the
@@ -1046,49 +1085,65 @@ int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M
   // Buffer offsets are 32-bit: a tile's rows must span less than 2 GiB.
   if ((size_t)256 * (size_t)cols * 2u >= (1u << 31) || (size_t)kBN * (size_t)(cols / 256) * 144u >= (1u << 31))
     return -7;
-  if (variant == VAR_BF16) {
-    const size_t n = (size_t)M * (size_t)cols;
-    void* xb = gemm_ws(n * 2u, ws, ws_cap, s);
-    if (!xb) return no_mem;
-    // a K-split launch accumulates into a zeroed output: zero it in the prepass when it is aligned
+  if (variant == VAR_BF16 || variant == VAR_F16) {
+    // Temporaries: the bf16 copy of X (bf16 variant), then a K-split plan's partial tiles and tile
+    // counters.  The counters start at zero: the bf16 prepass clears them in the same launch,
+    // otherwise a zero kernel does.
     Q4kPlan plan;
     q4k_plan(M, rows, cols, device_cus(), plan);
-    const size_t nout = (size_t)M * (size_t)rows;
-    const bool fuse = plan.l[0].splits > 1 && !(reinterpret_cast<uintptr_t>(out) & 15u) && nout % 4 == 0;
-    k_f16_to_bf16<<<(unsigned)((n / 8 + 255) / 256), 256, 0, s>>>(
-        reinterpret_cast<const uint4*>(X), static_cast<uint4*>(xb), n / 8, reinterpret_cast<float4*>(out),
-        fuse ? nout / 4 : 0);
-    const bool ok = launch_var<VAR_BF16>(out, w, static_cast<const uint16_t*>(xb), M, rows, cols, fuse, s);
-    gemm_ws_release(xb, ws, s);
+    const size_t n = (size_t)M * (size_t)cols;
+    const size_t xbytes = variant == VAR_BF16 ? (n * 2u + 255) & ~(size_t)255 : 0;
+    const size_t sbytes = q4k_split_bytes(plan);
+    void* tmp = nullptr;
+    if (xbytes + sbytes) {
+      tmp = gemm_ws(xbytes + sbytes, ws, ws_cap, s);
+      if (!tmp) return no_mem;
+    }
+    uint8_t* split_ws = static_cast<uint8_t*>(tmp) + xbytes;
+    const size_t cbytes = sbytes ? (((size_t)plan.l[0].ntiles * 4 + 255) & ~(size_t)255) : 0;
+    float* cnt = sbytes ? reinterpret_cast<float*>(split_ws + sbytes - cbytes) : nullptr;
+    const size_t ncnt4 = cbytes / 16;
+    const uint16_t* Xg = X;
+    if (variant == VAR_BF16) {
+      k_f16_to_bf16<<<(unsigned)((n / 8 + 255) / 256), 256, 0, s>>>(
+          reinterpret_cast<const uint4*>(X), static_cast<uint4*>(tmp), n / 8, reinterpret_cast<float4*>(cnt), ncnt4);
+      Xg = static_cast<const uint16_t*>(tmp);
+    } else if (sbytes) {
+      launch_zero(cnt, ncnt4 * 4, s);
+    }
+    const bool ok = variant == VAR_BF16 ? launch_var<VAR_BF16>(out, w, Xg, M, rows, cols, plan, split_ws, s)
+                                        : launch_var<VAR_F16>(out, w, Xg, M, rows, cols, plan, split_ws, s);
+    if (tmp) gemm_ws_release(tmp, ws, s);
     return ok ? 0 : -5;
   }
-  if (variant == VAR_F16) return launch_var<VAR_F16>(out, w, X, M, rows, cols, false, s) ? 0 : -5;
   if (variant == VAR_I8) {
     static LdsLimit lim;
     if (!lds_ready(reinterpret_cast<const void*>(&k_qgemm_q4k_i8), lim, 0)) return -5;
     const int ntile = (M + kI8BM - 1) / kI8BM, Mpad = ntile * kI8BM, nsl = cols / 64;
-    const size_t qbytes = ((size_t)M * cols + 255) & ~(size_t)255;
-    const size_t sbytes = (size_t)nsl * ntile * 4 * kI8BM * 4;
-    if ((size_t)nsl * ntile * 4 * kI8BM * 4 >= (1u << 31)) return -7;
-    uint8_t* qb = static_cast<uint8_t*>(gemm_ws(qbytes + sbytes, ws, ws_cap, s));
-    if (!qb) return no_mem;
-    int8_t* q = reinterpret_cast<int8_t*>(qb);
-    float* sc = reinterpret_cast<float*>(qb + qbytes);
     // two int8 workgroups fit a CU (44 KB LDS, <= 256 registers): aim for ~two per CU
     const int tiles = ((rows + kBN - 1) / kBN) * ntile;
     int splits = 1;
     while (tiles * splits < 448 && nsl / (splits * 2) >= 8) splits *= 2;
     const int per = split_per(nsl, splits);
     splits = (nsl + per - 1) / per;
-    // a K-split launch accumulates into a zeroed output: zero it in the prepass when it is aligned
-    const size_t nout = (size_t)M * (size_t)rows;
-    const bool fuse = splits > 1 && !(reinterpret_cast<uintptr_t>(out) & 15u) && nout % 4 == 0;
+    // Temporaries: the Q8 copy of X, its scales, then a K split's partial tiles and tile counters
+    // (cleared by the quantiser launch).
+    const size_t qbytes = ((size_t)M * cols + 255) & ~(size_t)255;
+    const size_t sbytes = (size_t)nsl * ntile * 4 * kI8BM * 4;
+    if (sbytes >= (1u << 31)) return -7;
+    const size_t pbytes = splits > 1 ? (size_t)tiles * splits * kI8BM * kBN * 4 : 0;
+    const size_t cbytes = splits > 1 ? (((size_t)tiles * 4 + 255) & ~(size_t)255) : 0;
+    uint8_t* qb = static_cast<uint8_t*>(gemm_ws(qbytes + sbytes + pbytes + cbytes, ws, ws_cap, s));
+    if (!qb) return no_mem;
+    int8_t* q = reinterpret_cast<int8_t*>(qb);
+    float* sc = reinterpret_cast<float*>(qb + qbytes);
+    float* part = splits > 1 ? reinterpret_cast<float*>(qb + qbytes + sbytes) : nullptr;
+    uint32_t* cnt = splits > 1 ? reinterpret_cast<uint32_t*>(qb + qbytes + sbytes + pbytes) : nullptr;
     const size_t nblk = (size_t)Mpad * (cols / 32);
-    k_quant_q8_gemm<<<(unsigned)((nblk + 255) / 256), 256, 0, s>>>(X, M, cols, Mpad, q, sc,
-                                                                    reinterpret_cast<float4*>(out), fuse ? nout / 4 : 0);
-    if (splits > 1 && !fuse) launch_zero(out, nout, s);
-    GemmGeo geo{M, rows, cols, (uint32_t)(cols / 256) * 144u, per, splits > 1 ? 1 : 0,
-                0x0F0F0F0Fu, 0xF0F0F0F0u, 0x000F000Fu, 0x00F000F0u};
+    k_quant_q8_gemm<<<(unsigned)((nblk + 255) / 256), 256, 0, s>>>(
+        X, M, cols, Mpad, q, sc, reinterpret_cast<float4*>(cnt), cbytes / 16);
+    GemmGeo geo{M, rows, cols, (uint32_t)(cols / 256) * 144u, per, 0x0F0F0F0Fu, 0xF0F0F0F0u, 0x000F000Fu,
+                0x00F000F0u, part, cnt};
     dim3 grid((rows + kBN - 1) / kBN, ntile, splits);
     k_qgemm_q4k_i8<<<grid, 256, 0, s>>>(static_cast<const uint8_t*>(w), q, sc, out, geo);
     gemm_ws_release(qb, ws, s);

@@ -56,7 +56,8 @@ struct Geo {
   uint32_t row_bytes;
   uint32_t w_records;  // bytes of W the copies may read (the tensor, rounded up to a dword)
   int per_split;       // K slices per workgroup along grid z (even: ranges start a half super-block)
-  int atomic_out;      // 1: accumulate into a zeroed output (split K)
+  float* part;         // K-split launches: partial tiles [tile][split][kBM * kBN]
+  uint32_t* cnt;       // ... and one arrival counter per tile, zero before the launch
 };
 
 template <int N>
@@ -412,6 +413,21 @@ __global__ __launch_bounds__(512) void k_qgemm_q6k(const uint8_t* __restrict__ W
   }
   if (kb < kb1) slice(kb, Par<0>{});
 
+  // K split: the split that finishes a tile last sums the partials in split order and stores it.
+  if (gridDim.z > 1) {
+    constexpr int NA = TM * TN * 16;
+    const int t = (int)(blockIdx.y * gridDim.x + blockIdx.x);
+    wait_vm<0>();  // no LDS copy in flight when the flag word of xs is written
+    float v[NA];
+#pragma unroll
+    for (int a = 0; a < NA; ++a) v[a] = acc[a / (TN * 16)][(a / 16) % TN][a % 16];
+    if (!split_k_last<NA, 512>(v, geo.part + (size_t)t * gridDim.z * (NA * 512), geo.cnt + t, (int)gridDim.z,
+                               (int)blockIdx.z, tid, reinterpret_cast<int*>(xs)))
+      return;
+#pragma unroll
+    for (int a = 0; a < NA; ++a) acc[a / (TN * 16)][(a / 16) % TN][a % 16] = v[a];
+  }
+
   // C layout of v_mfma_f32_32x32x*: element e of lane l is row 8*(e/4) + 4*(l/32) + e%4, col l%32.
 #pragma unroll
   for (int i = 0; i < TM; ++i)
@@ -422,23 +438,16 @@ __global__ __launch_bounds__(512) void k_qgemm_q6k(const uint8_t* __restrict__ W
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int m = m0 + 32 * (TM * wm + i) + 8 * (e >> 2) + 4 * g + (e & 3);
-        if (m < M) {
-          float* dst = Y + (size_t)m * N + n;
-          if (geo.atomic_out)
-            unsafeAtomicAdd(dst, acc[i][j][e]);
-          else
-            *dst = acc[i][j][e];
-        }
+        if (m < M) Y[(size_t)m * N + n] = acc[i][j][e];
       }
     }
 }
 
-void launch_zero(float* p, size_t n, hipStream_t s);
-
 namespace {
 
-// 128-token tiles; K split (fp32 atomics into a zeroed output) while the grid is smaller than ~one
-// workgroup per CU and each range keeps >= 8 slices.  Ranges are an even number of slices.
+// 128-token tiles; K split (partial tiles summed in split order by the last split of each tile)
+// while the grid is smaller than ~one workgroup per CU and each range keeps >= 8 slices.  Ranges are
+// an even number of slices, none empty.
 inline void q6k_plan(int M, int N, int K, int& splits, int& per) {
   const int tiles = ((N + kBN - 1) / kBN) * ((M + kBM - 1) / kBM), nsl = K / 64;
   splits = 1;
@@ -448,16 +457,21 @@ inline void q6k_plan(int M, int N, int K, int& splits, int& per) {
   splits = (nsl + per - 1) / per;
 }
 
+inline int q6k_tiles(int M, int N) { return ((N + kBN - 1) / kBN) * ((M + kBM - 1) / kBM); }
+
 template <int VAR>
-bool launch_var(float* out, const void* w, const uint16_t* X, int M, int N, int K, size_t row_bytes, bool zeroed,
+bool launch_var(float* out, const void* w, const uint16_t* X, int M, int N, int K, size_t row_bytes, void* split_ws,
                 hipStream_t s) {
   static LdsLimit lim;
   if (!lds_ready(reinterpret_cast<const void*>(&k_qgemm_q6k<VAR>), lim, 0)) return false;
   int splits, per;
   q6k_plan(M, N, K, splits, per);
-  if (splits > 1 && !zeroed) launch_zero(out, (size_t)M * N, s);
+  if (splits > 1 && !split_ws) return false;
   const uint32_t wrec = (uint32_t)(((size_t)N * row_bytes + 3u) & ~(size_t)3u);
-  Geo geo{M, N, K, (uint32_t)row_bytes, wrec, per, splits > 1 ? 1 : 0};
+  const size_t pbytes = (size_t)q6k_tiles(M, N) * splits * kBM * kBN * 4;
+  float* part = splits > 1 ? static_cast<float*>(split_ws) : nullptr;
+  uint32_t* cnt = splits > 1 ? reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(split_ws) + pbytes) : nullptr;
+  Geo geo{M, N, K, (uint32_t)row_bytes, wrec, per, part, cnt};
   dim3 grid((N + kBN - 1) / kBN, (M + kBM - 1) / kBM, splits);
   k_qgemm_q6k<VAR><<<grid, 64 * kWaves, 0, s>>>(static_cast<const uint8_t*>(w), X, out, geo);
   return true;
@@ -476,20 +490,24 @@ bool qgemm_deq_supported(uint32_t t, const void* w, const uint16_t* X, int K, in
   return true;
 }
 
-// 1 if the launch splits K (for callers that zero the output themselves).
-bool qgemm_deq_splits(int M, int N, int K) {
+// Workspace of the launch's K split: the partial tiles, then the tile counters (256-byte aligned;
+// the counters are the last `counters` bytes and must be zero at the launch), or 0 without a split.
+size_t qgemm_deq_split_bytes(int M, int N, int K, size_t* counters) {
   int splits, per;
   q6k_plan(M, N, K, splits, per);
-  return splits > 1;
+  if (splits <= 1) return *counters = 0;
+  const size_t tiles = (size_t)q6k_tiles(M, N);
+  *counters = (tiles * 4 + 255) & ~(size_t)255;
+  return tiles * splits * kBM * kBN * 4 + *counters;
 }
 
-// Launches the GEMM (X already 16-bit: fp16 for the fp16 variant, bf16 for the bf16 one).
-// zeroed: the caller zeroed the output of a K-split launch.
+// Launches the GEMM (X already 16-bit: fp16 for the fp16 variant, bf16 for the bf16 one); split_ws:
+// the qgemm_deq_split_bytes workspace, counters zero.
 bool launch_qgemm_deq(uint32_t t, float* out, const void* w, const uint16_t* X, int M, int N, int K, size_t row_bytes,
-                      bool bf16, bool zeroed, hipStream_t s) {
+                      bool bf16, void* split_ws, hipStream_t s) {
   if (t != T_Q6_K) return false;
-  return bf16 ? launch_var<VAR_BF16>(out, w, X, M, N, K, row_bytes, zeroed, s)
-              : launch_var<VAR_F16>(out, w, X, M, N, K, row_bytes, zeroed, s);
+  return bf16 ? launch_var<VAR_BF16>(out, w, X, M, N, K, row_bytes, split_ws, s)
+              : launch_var<VAR_F16>(out, w, X, M, N, K, row_bytes, split_ws, s);
 }
 
 }  // namespace qvx

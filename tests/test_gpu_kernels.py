@@ -448,9 +448,9 @@ def test_gemm_q4k_parity(cuda, variant, M, rows, cols):
 @pytest.mark.parametrize("variant", [qvx.GEMM_BF16, qvx.GEMM_F16, qvx.GEMM_I8])
 @pytest.mark.parametrize("offset", [0, 1, 3])
 def test_gemm_split_k_overwrites_stale_output(cuda, variant, offset):
-    """M = 128 splits K across workgroups that accumulate into an output zeroed first (in the bf16
-    prepass when the output is 16-byte aligned, by the zero kernel otherwise): NaN left in the output
-    buffer never leaks into the result, at any float offset, and nothing outside it is written."""
+    """M = 128 splits K across workgroups whose partial tiles the last split of each tile sums and
+    stores: NaN left in the output buffer never leaks into the result, at any float offset, and
+    nothing outside it is written."""
     rng = np.random.default_rng(77 + 10 * variant + offset)
     t, M, rows, cols = qvx.Q4_K, 128, 512, 1024
     w = random_weight(t, rows, cols, rng, scale=0.002)
@@ -467,6 +467,32 @@ def test_gemm_split_k_overwrites_stale_output(cuda, variant, offset):
     assert np.isfinite(got[offset:offset + M * rows]).all()
     assert max_rel(got[offset:offset + M * rows].reshape(M, rows), ref) <= GEMM_TOL
     assert np.isnan(got[:offset]).all() and np.isnan(got[offset + M * rows:]).all()
+
+
+@pytest.mark.parametrize("t,variant", [(qvx.Q4_K, qvx.GEMM_BF16), (qvx.Q4_K, qvx.GEMM_F16), (qvx.Q4_K, qvx.GEMM_I8),
+                                       (qvx.Q6_K, qvx.GEMM_BF16), (qvx.Q6_K, qvx.GEMM_F16)])
+@pytest.mark.parametrize("M,rows,cols", [(128, 14336, 4096), (37, 2048, 4096), (300, 4096, 14336)])
+def test_gemm_split_k_is_deterministic(cuda, t, variant, M, rows, cols):
+    """Shapes whose grid is smaller than the chip split K; the split that finishes a tile last adds
+    the partial tiles in split order 0, 1, ..., so repeated calls (whichever split finishes first)
+    give the same bits, and the result stays within the GEMM tolerance of the fp64 oracle on a
+    slice of rows (bf16 / fp16 variants)."""
+    if t == qvx.Q4_K:
+        plan = qvx.qgemm_plan_q4k(M, rows, cols)
+        assert variant == qvx.GEMM_I8 or plan[0]["splits"] > 1
+    W = qvx.empty_weight(t, rows, cols)
+    qvx.fill_synthetic_t(W, t, rows, cols, seed=31 + M + variant, scale_mul=1e-3)
+    X = cuda.empty((M, cols), dtype=cuda.float16, device="cuda")
+    qvx.fill_normal_t(X, seed=32 + M, mul=0.5)
+    runs = [qvx.qgemm_t(W, t, X, rows, cols, variant).cpu().numpy() for _ in range(3)]
+    for r in runs[1:]:
+        np.testing.assert_array_equal(r.view(np.uint32), runs[0].view(np.uint32))
+    idx = np.union1d(np.arange(0, rows, 97), [rows - 1])
+    rb = qvx.row_bytes(t, cols)
+    Wd = oracle.dequantize(t, W.cpu().numpy().reshape(rows, rb)[idx].reshape(-1), len(idx) * cols)
+    ref = X.cpu().numpy().astype(np.float64) @ Wd.reshape(len(idx), cols).astype(np.float64).T
+    if variant != qvx.GEMM_I8:  # the Q8 arithmetic has its own oracle test
+        assert max_rel(runs[0][:, idx], ref) <= GEMM_TOL
 
 
 DEQUANT_GEMM_TYPES = [qvx.Q6_K, qvx.Q8_0, qvx.Q4_0, qvx.Q5_0, qvx.Q5_K, qvx.Q4_1, qvx.Q5_1, qvx.Q8_1,

@@ -2,8 +2,8 @@
 scratch array instead of an allocation.  Called through the C ABI and checked against
 qvx_qgemm_f16 (the same kernels with a pool-allocated temporary) and against the fp64 oracle on a row
 slice, on two calls in a row whose second input is smaller (the scratch keeps the first call's
-contents), for every variant.  Shapes without a K split must match qvx_qgemm_f16 bit for bit; a
-K-split shape (fp32 atomics, whose order varies run to run) within 1e-6.
+contents), for every variant.  Both must match qvx_qgemm_f16 bit for bit: a K-split shape sums its
+partial tiles in split order, so its result does not depend on the run.
 """
 from __future__ import annotations
 
@@ -48,15 +48,12 @@ def _case(cuda, M, rows, cols, seed):
 def test_noalloc_matches_allocating_gemm_on_two_calls(cuda, variant):
     lib = qvx.lib()
     # first call: 256-token tiles, no K split; second: smaller, 128-token tiles with a K split
-    for n, (M, rows, cols, exact) in enumerate(((1536, 14336, 4096, True), (128, 2048, 4096, False))):
+    for n, (M, rows, cols) in enumerate(((1536, 14336, 4096), (128, 2048, 4096))):
         t, W, X, idx, Wd = _case(cuda, M, rows, cols, seed=900 + 10 * n + variant)
         got = _call(lib.qvx_qgemm_f16_noalloc, cuda, W, t, X, rows, cols, variant)
         want = _call(lib.qvx_qgemm_f16, cuda, W, t, X, rows, cols, variant)
         assert np.isfinite(got).all()
-        if exact:
-            np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
-        else:
-            assert max_rel(got, want) <= 1e-6
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
         X32 = X.cpu().numpy().astype(np.float32)
         if variant == qvx.GEMM_I8:
             q, s, _ = oracle.quantize_q8_act(X32)
