@@ -499,6 +499,369 @@ __global__ __launch_bounds__(512) void k_qgemm_q4k(const uint8_t* __restrict__ W
   }
 }
 
+// ---- Q6_K on the same pipeline --------------------------------------------------------------------
+// k_qgemm_q6k8<VAR>: the structure of k_qgemm_q4k<VAR, 128> (8 waves, wave w = weight rows
+// 32w..32w+31 of a 256-row tile and all 128 tokens; X slices three stages deep; B operands
+// dequantised in registers while the MFMAs run) for Q6_K weights.  Per super-block the tile's raw
+// blocks are staged whole, two stages: each row's dword-aligned window (the block's 210 bytes after
+// up to 2 lead bytes: 14 chunks of 16 bytes), copied by 7 LDS-DMA copies per wave, copy k moving
+// chunks 2k, 2k+1 of the wave's 32 rows (lane l: row l / 2, chunk 2k + l % 2), so the wave's part of
+// a stage is [k][row][2 chunks] (each wave copies and reads only its own rows).  Slice kb covers elements 64 (kb % 4) .. +63 of a block;
+// for its half n = (kb / 2) % 2 lane (row, g) reads ql bytes 64n + 16g .. +15 (QA) and
+// 64n + 32 + 16g .. +15 (QB), qh bytes 32n + 16g .. +15 (H), the half's 8 scale bytes and d, once per
+// half, and builds both slices of the half from them (i = 0..15, P = kb % 2):
+//   element 16g + i      = (P ? QA_i >> 4 : QA_i & 15) | (H_i bits 4P, 4P+1) << 4,   scale sc[8n + g + 4P]
+//   element 32 + 16g + i = (P ? QB_i >> 4 : QB_i & 15) | (H_i bits 4P+2, 4P+3) << 4, scale sc[8n + g + 2 + 4P]
+// -- the element order of the Q4_K kernel's B operands and X fragments.  A 6-bit code c goes into the
+// mantissa of the fp16 1024 (exactly 1024 + c) and v_fma_mix_f32 gives ds (1024 + c) - 1056 ds =
+// ds (c - 32) (ds = d * sc, exact in fp32; the bias rounds once, ~2^-14 ds) before the bf16 / fp16
+// rounding of the operand.
+struct Q6kGeo {
+  int M, N, K;
+  uint32_t row_bytes;  // a multiple of 4 (an even number of blocks): every row's blocks share one alignment
+  int per_split;       // K slices per split, a multiple of 4
+  uint32_t m0f, m30, mff;  // 0x0F0F0F0F, 0x30303030, 0x00FF00FF, at run time (see GemmGeo)
+  float* part;
+  uint32_t* cnt;
+};
+constexpr int kQ6Win = 224;              // LDS bytes of a row's block window (14 chunks)
+constexpr int kQ6WStage = kBN * kQ6Win;  // one super-block of a 256-row tile: 57344 bytes
+constexpr int kQ6Copies = kQ6Win / 32;   // 16-byte copies per wave per super-block: 7
+
+typedef uint32_t q6u32x2 __attribute__((ext_vector_type(2)));
+// LDS reads (the compiler does not track them; see lds_read16): 8 and 4 bytes.
+template <int OFF>
+__device__ inline q6u32x2 lds_read8(uint32_t addr) {
+  q6u32x2 r;
+  asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF) : "memory");
+  return r;
+}
+template <int OFF>
+__device__ inline uint32_t lds_read4(uint32_t addr) {
+  uint32_t r;
+  asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF) : "memory");
+  return r;
+}
+// A half's raw window reads as issued (untouched until q6k_wait: a copy would read them early).
+struct Q6kRaw {
+  u32x4 qa, qb, h;
+  uint32_t qa4, qb4, h4, sc2, d;
+  q6u32x2 sc;
+};
+// Issues the reads of half n of the lane's row window.  row: LDS byte address of the row's chunk 0
+// (the wave's part of the stage + 32 * row); chunk c sits at row + 1024 (c / 2) + 16 (c % 2), and the
+// chunk after an even chunk 16 bytes on, after an odd one 1008 bytes on (nx = 16 or 1008 for lane K
+// half g = 0 or 1).  QA is chunk 4n + g and the next chunk's first dword, QB chunk 4n + 2 + g (+1024),
+// H (qh bytes 32n + 16g: block dwords 32 + 8n + 4g) chunk 8 + 2n + g, the scales block dwords
+// 48 + 2n .. +2 and d dword 52 (chunks 12 and 13).
+__device__ inline void q6k_issue(uint32_t row, int n, int g, Q6kRaw& w) {
+  const uint32_t nx = g ? 1008u : 16u;
+  const uint32_t a1 = row + 2048u * (uint32_t)n + 16u * (uint32_t)g, a1n = a1 + nx;
+  const uint32_t a2 = row + 1024u * (uint32_t)(4 + n) + 16u * (uint32_t)g, a2n = a2 + nx;
+  const uint32_t a3 = row + 6144u + 8u * (uint32_t)n;
+  w.qa = lds_read16<0>(a1);
+  w.qa4 = lds_read4<0>(a1n);
+  w.qb = lds_read16<1024>(a1);
+  w.qb4 = lds_read4<1024>(a1n);
+  w.h = lds_read16<0>(a2);
+  w.h4 = lds_read4<0>(a2n);
+  w.sc = lds_read8<0>(a3);
+  w.sc2 = lds_read4<8>(a3);
+  w.d = lds_read4<6160>(row);
+}
+// Waits for the reads of q6k_issue and the 4 A fragments r (all are operands: no use moves above it).
+__device__ inline void q6k_wait(u32x4* r, Q6kRaw& w) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(w.qa), "+v"(w.qb), "+v"(w.h), "+v"(w.qa4),
+                 "+v"(w.qb4), "+v"(w.h4), "+v"(w.sc), "+v"(w.sc2), "+v"(w.d)::"memory");
+}
+__device__ inline void q6k_wait(Q6kRaw& w) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(w.qa), "+v"(w.qb), "+v"(w.h), "+v"(w.qa4), "+v"(w.qb4), "+v"(w.h4), "+v"(w.sc), "+v"(w.sc2),
+                 "+v"(w.d)::"memory");
+}
+// The half realigned by the block's lead bytes sh (0 or 2): 16 QA, QB and H bytes, 8 scale bytes, d.
+struct Q6kHalf {
+  uint32_t qa[4], qb[4], h[4], s[2];
+  float d;
+};
+__device__ inline void q6k_align(const Q6kRaw& w, uint32_t sh, Q6kHalf& o) {
+  o.qa[0] = align_bytes(w.qa.y, w.qa.x, sh);
+  o.qa[1] = align_bytes(w.qa.z, w.qa.y, sh);
+  o.qa[2] = align_bytes(w.qa.w, w.qa.z, sh);
+  o.qa[3] = align_bytes(w.qa4, w.qa.w, sh);
+  o.qb[0] = align_bytes(w.qb.y, w.qb.x, sh);
+  o.qb[1] = align_bytes(w.qb.z, w.qb.y, sh);
+  o.qb[2] = align_bytes(w.qb.w, w.qb.z, sh);
+  o.qb[3] = align_bytes(w.qb4, w.qb.w, sh);
+  o.h[0] = align_bytes(w.h.y, w.h.x, sh);
+  o.h[1] = align_bytes(w.h.z, w.h.y, sh);
+  o.h[2] = align_bytes(w.h.w, w.h.z, sh);
+  o.h[3] = align_bytes(w.h4, w.h.w, sh);
+  o.s[0] = align_bytes(w.sc.y, w.sc.x, sh);
+  o.s[1] = align_bytes(w.sc2, w.sc.y, sh);
+  o.d = f16lo(align_bytes(0u, w.d, sh));
+}
+// Stages the window at byte offset soff (dword aligned, the same for every row) of this wave's 32
+// rows: copy k, lane l moves chunk 2k + l % 2 of row l / 2 (voff = that row's offset + 16 (l % 2),
+// 16 bytes from a dword-aligned address) to byte 1024k + 16l of the wave's part of the stage.  Rows
+// past the tile's buffer range read as zeros.
+__device__ __attribute__((always_inline)) inline void q6k_copy(__amdgpu_buffer_rsrc_t wr, QVX_LDS uint8_t* dst,
+                                                              uint32_t voff, uint32_t soff, int k) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, dst + 1024 * k, 16, voff, soff + 32u * (uint32_t)k, 0, 0);
+}
+__device__ __attribute__((always_inline)) inline void q6k_stage(__amdgpu_buffer_rsrc_t wr, QVX_LDS uint8_t* dst,
+                                                               uint32_t voff, uint32_t soff) {
+#pragma unroll
+  for (int k = 0; k < kQ6Copies; ++k) q6k_copy(wr, dst, voff, soff, k);
+}
+
+template <int VAR>
+__global__ __launch_bounds__(512) void k_qgemm_q6k8(const uint8_t* __restrict__ W, const uint16_t* __restrict__ X,
+                                                    float* __restrict__ Y, Q6kGeo geo, TileMap tm) {
+  constexpr int BM = 128;
+  constexpr int MT = BM / 32, XI = BM / 64, XSTAGE = BM * 128;
+  constexpr int GT = MT, NG = 4, NS = GT * (NG - 1), NP = 10;  // one 4-tile A group per K16 step
+  __shared__ __attribute__((aligned(1024))) uint8_t xs[3 * XSTAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t ws[2 * kQ6WStage];
+
+  const int M = geo.M, N = geo.N, K = geo.K;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ln = lane & 31, g = lane >> 5;
+  int n0, m0, tile_id;
+  {
+    const int nb = (int)gridDim.x;
+    int b = (int)blockIdx.x;
+    if ((nb & 7) == 0) b = (b & 7) * (nb >> 3) + (b >> 3);  // XCD b % 8 takes a contiguous range
+    tile_id = b;
+    const int na = tm.cols_a * tm.mt_a;
+    if (b < na) {
+      n0 = (b / tm.mt_a) * kBN;
+      m0 = tm.base_a + (b % tm.mt_a) * BM;
+    } else {
+      b -= na;
+      n0 = (tm.cols_a + b / tm.mt_b) * kBN;
+      m0 = tm.base_b + (b % tm.mt_b) * BM;
+    }
+  }
+  const int nsl = K / 64;
+  const int kb0 = blockIdx.z * geo.per_split;  // a multiple of 4: splits start a super-block
+  const int kb1 = min(nsl, kb0 + geo.per_split);
+  const int sb_end = kb1 >> 2;
+
+  const uint32_t xrow_bytes = (uint32_t)K * 2u;
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(X + (size_t)m0 * K), (short)0, (int)((uint32_t)min(BM, M - m0) * xrow_bytes), (int)kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(W + (size_t)n0 * geo.row_bytes), (short)0, (int)((uint32_t)min(kBN, N - n0) * geo.row_bytes),
+      (int)kRsrcWord3);
+  uint32_t xoff[XI];
+#pragma unroll
+  for (int i = 0; i < XI; ++i) {
+    const uint32_t q = (uint32_t)((wave * XI + i) * 64 + lane), r = q >> 3, p = q & 7u;
+    xoff[i] = r * xrow_bytes + 16u * (p ^ xswz(r));
+  }
+  const uint32_t voff = (uint32_t)(32 * wave + (lane >> 1)) * geo.row_bytes + 16u * (uint32_t)(lane & 1);
+  QVX_LDS uint8_t* xs_l = (QVX_LDS uint8_t*)xs;
+  QVX_LDS uint8_t* ws_l = (QVX_LDS uint8_t*)ws;
+  auto issue_x1 = [&](int kb, int i) {
+    QVX_LDS uint8_t* dst = xs_l + (kb % 3) * XSTAGE + wave * XI * 1024;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, dst + i * 1024, 16, xoff[i], (uint32_t)kb * 128u, 0, 0);
+  };
+  auto issue_x = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < XI; ++i) issue_x1(kb, i);
+  };
+  auto issue_w = [&](int sb) {
+    q6k_stage(wr, ws_l + (sb & 1) * kQ6WStage + wave * 32 * kQ6Win, voff, (uint32_t)(sb * 210) & ~3u);
+  };
+  // After the prologue a super-block T is staged in two parts, copies 0-3 after the barrier of slice
+  // 4T - 6 and 4-6 after that of slice 4T - 5 (its stage was last read in slice 4T - 7); chunk_of(j)
+  // is the part slice j issues (-1: none), chunk_copies(j) its number of copies.
+  auto chunk_target = [&](int j) { return (j >> 2) + 2; };
+  auto chunk_of = [&](int j) {
+    const int q = j & 3;
+    if (j < kb0 || q < 2 || chunk_target(j) >= sb_end) return -1;
+    return q - 2;
+  };
+  auto chunk_copies = [&](int j) { const int c = chunk_of(j); return c < 0 ? 0 : c == 0 ? 4 : 3; };
+
+  const uint32_t xs_base = (uint32_t)(uintptr_t)xs_l;
+  const uint32_t row_base = (uint32_t)(uintptr_t)ws_l + (uint32_t)(wave * 32 * kQ6Win + 32 * ln);
+  const uint32_t sw = xswz((uint32_t)ln);
+  uint32_t a_rel[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const uint32_t kc = 4u * (uint32_t)(s >> 1) + 2u * (uint32_t)g + (uint32_t)(s & 1);
+    a_rel[s] = (uint32_t)ln * 128u + 16u * (kc ^ sw);
+  }
+  auto read_group = [&](uint32_t xb, int G, u32x4 (&r)[8]) {
+    read_frags(xb + a_rel[G], r, std::make_integer_sequence<int, GT>{});
+  };
+  // the half of slice kb: its stage row, half index and lead bytes
+  auto half_row = [&](int kb) { return row_base + (uint32_t)((kb >> 2) & 1) * kQ6WStage; };
+  auto half_sh = [&](int kb) { return (uint32_t)((kb >> 2) * 210) & 3u; };
+
+  f32x16_t acc[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[i][e] = 0.0f;
+
+  // Dequantisation pieces (this lane's row, slice parity P): 0 and 1 realign a freshly read half
+  // and form the slice's scales, 2..9 build 4 codes each (bn[sp][2hh], bn[sp][2hh + 1] for
+  // u = p - 2 = 2 sp + hh).
+  struct DeqState {
+    Q6kRaw raw;
+    Q6kHalf hf;
+    float ds[2], bias[2];
+  };
+  const uint32_t k1024 = 0x64006400u;
+  auto piece = [&](int p, int P, bool fresh, uint32_t sh, DeqState& st, i32x4_t (&bn)[4]) {
+    if (p == 0) {
+      if (fresh) q6k_align(st.raw, sh, st.hf);
+    } else if (p == 1) {
+      const uint32_t sw4 = st.hf.s[P];
+      const float sa = (float)(int)__builtin_amdgcn_sbfe((int)sw4, 8u * (uint32_t)g, 8u);
+      const float sb = (float)(int)__builtin_amdgcn_sbfe((int)sw4, 8u * (uint32_t)(g + 2), 8u);
+      st.ds[0] = st.hf.d * sa;
+      st.ds[1] = st.hf.d * sb;
+      st.bias[0] = -1056.0f * st.ds[0];
+      st.bias[1] = -1056.0f * st.ds[1];
+    } else {
+      const int u = p - 2, sp = u >> 1, hh = u & 1, w = (sp & 1) * 2 + hh;
+      const bool second = sp >= 2;
+      const uint32_t src = second ? st.hf.qb[w] : st.hf.qa[w];
+      const uint32_t hq = st.hf.h[w];
+      const uint32_t nib = (P ? src >> 4 : src) & geo.m0f;
+      const uint32_t hb = P ? (second ? hq >> 2 : hq) : (second ? hq << 2 : hq << 4);
+      const uint32_t code = __builtin_amdgcn_bitop3_b32(hb, geo.m30, nib, 0xEA);  // (hb & 0x30..) | nib
+      const uint32_t e = __builtin_amdgcn_bitop3_b32(code, geo.mff, k1024, 0xEA);
+      const uint32_t o = __builtin_amdgcn_bitop3_b32(code >> 8, geo.mff, k1024, 0xEA);
+      const half2_t he = __builtin_bit_cast(half2_t, e), ho = __builtin_bit_cast(half2_t, o);
+      const float ds = st.ds[second], bs = st.bias[second];
+      bn[sp][2 * hh] = (int)pack2<VAR>(__builtin_fmaf((float)he.x, ds, bs), __builtin_fmaf((float)ho.x, ds, bs));
+      bn[sp][2 * hh + 1] = (int)pack2<VAR>(__builtin_fmaf((float)he.y, ds, bs), __builtin_fmaf((float)ho.y, ds, bs));
+      pin(bn[sp]);
+    }
+  };
+
+  // One slice (parity P = kb % 2), as in the Q4_K kernel: group 0's fragments were read during the
+  // previous slice; group 0 issues X(kb+2) and, when slice kb+1 starts a half (P = 1), the LDS reads
+  // of that half; the barrier before the last group publishes X(kb+1) and frees stage kb % 3, and
+  // the slice's W part is issued after it.  The dequantisation of slice kb+1 goes between the MFMAs
+  // of groups 1..3, in the last slice too (on stale bytes, never used), so that no branch splits the
+  // MFMA sequence.
+  DeqState st;
+  auto slice = [&](int kb, auto Pc, const i32x4_t (&bc)[4], i32x4_t (&bn)[4], u32x4 (&a)[2][8]) {
+    constexpr int P = decltype(Pc)::value;
+    const uint32_t xb = xs_base + (uint32_t)(kb % 3) * XSTAGE;
+    const int kx = min(kb + 2, kb1 - 1);
+    const bool more = kb + 1 < kb1;
+    const uint32_t sh = half_sh(kb + 1);
+    const int ch = chunk_of(kb);
+    QVX_LDS uint8_t* wdst = ws_l + (chunk_target(kb) & 1) * kQ6WStage + wave * 32 * kQ6Win;
+    const uint32_t wso = (uint32_t)(chunk_target(kb) * 210) & ~3u;
+#pragma unroll
+    for (int G = 0; G < NG; ++G) {
+      u32x4(&cur)[8] = a[G & 1];
+      u32x4(&nxt)[8] = a[(G + 1) & 1];
+      if (G == 1 && P == 1)
+        q6k_wait(cur, st.raw);
+      else
+        lds_wait<GT>(cur);
+      if (G == NG - 1) {
+        if (more) {
+          // X(kb+1) landed; younger copies that may fly: the previous slice's W part (issued after
+          // its barrier, so after X(kb+1)) and X(kb+2) of group 0
+          const int young = chunk_copies(kb - 1);
+          if (young == 4)
+            wait_vm<4 + XI>();
+          else if (young == 3)
+            wait_vm<3 + XI>();
+          else
+            wait_vm<XI>();
+          __builtin_amdgcn_s_barrier();
+          if (ch == 0) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) q6k_copy(wr, wdst, voff, wso, c);
+          } else if (ch == 1) {
+#pragma unroll
+            for (int c = 4; c < 7; ++c) q6k_copy(wr, wdst, voff, wso, c);
+          }
+          read_group(xs_base + (uint32_t)((kb + 1) % 3) * XSTAGE, 0, nxt);
+        }
+      } else {
+        read_group(xb, G + 1, nxt);
+      }
+      if (G == 0 && P == 1) q6k_issue(half_row(kb + 1), ((kb + 1) >> 1) & 1, g, st.raw);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int t = 0; t < GT; ++t) {
+        acc[t] = mfma32<VAR>(__builtin_bit_cast(i32x4_t, cur[t]), bc[G], acc[t]);
+        if (G == 0 && t < XI) issue_x1(kx, t);
+        if (G > 0) {
+          const int slot = GT * (G - 1) + t;
+#pragma unroll
+          for (int p = 0; p < NP; ++p)
+            if (p * NS / NP == slot) piece(p, 1 - P, P == 1, sh, st, bn);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+
+  // prologue: super-block kb0/4 and X(kb0) staged, then the next super-block and X(kb0+1) issued
+  issue_w(kb0 >> 2);
+  issue_x(kb0);
+  wait_vm<0>();
+  __builtin_amdgcn_s_barrier();
+  if ((kb0 >> 2) + 1 < sb_end) issue_w((kb0 >> 2) + 1);
+  issue_x(min(kb0 + 1, kb1 - 1));
+
+  u32x4 a[2][8];
+  read_group(xs_base + (uint32_t)(kb0 % 3) * XSTAGE, 0, a[0]);
+  i32x4_t b0[4], b1[4];
+  {
+    q6k_issue(half_row(kb0), 0, g, st.raw);
+    q6k_wait(st.raw);
+    const uint32_t sh = half_sh(kb0);
+#pragma unroll
+    for (int p = 0; p < NP; ++p) piece(p, 0, true, sh, st, b0);
+  }
+
+  int kb = kb0;
+  for (; kb + 1 < kb1; kb += 2) {
+    slice(kb, std::integral_constant<int, 0>{}, b0, b1, a);
+    slice(kb + 1, std::integral_constant<int, 1>{}, b1, b0, a);
+  }
+  if (kb < kb1) slice(kb, std::integral_constant<int, 0>{}, b0, b1, a);
+  wait_vm<0>();
+
+  if (gridDim.z > 1) {
+    float v[MT * 16];
+#pragma unroll
+    for (int i = 0; i < MT * 16; ++i) v[i] = acc[i >> 4][i & 15];
+    if (!split_k_last<MT * 16, 512>(v, geo.part + (size_t)tile_id * gridDim.z * (MT * 16 * 512), geo.cnt + tile_id,
+                                    (int)gridDim.z, (int)blockIdx.z, tid, reinterpret_cast<int*>(xs)))
+      return;
+#pragma unroll
+    for (int i = 0; i < MT * 16; ++i) acc[i >> 4][i & 15] = v[i];
+  }
+
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+    const int n = n0 + 32 * wave + ln;
+    if (n >= N) continue;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int m = m0 + 32 * i + 8 * (e >> 2) + 4 * g + (e & 3);
+      if (m < M) Y[(size_t)m * N + n] = acc[i][e];
+    }
+  }
+}
+
 // ---- int8 variant --------------------------------------------------------------------------------
 // X is quantised per 32 values to int8 (scale sx = amax/127, the public quantiser's arithmetic) by a
 // prepass; the weight nibbles are int8 operands as they are.  Per 32-element block b (one Q4_K
@@ -990,6 +1353,44 @@ size_t q4k_split_bytes(const Q4kPlan& p) {
   return parts + (((size_t)L.ntiles * 4 + 255) & ~(size_t)255);
 }
 
+// The Q6_K kernel (k_qgemm_q6k8): 128-token tiles, K split while the grid is below ~200 workgroups,
+// as for the Q4_K kernel's small grids.
+void q6k8_plan(int M, int N, int K, int cus, Q4kPlan& p) {
+  const int nt = cdiv(N, kBN), nsl = K / 64, tiles = nt * cdiv(M, 128);
+  int splits = 1;
+  while (tiles * splits < 200 * cus / 256 && nsl / (splits * 2) >= 8) splits *= 2;
+  const int per = split_per(nsl, splits);
+  p.n = 1;
+  p.l[0] = Q4kLaunch{128, (nsl + per - 1) / per, tiles, TileMap{nt, cdiv(M, 128), 0, 1, 0}};
+}
+
+// 1 if k_qgemm_q6k8 takes this call: an even number of blocks a row (every row's blocks share one
+// dword alignment), W 4-byte and X 16-byte aligned, a tile's X rows and W rows within 31-bit buffer
+// offsets.
+bool q6k8_supported(const void* w, const uint16_t* X, int K, int N) {
+  if (K <= 0 || K % 512 != 0 || N <= 0) return false;
+  if ((reinterpret_cast<uintptr_t>(w) & 3u) || (reinterpret_cast<uintptr_t>(X) & 15u)) return false;
+  const size_t row_bytes = (size_t)(K / 256) * 210u;
+  return (size_t)128 * (size_t)K * 2u < (1u << 31) && (size_t)kBN * row_bytes < (1u << 31);
+}
+
+template <int VAR>
+bool launch_q6k8(float* out, const void* w, const uint16_t* X, int M, int N, int K, const Q4kPlan& p, void* ws,
+                 hipStream_t s) {
+  static LdsLimit lim;
+  if (!lds_ready(reinterpret_cast<const void*>(&k_qgemm_q6k8<VAR>), lim, 0)) return false;
+  const Q4kLaunch& L = p.l[0];
+  const size_t sb = q4k_split_bytes(p);
+  float* part = sb ? static_cast<float*>(ws) : nullptr;
+  uint32_t* cnt = sb ? reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(ws) + (size_t)L.ntiles * L.splits * 128 * kBN * 4)
+                     : nullptr;
+  if (L.splits > 1 && !ws) return false;
+  Q6kGeo geo{M, N, K, (uint32_t)(K / 256) * 210u, split_per(K / 64, L.splits), 0x0F0F0F0Fu, 0x30303030u,
+             0x00FF00FFu, part, cnt};
+  k_qgemm_q6k8<VAR><<<dim3(L.ntiles, 1, L.splits), 512, 0, s>>>(static_cast<const uint8_t*>(w), X, out, geo, L.tm);
+  return true;
+}
+
 // ws: the workspace of q4k_split_bytes(p) bytes, its counters already zero.
 template <int VAR>
 bool launch_var(float* out, const void* w, const uint16_t* X, int M, int N, int K, const Q4kPlan& p, void* ws,
@@ -1046,7 +1447,36 @@ int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M
     const TypeInfo* ti = type_info(t);
     if (!ti) return -1;
     const size_t row_bytes = (size_t)(cols / (int)ti->block) * ti->bytes;
-    // The other weight types: their rows dequantised into the MFMA tiles (cols % 64 == 0, aligned
+    // Q6_K with an even number of blocks a row: the Q4_K kernel's pipeline (k_qgemm_q6k8) ...
+    if (t == T_Q6_K && q6k8_supported(w, X, cols, rows)) {
+      Q4kPlan plan;
+      q6k8_plan(M, rows, cols, device_cus(), plan);
+      const size_t n = (size_t)M * (size_t)cols;
+      const size_t xbytes = variant == VAR_BF16 ? (n * 2u + 255) & ~(size_t)255 : 0;
+      const size_t sbytes = q4k_split_bytes(plan);
+      uint8_t* tmp = nullptr;
+      if (xbytes + sbytes) {
+        tmp = static_cast<uint8_t*>(gemm_ws(xbytes + sbytes, ws, ws_cap, s));
+        if (!tmp) return no_mem;
+      }
+      const size_t cbytes = sbytes ? (((size_t)plan.l[0].ntiles * 4 + 255) & ~(size_t)255) : 0;
+      float* cnt = sbytes ? reinterpret_cast<float*>(tmp + xbytes + sbytes - cbytes) : nullptr;
+      const uint16_t* Xg = X;
+      if (variant == VAR_BF16) {
+        k_f16_to_bf16<<<(unsigned)((n / 8 + 255) / 256), 256, 0, s>>>(
+            reinterpret_cast<const uint4*>(X), reinterpret_cast<uint4*>(tmp), n / 8, reinterpret_cast<float4*>(cnt),
+            cbytes / 16);
+        Xg = reinterpret_cast<const uint16_t*>(tmp);
+      } else if (sbytes) {
+        launch_zero(cnt, cbytes / 4, s);
+      }
+      const bool ok = variant == VAR_BF16
+                          ? launch_q6k8<VAR_BF16>(out, w, Xg, M, rows, cols, plan, sbytes ? tmp + xbytes : nullptr, s)
+                          : launch_q6k8<VAR_F16>(out, w, Xg, M, rows, cols, plan, sbytes ? tmp + xbytes : nullptr, s);
+      if (tmp) gemm_ws_release(tmp, ws, s);
+      return ok ? 0 : -5;
+    }
+    // ... the other weight types: their rows dequantised into the MFMA tiles (cols % 64 == 0, aligned
     // operands) ...
     if (qgemm_deq_supported(t, w, X, cols, rows, row_bytes)) {
       // Temporaries: the bf16 copy of X (bf16 variant), then a K split's partial tiles and tile

@@ -517,6 +517,35 @@ def test_gemm_other_types_parity(cuda, t, variant, M, rows, cols):
     assert max_rel(out.cpu().numpy(), ref) <= GEMM_TOL
 
 
+@pytest.mark.parametrize("variant", [qvx.GEMM_BF16, qvx.GEMM_F16])
+@pytest.mark.parametrize("M,rows,cols", [(37, 300, 512), (200, 300, 1536), (130, 520, 3072), (1, 256, 1024),
+                                         (300, 2100, 2048)])
+def test_gemm_q6k_pipeline_shapes(cuda, variant, M, rows, cols):
+    """Q6_K with an even number of blocks a row runs on the Q4_K kernel's pipeline (each super-block
+    of the tile's rows staged whole, dequantised in registers): ragged token and row tiles, K of one,
+    three and six super-block pairs, one K range (37 x 300 x 512), two splits of three super-blocks
+    (200 x 300 x 1536), four splits (130 x 520 x 3072, 300 x 2100 x 2048) and M = 1, against the
+    fp64 oracle.  The same call on a copy of W two bytes off its dword alignment, which the staged
+    copies cannot take, goes to the dequantise-then-library route and meets the same bound."""
+    rng = np.random.default_rng(M + rows + cols + variant)
+    t = qvx.Q6_K
+    w = random_weight(t, rows, cols, rng, scale=0.002)
+    X16 = (rng.standard_normal((M, cols)) * 0.5).astype(np.float16)
+    X = dev(cuda, X16.view(np.uint16))
+    ref = oracle.matmul_f64(w, t, X16.astype(np.float32), M, rows, cols)
+    out = qvx.qgemm_t(dev(cuda, w), t, X, rows, cols, variant)
+    cuda.cuda.synchronize()
+    assert max_rel(out.cpu().numpy(), ref) <= GEMM_TOL
+    buf = cuda.zeros(w.size + 16, dtype=cuda.uint8, device="cuda")
+    buf[2:2 + w.size] = cuda.from_numpy(w.reshape(-1).view(np.uint8)).to("cuda")
+    out2 = cuda.full((M, rows), float("nan"), dtype=cuda.float32, device="cuda")
+    rc = qvx.lib().qvx_qgemm_f16(out2.data_ptr(), buf.data_ptr() + 2, t, X.data_ptr(), M, rows, cols, variant,
+                                 cuda.cuda.current_stream().cuda_stream)
+    assert rc == qvx.OK
+    cuda.cuda.synchronize()
+    assert max_rel(out2.cpu().numpy(), ref) <= GEMM_TOL
+
+
 @pytest.mark.parametrize("t", [qvx.Q8_0, qvx.Q4_0, qvx.Q5_1])
 def test_gemm_32_blocks_odd_slices(cuda, t):
     """32-element block types at cols = 320 and cols = 96 (not a multiple of 64), against the
