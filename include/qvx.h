@@ -140,9 +140,10 @@ int qvx_interleave_rows16(void* d_dst, const void* d_a, const void* d_b, uint32_
  * No reference counterpart (the reference prefills token by token); semantics are qmatmulN's
  * with X converted fp16 -> fp32 exactly.  variant = QVX_GEMM_BF16 | QVX_GEMM_F16 | QVX_GEMM_I8;
  * tolerance 2e-2 max-relative against the exact sum.  type: every type qvx_qmatmul takes.  Q4_K
- * runs on the engine's raw-block MFMA kernels; Q6_K (cols a multiple of 64, X 16-byte and W 4-byte
- * aligned) on its dequantising MFMA kernel, each weight element rounded once from its exact value
- * to fp16 / bf16.  Other types, and Q6_K calls that kernel declines, are dequantised into a
+ * runs on the engine's raw-block MFMA kernels; Q6_K with X 16-byte and W 4-byte aligned on its own
+ * MFMA kernels (cols a multiple of 512: the Q4_K kernels' pipeline, blocks dequantised in
+ * registers; else cols a multiple of 64: a dequantising kernel), each weight element rounded to
+ * fp16 / bf16 from its dequantised value.  Other types, and Q6_K calls those kernels decline, are dequantised into a
  * stream-ordered 16-bit temporary (fp16, bf16 for QVX_GEMM_BF16) and multiplied by one rocBLAS
  * gemm_ex (fp32 accumulate), rocBLAS being loaded on first use (QVX_E_LIB when it is missing or
  * fails; these calls create a rocBLAS handle per host thread and device on first use, so they are

@@ -1,6 +1,8 @@
-// qvx_gemm_deq.hip -- prefill GEMM of Q6_K weights (Q4_K has its own kernels in qvx_gemm.hip): the
-// raw blocks of each half super-block are staged in LDS for the tile's 256 weight rows, each row's
-// 64-element K slices are dequantised from there into a 16-bit B tile in LDS, then bf16 / fp16 MFMA.
+// qvx_gemm_deq.hip -- prefill GEMM of Q6_K weights whose rows hold an odd number of blocks (rows of
+// an even number, W dword aligned, take k_qgemm_q6k8 in qvx_gemm.hip; Q4_K has its own kernels
+// there): the raw blocks of each half super-block are staged in LDS for the tile's 256 weight rows,
+// each row's 64-element K slices are dequantised from there into a 16-bit B tile in LDS, then
+// bf16 / fp16 MFMA.
 //
 // out[m, r] = sum_k X[m, k] * dequant(W)[r, k],  X [M, K] 16-bit, W raw GGUF blocks [N rows, K],
 // out fp32 [M, N].  No reference counterpart (the reference prefills token by token); the semantics
