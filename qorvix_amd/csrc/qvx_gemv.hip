@@ -848,50 +848,54 @@ __global__ __launch_bounds__(512) void k_gemv_q6n(const uint8_t* __restrict__ W,
     return W + (size_t)row * geo.row_bytes + (size_t)(u % upt) * 2 * 210;
   };
 
-  // The wave walks its steps: step i is half i%2 of super-block (i/2)%2 of unit w + 8 (i/4).  A
-  // step folds its two pairs into P0 + P1; a super-block's sum is (half 0) + (half 1), a unit's
+  // The wave walks its units u = w, w + 8, ...; unit step s (0..3) is half s%2 of super-block s/2.
+  // A step folds its two pairs into P0 + P1; a super-block's sum is (half 0) + (half 1), a unit's
   // (super-block 0) + (super-block 1): the balanced tree over the unit's 8 pairs.  The next step's
-  // raw bytes are loaded at the start of a step, the next pair's activations at the start of a
-  // pair (activations first, so that a wait for them never waits for the blocks behind them).
-  Q6Half cur, nxt;
+  // raw bytes are loaded at the start of a step into the other of two buffers, the next pair's
+  // activations at the start of a pair (activations first, so that a wait for them never waits for
+  // the blocks behind them).  Every load is unconditional (the wave's last step reloads its own
+  // unit's first half and pair) and no buffer is copied into the other, so the wait before each use
+  // counts exactly the loads issued after it: with a conditional load the compiler's waits fall back
+  // to ones that also wait for the prefetch just issued.
+  Q6Half ha, hb;
   float4 xr[2][KT][2];
-  auto step_unit = [&](int i) { return wave + 8 * (i >> 2); };
-  auto step_base = [&](int i) { return row_base(step_unit(i)) + (size_t)((i >> 1) & 1) * 210; };
-  auto step_pair = [&](int i) { return (step_unit(i) % upt) * 8 + ((i >> 1) & 1) * 4 + (i & 1) * 2; };
-  if (wave < units) {
-    q6_load_half(step_base(0), g, 0, cur, cur);
-    load_x(step_pair(0), xr[0]);
+  const int nu = wave < units ? (units - wave + 7) / 8 : 0;  // units of this wave
+  auto sbase = [&](int u, int st) { return row_base(u) + (size_t)(st >> 1) * 210; };
+  auto spair = [&](int u, int st) { return (u % upt) * 8 + (st >> 1) * 4 + (st & 1) * 2; };
+  if (nu > 0) {
+    q6_load_half(sbase(wave, 0), g, 0, ha, ha);
+    load_x(spair(wave, 0), xr[0]);
   }
   float H0[NV / 2], S0[NV / 2];
-#pragma unroll 1
-  for (int i = 0; step_unit(i) < units; ++i) {
-    const bool more = step_unit(i + 1) < units;
-    const int pair0 = step_pair(i), h = i & 1;
+  auto step = [&](int k, auto stc, const Q6Half& cur, Q6Half& nxt) __attribute__((always_inline)) {
+    constexpr int st = decltype(stc)::value, sn = (st + 1) & 3;
+    const int u = wave + 8 * k;
+    const int un = st == 3 ? wave + 8 * min(k + 1, nu - 1) : u;  // the next step's unit
+    const int pair0 = spair(u, st);
     float H[NV / 2];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       if (t == 0)
         load_x(pair0 + 1, xr[1]);
-      else if (more)
-        load_x(step_pair(i + 1), xr[0]);
+      else
+        load_x(spair(un, sn), xr[0]);
       __builtin_amdgcn_sched_barrier(0);
-      if (t == 0 && more) q6_load_half(step_base(i + 1), g, (i + 1) & 1, cur, nxt);
+      if (t == 0) q6_load_half(sbase(un, sn), g, sn & 1, cur, nxt);
       __builtin_amdgcn_sched_barrier(0);
       convert(xr[t]);
       float P[NV / 2];
-      q6_pair<NV>(cur, h, t, xq, 40, &sxc_all[wave][0][0][0], lane, P);
+      q6_pair<NV>(cur, st & 1, t, xq, 40, &sxc_all[wave][0][0][0], lane, P);
 #pragma unroll
-      for (int k = 0; k < NV / 2; ++k) H[k] = t == 0 ? P[k] : H[k] + P[k];
+      for (int kk = 0; kk < NV / 2; ++kk) H[kk] = t == 0 ? P[kk] : H[kk] + P[kk];
       __builtin_amdgcn_sched_barrier(0);
     }
-    if ((i & 3) == 0 || (i & 3) == 2) {
+    if constexpr (st == 0 || st == 2) {
 #pragma unroll
-      for (int k = 0; k < NV / 2; ++k) H0[k] = H[k];
-    } else if ((i & 3) == 1) {
+      for (int kk = 0; kk < NV / 2; ++kk) H0[kk] = H[kk];
+    } else if constexpr (st == 1) {
 #pragma unroll
-      for (int k = 0; k < NV / 2; ++k) S0[k] = H0[k] + H[k];
+      for (int kk = 0; kk < NV / 2; ++kk) S0[kk] = H0[kk] + H[kk];
     } else {
-      const int u = step_unit(i);
 #pragma unroll
       for (int j = 0; j < NJ; ++j)
 #pragma unroll
@@ -900,7 +904,13 @@ __global__ __launch_bounds__(512) void k_gemv_q6n(const uint8_t* __restrict__ W,
           res[((size_t)u * NV + 4 * j + 2 * g + b) * 32 + ln] = S0[kk] + (H0[kk] + H[kk]);
         }
     }
-    cur = nxt;
+  };
+#pragma unroll 1
+  for (int k = 0; k < nu; ++k) {
+    step(k, std::integral_constant<int, 0>{}, ha, hb);
+    step(k, std::integral_constant<int, 1>{}, hb, ha);
+    step(k, std::integral_constant<int, 2>{}, ha, hb);
+    step(k, std::integral_constant<int, 3>{}, hb, ha);
   }
   __syncthreads();
 
