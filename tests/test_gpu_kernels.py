@@ -518,13 +518,13 @@ def test_gemm_other_types_parity(cuda, t, variant, M, rows, cols):
 
 
 @pytest.mark.parametrize("variant", [qvx.GEMM_BF16, qvx.GEMM_F16])
-@pytest.mark.parametrize("M,rows,cols", [(37, 300, 512), (200, 300, 1536), (130, 520, 3072), (1, 256, 1024),
+@pytest.mark.parametrize("M,rows,cols", [(37, 300, 512), (200, 300, 2560), (130, 520, 3072), (1, 256, 1024),
                                          (300, 2100, 2048)])
 def test_gemm_q6k_pipeline_shapes(cuda, variant, M, rows, cols):
     """Q6_K with an even number of blocks a row runs on the Q4_K kernel's pipeline (each super-block
-    of the tile's rows staged whole, dequantised in registers): ragged token and row tiles, K of one,
-    three and six super-block pairs, one K range (37 x 300 x 512), two splits of three super-blocks
-    (200 x 300 x 1536), four splits (130 x 520 x 3072, 300 x 2100 x 2048) and M = 1, against the
+    of the tile's rows staged whole, dequantised in registers): ragged token and row tiles, K of one
+    to six super-block pairs, one K range (37 x 300 x 512, M = 1), two splits of five super-blocks
+    (200 x 300 x 2560) and two of six or four (130 x 520 x 3072, 300 x 2100 x 2048), against the
     fp64 oracle.  The same call on a copy of W two bytes off its dword alignment, which the staged
     copies cannot take, goes to the dequantise-then-library route and meets the same bound."""
     rng = np.random.default_rng(M + rows + cols + variant)
