@@ -21,7 +21,7 @@ ARCH = os.environ.get("QVX_ARCH", "gfx950")
 CFLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
-    "-std=c++17",
+    "-std=c++23",
     "-fPIC",
     "-fvisibility=hidden",
     "-Wall",
