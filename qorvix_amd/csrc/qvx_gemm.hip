@@ -506,10 +506,11 @@ __global__ __launch_bounds__(512) void k_qgemm_q4k(const uint8_t* __restrict__ W
 // blocks are staged whole, two stages: each row's dword-aligned window (the block's 210 bytes after
 // up to 2 lead bytes: 14 chunks of 16 bytes), copied by 7 LDS-DMA copies per wave, copy k moving
 // chunks 2k, 2k+1 of the wave's 32 rows (lane l: row l / 2, chunk 2k + l % 2), so the wave's part of
-// a stage is [k][row][2 chunks] (each wave copies and reads only its own rows).  Slice kb covers elements 64 (kb % 4) .. +63 of a block;
-// for its half n = (kb / 2) % 2 lane (row, g) reads ql bytes 64n + 16g .. +15 (QA) and
-// 64n + 32 + 16g .. +15 (QB), qh bytes 32n + 16g .. +15 (H), the half's 8 scale bytes and d, once per
-// half, and builds both slices of the half from them (i = 0..15, P = kb % 2):
+// a stage is [k][row][2 chunks] (each wave copies and reads only its own rows).  Slice kb covers
+// elements 64 (kb % 4) .. +63 of a block; for its half n = (kb / 2) % 2 lane (row, g) reads ql
+// bytes 64n + 16g .. +15 (QA) and 64n + 32 + 16g .. +15 (QB), qh bytes 32n + 16g .. +15 (H), the
+// half's 8 scale bytes and d, once per half, and builds both slices of the half from them
+// (i = 0..15, P = kb % 2):
 //   element 16g + i      = (P ? QA_i >> 4 : QA_i & 15) | (H_i bits 4P, 4P+1) << 4,   scale sc[8n + g + 4P]
 //   element 32 + 16g + i = (P ? QB_i >> 4 : QB_i & 15) | (H_i bits 4P+2, 4P+3) << 4, scale sc[8n + g + 2 + 4P]
 // -- the element order of the Q4_K kernel's B operands and X fragments.  A 6-bit code c goes into the
