@@ -30,15 +30,14 @@ def _call(fn, cuda, W, t, X, rows, cols, variant):
     return out.cpu().numpy()
 
 
-def _case(cuda, M, rows, cols, seed):
-    t = qvx.Q4_K
+def _case(cuda, M, rows, cols, seed, t=qvx.Q4_K):
     W = qvx.empty_weight(t, rows, cols)
     qvx.fill_synthetic_t(W, t, rows, cols, seed=seed, scale_mul=1e-3)
     X = cuda.empty((M, cols), dtype=cuda.float16, device="cuda")
     qvx.fill_normal_t(X, seed=seed + 1, mul=0.5)
     cuda.cuda.synchronize()
     idx = np.union1d(np.arange(0, rows, 29), [rows - 1])
-    rb = cols // 256 * 144
+    rb = qvx.row_bytes(t, cols)
     Wd = oracle.dequantize(t, W.cpu().numpy().reshape(rows, rb)[idx].reshape(-1), len(idx) * cols)
     Wd = Wd.reshape(len(idx), cols).astype(np.float64)
     return t, W, X, idx, Wd
@@ -61,6 +60,23 @@ def test_noalloc_matches_allocating_gemm_on_two_calls(cuda, variant):
             assert max_rel(got[:, idx], ref) <= I8_TOL
         else:
             assert max_rel(got[:, idx], X32.astype(np.float64) @ Wd.T) <= GEMM_TOL
+
+
+@pytest.mark.parametrize("variant", [qvx.GEMM_BF16, qvx.GEMM_F16])
+def test_noalloc_q6k_matches_allocating_gemm_on_two_calls(cuda, variant):
+    """Q6_K (the Q4_K kernels' pipeline) through the no-allocation entry point: a 256-tile call with
+    no K split (the bf16 copy of X, 56 MiB, in the scratch), then a smaller one whose four K splits
+    keep their partial tiles and counters in the scratch the first call left behind; both bit for
+    bit the allocating call's, and within the GEMM tolerance of the fp64 oracle on a row slice."""
+    lib = qvx.lib()
+    for n, (M, rows, cols) in enumerate(((2048, 4096, 14336), (128, 2048, 4096))):
+        t, W, X, idx, Wd = _case(cuda, M, rows, cols, seed=950 + 10 * n + variant, t=qvx.Q6_K)
+        got = _call(lib.qvx_qgemm_f16_noalloc, cuda, W, t, X, rows, cols, variant)
+        want = _call(lib.qvx_qgemm_f16, cuda, W, t, X, rows, cols, variant)
+        assert np.isfinite(got).all()
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+        X32 = X.cpu().numpy().astype(np.float64)
+        assert max_rel(got[:, idx], X32 @ Wd.T) <= GEMM_TOL
 
 
 def test_noalloc_rejects_calls_past_its_scratch(cuda):
