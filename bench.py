@@ -400,7 +400,8 @@ def dequant_leg(torch, stream, t, copies, reps=20):
 def gemm_leg(torch, stream, t, wps, copies, steps, cpu):
     """Q4_K 4096 -> 14336 prefill GEMM at M = 2048, 512, 128 in the bf16, fp16 and
     int8 variants, each call timed whole (prepass + GEMM) with HIP events on the launch stream, and the
-    reference CPU qmatmulN beside it on a 64-token sample."""
+    reference CPU qmatmulN beside it on a 64-token sample; then the Q6_K ffn_down GEMM (the Q6_K tensor
+    of a Q4_K_M layer) at M = 2048."""
     import qorvix_amd as qvx
     lib, sh, dev = qvx.lib(), stream.cuda_stream, stream.device
     gemm = {}
@@ -443,6 +444,36 @@ def gemm_leg(torch, stream, t, wps, copies, steps, cpu):
                                      "sample": f"first {ms_tok} of the {M} tokens (qmatmulN, X converted fp16->fp32)"}
                 log(f"[bench] GEMM M={M} CPU {kind}: {gf:.1f} GFLOP/s on a {ms_tok}-token sample")
             del X, Y
+        # the Q6_K prefill GEMM on Llama-3-8B's ffn_down (14336 -> 4096, the Q6_K tensor of a Q4_K_M
+        # layer), M = 2048, fp16 MFMA: four seeded weight copies cycled, each call timed whole
+        q6, q6r, q6c, q6m = qvx.Q6_K, 4096, 14336, 2048
+        w6 = [qvx.empty_weight(q6, q6r, q6c, dev) for _ in range(4)]
+        for i, w in enumerate(w6):
+            qvx.fill_synthetic_t(w, q6, q6r, q6c, seed=300 + i, scale_mul=1e-3)
+        X = torch.empty((q6m, q6c), dtype=torch.float16, device=dev)
+        qvx.fill_normal_t(X, seed=13, mul=0.5)
+        Y = torch.empty((q6m, q6r), dtype=torch.float32, device=dev)
+        def g6(i):
+            rc = lib.qvx_qgemm_f16(Y.data_ptr(), w6[i % 4].data_ptr(), q6, X.data_ptr(), q6m, q6r, q6c, qvx.GEMM_F16, sh)
+            if rc != 0:
+                raise RuntimeError(f"qvx_qgemm_f16 (Q6_K) failed: {qvx.strerror(rc)}")
+        for i in range(10):
+            g6(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(steps):
+            g6(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        tflops = 2.0 * q6m * q6r * q6c / (ms * 1e-3) / 1e12
+        gemm["q6k_ffn_down_f16_M2048"] = {"ms": round(ms, 4), "tflops": round(tflops, 1),
+                                           "frac_of_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4),
+                                           "shape": "Q6_K 14336->4096 (ffn_down), M=2048, fp16 MFMA"}
+        log(f"[bench] GEMM Q6_K ffn_down f16 M=2048: {ms * 1e3:.1f} us, {tflops:.1f} TFLOP/s "
+            f"({100 * tflops / BF16_PEAK_TFLOPS:.1f}% of bf16 peak)")
+        del X, Y, w6
     except RuntimeError as e:  # report, never hide: the JSON carries the error
         gemm["error"] = str(e)
         log(f"[bench] GEMM failed: {e}")
