@@ -495,6 +495,40 @@ def test_gemm_split_k_is_deterministic(cuda, t, variant, M, rows, cols):
         assert max_rel(runs[0][:, idx], ref) <= GEMM_TOL
 
 
+@pytest.mark.parametrize("t", [qvx.Q4_K, qvx.Q6_K])
+def test_gemm_split_k_concurrent_streams(cuda, t):
+    """K-split GEMMs issued on two streams at once, each call with its own pool workspace for the
+    partial tiles and counters, into distinct outputs: every output is bit-identical to the same
+    call made alone (overlapping calls on one device are safe for distinct outputs)."""
+    M, rows, cols = 128, 2048, 4096
+    W = qvx.empty_weight(t, rows, cols)
+    qvx.fill_synthetic_t(W, t, rows, cols, seed=71, scale_mul=1e-3)
+    Xs = [cuda.empty((M, cols), dtype=cuda.float16, device="cuda") for _ in range(2)]
+    for i, X in enumerate(Xs):
+        qvx.fill_normal_t(X, seed=72 + i, mul=0.5)
+    lib = qvx.lib()
+    cuda.cuda.synchronize()
+    alone = []
+    for X in Xs:
+        Y = cuda.empty((M, rows), dtype=cuda.float32, device="cuda")
+        assert lib.qvx_qgemm_f16(Y.data_ptr(), W.data_ptr(), t, X.data_ptr(), M, rows, cols, qvx.GEMM_BF16,
+                                 cuda.cuda.current_stream().cuda_stream) == qvx.OK
+        cuda.cuda.synchronize()
+        alone.append(Y.cpu().numpy())
+    streams = [cuda.cuda.Stream(), cuda.cuda.Stream()]
+    outs = [[cuda.full((M, rows), float("nan"), dtype=cuda.float32, device="cuda") for _ in range(6)]
+            for _ in range(2)]
+    cuda.cuda.synchronize()
+    for k in range(6):
+        for i in range(2):
+            assert lib.qvx_qgemm_f16(outs[i][k].data_ptr(), W.data_ptr(), t, Xs[i].data_ptr(), M, rows, cols,
+                                     qvx.GEMM_BF16, streams[i].cuda_stream) == qvx.OK
+    cuda.cuda.synchronize()
+    for i in range(2):
+        for k in range(6):
+            np.testing.assert_array_equal(outs[i][k].cpu().numpy().view(np.uint32), alone[i].view(np.uint32))
+
+
 DEQUANT_GEMM_TYPES = [qvx.Q6_K, qvx.Q8_0, qvx.Q4_0, qvx.Q5_0, qvx.Q5_K, qvx.Q4_1, qvx.Q5_1, qvx.Q8_1,
                       qvx.F16, qvx.BF16, qvx.F32]
 
