@@ -47,6 +47,7 @@ SIGNATURES = {
     "qvx_qmatmul": ([_vp, _vp, _u32, _vp, _i32, _i32, _vp], _i32),
     "qvx_qmatmul_n": ([_vp, _vp, _u32, _vp, _i32, _i32, _i32, _vp], _i32),
     "qvx_qmatmul_n_rmsnorm": ([_vp, _vp, _u32, _vp, _vp, _f32, _i32, _i32, _i32, _vp], _i32),
+    "qvx_qmatmul_group": ([_vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp], _i32),
     "qvx_qmatmul_swiglu": ([_vp, _vp, _u32, _vp, _vp, _f32, _i32, _i32, _i32, _vp], _i32),
     "qvx_interleave_rows16": ([_vp, _vp, _vp, _u32, _i32, _i32, _vp], _i32),
     "qvx_rmsnorm": ([_vp, _vp, _vp, _f32, _i32, _i32, _vp], _i32),
@@ -65,6 +66,7 @@ SIGNATURES = {
     "qvx_plan_add_qmatmul_n": ([_vp, _vp, _vp, _u32, _vp, _i32, _i32, _i32], _i32),
     "qvx_plan_add_qmatmul_n_rmsnorm": ([_vp, _vp, _vp, _u32, _vp, _vp, _f32, _i32, _i32, _i32], _i32),
     "qvx_plan_add_qmatmul_swiglu": ([_vp, _vp, _vp, _u32, _vp, _vp, _f32, _i32, _i32, _i32], _i32),
+    "qvx_plan_add_qmatmul_group": ([_vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32], _i32),
     "qvx_plan_fork": ([_vp], _i32),
     "qvx_plan_join": ([_vp], _i32),
     "qvx_plan_size": ([_vp], _i32),
@@ -193,6 +195,21 @@ def qmatmul_n(out: int, weight: int, ggml_type: int, X: int, nvec: int, rows: in
               stream: int = 0) -> int:
     """Batched form (runtime/src/qmatmul.cpp:64-115); out [nvec, rows]. Status."""
     return lib().qvx_qmatmul_n(out, weight, ggml_type, X, nvec, rows, cols, stream)
+
+
+GROUP_MAX = 8
+
+
+def qmatmul_group(outs, weights, types, rows, x: int, cols: int, stream: int = 0) -> int:
+    """outs[i] = W_i . x for the members (device pointers; types and row counts per member): the
+    decoder's q / k / v wmatmuls of one vector (runtime/src/text_model.cpp:147-149) in one call,
+    each output bit-identical to qmatmul's. Status."""
+    n = len(outs)
+    if not (len(weights) == len(types) == len(rows) == n):
+        raise ValueError("qmatmul_group: one output, weight, type and row count per member")
+    arr = C.c_void_p * max(n, 1)
+    return lib().qvx_qmatmul_group(arr(*outs), arr(*weights), (C.c_uint32 * max(n, 1))(*types),
+                                   (C.c_int32 * max(n, 1))(*rows), n, x, cols, stream)
 
 
 def qmatmul_n_rmsnorm(out: int, weight: int, ggml_type: int, X: int, norm_w: int, eps: float, nvec: int, rows: int,

@@ -56,6 +56,7 @@ int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M
 int launch_quantize_act_q8(const uint16_t* X, int M, int K, int8_t* q, float* scale, int32_t* qsum,
                            hipStream_t s);
 void launch_zero(float* p, size_t n, hipStream_t s);
+bool launch_gemv_group(const GemvMember* m, int n, const float* X, int cols, hipStream_t s);
 }  // namespace qvx
 
 using namespace qvx;
@@ -78,6 +79,7 @@ struct qvx_plan {
     int nvec, rows, cols;
     int group;  // calls sharing a group >= 0 are independent of each other (one fork); -1: in order
     GemvEpi epi;  // fused RMSNorm / SwiGLU (rows = the weight's rows: 2 ffn for SwiGLU)
+    std::vector<GemvMember> members;  // non-empty: a grouped call over X (nvec 1), out / w / type / rows unused
   };
   std::vector<Call> calls;
   int device = 0;
@@ -384,6 +386,42 @@ int qvx_qmatmul_n(float* d_out, const void* d_w, uint32_t type, const float* d_X
   return gemv(d_out, d_w, type, d_X, n_vec, rows, cols, as_stream(stream));
 }
 
+// Checks a grouped call's members as qvx_qmatmul checks each one and collects those with rows into
+// m (at most QVX_GROUP_MAX); *k = their count.
+static int group_members(float* const* d_out, const void* const* d_w, const uint32_t* types, const int* rows, int n,
+                         const float* d_x, int cols, GemvMember* m, int* k) {
+  if (n < 1 || n > QVX_GROUP_MAX) return QVX_E_NVEC;
+  if (!d_out || !d_w || !types || !rows) return QVX_E_NULL;
+  *k = 0;
+  for (int i = 0; i < n; ++i) {
+    const TypeInfo* ti = nullptr;
+    if (int rc = check_matmul(types[i], cols, &ti); rc != QVX_OK) return rc;
+    if (rows[i] <= 0) continue;  // nothing to compute, as for qvx_qmatmul
+    if (!d_out[i] || (cols > 0 && (!d_w[i] || !d_x))) return QVX_E_NULL;
+    const size_t row_bytes = cols > 0 ? (size_t)(cols / (int)ti->block) * ti->bytes : 0;
+    m[(*k)++] = GemvMember{d_w[i], d_out[i], types[i], rows[i], row_bytes};
+  }
+  return QVX_OK;
+}
+
+// One launch for the members when the grouped kernel takes them all, else one qmatmul each.
+static int gemv_group(const GemvMember* m, int k, const float* x, int cols, hipStream_t s) {
+  bool fast = cols > 0 && aligned16(x);
+  for (int i = 0; i < k; ++i) fast = fast && aligned16(m[i].w) && m[i].row_bytes % 16 == 0;
+  if (fast && launch_gemv_group(m, k, x, cols, s)) return hip_status();
+  for (int i = 0; i < k; ++i)
+    if (int rc = gemv(m[i].y, m[i].w, m[i].type, x, 1, m[i].rows, cols, s); rc != QVX_OK) return rc;
+  return QVX_OK;
+}
+
+int qvx_qmatmul_group(float* const* d_out, const void* const* d_w, const uint32_t* types, const int* rows, int n,
+                      const float* d_x, int cols, void* stream) {
+  GemvMember m[QVX_GROUP_MAX];
+  int k = 0;
+  if (int rc = group_members(d_out, d_w, types, rows, n, d_x, cols, m, &k); rc != QVX_OK) return rc;
+  return k ? gemv_group(m, k, d_x, cols, as_stream(stream)) : QVX_OK;
+}
+
 int qvx_qmatmul_n_rmsnorm(float* d_out, const void* d_w, uint32_t type, const float* d_X, const float* d_norm_w,
                           float eps, int n_vec, int rows, int cols, void* stream) {
   const TypeInfo* ti = nullptr;
@@ -587,6 +625,26 @@ int qvx_plan_add_qmatmul_n(qvx_plan* plan, float* d_out, const void* d_w, uint32
   return QVX_OK;
 }
 
+// One recorded call: a grouped call or a plain / fused GEMV.
+static int run_call(const qvx_plan::Call& c, hipStream_t s) {
+  if (!c.members.empty()) return gemv_group(c.members.data(), (int)c.members.size(), c.X, c.cols, s);
+  return gemv(c.out, c.w, c.type, c.X, c.nvec, c.rows, c.cols, s, c.epi);
+}
+
+int qvx_plan_add_qmatmul_group(qvx_plan* plan, float* const* d_out, const void* const* d_w, const uint32_t* types,
+                               const int* rows, int n, const float* d_x, int cols) {
+  if (!plan) return QVX_E_NULL;
+  if (plan->exec) return QVX_E_STATE;
+  GemvMember m[QVX_GROUP_MAX];
+  int k = 0;
+  if (int rc = group_members(d_out, d_w, types, rows, n, d_x, cols, m, &k); rc != QVX_OK) return rc;
+  if (k == 0) return QVX_OK;
+  qvx_plan::Call c{nullptr, nullptr, 0, d_x, 1, 0, cols, plan->open_group, GemvEpi{}, {}};
+  c.members.assign(m, m + k);
+  plan->calls.push_back(std::move(c));
+  return QVX_OK;
+}
+
 int qvx_plan_add_qmatmul_n_rmsnorm(qvx_plan* plan, float* d_out, const void* d_w, uint32_t type, const float* d_X,
                                    const float* d_norm_w, float eps, int n_vec, int rows, int cols) {
   if (plan && !d_norm_w && n_vec > 0 && rows > 0 && cols > 0) return QVX_E_NULL;
@@ -626,7 +684,7 @@ int qvx_plan_size(const qvx_plan* plan) { return plan ? (int)plan->calls.size() 
 int qvx_plan_run_eager(const qvx_plan* plan, void* stream) {
   if (!plan) return QVX_E_NULL;
   for (const auto& c : plan->calls)
-    if (int rc = gemv(c.out, c.w, c.type, c.X, c.nvec, c.rows, c.cols, as_stream(stream), c.epi); rc != QVX_OK) return rc;
+    if (int rc = run_call(c, as_stream(stream)); rc != QVX_OK) return rc;
   return QVX_OK;
 }
 
@@ -647,7 +705,7 @@ static int plan_record(const qvx_plan* plan, hipStream_t cs, std::vector<hipStre
     while (g >= 0 && i + n < calls.size() && calls[i + n].group == g) ++n;
     if (n == 1) {
       const auto& c = calls[i];
-      if (int rc = gemv(c.out, c.w, c.type, c.X, c.nvec, c.rows, c.cols, cs, c.epi); rc != QVX_OK) return rc;
+      if (int rc = run_call(c, cs); rc != QVX_OK) return rc;
       ++i;
       continue;
     }
@@ -662,7 +720,7 @@ static int plan_record(const qvx_plan* plan, hipStream_t cs, std::vector<hipStre
       const auto& c = calls[i + k];
       hipStream_t st = k == 0 ? cs : side[k - 1];
       if (k > 0 && hipStreamWaitEvent(st, fork, 0) != hipSuccess) return QVX_E_HIP;
-      if (int rc = gemv(c.out, c.w, c.type, c.X, c.nvec, c.rows, c.cols, st, c.epi); rc != QVX_OK) return rc;
+      if (int rc = run_call(c, st); rc != QVX_OK) return rc;
     }
     for (size_t k = 1; k < n; ++k) {
       hipEvent_t done = nullptr;

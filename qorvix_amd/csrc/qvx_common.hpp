@@ -118,6 +118,15 @@ constexpr int kMaxDevices = 64;
 constexpr size_t kLdsPerCU = 160 * 1024;
 constexpr size_t kLdsDefaultDyn = 64 * 1024;  // dynamic LDS a kernel may take without raising its limit
 
+// One member of a grouped GEMV launch: out = W . x for the launch's shared vector x.
+struct GemvMember {
+  const void* w;
+  float* y;
+  uint32_t type;
+  int rows;
+  size_t row_bytes;
+};
+
 // Per-kernel launch state: the kernel's static LDS (read once from its code object) and the
 // dynamic-LDS limit already set on each device (the attribute persists, so hipFuncSetAttribute runs
 // only when the limit has to grow: a decode loop does not pay for it on every launch).

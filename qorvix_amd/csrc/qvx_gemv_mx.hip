@@ -45,6 +45,7 @@
 #include <algorithm>
 
 #include "qvx_common.hpp"
+#include "qvx_gemv_valu.hpp"
 #include "qvx_norm.hpp"
 
 namespace qvx {
@@ -287,10 +288,12 @@ __device__ inline void mx_issue(__amdgpu_buffer_rsrc_t rsrc, const uint32_t (&of
 // EPI: EPI_NORM takes rmsnorm(x, NW, eps) as the activations (folded into the conversion: the
 // workgroup's tasks cover every element of its vectors); EPI_SWIGLU takes rows interleaved in
 // 16-row (gate, up) groups (geo.unit = 32) and writes silu(gate) * up, rows / 2 outputs a vector.
+// The kernel's body for workgroup b (the standalone kernel passes blockIdx.x, a grouped launch its
+// own block numbering).
 template <int NV, int NB, int TPT, int EPI>
-__global__ __launch_bounds__(1024) void k_gemv_mx(const uint8_t* __restrict__ W, const float* __restrict__ X,
-                                                  float* __restrict__ Y, int rows, int cols, MxGeo geo,
-                                                  const float* __restrict__ NW, float eps) {
+__device__ __forceinline__ void gemv_mx_body(const uint8_t* __restrict__ W, const float* __restrict__ X,
+                                             float* __restrict__ Y, int rows, int cols, const MxGeo& geo,
+                                             const float* __restrict__ NW, float eps, int b) {
   static_assert(NB >= 2 && NB <= 4, "the tile wait below covers up to 3 tiles ahead");
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   __shared__ __attribute__((aligned(16))) uint8_t ring[16 * NB * kTileBytes];
@@ -303,7 +306,6 @@ __global__ __launch_bounds__(1024) void k_gemv_mx(const uint8_t* __restrict__ W,
   float* meta = reinterpret_cast<float*>(lds + mx_frag_bytes(NV, nsb));
   QVX_LDS uint8_t* stage = (QVX_LDS uint8_t*)(ring + wave * NB * kTileBytes);
 
-  const int b = blockIdx.x;
   const int rb = b * geo.base + geo.unit * min(b, geo.rem), cnt = geo.base + (b < geo.rem ? geo.unit : 0);
   const int tq = wave % TQ, kq = wave / TQ;
   const int s0 = kq * nsb / KQ, s1 = (kq + 1) * nsb / KQ, nu = s1 - s0;
@@ -455,6 +457,13 @@ __global__ __launch_bounds__(1024) void k_gemv_mx(const uint8_t* __restrict__ W,
   }
   __syncthreads();
   mx_store<EPI>(red, Y, NV, rows, rb, cnt, TQ, KQ, tid);
+}
+
+template <int NV, int NB, int TPT, int EPI>
+__global__ __launch_bounds__(1024) void k_gemv_mx(const uint8_t* __restrict__ W, const float* __restrict__ X,
+                                                  float* __restrict__ Y, int rows, int cols, MxGeo geo,
+                                                  const float* __restrict__ NW, float eps) {
+  gemv_mx_body<NV, NB, TPT, EPI>(W, X, Y, rows, cols, geo, NW, eps, blockIdx.x);
 }
 
 // ---- batched form: 2..8 vectors a launch ------------------------------------------------------
@@ -950,6 +959,72 @@ static bool launch_mxj(const uint8_t* w, const float* X, float* Y, int nv, int r
   return true;
 }
 
+
+// ---- grouped launch: several one-vector GEMVs of the same activations -------------------------
+// Members share x.  Q4_K members run the matrix-core body above, a Q6_K member the VALU body of
+// qvx_gemv_valu.hpp, each with the geometry its own launch would take (mx_geometry / valu_grid), so
+// every row's arithmetic and summation order are its standalone kernel's and each member's outputs
+// are bit-identical to its own qvx_qmatmul.  Workgroups are numbered member after member, the Q6_K
+// member's first: they are the longest-latency ones (one row each, every lane's bytes in one load
+// round), so they start while the matrix-core workgroups still stream.  One launch pays the
+// dispatch ramp and the drain once for the whole group.
+constexpr int kGroupMx = 4;  // Q4_K members a launch
+
+struct GroupMx {
+  const uint8_t* w;
+  float* y;
+  int rows, nwg;
+  MxGeo geo;
+};
+struct GroupArgs {
+  GroupMx mx[kGroupMx];
+  int nmx;
+  const uint8_t* vw;  // the Q6_K member (vnwg = 0: none)
+  float* vy;
+  int vrows, vnwg;
+  Geo vgeo;
+};
+
+template <int TPT, int RMAX, bool CH>
+__global__ __launch_bounds__(1024) void k_gemv_group(const float* __restrict__ X, int cols, GroupArgs a) {
+  int b = blockIdx.x;
+  if (b < a.vnwg) {
+    constexpr int PF = prefetch_rows<T_Q6_K, 1>() < RMAX ? prefetch_rows<T_Q6_K, 1>() : RMAX;
+    const int sp = a.vgeo.Sp, t = threadIdx.x;
+    gemv_valu_body<T_Q6_K, 1, RMAX, TPT, PF, CH, false>(a.vw, X, a.vy, a.vrows, cols, a.vgeo, nullptr, 0.0f, b,
+                                                         t % sp, t / sp);
+    return;
+  }
+  b -= a.vnwg;
+  int i = 0;
+  while (i + 1 < a.nmx && b >= a.mx[i].nwg) {
+    b -= a.mx[i].nwg;
+    ++i;
+  }
+  gemv_mx_body<1, 2, TPT, 0>(a.mx[i].w, X, a.mx[i].y, a.mx[i].rows, cols, a.mx[i].geo, nullptr, 0.0f, b);
+}
+
+template <int TPT, int RMAX, bool CH>
+static bool launch_group_t(const float* X, int cols, const GroupArgs& a, int nwg, hipStream_t s) {
+  auto kern = &k_gemv_group<TPT, RMAX, CH>;
+  const size_t lds = std::max(mx_dyn_bytes(1, cols / 256), a.vnwg ? gemv_lds_bytes<T_Q6_K>(1, a.vgeo.S) : 0);
+  static LdsLimit lim;
+  if (!lds_ready(reinterpret_cast<const void*>(kern), lim, lds)) return false;
+  kern<<<(unsigned)nwg, 1024u, lds, s>>>(X, cols, a);
+  return true;
+}
+
+// Rows per VALU group, rounded up to an instantiated chunk (a chunk longer than the group's rows
+// clamps the extra loads to its last row and drops their results, so the outputs do not change).
+template <int TPT>
+static bool launch_group_tpt(const float* X, int cols, const GroupArgs& a, int nwg, int per_group, hipStream_t s) {
+  if (per_group <= 1) return launch_group_t<TPT, 1, false>(X, cols, a, nwg, s);
+  if (per_group <= 2) return launch_group_t<TPT, 2, false>(X, cols, a, nwg, s);
+  if (per_group <= 4) return launch_group_t<TPT, 4, false>(X, cols, a, nwg, s);
+  if (per_group <= 8) return launch_group_t<TPT, 8, false>(X, cols, a, nwg, s);
+  return launch_group_t<TPT, 8, true>(X, cols, a, nwg, s);
+}
+
 }  // namespace
 
 // 1 if the fused prologue / epilogue can run on this shape: the norm needs whole 512-element
@@ -1035,6 +1110,43 @@ bool launch_gemv_mx_q4k(const void* w, const float* X, float* Y, int nvec, int r
 
 int gemv_mxj_supported(int cols) {
   return cols > 0 && cols % 256 == 0 && gemv_mx_max_nv(cols) >= 1 ? 1 : 0;
+}
+
+
+// Grouped one-vector GEMV over members that share x (k_gemv_group): up to kGroupMx Q4_K members
+// on the matrix-core kernel and at most one Q6_K member on the VALU kernel, all 16-byte aligned
+// with 16-byte row pitches (the operands the standalone fast kernels take).  Returns false, having
+// launched nothing, when a member is outside that set: the caller then runs the members one by one.
+bool launch_gemv_group(const GemvMember* m, int n, const float* X, int cols, hipStream_t s) {
+  if (n < 1 || gemv_mx_max_nv(cols) < 1 || (cols / 256 * 32 + 1023) / 1024 > 2) return false;
+  GroupArgs a{};
+  int nwg = 0, per_group = 0;
+  for (int i = 0; i < n; ++i) {
+    if (m[i].type == T_Q4_K && a.nmx < kGroupMx && m[i].row_bytes < (1u << 24)) {
+      GroupMx& g = a.mx[a.nmx++];
+      g.w = static_cast<const uint8_t*>(m[i].w);
+      g.y = m[i].y;
+      g.rows = m[i].rows;
+      g.nwg = mx_geometry(m[i].rows, cols, m[i].row_bytes, g.geo);
+      nwg += g.nwg;
+    } else if (m[i].type == T_Q6_K && a.vnwg == 0) {
+      Geo geo{};
+      if (!geometry<T_Q6_K>(cols, m[i].row_bytes, geo) || geo.Sp * geo.G != 1024 ||
+          (geo.S * 2 * Lane<T_Q6_K>::kR + 1023) / 1024 != (cols / 256 * 32 + 1023) / 1024)
+        return false;  // a full 1024-thread workgroup, and the group's conversion-task count its own
+      a.vw = static_cast<const uint8_t*>(m[i].w);
+      a.vy = m[i].y;
+      a.vrows = m[i].rows;
+      a.vnwg = valu_grid(m[i].rows, geo, per_group);
+      a.vgeo = geo;
+      nwg += a.vnwg;
+    } else {
+      return false;
+    }
+  }
+  if (a.nmx == 0) return false;
+  return (cols / 256 * 32 + 1023) / 1024 <= 1 ? launch_group_tpt<1>(X, cols, a, nwg, per_group, s)
+                                               : launch_group_tpt<2>(X, cols, a, nwg, per_group, s);
 }
 
 }  // namespace qvx

@@ -290,6 +290,17 @@ class Plan:
         if rc != OK:
             raise QvxError(rc, "qvx_plan_add_qmatmul_swiglu")
 
+    def add_group(self, outs, ws, X) -> None:
+        """outs[i] = ws[i] . X for one vector X, as one grouped call (``qvx_plan_add_qmatmul_group``)."""
+        n = len(ws)
+        arr = C.c_void_p * n
+        rc = lib().qvx_plan_add_qmatmul_group(self._h, arr(*[o.data_ptr() for o in outs]),
+                                              arr(*[w.data.data_ptr() for w in ws]),
+                                              (C.c_uint32 * n)(*[w.type for w in ws]),
+                                              (C.c_int32 * n)(*[w.rows for w in ws]), n, X.data_ptr(), ws[0].cols)
+        if rc != OK:
+            raise QvxError(rc, "qvx_plan_add_qmatmul_group")
+
     def fork(self) -> None:
         rc = lib().qvx_plan_fork(self._h)
         if rc != OK:
@@ -334,10 +345,13 @@ class DecodeStep:
     """The weight side of one decode step at M vectors: activation stand-ins, per-projection
     outputs, and the plan of 7 GEMVs per layer + the LM head in the reference's order."""
 
-    def __init__(self, model: Model, m: int, seed: int = 9, device="cuda", concurrent: bool = False):
+    def __init__(self, model: Model, m: int, seed: int = 9, device="cuda", concurrent: bool = False,
+                 grouped: bool = False):
         import torch
         if concurrent and model.parts:
             raise ValueError("concurrent q/k/v and gate/up branches are for the unfused model")
+        if grouped and (concurrent or m != 1):
+            raise ValueError("grouped calls take one vector, in order")
         self.model, self.m = model, m
         f32 = dict(dtype=torch.float32, device=device)
         self.inputs = {k: torch.empty((m, c), **f32) for k, c in _input_widths(model).items()}
@@ -345,11 +359,20 @@ class DecodeStep:
             fill_normal_t(self.inputs[k], seed=seed + i)
         self.outputs = []
         self.plan = Plan()
+        pending = []  # grouped: the q/k/v or gate/up members collected so far
         for l, name, w, src in model.calls():
             y = torch.empty((m, w.rows), **f32)
             self.outputs.append((l, name, y))
-            # q/k/v read the same normed state, and so do gate/up: independent branches when asked
-            # (measured slower on MI355X: the graph's cross-branch joins cost more than the overlap)
+            if grouped and name in ("wq", "wk", "wqk", "wv", "ffn_gate", "ffn_up"):
+                # q/k/v read the same normed state (q|k stacked or not), and so do gate/up when they
+                # are not stacked: one grouped launch each
+                pending.append((y, w))
+                if name in ("wv", "ffn_up"):
+                    self.plan.add_group([o for o, _ in pending], [x for _, x in pending], self.inputs[src])
+                    pending = []
+                continue
+            # ... or independent graph branches when asked (measured slower on MI355X: the graph's
+            # cross-branch joins cost more than the overlap)
             if concurrent and name in ("wq", "ffn_gate"):
                 self.plan.fork()
             self.plan.add(y, w, self.inputs[src], m)

@@ -41,6 +41,30 @@ def test_plan_replays_match_eager(cuda, small_model, m, concurrent):
     step.plan.close()
 
 
+@pytest.mark.parametrize("stacked", [False, True])
+def test_grouped_plan_matches_plain(cuda, small_model, stacked):
+    """q/k/v and gate/up as grouped calls, or q|k stacked and grouped with v (4 launches a layer either
+    way): every output bit-identical to the ungrouped plan's on the same weights, on every replay."""
+    torch = cuda
+    model = small_model.fused() if stacked else small_model
+    plain = decode.DecodeStep(model, 1, seed=4)
+    grouped = decode.DecodeStep(model, 1, seed=4, grouped=True)
+    assert len(grouped.plan) == 2 * 4 + 1
+    s = torch.cuda.current_stream().cuda_stream
+    plain.replay(s)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for _, _, y in grouped.outputs:
+            y.fill_(float("nan"))
+        float(torch.randn(1 << 20, device="cuda").sum())
+        grouped.replay(s)
+        torch.cuda.synchronize()
+        for (l, name, y), (_, _, r) in zip(grouped.outputs, plain.outputs):
+            assert torch.equal(y.view(torch.int32), r.view(torch.int32)), (rep, l, name)
+    plain.plan.close()
+    grouped.plan.close()
+
+
 def test_plan_outputs_match_oracle(cuda, small_model):
     torch = cuda
     step = decode.DecodeStep(small_model, 2, seed=3)

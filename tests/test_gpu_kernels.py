@@ -529,6 +529,78 @@ def test_gemm_split_k_concurrent_streams(cuda, t):
             np.testing.assert_array_equal(outs[i][k].cpu().numpy().view(np.uint32), alone[i].view(np.uint32))
 
 
+GROUP_CASES = [
+    # the decoder's q / k / v (Q6_K v) and gate / up of Llama-3-8B
+    ("qkv", 4096, [(qvx.Q4_K, 4096), (qvx.Q4_K, 1024), (qvx.Q6_K, 1024)]),
+    ("gate_up", 4096, [(qvx.Q4_K, 14336), (qvx.Q4_K, 14336)]),
+    # two conversion tasks a thread (K = 16384), a Q6_K member of 8 rows a group
+    ("long_k", 16384, [(qvx.Q6_K, 4096), (qvx.Q4_K, 1000)]),
+    # ragged row counts (a Q6_K member of 5 rows a group), four Q4_K members
+    ("ragged", 2048, [(qvx.Q4_K, 777), (qvx.Q6_K, 20000), (qvx.Q4_K, 17), (qvx.Q4_K, 1), (qvx.Q4_K, 300)]),
+    # a Q6_K member walking its rows in chunks (10 rows a group)
+    ("chunked", 2048, [(qvx.Q6_K, 40000), (qvx.Q4_K, 64)]),
+    # outside the grouped kernel (two Q6_K members; five Q4_K; a Q8_0 member; a Q6_K row of 448
+    # slots, whose VALU workgroup is not 1024 threads): member by member
+    ("two_q6k", 4096, [(qvx.Q6_K, 1024), (qvx.Q6_K, 512)]),
+    ("q6k_k14336", 14336, [(qvx.Q4_K, 256), (qvx.Q6_K, 512)]),
+    ("five_q4k", 1024, [(qvx.Q4_K, 64)] * 5),
+    ("q8_0", 4096, [(qvx.Q4_K, 512), (qvx.Q8_0, 512)]),
+    # a member with no rows computes nothing
+    ("empty_member", 4096, [(qvx.Q4_K, 256), (qvx.Q6_K, 0), (qvx.Q6_K, 96)]),
+]
+
+
+@pytest.mark.parametrize("name,cols,members", GROUP_CASES, ids=[c[0] for c in GROUP_CASES])
+def test_qmatmul_group_matches_single_calls(cuda, name, cols, members):
+    """qvx_qmatmul_group: each member's output bit-identical to its own qvx_qmatmul, whether the
+    members run as one launch or one by one; a member's neighbours' rows stay untouched."""
+    torch = cuda
+    x = torch.empty(cols, dtype=torch.float32, device="cuda")
+    qvx.fill_normal_t(x, seed=81, mul=1.0)
+    ws, outs, refs = [], [], []
+    for i, (t, rows) in enumerate(members):
+        w = qvx.empty_weight(t, max(rows, 1), cols)
+        qvx.fill_synthetic_t(w, t, max(rows, 1), cols, seed=90 + i, scale_mul=1e-3)
+        ws.append(w)
+        outs.append(torch.full((rows + 16,), float("nan"), dtype=torch.float32, device="cuda"))
+        r = torch.empty(max(rows, 1), dtype=torch.float32, device="cuda")
+        assert qvx.qmatmul(r.data_ptr(), w.data_ptr(), t, x.data_ptr(), rows, cols) == qvx.OK
+        refs.append(r)
+    torch.cuda.synchronize()
+    for _ in range(2):
+        rc = qvx.qmatmul_group([o.data_ptr() for o in outs], [w.data_ptr() for w in ws], [t for t, _ in members],
+                               [r for _, r in members], x.data_ptr(), cols)
+        assert rc == qvx.OK
+        torch.cuda.synchronize()
+        for i, ((t, rows), o, r) in enumerate(zip(members, outs, refs)):
+            assert torch.equal(o[:rows].view(torch.int32), r[:rows].view(torch.int32)), (name, i)
+            assert torch.isnan(o[rows:]).all(), (name, i)
+
+
+def test_qmatmul_group_matches_oracle(cuda):
+    """The grouped q / k / v launch against the oracle (a slice of rows of each member)."""
+    torch = cuda
+    cols = 4096
+    members = [(qvx.Q4_K, 4096), (qvx.Q4_K, 1024), (qvx.Q6_K, 1024)]
+    x = torch.empty(cols, dtype=torch.float32, device="cuda")
+    qvx.fill_normal_t(x, seed=83, mul=1.0)
+    ws = []
+    for i, (t, rows) in enumerate(members):
+        w = qvx.empty_weight(t, rows, cols)
+        qvx.fill_synthetic_t(w, t, rows, cols, seed=95 + i, scale_mul=1e-3)
+        ws.append(w)
+    outs = [torch.empty(rows, dtype=torch.float32, device="cuda") for _, rows in members]
+    assert qvx.qmatmul_group([o.data_ptr() for o in outs], [w.data_ptr() for w in ws], [t for t, _ in members],
+                             [r for _, r in members], x.data_ptr(), cols) == qvx.OK
+    torch.cuda.synchronize()
+    xs = x.cpu().numpy()[None, :]
+    for (t, rows), w, o in zip(members, ws, outs):
+        rb = qvx.row_bytes(t, cols)
+        r0, nr = rows - 40, 40
+        ref = oracle.matmul_f64(w[r0 * rb:(r0 + nr) * rb].cpu().numpy(), t, xs, 1, nr, cols)
+        assert max_rel(o[r0:].cpu().numpy()[None, :], ref) <= 1e-3, t
+
+
 DEQUANT_GEMM_TYPES = [qvx.Q6_K, qvx.Q8_0, qvx.Q4_0, qvx.Q5_0, qvx.Q5_K, qvx.Q4_1, qvx.Q5_1, qvx.Q8_1,
                       qvx.F16, qvx.BF16, qvx.F32]
 
