@@ -194,6 +194,8 @@ def decode_sweep(torch, stream, steps, cpu=True):
     def time_step(mdl, m, concurrent, ops=None):
         if ops == "grouped":
             st = decode.DecodeStep(mdl, m, grouped=True)
+        elif ops == "fused_grouped":
+            st = decode.FusedDecodeStep(mdl, m, grouped=True)
         elif ops == "fused":
             st = decode.FusedDecodeStep(mdl, m)
         elif ops == "separate":
@@ -226,6 +228,7 @@ def decode_sweep(torch, stream, steps, cpu=True):
         ms_sep = time_step(model, m, False, ops="separate")
         ms_gr = time_step(model, m, False, ops="grouped") if m == 1 else None
         ms_fgr = time_step(fused, m, False, ops="grouped") if m == 1 else None
+        ms_ogr = time_step(fops, m, False, ops="fused_grouped") if m == 1 else None
         _, ab = decode.sweep_bytes(m)
         gbs = ab / (ms * 1e-3) / 1e9
         out[f"M{m}"] = {"ms_per_token": round(ms, 4), "algorithmic_bytes_per_token": ab, "gb_s": round(gbs, 1),
@@ -240,9 +243,13 @@ def decode_sweep(torch, stream, steps, cpu=True):
                             "gb_s_grouped_qkv_gateup": round(ab / (ms_gr * 1e-3) / 1e9, 1),
                             "ms_per_token_grouped_qk_v": round(ms_fgr, 4),
                             "gb_s_grouped_qk_v": round(ab / (ms_fgr * 1e-3) / 1e9, 1),
+                            "ms_per_token_fused_ops_grouped": round(ms_ogr, 4),
+                            "gb_s_fused_ops_grouped": round(ab / (ms_ogr * 1e-3) / 1e9, 1),
                             "grouped_note": "grouped_qkv_gateup: q, k, v (Q6_K) in one grouped launch and gate, "
                                             "up in another (qvx_qmatmul_group, 4 launches a layer); grouped_qk_v: "
-                                            "q|k stacked grouped with v, gate|up stacked (4 launches a layer)"}
+                                            "q|k stacked grouped with v, gate|up stacked (4 launches a layer); "
+                                            "fused_ops_grouped: the fused ops with q|k and v on the normed state "
+                                            "in one grouped launch (4 launches a layer)"}
                            if ms_gr else {}),
                         "fused_ops_note": "q|k and v with the attention RMSNorm folded in, o, gate|up with the FFN "
                                           "RMSNorm and the SwiGLU epilogue, down on that SwiGLU output, LM head with "
@@ -254,7 +261,8 @@ def decode_sweep(torch, stream, steps, cpu=True):
             f"q|k and gate|up stacked (5 GEMVs a layer); {ms_ops:.3f} ms/token with the norms and SwiGLU folded in "
             f"(the same ops as separate launches: {ms_sep:.3f})"
             + (f"; {ms_gr:.3f} ms/token with q/k/v and gate/up as grouped launches, {ms_fgr:.3f} with q|k stacked "
-               f"and grouped with v" if ms_gr else ""))
+               f"and grouped with v, {ms_ogr:.3f} fused ops with q|k and v grouped (4 launches a layer)"
+               if ms_gr else ""))
         if cpu:
             # the reference CPU operator on layer 0's seven projections and the LM head (same blocks,
             # seeded activations); per token = 32 x layer + LM head

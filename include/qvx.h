@@ -112,17 +112,18 @@ int qvx_rmsnorm(float* d_out, const float* d_x, const float* d_w, float eps, int
  * silu(z) = z / (1 + exp(-z)), in fp32. */
 int qvx_swiglu(float* d_out, const float* d_gate, const float* d_up, size_t n, void* stream);
 
-/* Grouped GEMV: d_out[i] = W_i . x for the n members (1 <= n <= QVX_GROUP_MAX, else QVX_E_NVEC),
- * each member's W_i of types[i] with rows[i] rows and the shared cols: the reference decoder's
- * consecutive wmatmuls of one activation vector, the q / k / v projections of xn
- * (runtime/src/text_model.cpp:147-149), in one call.  Each member's checks and outputs are
- * qvx_qmatmul's (d_out[i] is bit-identical to qvx_qmatmul(d_out[i], d_w[i], types[i], d_x,
- * rows[i], cols)); a member with rows[i] <= 0 computes nothing.  Up to 4 Q4_K members and one
- * Q6_K member with aligned operands and cols a multiple of 256 up to 16384 run as ONE launch
- * (the dispatch ramp and drain paid once); other groups run member by member. */
+/* Grouped GEMV: d_out[i] = W_i . xn for the n members (1 <= n <= QVX_GROUP_MAX, else QVX_E_NVEC),
+ * each member's W_i of types[i] with rows[i] rows and the shared cols, xn = rmsnorm(x, d_norm_w,
+ * eps) when d_norm_w is non-NULL, else x: the reference decoder's rmsnorm and the consecutive
+ * wmatmuls of its output, the q / k / v projections (runtime/src/text_model.cpp:146-149), in one
+ * call.  Each member's checks and outputs are qvx_qmatmul's, or qvx_qmatmul_n_rmsnorm's with a norm
+ * (d_out[i] is bit-identical to that call on member i alone); a member with rows[i] <= 0 computes
+ * nothing.  Up to 4 Q4_K members and one Q6_K member with aligned operands and cols a multiple of
+ * 256 up to 16384 (of 512 with a norm) run as ONE launch (the dispatch ramp and drain paid once,
+ * the norm folded into each workgroup's activation conversion); other groups run member by member. */
 #define QVX_GROUP_MAX 8
 int qvx_qmatmul_group(float* const* d_out, const void* const* d_w, const uint32_t* types, const int* rows, int n,
-                      const float* d_x, int cols, void* stream);
+                      const float* d_x, const float* d_norm_w, float eps, int cols, void* stream);
 /* y[v] = W . rmsnorm(x[v], norm_w, eps): the reference decoder's ops::rmsnorm followed by wmatmul
  * (runtime/src/text_model.cpp:146-149, 161-163, 171-172) in one call; the arguments and checks of
  * qvx_qmatmul_n plus d_norm_w [cols] (NULL -> QVX_E_NULL; cols > 16384 -> QVX_E_RANGE).  Where the GEMV kernel takes the shape
@@ -226,9 +227,11 @@ int qvx_plan_create(qvx_plan** plan);
  * rows <= 0 is accepted and records nothing.  Appending to an instantiated plan -> QVX_E_STATE. */
 int qvx_plan_add_qmatmul_n(qvx_plan* plan, float* d_out, const void* d_w, uint32_t type,
                            const float* d_X, int n_vec, int rows, int cols);
-/* Record a qvx_qmatmul_group call (the same arguments and checks). */
+/* Record a qvx_qmatmul_group call (the same arguments and checks; with a norm, every member must be
+ * one a kernel folds the norm into, as for qvx_plan_add_qmatmul_n_rmsnorm, else QVX_E_SHAPE). */
 int qvx_plan_add_qmatmul_group(qvx_plan* plan, float* const* d_out, const void* const* d_w, const uint32_t* types,
-                               const int* rows, int n, const float* d_x, int cols);
+                               const int* rows, int n, const float* d_x, const float* d_norm_w, float eps,
+                               int cols);
 /* Append a fused call (the arguments and checks of qvx_qmatmul_n_rmsnorm / qvx_qmatmul_swiglu).  A
  * replay allocates nothing, so only calls a kernel folds the norm / SwiGLU into are accepted
  * (others -> QVX_E_SHAPE). */

@@ -47,7 +47,7 @@ SIGNATURES = {
     "qvx_qmatmul": ([_vp, _vp, _u32, _vp, _i32, _i32, _vp], _i32),
     "qvx_qmatmul_n": ([_vp, _vp, _u32, _vp, _i32, _i32, _i32, _vp], _i32),
     "qvx_qmatmul_n_rmsnorm": ([_vp, _vp, _u32, _vp, _vp, _f32, _i32, _i32, _i32, _vp], _i32),
-    "qvx_qmatmul_group": ([_vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp], _i32),
+    "qvx_qmatmul_group": ([_vp, _vp, _vp, _vp, _i32, _vp, _vp, _f32, _i32, _vp], _i32),
     "qvx_qmatmul_swiglu": ([_vp, _vp, _u32, _vp, _vp, _f32, _i32, _i32, _i32, _vp], _i32),
     "qvx_interleave_rows16": ([_vp, _vp, _vp, _u32, _i32, _i32, _vp], _i32),
     "qvx_rmsnorm": ([_vp, _vp, _vp, _f32, _i32, _i32, _vp], _i32),
@@ -66,7 +66,7 @@ SIGNATURES = {
     "qvx_plan_add_qmatmul_n": ([_vp, _vp, _vp, _u32, _vp, _i32, _i32, _i32], _i32),
     "qvx_plan_add_qmatmul_n_rmsnorm": ([_vp, _vp, _vp, _u32, _vp, _vp, _f32, _i32, _i32, _i32], _i32),
     "qvx_plan_add_qmatmul_swiglu": ([_vp, _vp, _vp, _u32, _vp, _vp, _f32, _i32, _i32, _i32], _i32),
-    "qvx_plan_add_qmatmul_group": ([_vp, _vp, _vp, _vp, _vp, _i32, _vp, _i32], _i32),
+    "qvx_plan_add_qmatmul_group": ([_vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _f32, _i32], _i32),
     "qvx_plan_fork": ([_vp], _i32),
     "qvx_plan_join": ([_vp], _i32),
     "qvx_plan_size": ([_vp], _i32),
@@ -200,16 +200,18 @@ def qmatmul_n(out: int, weight: int, ggml_type: int, X: int, nvec: int, rows: in
 GROUP_MAX = 8
 
 
-def qmatmul_group(outs, weights, types, rows, x: int, cols: int, stream: int = 0) -> int:
-    """outs[i] = W_i . x for the members (device pointers; types and row counts per member): the
-    decoder's q / k / v wmatmuls of one vector (runtime/src/text_model.cpp:147-149) in one call,
-    each output bit-identical to qmatmul's. Status."""
+def qmatmul_group(outs, weights, types, rows, x: int, cols: int, stream: int = 0, norm_w: int = 0,
+                  eps: float = 1e-5) -> int:
+    """outs[i] = W_i . xn for the members (device pointers; types and row counts per member), xn =
+    rmsnorm(x, norm_w, eps) when norm_w else x: the decoder's rmsnorm and q / k / v wmatmuls
+    (runtime/src/text_model.cpp:146-149) in one call, each output bit-identical to qmatmul's (or
+    qmatmul_n_rmsnorm's). Status."""
     n = len(outs)
     if not (len(weights) == len(types) == len(rows) == n):
         raise ValueError("qmatmul_group: one output, weight, type and row count per member")
     arr = C.c_void_p * max(n, 1)
     return lib().qvx_qmatmul_group(arr(*outs), arr(*weights), (C.c_uint32 * max(n, 1))(*types),
-                                   (C.c_int32 * max(n, 1))(*rows), n, x, cols, stream)
+                                   (C.c_int32 * max(n, 1))(*rows), n, x, norm_w or None, eps, cols, stream)
 
 
 def qmatmul_n_rmsnorm(out: int, weight: int, ggml_type: int, X: int, norm_w: int, eps: float, nvec: int, rows: int,

@@ -56,7 +56,7 @@ int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M
 int launch_quantize_act_q8(const uint16_t* X, int M, int K, int8_t* q, float* scale, int32_t* qsum,
                            hipStream_t s);
 void launch_zero(float* p, size_t n, hipStream_t s);
-bool launch_gemv_group(const GemvMember* m, int n, const float* X, int cols, hipStream_t s);
+bool launch_gemv_group(const GemvMember* m, int n, const float* X, int cols, const GemvEpi& epi, hipStream_t s);
 }  // namespace qvx
 
 using namespace qvx;
@@ -404,22 +404,26 @@ static int group_members(float* const* d_out, const void* const* d_w, const uint
   return QVX_OK;
 }
 
-// One launch for the members when the grouped kernel takes them all, else one qmatmul each.
-static int gemv_group(const GemvMember* m, int k, const float* x, int cols, hipStream_t s) {
+// One launch for the members when the grouped kernel takes them all, else one qmatmul (or
+// qmatmul_n_rmsnorm) each.
+static int gemv_group(const GemvMember* m, int k, const float* x, int cols, const GemvEpi& epi, hipStream_t s) {
   bool fast = cols > 0 && aligned16(x);
   for (int i = 0; i < k; ++i) fast = fast && aligned16(m[i].w) && m[i].row_bytes % 16 == 0;
-  if (fast && launch_gemv_group(m, k, x, cols, s)) return hip_status();
+  if (fast && launch_gemv_group(m, k, x, cols, epi, s)) return hip_status();
   for (int i = 0; i < k; ++i)
-    if (int rc = gemv(m[i].y, m[i].w, m[i].type, x, 1, m[i].rows, cols, s); rc != QVX_OK) return rc;
+    if (int rc = gemv(m[i].y, m[i].w, m[i].type, x, 1, m[i].rows, cols, s, epi); rc != QVX_OK) return rc;
   return QVX_OK;
 }
 
 int qvx_qmatmul_group(float* const* d_out, const void* const* d_w, const uint32_t* types, const int* rows, int n,
-                      const float* d_x, int cols, void* stream) {
+                      const float* d_x, const float* d_norm_w, float eps, int cols, void* stream) {
   GemvMember m[QVX_GROUP_MAX];
   int k = 0;
   if (int rc = group_members(d_out, d_w, types, rows, n, d_x, cols, m, &k); rc != QVX_OK) return rc;
-  return k ? gemv_group(m, k, d_x, cols, as_stream(stream)) : QVX_OK;
+  GemvEpi epi;
+  epi.norm_w = d_norm_w;
+  epi.eps = eps;
+  return k ? gemv_group(m, k, d_x, cols, epi, as_stream(stream)) : QVX_OK;
 }
 
 int qvx_qmatmul_n_rmsnorm(float* d_out, const void* d_w, uint32_t type, const float* d_X, const float* d_norm_w,
@@ -627,19 +631,28 @@ int qvx_plan_add_qmatmul_n(qvx_plan* plan, float* d_out, const void* d_w, uint32
 
 // One recorded call: a grouped call or a plain / fused GEMV.
 static int run_call(const qvx_plan::Call& c, hipStream_t s) {
-  if (!c.members.empty()) return gemv_group(c.members.data(), (int)c.members.size(), c.X, c.cols, s);
+  if (!c.members.empty()) return gemv_group(c.members.data(), (int)c.members.size(), c.X, c.cols, c.epi, s);
   return gemv(c.out, c.w, c.type, c.X, c.nvec, c.rows, c.cols, s, c.epi);
 }
 
 int qvx_plan_add_qmatmul_group(qvx_plan* plan, float* const* d_out, const void* const* d_w, const uint32_t* types,
-                               const int* rows, int n, const float* d_x, int cols) {
+                               const int* rows, int n, const float* d_x, const float* d_norm_w, float eps,
+                               int cols) {
   if (!plan) return QVX_E_NULL;
   if (plan->exec) return QVX_E_STATE;
   GemvMember m[QVX_GROUP_MAX];
   int k = 0;
   if (int rc = group_members(d_out, d_w, types, rows, n, d_x, cols, m, &k); rc != QVX_OK) return rc;
   if (k == 0) return QVX_OK;
-  qvx_plan::Call c{nullptr, nullptr, 0, d_x, 1, 0, cols, plan->open_group, GemvEpi{}, {}};
+  GemvEpi epi;
+  epi.norm_w = d_norm_w;
+  epi.eps = eps;
+  if (d_norm_w && cols > 0)  // a replay allocates nothing: every member must take the folded norm
+    for (int i = 0; i < k; ++i)
+      if (!fused_route(m[i].type, 1, m[i].rows, cols, m[i].row_bytes,
+                       aligned16(m[i].w) && aligned16(d_x) && m[i].row_bytes % 16 == 0, epi))
+        return QVX_E_SHAPE;
+  qvx_plan::Call c{nullptr, nullptr, 0, d_x, 1, 0, cols, plan->open_group, epi, {}};
   c.members.assign(m, m + k);
   plan->calls.push_back(std::move(c));
   return QVX_OK;

@@ -985,14 +985,17 @@ struct GroupArgs {
   Geo vgeo;
 };
 
-template <int TPT, int RMAX, bool CH>
-__global__ __launch_bounds__(1024) void k_gemv_group(const float* __restrict__ X, int cols, GroupArgs a) {
+// NORM: every member takes rmsnorm(x, NW, eps) as its activations, folded into each body's
+// conversion as in its standalone kernel (qvx_qmatmul_n_rmsnorm's arithmetic).
+template <int TPT, int RMAX, bool CH, bool NORM>
+__global__ __launch_bounds__(1024) void k_gemv_group(const float* __restrict__ X, int cols, GroupArgs a,
+                                                     const float* __restrict__ NW, float eps) {
   int b = blockIdx.x;
   if (b < a.vnwg) {
     constexpr int PF = prefetch_rows<T_Q6_K, 1>() < RMAX ? prefetch_rows<T_Q6_K, 1>() : RMAX;
     const int sp = a.vgeo.Sp, t = threadIdx.x;
-    gemv_valu_body<T_Q6_K, 1, RMAX, TPT, PF, CH, false>(a.vw, X, a.vy, a.vrows, cols, a.vgeo, nullptr, 0.0f, b,
-                                                         t % sp, t / sp);
+    gemv_valu_body<T_Q6_K, 1, RMAX, TPT, PF, CH, NORM>(a.vw, X, a.vy, a.vrows, cols, a.vgeo, NW, eps, b, t % sp,
+                                                        t / sp);
     return;
   }
   b -= a.vnwg;
@@ -1001,28 +1004,31 @@ __global__ __launch_bounds__(1024) void k_gemv_group(const float* __restrict__ X
     b -= a.mx[i].nwg;
     ++i;
   }
-  gemv_mx_body<1, 2, TPT, 0>(a.mx[i].w, X, a.mx[i].y, a.mx[i].rows, cols, a.mx[i].geo, nullptr, 0.0f, b);
+  gemv_mx_body<1, 2, TPT, NORM ? EPI_NORM : 0>(a.mx[i].w, X, a.mx[i].y, a.mx[i].rows, cols, a.mx[i].geo, NW, eps,
+                                               b);
 }
 
-template <int TPT, int RMAX, bool CH>
-static bool launch_group_t(const float* X, int cols, const GroupArgs& a, int nwg, hipStream_t s) {
-  auto kern = &k_gemv_group<TPT, RMAX, CH>;
+template <int TPT, int RMAX, bool CH, bool NORM>
+static bool launch_group_t(const float* X, int cols, const GroupArgs& a, int nwg, const GemvEpi& epi,
+                           hipStream_t s) {
+  auto kern = &k_gemv_group<TPT, RMAX, CH, NORM>;
   const size_t lds = std::max(mx_dyn_bytes(1, cols / 256), a.vnwg ? gemv_lds_bytes<T_Q6_K>(1, a.vgeo.S) : 0);
   static LdsLimit lim;
   if (!lds_ready(reinterpret_cast<const void*>(kern), lim, lds)) return false;
-  kern<<<(unsigned)nwg, 1024u, lds, s>>>(X, cols, a);
+  kern<<<(unsigned)nwg, 1024u, lds, s>>>(X, cols, a, epi.norm_w, epi.eps);
   return true;
 }
 
 // Rows per VALU group, rounded up to an instantiated chunk (a chunk longer than the group's rows
 // clamps the extra loads to its last row and drops their results, so the outputs do not change).
-template <int TPT>
-static bool launch_group_tpt(const float* X, int cols, const GroupArgs& a, int nwg, int per_group, hipStream_t s) {
-  if (per_group <= 1) return launch_group_t<TPT, 1, false>(X, cols, a, nwg, s);
-  if (per_group <= 2) return launch_group_t<TPT, 2, false>(X, cols, a, nwg, s);
-  if (per_group <= 4) return launch_group_t<TPT, 4, false>(X, cols, a, nwg, s);
-  if (per_group <= 8) return launch_group_t<TPT, 8, false>(X, cols, a, nwg, s);
-  return launch_group_t<TPT, 8, true>(X, cols, a, nwg, s);
+template <int TPT, bool NORM>
+static bool launch_group_tpt(const float* X, int cols, const GroupArgs& a, int nwg, int per_group,
+                             const GemvEpi& epi, hipStream_t s) {
+  if (per_group <= 1) return launch_group_t<TPT, 1, false, NORM>(X, cols, a, nwg, epi, s);
+  if (per_group <= 2) return launch_group_t<TPT, 2, false, NORM>(X, cols, a, nwg, epi, s);
+  if (per_group <= 4) return launch_group_t<TPT, 4, false, NORM>(X, cols, a, nwg, epi, s);
+  if (per_group <= 8) return launch_group_t<TPT, 8, false, NORM>(X, cols, a, nwg, epi, s);
+  return launch_group_t<TPT, 8, true, NORM>(X, cols, a, nwg, epi, s);
 }
 
 }  // namespace
@@ -1115,10 +1121,12 @@ int gemv_mxj_supported(int cols) {
 
 // Grouped one-vector GEMV over members that share x (k_gemv_group): up to kGroupMx Q4_K members
 // on the matrix-core kernel and at most one Q6_K member on the VALU kernel, all 16-byte aligned
-// with 16-byte row pitches (the operands the standalone fast kernels take).  Returns false, having
-// launched nothing, when a member is outside that set: the caller then runs the members one by one.
-bool launch_gemv_group(const GemvMember* m, int n, const float* X, int cols, hipStream_t s) {
+// with 16-byte row pitches (the operands the standalone fast kernels take), optionally on
+// rmsnorm(x) (epi.norm_w; no SwiGLU).  Returns false, having launched nothing, when a member or the
+// epilogue is outside that set: the caller then runs the members one by one.
+bool launch_gemv_group(const GemvMember* m, int n, const float* X, int cols, const GemvEpi& epi, hipStream_t s) {
   if (n < 1 || gemv_mx_max_nv(cols) < 1 || (cols / 256 * 32 + 1023) / 1024 > 2) return false;
+  if (epi.swiglu || !mx_epi_supported(epi, 0, cols)) return false;
   GroupArgs a{};
   int nwg = 0, per_group = 0;
   for (int i = 0; i < n; ++i) {
@@ -1145,8 +1153,12 @@ bool launch_gemv_group(const GemvMember* m, int n, const float* X, int cols, hip
     }
   }
   if (a.nmx == 0) return false;
-  return (cols / 256 * 32 + 1023) / 1024 <= 1 ? launch_group_tpt<1>(X, cols, a, nwg, per_group, s)
-                                               : launch_group_tpt<2>(X, cols, a, nwg, per_group, s);
+  const bool tpt1 = (cols / 256 * 32 + 1023) / 1024 <= 1;
+  if (epi.norm_w)
+    return tpt1 ? launch_group_tpt<1, true>(X, cols, a, nwg, per_group, epi, s)
+                : launch_group_tpt<2, true>(X, cols, a, nwg, per_group, epi, s);
+  return tpt1 ? launch_group_tpt<1, false>(X, cols, a, nwg, per_group, epi, s)
+              : launch_group_tpt<2, false>(X, cols, a, nwg, per_group, epi, s);
 }
 
 }  // namespace qvx

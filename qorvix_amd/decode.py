@@ -290,14 +290,17 @@ class Plan:
         if rc != OK:
             raise QvxError(rc, "qvx_plan_add_qmatmul_swiglu")
 
-    def add_group(self, outs, ws, X) -> None:
-        """outs[i] = ws[i] . X for one vector X, as one grouped call (``qvx_plan_add_qmatmul_group``)."""
+    def add_group(self, outs, ws, X, norm_w=None, eps: float = 1e-5) -> None:
+        """outs[i] = ws[i] . xn for one vector X, xn = rmsnorm(X, norm_w, eps) when norm_w is given
+        else X, as one grouped call (``qvx_plan_add_qmatmul_group``)."""
         n = len(ws)
         arr = C.c_void_p * n
+        nw = norm_w.data_ptr() if norm_w is not None else None
         rc = lib().qvx_plan_add_qmatmul_group(self._h, arr(*[o.data_ptr() for o in outs]),
                                               arr(*[w.data.data_ptr() for w in ws]),
                                               (C.c_uint32 * n)(*[w.type for w in ws]),
-                                              (C.c_int32 * n)(*[w.rows for w in ws]), n, X.data_ptr(), ws[0].cols)
+                                              (C.c_int32 * n)(*[w.rows for w in ws]), n, X.data_ptr(), nw, eps,
+                                              ws[0].cols)
         if rc != OK:
             raise QvxError(rc, "qvx_plan_add_qmatmul_group")
 
@@ -389,15 +392,17 @@ class DecodeStep:
 
 class FusedDecodeStep:
     """One decode step at M vectors with the engine's fused decoder ops (5 launches a layer + the LM
-    head), in the reference's order (text_model.cpp:146-177) on a ``Model.fused_ops()`` model:
+    head; 4 with ``grouped``, q|k and v then sharing one launch at M = 1), in the reference's order (text_model.cpp:146-177) on a ``Model.fused_ops()`` model:
     per layer qk = Wqk . rmsnorm(x, attn_norm) and v = Wv . rmsnorm(x, attn_norm) (text_model.cpp:
     146-149), o = Wo . attn (:158), h = swiglu(Wgate . xn, Wup . xn) with xn = rmsnorm(x, ffn_norm)
     (:161-165), down = Wdown . h (:166); logits = Wlm . rmsnorm(x, output_norm) (:171-172).  x (the
     residual stream) and attn (the attention output) are seeded stand-ins, h is the SwiGLU output
     the step itself computes; one output buffer per projection, reused across layers."""
 
-    def __init__(self, model: Model, m: int, seed: int = 9, device="cuda"):
+    def __init__(self, model: Model, m: int, seed: int = 9, device="cuda", grouped: bool = False):
         import torch
+        if grouped and m != 1:
+            raise ValueError("grouped calls take one vector")
         self.model, self.m = model, m
         f32 = dict(dtype=torch.float32, device=device)
         l0 = model.layers[0]
@@ -411,9 +416,11 @@ class FusedDecodeStep:
         eps = model.eps
         for l, layer in enumerate(model.layers):
             an, fn = model.norms[l]["attn_norm"], model.norms[l]["ffn_norm"]
-            for k in ("wqk", "wq", "wk", "wv"):
-                if k in layer:
-                    self.plan.add_rmsnorm(self.out[k], layer[k], self.x, an, eps, m)
+            qkv = [k for k in ("wqk", "wq", "wk", "wv") if k in layer]
+            if grouped:  # q|k and v on the normed state in one launch (4 launches a layer)
+                self.plan.add_group([self.out[k] for k in qkv], [layer[k] for k in qkv], self.x, an, eps)
+            for k in qkv if not grouped else ():
+                self.plan.add_rmsnorm(self.out[k], layer[k], self.x, an, eps, m)
             self.plan.add(self.out["wo"], layer["wo"], self.attn, m)
             self.plan.add_swiglu(self.h, layer["ffn_gateup"], self.x, fn, eps, m)
             self.plan.add(self.out["ffn_down"], layer["ffn_down"], self.h, m)

@@ -103,18 +103,19 @@ def test_qmatmul_group_rejections():
     outs, ws = arr(FAKE, FAKE, FAKE), arr(FAKE, FAKE, FAKE)
     types = (C.c_uint32 * 3)(qvx.Q4_K, qvx.Q4_K, qvx.Q6_K)
     rows = (C.c_int32 * 3)(16, 16, 16)
-    assert lib.qvx_qmatmul_group(outs, ws, types, rows, 0, FAKE, 256, None) == qvx.E_NVEC
-    assert lib.qvx_qmatmul_group(outs, ws, types, rows, qvx.GROUP_MAX + 1, FAKE, 256, None) == qvx.E_NVEC
-    assert lib.qvx_qmatmul_group(None, ws, types, rows, 3, FAKE, 256, None) == qvx.E_NULL
-    assert lib.qvx_qmatmul_group(outs, ws, types, rows, 3, None, 256, None) == qvx.E_NULL
-    assert lib.qvx_qmatmul_group(outs, ws, types, rows, 3, FAKE, 300, None) == qvx.E_SHAPE  # cols % 256
+    assert lib.qvx_qmatmul_group(outs, ws, types, rows, 0, FAKE, None, 1e-5, 256, None) == qvx.E_NVEC
+    assert lib.qvx_qmatmul_group(outs, ws, types, rows, qvx.GROUP_MAX + 1, FAKE, None, 1e-5, 256, None) == qvx.E_NVEC
+    assert lib.qvx_qmatmul_group(None, ws, types, rows, 3, FAKE, None, 1e-5, 256, None) == qvx.E_NULL
+    assert lib.qvx_qmatmul_group(outs, ws, types, rows, 3, None, None, 1e-5, 256, None) == qvx.E_NULL
+    assert lib.qvx_qmatmul_group(outs, ws, types, rows, 3, FAKE, None, 1e-5, 300, None) == qvx.E_SHAPE  # cols % 256
     bad = (C.c_uint32 * 3)(qvx.Q4_K, 10, qvx.Q6_K)  # Q2_K
-    assert lib.qvx_qmatmul_group(outs, ws, bad, rows, 3, FAKE, 256, None) == qvx.E_TYPE
+    assert lib.qvx_qmatmul_group(outs, ws, bad, rows, 3, FAKE, None, 1e-5, 256, None) == qvx.E_TYPE
     nulls = arr(FAKE, None, FAKE)
-    assert lib.qvx_qmatmul_group(outs, nulls, types, rows, 3, FAKE, 256, None) == qvx.E_NULL
+    assert lib.qvx_qmatmul_group(outs, nulls, types, rows, 3, FAKE, None, 1e-5, 256, None) == qvx.E_NULL
     # members without rows compute nothing: all empty is a successful no-op
+    # a norm with no members to compute is checked no further
     none = (C.c_int32 * 3)(0, -1, 0)
-    assert lib.qvx_qmatmul_group(outs, nulls, types, none, 3, FAKE, 256, None) == qvx.OK
+    assert lib.qvx_qmatmul_group(outs, nulls, types, none, 3, FAKE, None, 1e-5, 256, None) == qvx.OK
 
 
 def test_gemm_and_dequant_rejections():

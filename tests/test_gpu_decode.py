@@ -65,6 +65,33 @@ def test_grouped_plan_matches_plain(cuda, small_model, stacked):
     grouped.plan.close()
 
 
+def test_fused_grouped_step_matches_fused(cuda, small_model):
+    """The fused decode step with q|k and v on the normed state as one grouped launch (4 launches a
+    layer): every output bit-identical to the 5-launch step's."""
+    torch = cuda
+    fops = small_model.fused_ops()
+    five = decode.FusedDecodeStep(fops, 1, seed=6)
+    four = decode.FusedDecodeStep(fops, 1, seed=6, grouped=True)
+    assert five.launches() == 2 * 5 + 1 and four.launches() == 2 * 4 + 1
+    s = torch.cuda.current_stream().cuda_stream
+    five.replay(s)
+    torch.cuda.synchronize()
+    ref = {k: v.clone() for k, v in five.out.items()}
+    ref_h, ref_lg = five.h.clone(), five.logits.clone()
+    for rep in range(3):
+        for v in list(four.out.values()) + [four.h, four.logits]:
+            v.fill_(float("nan"))
+        float(torch.randn(1 << 20, device="cuda").sum())
+        four.replay(s)
+        torch.cuda.synchronize()
+        for k, r in ref.items():
+            assert torch.equal(four.out[k].view(torch.int32), r.view(torch.int32)), (rep, k)
+        assert torch.equal(four.h.view(torch.int32), ref_h.view(torch.int32)), rep
+        assert torch.equal(four.logits.view(torch.int32), ref_lg.view(torch.int32)), rep
+    five.plan.close()
+    four.plan.close()
+
+
 def test_plan_outputs_match_oracle(cuda, small_model):
     torch = cuda
     step = decode.DecodeStep(small_model, 2, seed=3)

@@ -550,13 +550,19 @@ GROUP_CASES = [
 ]
 
 
+@pytest.mark.parametrize("norm", [False, True], ids=["plain", "rmsnorm"])
 @pytest.mark.parametrize("name,cols,members", GROUP_CASES, ids=[c[0] for c in GROUP_CASES])
-def test_qmatmul_group_matches_single_calls(cuda, name, cols, members):
-    """qvx_qmatmul_group: each member's output bit-identical to its own qvx_qmatmul, whether the
-    members run as one launch or one by one; a member's neighbours' rows stay untouched."""
+def test_qmatmul_group_matches_single_calls(cuda, name, cols, members, norm):
+    """qvx_qmatmul_group: each member's output bit-identical to its own qvx_qmatmul (with a norm: its
+    own qvx_qmatmul_n_rmsnorm), whether the members run as one launch or one by one; a member's
+    neighbours' rows stay untouched."""
     torch = cuda
     x = torch.empty(cols, dtype=torch.float32, device="cuda")
     qvx.fill_normal_t(x, seed=81, mul=1.0)
+    nw = torch.empty(cols, dtype=torch.float32, device="cuda")
+    qvx.fill_normal_t(nw, seed=82, mul=0.2)
+    nw.add_(1.0)
+    eps = 1e-5
     ws, outs, refs = [], [], []
     for i, (t, rows) in enumerate(members):
         w = qvx.empty_weight(t, max(rows, 1), cols)
@@ -564,12 +570,17 @@ def test_qmatmul_group_matches_single_calls(cuda, name, cols, members):
         ws.append(w)
         outs.append(torch.full((rows + 16,), float("nan"), dtype=torch.float32, device="cuda"))
         r = torch.empty(max(rows, 1), dtype=torch.float32, device="cuda")
-        assert qvx.qmatmul(r.data_ptr(), w.data_ptr(), t, x.data_ptr(), rows, cols) == qvx.OK
+        if norm:
+            assert qvx.qmatmul_n_rmsnorm(r.data_ptr(), w.data_ptr(), t, x.data_ptr(), nw.data_ptr(), eps, 1, rows,
+                                         cols) == qvx.OK
+        else:
+            assert qvx.qmatmul(r.data_ptr(), w.data_ptr(), t, x.data_ptr(), rows, cols) == qvx.OK
         refs.append(r)
     torch.cuda.synchronize()
     for _ in range(2):
         rc = qvx.qmatmul_group([o.data_ptr() for o in outs], [w.data_ptr() for w in ws], [t for t, _ in members],
-                               [r for _, r in members], x.data_ptr(), cols)
+                               [r for _, r in members], x.data_ptr(), cols, norm_w=nw.data_ptr() if norm else 0,
+                               eps=eps)
         assert rc == qvx.OK
         torch.cuda.synchronize()
         for i, ((t, rows), o, r) in enumerate(zip(members, outs, refs)):
