@@ -299,19 +299,43 @@ def decode_sweep(torch, stream, steps, cpu=True):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / reps, st.flops()
 
+    def time_prefill_graph(mdl, mp, reps=3):
+        # the same step captured into one graph (every GEMM through the no-allocation entry point)
+        st = decode.PrefillStep(mdl, mp)
+        st.capture()
+        cur = torch.cuda.current_stream()
+        st.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(cur)
+        for _ in range(reps):
+            st.replay()
+        e1.record(cur)
+        torch.cuda.synchronize()
+        del st
+        return e0.elapsed_time(e1) / reps
+
     pre = {}
     for mp in (512, 2048):
         ms, flops = time_prefill(model, mp)
         ms_fu, _ = time_prefill(fused, mp)
+        ms_g = time_prefill_graph(model, mp)
+        ms_gfu = time_prefill_graph(fused, mp)
         tf = flops / (ms * 1e-3) / 1e12
         tbt = mp * out["M1"]["ms_per_token"]
         pre[f"M{mp}"] = {"ms": round(ms, 3), "tokens_per_s": round(mp / (ms * 1e-3), 1), "tflops": round(tf, 1),
                          "frac_of_bf16_peak": round(tf / BF16_PEAK_TFLOPS, 4), "runs_timed": 3,
                          "token_by_token_ms": round(tbt, 2), "speedup_vs_token_by_token": round(tbt / ms, 1),
                          "ms_fused_qk_gateup": round(ms_fu, 3),
-                         "tokens_per_s_fused_qk_gateup": round(mp / (ms_fu * 1e-3), 1)}
+                         "tokens_per_s_fused_qk_gateup": round(mp / (ms_fu * 1e-3), 1),
+                         "ms_graph": round(ms_g, 3), "tokens_per_s_graph": round(mp / (ms_g * 1e-3), 1),
+                         "tflops_graph": round(flops / (ms_g * 1e-3) / 1e12, 1),
+                         "ms_graph_fused_qk_gateup": round(ms_gfu, 3),
+                         "graph_note": "the step captured into one HIP graph (qvx_qgemm_f16_noalloc), "
+                                       "replayed: no host launch gaps"}
         log(f"[bench] prefill M={mp}: {ms:.2f} ms ({mp / (ms * 1e-3):.0f} tokens/s, {tf:.0f} TFLOP/s); token by token "
-            f"{tbt:.1f} ms; {ms_fu:.2f} ms with q|k and gate|up stacked")
+            f"{tbt:.1f} ms; {ms_fu:.2f} ms with q|k and gate|up stacked; as one graph {ms_g:.2f} ms "
+            f"({mp / (ms_g * 1e-3):.0f} tokens/s), stacked {ms_gfu:.2f} ms")
     out["prefill"] = {"workload": "Llama-3-8B Q4_K_M prompt prefill: 32 x 7 projections as GEMMs over M positions "
                                   "(fp16 activations) + the Q6_K LM head on the last position", **pre}
     del model, fused, fops
