@@ -18,8 +18,9 @@
  *  - Device entry points take device pointers and a hipStream_t passed as `void*` (NULL = the
  *    null stream).  They are asynchronous and stream-ordered, like the CUDA backend's matmulS
  *    launch (cuda/src/cuda_backend.cu:1534-1542).  They allocate no device memory, except
- *    qvx_qgemm_f16, which takes stream-ordered temporaries (the converted activations, the partial
- *    tiles of a K split, or the dequantised weight) from a memory pool the library owns per device.
+ *    qvx_qgemm_f16 and qvx_gemm16, which take stream-ordered temporaries (the converted activations,
+ *    the partial tiles of a K split, or the dequantised weight) from a memory pool the library owns
+ *    per device.
  *  - Entry points ending in _host take host pointers and are synchronous: the exact calling
  *    convention of the reference's CPU operator, for a CPU-side drop-in.
  *  - Calls that overlap on one device are safe for distinct outputs; the library holds no
@@ -46,7 +47,7 @@ extern "C" {
 #define QVX_E_STATE (-8)   /* a plan launched before qvx_plan_instantiate, or changed after it */
 #define QVX_E_FORMAT (-9)  /* malformed GGUF data (qvx_gguf_last_error() says what) */
 #define QVX_E_IO (-10)     /* a file could not be opened or mapped */
-#define QVX_E_LIB (-11)    /* a runtime library the call needs (rocBLAS) is missing or failed */
+#define QVX_E_LIB (-11)    /* a runtime library the call needs is missing or failed (no current call needs one) */
 
 /* GEMM variants for qvx_qgemm_f16 */
 #define QVX_GEMM_BF16 0 /* X rounded to bf16; raw weight blocks staged in LDS, dequantised to bf16; bf16 MFMA */
@@ -151,33 +152,32 @@ int qvx_interleave_rows16(void* d_dst, const void* d_a, const void* d_b, uint32_
 /* Prefill GEMM: out[m * rows + r] = sum_k X[m, k] * dequant(W)[r, k] for m < M, X fp16 [M, cols].
  * No reference counterpart (the reference prefills token by token); semantics are qmatmulN's
  * with X converted fp16 -> fp32 exactly.  variant = QVX_GEMM_BF16 | QVX_GEMM_F16 | QVX_GEMM_I8;
- * tolerance 2e-2 max-relative against the exact sum.  type: every type qvx_qmatmul takes.  Q4_K
- * runs on the engine's raw-block MFMA kernels; Q6_K with X 16-byte and W 4-byte aligned on its own
- * MFMA kernels (cols a multiple of 512: the Q4_K kernels' pipeline, blocks dequantised in
- * registers; else cols a multiple of 64: a dequantising kernel), each weight element rounded to
- * fp16 / bf16 from its dequantised value.  Other types, and Q6_K calls those kernels decline, are dequantised into a
- * stream-ordered 16-bit temporary (fp16, bf16 for QVX_GEMM_BF16) and multiplied by one rocBLAS
- * gemm_ex (fp32 accumulate), rocBLAS being loaded on first use (QVX_E_LIB when it is missing or
- * fails; these calls create a rocBLAS handle per host thread and device on first use, so they are
- * not for graph capture).  QVX_GEMM_I8 takes Q4_K only (other types: QVX_E_TYPE).  Grids smaller
- * than the chip (small M) split K across workgroups; the last split of each output tile adds the
- * partial tiles in split order, so every call returns the same bits for the same inputs. */
+ * tolerance 2e-2 max-relative against the exact sum.  type: every type qvx_qmatmul takes, each on the
+ * engine's own matrix-core kernels (no library GEMM), each weight element rounded to fp16 / bf16
+ * from its exact dequantised value.  Q4_K runs on raw-block MFMA kernels; Q6_K with X 16-byte and W
+ * 4-byte aligned on its own raw-block MFMA kernels (cols a multiple of 512: the Q4_K kernels'
+ * pipeline, blocks dequantised in registers; else cols a multiple of 64: a dequantising kernel).
+ * Other types, and Q6_K calls those kernels decline, are dequantised into a stream-ordered 16-bit
+ * temporary (fp16, bf16 for QVX_GEMM_BF16; per panel of rows) and multiplied by the plain 16-bit MFMA
+ * GEMM of qvx_gemm16.  QVX_GEMM_I8 takes Q4_K only (other types: QVX_E_TYPE).  Grids smaller than
+ * the chip (small M) split K across workgroups; the last split of each output tile adds the partial
+ * tiles in split order, so every call returns the same bits for the same inputs. */
 int qvx_qgemm_f16(float* d_out, const void* d_w, uint32_t type, const uint16_t* d_X, int M,
                   int rows, int cols, int variant, void* stream);
 
 /* The prefill GEMM without any device allocation: the arguments, checks, kernels and results of
- * qvx_qgemm_f16 for the engine's own GEMM kernels, for callers that cannot allocate (code under HIP
- * graph capture, tight serving loops, harnesses that forbid hipMalloc).  No reference counterpart.
- * Its temporaries (the bf16 or Q8 copy of X) live in one fixed scratch array per device, of
- * QVX_NOALLOC_SCRATCH_BYTES, held from the first call on a device until the process ends; no call
- * makes hipMalloc, hipFree or an allocating library call.  Limits: the weight type must be Q4_K,
- * or Q6_K with cols a multiple of 64, X 16-byte and W 4-byte aligned, and not QVX_GEMM_I8 (other
- * calls: QVX_E_TYPE, as their GEMM goes through a library that allocates); a call whose
- * temporaries exceed the scratch -> QVX_E_RANGE (QVX_GEMM_BF16 needs 2*M*cols bytes, QVX_GEMM_I8
- * about 1.25*M*cols, QVX_GEMM_F16 none; plus, when a grid smaller than the chip splits K, 128 KiB
- * of partial tile per tile and split -- qvx_qgemm_plan_q4k reports both for Q4_K).  Every call on a device shares that device's scratch:
- * calls that overlap on one device (different streams, or host threads) race and must be ordered by
- * the caller. */
+ * qvx_qgemm_f16, for callers that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No reference counterpart.  Its temporaries (the bf16 or Q8 copy
+ * of X, a K split's partial tiles, and for the types without a raw-block kernel the 16-bit weight)
+ * live in one fixed scratch array per device, of QVX_NOALLOC_SCRATCH_BYTES, held from the first call
+ * on a device until the process ends; no call makes hipMalloc, hipFree or an allocating library
+ * call.  A call whose temporaries exceed the scratch -> QVX_E_RANGE (QVX_GEMM_BF16 needs 2*M*cols
+ * bytes, QVX_GEMM_I8 about 1.25*M*cols, QVX_GEMM_F16 none; plus, when a grid smaller than the chip
+ * splits K, 128 KiB of partial tile per tile and split -- qvx_qgemm_plan_q4k reports both for Q4_K;
+ * the types dequantised to 16 bits run panel by panel of at least 256 weight rows, each panel's
+ * 16-bit weight (2*256*cols bytes at the least) sharing the scratch with the copy of X).  Every call
+ * on a device shares that device's scratch: calls that overlap on one device (different streams, or
+ * host threads) race and must be ordered by the caller. */
 #define QVX_NOALLOC_SCRATCH_BYTES (64u << 20)
 int qvx_qgemm_f16_noalloc(float* d_out, const void* d_w, uint32_t type, const uint16_t* d_X, int M,
                           int rows, int cols, int variant, void* stream);
@@ -190,6 +190,22 @@ int qvx_qgemm_f16_noalloc(float* d_out, const void* d_w, uint32_t type, const ui
  * base_a, the remaining columns mt_b tiles from token base_b -- and returns the number of launches
  * (1 or 2), or QVX_E_SHAPE when M, rows or cols is not positive or cols % 256 != 0. */
 int qvx_qgemm_plan_q4k(int M, int rows, int cols, int cus, int* desc, int cap);
+
+/* Plain 16-bit GEMM on the matrix cores: out[m * N + n] = sum_k X[m, k] * B[n, k], X [M, K] and
+ * B [N, K] row-major bf16 (variant QVX_GEMM_BF16) or fp16 (QVX_GEMM_F16) bits, fp32 accumulation
+ * and output.  No reference counterpart: the GEMM behind qvx_qgemm_f16 for weights dequantised to
+ * 16 bits (qvx_dequantize16), for callers that keep a dequantised copy of a weight and multiply it
+ * many times.  The kernel takes K in multiples of 64 and 16-byte-aligned operands; other calls run
+ * on zero-padded copies from the library's stream-ordered pool, as do the partial tiles of a K split
+ * (grids smaller than the chip; the partials are added in split order, so results do not vary
+ * between runs).  M, N or K < 0 -> QVX_E_SHAPE; M or N == 0 is a no-op; K == 0 writes zeros. */
+int qvx_gemm16(float* d_out, const uint16_t* d_X, const uint16_t* d_B, int M, int N, int K, int variant,
+               void* stream);
+
+/* Dequantise the first n / blockSize whole blocks of `type` to 16 bits: the reference's dequantised
+ * value (dequant.cpp:277-296) rounded once to nearest-even bf16 (bf16 != 0) or fp16 -- the weight
+ * operand of the prefill GEMM.  No reference counterpart. */
+int qvx_dequantize16(uint32_t type, const void* d_src, uint16_t* d_dst, size_t n, int bf16, void* stream);
 
 /* Per-32 Q8 activation quantiser used by QVX_GEMM_I8 (no reference counterpart): for row m and
  * block j, scale = amax/127, q = round-half-away(x * 127/amax) clamped to +-127, qsum = sum q.

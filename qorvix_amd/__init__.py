@@ -57,6 +57,8 @@ SIGNATURES = {
     "qvx_qgemm_f16": ([_vp, _vp, _u32, _vp, _i32, _i32, _i32, _i32, _vp], _i32),
     "qvx_qgemm_f16_noalloc": ([_vp, _vp, _u32, _vp, _i32, _i32, _i32, _i32, _vp], _i32),
     "qvx_qgemm_plan_q4k": ([_i32, _i32, _i32, _i32, _vp, _i32], _i32),
+    "qvx_gemm16": ([_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp], _i32),
+    "qvx_dequantize16": ([_u32, _vp, _vp, _sz, _i32, _vp], _i32),
     "qvx_quantize_act_q8": ([_vp, _i32, _i32, _vp, _vp, _vp, _vp], _i32),
     "qvx_fill_synthetic": ([_vp, _u32, _i32, _i32, _u64, _f32, _vp], _i32),
     "qvx_fill_normal_f32": ([_vp, _sz, _u64, _f32, _vp], _i32),
@@ -315,6 +317,29 @@ def qgemm_t(w, ggml_type: int, X, rows: int, cols: int, variant: int = GEMM_BF16
         out = torch.empty((M, rows), dtype=torch.float32, device=X.device)
     _check(lib().qvx_qgemm_f16(out.data_ptr(), w.data_ptr(), ggml_type, X.data_ptr(), M, rows, cols, variant,
                                _stream()), "qvx_qgemm_f16")
+    return out
+
+
+def gemm16_t(X, B, variant: int = GEMM_BF16, out=None):
+    """out fp32 [M, N] = X [M, K] . B [N, K]^T for 16-bit device tensors (bf16 or fp16 bits, any
+    16-bit dtype): the engine's plain matrix-core GEMM (qvx_gemm16)."""
+    import torch
+    M, K = X.shape
+    N = B.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32, device=X.device)
+    _check(lib().qvx_gemm16(out.data_ptr(), X.data_ptr(), B.data_ptr(), M, N, K, variant, _stream()), "qvx_gemm16")
+    return out
+
+
+def dequantize16_t(w, ggml_type: int, n: int, bf16: bool, out=None):
+    """The first n elements of a device weight as 16-bit values (qvx_dequantize16): the reference's
+    dequantised value rounded once to bf16 (bf16=True) or fp16; an int16 tensor of the bits."""
+    import torch
+    if out is None:
+        out = torch.empty(n, dtype=torch.int16, device=w.device)
+    _check(lib().qvx_dequantize16(ggml_type, w.data_ptr(), out.data_ptr(), n, 1 if bf16 else 0, _stream()),
+           "qvx_dequantize16")
     return out
 
 

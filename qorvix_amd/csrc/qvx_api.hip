@@ -53,6 +53,9 @@ bool launch_gemv_q6n(const void* w, const float* X, float* Y, int nvec, int rows
                      hipStream_t s);
 int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M, int rows, int cols,
                  int variant, hipStream_t s, void* ws, size_t ws_cap);
+int launch_gemm16_entry(float* out, const uint16_t* X, const uint16_t* B, int M, int N, int K, bool bf16,
+                        hipStream_t s);
+bool launch_dequant16(uint32_t t, const void* src, uint16_t* dst, size_t n, bool bf16, hipStream_t s);
 int launch_quantize_act_q8(const uint16_t* X, int M, int K, int8_t* q, float* scale, int32_t* qsum,
                            hipStream_t s);
 void launch_zero(float* p, size_t n, hipStream_t s);
@@ -356,7 +359,7 @@ const char* qvx_strerror(int code) {
     case QVX_E_STATE: return "plan not instantiated, or changed after instantiation";
     case QVX_E_FORMAT: return "malformed GGUF data";
     case QVX_E_IO: return "file could not be opened or mapped";
-    case QVX_E_LIB: return "a runtime library the call needs (rocBLAS) is missing or failed";
+    case QVX_E_LIB: return "a runtime library the call needs is missing or failed";
     default: return "unknown qvx status";
   }
 }
@@ -550,15 +553,36 @@ int qvx_qgemm_f16_noalloc(float* d_out, const void* d_w, uint32_t type, const ui
     return hip_status();
   }
   if (!d_w || !d_X) return QVX_E_NULL;
-  // the other weight types run without allocating only on the dequantising MFMA kernel (cols a
-  // multiple of 64, X 16-byte and W 4-byte aligned); their fallback GEMM allocates
-  if (type != T_Q4_K &&
-      !qgemm_deq_supported(type, d_w, d_X, cols, rows, (size_t)(cols / (int)ti->block) * ti->bytes))
-    return QVX_E_TYPE;
   void* ws = scratch_ptr();
   if (!ws) return QVX_E_HIP;
   const int rc = launch_qgemm(d_out, d_w, type, d_X, M, rows, cols, variant, as_stream(stream), ws, kScratchBytes);
   if (rc != QVX_OK) return rc;
+  return hip_status();
+}
+
+int qvx_gemm16(float* d_out, const uint16_t* d_X, const uint16_t* d_B, int M, int N, int K, int variant,
+               void* stream) {
+  if (variant != QVX_GEMM_BF16 && variant != QVX_GEMM_F16) return QVX_E_VARIANT;
+  if (M < 0 || N < 0 || K < 0) return QVX_E_SHAPE;
+  if (M == 0 || N == 0) return QVX_OK;
+  if (!d_out) return QVX_E_NULL;
+  if (K == 0) {
+    launch_zero(d_out, (size_t)M * (size_t)N, as_stream(stream));
+    return hip_status();
+  }
+  if (!d_X || !d_B) return QVX_E_NULL;
+  const int rc = launch_gemm16_entry(d_out, d_X, d_B, M, N, K, variant == QVX_GEMM_BF16, as_stream(stream));
+  if (rc != QVX_OK) return rc;
+  return hip_status();
+}
+
+int qvx_dequantize16(uint32_t type, const void* d_src, uint16_t* d_dst, size_t n, int bf16, void* stream) {
+  const TypeInfo* t = type_info(type);
+  if (!t || !can_dequantize(type)) return QVX_E_TYPE;
+  n -= n % t->block;  // whole blocks, as qvx_dequantize
+  if (n == 0) return QVX_OK;
+  if (!d_src || !d_dst) return QVX_E_NULL;
+  if (!launch_dequant16(type, d_src, d_dst, n, bf16 != 0, as_stream(stream))) return QVX_E_HIP;
   return hip_status();
 }
 

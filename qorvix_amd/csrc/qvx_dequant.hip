@@ -114,6 +114,14 @@ __device__ inline uint16_t to_bf16(float f) {
   return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
 }
 
+// fp32 -> fp16 bits, round to nearest even.  The value is pinned first: otherwise the compiler folds
+// the product that produced it and the conversion into one mixed-precision multiply-add with a +0
+// addend, which turns a -0 product (a zero code times a negative scale) into +0.
+__device__ inline uint16_t to_f16(float f) {
+  asm volatile("" : "+v"(f));
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
 template <uint32_t T, int QK, int BB, bool BF>
 __global__ __launch_bounds__(256) void k_dequant16(const uint8_t* __restrict__ src, uint16_t* __restrict__ dst,
                                                    size_t n) {
@@ -126,7 +134,7 @@ __global__ __launch_bounds__(256) void k_dequant16(const uint8_t* __restrict__ s
     const size_t blk = i / QK;
     v = deq_elem<T>(src + blk * BB, (int)(i - blk * QK));
   }
-  dst[i] = BF ? to_bf16(v) : __builtin_bit_cast(uint16_t, (_Float16)v);
+  dst[i] = BF ? to_bf16(v) : to_f16(v);
 }
 
 // Eight consecutive elements per thread (always inside one block: every block size is a multiple
@@ -153,8 +161,8 @@ __global__ __launch_bounds__(256) void k_dequant16x8(const uint8_t* __restrict__
   uint32_t w[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const uint32_t lo = BF ? to_bf16(v[2 * j]) : __builtin_bit_cast(uint16_t, (_Float16)v[2 * j]);
-    const uint32_t hi = BF ? to_bf16(v[2 * j + 1]) : __builtin_bit_cast(uint16_t, (_Float16)v[2 * j + 1]);
+    const uint32_t lo = BF ? to_bf16(v[2 * j]) : to_f16(v[2 * j]);
+    const uint32_t hi = BF ? to_bf16(v[2 * j + 1]) : to_f16(v[2 * j + 1]);
     w[j] = lo | (hi << 16);
   }
   dst[g] = make_uint4(w[0], w[1], w[2], w[3]);
@@ -180,8 +188,8 @@ __global__ __launch_bounds__(256) void k_dequant16_lds(const uint8_t* __restrict
   uint32_t w[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const uint32_t lo = BF ? to_bf16(v[2 * j]) : __builtin_bit_cast(uint16_t, (_Float16)v[2 * j]);
-    const uint32_t hi = BF ? to_bf16(v[2 * j + 1]) : __builtin_bit_cast(uint16_t, (_Float16)v[2 * j + 1]);
+    const uint32_t lo = BF ? to_bf16(v[2 * j]) : to_f16(v[2 * j]);
+    const uint32_t hi = BF ? to_bf16(v[2 * j + 1]) : to_f16(v[2 * j + 1]);
     w[j] = lo | (hi << 16);
   }
   dst[i / 8] = make_uint4(w[0], w[1], w[2], w[3]);

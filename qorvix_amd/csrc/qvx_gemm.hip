@@ -1263,6 +1263,8 @@ bool launch_q4k(float* out, const void* w, const uint16_t* X, int M, int N, int 
   return true;
 }
 
+}  // namespace
+
 // Compute units of the current device (cached per device).
 int device_cus() {
   static std::atomic<int> cache[kMaxDevices] = {};
@@ -1275,6 +1277,8 @@ int device_cus() {
   }
   return n;
 }
+
+namespace {
 
 inline int cdiv(int a, int b) { return (a + b - 1) / b; }
 
@@ -1421,9 +1425,10 @@ int q4k_plan_desc(int M, int N, int K, int cus, int* desc, int cap) {
   return p.n;
 }
 
-// Returns a QVX status (0 ok, -1 type, -5 HIP, -7 range).
-int launch_qgemm_dequant(float* out, const void* w, uint32_t t, const uint16_t* X, int M, int rows, int cols,
-                         bool bf16, hipStream_t s);
+// The prefill GEMM through a 16-bit dequantised weight and the plain MFMA GEMM (qvx_gemm16.hip);
+// returns a QVX status (0 ok, -1 type, -5 HIP, -7 range).
+int launch_qgemm_via16(float* out, const void* w, uint32_t t, const uint16_t* X, int M, int rows, int cols, bool bf16,
+                       hipStream_t s, void* ws, size_t ws_cap);
 // The dequantising MFMA GEMM of the other weight types (qvx_gemm_deq.hip).
 bool qgemm_deq_supported(uint32_t t, const void* w, const uint16_t* X, int K, int N, size_t row_bytes);
 size_t qgemm_deq_split_bytes(int M, int N, int K, size_t* counters);
@@ -1507,11 +1512,9 @@ int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M
       if (tmp) gemm_ws_release(tmp, ws, s);
       return ok ? 0 : -5;
     }
-    // ... else dequantised whole to 16 bits, then a library GEMM, which allocates (its handle, the
-    // 16-bit weight): not for the no-allocation entry point.
-    if (ws) return -1;
-    if ((size_t)rows * (size_t)cols >= (1ull << 31) || (size_t)M * (size_t)cols >= (1ull << 31)) return -7;
-    return launch_qgemm_dequant(out, w, t, X, M, rows, cols, variant == VAR_BF16, s);
+    // ... else dequantised into 16 bits per panel of rows, then the plain 16-bit MFMA GEMM
+    // (qvx_gemm16.hip).
+    return launch_qgemm_via16(out, w, t, X, M, rows, cols, variant == VAR_BF16, s, ws, ws_cap);
   }
   if ((reinterpret_cast<uintptr_t>(w) & 15u) || (reinterpret_cast<uintptr_t>(X) & 15u)) return -7;
   // Buffer offsets are 32-bit: a tile's rows must span less than 2 GiB.

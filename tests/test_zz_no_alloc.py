@@ -79,6 +79,27 @@ def test_noalloc_q6k_matches_allocating_gemm_on_two_calls(cuda, variant):
         assert max_rel(got[:, idx], X32 @ Wd.T) <= GEMM_TOL
 
 
+@pytest.mark.parametrize("t", [qvx.Q8_0, qvx.Q4_0])
+@pytest.mark.parametrize("variant", [qvx.GEMM_BF16, qvx.GEMM_F16])
+def test_noalloc_dequant16_types_match_allocating_gemm_on_two_calls(cuda, t, variant):
+    """Q8_0 / Q4_0 (weight dequantised to 16 bits, then the plain MFMA GEMM) through the
+    no-allocation entry point: first 2048 x 11008 x 4096, whose 90 MB 16-bit weight does not fit the
+    scratch and runs in two panels of rows (128-token tiles, no K split, where the allocating call
+    runs the whole weight on 256-token tiles: both add each output's K16 products in the same order,
+    so the bits agree); then a smaller call with eight K splits, whose partial tiles and counters
+    reuse the scratch the first call left behind.  Both bit for bit the allocating call's and within
+    the GEMM tolerance of the fp64 oracle on a row slice."""
+    lib = qvx.lib()
+    for n, (M, rows, cols) in enumerate(((2048, 11008, 4096), (128, 2048, 4096))):
+        t_, W, X, idx, Wd = _case(cuda, M, rows, cols, seed=970 + 10 * n + variant + t, t=t)
+        got = _call(lib.qvx_qgemm_f16_noalloc, cuda, W, t, X, rows, cols, variant)
+        want = _call(lib.qvx_qgemm_f16, cuda, W, t, X, rows, cols, variant)
+        assert np.isfinite(got).all()
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+        X32 = X.cpu().numpy().astype(np.float64)
+        assert max_rel(got[:, idx], X32 @ Wd.T) <= GEMM_TOL
+
+
 def test_noalloc_rejects_calls_past_its_scratch(cuda):
     """The bf16 copy of X needs 2 * M * cols bytes: past QVX_NOALLOC_SCRATCH_BYTES (64 MiB) the call is
     refused before any work, and the output is untouched; the fp16 variant needs no scratch."""
