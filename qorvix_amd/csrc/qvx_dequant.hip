@@ -195,6 +195,135 @@ __global__ __launch_bounds__(256) void k_dequant16_lds(const uint8_t* __restrict
   dst[i / 8] = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+// ---- 16-bit dequantisation, wide workgroups -------------------------------------------------------
+// Eight consecutive elements e0 .. e0 + 7 (e0 % 8 == 0) of one block in LDS, decoded with the block's
+// header read once: they always share one scale (Q8_0 / Q4_0: the block's, Q4_K: one 32-element
+// sub-block's, Q6_K: one 16-element scale group's).  Same formulas and operand order as deq_elem; the
+// fp16 scales are converted by the hardware (exact for every finite value, subnormals included).
+__device__ inline uint32_t lds_u32_at(const uint8_t* p) {  // 4 bytes at any address, from aligned dwords
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(a & ~(uintptr_t)3);
+  return align_bytes(w[1], w[0], (uint32_t)(a & 3));
+}
+__device__ inline float f16at(const uint8_t* p) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);  // 2-byte aligned
+  const uint32_t w = *reinterpret_cast<const uint32_t*>(a & ~(uintptr_t)3);
+  return (a & 2) ? f16hi(w) : f16lo(w);
+}
+
+template <uint32_t T>
+__device__ inline void deq8(const uint8_t* b, int e0, float (&v)[8]) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) v[k] = deq_elem<T>(b, e0 + k);
+}
+template <>
+__device__ inline void deq8<T_Q8_0>(const uint8_t* b, int e0, float (&v)[8]) {
+  const float d = f16at(b);
+  const uint32_t w0 = lds_u32_at(b + 2 + e0), w1 = lds_u32_at(b + 6 + e0);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    v[k] = d * (float)(int8_t)(w0 >> (8 * k));
+    v[4 + k] = d * (float)(int8_t)(w1 >> (8 * k));
+  }
+}
+template <>
+__device__ inline void deq8<T_Q4_0>(const uint8_t* b, int e0, float (&v)[8]) {
+  const float d = f16at(b);
+  const int o = e0 & 15, sh = e0 < 16 ? 0 : 4;
+  const uint32_t w0 = lds_u32_at(b + 2 + o) >> sh, w1 = lds_u32_at(b + 6 + o) >> sh;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    v[k] = (float)((int)((w0 >> (8 * k)) & 15u) - 8) * d;
+    v[4 + k] = (float)((int)((w1 >> (8 * k)) & 15u) - 8) * d;
+  }
+}
+template <>
+__device__ inline void deq8<T_Q4_K>(const uint8_t* b, int e0, float (&v)[8]) {
+  const int c = e0 >> 6, l = e0 & 63, hi = l >> 5;
+  uint32_t sc, m;
+  k4_scale_min(2 * c + hi, b + 4, sc, m);
+  const float ds = f16at(b) * (float)sc;
+  const float dm = f16at(b + 2) * (float)m;
+  const int sh = hi ? 4 : 0;
+  const uint32_t* q = reinterpret_cast<const uint32_t*>(b + 16 + 32 * c + (l & 31));  // 4-byte aligned
+  const uint32_t w0 = q[0] >> sh, w1 = q[1] >> sh;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    v[k] = ds * (float)((w0 >> (8 * k)) & 15u) - dm;
+    v[4 + k] = ds * (float)((w1 >> (8 * k)) & 15u) - dm;
+  }
+}
+template <>
+__device__ inline void deq8<T_Q6_K>(const uint8_t* b, int e0, float (&v)[8]) {
+  const int h = e0 >> 7, p = e0 & 127, quarter = p >> 5, l = p & 31;
+  const uint32_t a0 = lds_u32_at(b + 64 * h + l + 32 * (quarter & 1));
+  const uint32_t a1 = lds_u32_at(b + 64 * h + l + 32 * (quarter & 1) + 4);
+  const uint32_t h0 = lds_u32_at(b + 128 + 32 * h + l), h1 = lds_u32_at(b + 128 + 32 * h + l + 4);
+  const int nsh = (quarter & 2) ? 4 : 0, hsh = 2 * quarter;
+  const float d = f16at(b + 208);
+  const float ds = d * (float)(int8_t)b[192 + 8 * h + (l >> 4) + 2 * quarter];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int q0 = (int)(((a0 >> (8 * k + nsh)) & 15u) | (((h0 >> (8 * k + hsh)) & 3u) << 4));
+    const int q1 = (int)(((a1 >> (8 * k + nsh)) & 15u) | (((h1 >> (8 * k + hsh)) & 3u) << 4));
+    v[k] = ds * (float)(q0 - 32);
+    v[4 + k] = ds * (float)(q1 - 32);
+  }
+}
+
+constexpr int kWideElems = 8192;  // elements per workgroup of the wide 16-bit dequantiser
+
+// A workgroup's 8192 elements are whole blocks; their bytes (a multiple of 16 in every block format at
+// this size) are copied from a 16-byte-aligned source into LDS with 16-byte loads (the tensor's last
+// bytes one at a time), then each thread decodes eight consecutive elements per round, four rounds,
+// and stores them as one 16-byte vector (a wave stores 1 KiB contiguous).  n: whole blocks.
+template <uint32_t T, int QK, int BB, bool BF>
+__global__ __launch_bounds__(256) void k_dequant16_wide(const uint8_t* __restrict__ src, uint4* __restrict__ dst,
+                                                        size_t n) {
+  constexpr int kBytes = kWideElems / QK * BB;
+  static_assert(kWideElems % QK == 0 && kBytes % 16 == 0, "workgroup span must be whole blocks and 16-byte units");
+  __shared__ __attribute__((aligned(16))) uint32_t sm[kBytes / 4 + 4];
+  const int tid = threadIdx.x;
+  const size_t b0 = (size_t)blockIdx.x * kBytes;
+  const size_t avail = min((size_t)kBytes, n / QK * BB - b0);
+  const uint4* g16 = reinterpret_cast<const uint4*>(src + b0);
+  for (int k = tid; k < (int)(avail / 16); k += 256) reinterpret_cast<uint4*>(sm)[k] = g16[k];
+  const int full = (int)(avail & ~(size_t)15);
+  if (tid < (int)(avail & 15)) reinterpret_cast<uint8_t*>(sm)[full + tid] = src[b0 + full + tid];
+  __syncthreads();
+  const uint8_t* sb = reinterpret_cast<const uint8_t*>(sm);
+#pragma unroll
+  for (int r = 0; r < kWideElems / 2048; ++r) {
+    const int e0 = r * 2048 + 8 * tid;
+    const size_t i = (size_t)blockIdx.x * kWideElems + e0;
+    if (i >= n) break;
+    float v[8];
+    deq8<T>(sb + (e0 / QK) * BB, e0 % QK, v);
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t lo = BF ? to_bf16(v[2 * j]) : to_f16(v[2 * j]);
+      const uint32_t hi = BF ? to_bf16(v[2 * j + 1]) : to_f16(v[2 * j + 1]);
+      w[j] = lo | (hi << 16);
+    }
+    dst[i / 8] = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+template <bool BF>
+bool launch_dequant16_wide(uint32_t t, const uint8_t* b, uint4* d8, size_t n, hipStream_t s) {
+  const unsigned grid = (unsigned)((n + kWideElems - 1) / kWideElems);
+  switch (t) {
+    case T_Q8_0: k_dequant16_wide<T_Q8_0, 32, 34, BF><<<grid, 256, 0, s>>>(b, d8, n); return true;
+    case T_Q4_0: k_dequant16_wide<T_Q4_0, 32, 18, BF><<<grid, 256, 0, s>>>(b, d8, n); return true;
+    case T_Q5_0: k_dequant16_wide<T_Q5_0, 32, 22, BF><<<grid, 256, 0, s>>>(b, d8, n); return true;
+    case T_Q4_K: k_dequant16_wide<T_Q4_K, 256, 144, BF><<<grid, 256, 0, s>>>(b, d8, n); return true;
+    case T_Q5_K: k_dequant16_wide<T_Q5_K, 256, 176, BF><<<grid, 256, 0, s>>>(b, d8, n); return true;
+    case T_Q6_K: k_dequant16_wide<T_Q6_K, 256, 210, BF><<<grid, 256, 0, s>>>(b, d8, n); return true;
+    default: return false;
+  }
+}
+
 template <bool BF>
 bool launch_dequant16_lds(uint32_t t, const uint8_t* b, uint4* d8, size_t n, hipStream_t s) {
   const unsigned grid = (unsigned)((n + kStageElems - 1) / kStageElems);
@@ -218,6 +347,11 @@ bool launch_dequant16_t(uint32_t t, const void* src, uint16_t* dst, size_t n, hi
   const auto* b = static_cast<const uint8_t*>(src);
   // block types over whole blocks: the LDS-staged kernel (source 4-byte, destination 16-byte aligned)
   const size_t qk = (t == T_Q4_K || t == T_Q5_K || t == T_Q6_K) ? 256 : 32;
+  // the wide kernel: 16-byte-aligned source and destination
+  if (t != T_F32 && t != T_F16 && t != T_BF16 && n % qk == 0 && (reinterpret_cast<uintptr_t>(src) & 15u) == 0 &&
+      (reinterpret_cast<uintptr_t>(dst) & 15u) == 0 &&
+      launch_dequant16_wide<BF>(t, b, reinterpret_cast<uint4*>(dst), n, s))
+    return true;
   if (t != T_F32 && t != T_F16 && t != T_BF16 && n % qk == 0 && (reinterpret_cast<uintptr_t>(src) & 3u) == 0 &&
       (reinterpret_cast<uintptr_t>(dst) & 15u) == 0 &&
       launch_dequant16_lds<BF>(t, b, reinterpret_cast<uint4*>(dst), n, s))

@@ -8,7 +8,10 @@
 // once); the semantics are qmatmulN's (runtime/src/qmatmul.cpp:64-115) with X converted fp16 -> fp32
 // exactly.  The reference has no GEMM (it prefills token by token).
 //
-// Workgroup = 512 threads, 8 waves, a BM x 256 output tile (BM = 256 or 128 tokens x 256 weight rows).
+// Two kernels: k_gemm16q (below), 256 threads on 256-token x 256-row tiles, for grids that fill the
+// chip; and k_gemm16, 8 waves on 128-token tiles with a K split, for the smaller grids.
+//
+// k_gemm16: workgroup = 512 threads, 8 waves, a BM x 256 output tile (BM = 256 or 128 tokens x 256 weight rows).
 // Wave w owns weight rows 64 (w % 4) .. +63 and tokens (BM / 2) (w / 4) .. + BM/2 - 1:
 // 2 x BM/64 tiles of v_mfma_f32_32x32x16_{bf16,f16}, accumulators in registers.
 // K advances in slices of KS elements (32 at BM = 256, 64 at BM = 128); both operands of a slice are
@@ -105,6 +108,15 @@ __device__ inline f32x16_t mfma32(const u32x4& a, const u32x4& b, f32x16_t c) {
 // Waits for every LDS read in flight; the fragments are operands, so no MFMA moves above the wait.
 template <int NF>
 __device__ inline void lds_wait_all(u32x4 (&f)[NF]);
+template <>
+__device__ inline void lds_wait_all<6>(u32x4 (&f)[6]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5])::"memory");
+}
+template <>
+__device__ inline void lds_wait_all<8>(u32x4 (&f)[8]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]), "+v"(f[6]), "+v"(f[7])::"memory");
+}
 template <>
 __device__ inline void lds_wait_all<12>(u32x4 (&f)[12]) {
   asm volatile("s_waitcnt lgkmcnt(0)"
@@ -293,6 +305,174 @@ __global__ __launch_bounds__(512) void k_gemm16(const uint16_t* __restrict__ X, 
   }
 }
 
+// ---- 4-wave form: one wave per SIMD, 128 x 128 wave tiles ------------------------------------------
+// k_gemm16q<VAR, BM, KS, NST>: a BM-token x 256-row tile per 256-thread workgroup; wave w owns tokens
+// (BM / 2) (w / 2) .. + BM/2 - 1 and weight rows 128 (w % 2) .. +127 (BM / 64 x 4 tiles of
+// v_mfma_f32_32x32x16_*; at BM = 256, 256 accumulators held in the accumulation registers).  The
+// product runs BM = 256; at BM = 128 this form measured 3-8 % slower than the 8-wave kernel on the
+// same tiles, which therefore keeps the 128-token tiles.  Per K16 step a wave reads 8 fragments (8 KiB) for
+// 16 MFMAs, two thirds of the LDS traffic per MFMA of the 8-wave form's 64 x 128 wave tiles.  K
+// advances in KS-element slices through NST stages (X rows, then B rows, KS * 2 bytes a row, the
+// 8-wave form's layout and swizzles), each filled by buffer_load ... lds NST - 1 slices ahead.  The
+// product path runs KS = 64 with two 64 KiB stages: a copy then moves whole 128-byte lines of a row
+// (32-element slices read each line twice, in two slices, and measured 10 % slower on MI355X at
+// 2048 x 14336 x 4096 even with four or five stages).  The wave software-pipelines itself: while the
+// 16 MFMAs of one step issue, the fragment reads of the next step issue between them (and, in a
+// slice's last step, the copies of slice j + NST and the first reads of slice j + 1), so the matrix
+// pipe waits on LDS only when a read is late.  One barrier per slice, before its last step: every
+// wave has then read the whole slice (the last step's fragments are in registers), so the slice's
+// stage is refilled during that step, and each wave has waited for its copies of slice j + 1 before
+// it.  The K order of the products is the 8-wave form's (K16 steps in order into each accumulator),
+// so both forms give the same bits.
+template <int VAR, int BM, int KS, int NST>
+__global__ __launch_bounds__(256) void k_gemm16q(const uint16_t* __restrict__ X, const uint16_t* __restrict__ B,
+                                                 float* __restrict__ Y, Geo geo) {
+  constexpr int RB = KS * 2, CPR = KS / 8;
+  constexpr int XST = BM * RB;           // X part of a stage
+  constexpr int STB = XST + kBN * RB;    // one stage: X rows, then B rows
+  constexpr int CPS = STB / 1024 / 4;    // 1 KiB copies per wave per slice
+  constexpr int XC = XST / 1024;         // copies of a slice that move X
+  constexpr int ST = KS / 16;            // K16 steps a slice
+  constexpr int TM = BM / 64;            // 32-token tiles of a wave (it covers BM / 2 tokens)
+  constexpr int NF = TM + 4;             // fragments a step: TM of X, 4 of B
+  constexpr int NS = 4 * TM;             // MFMAs a step
+  constexpr int YOUNG = (NST - 2) * CPS;
+  static_assert(NST >= 2 && NST * STB <= 160 * 1024, "LDS budget");
+  static_assert(ST % 2 == 0 && (BM == 128 || BM == 256), "tile shape");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NST * STB];
+  const int M = geo.M, N = geo.N, K = geo.K;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int ln = lane & 31, g = lane >> 5;
+  int tile;
+  {
+    const int nb = (int)gridDim.x;
+    int b = (int)blockIdx.x;
+    if ((nb & 7) == 0) b = (b & 7) * (nb >> 3) + (b >> 3);  // XCD b % 8 takes a contiguous range
+    tile = b;
+  }
+  const int n0 = (tile / geo.mt) * kBN, m0 = (tile % geo.mt) * BM;
+  const int kb0 = 0, L = K / KS;  // no K split: the plan runs this kernel on grids that fill the chip
+  if (m0 >= M || n0 >= N) return;
+  const uint32_t row_bytes = (uint32_t)K * 2u;
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(X + (size_t)m0 * K), (short)0, (int)((uint32_t)min(BM, M - m0) * row_bytes), (int)kRsrcWord3);
+  const __amdgpu_buffer_rsrc_t br = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(B + (size_t)n0 * K), (short)0, (int)((uint32_t)min(kBN, N - n0) * row_bytes), (int)kRsrcWord3);
+  // Copy i of this wave moves 1 KiB of a stage: c = wave * CPS + i, chunk q = 64 (c mod X / B) + lane
+  // -> row q / CPR, LDS slot q % CPR holds global chunk slot ^ swz(row).  c < XC: X rows, else B rows.
+  uint32_t voff[CPS];
+  bool isx[CPS];
+#pragma unroll
+  for (int i = 0; i < CPS; ++i) {
+    const int c = wave * CPS + i;
+    isx[i] = c < XC;
+    const uint32_t q = (uint32_t)((isx[i] ? c : c - XC) * 64 + lane), r = q / CPR, p = q % CPR;
+    voff[i] = r * row_bytes + 16u * (p ^ swz<CPR>(r));
+  }
+  QVX_LDS uint8_t* lds_l = (QVX_LDS uint8_t*)lds;
+  const uint32_t lds_base = (uint32_t)(uintptr_t)lds_l;
+  auto copy1 = [&](int j, int i) {  // copy i of slice j (relative to kb0)
+    QVX_LDS uint8_t* st = lds_l + (j % NST) * STB + (wave * CPS + i) * 1024;
+    copy_lds16(isx[i] ? xr : br, st, voff[i], (uint32_t)(kb0 + j) * (uint32_t)RB);
+  };
+  uint32_t frel[ST];
+#pragma unroll
+  for (int s = 0; s < ST; ++s) frel[s] = (uint32_t)ln * RB + 16u * ((2u * s + (uint32_t)g) ^ swz<CPR>((uint32_t)ln));
+  const uint32_t xw = (uint32_t)(wm * (BM / 2)) * RB;
+  const uint32_t bw = (uint32_t)XST + (uint32_t)(wn * 128) * RB;
+  // Fragment k of step s of slice j: X tiles 0 .. TM - 1, then B tiles 0 .. 3.
+  auto read1 = [&](int j, int s, int k) -> u32x4 {
+    const bool isa = k < TM;
+    const int t = isa ? k : k - TM;
+    const uint32_t st = lds_base + (uint32_t)(j % NST) * STB + frel[s] + (isa ? xw : bw);
+    switch (t) {
+      case 0: return lds_read16<0>(st);
+      case 1: return lds_read16<32 * RB>(st);
+      case 2: return lds_read16<64 * RB>(st);
+      default: return lds_read16<96 * RB>(st);
+    }
+  };
+  f32x16_t acc[TM][4];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][n][e] = 0.0f;
+  u32x4 f[2][NF];
+#pragma unroll
+  for (int j = 0; j < NST; ++j)
+    if (j < L)
+#pragma unroll
+      for (int i = 0; i < CPS; ++i) copy1(j, i);
+  if (L >= NST)
+    wait_vm<(NST - 1) * CPS>();
+  else
+    wait_vm<0>();
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int k = 0; k < NF; ++k) f[0][k] = read1(0, 0, k);
+  lds_wait_all<NF>(f[0]);
+  // One slice; REFILL: the copies of slice j + NST are issued, MORE: slice j + 1 follows.  In every
+  // step but the last the next step's fragments are read between the MFMAs; the barrier follows the
+  // step before the last, and the last step issues the copies of slice j + NST (spread evenly) and the
+  // first fragments of slice j + 1 (in its second half).
+  auto slice = [&]<bool REFILL, bool MORE>(int j) {
+#pragma unroll
+    for (int s = 0; s < ST; ++s) {
+      u32x4(&cur)[NF] = f[s & 1];
+      u32x4(&nxt)[NF] = f[(s + 1) & 1];
+      const bool last = s == ST - 1;
+#pragma unroll
+      for (int k = 0; k < NS; ++k) {
+        acc[k >> 2][k & 3] = mfma32<VAR>(cur[k >> 2], cur[TM + (k & 3)], acc[k >> 2][k & 3]);
+        if (!last) {
+          if (k < NF) nxt[k] = read1(j, s + 1, k);
+        } else {
+          if constexpr (REFILL)
+#pragma unroll
+            for (int i = 0; i < CPS; ++i)
+              if (i * NS / CPS == k) copy1(j + NST, i);
+          if constexpr (MORE)
+#pragma unroll
+            for (int r = 0; r < NF; ++r)
+              if (NS / 2 + r * (NS / 2) / NF == k) nxt[r] = read1(j + 1, 0, r);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (!last || MORE) lds_wait_all<NF>(nxt);
+      if (s == ST - 2) {
+        if (j + NST - 1 < L)
+          wait_vm<YOUNG>();
+        else
+          wait_vm<0>();
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+  int j = 0;
+  for (; j + NST < L; ++j) slice.template operator()<true, true>(j);
+  for (; j + 1 < L; ++j) slice.template operator()<false, true>(j);
+  slice.template operator()<false, false>(j);
+
+#pragma unroll
+  for (int n = 0; n < 4; ++n) {
+    const int col = n0 + 128 * wn + 32 * n + ln;
+    if (col >= N) continue;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = m0 + (BM / 2) * wm + 32 * i + 8 * (e >> 2) + 4 * g + (e & 3);
+        if (m < M) Y[(size_t)m * geo.ldy + col] = acc[i][n][e];
+      }
+  }
+}
+
 // ---- operand preparation --------------------------------------------------------------------------
 // X fp16 [M, K] -> 16-bit [M, Kp] (fp16 as is, or rounded to bf16), zero columns K .. Kp - 1: for
 // calls whose K is not a multiple of the slice or whose X is not 16-byte aligned.  One thread per
@@ -363,39 +543,60 @@ inline int cdiv(int a, int b) { return (a + b - 1) / b; }
 
 int device_cus();
 
-// Launch plan of k_gemm16 for M x N x K (K a multiple of 64): BM = 256 tokens (KS 32) when the
-// 256-token grid fills most of the chip, else 128 tokens (KS 64) with a K split while the grid is
-// below ~200 workgroups and each split keeps >= 8 slices.
+// Launch plan for M x N x K (K a multiple of 64): one or two launches over consecutive columns of 256
+// weight rows.  A part runs 256-token tiles on the 4-wave kernel (k_gemm16q) or 128-token tiles on
+// the 8-wave kernel (k_gemm16, 64-element slices); only a single 128-token part splits K (while its
+// grid is below ~200 workgroups and each split keeps >= 8 slices).  The parts are chosen by rounds of
+// workgroups times tile time, a 128-token tile costing 0.65 of a 256-token one (measured on MI355X:
+// 63-65 us for one round of 128-token tiles at K = 4096, ~100 us a round of 256-token tiles): e.g.
+// 2048 x 11008 runs one full round of 256-token tiles over 32 columns and the other 11 columns as
+// one round of 128-token tiles (1.65 rounds of 256-token tile time, where a uniform grid takes 2).
+struct G16Part {
+  int bm, col0, ncols, mt, ntiles, splits, per;
+};
 struct G16Plan {
-  int bm, ks, mt, ntiles, splits, per;
+  int n;
+  G16Part p[2];
 };
 
 G16Plan gemm16_plan(int M, int N, int K, int cus, int max_splits = 64) {
-  G16Plan p{};
-  const int nt = cdiv(N, kBN);
-  if (nt * cdiv(M, 256) >= 200 * cus / 256) {
-    p.bm = 256;
-    p.ks = 32;
-  } else {
-    p.bm = 128;
-    p.ks = 64;
+  const int nt = cdiv(N, kBN), nsl = K / 64;
+  const int m256 = cdiv(M, 256), m128 = cdiv(M, 128);
+  auto rounds = [&](int tiles) { return (double)cdiv(tiles, cus); };
+  constexpr double kT128 = 0.65;
+  G16Plan pl{};
+  pl.n = 1;
+  // uniform 128-token tiles, K split while the grid is small
+  G16Part q{128, 0, nt, m128, nt * m128, 1, nsl};
+  while (q.ntiles * q.splits < 200 * cus / 256 && nsl / (q.splits * 2) >= 8 && q.splits * 2 <= max_splits)
+    q.splits *= 2;
+  q.per = cdiv(nsl, q.splits);
+  q.splits = cdiv(nsl, q.per);
+  pl.p[0] = q;
+  double best = rounds(q.ntiles * q.splits) * kT128 / q.splits + (q.splits > 1 ? 0.02 : 0.0);
+  // uniform 256-token tiles
+  if (const double c = rounds(nt * m256); c < best - 1e-9) {
+    best = c;
+    pl.p[0] = G16Part{256, 0, nt, m256, nt * m256, 1, nsl};
   }
-  p.mt = cdiv(M, p.bm);
-  p.ntiles = nt * p.mt;
-  const int nsl = K / p.ks;
-  p.splits = 1;
-  if (p.bm == 128)
-    while (p.ntiles * p.splits < 200 * cus / 256 && nsl / (p.splits * 2) >= 8 && p.splits * 2 <= max_splits)
-      p.splits *= 2;
-  p.per = cdiv(nsl, p.splits);
-  p.splits = cdiv(nsl, p.per);
-  return p;
+  // 256-token tiles on the first c1 columns, 128-token tiles on the rest
+  for (int c1 = 1; c1 < nt; ++c1) {
+    const double c = rounds(c1 * m256) + rounds((nt - c1) * m128) * kT128 + 0.03;
+    if (c < best - 1e-9) {
+      best = c;
+      pl.n = 2;
+      pl.p[0] = G16Part{256, 0, c1, m256, c1 * m256, 1, nsl};
+      pl.p[1] = G16Part{128, c1, nt - c1, m128, (nt - c1) * m128, 1, nsl};
+    }
+  }
+  return pl;
 }
 
 // Bytes of a plan's K-split workspace (partial tiles, then the counters, whose size *cbytes is
 // 256-byte aligned); 0 without a split.
-size_t gemm16_split_bytes(const G16Plan& p, size_t* cbytes) {
-  if (p.splits <= 1) {
+size_t gemm16_split_bytes(const G16Plan& pl, size_t* cbytes) {
+  const G16Part& p = pl.p[0];
+  if (pl.n != 1 || p.splits <= 1) {
     *cbytes = 0;
     return 0;
   }
@@ -403,26 +604,33 @@ size_t gemm16_split_bytes(const G16Plan& p, size_t* cbytes) {
   return (size_t)p.ntiles * p.splits * p.bm * kBN * 4 + *cbytes;
 }
 
-// Launches the GEMM of plan p; split_ws: gemm16_split_bytes(p) bytes, counters (its last cbytes)
+// Launches the GEMM of plan pl; split_ws: gemm16_split_bytes(pl) bytes, counters (its last cbytes)
 // zero.  X and B rows are K 16-bit values (K % 64 == 0), both 16-byte aligned.
-bool launch_gemm16(const G16Plan& p, float* out, int ldy, const uint16_t* X, const uint16_t* B, int M, int N, int K,
+bool launch_gemm16(const G16Plan& pl, float* out, int ldy, const uint16_t* X, const uint16_t* B, int M, int N, int K,
                    bool bf16, void* split_ws, hipStream_t s) {
   size_t cb = 0;
-  const size_t sb = gemm16_split_bytes(p, &cb);
+  const size_t sb = gemm16_split_bytes(pl, &cb);
   if (sb && !split_ws) return false;
-  Geo geo{M, N, K, ldy, p.mt, p.per, sb ? static_cast<float*>(split_ws) : nullptr,
-          sb ? reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(split_ws) + sb - cb) : nullptr};
-  const dim3 grid((unsigned)p.ntiles, 1, (unsigned)p.splits);
-  if (p.bm == 256) {
-    if (bf16)
-      k_gemm16<VAR_BF16, 256, 32><<<grid, 512, 0, s>>>(X, B, out, geo);
-    else
-      k_gemm16<VAR_F16, 256, 32><<<grid, 512, 0, s>>>(X, B, out, geo);
-  } else {
-    if (bf16)
-      k_gemm16<VAR_BF16, 128, 64><<<grid, 512, 0, s>>>(X, B, out, geo);
-    else
-      k_gemm16<VAR_F16, 128, 64><<<grid, 512, 0, s>>>(X, B, out, geo);
+  for (int i = 0; i < pl.n; ++i) {
+    const G16Part& p = pl.p[i];
+    const int r0 = p.col0 * kBN, nr = std::min(N - r0, p.ncols * kBN);
+    if (nr <= 0) continue;
+    Geo geo{M, nr, K, ldy, p.mt, p.per, sb ? static_cast<float*>(split_ws) : nullptr,
+            sb ? reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(split_ws) + sb - cb) : nullptr};
+    const uint16_t* Bp = B + (size_t)r0 * K;
+    float* op = out + r0;
+    const dim3 grid((unsigned)p.ntiles, 1, (unsigned)p.splits);
+    if (p.bm == 256) {
+      if (bf16)
+        k_gemm16q<VAR_BF16, 256, 64, 2><<<grid, 256, 0, s>>>(X, Bp, op, geo);
+      else
+        k_gemm16q<VAR_F16, 256, 64, 2><<<grid, 256, 0, s>>>(X, Bp, op, geo);
+    } else {
+      if (bf16)
+        k_gemm16<VAR_BF16, 128, 64><<<grid, 512, 0, s>>>(X, Bp, op, geo);
+      else
+        k_gemm16<VAR_F16, 128, 64><<<grid, 512, 0, s>>>(X, Bp, op, geo);
+    }
   }
   return true;
 }

@@ -5,9 +5,8 @@ k_gemm16.
 qvx_gemm16 is checked on exactly representable operands: X and B are 16-bit values, so the exact
 product is the fp64 sum of their fp32 values, and the only error left is fp32 accumulation (bar 1e-4
 max-relative: a transposed operand, a wrong K chunk or a misplaced tile is off by O(1)).  The shapes
-take both tile kernels (256-token tiles with 32-element slices, 128-token tiles with 64-element
-slices), ragged M and N, a K split, K not a multiple of 64 and unaligned operands (zero-padded
-copies).  The prefill route is held to the GEMM bar of the fp64 oracle at the BASELINE Q8_0 / Q4_0
+take both tile kernels (the 4-wave kernel on 256-token tiles, the 8-wave kernel on 128-token tiles),
+ragged M and N, a K split, K not a multiple of 64 and unaligned operands (zero-padded copies).  The prefill route is held to the GEMM bar of the fp64 oracle at the BASELINE Q8_0 / Q4_0
 shapes (a row slice), and its 16-bit weight to the oracle's dequantised value rounded once.
 """
 from __future__ import annotations
@@ -53,8 +52,9 @@ def _gemm16(cuda, Xb, Bb, variant, x_off=0, b_off=0):
 
 @pytest.mark.parametrize("variant", [qvx.GEMM_BF16, qvx.GEMM_F16])
 @pytest.mark.parametrize("M,N,K,x_off,b_off", [
-    (1900, 6500, 128, 0, 0),    # 256-token tiles (26 x 8 = 208 tiles), ragged last tile in M and N
-    (300, 520, 192, 0, 0),      # 128-token tiles, ragged, three 64-element slices
+    (1900, 6500, 128, 0, 0),    # 4-wave kernel (26 x 8 = 208 tiles), ragged last tile in M and N
+    (300, 520, 192, 0, 0),      # 8-wave kernel, ragged, three 64-element slices
+    (2048, 11000, 128, 0, 0),   # two launches: 32 columns of 256-token tiles, 11 of 128-token tiles
     (128, 512, 2048, 0, 0),     # 2 tiles: four K splits of 8 slices, summed in split order
     (70, 100, 100, 0, 0),       # K not a multiple of 64: zero-padded copies of both operands
     (64, 256, 512, 2, 6),       # operands off 16-byte alignment: padded copies
@@ -134,3 +134,34 @@ def test_prefill_via16_config_shapes(cuda, t, rows, cols, M):
         cuda.cuda.synchronize()
         got2 = out2.cpu().numpy()
         assert max_rel(got2[:, idx], ref) <= GEMM_TOL, variant
+
+
+@pytest.mark.parametrize("bf16", [True, False])
+def test_dequantize16_scale_edge_values(cuda, bf16):
+    """16-bit dequantisation with fp16 scales at their extremes (subnormal, smallest normal, max,
+    negative, signed zero) and extreme quants, against the oracle's value rounded once (fp16 overflow to
+    Inf included).  The tensors end in a partial workgroup span, and Q8_0 / Q6_K in a span whose byte
+    count is not a multiple of 16."""
+    from test_gpu_kernels import dev
+    specials = [0x0001, 0x03FF, 0x0400, 0x7BFF, 0x8001, 0xFBFF, 0x0000, 0x8000, 0x3C00]
+    rng = np.random.default_rng(6)
+    blocks = []
+    for d in specials:
+        for dm in specials:
+            b = rng.integers(0, 256, 144, dtype=np.uint8)
+            b[0], b[1], b[2], b[3] = d & 0xFF, d >> 8, dm & 0xFF, dm >> 8
+            blocks.append(b)
+    cases = [(qvx.Q4_K, np.concatenate(blocks), len(blocks) * 256)]
+    for t, off, bb, qk in ((qvx.Q6_K, 208, 210, 256), (qvx.Q8_0, 0, 34, 32), (qvx.Q4_0, 0, 18, 32)):
+        blocks = []
+        for d in specials:
+            for fill in (0x00, 0xFF, 0x80, 0x7F):
+                b = np.full(bb, fill, np.uint8)
+                b[off], b[off + 1] = d & 0xFF, d >> 8
+                blocks.append(b)
+        cases.append((t, np.concatenate(blocks), len(blocks) * qk))
+    for t, w, n in cases:
+        got = qvx.dequantize16_t(dev(cuda, w), t, n, bf16).cpu().numpy().view(np.uint16)
+        with np.errstate(over="ignore"):
+            want, _ = _bits16(oracle.dequantize(t, w, n).astype(np.float32), bf16)
+        np.testing.assert_array_equal(got, want, err_msg=f"type {t}")
