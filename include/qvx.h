@@ -10,11 +10,15 @@
  * Conventions
  *  - `type` is the raw on-disk ggml type id (Q4_0 = 2, Q8_0 = 8, Q4_K = 12, Q6_K = 14, F32 = 0, ...).
  *  - Every call returns QVX_OK (0) or a negative QVX_E_* code.  All argument checks run before any
- *    device work, so `out` is untouched on failure -- the reference's `false` cases map one for one:
+ *    device work, so `out` is untouched on a check's failure (QVX_E_TYPE, _SHAPE, _NVEC, _NULL,
+ *    _VARIANT, _RANGE) -- the reference's `false` cases map one for one:
  *      unknown / unsupported type        -> QVX_E_TYPE   (qmatmul.cpp:30-31)
  *      blockSize > 256 or cols % bs != 0 -> QVX_E_SHAPE  (qmatmul.cpp:32-33, :70-72)
  *      n_vec <= 0                        -> QVX_E_NVEC   (qmatmul.cpp:66)
  *    rows <= 0 is a successful no-op and cols == 0 writes zeros, as the reference's loops do.
+ *    QVX_E_HIP reports a runtime failure after the checks passed (a launch the runtime refused, a
+ *    failed allocation or copy); calls that issue several launches (a batch in chunks of vectors, a
+ *    GEMM in panels) may then have written part of `out`, whose contents are unspecified.
  *  - Device entry points take device pointers and a hipStream_t passed as `void*` (NULL = the
  *    null stream).  They are asynchronous and stream-ordered, like the CUDA backend's matmulS
  *    launch (cuda/src/cuda_backend.cu:1534-1542).  They allocate no device memory, except
@@ -83,14 +87,34 @@ float qvx_bf16_to_float(uint16_t b);
 /* ---- device entry points (device pointers, stream-ordered) --------------------------------- */
 
 /* out[r] = dot(dequant(row r of W), x), r < rows.  Replaces qmatmul (qmatmul.cpp:28-62).
- * fp32 accumulation; within max|y-ref|/max|ref| <= 1e-3 of the exact sum. */
+ * fp32 accumulation; within max|y-ref|/max|ref| <= 1e-3 of the exact sum.  The quantised-weight
+ * kernels convert x per 64-element slot to 15-bit fixed point scaled by the slot's largest |x|, so an
+ * element's conversion error is at most 3.1e-5 of that maximum (outlier channels of 1000x the typical
+ * magnitude stay within the bar).  A non-finite activation makes its slot's step NaN: every output is
+ * then NaN exactly where the reference's fp32 sum is non-finite (where the reference gives +-Inf, the
+ * engine gives NaN). */
 int qvx_qmatmul(float* d_out, const void* d_w, uint32_t type, const float* d_x, int rows, int cols,
                 void* stream);
 
 /* out[v * rows + r] for v < n_vec.  Replaces qmatmulN (qmatmul.cpp:64-115).  Each output is
- * bit-identical to qvx_qmatmul on that vector, as the reference promises (qmatmul.hpp:31-32). */
+ * bit-identical to qvx_qmatmul on that vector, as the reference promises (qmatmul.hpp:31-32).
+ * Q4_K batches of 16 vectors or more on the one-vector kernel's shapes (cols a multiple of 256 up to
+ * 32768, aligned operands) run on a many-vector form: the activations are converted once into a
+ * stream-ordered temporary from the library's pool (nvec * cols * 2.25 bytes), then the weights are
+ * streamed once per 64 vectors -- the reference's "dequantize each block once for all nVec dot
+ * products" (qmatmul.hpp:24-32); smaller batches stream them once per 8 vectors and allocate
+ * nothing.  Calls recorded in a plan never take the many-vector form (a replay allocates nothing). */
 int qvx_qmatmul_n(float* d_out, const void* d_w, uint32_t type, const float* d_X, int n_vec,
                   int rows, int cols, void* stream);
+
+/* out[v * rows + r] = (W . X[v])[r] + bias[r] (d_bias [rows] fp32; NULL: no bias, exactly
+ * qvx_qmatmul_n): the reference's wmatmulBias / wmatmulNBias (runtime/include/qorvix/runtime/
+ * weights.hpp:58-80), the bias added after the product in fp32, so each output is the bit pattern of
+ * qvx_qmatmul_n's output plus bias[r].  The arguments and checks of qvx_qmatmul_n.  Q4_K batches of
+ * 16 vectors or more run on the many-vector form (below), which adds the bias in its epilogue; other
+ * calls run the product, then one bias-add launch. */
+int qvx_qmatmul_n_bias(float* d_out, const void* d_w, uint32_t type, const float* d_X, const float* d_bias,
+                       int n_vec, int rows, int cols, void* stream);
 
 /* Dequantise the first n / blockSize whole blocks of `type` to fp32, bit-exact with the reference's
  * dequantize (dequant.cpp:277-296) for every value but NaN payloads.  As there, n is not required

@@ -46,6 +46,7 @@ SIGNATURES = {
     "qvx_bf16_to_float": ([C.c_uint16], _f32),
     "qvx_qmatmul": ([_vp, _vp, _u32, _vp, _i32, _i32, _vp], _i32),
     "qvx_qmatmul_n": ([_vp, _vp, _u32, _vp, _i32, _i32, _i32, _vp], _i32),
+    "qvx_qmatmul_n_bias": ([_vp, _vp, _u32, _vp, _vp, _i32, _i32, _i32, _vp], _i32),
     "qvx_qmatmul_n_rmsnorm": ([_vp, _vp, _u32, _vp, _vp, _f32, _i32, _i32, _i32, _vp], _i32),
     "qvx_qmatmul_group": ([_vp, _vp, _vp, _vp, _i32, _vp, _vp, _f32, _i32, _vp], _i32),
     "qvx_qmatmul_swiglu": ([_vp, _vp, _u32, _vp, _vp, _f32, _i32, _i32, _i32, _vp], _i32),
@@ -214,6 +215,13 @@ def qmatmul_group(outs, weights, types, rows, x: int, cols: int, stream: int = 0
     arr = C.c_void_p * max(n, 1)
     return lib().qvx_qmatmul_group(arr(*outs), arr(*weights), (C.c_uint32 * max(n, 1))(*types),
                                    (C.c_int32 * max(n, 1))(*rows), n, x, norm_w or None, eps, cols, stream)
+
+
+def qmatmul_n_bias(out: int, weight: int, ggml_type: int, X: int, bias: int, nvec: int, rows: int, cols: int,
+                   stream: int = 0) -> int:
+    """wmatmulNBias (runtime/include/qorvix/runtime/weights.hpp:68-80) on device pointers: the product
+    plus bias[rows] (bias 0 = no bias). Status."""
+    return lib().qvx_qmatmul_n_bias(out, weight, ggml_type, X, bias, nvec, rows, cols, stream)
 
 
 def qmatmul_n_rmsnorm(out: int, weight: int, ggml_type: int, X: int, norm_w: int, eps: float, nvec: int, rows: int,

@@ -60,6 +60,11 @@ int launch_quantize_act_q8(const uint16_t* X, int M, int K, int8_t* q, float* sc
                            hipStream_t s);
 void launch_zero(float* p, size_t n, hipStream_t s);
 bool launch_gemv_group(const GemvMember* m, int n, const float* X, int cols, const GemvEpi& epi, hipStream_t s);
+size_t gemv_many_ws_bytes(int nvec, int cols);
+int gemv_many_supported(int cols, size_t row_bytes);
+bool launch_gemv_q4k_many(const void* w, const float* X, float* Y, const float* bias, int nvec, int rows, int cols,
+                          size_t row_bytes, void* ws, hipStream_t s);
+void launch_add_bias(float* out, const float* bias, int nvec, int rows, hipStream_t s);
 }  // namespace qvx
 
 using namespace qvx;
@@ -137,6 +142,9 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 // Q4_K: the vector count a chunk may have on the one-vector matrix-core kernel before the batched
 // forms take over (measured faster there), and whether the whole-row batched form takes the row.
+// Smallest Q4_K batch the many-vector form takes (measured crossover with the chunked forms).
+constexpr int kManyMin = 16;
+
 inline int q4k_small(int cols) { return std::min(gemv_mxb_supported(cols) ? 3 : 2, gemv_mx_max_nv(cols)); }
 
 // 1 if the routing below sends every chunk of this call to a kernel that folds `epi` in.
@@ -199,6 +207,7 @@ int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int
   const int nout = epi.swiglu ? rows / 2 : rows;
   if (cols <= 0) {  // no columns: every dot product is empty (the reference writes 0.0f; silu(0) * 0 = 0)
     launch_zero(out, (size_t)nout * (size_t)nvec, s);
+    if (epi.bias) launch_add_bias(out, epi.bias, nvec, rows, s);
     return hip_status();
   }
   if (!w || !X) return QVX_E_NULL;
@@ -206,6 +215,27 @@ int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int
   const bool fast = aligned16(w) && aligned16(X) && row_bytes % 16 == 0;
   if (epi.flags() && !fused_route(type, nvec, rows, cols, row_bytes, fast, epi))
     return gemv_unfused(out, w, type, X, nvec, rows, cols, s, epi);
+  // Q4_K batches of kManyMin vectors or more (encoder and prefill sizes): activations converted once,
+  // the weights streamed once per 64 vectors, bit-identical per vector to the one-vector kernel
+  // (k_gemv_q4k_many), with the bias added in its epilogue.  It takes a stream-ordered workspace, so
+  // graph-captured plans (no_alloc) keep the chunked forms below.
+  if (fast && type == T_Q4_K && !epi.flags() && !epi.no_alloc && nvec >= kManyMin &&
+      gemv_many_supported(cols, row_bytes)) {
+    void* ws = gemm_temp_alloc(gemv_many_ws_bytes(nvec, cols), s);
+    if (ws) {
+      const bool ok = launch_gemv_q4k_many(w, X, out, epi.bias, nvec, rows, cols, row_bytes, ws, s);
+      gemm_temp_free(ws, s);
+      if (!ok) return refused();
+      return hip_status();
+    }
+  }
+  if (epi.bias) {  // every other route: the plain product, then the bias add
+    GemvEpi plain = epi;
+    plain.bias = nullptr;
+    if (int rc = gemv(out, w, type, X, nvec, rows, cols, s, plain); rc != QVX_OK) return rc;
+    launch_add_bias(out, epi.bias, nvec, rows, s);
+    return hip_status();
+  }
   // Unquantised weights stream through the float kernel.
   if (fast && (type == T_F32 || type == T_F16 || type == T_BF16) &&
       launch_gemv_float(type, w, X, out, nvec, rows, cols, row_bytes, s))
@@ -274,24 +304,17 @@ struct DeviceGuard {
   }
 };
 
-// Device buffer reused by the synchronous host-pointer entry points (one per calling thread).
+// Device staging of the synchronous host-pointer entry points: a stream-ordered block of the library's
+// memory pool on the null stream (the stream their synchronous copies run on), returned to the pool
+// when the call ends.  No per-thread state, so nothing is freed from a thread-exit destructor while
+// the HIP runtime may already be tearing down.
 struct HostStage {
   void* p = nullptr;
-  size_t cap = 0;
-  ~HostStage() {
-    if (p) (void)hipFree(p);
-  }
-  void* get(size_t n) {
-    if (n <= cap) return p;
-    if (p) (void)hipFree(p);
-    p = nullptr;
-    cap = 0;
-    if (hipMalloc(&p, n) != hipSuccess) return nullptr;
-    cap = n;
-    return p;
-  }
+  explicit HostStage(size_t n) : p(gemm_temp_alloc(n, nullptr)) {}
+  ~HostStage() { gemm_temp_free(p, nullptr); }
+  HostStage(const HostStage&) = delete;
+  HostStage& operator=(const HostStage&) = delete;
 };
-thread_local HostStage g_stage;
 
 inline size_t align_up(size_t n) { return (n + 255) & ~size_t(255); }
 
@@ -427,6 +450,13 @@ int qvx_qmatmul_group(float* const* d_out, const void* const* d_w, const uint32_
   epi.norm_w = d_norm_w;
   epi.eps = eps;
   return k ? gemv_group(m, k, d_x, cols, epi, as_stream(stream)) : QVX_OK;
+}
+
+int qvx_qmatmul_n_bias(float* d_out, const void* d_w, uint32_t type, const float* d_X, const float* d_bias,
+                       int n_vec, int rows, int cols, void* stream) {
+  GemvEpi epi;
+  epi.bias = d_bias;
+  return gemv(d_out, d_w, type, d_X, n_vec, rows, cols, as_stream(stream), epi);
 }
 
 int qvx_qmatmul_n_rmsnorm(float* d_out, const void* d_w, uint32_t type, const float* d_X, const float* d_norm_w,
@@ -656,7 +686,9 @@ int qvx_plan_add_qmatmul_n(qvx_plan* plan, float* d_out, const void* d_w, uint32
 // One recorded call: a grouped call or a plain / fused GEMV.
 static int run_call(const qvx_plan::Call& c, hipStream_t s) {
   if (!c.members.empty()) return gemv_group(c.members.data(), (int)c.members.size(), c.X, c.cols, c.epi, s);
-  return gemv(c.out, c.w, c.type, c.X, c.nvec, c.rows, c.cols, s, c.epi);
+  GemvEpi epi = c.epi;
+  epi.no_alloc = true;  // a captured call may not allocate
+  return gemv(c.out, c.w, c.type, c.X, c.nvec, c.rows, c.cols, s, epi);
 }
 
 int qvx_plan_add_qmatmul_group(qvx_plan* plan, float* const* d_out, const void* const* d_w, const uint32_t* types,
@@ -838,7 +870,8 @@ int qvx_qmatmul_n_host(float* out, const void* w, uint32_t type, const float* X,
   const size_t wb = (size_t)rows * (size_t)(cols / (int)ti->block) * ti->bytes;
   const size_t xb = sizeof(float) * (size_t)n_vec * (size_t)cols;
   const size_t ob = sizeof(float) * (size_t)n_vec * (size_t)rows;
-  auto* base = static_cast<uint8_t*>(g_stage.get(align_up(wb) + align_up(xb) + align_up(ob)));
+  HostStage stage(align_up(wb) + align_up(xb) + align_up(ob));
+  auto* base = static_cast<uint8_t*>(stage.p);
   if (!base) return QVX_E_HIP;
   void* dw = base;
   auto* dx = reinterpret_cast<float*>(base + align_up(wb));
@@ -862,7 +895,8 @@ int qvx_dequantize_host(uint32_t type, const void* src, float* dst, size_t n) {
   if (n == 0) return QVX_OK;
   if (!src || !dst) return QVX_E_NULL;
   const size_t sb = n / t->block * t->bytes, db = n * sizeof(float);
-  auto* base = static_cast<uint8_t*>(g_stage.get(align_up(sb) + align_up(db)));
+  HostStage stage(align_up(sb) + align_up(db));
+  auto* base = static_cast<uint8_t*>(stage.p);
   if (!base) return QVX_E_HIP;
   auto* ddst = reinterpret_cast<float*>(base + align_up(sb));
   if (hipMemcpy(base, src, sb, hipMemcpyHostToDevice) != hipSuccess) return hip_status();

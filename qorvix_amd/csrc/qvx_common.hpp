@@ -168,10 +168,15 @@ inline bool lds_ready(const void* kern, LdsLimit& lim, size_t dyn) {
 // Visibility across the XCDs' separate L2 caches without flushing or invalidating them (a
 // device-scope fence writes back and drops the whole L2, which costs the tiles still running their
 // K loop far more than this epilogue): the partials are written and read with device-scope relaxed
-// atomic accesses, which the compiler issues coherent at device scope (sc1); every wave waits for
-// its partial stores to complete (vmcnt 0) before the barrier after which the counter is
-// incremented (a device-scope atomic), and the last split issues its loads only after that atomic
-// has returned.
+// atomic accesses, which the compiler issues coherent at device scope (sc1), so each store reaches
+// the device-coherent level when it completes and each load reads from it.  Every wave waits for its
+// partial stores to complete (s_waitcnt vmcnt(0), an asm statement with a memory clobber, so the
+// compiler keeps every store above it) before the barrier after which the counter is incremented (a
+// device-scope atomic), and the last split issues its loads only after that atomic has returned.  No
+// release / acquire fence is needed on top: completion of a coherent store is the point at which
+// other XCDs can see it, and the counter's atomic is ordered after those completions by the wait and
+// the barrier; the loads are ordered after the atomic by its returned value (a data dependence
+// through the LDS flag and the second barrier).
 template <int NA, int NTHR>
 __device__ __forceinline__ bool split_k_last(float (&acc)[NA], float* __restrict__ part, uint32_t* cnt, int S,
                                              int z, int tid, int* last) {
@@ -180,7 +185,7 @@ __device__ __forceinline__ bool split_k_last(float (&acc)[NA], float* __restrict
 #pragma unroll
   for (int a = 0; a < NA; ++a)
     __hip_atomic_store(mine + (a * NTHR + tid), acc[a], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __builtin_amdgcn_s_waitcnt(0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (tid == 0)
     *last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(S - 1);

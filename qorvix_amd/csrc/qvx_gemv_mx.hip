@@ -1169,4 +1169,292 @@ bool launch_gemv_group(const GemvMember* m, int n, const float* X, int cols, con
               : launch_group_tpt<2, false>(X, cols, a, nwg, per_group, epi, s);
 }
 
+
+// ---- many vectors: one weight pass per call -----------------------------------------------------
+// qvx_qmatmul_n at encoder and prefill batch sizes (nvec in the tens to thousands) streams the
+// weights once per 64 vectors instead of once per 8, with every output bit-identical to the
+// one-vector kernel's (the reference's promise for qmatmulN, runtime/include/qorvix/runtime/
+// qmatmul.hpp:31-32).  Two launches:
+//  * k_q4k_many_conv converts every 64-element group of every vector once, with the shared quantiser
+//    mx_quantize (the same 8-lane task groups), into a workspace: A fragments [v][s][sb][part][32 B]
+//    (qh bytes of sub-block sb's 32 elements, then its ql bytes) and records [v][s][g] = (sx, Qa, Qb).
+//  * k_gemv_q4k_many: a 256-thread workgroup owns 32 weight rows x 64 vectors (wave w: vectors
+//    16w..16w+15).  Per sub-block one v_mfma_i32_32x32x32_i8 takes A = 32 rows (vector, qh / ql) x 32
+//    elements and B = the 32 rows' codes (low nibbles of the group's qs bytes, or high nibbles), so
+//    lane (row j, half h) ends with the exact integer sums n.qh, n.ql of 8 vectors; it then applies
+//    the one-vector kernel's fold to each (the same integers ta = sum n q and tb = 16 sum n q, the same
+//    float expression), accumulates each group over the super-blocks of each K range of that kernel's
+//    geometry (KQ ranges of mx_geometry, walked in its order), and adds the ranges in order, each as
+//    (g0 + g2) + (g1 + g3).  An optional bias is added last (out = sum + bias[r], the reference's
+//    wmatmulNBias, runtime/include/qorvix/runtime/weights.hpp:68-80).
+constexpr int kManyRows = 32;  // weight rows a workgroup
+
+__global__ __launch_bounds__(256) void k_q4k_many_conv(const float* __restrict__ X, int nvec, int cols,
+                                                       uint8_t* __restrict__ frag, float4* __restrict__ meta) {
+  const int nsb = cols / 256, per = nsb * 32;
+  const int ntask = nvec * per;
+  const int t0 = (int)blockIdx.x * 256 + (int)threadIdx.x, t = min(t0, ntask - 1);
+  const int v = t / per, r = t - v * per;
+  const float4* src = reinterpret_cast<const float4*>(X + (size_t)v * cols + 8 * r);
+  const XQ8 q = mx_quantize(src[0], src[1]);  // every lane takes part: DPP across the 8 tasks of a group
+  if (t0 >= ntask) return;
+  const int sblk = r >> 5, g = (r >> 3) & 3, part = r & 7;
+  const int sb = 2 * g + (part >> 2), off = 8 * (part & 3);
+  uint8_t* base = frag + (((size_t)v * nsb + sblk) * 8 + sb) * 64;
+  *reinterpret_cast<uint2*>(base + off) = make_uint2(q.h0, q.h1);
+  *reinterpret_cast<uint2*>(base + 32 + off) = make_uint2(q.l0, q.l1);
+  float* m = reinterpret_cast<float*>(meta + ((size_t)v * nsb + sblk) * 4 + g);
+  if (part == 0) {
+    m[0] = q.sx;
+    m[1] = (float)q.sq;
+  }
+  if (part == 4) m[2] = (float)q.sq;
+}
+
+// Lane (j, h)'s 8 vectors are u = 4 q + 2 h + m (q = 0..3, m = 0..1) of the wave's 16; their records
+// sit at 8 h + 2 q + m in the wave's LDS rows, so a lane reads its 8 with two 16-byte reads per field.
+__device__ inline int many_pos(int u) { return 8 * ((u >> 1) & 1) + 2 * (u >> 2) + (u & 1); }
+
+typedef int i32x16_t __attribute__((ext_vector_type(16)));
+
+// One super-block's operands for a lane: header, the lane's half of the four groups' code bytes, the A
+// fragments of the eight sub-blocks (its row: vector j / 2, qh or ql) and the record it loads for the
+// wave.  Loaded one step ahead of use.
+struct ManyStep {
+  uint4 hd, qv[4], av[8];
+  float4 mv;
+};
+
+// NVB: 16-vector blocks a workgroup (1, 2, 4); the 4 / NVB waves of a block take the K ranges of the
+// one-vector geometry round-robin, and the ranges' partials are added in range order through LDS.
+template <bool BIAS, int NVB>
+__global__ __launch_bounds__(256) void k_gemv_q4k_many(const uint8_t* __restrict__ W, const uint8_t* __restrict__ frag,
+                                                       const float4* __restrict__ meta, float* __restrict__ Y,
+                                                       const float* __restrict__ bias, int rows, int cols, int nvec,
+                                                       uint32_t row_bytes, int KQ, int nvt) {
+  constexpr int WK = 4 / NVB;  // waves per vector block
+  __shared__ __attribute__((aligned(16))) float rec[4][4][3][16];  // [wave][group][sx, Qa, Qb][position]
+  __shared__ __attribute__((aligned(16))) float red[WK > 1 ? NVB * 16 * 64 * 8 : 4];  // [vb][kq][lane][8]
+  const int nsb = cols / 256;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wv = wave % NVB, wkq = wave / NVB;  // vector block, K-range phase
+  int b = (int)blockIdx.x;
+  {
+    const int nb = (int)gridDim.x;
+    if ((nb & 7) == 0) b = (b & 7) * (nb >> 3) + (b >> 3);  // an XCD takes consecutive tiles: one row block
+  }
+  const int rt = b / nvt, vt = b - rt * nvt;
+  const int j = lane & 31, h = lane >> 5;
+  const int r = rt * kManyRows + j, rr = min(r, rows - 1);
+  const int vb = vt * 16 * NVB + 16 * wv;
+  const uint8_t* wp = W + (size_t)rr * row_bytes;
+  const int va = min(vb + (j >> 1), nvec - 1);  // A row j = (vector j / 2, part j % 2)
+  const uint8_t* ap = frag + (size_t)va * nsb * 512 + (j & 1) * 32 + 16 * h;
+  // record this lane loads for the wave (vector l / 4, group l % 4) and where it goes
+  const int mu = lane >> 2, mg = lane & 3;
+  const float4* mp = meta + (size_t)min(vb + mu, nvec - 1) * nsb * 4 + mg;
+  const uint32_t mw = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)&rec[wave][mg][0][many_pos(mu)];
+  const uint32_t mr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)&rec[wave][0][0][8 * h];
+
+  auto load = [&](int sblk, ManyStep& d) {
+    const uint8_t* wb = wp + (size_t)sblk * 144;
+    d.hd = *reinterpret_cast<const uint4*>(wb);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) d.qv[c] = *reinterpret_cast<const uint4*>(wb + 16 + 32 * c + 16 * h);
+    const uint8_t* fb = ap + (size_t)sblk * 512;
+#pragma unroll
+    for (int sb = 0; sb < 8; ++sb) d.av[sb] = *reinterpret_cast<const uint4*>(fb + 64 * sb);
+    d.mv = mp[(size_t)sblk * 4];
+  };
+  // this wave's K ranges kq = wkq, wkq + WK, ...; steps walk each range in the one-vector order
+  auto range = [&](int kq, int& s0, int& s1, bool& back) {
+    s0 = kq * nsb / KQ;
+    s1 = (kq + 1) * nsb / KQ;
+    back = KQ > 1 && !(kq & 1);  // SbOrder
+  };
+  auto sblk_of = [&](int kq, int u) {
+    int s0, s1;
+    bool back;
+    range(kq, s0, s1, back);
+    return back ? s1 - 1 - u : s0 + u;
+  };
+
+  float acc[8][4], fin[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) fin[k] = 0.0f;
+  // first step of the wave
+  int kq = wkq, u = 0;
+  auto advance = [&](int& q, int& uu) {  // next (range, position) of this wave; q >= KQ when done
+    int s0, s1;
+    bool back;
+    range(q, s0, s1, back);
+    if (++uu >= s1 - s0) {
+      uu = 0;
+      for (q += WK; q < KQ; q += WK) {
+        range(q, s0, s1, back);
+        if (s1 > s0) break;
+      }
+    }
+  };
+  {  // skip leading empty ranges
+    int s0, s1;
+    bool back;
+    range(kq, s0, s1, back);
+    while (kq < KQ && s1 <= s0) {
+      kq += WK;
+      if (kq < KQ) range(kq, s0, s1, back);
+    }
+  }
+  ManyStep cur, nxt;
+  if (kq < KQ) load(sblk_of(kq, 0), cur);
+  int cur_kq = kq;
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[k][c] = 0.0f;
+  // ranges this wave owns that are empty still contribute (0 + 0) + (0 + 0) = +0 to their slot
+  if constexpr (WK > 1) {
+    for (int q = wkq; q < KQ; q += WK) {
+      int s0, s1;
+      bool back;
+      range(q, s0, s1, back);
+      if (s1 <= s0)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) red[((wv * KQ + q) * 64 + lane) * 8 + k] = 0.0f;
+    }
+  }
+  while (cur_kq < KQ) {
+    int nkq = cur_kq, nu = u;
+    advance(nkq, nu);
+    if (nkq < KQ) load(sblk_of(nkq, nu), nxt);  // next step's operands in flight during this one
+    // the wave's records of this super-block into its LDS rows (wave-private: no barrier)
+    asm volatile("ds_write_b32 %0, %1 offset:0\n\tds_write_b32 %0, %2 offset:64\n\tds_write_b32 %0, %3 offset:128"
+                 ::"v"(mw), "v"(cur.mv.x), "v"(cur.mv.y), "v"(cur.mv.z) : "memory");
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const u32x4 hd = {cur.hd.x, cur.hd.y, cur.hd.z, cur.hd.w};
+    const float d = f16lo(hd.x), dmin = f16hi(hd.x);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint4 q = cur.qv[c];
+      const v4i bl = {(int)(q.x & 0x0F0F0F0Fu), (int)(q.y & 0x0F0F0F0Fu), (int)(q.z & 0x0F0F0F0Fu),
+                      (int)(q.w & 0x0F0F0F0Fu)};
+      const v4i bh = {(int)((q.x >> 4) & 0x0F0F0F0Fu), (int)((q.y >> 4) & 0x0F0F0F0Fu),
+                      (int)((q.z >> 4) & 0x0F0F0F0Fu), (int)((q.w >> 4) & 0x0F0F0F0Fu)};
+      const v4i a0 = __builtin_bit_cast(v4i, cur.av[2 * c]), a1 = __builtin_bit_cast(v4i, cur.av[2 * c + 1]);
+      const i32x16_t lo = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bl, i32x16_t{}, 0, 0, 0);
+      const i32x16_t hi = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bh, i32x16_t{}, 0, 0, 0);
+      float sca, scb16, mna, mnb;
+      q4k_group_scales(hd, c, sca, scb16, mna, mnb);
+      float sx[8], qa[8], qb[8];
+      {
+        const uint32_t ra = mr + (uint32_t)c * 192u;
+        float4 t0, t1, t2, t3, t4, t5;
+        asm volatile("ds_read_b128 %0, %6 offset:0\n\tds_read_b128 %1, %6 offset:16\n\t"
+                     "ds_read_b128 %2, %6 offset:64\n\tds_read_b128 %3, %6 offset:80\n\t"
+                     "ds_read_b128 %4, %6 offset:128\n\tds_read_b128 %5, %6 offset:144\n\ts_waitcnt lgkmcnt(0)"
+                     : "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3), "=&v"(t4), "=&v"(t5)
+                     : "v"(ra)
+                     : "memory");
+        const float4 tt[6] = {t0, t1, t2, t3, t4, t5};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          sx[k] = tt[0][k];
+          sx[4 + k] = tt[1][k];
+          qa[k] = tt[2][k];
+          qa[4 + k] = tt[3][k];
+          qb[k] = tt[4][k];
+          qb[4 + k] = tt[5][k];
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int e = 4 * (k >> 1) + 2 * (k & 1);  // D rows of vector k: qh at e, ql at e + 1
+        const int ta = (int)((uint32_t)lo[e] << 7) + lo[e + 1];                        // sum n q, 2c
+        const int tb = (int)((((uint32_t)hi[e] << 7) + (uint32_t)hi[e + 1]) << 4);    // 16 sum n q, 2c+1
+        const float t = __builtin_fmaf((float)tb, scb16, (float)ta * sca);
+        const float w = __builtin_fmaf(qb[k], mnb, qa[k] * mna);
+        acc[k][c] = __builtin_fmaf(__builtin_fmaf(d, t, -dmin * w), sx[k], acc[k][c]);
+      }
+    }
+    if (nkq != cur_kq) {  // the range ends: its partial, groups as (g0 + g2) + (g1 + g3)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float pk = (acc[k][0] + acc[k][2]) + (acc[k][1] + acc[k][3]);
+        if constexpr (WK > 1)
+          red[((wv * KQ + cur_kq) * 64 + lane) * 8 + k] = pk;
+        else
+          fin[k] += pk;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[k][c] = 0.0f;
+      }
+    }
+    cur = nxt;
+    cur_kq = nkq;
+    u = nu;
+  }
+  if constexpr (WK > 1) {
+    __syncthreads();
+    if (wkq != 0) return;
+    for (int q = 0; q < KQ; ++q)  // every range in order, as the one-vector kernel adds its waves
+#pragma unroll
+      for (int k = 0; k < 8; ++k) fin[k] += red[((wv * KQ + q) * 64 + lane) * 8 + k];
+  } else {
+    // ranges with no super-block add (0 + 0) + (0 + 0) = +0, which changes nothing after the first
+  }
+  if (r >= rows) return;
+  const float bv = BIAS ? bias[r] : 0.0f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int v = vb + 4 * (k >> 1) + 2 * h + (k & 1);
+    if (v < nvec) Y[(size_t)v * rows + r] = BIAS ? fin[k] + bv : fin[k];
+  }
+}
+
+// Workspace bytes of the many-vector form for nvec x cols (A fragments, then the records).
+size_t gemv_many_ws_bytes(int nvec, int cols) {
+  const size_t nsb = (size_t)(cols / 256);
+  return (size_t)nvec * nsb * 512 + (size_t)nvec * nsb * 64;
+}
+
+// 1 if the many-vector form takes this call: the shapes the one-vector matrix-core kernel takes (its
+// outputs are bit-identical to that kernel's), whole 256-element super-blocks.
+int gemv_many_supported(int cols, size_t row_bytes) {
+  return gemv_mx_max_nv(cols) >= 1 && row_bytes < (1u << 24) ? 1 : 0;
+}
+
+// Q4_K GEMV of nvec vectors in one weight pass per 64 vectors (bias may be null).  ws: the
+// gemv_many_ws_bytes workspace, 16-byte aligned.  Returns false, having launched nothing, when the
+// shape is not handled here.
+bool launch_gemv_q4k_many(const void* w, const float* X, float* Y, const float* bias, int nvec, int rows, int cols,
+                          size_t row_bytes, void* ws, hipStream_t s) {
+  if (!gemv_many_supported(cols, row_bytes) || nvec < 1 || rows < 1 || !ws) return false;
+  MxGeo geo{};
+  (void)mx_geometry(rows, cols, row_bytes, geo);
+  const int nsb = cols / 256;
+  auto* frag = static_cast<uint8_t*>(ws);
+  auto* meta = reinterpret_cast<float4*>(frag + (size_t)nvec * nsb * 512);
+  const size_t ntask = (size_t)nvec * nsb * 32;
+  k_q4k_many_conv<<<(unsigned)((ntask + 255) / 256), 256, 0, s>>>(X, nvec, cols, frag, meta);
+  // vector blocks a workgroup: 4 (one wave each) from 64 vectors; fewer for smaller batches, whose
+  // spare waves split the K ranges instead of computing clamped duplicates
+  const int nvb = nvec > 32 ? 4 : nvec > 16 ? 2 : 1;
+  const int nvt = (nvec + 16 * nvb - 1) / (16 * nvb), nrt = (rows + kManyRows - 1) / kManyRows;
+  const unsigned grid = (unsigned)(nvt * nrt);
+  const auto* wb = static_cast<const uint8_t*>(w);
+  const uint32_t rb = (uint32_t)row_bytes;
+#define QVX_MANY(B, N) k_gemv_q4k_many<B, N><<<grid, 256, 0, s>>>(wb, frag, meta, Y, bias, rows, cols, nvec, rb, geo.KQ, nvt)
+  if (bias) {
+    if (nvb == 4) QVX_MANY(true, 4);
+    else if (nvb == 2) QVX_MANY(true, 2);
+    else QVX_MANY(true, 1);
+  } else {
+    if (nvb == 4) QVX_MANY(false, 4);
+    else if (nvb == 2) QVX_MANY(false, 2);
+    else QVX_MANY(false, 1);
+  }
+#undef QVX_MANY
+  return true;
+}
+
 }  // namespace qvx

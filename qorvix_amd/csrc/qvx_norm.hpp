@@ -102,6 +102,8 @@ struct GemvEpi {
   const float* norm_w = nullptr;  // non-null: the activations are rmsnorm(x, norm_w, eps)
   float eps = 0.0f;
   bool swiglu = false;  // weight rows interleaved in 16-row (gate, up) groups; out = silu(gate) * up
+  const float* bias = nullptr;  // non-null (plain calls only): out = W . x + bias, the add last
+  bool no_alloc = false;  // the call must not take stream-ordered temporaries (graph-captured plans)
   int flags() const { return (norm_w ? EPI_NORM : 0) | (swiglu ? EPI_SWIGLU : 0); }
 };
 

@@ -65,9 +65,23 @@ __global__ __launch_bounds__(256) void k_swiglu_il(float* __restrict__ out, cons
   out[i] = silu_mul(yv[g], yv[g + 16]);
 }
 
+// out[v, r] += bias[r]: the reference's bias add after the product (runtime/include/qorvix/runtime/
+// weights.hpp:58-80, one fp32 add per output), for the routes whose kernels do not fold it in.
+__global__ __launch_bounds__(256) void k_add_bias(float* __restrict__ out, const float* __restrict__ bias, int rows,
+                                                  size_t n) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  out[i] += bias[i % (size_t)rows];
+}
+
 inline unsigned blocks256(size_t n) { return (unsigned)((n + 255) / 256); }
 
 }  // namespace
+
+void launch_add_bias(float* out, const float* bias, int nvec, int rows, hipStream_t s) {
+  const size_t n = (size_t)nvec * (size_t)rows;
+  if (n) k_add_bias<<<blocks256(n), 256, 0, s>>>(out, bias, rows, n);
+}
 
 void launch_rmsnorm(float* out, const float* x, const float* w, float eps, int nvec, int n, hipStream_t s) {
   k_rmsnorm<<<(unsigned)nvec, kNormThreads, 0, s>>>(out, x, w, n, eps);

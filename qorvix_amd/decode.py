@@ -401,6 +401,14 @@ class FusedDecodeStep:
 
     def __init__(self, model: Model, m: int, seed: int = 9, device="cuda", grouped: bool = False):
         import torch
+        # every fused launch folds a norm into its activations: refuse a model without them rather than
+        # run the projections on un-normed inputs
+        for l in range(len(model.layers)):
+            for k in ("attn_norm", "ffn_norm"):
+                if l >= len(model.norms) or model.norms[l].get(k) is None:
+                    raise ValueError(f"FusedDecodeStep needs {k} of layer {l}; the model has none")
+        if model.lm_head is not None and model.output_norm is None:
+            raise ValueError("FusedDecodeStep needs output_norm for the LM head; the model has none")
         if grouped and m != 1:
             raise ValueError("grouped calls take one vector")
         self.model, self.m = model, m

@@ -141,6 +141,12 @@ def test_gemm_and_dequant_rejections():
     assert lib.qvx_qgemm_f16_noalloc(FAKE, FAKE, 10, FAKE, 128, 256, 256, qvx.GEMM_F16, None) == qvx.E_TYPE
     assert lib.qvx_qgemm_f16_noalloc(FAKE, FAKE, qvx.Q4_K, FAKE, 128, 0, 256, qvx.GEMM_F16, None) == qvx.OK
     assert lib.qvx_qgemm_f16_noalloc(None, FAKE, qvx.Q4_K, FAKE, 128, 4, 256, qvx.GEMM_F16, None) == qvx.E_NULL
+    # qvx_qmatmul_n_bias: qvx_qmatmul_n's checks (wmatmulNBias = qmatmulN + the bias add)
+    assert lib.qvx_qmatmul_n_bias(FAKE, FAKE, qvx.Q4_K, FAKE, FAKE, 0, 4, 256, None) == qvx.E_NVEC
+    assert lib.qvx_qmatmul_n_bias(FAKE, FAKE, qvx.Q4_K, FAKE, FAKE, 2, 4, 300, None) == qvx.E_SHAPE
+    assert lib.qvx_qmatmul_n_bias(FAKE, FAKE, 10, FAKE, FAKE, 2, 4, 256, None) == qvx.E_TYPE
+    assert lib.qvx_qmatmul_n_bias(FAKE, FAKE, qvx.Q4_K, FAKE, FAKE, 2, 0, 256, None) == qvx.OK
+    assert lib.qvx_qmatmul_n_bias(None, FAKE, qvx.Q4_K, FAKE, FAKE, 2, 4, 256, None) == qvx.E_NULL
     assert lib.qvx_gemm16(FAKE, FAKE, FAKE, 4, 4, 64, qvx.GEMM_I8, None) == qvx.E_VARIANT
     assert lib.qvx_gemm16(FAKE, FAKE, FAKE, -1, 4, 64, qvx.GEMM_BF16, None) == qvx.E_SHAPE
     assert lib.qvx_gemm16(FAKE, FAKE, FAKE, 0, 4, 64, qvx.GEMM_BF16, None) == qvx.OK

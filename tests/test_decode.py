@@ -83,3 +83,21 @@ def test_fused_model_stacks_same_input_pairs():
     assert f.parts["wqk"] == (("wq", 16), ("wk", 4))
     # the unfused model keeps the reference's 7 calls per layer
     assert [n for l, n, _, _ in m.calls() if l == 0] == [s[0] for s in decode.LAYER_SPECS]
+
+
+def test_fused_step_refuses_a_model_without_norms():
+    """Every launch of FusedDecodeStep folds an RMSNorm into its activations; a model whose GGUF file
+    lacks a norm tensor is refused up front (before any device work) instead of running un-normed."""
+    import pytest
+
+    m = decode.Model(lm_head=None, norms=[{"attn_norm": object(), "ffn_norm": None}], output_norm=None)
+    m.layers.append({})
+    with pytest.raises(ValueError, match="ffn_norm of layer 0"):
+        decode.FusedDecodeStep(m, 1)
+    m.norms = []
+    with pytest.raises(ValueError, match="attn_norm of layer 0"):
+        decode.FusedDecodeStep(m, 1)
+    m.norms = [{"attn_norm": object(), "ffn_norm": object()}]
+    m.lm_head = object()
+    with pytest.raises(ValueError, match="output_norm"):
+        decode.FusedDecodeStep(m, 1)

@@ -620,11 +620,10 @@ DEQUANT_GEMM_TYPES = [qvx.Q6_K, qvx.Q8_0, qvx.Q4_0, qvx.Q5_0, qvx.Q5_K, qvx.Q4_1
 @pytest.mark.parametrize("variant", [qvx.GEMM_BF16, qvx.GEMM_F16])
 @pytest.mark.parametrize("M,rows,cols", [(128, 512, 1024), (37, 300, 256), (37, 300, 2304)])
 def test_gemm_other_types_parity(cuda, t, variant, M, rows, cols):
-    """The weight types other than Q4_K (Q6_K on the dequantising MFMA GEMM, the rest dequantised to
-    16 bits for the library GEMM), within the GEMM tolerance of the fp64 oracle: 128 x 512 x 1024
-    takes two K splits of 8 slices, 37 x 300 x 256 one range of 4 slices with a ragged tile in both M
-    and N, and 37 x 300 x 2304 four splits of 9 slices (an odd range: its last slice runs outside
-    the MFMA kernel's two-slice loop)."""
+    """The weight types other than Q4_K (Q6_K on its raw-block MFMA kernels: k_qgemm_q6k8 at cols 512 and
+    1024, k_qgemm_deq at the odd block counts of cols 256 and 2304; the rest dequantised to 16 bits for
+    the plain MFMA GEMM), within the GEMM tolerance of the fp64 oracle, on 128 x 512 x 1024, 37 x 300 x
+    256 (ragged tiles in M and N) and 37 x 300 x 2304 (K split into ranges of an odd length)."""
     rng = np.random.default_rng(M + rows + cols + 3 * t + variant)
     w = random_weight(t, rows, cols, rng, scale=0.002)
     X16 = (rng.standard_normal((M, cols)) * 0.5).astype(np.float16)
@@ -643,7 +642,8 @@ def test_gemm_q6k_pipeline_shapes(cuda, variant, M, rows, cols):
     to six super-block pairs, one K range (37 x 300 x 512, M = 1), two splits of five super-blocks
     (200 x 300 x 2560) and two of six or four (130 x 520 x 3072, 300 x 2100 x 2048), against the
     fp64 oracle.  The same call on a copy of W two bytes off its dword alignment, which the staged
-    copies cannot take, goes to the dequantise-then-library route and meets the same bound."""
+    copies cannot take, goes to the 16-bit dequantiser and the plain MFMA GEMM and meets the same
+    bound."""
     rng = np.random.default_rng(M + rows + cols + variant)
     t = qvx.Q6_K
     w = random_weight(t, rows, cols, rng, scale=0.002)
@@ -686,21 +686,22 @@ def _round16(v32, bf16):
     return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
 
 
-@pytest.mark.parametrize("t", DEQUANT_GEMM_TYPES)
+@pytest.mark.parametrize("t,cols", [(t, 512) for t in DEQUANT_GEMM_TYPES] + [(qvx.Q6_K, 2304)])
 @pytest.mark.parametrize("variant", [qvx.GEMM_BF16, qvx.GEMM_F16])
 @pytest.mark.parametrize("src_offset", [0, 2])
-def test_gemm_dequant16_bit_exact(cuda, t, variant, src_offset):
+def test_gemm_dequant16_bit_exact(cuda, t, cols, variant, src_offset):
     """The 16-bit weight operand of the GEMM, read back exactly: with X the identity (M = cols),
     out[m, r] = W16[r, m] (one nonzero product per sum, exact in fp32), which must equal the oracle's
-    dequantised fp32 value rounded once to fp16 / bf16.  src_offset 0 runs the dequantising MFMA
-    kernel (every weight element of the 300 x 512 matrix passes through its LDS B tile); 2 moves the
-    blocks off 4-byte alignment, which that kernel declines, so the dequantise-and-library fallback
-    (its unstaged dequantiser) runs; the other types always take that fallback.  Zeros are compared
-    without their sign."""
+    dequantised fp32 value rounded once to fp16 / bf16.  Which kernel builds the operand: Q6_K at
+    cols 512 (an even number of blocks a row) on k_qgemm_q6k8, at cols 2304 (an odd number) on the
+    dequantising MFMA kernel k_qgemm_deq, in both cases in registers or LDS from the raw blocks;
+    src_offset 2 moves the blocks off 4-byte alignment, which both decline, and every other type always
+    goes through the 16-bit dequantiser (qvx_dequantize16's kernels) and the plain MFMA GEMM.  Zeros are
+    compared without their sign."""
     if t == qvx.F32 and src_offset:
         pytest.skip("fp32 weights are 4-byte values: a 2-byte offset is not a layout they come in")
-    rng = np.random.default_rng(5 * t + variant + src_offset)
-    rows, cols = 300, 512
+    rng = np.random.default_rng(5 * t + variant + src_offset + cols)
+    rows = 300
     w = random_weight(t, rows, cols, rng, scale=0.002)
     raw = cuda.zeros(w.size + 16, dtype=cuda.uint8, device="cuda")
     raw[src_offset:src_offset + w.size].copy_(cuda.from_numpy(w))
@@ -734,8 +735,9 @@ def test_gemm_float_weights_ragged_tail(cuda, t):
 
 
 def test_gemm_q6k_ffn_down_shape(cuda):
-    """The Q4_K_M model's Q6_K ffn_down (14336 -> 4096) at M = 64 (16 K splits of 14 slices) on the
-    dequantising MFMA kernel, and the int8 variant refused for it."""
+    """The Q4_K_M model's Q6_K ffn_down (14336 -> 4096) at M = 64 on k_qgemm_q6k8 (K = 14336 is a
+    whole number of super-block pairs; 128-token tiles, K split 8 ways), and the int8 variant refused
+    for it."""
     t, M, rows, cols = qvx.Q6_K, 64, 4096, 14336
     W = qvx.empty_weight(t, rows, cols)
     qvx.fill_synthetic_t(W, t, rows, cols, seed=41, scale_mul=1e-3)

@@ -79,6 +79,23 @@ def test_noalloc_q6k_matches_allocating_gemm_on_two_calls(cuda, variant):
         assert max_rel(got[:, idx], X32 @ Wd.T) <= GEMM_TOL
 
 
+@pytest.mark.parametrize("variant", [qvx.GEMM_BF16, qvx.GEMM_F16])
+def test_noalloc_q6k_odd_blocks_matches_allocating_gemm(cuda, variant):
+    """Q6_K rows of an odd number of super-blocks (cols 2304) run on the dequantising MFMA kernel
+    k_qgemm_deq; at M = 128 its grid is small, so K splits and the partial tiles and counters live in
+    the scratch.  Two calls, the second smaller; bit for bit the allocating call's, and within the GEMM
+    tolerance of the fp64 oracle on a row slice."""
+    lib = qvx.lib()
+    for n, (M, rows, cols) in enumerate(((128, 4096, 2304), (64, 1024, 2304))):
+        t, W, X, idx, Wd = _case(cuda, M, rows, cols, seed=990 + 10 * n + variant, t=qvx.Q6_K)
+        got = _call(lib.qvx_qgemm_f16_noalloc, cuda, W, t, X, rows, cols, variant)
+        want = _call(lib.qvx_qgemm_f16, cuda, W, t, X, rows, cols, variant)
+        assert np.isfinite(got).all()
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+        X32 = X.cpu().numpy().astype(np.float64)
+        assert max_rel(got[:, idx], X32 @ Wd.T) <= GEMM_TOL
+
+
 @pytest.mark.parametrize("t", [qvx.Q8_0, qvx.Q4_0])
 @pytest.mark.parametrize("variant", [qvx.GEMM_BF16, qvx.GEMM_F16])
 def test_noalloc_dequant16_types_match_allocating_gemm_on_two_calls(cuda, t, variant):
