@@ -100,10 +100,12 @@ int qvx_qmatmul(float* d_out, const void* d_w, uint32_t type, const float* d_x, 
  * bit-identical to qvx_qmatmul on that vector, as the reference promises (qmatmul.hpp:31-32).
  * Q4_K batches of 16 vectors or more on the one-vector kernel's shapes (cols a multiple of 256 up to
  * 32768, aligned operands) run on a many-vector form: the activations are converted once into a
- * stream-ordered temporary from the library's pool (nvec * cols * 2.25 bytes), then the weights are
- * streamed once per 64 vectors -- the reference's "dequantize each block once for all nVec dot
+ * stream-ordered temporary from the library's pool (nvec * cols * 2.25 bytes, plus 2 KiB per 32-row
+ * tile and K range for batches up to 32 vectors), then the weights are streamed once per 64 vectors
+ * (once per 16 up to 32 vectors) -- the reference's "dequantize each block once for all nVec dot
  * products" (qmatmul.hpp:24-32); smaller batches stream them once per 8 vectors and allocate
- * nothing.  Calls recorded in a plan never take the many-vector form (a replay allocates nothing). */
+ * nothing.  A plan gives its many-vector calls a workspace of its own, allocated by
+ * qvx_plan_instantiate, so its replays allocate nothing. */
 int qvx_qmatmul_n(float* d_out, const void* d_w, uint32_t type, const float* d_X, int n_vec,
                   int rows, int cols, void* stream);
 
@@ -291,11 +293,14 @@ int qvx_plan_join(qvx_plan* plan);
 /* Number of recorded calls. */
 int qvx_plan_size(const qvx_plan* plan);
 /* Capture the recorded calls into a HIP graph on the plan's device and instantiate it (an open
- * fork is joined first). */
+ * fork is joined first).  Allocates the device workspace of the plan's many-vector calls (one slice
+ * shared by the calls in order, disjoint slices for the calls of one fork), freed with the plan. */
 int qvx_plan_instantiate(qvx_plan* plan);
 /* Replay the graph on `stream` (stream-ordered, asynchronous).  Not instantiated -> QVX_E_STATE. */
 int qvx_plan_launch(qvx_plan* plan, void* stream);
-/* Issue the recorded calls one by one on `stream` (no graph): the same kernels and arguments. */
+/* Issue the recorded calls one by one on `stream` (no graph): the same kernels and arguments once
+ * the plan is instantiated; before that a many-vector call, having no workspace yet, takes the
+ * chunked batched form (the same output bits). */
 int qvx_plan_run_eager(const qvx_plan* plan, void* stream);
 /* Free the plan and its graph (NULL is a no-op). */
 void qvx_plan_destroy(qvx_plan* plan);

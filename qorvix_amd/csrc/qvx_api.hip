@@ -60,7 +60,7 @@ int launch_quantize_act_q8(const uint16_t* X, int M, int K, int8_t* q, float* sc
                            hipStream_t s);
 void launch_zero(float* p, size_t n, hipStream_t s);
 bool launch_gemv_group(const GemvMember* m, int n, const float* X, int cols, const GemvEpi& epi, hipStream_t s);
-size_t gemv_many_ws_bytes(int nvec, int cols);
+size_t gemv_many_ws_bytes(int nvec, int rows, int cols, size_t row_bytes);
 int gemv_many_supported(int cols, size_t row_bytes);
 bool launch_gemv_q4k_many(const void* w, const float* X, float* Y, const float* bias, int nvec, int rows, int cols,
                           size_t row_bytes, void* ws, hipStream_t s);
@@ -88,8 +88,10 @@ struct qvx_plan {
     int group;  // calls sharing a group >= 0 are independent of each other (one fork); -1: in order
     GemvEpi epi;  // fused RMSNorm / SwiGLU (rows = the weight's rows: 2 ffn for SwiGLU)
     std::vector<GemvMember> members;  // non-empty: a grouped call over X (nvec 1), out / w / type / rows unused
+    size_t ws_off = 0, ws_bytes = 0;  // its slice of the plan's workspace (the many-vector form)
   };
   std::vector<Call> calls;
+  void* ws = nullptr;  // device workspace of the recorded calls, allocated by qvx_plan_instantiate
   int device = 0;
   int open_group = -1;  // the fork being recorded, -1 if none
   int groups = 0;
@@ -197,6 +199,15 @@ int gemv_unfused(float* out, const void* w, uint32_t type, const float* X, int n
 // out = W . x per vector, optionally with the activations normalised (epi.norm_w) and / or the
 // interleaved gate|up rows gated (epi.swiglu: rows / 2 outputs a vector).  The argument checks are
 // the plain operator's.
+// Workspace bytes of the many-vector Q4_K form if a call takes it, else 0.
+inline size_t many_route_bytes(uint32_t type, int nvec, int rows, int cols, size_t row_bytes, bool fast,
+                               const GemvEpi& epi) {
+  if (!fast || type != T_Q4_K || epi.flags() || nvec < kManyMin || rows <= 0 || cols <= 0 ||
+      !gemv_many_supported(cols, row_bytes))
+    return 0;
+  return gemv_many_ws_bytes(nvec, rows, cols, row_bytes);
+}
+
 int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int rows, int cols, hipStream_t s,
          const GemvEpi& epi) {
   const TypeInfo* ti = nullptr;
@@ -217,14 +228,15 @@ int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int
     return gemv_unfused(out, w, type, X, nvec, rows, cols, s, epi);
   // Q4_K batches of kManyMin vectors or more (encoder and prefill sizes): activations converted once,
   // the weights streamed once per 64 vectors, bit-identical per vector to the one-vector kernel
-  // (k_gemv_q4k_many), with the bias added in its epilogue.  It takes a stream-ordered workspace, so
-  // graph-captured plans (no_alloc) keep the chunked forms below.
-  if (fast && type == T_Q4_K && !epi.flags() && !epi.no_alloc && nvec >= kManyMin &&
-      gemv_many_supported(cols, row_bytes)) {
-    void* ws = gemm_temp_alloc(gemv_many_ws_bytes(nvec, cols), s);
+  // (k_gemv_q4k_many), with the bias added in its epilogue.  Its workspace is the caller's (a plan
+  // sizes one at instantiation) or a stream-ordered temporary; a call that may not allocate and has
+  // no workspace keeps the chunked forms below.
+  if (const size_t need = many_route_bytes(type, nvec, rows, cols, row_bytes, fast, epi)) {
+    const bool own = epi.ws && epi.ws_bytes >= need;
+    void* ws = own ? epi.ws : epi.no_alloc ? nullptr : gemm_temp_alloc(need, s);
     if (ws) {
       const bool ok = launch_gemv_q4k_many(w, X, out, epi.bias, nvec, rows, cols, row_bytes, ws, s);
-      gemm_temp_free(ws, s);
+      if (!own) gemm_temp_free(ws, s);
       if (!ok) return refused();
       return hip_status();
     }
@@ -684,11 +696,45 @@ int qvx_plan_add_qmatmul_n(qvx_plan* plan, float* d_out, const void* d_w, uint32
 }
 
 // One recorded call: a grouped call or a plain / fused GEMV.
-static int run_call(const qvx_plan::Call& c, hipStream_t s) {
+static int run_call(const qvx_plan& plan, const qvx_plan::Call& c, hipStream_t s) {
   if (!c.members.empty()) return gemv_group(c.members.data(), (int)c.members.size(), c.X, c.cols, c.epi, s);
   GemvEpi epi = c.epi;
   epi.no_alloc = true;  // a captured call may not allocate
+  if (plan.ws && c.ws_bytes) {
+    epi.ws = static_cast<uint8_t*>(plan.ws) + c.ws_off;
+    epi.ws_bytes = c.ws_bytes;
+  }
   return gemv(c.out, c.w, c.type, c.X, c.nvec, c.rows, c.cols, s, epi);
+}
+
+// Lays out the plan's workspace: each call that takes the many-vector form gets a 256-byte aligned
+// slice; calls in order share offset 0, the calls of one fork (which run concurrently) get disjoint
+// slices.  Returns the bytes the plan needs.
+static size_t plan_ws_layout(qvx_plan& plan) {
+  size_t total = 0;
+  for (size_t i = 0; i < plan.calls.size();) {
+    const int g = plan.calls[i].group;
+    size_t n = 1;
+    while (g >= 0 && i + n < plan.calls.size() && plan.calls[i + n].group == g) ++n;
+    size_t off = 0;
+    for (size_t k = i; k < i + n; ++k) {
+      auto& c = plan.calls[k];
+      c.ws_off = c.ws_bytes = 0;
+      if (!c.members.empty() || c.cols <= 0 || c.rows <= 0) continue;
+      const TypeInfo* ti = type_info(c.type);
+      if (!ti || ti->block == 0) continue;
+      const size_t row_bytes = (size_t)(c.cols / (int)ti->block) * ti->bytes;
+      const bool fast = aligned16(c.w) && aligned16(c.X) && row_bytes % 16 == 0;
+      const size_t need = many_route_bytes(c.type, c.nvec, c.rows, c.cols, row_bytes, fast, c.epi);
+      if (!need) continue;
+      c.ws_off = off;
+      c.ws_bytes = need;
+      off += (need + 255) & ~(size_t)255;
+    }
+    if (off > total) total = off;
+    i += n;
+  }
+  return total;
 }
 
 int qvx_plan_add_qmatmul_group(qvx_plan* plan, float* const* d_out, const void* const* d_w, const uint32_t* types,
@@ -753,7 +799,7 @@ int qvx_plan_size(const qvx_plan* plan) { return plan ? (int)plan->calls.size() 
 int qvx_plan_run_eager(const qvx_plan* plan, void* stream) {
   if (!plan) return QVX_E_NULL;
   for (const auto& c : plan->calls)
-    if (int rc = run_call(c, as_stream(stream)); rc != QVX_OK) return rc;
+    if (int rc = run_call(*plan, c, as_stream(stream)); rc != QVX_OK) return rc;
   return QVX_OK;
 }
 
@@ -774,7 +820,7 @@ static int plan_record(const qvx_plan* plan, hipStream_t cs, std::vector<hipStre
     while (g >= 0 && i + n < calls.size() && calls[i + n].group == g) ++n;
     if (n == 1) {
       const auto& c = calls[i];
-      if (int rc = run_call(c, cs); rc != QVX_OK) return rc;
+      if (int rc = run_call(*plan, c, cs); rc != QVX_OK) return rc;
       ++i;
       continue;
     }
@@ -789,7 +835,7 @@ static int plan_record(const qvx_plan* plan, hipStream_t cs, std::vector<hipStre
       const auto& c = calls[i + k];
       hipStream_t st = k == 0 ? cs : side[k - 1];
       if (k > 0 && hipStreamWaitEvent(st, fork, 0) != hipSuccess) return QVX_E_HIP;
-      if (int rc = run_call(c, st); rc != QVX_OK) return rc;
+      if (int rc = run_call(*plan, c, st); rc != QVX_OK) return rc;
     }
     for (size_t k = 1; k < n; ++k) {
       hipEvent_t done = nullptr;
@@ -808,6 +854,13 @@ int qvx_plan_instantiate(qvx_plan* plan) {
   plan->open_group = -1;
   DeviceGuard guard(plan->device);
   if (!guard.ok) return QVX_E_HIP;
+  if (const size_t wsb = plan_ws_layout(*plan)) {
+    if (hipMalloc(&plan->ws, wsb) != hipSuccess) {
+      plan->ws = nullptr;
+      (void)hipGetLastError();
+      return QVX_E_HIP;
+    }
+  }
   // Capture on streams of the plan's own (default priority), in thread-local mode: the GEMV
   // launches make no calls that capture forbids.
   hipStream_t cs = nullptr;
@@ -829,6 +882,8 @@ int qvx_plan_instantiate(qvx_plan* plan) {
   (void)hipStreamDestroy(cs);
   if (rc != QVX_OK) {
     if (graph) (void)hipGraphDestroy(graph);
+    if (plan->ws) (void)hipFree(plan->ws);
+    plan->ws = nullptr;
     (void)hipGetLastError();
     return rc;
   }
@@ -850,6 +905,7 @@ void qvx_plan_destroy(qvx_plan* plan) {
     DeviceGuard guard(plan->device);
     if (plan->exec) (void)hipGraphExecDestroy(plan->exec);
     if (plan->graph) (void)hipGraphDestroy(plan->graph);
+    if (plan->ws) (void)hipFree(plan->ws);
   }
   delete plan;
 }

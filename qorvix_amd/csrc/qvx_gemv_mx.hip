@@ -1178,8 +1178,9 @@ bool launch_gemv_group(const GemvMember* m, int n, const float* X, int cols, con
 //  * k_q4k_many_conv converts every 64-element group of every vector once, with the shared quantiser
 //    mx_quantize (the same 8-lane task groups), into a workspace: A fragments [v][s][sb][part][32 B]
 //    (qh bytes of sub-block sb's 32 elements, then its ql bytes) and records [v][s][g] = (sx, Qa, Qb).
-//  * k_gemv_q4k_many: a 256-thread workgroup owns 32 weight rows x 64 vectors (wave w: vectors
-//    16w..16w+15).  Per sub-block one v_mfma_i32_32x32x32_i8 takes A = 32 rows (vector, qh / ql) x 32
+//  * k_gemv_q4k_many: a wave owns 32 weight rows x 16 vectors and one or more K ranges (the launch
+//    shape, many_shape, decides how the tile's vectors and ranges spread over waves and workgroups).
+//    Per sub-block one v_mfma_i32_32x32x32_i8 takes A = 32 rows (vector, qh / ql) x 32
 //    elements and B = the 32 rows' codes (low nibbles of the group's qs bytes, or high nibbles), so
 //    lane (row j, half h) ends with the exact integer sums n.qh, n.ql of 8 vectors; it then applies
 //    the one-vector kernel's fold to each (the same integers ta = sum n q and tb = 16 sum n q, the same
@@ -1189,11 +1190,14 @@ bool launch_gemv_group(const GemvMember* m, int n, const float* X, int cols, con
 //    wmatmulNBias, runtime/include/qorvix/runtime/weights.hpp:68-80).
 constexpr int kManyRows = 32;  // weight rows a workgroup
 
+// Also zeroes the ncnt tile counters of the product launch that follows it on the stream.
 __global__ __launch_bounds__(256) void k_q4k_many_conv(const float* __restrict__ X, int nvec, int cols,
-                                                       uint8_t* __restrict__ frag, float4* __restrict__ meta) {
+                                                       uint8_t* __restrict__ frag, float4* __restrict__ meta,
+                                                       uint32_t* __restrict__ cnt, int ncnt) {
   const int nsb = cols / 256, per = nsb * 32;
   const int ntask = nvec * per;
   const int t0 = (int)blockIdx.x * 256 + (int)threadIdx.x, t = min(t0, ntask - 1);
+  if (t0 < ncnt) cnt[t0] = 0u;
   const int v = t / per, r = t - v * per;
   const float4* src = reinterpret_cast<const float4*>(X + (size_t)v * cols + 8 * r);
   const XQ8 q = mx_quantize(src[0], src[1]);  // every lane takes part: DPP across the 8 tasks of a group
@@ -1225,26 +1229,41 @@ struct ManyStep {
   float4 mv;
 };
 
-// NVB: 16-vector blocks a workgroup (1, 2, 4); the 4 / NVB waves of a block take the K ranges of the
-// one-vector geometry round-robin, and the ranges' partials are added in range order through LDS.
-template <bool BIAS, int NVB>
-__global__ __launch_bounds__(256) void k_gemv_q4k_many(const uint8_t* __restrict__ W, const uint8_t* __restrict__ frag,
-                                                       const float4* __restrict__ meta, float* __restrict__ Y,
-                                                       const float* __restrict__ bias, int rows, int cols, int nvec,
-                                                       uint32_t row_bytes, int KQ, int nvt) {
-  constexpr int WK = 4 / NVB;  // waves per vector block
-  __shared__ __attribute__((aligned(16))) float rec[4][4][3][16];  // [wave][group][sx, Qa, Qb][position]
+// Launch shape: NVB 16-vector blocks a workgroup (1 or 4), WK waves per block, Z workgroups per tile
+// (32 rows x 16 NVB vectors) splitting its K ranges.
+struct ManyShape {
+  int nvb, wk, z, nvt, nrt, KQ;
+};
+
+// Wave wk of split z takes the K ranges kq = z WK + wk, + WK Z, ... (kq < KQ) of the one-vector
+// geometry, walking each in that kernel's order.  The ranges' partials are added in range order
+// from 0.0f: inside the wave when it takes them all (WK = Z = 1), through LDS when the workgroup's
+// waves share them (Z = 1), and through `part` when Z > 1 (NVB = 1): each workgroup stores its
+// ranges' partials with device-coherent stores, waits for them, and counts itself in at the tile's
+// counter (zeroed by the conversion launch); the last one to arrive reads every range back in order
+// and stores the tile -- the protocol of split_k_last.
+// PF: load each step's operands one step ahead (more registers, fewer waves a SIMD); without it a
+// step's loads are issued at the end of the step before and the other waves cover their latency.
+template <bool BIAS, int NVB, int WK, bool PF>
+__global__ __launch_bounds__(64 * NVB * WK, PF ? 2 : 3) void k_gemv_q4k_many(
+    const uint8_t* __restrict__ W, const uint8_t* __restrict__ frag, const float4* __restrict__ meta,
+    float* __restrict__ Y, const float* __restrict__ bias, int rows, int cols, int nvec, uint32_t row_bytes, int KQ,
+    int nvt, int Z, float* __restrict__ part, uint32_t* __restrict__ cnt) {
+  constexpr int NW = NVB * WK;
+  __shared__ __attribute__((aligned(16))) float rec[NW][4][3][16];  // [wave][group][sx, Qa, Qb][position]
   __shared__ __attribute__((aligned(16))) float red[WK > 1 ? NVB * 16 * 64 * 8 : 4];  // [vb][kq][lane][8]
+  __shared__ int last;
   const int nsb = cols / 256;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wv = wave % NVB, wkq = wave / NVB;  // vector block, K-range phase
+  const int wv = wave % NVB, wk = wave / NVB;  // vector block, K-range phase
   int b = (int)blockIdx.x;
   {
     const int nb = (int)gridDim.x;
     if ((nb & 7) == 0) b = (b & 7) * (nb >> 3) + (b >> 3);  // an XCD takes consecutive tiles: one row block
   }
-  const int rt = b / nvt, vt = b - rt * nvt;
+  const int tile = b / Z, z = b - tile * Z;
+  const int rt = tile / nvt, vt = tile - rt * nvt;
   const int j = lane & 31, h = lane >> 5;
   const int r = rt * kManyRows + j, rr = min(r, rows - 1);
   const int vb = vt * 16 * NVB + 16 * wv;
@@ -1256,6 +1275,7 @@ __global__ __launch_bounds__(256) void k_gemv_q4k_many(const uint8_t* __restrict
   const float4* mp = meta + (size_t)min(vb + mu, nvec - 1) * nsb * 4 + mg;
   const uint32_t mw = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)&rec[wave][mg][0][many_pos(mu)];
   const uint32_t mr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)&rec[wave][0][0][8 * h];
+  float* tpart = part + (((size_t)tile * NVB + wv) * KQ) * 512 + lane * 8;  // [kq][lane][8] of this block
 
   auto load = [&](int sblk, ManyStep& d) {
     const uint8_t* wb = wp + (size_t)sblk * 144;
@@ -1267,7 +1287,6 @@ __global__ __launch_bounds__(256) void k_gemv_q4k_many(const uint8_t* __restrict
     for (int sb = 0; sb < 8; ++sb) d.av[sb] = *reinterpret_cast<const uint4*>(fb + 64 * sb);
     d.mv = mp[(size_t)sblk * 4];
   };
-  // this wave's K ranges kq = wkq, wkq + WK, ...; steps walk each range in the one-vector order
   auto range = [&](int kq, int& s0, int& s1, bool& back) {
     s0 = kq * nsb / KQ;
     s1 = (kq + 1) * nsb / KQ;
@@ -1279,55 +1298,73 @@ __global__ __launch_bounds__(256) void k_gemv_q4k_many(const uint8_t* __restrict
     range(kq, s0, s1, back);
     return back ? s1 - 1 - u : s0 + u;
   };
-
-  float acc[8][4], fin[8];
-#pragma unroll
-  for (int k = 0; k < 8; ++k) fin[k] = 0.0f;
-  // first step of the wave
-  int kq = wkq, u = 0;
+  const int qstep = WK * Z;
   auto advance = [&](int& q, int& uu) {  // next (range, position) of this wave; q >= KQ when done
     int s0, s1;
     bool back;
     range(q, s0, s1, back);
     if (++uu >= s1 - s0) {
       uu = 0;
-      for (q += WK; q < KQ; q += WK) {
+      for (q += qstep; q < KQ; q += qstep) {
         range(q, s0, s1, back);
         if (s1 > s0) break;
       }
     }
   };
+  float fin[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) fin[k] = 0.0f;
+  // a range's partial, groups as (g0 + g2) + (g1 + g3)
+  auto put = [&](int q, const float (&pk)[8]) {
+    if (Z > 1) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        __hip_atomic_store(tpart + (size_t)q * 512 + k, pk[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else if constexpr (WK > 1) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) red[((wv * KQ + q) * 64 + lane) * 8 + k] = pk[k];
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) fin[k] += pk[k];
+    }
+  };
+
+  const int q0 = z * WK + wk;
+  int kq = q0, u = 0;
   {  // skip leading empty ranges
     int s0, s1;
     bool back;
-    range(kq, s0, s1, back);
+    if (kq < KQ) range(kq, s0, s1, back);
     while (kq < KQ && s1 <= s0) {
-      kq += WK;
+      kq += qstep;
       if (kq < KQ) range(kq, s0, s1, back);
     }
   }
   ManyStep cur, nxt;
   if (kq < KQ) load(sblk_of(kq, 0), cur);
   int cur_kq = kq;
+  // ranges this wave owns that are empty still contribute (0 + 0) + (0 + 0) = +0 to their slot
+  if (Z > 1 || WK > 1) {
+    for (int q = q0; q < KQ; q += qstep) {
+      int s0, s1;
+      bool back;
+      range(q, s0, s1, back);
+      if (s1 <= s0) {
+        const float zero[8] = {};
+        put(q, zero);
+      }
+    }
+  }
+  float acc[8][4];
 #pragma unroll
   for (int k = 0; k < 8; ++k)
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[k][c] = 0.0f;
-  // ranges this wave owns that are empty still contribute (0 + 0) + (0 + 0) = +0 to their slot
-  if constexpr (WK > 1) {
-    for (int q = wkq; q < KQ; q += WK) {
-      int s0, s1;
-      bool back;
-      range(q, s0, s1, back);
-      if (s1 <= s0)
-#pragma unroll
-        for (int k = 0; k < 8; ++k) red[((wv * KQ + q) * 64 + lane) * 8 + k] = 0.0f;
-    }
-  }
   while (cur_kq < KQ) {
     int nkq = cur_kq, nu = u;
     advance(nkq, nu);
-    if (nkq < KQ) load(sblk_of(nkq, nu), nxt);  // next step's operands in flight during this one
+    if constexpr (PF)
+      if (nkq < KQ) load(sblk_of(nkq, nu), nxt);  // next step's operands in flight during this one
     // the wave's records of this super-block into its LDS rows (wave-private: no barrier)
     asm volatile("ds_write_b32 %0, %1 offset:0\n\tds_write_b32 %0, %2 offset:64\n\tds_write_b32 %0, %3 offset:128"
                  ::"v"(mw), "v"(cur.mv.x), "v"(cur.mv.y), "v"(cur.mv.z) : "memory");
@@ -1346,6 +1383,9 @@ __global__ __launch_bounds__(256) void k_gemv_q4k_many(const uint8_t* __restrict
       const i32x16_t hi = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bh, i32x16_t{}, 0, 0, 0);
       float sca, scb16, mna, mnb;
       q4k_group_scales(hd, c, sca, scb16, mna, mnb);
+      // fma((float)(16 S), scb16, p) == fma((float)S, 16 scb16, p): 16 S and 16 scb16 = the 6-bit
+      // scale are exact, so both products are the same real and the fma rounds it once
+      const float scb = scb16 * 16.0f;
       float sx[8], qa[8], qb[8];
       {
         const uint32_t ra = mr + (uint32_t)c * 192u;
@@ -1370,37 +1410,47 @@ __global__ __launch_bounds__(256) void k_gemv_q4k_many(const uint8_t* __restrict
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const int e = 4 * (k >> 1) + 2 * (k & 1);  // D rows of vector k: qh at e, ql at e + 1
-        const int ta = (int)((uint32_t)lo[e] << 7) + lo[e + 1];                        // sum n q, 2c
-        const int tb = (int)((((uint32_t)hi[e] << 7) + (uint32_t)hi[e + 1]) << 4);    // 16 sum n q, 2c+1
-        const float t = __builtin_fmaf((float)tb, scb16, (float)ta * sca);
+        const int ta = (int)((uint32_t)lo[e] << 7) + lo[e + 1];                 // sum n q, sub-block 2c
+        const int tb = (int)(((uint32_t)hi[e] << 7) + (uint32_t)hi[e + 1]);    // sum n q, 2c + 1
+        const float t = __builtin_fmaf((float)tb, scb, (float)ta * sca);
         const float w = __builtin_fmaf(qb[k], mnb, qa[k] * mna);
         acc[k][c] = __builtin_fmaf(__builtin_fmaf(d, t, -dmin * w), sx[k], acc[k][c]);
       }
     }
-    if (nkq != cur_kq) {  // the range ends: its partial, groups as (g0 + g2) + (g1 + g3)
+    if (nkq != cur_kq) {  // the range ends
+      float pk[8];
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        const float pk = (acc[k][0] + acc[k][2]) + (acc[k][1] + acc[k][3]);
-        if constexpr (WK > 1)
-          red[((wv * KQ + cur_kq) * 64 + lane) * 8 + k] = pk;
-        else
-          fin[k] += pk;
+        pk[k] = (acc[k][0] + acc[k][2]) + (acc[k][1] + acc[k][3]);
 #pragma unroll
         for (int c = 0; c < 4; ++c) acc[k][c] = 0.0f;
       }
+      put(cur_kq, pk);
     }
-    cur = nxt;
+    if constexpr (PF)
+      cur = nxt;
+    else if (nkq < KQ)
+      load(sblk_of(nkq, nu), cur);
     cur_kq = nkq;
     u = nu;
   }
-  if constexpr (WK > 1) {
+  if (Z > 1) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's partial stores have completed
     __syncthreads();
-    if (wkq != 0) return;
+    if (tid == 0)
+      last = __hip_atomic_fetch_add(cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(Z - 1);
+    __syncthreads();
+    if (!last || wk != 0) return;
     for (int q = 0; q < KQ; ++q)  // every range in order, as the one-vector kernel adds its waves
 #pragma unroll
+      for (int k = 0; k < 8; ++k)
+        fin[k] += __hip_atomic_load(tpart + (size_t)q * 512 + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else if constexpr (WK > 1) {
+    __syncthreads();
+    if (wk != 0) return;
+    for (int q = 0; q < KQ; ++q)
+#pragma unroll
       for (int k = 0; k < 8; ++k) fin[k] += red[((wv * KQ + q) * 64 + lane) * 8 + k];
-  } else {
-    // ranges with no super-block add (0 + 0) + (0 + 0) = +0, which changes nothing after the first
   }
   if (r >= rows) return;
   const float bv = BIAS ? bias[r] : 0.0f;
@@ -1411,10 +1461,38 @@ __global__ __launch_bounds__(256) void k_gemv_q4k_many(const uint8_t* __restrict
   }
 }
 
-// Workspace bytes of the many-vector form for nvec x cols (A fragments, then the records).
-size_t gemv_many_ws_bytes(int nvec, int cols) {
+// The launch shape for nvec x rows x cols.  Above 32 vectors, 64 vectors a workgroup (a wave each,
+// every K range in the wave: the weights are read once per 64 vectors).  Up to 32, 16 vectors a
+// workgroup and one wave per K range (up to 8 a workgroup, the rest split over workgroups), which
+// keeps the CUs busy on small batches and on weights of few rows.  Measured on MI355X (Q4_K 14336 x
+// 4096, 4096 x 14336, 4096 x 4096, 1024 x 4096): the 16-vector shape is 1.3-3x faster at 16 and 32
+// vectors and up to 3x slower from 128 on (it reads the weights once per 16 vectors).
+static ManyShape many_shape(int nvec, int rows, int cols, size_t row_bytes) {
+  MxGeo geo{};
+  (void)mx_geometry(rows, cols, row_bytes, geo);
+  ManyShape m{};
+  m.KQ = geo.KQ;
+  m.nrt = (rows + kManyRows - 1) / kManyRows;
+  if (nvec > 32) {
+    m.nvb = 4;
+    m.wk = 1;
+    m.z = 1;
+    m.nvt = (nvec + 63) / 64;
+  } else {
+    m.nvb = 1;
+    m.wk = m.KQ < 8 ? m.KQ : 8;
+    m.z = m.KQ / m.wk;
+    m.nvt = (nvec + 15) / 16;
+  }
+  return m;
+}
+
+// Workspace bytes of a shape: A fragments, records, then (Z > 1) the partials and the tile counters.
+static size_t many_ws_bytes(const ManyShape& m, int nvec, int cols) {
   const size_t nsb = (size_t)(cols / 256);
-  return (size_t)nvec * nsb * 512 + (size_t)nvec * nsb * 64;
+  size_t n = (size_t)nvec * nsb * 512 + (size_t)nvec * nsb * 64;
+  if (m.z > 1) n += (size_t)m.nrt * m.nvt * m.nvb * m.KQ * 512 * 4 + (size_t)m.nrt * m.nvt * 4;
+  return n;
 }
 
 // 1 if the many-vector form takes this call: the shapes the one-vector matrix-core kernel takes (its
@@ -1423,38 +1501,59 @@ int gemv_many_supported(int cols, size_t row_bytes) {
   return gemv_mx_max_nv(cols) >= 1 && row_bytes < (1u << 24) ? 1 : 0;
 }
 
-// Q4_K GEMV of nvec vectors in one weight pass per 64 vectors (bias may be null).  ws: the
+// Workspace bytes of the many-vector form for this call.
+size_t gemv_many_ws_bytes(int nvec, int rows, int cols, size_t row_bytes) {
+  return many_ws_bytes(many_shape(nvec, rows, cols, row_bytes), nvec, cols);
+}
+
+// The many-vector form with a given shape (ws: many_ws_bytes of it, 16-byte aligned).
+bool launch_gemv_q4k_many_shape(const void* w, const float* X, float* Y, const float* bias, int nvec, int rows,
+                                int cols, size_t row_bytes, void* ws, const ManyShape& m, hipStream_t s) {
+  const int nsb = cols / 256;
+  auto* frag = static_cast<uint8_t*>(ws);
+  auto* meta = reinterpret_cast<float4*>(frag + (size_t)nvec * nsb * 512);
+  float* part = reinterpret_cast<float*>(frag + (size_t)nvec * nsb * 576);
+  const int ntile = m.nrt * m.nvt;
+  uint32_t* cnt = m.z > 1 ? reinterpret_cast<uint32_t*>(part + (size_t)ntile * m.nvb * m.KQ * 512) : nullptr;
+  const int ncnt = m.z > 1 ? ntile : 0;
+  const size_t ntask = (size_t)nvec * nsb * 32;
+  const size_t nthr = ntask > (size_t)ncnt ? ntask : (size_t)ncnt;
+  k_q4k_many_conv<<<(unsigned)((nthr + 255) / 256), 256, 0, s>>>(X, nvec, cols, frag, meta, cnt, ncnt);
+  const unsigned grid = (unsigned)((int64_t)ntile * m.z);
+  const unsigned thr = (unsigned)(64 * m.nvb * m.wk);
+  const auto* wb = static_cast<const uint8_t*>(w);
+  const uint32_t rb = (uint32_t)row_bytes;
+#define QVX_MANY(B, N, K, P)                                                                                  \
+  k_gemv_q4k_many<B, N, K, P><<<grid, thr, 0, s>>>(wb, frag, meta, Y, bias, rows, cols, nvec, rb, m.KQ, m.nvt, \
+                                                   m.z, part, cnt)
+#define QVX_MANY_WK(B)                          \
+  switch (m.wk) {                               \
+    case 1: QVX_MANY(B, 1, 1, true); break;     \
+    case 2: QVX_MANY(B, 1, 2, true); break;     \
+    case 4: QVX_MANY(B, 1, 4, true); break;     \
+    default: QVX_MANY(B, 1, 8, true); break;    \
+  }
+  if (m.nvb == 4) {
+    if (bias) QVX_MANY(true, 4, 1, false);
+    else QVX_MANY(false, 4, 1, false);
+  } else if (bias) {
+    QVX_MANY_WK(true)
+  } else {
+    QVX_MANY_WK(false)
+  }
+#undef QVX_MANY_WK
+#undef QVX_MANY
+  return true;
+}
+
+// Q4_K GEMV of nvec vectors with the activations converted once (bias may be null).  ws: the
 // gemv_many_ws_bytes workspace, 16-byte aligned.  Returns false, having launched nothing, when the
 // shape is not handled here.
 bool launch_gemv_q4k_many(const void* w, const float* X, float* Y, const float* bias, int nvec, int rows, int cols,
                           size_t row_bytes, void* ws, hipStream_t s) {
   if (!gemv_many_supported(cols, row_bytes) || nvec < 1 || rows < 1 || !ws) return false;
-  MxGeo geo{};
-  (void)mx_geometry(rows, cols, row_bytes, geo);
-  const int nsb = cols / 256;
-  auto* frag = static_cast<uint8_t*>(ws);
-  auto* meta = reinterpret_cast<float4*>(frag + (size_t)nvec * nsb * 512);
-  const size_t ntask = (size_t)nvec * nsb * 32;
-  k_q4k_many_conv<<<(unsigned)((ntask + 255) / 256), 256, 0, s>>>(X, nvec, cols, frag, meta);
-  // vector blocks a workgroup: 4 (one wave each) from 64 vectors; fewer for smaller batches, whose
-  // spare waves split the K ranges instead of computing clamped duplicates
-  const int nvb = nvec > 32 ? 4 : nvec > 16 ? 2 : 1;
-  const int nvt = (nvec + 16 * nvb - 1) / (16 * nvb), nrt = (rows + kManyRows - 1) / kManyRows;
-  const unsigned grid = (unsigned)(nvt * nrt);
-  const auto* wb = static_cast<const uint8_t*>(w);
-  const uint32_t rb = (uint32_t)row_bytes;
-#define QVX_MANY(B, N) k_gemv_q4k_many<B, N><<<grid, 256, 0, s>>>(wb, frag, meta, Y, bias, rows, cols, nvec, rb, geo.KQ, nvt)
-  if (bias) {
-    if (nvb == 4) QVX_MANY(true, 4);
-    else if (nvb == 2) QVX_MANY(true, 2);
-    else QVX_MANY(true, 1);
-  } else {
-    if (nvb == 4) QVX_MANY(false, 4);
-    else if (nvb == 2) QVX_MANY(false, 2);
-    else QVX_MANY(false, 1);
-  }
-#undef QVX_MANY
-  return true;
+  return launch_gemv_q4k_many_shape(w, X, Y, bias, nvec, rows, cols, row_bytes, ws,
+                                    many_shape(nvec, rows, cols, row_bytes), s);
 }
 
 }  // namespace qvx

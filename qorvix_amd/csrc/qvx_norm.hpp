@@ -104,6 +104,8 @@ struct GemvEpi {
   bool swiglu = false;  // weight rows interleaved in 16-row (gate, up) groups; out = silu(gate) * up
   const float* bias = nullptr;  // non-null (plain calls only): out = W . x + bias, the add last
   bool no_alloc = false;  // the call must not take stream-ordered temporaries (graph-captured plans)
+  void* ws = nullptr;     // non-null: workspace the caller owns for the many-vector Q4_K form
+  size_t ws_bytes = 0;
   int flags() const { return (norm_w ? EPI_NORM : 0) | (swiglu ? EPI_SWIGLU : 0); }
 };
 

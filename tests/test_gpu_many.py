@@ -3,11 +3,13 @@ bias epilogue (qvx_qmatmul_n_bias, the reference's wmatmulNBias).
 
 The reference promises that qmatmulN is bit-identical to qmatmul per vector
 (runtime/include/qorvix/runtime/qmatmul.hpp:31-32).  The many-vector form converts the activations
-once and streams the weights once per 64 vectors; these tests hold every output to the one-vector
-call's bits (qvx_qmatmul), and to the chunked batched forms' (a plan replay, which never takes the
-many-vector form), at shapes whose one-vector geometry walks K in 4 and 16 ranges (including the
-backward walks of even ranges), with ragged rows and a vector count that is not a multiple of 64.
-The bias add is one fp32 add after the product: out == product + bias bit for bit.
+once and streams the weights once per 64 vectors (once per 16, with the K ranges split over
+workgroups, up to 32 vectors); these tests hold every output to the one-vector call's bits
+(qvx_qmatmul), and to the chunked batched forms' (calls of 8 vectors), at shapes whose one-vector
+geometry walks K in 1, 4 and 16 ranges (including the backward walks of even ranges), with ragged
+rows and vector counts on both sides of 32 and not multiples of 16 or 64.  A plan replays the
+many-vector form from its own workspace, also for calls in one fork.  The bias add is one fp32 add
+after the product: out == product + bias bit for bit.
 """
 from __future__ import annotations
 
@@ -40,8 +42,21 @@ def _many(cuda, W, t, X, rows, cols, bias=None):
     return out
 
 
+def _chunked(cuda, W, t, X, rows, cols):
+    """qvx_qmatmul_n in calls of 8 vectors: the chunked batched forms."""
+    n = X.shape[0]
+    ref = cuda.full((n, rows), float("nan"), dtype=cuda.float32, device="cuda")
+    s = cuda.cuda.current_stream().cuda_stream
+    for v0 in range(0, n, 8):
+        k = min(8, n - v0)
+        rc = qvx.qmatmul_n(ref[v0].data_ptr(), W.data_ptr(), t, X[v0].data_ptr(), k, rows, cols, s)
+        assert rc == qvx.OK, qvx.strerror(rc)
+    return ref
+
+
 @pytest.mark.parametrize("rows,cols,nvec", [(14336, 4096, 64), (4096, 14336, 100), (1000, 4096, 37),
-                                            (1024, 2048, 16), (300, 768, 130)])
+                                            (1024, 2048, 16), (300, 768, 130), (4096, 14336, 16),
+                                            (14336, 4096, 29), (128256, 4096, 20), (4096, 4096, 32)])
 def test_many_bit_identical_to_single_vector_calls(cuda, rows, cols, nvec):
     t = qvx.Q4_K
     W = _weight(cuda, t, rows, cols, seed=rows + nvec)
@@ -52,14 +67,38 @@ def test_many_bit_identical_to_single_vector_calls(cuda, rows, cols, nvec):
         assert qvx.qmatmul(one.data_ptr(), W.data_ptr(), t, X[v].data_ptr(), rows, cols) == qvx.OK
         cuda.cuda.synchronize()
         assert cuda.equal(got[v].view(cuda.int32), one.view(cuda.int32)), v
-    # the chunked batched forms (a plan replay never takes the many-vector form) agree everywhere
-    plan = decode.Plan()
-    ref = cuda.full((nvec, rows), float("nan"), dtype=cuda.float32, device="cuda")
-    plan.add(ref, decode.DevWeight(W, t, rows, cols), X, nvec)
-    plan.instantiate()
-    plan.launch(cuda.cuda.current_stream().cuda_stream)
+    # the chunked batched forms agree everywhere
+    ref = _chunked(cuda, W, t, X, rows, cols)
     cuda.cuda.synchronize()
     assert cuda.equal(got.view(cuda.int32), ref.view(cuda.int32))
+
+
+def test_plan_replays_many_vector_calls(cuda):
+    """A plan's many-vector calls (in order, and two in one fork, which need disjoint workspace
+    slices) replay bit-identically to the direct calls, several times with eager work between."""
+    t = qvx.Q4_K
+    shapes = [(4096, 14336, 16), (14336, 4096, 48), (4096, 4096, 24)]
+    Ws = [_weight(cuda, t, r, c, seed=40 + i) for i, (r, c, n) in enumerate(shapes)]
+    Xs = [qvx.fill_normal_t(cuda.empty((n, c), dtype=cuda.float32, device="cuda"), seed=50 + i)
+          for i, (r, c, n) in enumerate(shapes)]
+    want = [_many(cuda, W, t, X, r, c) for W, X, (r, c, n) in zip(Ws, Xs, shapes)]
+    outs = [cuda.full((n, r), float("nan"), dtype=cuda.float32, device="cuda") for (r, c, n) in shapes]
+    plan = decode.Plan()
+    plan.add(outs[0], decode.DevWeight(Ws[0], t, *shapes[0][:2]), Xs[0], shapes[0][2])
+    plan.fork()
+    for i in (1, 2):
+        plan.add(outs[i], decode.DevWeight(Ws[i], t, *shapes[i][:2]), Xs[i], shapes[i][2])
+    plan.join()
+    plan.instantiate()
+    s = cuda.cuda.current_stream().cuda_stream
+    for rep in range(3):
+        for o in outs:
+            o.fill_(float("nan"))
+        plan.launch(s)
+        cuda.cuda.synchronize()
+        for i in range(3):
+            assert cuda.equal(outs[i].view(cuda.int32), want[i].view(cuda.int32)), (rep, i)
+    plan.close()
 
 
 def test_many_matches_oracle_at_encoder_batch(cuda):
