@@ -284,7 +284,7 @@ def decode_sweep(torch, stream, steps, cpu=True):
                                              "per token = 32 x layer + LM head"}
             log(f"[bench] sweep M={m} CPU {kind}: {cpu_ms:.1f} ms/token ({ab / (cpu_ms * 1e-3) / 1e9:.1f} GB/s)")
     # Prefill: M prompt positions through every projection as one GEMM each (qvx_qgemm_f16, fp16 X;
-    # Q4_K on the MFMA kernels, the Q6_K tensors through the dequantising library GEMM) and the LM head
+    # Q4_K and Q6_K on the hand-written raw-block MFMA kernels) and the LM head
     # on the last position.  The reference prefills token by token (generator.cpp:24-28), one decode
     # step per position: its equivalent here is M x the M = 1 sweep time.
     def time_prefill(mdl, mp, reps=3):
@@ -520,10 +520,93 @@ def gemm_leg(torch, stream, t, wps, copies, steps, cpu):
         log(f"[bench] GEMM Q6_K ffn_down f16 M=2048: {ms * 1e3:.1f} us, {tflops:.1f} TFLOP/s "
             f"({100 * tflops / BF16_PEAK_TFLOPS:.1f}% of bf16 peak)")
         del X, Y, w6
+        # the other on-path formats' prefill GEMM (BASELINE configs[0..1] weights at M = 2048, bf16):
+        # 16-bit dequantisation of the weight, then the plain matrix-core GEMM, timed together
+        for name, tq, r, c in (("Q8_0 4096x4096", qvx.Q8_0, 4096, 4096), ("Q4_0 up 4096->11008", qvx.Q4_0, 11008, 4096),
+                               ("Q4_0 down 11008->4096", qvx.Q4_0, 4096, 11008)):
+            M = 2048
+            wq = [qvx.empty_weight(tq, r, c, dev) for _ in range(4)]
+            for i, w in enumerate(wq):
+                qvx.fill_synthetic_t(w, tq, r, c, seed=400 + i, scale_mul=1e-3)
+            X = torch.empty((M, c), dtype=torch.float16, device=dev)
+            qvx.fill_normal_t(X, seed=14, mul=0.5)
+            Y = torch.empty((M, r), dtype=torch.float32, device=dev)
+            def gq(i):
+                rc = lib.qvx_qgemm_f16(Y.data_ptr(), wq[i % 4].data_ptr(), tq, X.data_ptr(), M, r, c, qvx.GEMM_BF16, sh)
+                if rc != 0:
+                    raise RuntimeError(f"qvx_qgemm_f16 ({name}) failed: {qvx.strerror(rc)}")
+            for i in range(10):
+                gq(i)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for i in range(steps):
+                gq(i)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / steps
+            tflops = 2.0 * M * r * c / (ms * 1e-3) / 1e12
+            gemm[f"{name.split()[0].lower()}_{r}x{c}_bf16_M2048"] = {
+                "ms": round(ms, 4), "tflops": round(tflops, 1), "frac_of_bf16_peak": round(tflops / BF16_PEAK_TFLOPS, 4),
+                "shape": f"{name}, M=2048, bf16 MFMA (16-bit dequantisation + plain GEMM, one call)"}
+            log(f"[bench] GEMM {name} bf16 M=2048: {ms * 1e3:.1f} us, {tflops:.1f} TFLOP/s "
+                f"({100 * tflops / BF16_PEAK_TFLOPS:.1f}% of bf16 peak)")
+            del X, Y, wq
     except RuntimeError as e:  # report, never hide: the JSON carries the error
         gemm["error"] = str(e)
         log(f"[bench] GEMM failed: {e}")
     return gemm
+
+
+def qmatmul_n_leg(torch, stream, steps, cpu):
+    """qvx_qmatmul_n at encoder batch sizes (the reference's qmatmulN / wmatmulNBias callers, BERT /
+    CLIP / Whisper encoders at nVec 256-577): Q4_K 4096 -> 14336 with fp32 X at M = 16, 64 and 512,
+    every output bit-identical to the one-vector call.  Four seeded weight copies cycled, direct calls
+    timed with HIP events on the launch stream; the reference CPU qmatmulN beside it on 64 vectors."""
+    import qorvix_amd as qvx
+    lib, sh, dev = qvx.lib(), stream.cuda_stream, stream.device
+    t = qvx.Q4_K
+    out = {"workload": "qvx_qmatmul_n, Q4_K 4096->14336, fp32 X [M,4096], fp32 out (activations converted "
+                       "once, weights streamed once per 64 vectors)"}
+    try:
+        ws = [qvx.empty_weight(t, ROWS, COLS, dev) for _ in range(4)]
+        for i, w in enumerate(ws):
+            qvx.fill_synthetic_t(w, t, ROWS, COLS, seed=500 + i, scale_mul=1e-3)
+        for M in (16, 64, 512):
+            X = torch.empty((M, COLS), dtype=torch.float32, device=dev)
+            qvx.fill_normal_t(X, seed=15)
+            Y = torch.empty((M, ROWS), dtype=torch.float32, device=dev)
+            def q(i):
+                rc = lib.qvx_qmatmul_n(Y.data_ptr(), ws[i % 4].data_ptr(), t, X.data_ptr(), M, ROWS, COLS, sh)
+                if rc != 0:
+                    raise RuntimeError(f"qvx_qmatmul_n failed: {qvx.strerror(rc)}")
+            for i in range(10):
+                q(i)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for i in range(steps):
+                q(i)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) / steps * 1e3
+            tops = 2.0 * M * ROWS * COLS / (us * 1e-6) / 1e12
+            rec = {"us": round(us, 2), "effective_tops": round(tops, 1), "us_per_vector": round(us / M, 3)}
+            note = ""
+            if cpu and M == 64:
+                kind, fn, dot, cores = cpu_operator()
+                sec, runs = cpu_time(fn, ws[0].cpu().numpy(), t, X.cpu().numpy(), M, ROWS, COLS)
+                rec["cpu"] = {"kind": kind, "us": round(sec * 1e6, 1), "runs": runs, "threads": cores, "dot_kernel": dot}
+                note = f"; CPU {kind} {sec * 1e3:.2f} ms"
+            out[f"M{M}"] = rec
+            log(f"[bench] qmatmul_n Q4_K 4096->14336 M={M}: {us:.1f} us ({us / M:.2f} us/vector, "
+                f"{tops:.1f} effective TOP/s){note}")
+            del X, Y
+        del ws
+    except RuntimeError as e:  # report, never hide
+        out["error"] = str(e)
+        log(f"[bench] qmatmul_n failed: {e}")
+    return out
 
 
 def calibration_copy(torch, dev, mib):
@@ -670,6 +753,9 @@ def main():
             deq = {"error": str(e)}
             log(f"[bench] dequantize failed: {e}")
 
+    # ---- qmatmul_n at encoder batch sizes ---------------------------------------------------------
+    qn = {} if args.gemv_only else qmatmul_n_leg(torch, stream, args.gemm_steps, cpu=not args.no_cpu)
+
     # ---- every GEMV point of BASELINE configs[0..2] ----------------------------------------------
     cfgs = []
     if not args.gemv_only:
@@ -766,6 +852,7 @@ def main():
             "runs": gemm,
         },
         "config_gemvs": cfgs,
+        "qmatmul_n": qn,
         "sweep": sweep,
         "cpu_baseline": cpu,
         "dequant": deq,
