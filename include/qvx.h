@@ -22,13 +22,16 @@
  *  - Device entry points take device pointers and a hipStream_t passed as `void*` (NULL = the
  *    null stream).  They are asynchronous and stream-ordered, like the CUDA backend's matmulS
  *    launch (cuda/src/cuda_backend.cu:1534-1542).  They allocate no device memory, except
- *    qvx_qgemm_f16 and qvx_gemm16, which take stream-ordered temporaries (the converted activations,
- *    the partial tiles of a K split, or the dequantised weight) from a memory pool the library owns
- *    per device.
+ *    qvx_qgemm_f16, qvx_gemm16, the many-vector form of qvx_qmatmul_n and the unfused norm route,
+ *    which take stream-ordered temporaries (the converted activations, the partial tiles of a K
+ *    split, or the dequantised weight) from a memory pool the library owns per device.  Each stream
+ *    keeps its last temporary for its next call (no pool call between back-to-back calls), so a
+ *    caller that destroys a stream must first let the qvx calls issued to it finish (synchronize the
+ *    stream): a new stream may be handed the same handle.
  *  - Entry points ending in _host take host pointers and are synchronous: the exact calling
  *    convention of the reference's CPU operator, for a CPU-side drop-in.
  *  - Calls that overlap on one device are safe for distinct outputs; the library holds no
- *    mutable per-call state (the GEMM temporaries are per call and stream-ordered).
+ *    mutable per-call state (the GEMM temporaries are per call, or per stream, and stream-ordered).
  */
 #ifndef QVX_H
 #define QVX_H

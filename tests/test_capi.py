@@ -39,6 +39,18 @@ def test_nm_exports_match_header():
     assert exported == declared_functions()
 
 
+def test_library_loads_beside_torchs_hip_runtime():
+    """The library loads in a process whose HIP runtime is the one torch bundles (the GPU tests'
+    setup): every versioned HIP symbol it imports must exist there, which a call new to a later ROCm
+    (e.g. an API tagged hip_7.1) would break on the GPU box."""
+    import subprocess
+    import sys
+    code = ("import torch, ctypes, sys; sys.path.insert(0, %r); import qorvix_amd as q; "
+            "ctypes.CDLL(q.LIB_PATH); print('ok')" % ROOT)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stderr[-2000:]
+
+
 def test_version_and_errors():
     assert "gfx950" in qvx.version()
     assert qvx.strerror(qvx.E_TYPE).startswith("unsupported")

@@ -96,6 +96,12 @@ def test_gemm_q4k_stacked_gate_up_m257(cuda):
     _check_gemm(cuda, qvx.Q4_K, 257, 28672, 4096, ALL16, seed=7300)
 
 
+def test_gemm_q4k_ragged_256_token_tiles(cuda):
+    """256-token tiles (the 4-wave kernel) with a ragged last row tile and a ragged last token tile:
+    M = 1800, 14000 rows (55 columns of 256, the last of 176 rows)."""
+    _check_gemm(cuda, qvx.Q4_K, 1800, 14000, 4096, ALL16, seed=7350)
+
+
 def test_gemm_q4k_ffn_down_shape(cuda):
     """K = 14336 (a Q4_K ffn_down, 14336 -> 4096) at M = 2048 and M = 300."""
     _check_gemm(cuda, qvx.Q4_K, 2048, 4096, 14336, ALL16, seed=7400)
