@@ -120,6 +120,12 @@ __device__ inline void lds_wait8_1(u32x4* r, u32x4* w) {
 }
 
 __device__ inline uint32_t xswz(uint32_t r) { return (r ^ ((r >> 3) & 3u)) & 7u; }
+
+// Copy global -> LDS, 16 bytes a lane (a device function of its own: called from a lambda, the target
+// builtin makes the host pass drop the kernel's launch stub).
+__device__ inline void copy_lds16(__amdgpu_buffer_rsrc_t r, QVX_LDS uint8_t* dst, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, voff, soff, 0, 0);
+}
 // Quant-byte rows of a W stage are 64 bytes apart; 16-byte chunk p of row r sits at slot p ^ qswz(r),
 // which keeps the reads of 16 consecutive rows (one chunk each) on distinct banks.
 __device__ inline uint32_t qswz(uint32_t r) { return ((r >> 1) ^ (r >> 3)) & 3u; }
@@ -499,33 +505,42 @@ __global__ __launch_bounds__(512) void k_qgemm_q4k(const uint8_t* __restrict__ W
   }
 }
 
-// ---- 4-wave form: one wave per SIMD, 256 tokens x 64 weight rows a wave ----------------------------
-// k_qgemm_q4kq<VAR>: a 256-token x 256-row tile per 256-thread workgroup; wave w owns weight rows
-// 64w..64w+63 and all 256 tokens (8 x 2 tiles of v_mfma_f32_32x32x16_*, 256 accumulators in the
-// accumulation registers).  Each weight element is dequantised once per workgroup, by the wave that
-// owns its row, and each wave reads every X fragment of a slice: per K16 step 8 A fragments (8 KiB)
-// and two B fragments for 16 MFMAs, half the LDS traffic per MFMA of the 8-wave kernel above, whose
-// waves each read all BM tokens' fragments for 32 rows.  K advances in 64-element slices (group c of
-// a super-block) through three 44 KiB stages filled by buffer_load ... lds two slices ahead: X rows
-// (128 bytes, chunks swizzled as above), the 256 super-block headers (16 bytes each) and the 256 rows'
-// 32 quant bytes of group c (the two 16-byte halves of row r swapped when bit 3 of r is set, so the
-// reads of 16 consecutive rows hit distinct banks).  Lane (n, g) of row tile t takes the header and
-// quant bytes 16g..16g+15 of row 64w + 32t + n once per slice and makes the B operands of the four
-// K16 steps from them (low nibbles 0-7, 8-15, high nibbles 0-7, 8-15 -- the element order of the
-// 8-wave kernel, and the A fragments are read in that order), one step ahead, between the MFMAs,
-// with the 8-wave kernel's main-loop arithmetic (the fp16-1024 mantissa insertion and v_fma_mix
-// evaluation).  One barrier per slice, before its last step: every wave has then read the
-// slice's X, so its stage is refilled during that step, and has waited for its copies of the next
-// slice, whose headers and quant bytes it reads right after the barrier.
-template <int VAR>
+// ---- 4-wave form: one wave per SIMD, BM tokens x 64 weight rows a wave ------------------------------
+// k_qgemm_q4kq<VAR, BM>: a BM-token x 256-row tile per 256-thread workgroup; wave w owns weight rows
+// 64w..64w+63 and all BM tokens (BM/32 x 2 tiles of v_mfma_f32_32x32x16_*, the accumulators in the
+// accumulation registers).  The product runs BM = 256 (at BM = 128, with or without a K split, this
+// form measured 8-16 % slower than the 8-wave kernel on the same tiles, which keeps them).  Each weight element is dequantised once per
+// workgroup, by the wave that owns its row, and each wave reads every X fragment of a slice: per K16
+// step BM/32 A fragments and two B fragments for BM/16 MFMAs, half the LDS traffic per MFMA of the
+// 8-wave kernel above, whose waves each read all BM tokens' fragments for 32 rows.  K advances in
+// 64-element slices (group c of a super-block) through three stages filled by buffer_load ... lds
+// two slices ahead: X rows (128 bytes, chunks swizzled as above), the 256 super-block headers (16
+// bytes each) and the 256 rows' 32 quant bytes of group c (the two 16-byte halves of row r swapped
+// when bit 3 of r is set, so the reads of 16 consecutive rows hit distinct banks).  Lane (n, g) of
+// row tile t takes the header and quant bytes 16g..16g+15 of row 64w + 32t + n once per slice and
+// makes the B operands of the four K16 steps from them (low nibbles 0-7, 8-15, high nibbles 0-7,
+// 8-15 -- the element order of the 8-wave kernel, and the A fragments are read in that order), one
+// step ahead, between the MFMAs, with the 8-wave kernel's main-loop arithmetic (the fp16-1024
+// mantissa insertion and v_fma_mix evaluation).  One barrier per slice, before its last step: every
+// wave has then read the slice's X, so its stage is refilled during that step, and has waited for
+// its copies of the next slice, whose headers and quant bytes it reads right after the barrier.
+template <int VAR, int BM>
 __global__ __launch_bounds__(256) void k_qgemm_q4kq(const uint8_t* __restrict__ W, const uint16_t* __restrict__ X,
                                                     float* __restrict__ Y, GemmGeo geo, TileMap tm) {
-  constexpr int BM = 256, NST = 3;
+  static_assert(BM == 256 || BM == 128, "tile tokens");
+  constexpr int NST = 3;
+  constexpr int TT = BM / 32;           // 32-token tiles of a wave
+  constexpr int NK = 2 * TT;            // MFMAs a K16 step
   constexpr int XST = BM * 128;         // X rows of a slice
   constexpr int HST = kBN * 16;         // the tile's super-block headers
   constexpr int QST = kBN * 32;         // quant bytes of group c of the tile's rows
-  constexpr int STB = XST + HST + QST;  // 44 KiB a stage
-  constexpr int CPW = 11;               // copies per wave per slice: 8 X, 1 header, 2 quant
+  constexpr int STB = XST + HST + QST;  // one stage
+  constexpr int XC = BM / 32;           // X copies per wave per slice
+  constexpr int CPW = XC + 3;           // copies per wave per slice: X, 1 header, 2 quant
+  // slots within a step: the B operand pieces of the next step; in the last step the wait for the
+  // next slice's headers and quant bytes, its first A fragments, its scales
+  constexpr int RW = NK >= 16 ? 3 : 2;
+  auto piece_slot = [](int p) { return NK >= 16 ? 8 + 2 * p : NK - 4 + p; };
   __shared__ __attribute__((aligned(1024))) uint8_t lds[NST * STB];
   const int M = geo.M, N = geo.N, K = geo.K;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -546,7 +561,7 @@ __global__ __launch_bounds__(256) void k_qgemm_q4kq(const uint8_t* __restrict__ 
       m0 = tm.base_b + (b % tm.mt_b) * BM;
     }
   }
-  const int L = K / 64;
+  const int kb0 = 0, NJ = K / 64;  // no K split: the plan runs this kernel on grids that fill the chip
   if (m0 >= M || n0 >= N) return;
   const uint32_t xrow_bytes = (uint32_t)K * 2u;
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
@@ -554,13 +569,13 @@ __global__ __launch_bounds__(256) void k_qgemm_q4kq(const uint8_t* __restrict__ 
   const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(W + (size_t)n0 * geo.row_bytes), (short)0, (int)((uint32_t)min(kBN, N - n0) * geo.row_bytes),
       (int)kRsrcWord3);
-  // Copy offsets of this wave.  X copy i: chunk q = (8w + i) * 64 + lane -> row q / 8, LDS slot q % 8
-  // holds global chunk slot ^ xswz(row).  Header copy: row 64w + lane.  Quant copy i: LDS slot
+  // Copy offsets of this wave.  X copy i: chunk q = (XC w + i) * 64 + lane -> row q / 8, LDS slot
+  // q % 8 holds global chunk slot ^ xswz(row).  Header copy: row 64w + lane.  Quant copy i: LDS slot
   // q = (2w + i) * 64 + lane -> row q / 2, half q % 2 holds global half (q % 2) ^ (row >> 3 & 1).
-  uint32_t xoff[8], qoff[2];
+  uint32_t xoff[XC], qoff[2];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const uint32_t q = (uint32_t)((8 * wave + i) * 64 + lane), r = q >> 3, p = q & 7u;
+  for (int i = 0; i < XC; ++i) {
+    const uint32_t q = (uint32_t)((XC * wave + i) * 64 + lane), r = q >> 3, p = q & 7u;
     xoff[i] = r * xrow_bytes + 16u * (p ^ xswz(r));
   }
   const uint32_t hoff = (uint32_t)(64 * wave + lane) * geo.row_bytes;
@@ -571,16 +586,16 @@ __global__ __launch_bounds__(256) void k_qgemm_q4kq(const uint8_t* __restrict__ 
   }
   QVX_LDS uint8_t* lds_l = (QVX_LDS uint8_t*)lds;
   const uint32_t lds_base = (uint32_t)(uintptr_t)lds_l;
-  auto copy1 = [&](int j, int i) {  // copy i (0..10) of slice j
+  auto copy1 = [&](int j, int i) {  // copy i (0..CPW-1) of slice kb0 + j
     QVX_LDS uint8_t* st = lds_l + (j % NST) * STB;
-    const uint32_t sbo = (uint32_t)(j >> 2) * 144u;
-    if (i < 8)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, st + (8 * wave + i) * 1024, 16, xoff[i], (uint32_t)j * 128u, 0, 0);
-    else if (i == 8)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, st + XST + wave * 1024, 16, hoff, sbo, 0, 0);
+    const int kb = kb0 + j;
+    const uint32_t sbo = (uint32_t)(kb >> 2) * 144u;
+    if (i < XC)
+      copy_lds16(xr, st + (XC * wave + i) * 1024, xoff[i], (uint32_t)kb * 128u);
+    else if (i == XC)
+      copy_lds16(wr, st + XST + wave * 1024, hoff, sbo);
     else
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, st + XST + HST + (2 * wave + i - 9) * 1024, 16, qoff[i - 9],
-                                               sbo + 32u * (uint32_t)(j & 3), 0, 0);
+      copy_lds16(wr, st + XST + HST + (2 * wave + i - XC - 1) * 1024, qoff[i - XC - 1], sbo + 32u * (uint32_t)(kb & 3));
   };
   // A fragment reads: step s takes chunk kc = 2g + (s & 1) + 4 (s >> 1) of token row 32 tt + ln.
   const uint32_t sw = xswz((uint32_t)ln);
@@ -655,9 +670,9 @@ __global__ __launch_bounds__(256) void k_qgemm_q4kq(const uint8_t* __restrict__ 
     pin(bo[t]);
   };
 
-  f32x16_t acc[8][2];
+  f32x16_t acc[TT][2];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < TT; ++i)
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -666,28 +681,28 @@ __global__ __launch_bounds__(256) void k_qgemm_q4kq(const uint8_t* __restrict__ 
   // prologue: slices 0..2 in flight, slice 0's operands of step 0 in registers
 #pragma unroll
   for (int j = 0; j < NST; ++j)
-    if (j < L)
+    if (j < NJ)
 #pragma unroll
       for (int i = 0; i < CPW; ++i) copy1(j, i);
-  if (L > 2)
+  if (NJ > 2)
     wait_vm<2 * CPW>();
-  else if (L > 1)
+  else if (NJ > 1)
     wait_vm<CPW>();
   else
     wait_vm<0>();
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
-  u32x4 a[2][8];
+  u32x4 a[2][8];  // entries >= TT unused
   i32x4_t bf[2][2];
   Raw raw;
   Sc sc[2];
   read_raw(0, raw);
 #pragma unroll
-  for (int tt = 0; tt < 8; ++tt) a[0][tt] = read_a(0, 0, tt);
+  for (int tt = 0; tt < TT; ++tt) a[0][tt] = read_a(0, 0, tt);
   asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(raw.h[0]), "+v"(raw.h[1]), "+v"(raw.q[0]), "+v"(raw.q[1]) ::"memory");
-  lds_wait<8>(a[0]);
+  lds_wait<TT>(a[0]);
   {
-    const ScaleSel sel = scale_sel(0);
+    const ScaleSel sel = scale_sel(kb0 & 3);
     scales(raw.h[0], sel, sc[0]);
     scales(raw.h[1], sel, sc[1]);
 #pragma unroll
@@ -715,37 +730,40 @@ __global__ __launch_bounds__(256) void k_qgemm_q4kq(const uint8_t* __restrict__ 
         if constexpr (MORE) read_raw(j + 1, raw);
       }
 #pragma unroll
-      for (int k = 0; k < 16; ++k) {
+      for (int k = 0; k < NK; ++k) {
         const int tt = k >> 1, t = k & 1;
         acc[tt][t] = mfma32<VAR>(__builtin_bit_cast(i32x4_t, cur[tt]), bc[t], acc[tt][t]);
         if (s < 3) {
-          if (k < 8) nxt[k] = read_a(j, s + 1, k);
-          if (k >= 8 && (k & 1) == 0) deq_piece(raw, sc, s + 1, (k - 8) >> 1, bn);
+          if (k < TT) nxt[k] = read_a(j, s + 1, k);
+#pragma unroll
+          for (int p = 0; p < 4; ++p)
+            if (k == piece_slot(p)) deq_piece(raw, sc, s + 1, p, bn);
         } else {
           if constexpr (REFILL)
             if (k < CPW) copy1(j + NST, k);
           if constexpr (MORE) {
-            if (k == 3) {
+            if (k == RW)
               asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(raw.h[0]), "+v"(raw.h[1]), "+v"(raw.q[0]), "+v"(raw.q[1])::"memory");
-            }
-            if (k >= 4 && k < 12) nxt[k - 4] = read_a(j + 1, 0, k - 4);
-            if (k == 5) {
-              const ScaleSel sel = scale_sel((j + 1) & 3);
+            if (k > RW && k <= RW + TT) nxt[k - RW - 1] = read_a(j + 1, 0, k - RW - 1);
+            if (k == RW + 2) {
+              const ScaleSel sel = scale_sel((kb0 + j + 1) & 3);
               scales(raw.h[0], sel, sc[0]);
               scales(raw.h[1], sel, sc[1]);
             }
-            if (k >= 8 && (k & 1) == 0) deq_piece(raw, sc, 0, (k - 8) >> 1, bn);
+#pragma unroll
+            for (int p = 0; p < 4; ++p)
+              if (k == piece_slot(p)) deq_piece(raw, sc, 0, p, bn);
           }
         }
         __builtin_amdgcn_sched_barrier(0);
       }
-      if (s < 3 || MORE) lds_wait<8>(nxt);
+      if (s < 3 || MORE) lds_wait<TT>(nxt);
     }
   };
   int j = 0;
-  for (; j + NST < L; ++j) slice.template operator()<true, true, true>(j);
-  for (; j + 2 < L; ++j) slice.template operator()<false, true, true>(j);
-  for (; j + 1 < L; ++j) slice.template operator()<false, true, false>(j);
+  for (; j + NST < NJ; ++j) slice.template operator()<true, true, true>(j);
+  for (; j + 2 < NJ; ++j) slice.template operator()<false, true, true>(j);
+  for (; j + 1 < NJ; ++j) slice.template operator()<false, true, false>(j);
   slice.template operator()<false, false, false>(j);
 
 #pragma unroll
@@ -753,7 +771,7 @@ __global__ __launch_bounds__(256) void k_qgemm_q4kq(const uint8_t* __restrict__ 
     const int n = n0 + 64 * wave + 32 * t + ln;
     if (n >= N) continue;
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < TT; ++i)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int m = m0 + 32 * i + 8 * (e >> 2) + 4 * g + (e & 3);
@@ -1603,13 +1621,15 @@ bool launch_q4k(float* out, const void* w, const uint16_t* X, int M, int N, int 
   return true;
 }
 
-template <int VAR>
-bool launch_q4kq(float* out, const void* w, const uint16_t* X, int M, int N, int K, const Q4kLaunch& L, hipStream_t s) {
+template <int VAR, int BM>
+bool launch_q4kq(float* out, const void* w, const uint16_t* X, int M, int N, int K, const Q4kLaunch& L,
+                 hipStream_t s) {
   static LdsLimit lim;
-  if (!lds_ready(reinterpret_cast<const void*>(&k_qgemm_q4kq<VAR>), lim, 0)) return false;
-  if (L.bm != 256 || L.splits != 1) return false;
-  GemmGeo geo{M, N, K, (uint32_t)(K / 256) * 144u, K / 64, 0x0F0F0F0Fu, 0xF0F0F0F0u, 0x000F000Fu, 0x00F000F0u, nullptr, nullptr};
-  k_qgemm_q4kq<VAR><<<dim3(L.ntiles), 256, 0, s>>>(static_cast<const uint8_t*>(w), X, out, geo, L.tm);
+  if (!lds_ready(reinterpret_cast<const void*>(&k_qgemm_q4kq<VAR, BM>), lim, 0)) return false;
+  if (L.bm != BM || L.splits != 1) return false;
+  GemmGeo geo{M, N, K, (uint32_t)(K / 256) * 144u, K / 64, 0x0F0F0F0Fu, 0xF0F0F0F0u, 0x000F000Fu, 0x00F000F0u,
+              nullptr, nullptr};
+  k_qgemm_q4kq<VAR, BM><<<dim3(L.ntiles), 256, 0, s>>>(static_cast<const uint8_t*>(w), X, out, geo, L.tm);
   return true;
 }
 
@@ -1695,7 +1715,7 @@ template <int VAR>
 bool launch_one(float* out, const void* w, const uint16_t* X, int M, int N, int K, const Q4kLaunch& L,
                 float* part, uint32_t* cnt, hipStream_t s) {
   switch (L.bm) {
-    case 256: return L.splits == 1 ? launch_q4kq<VAR>(out, w, X, M, N, K, L, s) : false;
+    case 256: return launch_q4kq<VAR, 256>(out, w, X, M, N, K, L, s);
     case 192: return launch_q4k<VAR, 192>(out, w, X, M, N, K, L, part, cnt, s);
     case 128: return launch_q4k<VAR, 128>(out, w, X, M, N, K, L, part, cnt, s);
     default: return false;

@@ -39,6 +39,14 @@ def test_nm_exports_match_header():
     assert exported == declared_functions()
 
 
+def test_no_undefined_engine_symbols():
+    """Every kernel's launch stub is defined: a kernel whose stub the host pass dropped (a target
+    builtin called from a lambda does that) leaves an undefined qvx:: symbol that fails the load."""
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--undefined-only", qvx.LIB_PATH], capture_output=True, text=True).stdout
+    assert not [ln for ln in out.splitlines() if "3qvx" in ln], out
+
+
 def test_library_loads_beside_torchs_hip_runtime():
     """The library loads in a process whose HIP runtime is the one torch bundles (the GPU tests'
     setup): every versioned HIP symbol it imports must exist there, which a call new to a later ROCm
