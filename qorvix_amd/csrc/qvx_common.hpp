@@ -191,22 +191,23 @@ __device__ __forceinline__ bool split_k_last(float (&acc)[NA], float* __restrict
     *last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(S - 1);
   __syncthreads();
   if (!*last) return false;
-  // every partial (this split's too) is read back, so acc is free while the sums build up in it
+  // Every partial (this split's too) is read back, so acc is free while the sum builds up in it, in
+  // split order.  A split's NA loads are issued together and waited for once: one memory round trip
+  // per split (issued 16 at a time, the sums took NA / 16 round trips per split, which made the
+  // epilogue of a 4-way split cost more than its K loop at M = 128).
   static_assert(NA % 16 == 0, "accumulators come in 16s");
   auto ld = [&](int zz, int a) {
     return __hip_atomic_load(part + (size_t)zz * kSplit + (a * NTHR + tid), __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
   };
 #pragma unroll
-  for (int a0 = 0; a0 < NA; a0 += 16) {
-    float sum[16];
+  for (int a = 0; a < NA; ++a) acc[a] = ld(0, a);
+  for (int zz = 1; zz < S; ++zz) {
+    float t[NA];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) sum[j] = ld(0, a0 + j);
-    for (int zz = 1; zz < S; ++zz)
+    for (int a = 0; a < NA; ++a) t[a] = ld(zz, a);
 #pragma unroll
-      for (int j = 0; j < 16; ++j) sum[j] += ld(zz, a0 + j);
-#pragma unroll
-    for (int j = 0; j < 16; ++j) acc[a0 + j] = sum[j];
+    for (int a = 0; a < NA; ++a) acc[a] += t[a];
   }
   return true;
 }
