@@ -137,8 +137,8 @@ __device__ __attribute__((always_inline)) inline void q6_codes(const Q6Half& r, 
 }
 
 // One slot pair (h, t) of a super-block half r for this lane's row (l%32): each vector's pair sum
-// p(slot 2p) + p(slot 2p+1), for the 8 (NV = 16) or 4 (NV = 8) vectors v = 4j + 2g + b this lane's
-// accumulators hold.  xrec: the pair's converted-activation records (record (v, e) at word
+// p(slot 2p) + p(slot 2p+1), for the 8 (NV = 16), 4 (NV = 8) or 2 (NV = 4) vectors v = 4j + 2g + b
+// this lane's accumulators hold.  xrec: the pair's converted-activation records (record (v, e) at word
 // v*vstride + 20 e, the convert_task<2> layout); sxc: the pair's compact steps, sx of (e, g, 2j + b)
 // at e*NV + g*NV/2 + 2j + b.
 template <int NV>
@@ -154,11 +154,11 @@ __device__ __attribute__((always_inline)) inline void q6_pair(const Q6Half& r, i
 #pragma unroll
   for (int i = 0; i < 4; ++i) s4[i] = r.sh ? align_bytes(r.sc[i + 1], r.sc[i], 2u) : r.sc[i + 1];
   const float d = f16lo(r.d);
-  float4 sxv[2][NV / 8];
+  float sxv[2][NV / 2];
 #pragma unroll
   for (int e = 0; e < 2; ++e)
 #pragma unroll
-    for (int k = 0; k < NV / 8; ++k) sxv[e][k] = reinterpret_cast<const float4*>(sxc + e * NV + g * (NV / 2))[k];
+    for (int k = 0; k < NV / 2; ++k) sxv[e][k] = sxc[e * NV + g * (NV / 2) + k];
   // A operand of quarter q = e + 2 run: vector av, part ap, elements 8g..8g+7 of the run; lanes past
   // the launch's NV vectors hold zeros
   uint64_t av4[4];
@@ -190,8 +190,7 @@ __device__ __attribute__((always_inline)) inline void q6_pair(const Q6Half& r, i
         const int ta = (int)(((uint32_t)Ca[4 * j + 2 * b] << 7) + (uint32_t)Ca[4 * j + 2 * b + 1]);
         const int tb = (int)(((uint32_t)Cb[4 * j + 2 * b] << 7) + (uint32_t)Cb[4 * j + 2 * b + 1]);
         const int k = 2 * j + b;
-        const float4 s4v = sxv[e][k >> 2];
-        const float sx = (k & 3) == 0 ? s4v.x : (k & 3) == 1 ? s4v.y : (k & 3) == 2 ? s4v.z : s4v.w;
+        const float sx = sxv[e][k];
         float pe = L6::fold(d, sa, sb, ta, tb) * (sx * keep);
         asm volatile("" : "+v"(pe));  // rounded before the pair add, as in the VALU kernel
         if (e == 0)
@@ -346,7 +345,7 @@ template <int NV>
 __global__ __launch_bounds__(512) void k_gemv_q6w(const uint8_t* __restrict__ W, const float* __restrict__ X,
                                                   float* __restrict__ Y, int rows, int cols, int nv,
                                                   uint32_t row_bytes) {
-  static_assert(NV == 8 || NV == 16, "8 or 16 vectors a launch");
+  static_assert(NV == 4 || NV == 8 || NV == 16, "4, 8 or 16 vectors a launch");
   constexpr int NT = 32 * NV;  // conversion tasks of a super-block: (vector, slot of 8, part of 4)
   __shared__ __attribute__((aligned(16))) uint32_t xq[2][NV * 8 * 20];        // records (v, slot) of a super-block
   __shared__ __attribute__((aligned(16))) float sxc[2][4][2][2][NV / 2];     // [buf][pair][e][g][2j + b]
@@ -510,8 +509,9 @@ bool launch_gemv_q6n(const void* w, const float* X, float* Y, int nvec, int rows
     float* Yv = Y + (size_t)v0 * rows;
     bool ok;
     if (wide)
-      ok = nv <= 8 ? launch_q6w_t<8>(w, Xv, Yv, nv, rows, cols, row_bytes, s)
-                   : launch_q6w_t<16>(w, Xv, Yv, nv, rows, cols, row_bytes, s);
+      ok = nv <= 4   ? launch_q6w_t<4>(w, Xv, Yv, nv, rows, cols, row_bytes, s)
+           : nv <= 8 ? launch_q6w_t<8>(w, Xv, Yv, nv, rows, cols, row_bytes, s)
+                     : launch_q6w_t<16>(w, Xv, Yv, nv, rows, cols, row_bytes, s);
     else
       ok = nv <= 8 ? launch_q6n_t<8>(w, Xv, Yv, nv, rows, cols, geo, s)
                    : launch_q6n_t<16>(w, Xv, Yv, nv, rows, cols, geo, s);
