@@ -185,7 +185,8 @@ int qvx_interleave_rows16(void* d_dst, const void* d_a, const void* d_b, uint32_
  * engine's own matrix-core kernels (no library GEMM), each weight element rounded to fp16 / bf16
  * from its exact dequantised value.  Q4_K runs on raw-block MFMA kernels; Q6_K with X 16-byte and W
  * 4-byte aligned on its own raw-block MFMA kernels (cols a multiple of 512: the Q4_K kernels'
- * pipeline, blocks dequantised in registers; else cols a multiple of 64: a dequantising kernel).
+ * pipeline, blocks dequantised in registers; else cols a multiple of 64: a dequantising kernel),
+ * except from M = 1024 on a weight of >= 32 Mi elements, where the 16-bit route below is faster.
  * Other types, and Q6_K calls those kernels decline, are dequantised into a stream-ordered 16-bit
  * temporary (fp16, bf16 for QVX_GEMM_BF16; per panel of rows) and multiplied by the plain 16-bit MFMA
  * GEMM of qvx_gemm16.  QVX_GEMM_I8 takes Q4_K only (other types: QVX_E_TYPE).  Grids smaller than
@@ -196,7 +197,9 @@ int qvx_qgemm_f16(float* d_out, const void* d_w, uint32_t type, const uint16_t* 
 
 /* The prefill GEMM without any device allocation: the arguments, checks, kernels and results of
  * qvx_qgemm_f16, for callers that cannot allocate (code under HIP graph capture, tight serving loops,
- * harnesses that forbid hipMalloc).  No reference counterpart.  Its temporaries (the bf16 or Q8 copy
+ * harnesses that forbid hipMalloc).  No reference counterpart.  One exception: the large Q6_K calls
+ * qvx_qgemm_f16 runs through a 16-bit weight (M >= 1024, >= 32 Mi weight elements) stay on the
+ * raw-block kernel here, whose results agree with those within the GEMM tolerance, not bit for bit.  Its temporaries (the bf16 or Q8 copy
  * of X, a K split's partial tiles, and for the types without a raw-block kernel the 16-bit weight)
  * live in one fixed scratch array per device, of QVX_NOALLOC_SCRATCH_BYTES, held from the first call
  * on a device until the process ends; no call makes hipMalloc, hipFree or an allocating library

@@ -1827,7 +1827,14 @@ int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M
     const TypeInfo* ti = type_info(t);
     if (!ti) return -1;
     const size_t row_bytes = (size_t)(cols / (int)ti->block) * ti->bytes;
-    // Q6_K with an even number of blocks a row: the Q4_K kernel's pipeline (k_qgemm_q6k8) ...
+    // Q6_K with an even number of blocks a row: the Q4_K kernel's pipeline (k_qgemm_q6k8), except
+    // for large calls that may allocate: from M = 1024 on a weight of >= 32 Mi elements the weight
+    // dequantised to 16 bits and the plain GEMM are faster (measured on MI355X, ffn_down 14336 ->
+    // 4096: M = 1024 / 2048 / 4096 in 163 / 263 / 449 us against 182 / 329 / 664 on k_qgemm_q6k8,
+    // fp16), while the no-allocation call keeps the raw-block kernel (its scratch cannot hold the
+    // 16-bit weight) ...
+    if (t == T_Q6_K && !ws && M >= 1024 && (size_t)rows * (size_t)cols >= ((size_t)32 << 20))
+      return launch_qgemm_via16(out, w, t, X, M, rows, cols, variant == VAR_BF16, s, ws, ws_cap);
     if (t == T_Q6_K && q6k8_supported(w, X, cols, rows)) {
       Q4kPlan plan;
       q6k8_plan(M, rows, cols, device_cus(), plan);

@@ -66,15 +66,21 @@ def test_noalloc_matches_allocating_gemm_on_two_calls(cuda, variant):
 def test_noalloc_q6k_matches_allocating_gemm_on_two_calls(cuda, variant):
     """Q6_K (the Q4_K kernels' pipeline) through the no-allocation entry point: a 256-tile call with
     no K split (the bf16 copy of X, 56 MiB, in the scratch), then a smaller one whose four K splits
-    keep their partial tiles and counters in the scratch the first call left behind; both bit for
-    bit the allocating call's, and within the GEMM tolerance of the fp64 oracle on a row slice."""
+    keep their partial tiles and counters in the scratch the first call left behind; both within the
+    GEMM tolerance of the fp64 oracle on a row slice.  The second is bit for bit the allocating
+    call's; the first is a call the allocating entry point runs through the 16-bit weight and the
+    plain GEMM instead (M >= 1024 on a weight of >= 32 Mi elements), so there the two agree within
+    the GEMM tolerance of each other."""
     lib = qvx.lib()
     for n, (M, rows, cols) in enumerate(((2048, 4096, 14336), (128, 2048, 4096))):
         t, W, X, idx, Wd = _case(cuda, M, rows, cols, seed=950 + 10 * n + variant, t=qvx.Q6_K)
         got = _call(lib.qvx_qgemm_f16_noalloc, cuda, W, t, X, rows, cols, variant)
         want = _call(lib.qvx_qgemm_f16, cuda, W, t, X, rows, cols, variant)
         assert np.isfinite(got).all()
-        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+        if M >= 1024 and rows * cols >= 32 << 20:
+            assert max_rel(got, want.astype(np.float64)) <= GEMM_TOL
+        else:
+            np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
         X32 = X.cpu().numpy().astype(np.float64)
         assert max_rel(got[:, idx], X32 @ Wd.T) <= GEMM_TOL
 
