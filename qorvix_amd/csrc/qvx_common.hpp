@@ -192,22 +192,28 @@ __device__ __forceinline__ bool split_k_last(float (&acc)[NA], float* __restrict
   __syncthreads();
   if (!*last) return false;
   // Every partial (this split's too) is read back, so acc is free while the sum builds up in it, in
-  // split order.  A split's NA loads are issued together and waited for once: one memory round trip
-  // per split (issued 16 at a time, the sums took NA / 16 round trips per split, which made the
-  // epilogue of a 4-way split cost more than its K loop at M = 128).
+  // split order.  The loads of a split go out CH at a time (CH <= 64 accumulators) and are
+  // waited for together: one memory round trip per split and chunk.  (16 at a time, the sums took
+  // NA / 16 round trips per split, which slowed a 4-way split at M = 128; all NA at once raised a
+  // 128-accumulator kernel past the registers of two waves a SIMD.)
   static_assert(NA % 16 == 0, "accumulators come in 16s");
+  constexpr int CH = NA <= 64 ? NA : NA % 64 == 0 ? 64 : NA % 48 == 0 ? 48 : 16;
+  static_assert(NA % CH == 0, "whole chunks");
   auto ld = [&](int zz, int a) {
     return __hip_atomic_load(part + (size_t)zz * kSplit + (a * NTHR + tid), __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
   };
 #pragma unroll
-  for (int a = 0; a < NA; ++a) acc[a] = ld(0, a);
-  for (int zz = 1; zz < S; ++zz) {
-    float t[NA];
+  for (int a0 = 0; a0 < NA; a0 += CH) {
 #pragma unroll
-    for (int a = 0; a < NA; ++a) t[a] = ld(zz, a);
+    for (int a = 0; a < CH; ++a) acc[a0 + a] = ld(0, a0 + a);
+    for (int zz = 1; zz < S; ++zz) {
+      float t[CH];
 #pragma unroll
-    for (int a = 0; a < NA; ++a) acc[a] += t[a];
+      for (int a = 0; a < CH; ++a) t[a] = ld(zz, a0 + a);
+#pragma unroll
+      for (int a = 0; a < CH; ++a) acc[a0 + a] += t[a];
+    }
   }
   return true;
 }
