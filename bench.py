@@ -35,7 +35,7 @@ BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 / fp16 MFMA
 ROWS, COLS = 14336, 4096       # Q4_K gate/up projection of Llama-3-8B
 Q4K_ROW_BYTES = COLS // 256 * 144
 GEMV_KERNEL = "qvx::k_gemv_mx<1, 2, 1, 0>"   # matrix-core Q4_K GEMV, one vector per launch, no fused epilogue
-GEMM_KERNEL = "qvx::k_qgemm_q4kq<0> + qvx::k_qgemm_q4k<0, 192>"  # bf16, the two launches of the M=2048 plan
+GEMM_KERNEL = "qvx::k_qgemm_q4kq<0, 256> + qvx::k_qgemm_q4k<0, 192>"  # bf16, the two launches of the M=2048 plan
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4k_gemv_4096x14336_m1.traffic.json")
 
 
