@@ -101,8 +101,9 @@ int qvx_qmatmul(float* d_out, const void* d_w, uint32_t type, const float* d_x, 
 
 /* out[v * rows + r] for v < n_vec.  Replaces qmatmulN (qmatmul.cpp:64-115).  Each output is
  * bit-identical to qvx_qmatmul on that vector, as the reference promises (qmatmul.hpp:31-32).
- * Q4_K batches of 16 vectors or more on the one-vector kernel's shapes (cols a multiple of 256 up to
- * 32768, aligned operands) run on a many-vector form: the activations are converted once into a
+ * Q4_K batches of 12 vectors or more on weights of >= 32 Mi elements, and of 24 or more on smaller
+ * ones, on the one-vector kernel's shapes (cols a multiple of 256 up to 32768, aligned operands) run
+ * on a many-vector form: the activations are converted once into a
  * stream-ordered temporary from the library's pool (nvec * cols * 2.25 bytes, plus 2 KiB per 32-row
  * tile and K range for batches up to 32 vectors), then the weights are streamed once per 64 vectors
  * (once per 16 up to 32 vectors) -- the reference's "dequantize each block once for all nVec dot
@@ -115,8 +116,8 @@ int qvx_qmatmul_n(float* d_out, const void* d_w, uint32_t type, const float* d_X
 /* out[v * rows + r] = (W . X[v])[r] + bias[r] (d_bias [rows] fp32; NULL: no bias, exactly
  * qvx_qmatmul_n): the reference's wmatmulBias / wmatmulNBias (runtime/include/qorvix/runtime/
  * weights.hpp:58-80), the bias added after the product in fp32, so each output is the bit pattern of
- * qvx_qmatmul_n's output plus bias[r].  The arguments and checks of qvx_qmatmul_n.  Q4_K batches of
- * 16 vectors or more run on the many-vector form (below), which adds the bias in its epilogue; other
+ * qvx_qmatmul_n's output plus bias[r].  The arguments and checks of qvx_qmatmul_n.  The Q4_K batches
+ * qvx_qmatmul_n runs on its many-vector form (above) add the bias in its epilogue; other
  * calls run the product, then one bias-add launch. */
 int qvx_qmatmul_n_bias(float* d_out, const void* d_w, uint32_t type, const float* d_X, const float* d_bias,
                        int n_vec, int rows, int cols, void* stream);

@@ -142,10 +142,18 @@ inline int check_matmul(uint32_t type, int cols, const TypeInfo** ti) {
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Whether a Q4_K batch takes the many-vector form rather than chunks of 8 vectors.  The form costs
+// a conversion launch and a K-range chain per wave whatever the batch (17-22 us in graph replays on
+// MI355X), against ~10 us per 8-vector chunk of a 4096 x 4096 weight and 14-26 us of a 58.7 M-element
+// one: measured, it wins from 12 vectors on weights of >= 32 Mi elements (14336 x 4096 at 12: 20.2
+// against 24.3 us; 4096 x 14336: 32.8 against 41.4), and on smaller weights only from ~24 (4096 x
+// 4096 at 16: 22 against 19 us).
+inline bool many_batch(int nvec, int rows, int cols) {
+  return nvec >= 24 || (nvec >= 12 && (int64_t)rows * cols >= ((int64_t)32 << 20));
+}
+
 // Q4_K: the vector count a chunk may have on the one-vector matrix-core kernel before the batched
 // forms take over (measured faster there), and whether the whole-row batched form takes the row.
-// Smallest Q4_K batch the many-vector form takes (measured crossover with the chunked forms).
-constexpr int kManyMin = 16;
 
 inline int q4k_small(int cols) { return std::min(gemv_mxb_supported(cols) ? 3 : 2, gemv_mx_max_nv(cols)); }
 
@@ -202,7 +210,7 @@ int gemv_unfused(float* out, const void* w, uint32_t type, const float* X, int n
 // Workspace bytes of the many-vector Q4_K form if a call takes it, else 0.
 inline size_t many_route_bytes(uint32_t type, int nvec, int rows, int cols, size_t row_bytes, bool fast,
                                const GemvEpi& epi) {
-  if (!fast || type != T_Q4_K || epi.flags() || nvec < kManyMin || rows <= 0 || cols <= 0 ||
+  if (!fast || type != T_Q4_K || epi.flags() || rows <= 0 || cols <= 0 || !many_batch(nvec, rows, cols) ||
       !gemv_many_supported(cols, row_bytes))
     return 0;
   return gemv_many_ws_bytes(nvec, rows, cols, row_bytes);
@@ -226,7 +234,7 @@ int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int
   const bool fast = aligned16(w) && aligned16(X) && row_bytes % 16 == 0;
   if (epi.flags() && !fused_route(type, nvec, rows, cols, row_bytes, fast, epi))
     return gemv_unfused(out, w, type, X, nvec, rows, cols, s, epi);
-  // Q4_K batches of kManyMin vectors or more (encoder and prefill sizes): activations converted once,
+  // Q4_K batches of 12-24 vectors or more (many_batch; encoder and prefill sizes): activations converted once,
   // the weights streamed once per 64 vectors, bit-identical per vector to the one-vector kernel
   // (k_gemv_q4k_many), with the bias added in its epilogue.  Its workspace is the caller's (a plan
   // sizes one at instantiation) or a stream-ordered temporary; a call that may not allocate and has

@@ -4,7 +4,8 @@ bias epilogue (qvx_qmatmul_n_bias, the reference's wmatmulNBias).
 The reference promises that qmatmulN is bit-identical to qmatmul per vector
 (runtime/include/qorvix/runtime/qmatmul.hpp:31-32).  The many-vector form converts the activations
 once and streams the weights once per 64 vectors (once per 16, with the K ranges split over
-workgroups, up to 32 vectors); these tests hold every output to the one-vector call's bits
+workgroups, up to 32 vectors; it takes batches from 12 vectors on weights of >= 32 Mi elements and
+from 24 on smaller ones); these tests hold every output to the one-vector call's bits
 (qvx_qmatmul), and to the chunked batched forms' (calls of 8 vectors), at shapes whose one-vector
 geometry walks K in 1, 4 and 16 ranges (including the backward walks of even ranges), with ragged
 rows and vector counts on both sides of 32 and not multiples of 16 or 64.  A plan replays the
@@ -55,8 +56,9 @@ def _chunked(cuda, W, t, X, rows, cols):
 
 
 @pytest.mark.parametrize("rows,cols,nvec", [(14336, 4096, 64), (4096, 14336, 100), (1000, 4096, 37),
-                                            (1024, 2048, 16), (300, 768, 130), (4096, 14336, 16),
-                                            (14336, 4096, 29), (128256, 4096, 20), (4096, 4096, 32)])
+                                            (1024, 2048, 24), (300, 768, 130), (4096, 14336, 16),
+                                            (14336, 4096, 12), (14336, 4096, 29), (128256, 4096, 20),
+                                            (4096, 4096, 32)])
 def test_many_bit_identical_to_single_vector_calls(cuda, rows, cols, nvec):
     t = qvx.Q4_K
     W = _weight(cuda, t, rows, cols, seed=rows + nvec)
