@@ -51,6 +51,9 @@ int q4k_plan_desc(int M, int N, int K, int cus, int* desc, int cap);
 bool gemv_q6n_supported(int rows, int cols, size_t row_bytes);
 bool launch_gemv_q6n(const void* w, const float* X, float* Y, int nvec, int rows, int cols, size_t row_bytes,
                      hipStream_t s);
+bool gemv_q6s_route(int nvec, int rows, int cols, size_t row_bytes, size_t* ws_bytes);
+bool launch_gemv_q6s(const void* w, const float* X, float* Y, int nvec, int rows, int cols, size_t row_bytes,
+                     void* ws, hipStream_t s);
 int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M, int rows, int cols,
                  int variant, hipStream_t s, void* ws, size_t ws_cap);
 int launch_gemm16_entry(float* out, const uint16_t* X, const uint16_t* B, int M, int N, int K, bool bf16,
@@ -207,13 +210,18 @@ int gemv_unfused(float* out, const void* w, uint32_t type, const float* X, int n
 // out = W . x per vector, optionally with the activations normalised (epi.norm_w) and / or the
 // interleaved gate|up rows gated (epi.swiglu: rows / 2 outputs a vector).  The argument checks are
 // the plain operator's.
-// Workspace bytes of the many-vector Q4_K form if a call takes it, else 0.
-inline size_t many_route_bytes(uint32_t type, int nvec, int rows, int cols, size_t row_bytes, bool fast,
-                               const GemvEpi& epi) {
-  if (!fast || type != T_Q4_K || epi.flags() || rows <= 0 || cols <= 0 || !many_batch(nvec, rows, cols) ||
-      !gemv_many_supported(cols, row_bytes))
-    return 0;
-  return gemv_many_ws_bytes(nvec, rows, cols, row_bytes);
+// Workspace bytes of the form a call takes if that form needs one (the many-vector Q4_K form, the
+// split Q6_K form), else 0.
+inline size_t ws_route_bytes(uint32_t type, int nvec, int rows, int cols, size_t row_bytes, bool fast,
+                             const GemvEpi& epi) {
+  if (!fast || epi.flags() || rows <= 0 || cols <= 0) return 0;
+  if (type == T_Q4_K) {
+    if (!many_batch(nvec, rows, cols) || !gemv_many_supported(cols, row_bytes)) return 0;
+    return gemv_many_ws_bytes(nvec, rows, cols, row_bytes);
+  }
+  size_t need = 0;
+  if (type == T_Q6_K && q6_batched(nvec, rows) && gemv_q6s_route(nvec, rows, cols, row_bytes, &need)) return need;
+  return 0;
 }
 
 int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int rows, int cols, hipStream_t s,
@@ -234,18 +242,24 @@ int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int
   const bool fast = aligned16(w) && aligned16(X) && row_bytes % 16 == 0;
   if (epi.flags() && !fused_route(type, nvec, rows, cols, row_bytes, fast, epi))
     return gemv_unfused(out, w, type, X, nvec, rows, cols, s, epi);
-  // Q4_K batches of 12-24 vectors or more (many_batch; encoder and prefill sizes): activations converted once,
-  // the weights streamed once per 64 vectors, bit-identical per vector to the one-vector kernel
-  // (k_gemv_q4k_many), with the bias added in its epilogue.  Its workspace is the caller's (a plan
-  // sizes one at instantiation) or a stream-ordered temporary; a call that may not allocate and has
-  // no workspace keeps the chunked forms below.
-  if (const size_t need = many_route_bytes(type, nvec, rows, cols, row_bytes, fast, epi)) {
+  // Forms with a workspace, which is the caller's (a plan sizes one at instantiation) or a
+  // stream-ordered temporary; a call that may not allocate and has no workspace keeps the forms
+  // below.
+  //  * Q4_K batches of 12-24 vectors or more (many_batch; encoder and prefill sizes): activations
+  //    converted once, the weights streamed once per 64 vectors, bit-identical per vector to the
+  //    one-vector kernel (k_gemv_q4k_many), with the bias added in its epilogue.
+  //  * Q6_K batches on weights of fewer than 65536 rows (q6_batched): the K range split over
+  //    workgroups (k_gemv_q6s), bit-identical per vector to the VALU kernel; a bias is added after.
+  if (const size_t need = ws_route_bytes(type, nvec, rows, cols, row_bytes, fast, epi)) {
     const bool own = epi.ws && epi.ws_bytes >= need;
     void* ws = own ? epi.ws : epi.no_alloc ? nullptr : gemm_temp_alloc(need, s);
     if (ws) {
-      const bool ok = launch_gemv_q4k_many(w, X, out, epi.bias, nvec, rows, cols, row_bytes, ws, s);
+      const bool ok = type == T_Q4_K
+                          ? launch_gemv_q4k_many(w, X, out, epi.bias, nvec, rows, cols, row_bytes, ws, s)
+                          : launch_gemv_q6s(w, X, out, nvec, rows, cols, row_bytes, ws, s);
       if (!own) gemm_temp_free(ws, s);
       if (!ok) return refused();
+      if (type != T_Q4_K && epi.bias) launch_add_bias(out, epi.bias, nvec, rows, s);
       return hip_status();
     }
   }
@@ -733,7 +747,7 @@ static size_t plan_ws_layout(qvx_plan& plan) {
       if (!ti || ti->block == 0) continue;
       const size_t row_bytes = (size_t)(c.cols / (int)ti->block) * ti->bytes;
       const bool fast = aligned16(c.w) && aligned16(c.X) && row_bytes % 16 == 0;
-      const size_t need = many_route_bytes(c.type, c.nvec, c.rows, c.cols, row_bytes, fast, c.epi);
+      const size_t need = ws_route_bytes(c.type, c.nvec, c.rows, c.cols, row_bytes, fast, c.epi);
       if (!need) continue;
       c.ws_off = off;
       c.ws_bytes = need;

@@ -92,11 +92,9 @@ struct Q6Half {
   u32x3a4_t ql[4], qh[2];
   uint32_t sc[5], d, sh;
 };
-// Loads half h's pieces; the scales, d and misalignment with h = 0, from `first` (the same
-// super-block's half 0) with h = 1.
-__device__ __attribute__((always_inline)) inline void q6_load_half(const uint8_t* base, int g, int h,
-                                                                   const Q6Half& first, Q6Half& r) {
-  const uint32_t sh = (uint32_t)(uintptr_t)base & 3u;
+// The code pieces of half h (ql, qh windows) and the super-block's scales, d and misalignment.
+__device__ __attribute__((always_inline)) inline void q6_load_codes(const uint8_t* base, uint32_t sh, int g, int h,
+                                                                    Q6Half& r) {
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int off = 64 * h + 32 * (k >> 1) + 16 * (k & 1) + 8 * g;
@@ -107,18 +105,34 @@ __device__ __attribute__((always_inline)) inline void q6_load_half(const uint8_t
     const int off = 128 + 32 * h + 16 * k + 8 * g;
     r.qh[k] = *reinterpret_cast<const u32x3a4_t*>(base + off - sh);
   }
-  if (h == 0) {
-    r.sh = sh;
-    const uint8_t* sw = base + 190 - ((sh + 2u) & 3u);  // [188, 208) or [190, 210) of the super-block
+}
+__device__ __attribute__((always_inline)) inline void q6_load_scales(const uint8_t* base, uint32_t sh, Q6Half& r) {
+  r.sh = sh;
+  const uint8_t* sw = base + 190 - ((sh + 2u) & 3u);  // [188, 208) or [190, 210) of the super-block
 #pragma unroll
-    for (int k = 0; k < 5; ++k) r.sc[k] = ldg4(sw + 4 * k);
-    r.d = ldg2(base + 208);
+  for (int k = 0; k < 5; ++k) r.sc[k] = ldg4(sw + 4 * k);
+  r.d = ldg2(base + 208);
+}
+// Loads half h's pieces; the scales, d and misalignment with h = 0, from `first` (the same
+// super-block's half 0) with h = 1.
+__device__ __attribute__((always_inline)) inline void q6_load_half(const uint8_t* base, int g, int h,
+                                                                   const Q6Half& first, Q6Half& r) {
+  const uint32_t sh = (uint32_t)(uintptr_t)base & 3u;
+  q6_load_codes(base, sh, g, h, r);
+  if (h == 0) {
+    q6_load_scales(base, sh, r);
   } else {
     r.sh = first.sh;
 #pragma unroll
     for (int k = 0; k < 5; ++k) r.sc[k] = first.sc[k];
     r.d = first.d;
   }
+}
+// Half h's pieces and its super-block's scales (a step that does not follow its half 0).
+__device__ __attribute__((always_inline)) inline void q6_load_step(const uint8_t* base, int g, int h, Q6Half& r) {
+  const uint32_t sh = (uint32_t)(uintptr_t)base & 3u;
+  q6_load_codes(base, sh, g, h, r);
+  q6_load_scales(base, sh, r);
 }
 // 16 signed codes (code - 32) of quarter Q (elements 8g..8g+7 of it) of pair t as two dwords.
 template <int Q>
@@ -136,36 +150,45 @@ __device__ __attribute__((always_inline)) inline void q6_codes(const Q6Half& r, 
   }
 }
 
+// A lane's activation operands of one slot pair: its four A fragments (quarter q = e + 2 run: vector
+// av = l%32 / 2, part ap = l%2 (qh / ql), elements 8g..8g+7 of the run; lanes past the launch's NV
+// vectors hold zeros) and the steps sx of the NV/2 vectors v = 4j + 2g + b its accumulators hold.
+template <int NV>
+struct Q6Act {
+  uint64_t a[4];
+  float sx[2][NV / 2];
+};
+// Reads a pair's operands from its converted-activation records (record (v, e) at word v*vstride +
+// 20 e, the convert_task<2> layout) and compact steps (sx of (e, g, 2j + b) at e*NV + g*NV/2 + 2j + b),
+// in LDS or in global memory.
+template <int NV>
+__device__ __attribute__((always_inline)) inline void q6_act_load(const uint32_t* xrec, int vstride, const float* sxc,
+                                                                  int lane, Q6Act<NV>& x) {
+  const int ln = lane & 31, g = lane >> 5, av = ln >> 1, ap = ln & 1;
+#pragma unroll
+  for (int e = 0; e < 2; ++e)
+#pragma unroll
+    for (int k = 0; k < NV / 2; ++k) x.sx[e][k] = sxc[e * NV + g * (NV / 2) + k];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    x.a[q] = av < NV ? *reinterpret_cast<const uint64_t*>(xrec + av * vstride + (q & 1) * 20 + ap * 8 + 4 * (q >> 1) + 2 * g)
+                     : 0ull;
+}
+
 // One slot pair (h, t) of a super-block half r for this lane's row (l%32): each vector's pair sum
 // p(slot 2p) + p(slot 2p+1), for the 8 (NV = 16), 4 (NV = 8) or 2 (NV = 4) vectors v = 4j + 2g + b
-// this lane's accumulators hold.  xrec: the pair's converted-activation records (record (v, e) at word
-// v*vstride + 20 e, the convert_task<2> layout); sxc: the pair's compact steps, sx of (e, g, 2j + b)
-// at e*NV + g*NV/2 + 2j + b.
+// this lane's accumulators hold.
 template <int NV>
-__device__ __attribute__((always_inline)) inline void q6_pair(const Q6Half& r, int h, int t, const uint32_t* xrec,
-                                                              int vstride, const float* sxc, int lane,
-                                                              float (&P)[NV / 2]) {
+__device__ __attribute__((always_inline)) inline void q6_pair_fold(const Q6Half& r, int h, int t, const Q6Act<NV>& x,
+                                                                   int lane, float (&P)[NV / 2]) {
   using L6 = Lane<T_Q6_K>;
   constexpr int NJ = NV / 4;
-  const int ln = lane & 31, g = lane >> 5, av = ln >> 1, ap = ln & 1;
   const float keep = 1.0f;
   // 6-bit scales of slots e = 0, 1: sc[8h + t + 2e] and sc[8h + t + 2e + 4]
   uint32_t s4[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) s4[i] = r.sh ? align_bytes(r.sc[i + 1], r.sc[i], 2u) : r.sc[i + 1];
   const float d = f16lo(r.d);
-  float sxv[2][NV / 2];
-#pragma unroll
-  for (int e = 0; e < 2; ++e)
-#pragma unroll
-    for (int k = 0; k < NV / 2; ++k) sxv[e][k] = sxc[e * NV + g * (NV / 2) + k];
-  // A operand of quarter q = e + 2 run: vector av, part ap, elements 8g..8g+7 of the run; lanes past
-  // the launch's NV vectors hold zeros
-  uint64_t av4[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q)
-    av4[q] = av < NV ? *reinterpret_cast<const uint64_t*>(xrec + av * vstride + (q & 1) * 20 + ap * 8 + 4 * (q >> 1) + 2 * g)
-                     : 0ull;
   float p0[NV / 2];
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
@@ -179,8 +202,8 @@ __device__ __attribute__((always_inline)) inline void q6_pair(const Q6Half& r, i
     }
     typedef int v16i __attribute__((ext_vector_type(16)));
     const v16i zero = {};
-    const v16i Ca = __builtin_amdgcn_mfma_i32_32x32x16_i8((long)av4[e], (long)(((uint64_t)ca[1] << 32) | ca[0]), zero, 0, 0, 0);
-    const v16i Cb = __builtin_amdgcn_mfma_i32_32x32x16_i8((long)av4[e + 2], (long)(((uint64_t)cb[1] << 32) | cb[0]), zero, 0, 0, 0);
+    const v16i Ca = __builtin_amdgcn_mfma_i32_32x32x16_i8((long)x.a[e], (long)(((uint64_t)ca[1] << 32) | ca[0]), zero, 0, 0, 0);
+    const v16i Cb = __builtin_amdgcn_mfma_i32_32x32x16_i8((long)x.a[e + 2], (long)(((uint64_t)cb[1] << 32) | cb[0]), zero, 0, 0, 0);
     const float sa = (float)(int)__builtin_amdgcn_sbfe((int)s4[2 * h], 8u * (uint32_t)(t + 2 * e), 8u);
     const float sb = (float)(int)__builtin_amdgcn_sbfe((int)s4[2 * h + 1], 8u * (uint32_t)(t + 2 * e), 8u);
 #pragma unroll
@@ -190,7 +213,7 @@ __device__ __attribute__((always_inline)) inline void q6_pair(const Q6Half& r, i
         const int ta = (int)(((uint32_t)Ca[4 * j + 2 * b] << 7) + (uint32_t)Ca[4 * j + 2 * b + 1]);
         const int tb = (int)(((uint32_t)Cb[4 * j + 2 * b] << 7) + (uint32_t)Cb[4 * j + 2 * b + 1]);
         const int k = 2 * j + b;
-        const float sx = sxv[e][k];
+        const float sx = x.sx[e][k];
         float pe = L6::fold(d, sa, sb, ta, tb) * (sx * keep);
         asm volatile("" : "+v"(pe));  // rounded before the pair add, as in the VALU kernel
         if (e == 0)
@@ -199,6 +222,15 @@ __device__ __attribute__((always_inline)) inline void q6_pair(const Q6Half& r, i
           P[k] = p0[k] + pe;
       }
   }
+}
+
+template <int NV>
+__device__ __attribute__((always_inline)) inline void q6_pair(const Q6Half& r, int h, int t, const uint32_t* xrec,
+                                                              int vstride, const float* sxc, int lane,
+                                                              float (&P)[NV / 2]) {
+  Q6Act<NV> x;
+  q6_act_load<NV>(xrec, vstride, sxc, lane, x);
+  q6_pair_fold<NV>(r, h, t, x, lane, P);
 }
 
 template <int NV>
@@ -516,6 +548,306 @@ bool launch_gemv_q6n(const void* w, const float* X, float* Y, int nvec, int rows
       ok = nv <= 8 ? launch_q6n_t<8>(w, Xv, Yv, nv, rows, cols, geo, s)
                    : launch_q6n_t<16>(w, Xv, Yv, nv, rows, cols, geo, s);
     if (!ok) return false;
+  }
+  return true;
+}
+
+// ---- batched Q6_K with the K range split over workgroups ---------------------------------------
+// The narrow form's arithmetic and summation order, re-cut for weights whose 32-row tiles are too
+// few to fill the chip one workgroup each (4096-row weights: 128 tiles):
+//  * Workgroup b (16 waves) owns 64-slot block blk = b % nb of its rows and the tiles b / nb,
+//    b / nb + P, ... (P workgroups a block).  Wave w owns step w of the block (a step is one half
+//    super-block: the block's slot pairs 2w and 2w + 1), so its activation operands -- the
+//    convert_task<2> records and steps of those two pairs for every vector -- are the same for
+//    every tile: the wave converts them once, through LDS, into registers.
+//  * Tiles stream through a two-stage LDS ring: a tile's block (32 rows x 1680 bytes) is copied by
+//    buffer_load_dword ... lds (rows 421 dwords apart: on distinct banks) while the previous tile is
+//    folded.  Each
+//    wave folds its step for the tile's 32 rows ((pair 0) + (pair 1), the narrow form's step
+//    sum) and the workgroup sums the 16 steps as a balanced tree, which is the narrow form's
+//    unit = (H0 + H1) + (H2 + H3), block = (U0 + U1) + (U2 + U3).
+//  * A row of one block is written as it is.  Otherwise the block sums go to the workspace and a
+//    second launch (k_q6s_sum) adds each output's nb block sums in block order from 0.0f.
+// Each output therefore has the narrow form's bits, which are the VALU kernel's.
+#define QVX_LDS __attribute__((address_space(3)))
+constexpr uint32_t kQ6sRsrcWord3 = 0x00020000u;              // raw buffer, 32-bit data (gfx9)
+constexpr int kQ6sRowBytes = 8 * 210;                        // a row's 64-slot block
+constexpr int kQ6sRowWords = kQ6sRowBytes / 4 + 1;           // LDS dwords a staged row: odd, so 32 rows
+                                                             // fall on distinct banks
+constexpr int kQ6sStage = 32 * kQ6sRowWords * 4;             // LDS bytes of a ring stage
+constexpr int kQ6sRowCopies = (kQ6sRowBytes / 4 + 63) / 64;  // 64-dword copies a row: 7, the last one
+constexpr int kQ6sLastLanes = kQ6sRowBytes / 4 - 64 * (kQ6sRowCopies - 1);  // ... 36 lanes wide
+constexpr int kQ6sWaveCopies = 2 * kQ6sRowCopies;            // copies a wave a tile (2 rows): 14
+
+// Copy global -> LDS, 4 bytes a lane (buffer_load_dword ... lds: lane l's dword, from byte voff +
+// soff of the buffer, lands at LDS byte dst + 4 l).  Written as inline asm so that the compiler,
+// which does not see it as an LDS write, inserts no wait for it before LDS reads: the kernel waits
+// for its copies itself (q6s_wait_vm), which lets one stage be read while the other is being copied
+// into.  The s_nop is the wait state the hardware needs between the M0 write and the copy.
+__device__ inline void q6s_copy4(__amdgpu_buffer_rsrc_t r, uint32_t dst, uint32_t voff, uint32_t soff) {
+  asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(dst)
+               : "memory");
+}
+// s_waitcnt vmcnt(N), other counters untouched (gfx9 encoding); a compiler barrier for memory.
+template <int N>
+__device__ inline void q6s_wait_vm() {
+  static_assert(N >= 0 && N < 63, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// A 16-byte global load whose wait the kernel places itself (q6s_wait_x): the compiler, which does
+// not see the load, does not wait for the ring copies issued after it before the value's first use.
+typedef float q6s_f4 __attribute__((ext_vector_type(4)));
+__device__ inline q6s_f4 q6s_ldx(const float* p) {
+  q6s_f4 r;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p));
+  return r;
+}
+// Waits until at most N vector memory operations are outstanding; the loaded values are operands,
+// so no use of them moves above the wait.
+template <int N>
+__device__ inline void q6s_wait_x(q6s_f4* a, q6s_f4* b, int n) {
+  if (n == 2)
+    asm volatile("s_waitcnt vmcnt(%4)" : "+v"(a[0]), "+v"(a[1]), "+v"(b[0]), "+v"(b[1]) : "n"(N) : "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(%8)"
+                 : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3])
+                 : "n"(N)
+                 : "memory");
+}
+// Workgroup barrier for LDS only: this wave's LDS accesses complete, then s_barrier.  (__syncthreads
+// would also wait for the ring's copies in flight.)
+__device__ inline void q6s_lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+struct Q6sGeo {
+  int nb;     // 64-slot blocks a row (cols / 2048)
+  int ntile;  // 32-row tiles
+  int P;      // workgroups a block
+  uint32_t row_bytes;
+};
+
+template <int NV>
+__global__ __launch_bounds__(1024) void k_gemv_q6s(const uint8_t* __restrict__ W, const float* __restrict__ X,
+                                                   float* __restrict__ Y, int rows, int cols, int nv, Q6sGeo geo,
+                                                   float* __restrict__ part) {
+  static_assert(NV == 8 || NV == 16, "8 or 16 vectors a launch");
+  using L6 = Lane<T_Q6_K>;
+  constexpr int NJ = NV / 4, NO = NV * 32;
+  constexpr int RW = NV * 40 + 2 * NV;  // words of one pair's converted operands: records, then steps
+  static_assert(16 * 2 * RW * 4 <= kQ6sStage + 16 * NO * 4, "conversion scratch fits in stage 1 + sums");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kQ6sStage + (NV == 8 ? 2 : 1) * 16 * NO * 4];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ln = lane & 31, g = lane >> 5;
+  const int blk = (int)blockIdx.x % geo.nb, pi = (int)blockIdx.x / geo.nb;
+  const int ntl = pi < geo.ntile ? (geo.ntile - pi + geo.P - 1) / geo.P : 0;  // tiles of this workgroup
+  const uint32_t lds_base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(QVX_LDS uint8_t*)lds);
+
+  // Copy of the workgroup's j-th tile into stage s: wave w copies rows 2w and 2w + 1, each row's
+  // block as 7 copies of 64 dwords (the last one 36 lanes wide) into kQ6sRowWords dwords of LDS (the
+  // last dword is padding, never written).  Rows past the weight repeat its last row.
+  auto issue = [&](int j, int s) __attribute__((always_inline)) {
+    const int r0 = (pi + j * geo.P) * 32, nr = min(32, rows - r0);
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(W + (size_t)r0 * geo.row_bytes), (short)0, (int)((uint32_t)nr * geo.row_bytes), (int)kQ6sRsrcWord3);
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const int r = min(2 * wave + rr, nr - 1);
+      const uint32_t so = (uint32_t)r * geo.row_bytes + (uint32_t)blk * kQ6sRowBytes;
+      const uint32_t dst = lds_base + (uint32_t)(s * kQ6sStage + (2 * wave + rr) * kQ6sRowWords * 4);
+#pragma unroll
+      for (int i = 0; i < kQ6sRowCopies; ++i)
+        if (i + 1 < kQ6sRowCopies || lane < kQ6sLastLanes) q6s_copy4(rsrc, dst + 256u * i, 4u * lane, so + 256u * i);
+    }
+  };
+  if (ntl == 0) return;  // the whole workgroup
+
+  // The wave's operands: pairs blk*32 + 2 wave + t (t = 0, 1) of every vector, converted into its
+  // slice of stage 1 (not yet copied into) and read back into registers.  The activations are
+  // requested before tile 0's copies and waited for with those still in flight.
+  Q6Act<NV> xa[2];
+  {
+    constexpr int NT = 16 * NV / 64;  // conversion tasks a lane: 8 NV a pair
+    uint32_t* cw = reinterpret_cast<uint32_t*>(lds + kQ6sStage) + wave * 2 * RW;
+    static_assert(NT == 2 || NT == 4, "two or four tasks a lane");
+    q6s_f4 y0[NT], y1[NT];
+#pragma unroll
+    for (int k = 0; k < NT; ++k) {
+      const int T = lane + 64 * k, t = T / (8 * NV), tt = T - t * 8 * NV;
+      const int v = tt >> 3, e = (tt >> 2) & 1, part4 = tt & 3;
+      const int slot = 2 * (blk * 32 + 2 * wave + t) + e;
+      const float* src = X + (size_t)min(v, nv - 1) * cols + L6::xoff(slot, part4 >> 1) + 8 * (part4 & 1);
+      y0[k] = q6s_ldx(src);
+      y1[k] = q6s_ldx(src + 4);
+    }
+    issue(0, 0);
+    q6s_wait_x<kQ6sWaveCopies>(y0, y1, NT);
+    float4 x0[NT], x1[NT];
+#pragma unroll
+    for (int k = 0; k < NT; ++k) {
+      const int T = lane + 64 * k, tt = T % (8 * NV);
+      const bool pad = (tt >> 3) >= nv;  // padding vectors: zero records
+      x0[k] = pad ? make_float4(0.0f, 0.0f, 0.0f, 0.0f) : make_float4(y0[k].x, y0[k].y, y0[k].z, y0[k].w);
+      x1[k] = pad ? make_float4(0.0f, 0.0f, 0.0f, 0.0f) : make_float4(y1[k].x, y1[k].y, y1[k].z, y1[k].w);
+    }
+#pragma unroll
+    for (int k = 0; k < NT; ++k) {
+      const int T = lane + 64 * k, t = T / (8 * NV), tt = T - t * 8 * NV;
+      const int v = tt >> 3, e = (tt >> 2) & 1;
+      uint32_t* rw = cw + t * RW;
+      float* so = reinterpret_cast<float*>(rw + NV * 40) + e * NV + ((v >> 1) & 1) * (NV / 2) + 2 * (v >> 2) + (v & 1);
+      convert_task<2>(x0[k], x1[k], tt, true, rw, so);
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      q6_act_load<NV>(cw + t * RW, 40, reinterpret_cast<const float*>(cw + t * RW + NV * 40), lane, xa[t]);
+  }
+  // every wave's operands are in registers: stage 1 is free (the 16-vector loop copies tile 1 into
+  // it now; the 8-vector loop at the top of tile 0)
+  q6s_lds_barrier();
+  if (NV != 8 && ntl > 1) issue(1, 1);
+
+  const int sbk = wave >> 1, h = wave & 1;  // the wave's super-block of the block, half
+  const uint32_t pb = (uint32_t)sbk * 210u;
+  auto read_tile = [&](int s, Q6Half& hw) __attribute__((always_inline)) {
+    const uint8_t* base = lds + s * kQ6sStage + ln * (4 * kQ6sRowWords) + pb;
+    q6_load_codes(base, pb & 3u, g, h, hw);
+    q6_load_scales(base, pb & 3u, hw);
+  };
+  auto fold_tile = [&](const Q6Half& hw, float* rb) __attribute__((always_inline)) {
+    float P0[NV / 2], P1[NV / 2];
+    q6_pair_fold<NV>(hw, h, 0, xa[0], lane, P0);
+    q6_pair_fold<NV>(hw, h, 1, xa[1], lane, P1);
+#pragma unroll
+    for (int jj = 0; jj < NJ; ++jj)
+#pragma unroll
+      for (int b = 0; b < 2; ++b) rb[wave * NO + (4 * jj + 2 * g + b) * 32 + ln] = P0[2 * jj + b] + P1[2 * jj + b];
+  };
+  // The block sum of each output o = (vector, row) of the workgroup's jt-th tile: the balanced tree
+  // over the 16 step sums, four threads an output -- thread k adds steps 4k..4k+3 (a unit), then
+  // the four units (U0 + U1) + (U2 + U3) across the quad (commutative adds: every lane of the quad
+  // holds the same bits).
+  auto combine = [&](int jt, const float* rb) __attribute__((always_inline)) {
+    const int tile = pi + jt * geo.P;
+#pragma unroll
+    for (int o4 = tid; o4 < 4 * NO; o4 += 1024) {
+      const int o = o4 >> 2, k = o4 & 3;
+      float u = (rb[(4 * k) * NO + o] + rb[(4 * k + 1) * NO + o]) + (rb[(4 * k + 2) * NO + o] + rb[(4 * k + 3) * NO + o]);
+      u = u + dpp<kXor1>(u);
+      u = u + dpp<kXor2>(u);
+      if (k == 0) {
+        const int v = o >> 5, r = tile * 32 + (o & 31);
+        if (geo.nb == 1) {
+          if (v < nv && r < rows) Y[(size_t)v * rows + r] = u;
+        } else {
+          part[((size_t)tile * geo.nb + blk) * NO + o] = u;
+        }
+      }
+    }
+  };
+
+  // Tile j.  With 8 vectors: one barrier a tile, after which tile j + 1 is copied into the other
+  // stage (whose tile j - 1 every wave has read), tile j is read and folded into one of two
+  // step-sum buffers, and the block sums of tile j - 1 are formed from the other.  With 16 (room for
+  // one buffer): tile j + 2 is copied once every wave has read tile j, and tile j's block sums are
+  // formed after a second barrier.
+  float* res = reinterpret_cast<float*>(lds + 2 * kQ6sStage);
+  for (int j = 0; j < ntl; ++j) {
+    const int s = j & 1;
+    Q6Half hw;
+    if constexpr (NV == 8) {
+      q6s_wait_vm<0>();  // tile j's copies (and the block-sum stores issued since)
+      q6s_lds_barrier();
+      if (j + 1 < ntl) issue(j + 1, s ^ 1);
+      read_tile(s, hw);
+      if (j > 0) combine(j - 1, res + ((j - 1) & 1) * 16 * NO);
+      fold_tile(hw, res + (j & 1) * 16 * NO);
+    } else {
+      // this wave's copies of tile j are done when at most tile j + 1's are still in flight (loads
+      // complete in order; the block-sum stores in between are not counted: they may complete in
+      // any order)
+      if (j + 1 < ntl) q6s_wait_vm<kQ6sWaveCopies>();
+      else q6s_wait_vm<0>();
+      q6s_lds_barrier();
+      read_tile(s, hw);
+      fold_tile(hw, res);
+      q6s_lds_barrier();  // stage s has been read, the step sums are complete
+      if (j + 2 < ntl) issue(j + 2, s);
+      combine(j, res);
+    }
+  }
+  if constexpr (NV == 8) {
+    if (ntl > 0) {
+      q6s_lds_barrier();
+      combine(ntl - 1, res + ((ntl - 1) & 1) * 16 * NO);
+    }
+  }
+}
+
+// out[v, r] = the nb block sums of (v, r) added in block order from 0.0f (NO = 32 x the launch's
+// padded vector count; part as k_gemv_q6s writes it).
+__global__ __launch_bounds__(256) void k_q6s_sum(const float* __restrict__ part, float* __restrict__ Y, int rows,
+                                                 int nv, int nb, int NO, int ntile) {
+  const int idx = (int)blockIdx.x * 256 + (int)threadIdx.x;
+  if (idx >= ntile * NO) return;
+  const int tile = idx / NO, o = idx - tile * NO, v = o >> 5, r = tile * 32 + (o & 31);
+  if (v >= nv || r >= rows) return;
+  const float* p = part + (size_t)tile * nb * NO + o;
+  float sum = 0.0f;
+  for (int k0 = 0; k0 < nb; k0 += 8) {  // eight block sums in flight at a time, added in order
+    float b8[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) b8[k] = p[(size_t)min(k0 + k, nb - 1) * NO];
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (k0 + k < nb) sum += b8[k];
+  }
+  Y[(size_t)v * rows + r] = sum;
+}
+
+int device_cus();
+
+inline Q6sGeo q6s_geometry(int rows, int cols, size_t row_bytes) {
+  Q6sGeo geo;
+  geo.nb = cols / 2048;
+  geo.ntile = (rows + 31) / 32;
+  geo.P = std::max(1, std::min(geo.ntile, device_cus() / geo.nb));
+  geo.row_bytes = (uint32_t)row_bytes;
+  return geo;
+}
+
+// 1 if the split form takes the call (the narrow form's shapes, rows below the wide form's), and
+// its workspace bytes through *ws_bytes (the block sums; none for rows of one block).
+bool gemv_q6s_route(int nvec, int rows, int cols, size_t row_bytes, size_t* ws_bytes) {
+  Q6nGeo ngeo;
+  if (rows >= kQ6wRows || nvec <= 0 || !q6n_geometry(rows, cols, row_bytes, ngeo)) return false;
+  if (ws_bytes) {
+    const int nvp = nvec <= 8 ? 8 : 16, nb = cols / 2048;
+    *ws_bytes = nb > 1 ? (size_t)((rows + 31) / 32) * nb * nvp * 32 * 4 : 0;
+  }
+  return true;
+}
+
+// qmatmul_n over Q6_K on the split form, 16 vectors a launch (8 when the whole call has at most 8),
+// each launch followed by the in-order sum of its block sums when rows have several blocks.
+bool launch_gemv_q6s(const void* w, const float* X, float* Y, int nvec, int rows, int cols, size_t row_bytes,
+                     void* ws, hipStream_t s) {
+  if (!gemv_q6s_route(nvec, rows, cols, row_bytes, nullptr)) return false;
+  const Q6sGeo geo = q6s_geometry(rows, cols, row_bytes);
+  if (geo.nb > 1 && !ws) return false;
+  const int nvp = nvec <= 8 ? 8 : 16, NO = nvp * 32;
+  const auto* wb = static_cast<const uint8_t*>(w);
+  auto* part = static_cast<float*>(ws);
+  const unsigned grid = (unsigned)(geo.nb * geo.P);
+  for (int v0 = 0; v0 < nvec; v0 += nvp) {
+    const int nv = std::min(nvp, nvec - v0);
+    const float* Xv = X + (size_t)v0 * cols;
+    float* Yv = Y + (size_t)v0 * rows;
+    if (nvp == 8) k_gemv_q6s<8><<<grid, 1024, 0, s>>>(wb, Xv, Yv, rows, cols, nv, geo, part);
+    else k_gemv_q6s<16><<<grid, 1024, 0, s>>>(wb, Xv, Yv, rows, cols, nv, geo, part);
+    if (geo.nb > 1)
+      k_q6s_sum<<<(unsigned)((geo.ntile * NO + 255) / 256), 256, 0, s>>>(part, Yv, rows, nv, geo.nb, NO, geo.ntile);
   }
   return true;
 }
