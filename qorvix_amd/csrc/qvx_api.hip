@@ -48,9 +48,6 @@ void launch_fill_normal_f16(uint16_t* x, size_t n, uint64_t seed, float mul, hip
 void launch_read16(const void* src, size_t n16, uint32_t* flag, hipStream_t s);
 bool qgemm_deq_supported(uint32_t t, const void* w, const uint16_t* X, int K, int N, size_t row_bytes);
 int q4k_plan_desc(int M, int N, int K, int cus, int* desc, int cap);
-bool gemv_q6n_supported(int rows, int cols, size_t row_bytes);
-bool launch_gemv_q6n(const void* w, const float* X, float* Y, int nvec, int rows, int cols, size_t row_bytes,
-                     hipStream_t s);
 bool gemv_q6s_route(int nvec, int rows, int cols, size_t row_bytes, size_t* ws_bytes);
 bool launch_gemv_q6s(const void* w, const float* X, float* Y, int nvec, int rows, int cols, size_t row_bytes,
                      void* ws, hipStream_t s);
@@ -105,13 +102,13 @@ struct qvx_plan {
 namespace {
 
 constexpr int kMaxBlock = 256;  // largest block the operator accepts (qmatmul.cpp:11)
-// Whether a Q6_K batch takes the matrix-core form (measured crossovers against the VALU kernel on
-// MI355X: 128256 rows from 3 vectors, 14336 from 5, 4096 from 8, fewer rows from 12).
-inline bool q6_batched(int nvec, int rows) {
-  if (rows >= 65536) return nvec >= 3;
-  if (rows >= 8192) return nvec >= 5;
-  if (rows >= 4096) return nvec >= 8;
-  return nvec >= 12;
+// Whether a Q6_K batch takes the matrix-core form (measured crossovers against the VALU kernel, four
+// vectors a launch, on MI355X, graph-replayed): from 3 vectors on rows of >= 8192 elements or
+// weights of >= 65536 rows (4096 x 14336 at 3: 17.9 against 26.7 us; 128256 x 4096 at 3: 113 against
+// 126 us on the form it replaced), else from 5 (4096 x 4096 at 4: 9.1 against 7.2 us, at 5: 9.2
+// against 11.5).
+inline bool q6_batched(int nvec, int rows, int cols) {
+  return nvec >= 5 || (nvec >= 3 && (cols >= 8192 || rows >= 65536));
 }
 
 inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
@@ -220,7 +217,7 @@ inline size_t ws_route_bytes(uint32_t type, int nvec, int rows, int cols, size_t
     return gemv_many_ws_bytes(nvec, rows, cols, row_bytes);
   }
   size_t need = 0;
-  if (type == T_Q6_K && q6_batched(nvec, rows) && gemv_q6s_route(nvec, rows, cols, row_bytes, &need)) return need;
+  if (type == T_Q6_K && q6_batched(nvec, rows, cols) && gemv_q6s_route(nvec, rows, cols, row_bytes, &need)) return need;
   return 0;
 }
 
@@ -248,8 +245,8 @@ int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int
   //  * Q4_K batches of 12-24 vectors or more (many_batch; encoder and prefill sizes): activations
   //    converted once, the weights streamed once per 64 vectors, bit-identical per vector to the
   //    one-vector kernel (k_gemv_q4k_many), with the bias added in its epilogue.
-  //  * Q6_K batches on weights of fewer than 65536 rows (q6_batched): the K range split over
-  //    workgroups (k_gemv_q6s), bit-identical per vector to the VALU kernel; a bias is added after.
+  //  * Q6_K batches (q6_batched): the matrix-core form with the K range split over workgroups
+  //    (k_gemv_q6s), bit-identical per vector to the VALU kernel; a bias is added after.
   if (const size_t need = ws_route_bytes(type, nvec, rows, cols, row_bytes, fast, epi)) {
     const bool own = epi.ws && epi.ws_bytes >= need;
     void* ws = own ? epi.ws : epi.no_alloc ? nullptr : gemm_temp_alloc(need, s);
@@ -297,13 +294,14 @@ int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int
     }
     return hip_status();
   }
-  // Q6_K batches stream the weights once per 16 vectors on the matrix-core form (rows of
-  // 2048-element multiples), bit-identical per vector to the VALU kernel that takes single vectors.
-  // Below the measured crossovers (few rows leave that form's grid thin) the VALU kernel, four
-  // vectors a launch, is faster.
-  if (fast && type == T_Q6_K && q6_batched(nvec, rows) && !epi.flags() && gemv_q6n_supported(rows, cols, row_bytes)) {
-    if (!launch_gemv_q6n(w, X, out, nvec, rows, cols, row_bytes, s)) return refused();
-    return hip_status();
+  // Q6_K batches of rows of one 64-slot block take the matrix-core form here (it needs no
+  // workspace); longer rows took it above, or (no workspace) stay on the VALU kernel below.
+  if (fast && type == T_Q6_K && q6_batched(nvec, rows, cols) && !epi.flags()) {
+    size_t need = 0;
+    if (gemv_q6s_route(nvec, rows, cols, row_bytes, &need) && need == 0) {
+      if (!launch_gemv_q6s(w, X, out, nvec, rows, cols, row_bytes, nullptr, s)) return refused();
+      return hip_status();
+    }
   }
   const int mx = (fast && type == T_Q4_K) ? gemv_mx_max_nv(cols) : 0;
   if (mx > 0) {

@@ -60,28 +60,15 @@ __global__ __launch_bounds__((gemv_threads<T, NV>())) void k_gemv(const uint8_t*
 //  * the same reduction.  The VALU kernel sums a row's slot partials over 64-lane spans with DPP and
 //    permlane swaps: a balanced pairwise tree over each 64 consecutive slots, then, for rows of
 //    more than 64 slots, those 64-slot sums in order from 0.  Here a lane adds the two slots of a
-//    pair (tree level 1), keeps a carry stack over the 8 pairs of a unit (16 slots, levels 2-4),
-//    and the combine step adds the four units of a 64-slot block (levels 5-6), then the blocks in
-//    the same order from 0.
+//    pair (tree level 1); a step (one half super-block: two pairs) sums its pairs (level 2); the
+//    16 steps of a 64-slot block are summed as a balanced tree (levels 3-6); the blocks in the same
+//    order from 0.
 // MFMA (v_mfma_i32_32x32x16_i8, one per 16-element quarter of a slot pair): A = 32 rows (vector v,
 // part p: qh / ql) x the quarter's 16 fixed-point activation bytes; B = the quarter's 16 signed
 // codes (code - 32) of 32 weight rows.  Lane l supplies row / column l%32 and K elements
 // 8 (l/32)..+7 of both operands; its accumulator holds column l%32 (weight row) and rows
 // 8j + 4 (l/32) + i (i, j = 0..3): the qh and ql sums of vectors 4j + 2 (l/32) + {0, 1}.  The run
 // sum is T = (qh sum) * 128 + (ql sum), as dotq forms it.
-// Work: a unit is one 32-row tile x 16 slots (8 pairs, two super-blocks).  Workgroup b owns tpw
-// tiles and all upt = S/16 units of each; its 8 waves take units w, w+8, ...  Per pair a wave
-// converts the pair's activations for all vectors into a private LDS buffer (X read from L2),
-// reads its A fragments back, builds B from the raw blocks (loaded a super-block ahead as
-// dword-aligned windows and realigned, as the VALU kernel reads them), runs four MFMAs and folds.
-// Unit sums go to LDS; after a barrier the workgroup combines them per (tile, vector, row).
-struct Q6nGeo {
-  int S;      // slots per row (cols / 32), a multiple of 64
-  int ntile;  // 32-row tiles
-  int upt;    // 16-slot units per tile
-  int tpw;    // tiles per workgroup
-  uint32_t row_bytes;
-};
 typedef uint32_t u32x3a4_t __attribute__((ext_vector_type(3), aligned(4)));
 
 // Raw bytes of half h of one super-block of a lane's row (l%32) for its K half g = l/32: the ql
@@ -112,27 +99,6 @@ __device__ __attribute__((always_inline)) inline void q6_load_scales(const uint8
 #pragma unroll
   for (int k = 0; k < 5; ++k) r.sc[k] = ldg4(sw + 4 * k);
   r.d = ldg2(base + 208);
-}
-// Loads half h's pieces; the scales, d and misalignment with h = 0, from `first` (the same
-// super-block's half 0) with h = 1.
-__device__ __attribute__((always_inline)) inline void q6_load_half(const uint8_t* base, int g, int h,
-                                                                   const Q6Half& first, Q6Half& r) {
-  const uint32_t sh = (uint32_t)(uintptr_t)base & 3u;
-  q6_load_codes(base, sh, g, h, r);
-  if (h == 0) {
-    q6_load_scales(base, sh, r);
-  } else {
-    r.sh = first.sh;
-#pragma unroll
-    for (int k = 0; k < 5; ++k) r.sc[k] = first.sc[k];
-    r.d = first.d;
-  }
-}
-// Half h's pieces and its super-block's scales (a step that does not follow its half 0).
-__device__ __attribute__((always_inline)) inline void q6_load_step(const uint8_t* base, int g, int h, Q6Half& r) {
-  const uint32_t sh = (uint32_t)(uintptr_t)base & 3u;
-  q6_load_codes(base, sh, g, h, r);
-  q6_load_scales(base, sh, r);
 }
 // 16 signed codes (code - 32) of quarter Q (elements 8g..8g+7 of it) of pair t as two dwords.
 template <int Q>
@@ -224,351 +190,19 @@ __device__ __attribute__((always_inline)) inline void q6_pair_fold(const Q6Half&
   }
 }
 
-template <int NV>
-__device__ __attribute__((always_inline)) inline void q6_pair(const Q6Half& r, int h, int t, const uint32_t* xrec,
-                                                              int vstride, const float* sxc, int lane,
-                                                              float (&P)[NV / 2]) {
-  Q6Act<NV> x;
-  q6_act_load<NV>(xrec, vstride, sxc, lane, x);
-  q6_pair_fold<NV>(r, h, t, x, lane, P);
-}
-
-template <int NV>
-__global__ __launch_bounds__(512) void k_gemv_q6n(const uint8_t* __restrict__ W, const float* __restrict__ X,
-                                                  float* __restrict__ Y, int rows, int cols, int nv, Q6nGeo geo) {
-  static_assert(NV == 8 || NV == 16, "8 or 16 vectors a launch");
-  constexpr int XW = NV * 2 * 20;  // words of a wave's converted activations: (vector, slot e) records
-  constexpr int NJ = NV / 4;       // accumulator row groups j holding real vectors
-  __shared__ __attribute__((aligned(16))) uint32_t xq_all[8][XW];
-  __shared__ __attribute__((aligned(16))) float sxc_all[8][2][2][NV / 2];  // [wave][slot e][g][2j + b]
-  extern __shared__ __attribute__((aligned(16))) float res[];              // [unit][vector][32 rows]
-  using L6 = Lane<T_Q6_K>;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int ln = lane & 31, g = lane >> 5;
-  uint32_t* xq = xq_all[wave];
-  const int upt = geo.upt, units = geo.tpw * upt, tile0 = blockIdx.x * geo.tpw;
-
-
-  // Conversion tasks of a pair: t = lane + 64 k (k < NV/8): record vs = t/4 = (vector, e), part t%4.
-  constexpr int KT = NV / 8;
-  auto task_ptr = [&](int pair, int k) {
-    const int t = lane + 64 * k, vs = t >> 2, part = t & 3, v = min(vs >> 1, nv - 1), e = vs & 1;
-    return X + (size_t)v * cols + L6::xoff(2 * pair + e, part >> 1) + 8 * (part & 1);
-  };
-  auto load_x = [&](int pair, float4 (&xr)[KT][2]) __attribute__((always_inline)) {
-#pragma unroll
-    for (int k = 0; k < KT; ++k) {
-      const float4* p = reinterpret_cast<const float4*>(task_ptr(pair, k));
-      xr[k][0] = p[0];
-      xr[k][1] = p[1];
-    }
-  };
-  auto convert = [&](const float4 (&xr)[KT][2]) __attribute__((always_inline)) {
-#pragma unroll
-    for (int k = 0; k < KT; ++k) {
-      const int t = lane + 64 * k, vs = t >> 2, v = vs >> 1, e = vs & 1;
-      float* so = &sxc_all[wave][e][(v >> 1) & 1][2 * (v >> 2) + (v & 1)];
-      convert_task<2>(xr[k][0], xr[k][1], t, v < nv, xq, so);
-    }
-  };
-  auto row_base = [&](int u) {
-    const int tile = tile0 + u / upt;
-    const int row = min(tile * 32 + ln, rows - 1);
-    return W + (size_t)row * geo.row_bytes + (size_t)(u % upt) * 2 * 210;
-  };
-
-  // The wave walks its units u = w, w + 8, ...; unit step s (0..3) is half s%2 of super-block s/2.
-  // A step folds its two pairs into P0 + P1; a super-block's sum is (half 0) + (half 1), a unit's
-  // (super-block 0) + (super-block 1): the balanced tree over the unit's 8 pairs.  The next step's
-  // raw bytes are loaded at the start of a step into the other of two buffers, the next pair's
-  // activations at the start of a pair (activations first, so that a wait for them never waits for
-  // the blocks behind them).  Every load is unconditional (the wave's last step reloads its own
-  // unit's first half and pair) and no buffer is copied into the other, so the wait before each use
-  // counts exactly the loads issued after it: with a conditional load the compiler's waits fall back
-  // to ones that also wait for the prefetch just issued.
-  Q6Half ha, hb;
-  float4 xr[2][KT][2];
-  const int nu = wave < units ? (units - wave + 7) / 8 : 0;  // units of this wave
-  auto sbase = [&](int u, int st) { return row_base(u) + (size_t)(st >> 1) * 210; };
-  auto spair = [&](int u, int st) { return (u % upt) * 8 + (st >> 1) * 4 + (st & 1) * 2; };
-  if (nu > 0) {
-    q6_load_half(sbase(wave, 0), g, 0, ha, ha);
-    load_x(spair(wave, 0), xr[0]);
-  }
-  float H0[NV / 2], S0[NV / 2];
-  auto step = [&](int k, auto stc, const Q6Half& cur, Q6Half& nxt) __attribute__((always_inline)) {
-    constexpr int st = decltype(stc)::value, sn = (st + 1) & 3;
-    const int u = wave + 8 * k;
-    const int un = st == 3 ? wave + 8 * min(k + 1, nu - 1) : u;  // the next step's unit
-    const int pair0 = spair(u, st);
-    float H[NV / 2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      if (t == 0)
-        load_x(pair0 + 1, xr[1]);
-      else
-        load_x(spair(un, sn), xr[0]);
-      __builtin_amdgcn_sched_barrier(0);
-      if (t == 0) q6_load_half(sbase(un, sn), g, sn & 1, cur, nxt);
-      __builtin_amdgcn_sched_barrier(0);
-      convert(xr[t]);
-      float P[NV / 2];
-      q6_pair<NV>(cur, st & 1, t, xq, 40, &sxc_all[wave][0][0][0], lane, P);
-#pragma unroll
-      for (int kk = 0; kk < NV / 2; ++kk) H[kk] = t == 0 ? P[kk] : H[kk] + P[kk];
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if constexpr (st == 0 || st == 2) {
-#pragma unroll
-      for (int kk = 0; kk < NV / 2; ++kk) H0[kk] = H[kk];
-    } else if constexpr (st == 1) {
-#pragma unroll
-      for (int kk = 0; kk < NV / 2; ++kk) S0[kk] = H0[kk] + H[kk];
-    } else {
-#pragma unroll
-      for (int j = 0; j < NJ; ++j)
-#pragma unroll
-        for (int b = 0; b < 2; ++b) {
-          const int kk = 2 * j + b;
-          res[((size_t)u * NV + 4 * j + 2 * g + b) * 32 + ln] = S0[kk] + (H0[kk] + H[kk]);
-        }
-    }
-  };
-#pragma unroll 1
-  for (int k = 0; k < nu; ++k) {
-    step(k, std::integral_constant<int, 0>{}, ha, hb);
-    step(k, std::integral_constant<int, 1>{}, hb, ha);
-    step(k, std::integral_constant<int, 2>{}, ha, hb);
-    step(k, std::integral_constant<int, 3>{}, hb, ha);
-  }
-  __syncthreads();
-
-  // Combine: units of a 64-slot block as ((U0 + U1) + (U2 + U3)), blocks in order from 0 (a row of
-  // one block takes its block sum as it is).
-  const int nb = geo.S / 64, per_tile = NV * 32;
-  for (int idx = tid; idx < geo.tpw * per_tile; idx += 512) {
-    const int tl = idx / per_tile, v = (idx % per_tile) >> 5, r = idx & 31;
-    const int row = (tile0 + tl) * 32 + r;
-    if (v >= nv || tile0 + tl >= geo.ntile || row >= rows) continue;
-    const float* U = res + ((size_t)tl * upt * NV + v) * 32 + r;
-    auto blk = [&](int k) {
-      const size_t st = (size_t)NV * 32;
-      return (U[(4 * k) * st] + U[(4 * k + 1) * st]) + (U[(4 * k + 2) * st] + U[(4 * k + 3) * st]);
-    };
-    float sum;
-    if (nb == 1) {
-      sum = blk(0);
-    } else {
-      sum = 0.0f;
-      for (int k = 0; k < nb; ++k) sum += blk(k);
-    }
-    Y[(size_t)v * rows + row] = sum;
-  }
-}
-
-// Wide form (tall weights: rows >= kQ6wRows): the same arithmetic with the activation conversion
-// shared by a workgroup.  Its 8 waves take 8 consecutive 32-row tiles and walk the super-blocks in
-// lockstep: while the waves fold super-block s from one LDS buffer, the workgroup converts s+1 into
-// the other (one conversion task a thread, X loaded a super-block ahead), and one barrier per
-// super-block swaps them.  Each wave keeps the whole row: super-block sums ((P0 + P1) + (P2 + P3)),
-// a carry stack over the 8 super-blocks of a 64-slot block, and the blocks summed in order from 0.
-template <int NV>
-__global__ __launch_bounds__(512) void k_gemv_q6w(const uint8_t* __restrict__ W, const float* __restrict__ X,
-                                                  float* __restrict__ Y, int rows, int cols, int nv,
-                                                  uint32_t row_bytes) {
-  static_assert(NV == 4 || NV == 8 || NV == 16, "4, 8 or 16 vectors a launch");
-  constexpr int NT = 32 * NV;  // conversion tasks of a super-block: (vector, slot of 8, part of 4)
-  __shared__ __attribute__((aligned(16))) uint32_t xq[2][NV * 8 * 20];        // records (v, slot) of a super-block
-  __shared__ __attribute__((aligned(16))) float sxc[2][4][2][2][NV / 2];     // [buf][pair][e][g][2j + b]
-  using L6 = Lane<T_Q6_K>;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int ln = lane & 31, g = lane >> 5;
-  const int nsb = cols / 256, S = cols / 32;
-  const int tile = blockIdx.x * 8 + wave;
-  const uint8_t* rowp = W + (size_t)min(tile * 32 + ln, rows - 1) * row_bytes;
-
-  // conversion task t = tid: record vs = t/4 = (vector v, slot q of the super-block), part t%4
-  const int cv = min((tid >> 2) >> 3, nv - 1), cq = (tid >> 2) & 7, cpart = tid & 3;
-  const bool ctask = tid < NT;
-  auto load_x = [&](int sb, float4& x0, float4& x1) {
-    if (ctask) {
-      const float4* p = reinterpret_cast<const float4*>(X + (size_t)cv * cols + L6::xoff(8 * sb + cq, cpart >> 1) +
-                                                        8 * (cpart & 1));
-      x0 = p[0];
-      x1 = p[1];
-    }
-  };
-  auto convert = [&](int buf, const float4& x0, const float4& x1) {
-    if (ctask) {
-      const int v = (tid >> 2) >> 3;
-      float* so = &sxc[buf][cq >> 1][cq & 1][(v >> 1) & 1][2 * (v >> 2) + (v & 1)];
-      convert_task<2>(x0, x1, tid, v < nv, xq[buf], so);
-    }
-  };
-
-  float4 x0, x1;
-  load_x(0, x0, x1);
-  convert(0, x0, x1);
-  if (nsb > 1) load_x(1, x0, x1);
-  Q6Half cur, nxt;
-  q6_load_half(rowp, g, 0, cur, cur);
-  __syncthreads();
-
-  float st[3][NV / 2], run[NV / 2];
-#pragma unroll
-  for (int k = 0; k < NV / 2; ++k) run[k] = 0.0f;
-#pragma unroll 1
-  for (int sb = 0; sb < nsb; ++sb) {
-    const int buf = sb & 1;
-    if (sb + 1 < nsb) {
-      convert(buf ^ 1, x0, x1);
-      if (sb + 2 < nsb) load_x(sb + 2, x0, x1);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    float T[NV / 2], H[NV / 2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      // next half-step's raw bytes: half 1 of this super-block, or half 0 of the next
-      if (h == 0)
-        q6_load_half(rowp + (size_t)sb * 210, g, 1, cur, nxt);
-      else if (sb + 1 < nsb)
-        q6_load_half(rowp + (size_t)(sb + 1) * 210, g, 0, cur, nxt);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        float P[NV / 2];
-        const int pp = 2 * h + t;
-        q6_pair<NV>(cur, h, t, &xq[buf][2 * pp * 20], 8 * 20, &sxc[buf][pp][0][0][0], lane, P);
-#pragma unroll
-        for (int k = 0; k < NV / 2; ++k) H[k] = t == 0 ? P[k] : H[k] + P[k];
-        __builtin_amdgcn_sched_barrier(0);
-      }
-#pragma unroll
-      for (int k = 0; k < NV / 2; ++k) T[k] = h == 0 ? H[k] : T[k] + H[k];
-      cur = nxt;
-    }
-    // carry stack over the 8 super-blocks of a 64-slot block, then the running sum of blocks
-    const int q = sb & 7;
-#pragma unroll
-    for (int k = 0; k < NV / 2; ++k) {
-      float c = T[k];
-      if (q & 1) {
-        c = st[0][k] + c;
-        if (q & 2) {
-          c = st[1][k] + c;
-          if (q & 4) {
-            c = st[2][k] + c;
-            run[k] = S == 64 ? c : run[k] + c;
-          } else {
-            st[2][k] = c;
-          }
-        } else {
-          st[1][k] = c;
-        }
-      } else {
-        st[0][k] = c;
-      }
-    }
-    __syncthreads();  // buffer `buf` is free for the conversion two super-blocks on; `buf ^ 1` is ready
-  }
-  const int row = tile * 32 + ln;
-  if (row < rows) {
-#pragma unroll
-    for (int j = 0; j < NV / 4; ++j)
-#pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        const int v = 4 * j + 2 * g + b;
-        if (v < nv) Y[(size_t)v * rows + row] = run[2 * j + b];
-      }
-  }
-}
-
-constexpr int kQ6wRows = 65536;  // rows from which the wide form (8 tiles a workgroup) fills the chip
-
-template <int NV>
-static bool launch_q6w_t(const void* w, const float* X, float* Y, int nv, int rows, int cols, size_t row_bytes,
-                         hipStream_t s) {
-  static LdsLimit lim;
-  if (!lds_ready(reinterpret_cast<const void*>(&k_gemv_q6w<NV>), lim, 0)) return false;
-  const int nwg = ((rows + 31) / 32 + 7) / 8;
-  k_gemv_q6w<NV><<<nwg, 512, 0, s>>>(static_cast<const uint8_t*>(w), X, Y, rows, cols, nv, (uint32_t)row_bytes);
-  return true;
-}
-
-// LDS bytes of the unit sums (dynamic) for a launch.
-inline size_t q6n_res_bytes(int nv_t, const Q6nGeo& geo) { return (size_t)geo.tpw * geo.upt * nv_t * 32 * 4; }
-
-template <int NV>
-static bool launch_q6n_t(const void* w, const float* X, float* Y, int nv, int rows, int cols, const Q6nGeo& geo,
-                         hipStream_t s) {
-  static LdsLimit lim;
-  const size_t dyn = q6n_res_bytes(NV, geo);
-  if (!lds_ready(reinterpret_cast<const void*>(&k_gemv_q6n<NV>), lim, dyn)) return false;
-  const int nwg = (geo.ntile + geo.tpw - 1) / geo.tpw;
-  k_gemv_q6n<NV><<<nwg, 512, dyn, s>>>(static_cast<const uint8_t*>(w), X, Y, rows, cols, nv, geo);
-  return true;
-}
-
-static bool q6n_geometry(int rows, int cols, size_t row_bytes, Q6nGeo& geo) {
-  if (cols % 2048 != 0 || rows <= 0 || row_bytes > 0xFFFFFFFFull) return false;
-  geo.S = cols / 32;
-  geo.ntile = (rows + 31) / 32;
-  geo.upt = geo.S / 16;
-  geo.tpw = std::max(1, 8 / geo.upt);
-  geo.row_bytes = (uint32_t)row_bytes;
-  return q6n_res_bytes(16, geo) <= 96 * 1024;
-}
-
-// 1 if the batched matrix-core Q6_K form takes this shape (cols a multiple of 2048, rows whose unit
-// sums fit in LDS).
-bool gemv_q6n_supported(int rows, int cols, size_t row_bytes) {
-  Q6nGeo geo;
-  return q6n_geometry(rows, cols, row_bytes, geo);
-}
-
-// qmatmul_n over Q6_K on the matrix-core form, 16 vectors a launch (the last launch 8 when at most
-// 8 remain).  Returns false, having launched nothing past the failing launch, when refused.
-bool launch_gemv_q6n(const void* w, const float* X, float* Y, int nvec, int rows, int cols, size_t row_bytes,
-                     hipStream_t s) {
-  Q6nGeo geo;
-  if (!q6n_geometry(rows, cols, row_bytes, geo)) return false;
-  const bool wide = rows >= kQ6wRows;
-  for (int v0 = 0; v0 < nvec; v0 += 16) {
-    const int nv = std::min(16, nvec - v0);
-    const float* Xv = X + (size_t)v0 * cols;
-    float* Yv = Y + (size_t)v0 * rows;
-    bool ok;
-    if (wide)
-      ok = nv <= 4   ? launch_q6w_t<4>(w, Xv, Yv, nv, rows, cols, row_bytes, s)
-           : nv <= 8 ? launch_q6w_t<8>(w, Xv, Yv, nv, rows, cols, row_bytes, s)
-                     : launch_q6w_t<16>(w, Xv, Yv, nv, rows, cols, row_bytes, s);
-    else
-      ok = nv <= 8 ? launch_q6n_t<8>(w, Xv, Yv, nv, rows, cols, geo, s)
-                   : launch_q6n_t<16>(w, Xv, Yv, nv, rows, cols, geo, s);
-    if (!ok) return false;
-  }
-  return true;
-}
-
-// ---- batched Q6_K with the K range split over workgroups ---------------------------------------
-// The narrow form's arithmetic and summation order, re-cut for weights whose 32-row tiles are too
-// few to fill the chip one workgroup each (4096-row weights: 128 tiles):
-//  * Workgroup b (16 waves) owns 64-slot block blk = b % nb of its rows and the tiles b / nb,
-//    b / nb + P, ... (P workgroups a block).  Wave w owns step w of the block (a step is one half
-//    super-block: the block's slot pairs 2w and 2w + 1), so its activation operands -- the
+// Work decomposition (k_gemv_q6s, 16 waves a workgroup):
+//  * Workgroup b owns 64-slot block blk = b % nb of its rows and the 32-row tiles b / nb,
+//    b / nb + P, ... (P workgroups a block, about one workgroup a CU in all).  Wave w owns step w of
+//    the block (the block's slot pairs 2w and 2w + 1), so its activation operands -- the
 //    convert_task<2> records and steps of those two pairs for every vector -- are the same for
 //    every tile: the wave converts them once, through LDS, into registers.
 //  * Tiles stream through a two-stage LDS ring: a tile's block (32 rows x 1680 bytes) is copied by
 //    buffer_load_dword ... lds (rows 421 dwords apart: on distinct banks) while the previous tile is
-//    folded.  Each
-//    wave folds its step for the tile's 32 rows ((pair 0) + (pair 1), the narrow form's step
-//    sum) and the workgroup sums the 16 steps as a balanced tree, which is the narrow form's
-//    unit = (H0 + H1) + (H2 + H3), block = (U0 + U1) + (U2 + U3).
+//    folded.  Each wave folds its step for the tile's 32 rows (four MFMAs a pair, the B codes built
+//    from the raw bytes as dword-aligned windows realigned, as the VALU kernel reads them), and the
+//    workgroup sums the 16 step sums of each output as a balanced tree.
 //  * A row of one block is written as it is.  Otherwise the block sums go to the workspace and a
 //    second launch (k_q6s_sum) adds each output's nb block sums in block order from 0.0f.
-// Each output therefore has the narrow form's bits, which are the VALU kernel's.
 #define QVX_LDS __attribute__((address_space(3)))
 constexpr uint32_t kQ6sRsrcWord3 = 0x00020000u;              // raw buffer, 32-bit data (gfx9)
 constexpr int kQ6sRowBytes = 8 * 210;                        // a row's 64-slot block
@@ -817,11 +451,10 @@ inline Q6sGeo q6s_geometry(int rows, int cols, size_t row_bytes) {
   return geo;
 }
 
-// 1 if the split form takes the call (the narrow form's shapes, rows below the wide form's), and
-// its workspace bytes through *ws_bytes (the block sums; none for rows of one block).
+// 1 if the batched form takes the shape (K a multiple of 2048, row pitch below 4 GiB), and its
+// workspace bytes for nvec vectors through *ws_bytes (the block sums; none for rows of one block).
 bool gemv_q6s_route(int nvec, int rows, int cols, size_t row_bytes, size_t* ws_bytes) {
-  Q6nGeo ngeo;
-  if (rows >= kQ6wRows || nvec <= 0 || !q6n_geometry(rows, cols, row_bytes, ngeo)) return false;
+  if (cols <= 0 || cols % 2048 != 0 || rows <= 0 || nvec <= 0 || row_bytes > 0xFFFFFFFFull / 64) return false;
   if (ws_bytes) {
     const int nvp = nvec <= 8 ? 8 : 16, nb = cols / 2048;
     *ws_bytes = nb > 1 ? (size_t)((rows + 31) / 32) * nb * nvp * 32 * 4 : 0;
@@ -829,7 +462,7 @@ bool gemv_q6s_route(int nvec, int rows, int cols, size_t row_bytes, size_t* ws_b
   return true;
 }
 
-// qmatmul_n over Q6_K on the split form, 16 vectors a launch (8 when the whole call has at most 8),
+// qmatmul_n over Q6_K on the batched form, 16 vectors a launch (8 when the whole call has at most 8),
 // each launch followed by the in-order sum of its block sums when rows have several blocks.
 bool launch_gemv_q6s(const void* w, const float* X, float* Y, int nvec, int rows, int cols, size_t row_bytes,
                      void* ws, hipStream_t s) {

@@ -103,6 +103,31 @@ def test_plan_replays_many_vector_calls(cuda):
     plan.close()
 
 
+def test_plan_replays_batched_q6k_calls(cuda):
+    """The batched Q6_K form in a plan (block sums in the plan's workspace, rows of several blocks;
+    a one-block call needs none): replays bit-identical to the direct calls, several times."""
+    t = qvx.Q6_K
+    shapes = [(4096, 14336, 8), (1000, 4096, 16), (4096, 2048, 6)]
+    Ws = [_weight(cuda, t, r, c, seed=60 + i) for i, (r, c, n) in enumerate(shapes)]
+    Xs = [qvx.fill_normal_t(cuda.empty((n, c), dtype=cuda.float32, device="cuda"), seed=70 + i)
+          for i, (r, c, n) in enumerate(shapes)]
+    want = [_many(cuda, W, t, X, r, c) for W, X, (r, c, n) in zip(Ws, Xs, shapes)]
+    outs = [cuda.full((n, r), float("nan"), dtype=cuda.float32, device="cuda") for (r, c, n) in shapes]
+    plan = decode.Plan()
+    for i in range(3):
+        plan.add(outs[i], decode.DevWeight(Ws[i], t, *shapes[i][:2]), Xs[i], shapes[i][2])
+    plan.instantiate()
+    s = cuda.cuda.current_stream().cuda_stream
+    for rep in range(3):
+        for o in outs:
+            o.fill_(float("nan"))
+        plan.launch(s)
+        cuda.cuda.synchronize()
+        for i in range(3):
+            assert cuda.equal(outs[i].view(cuda.int32), want[i].view(cuda.int32)), (rep, i)
+    plan.close()
+
+
 def test_many_matches_oracle_at_encoder_batch(cuda):
     """BASELINE's Q4_K 14336 x 4096 weight at 512 vectors (the verdict's encoder-size point) against the
     fp64 oracle on a row slice, within the GEMV bar."""
