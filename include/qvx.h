@@ -108,8 +108,12 @@ int qvx_qmatmul(float* d_out, const void* d_w, uint32_t type, const float* d_x, 
  * tile and K range for batches up to 32 vectors), then the weights are streamed once per 64 vectors
  * (once per 16 up to 32 vectors) -- the reference's "dequantize each block once for all nVec dot
  * products" (qmatmul.hpp:24-32); smaller batches stream them once per 8 vectors and allocate
- * nothing.  A plan gives its many-vector calls a workspace of its own, allocated by
- * qvx_plan_instantiate, so its replays allocate nothing. */
+ * nothing.  Q6_K batches of 5 vectors or more (3 or more on rows of >= 8192 elements or weights of
+ * >= 65536 rows) with cols a multiple of 2048 stream the weights once per 16 vectors on a
+ * matrix-core form whose K range is split over workgroups by 2048-element blocks; for rows of more
+ * than one block it takes a stream-ordered temporary for the block sums (rows/32 * blocks * 2 or 4
+ * KiB; without one the batch runs on the VALU kernel, four vectors a launch).  A plan gives these
+ * calls a workspace of its own, allocated by qvx_plan_instantiate, so its replays allocate nothing. */
 int qvx_qmatmul_n(float* d_out, const void* d_w, uint32_t type, const float* d_X, int n_vec,
                   int rows, int cols, void* stream);
 
