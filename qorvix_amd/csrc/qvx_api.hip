@@ -49,6 +49,9 @@ void launch_read16(const void* src, size_t n16, uint32_t* flag, hipStream_t s);
 bool qgemm_deq_supported(uint32_t t, const void* w, const uint16_t* X, int K, int N, size_t row_bytes);
 int q4k_plan_desc(int M, int N, int K, int cus, int* desc, int cap);
 bool gemv_q6s_route(int nvec, int rows, int cols, size_t row_bytes, size_t* ws_bytes);
+bool gemv_q4s_route(int nvec, int rows, int cols, size_t row_bytes, size_t* ws_bytes);
+bool launch_gemv_q4s(const void* w, const float* X, float* Y, const float* bias, int nvec, int rows, int cols,
+                     size_t row_bytes, void* ws, hipStream_t s);
 bool launch_gemv_q6s(const void* w, const float* X, float* Y, int nvec, int rows, int cols, size_t row_bytes,
                      void* ws, hipStream_t s);
 int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M, int rows, int cols,
@@ -207,18 +210,42 @@ int gemv_unfused(float* out, const void* w, uint32_t type, const float* X, int n
 // out = W . x per vector, optionally with the activations normalised (epi.norm_w) and / or the
 // interleaved gate|up rows gated (epi.swiglu: rows / 2 outputs a vector).  The argument checks are
 // the plain operator's.
-// Workspace bytes of the form a call takes if that form needs one (the many-vector Q4_K form, the
-// split Q6_K form), else 0.
+// Whether a Q4_K batch takes the split form (k_gemv_q4s) rather than the many-vector form or chunks
+// of 8 on the one-vector / batched forms.  Measured on MI355X (graph-replayed): it wins on long rows
+// from 5 vectors (4096 x 14336 at 8: 20.5 against 26.0 us, at 16: 28.8 against 34.0 on the
+// many-vector form; at 4: 20.1 against 17.1) and on small weights from 12 (1024 x 4096 at 16: 12.7
+// against 17.6), up to 23 vectors; on 4096-element rows of larger weights the other forms are faster
+// (14336 x 4096 at 8: 17.7 against 14.3).  Its fixed cost (a conversion per workgroup, the partial
+// sums' launch) is ~9 us.
+inline bool q4s_batch(int nvec, int rows, int cols) {
+  if (nvec > 23) return false;
+  return (cols >= 8192 && nvec >= 5) || ((int64_t)rows * cols <= ((int64_t)4 << 20) && nvec >= 12);
+}
+
+// The forms that take a workspace, and the bytes of the one a call takes (0: none).
+enum WsForm { WS_NONE, WS_MANY, WS_Q4S, WS_Q6S };
+inline WsForm ws_route(uint32_t type, int nvec, int rows, int cols, size_t row_bytes, bool fast, const GemvEpi& epi,
+                       size_t* bytes) {
+  *bytes = 0;
+  if (!fast || epi.flags() || rows <= 0 || cols <= 0) return WS_NONE;
+  if (type == T_Q4_K) {
+    if (q4s_batch(nvec, rows, cols) && gemv_q4s_route(nvec, rows, cols, row_bytes, bytes)) return WS_Q4S;
+    if (many_batch(nvec, rows, cols) && gemv_many_supported(cols, row_bytes)) {
+      *bytes = gemv_many_ws_bytes(nvec, rows, cols, row_bytes);
+      return WS_MANY;
+    }
+    *bytes = 0;
+    return WS_NONE;
+  }
+  if (type == T_Q6_K && q6_batched(nvec, rows, cols) && gemv_q6s_route(nvec, rows, cols, row_bytes, bytes) && *bytes)
+    return WS_Q6S;
+  *bytes = 0;
+  return WS_NONE;
+}
 inline size_t ws_route_bytes(uint32_t type, int nvec, int rows, int cols, size_t row_bytes, bool fast,
                              const GemvEpi& epi) {
-  if (!fast || epi.flags() || rows <= 0 || cols <= 0) return 0;
-  if (type == T_Q4_K) {
-    if (!many_batch(nvec, rows, cols) || !gemv_many_supported(cols, row_bytes)) return 0;
-    return gemv_many_ws_bytes(nvec, rows, cols, row_bytes);
-  }
-  size_t need = 0;
-  if (type == T_Q6_K && q6_batched(nvec, rows, cols) && gemv_q6s_route(nvec, rows, cols, row_bytes, &need)) return need;
-  return 0;
+  size_t b = 0;
+  return ws_route(type, nvec, rows, cols, row_bytes, fast, epi, &b) == WS_NONE ? 0 : b;
 }
 
 int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int rows, int cols, hipStream_t s,
@@ -245,18 +272,21 @@ int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int
   //  * Q4_K batches of 12-24 vectors or more (many_batch; encoder and prefill sizes): activations
   //    converted once, the weights streamed once per 64 vectors, bit-identical per vector to the
   //    one-vector kernel (k_gemv_q4k_many), with the bias added in its epilogue.
+  //  * smaller Q4_K batches (q4s_batch): the K ranges split over workgroups (k_gemv_q4s), bit-identical
+  //    per vector to the one-vector kernel, the bias added in its sum launch;
   //  * Q6_K batches (q6_batched): the matrix-core form with the K range split over workgroups
   //    (k_gemv_q6s), bit-identical per vector to the VALU kernel; a bias is added after.
-  if (const size_t need = ws_route_bytes(type, nvec, rows, cols, row_bytes, fast, epi)) {
+  size_t need = 0;
+  if (const WsForm form = ws_route(type, nvec, rows, cols, row_bytes, fast, epi, &need); form != WS_NONE) {
     const bool own = epi.ws && epi.ws_bytes >= need;
     void* ws = own ? epi.ws : epi.no_alloc ? nullptr : gemm_temp_alloc(need, s);
     if (ws) {
-      const bool ok = type == T_Q4_K
-                          ? launch_gemv_q4k_many(w, X, out, epi.bias, nvec, rows, cols, row_bytes, ws, s)
-                          : launch_gemv_q6s(w, X, out, nvec, rows, cols, row_bytes, ws, s);
+      const bool ok = form == WS_MANY ? launch_gemv_q4k_many(w, X, out, epi.bias, nvec, rows, cols, row_bytes, ws, s)
+                      : form == WS_Q4S ? launch_gemv_q4s(w, X, out, epi.bias, nvec, rows, cols, row_bytes, ws, s)
+                                       : launch_gemv_q6s(w, X, out, nvec, rows, cols, row_bytes, ws, s);
       if (!own) gemm_temp_free(ws, s);
       if (!ok) return refused();
-      if (type != T_Q4_K && epi.bias) launch_add_bias(out, epi.bias, nvec, rows, s);
+      if (form == WS_Q6S && epi.bias) launch_add_bias(out, epi.bias, nvec, rows, s);
       return hip_status();
     }
   }

@@ -1546,6 +1546,405 @@ bool launch_gemv_q4k_many_shape(const void* w, const float* X, float* Y, const f
   return true;
 }
 
+// ---- batched Q4_K with the K range split over workgroups -------------------------------------------
+// qvx_qmatmul_n over Q4_K, NV (8 or 16) vectors a launch, each weight byte streamed once, every output
+// bit-identical to the one-vector kernel's (k_gemv_mx): the many-vector form's arithmetic per group
+// (the same MFMA sums, the same fold), the same chains and the same order of the K ranges.
+//  * Columns: RPC consecutive whole K ranges of mx_geometry (C super-blocks, at most 8), so every
+//    range's chain stays in one workgroup.  Workgroup b (16 waves) owns column b % ncol and the
+//    32-row tiles b / ncol, b / ncol + P, ...  Its items are the column's (super-block, group) pairs,
+//    item i = 4 sbl + c, taken by wave i % 16 (one or two a wave).  A wave's A fragments (sub-blocks
+//    2c and 2c + 1, 16 vectors x qh / ql) are the same for every tile: converted once (mx_quantize,
+//    through LDS, into registers); the records (Qa, Qb for the fold, sx for the chains) stay in LDS.
+//  * Tiles stream through a two-stage LDS ring (32 rows x the column's bytes, copied by
+//    buffer_load_dword ... lds, rows an odd number of dwords apart).  Per tile and item the wave runs
+//    the group's two v_mfma_i32_32x32x32_i8 and the fold V = fma(d, t, -dmin w) per (row, vector)
+//    into LDS; then four threads an output (one a group) run each range's chain A_c = fma(V, sx, A_c)
+//    over its super-blocks in the one-vector kernel's walk order (SbOrder) and add (A0 + A2) +
+//    (A1 + A3) across the quad: the range's partial, stored to the workspace.
+//  * k_q4s_sum adds each output's KQ range partials in order from 0.0f, then the bias.
+struct Q4sGeo {
+  int nsb;     // super-blocks a row
+  int KQ;      // K ranges of the one-vector geometry
+  int RPC;     // ranges a column
+  int ncol;    // columns (KQ / RPC)
+  int ntile;   // 32-row tiles
+  int P;       // workgroups a column
+  int C;       // super-blocks of the widest column (<= 4 IPW)
+  uint32_t row_bytes;
+};
+
+// The range kq's super-blocks [s0, s1) and walk direction (SbOrder: even ranges backward).
+__device__ __host__ inline void q4s_range(int kq, int nsb, int KQ, int& s0, int& s1, bool& back) {
+  s0 = kq * nsb / KQ;
+  s1 = (kq + 1) * nsb / KQ;
+  back = KQ > 1 && !(kq & 1);
+}
+
+// A 16-byte global load whose wait the kernel places itself (q4s_wait_x), before tile 0's copies:
+// the compiler, which does not see those, would otherwise wait for them too at the value's first use.
+typedef float q4s_f4 __attribute__((ext_vector_type(4)));
+__device__ inline q4s_f4 q4s_ldx(const float* p) {
+  q4s_f4 r;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p));
+  return r;
+}
+// Waits until at most N vector memory operations are outstanding; the loaded values are operands,
+// so no use of them moves above the wait.
+template <int N, int K>
+__device__ inline void q4s_wait_x(q4s_f4* a, q4s_f4* b) {
+  if constexpr (K == 1)
+    asm volatile("s_waitcnt vmcnt(%2)" : "+v"(a[0]), "+v"(b[0]) : "n"(N) : "memory");
+  else if constexpr (K == 2)
+    asm volatile("s_waitcnt vmcnt(%4)" : "+v"(a[0]), "+v"(a[1]), "+v"(b[0]), "+v"(b[1]) : "n"(N) : "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(%8)"
+                 : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3])
+                 : "n"(N)
+                 : "memory");
+}
+// s_waitcnt vmcnt(0) that memory accesses cannot move across.
+__device__ inline void q4s_wait_vm0() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Workgroup barrier for LDS only (see q6s_lds_barrier).
+__device__ inline void q4s_lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// Copy global -> LDS, 4 bytes a lane, as inline asm (see q6s_copy4: the kernel waits for its copies
+// itself; the s_nop is the wait state between the M0 write and the copy).
+__device__ inline void q4s_copy4(__amdgpu_buffer_rsrc_t r, uint32_t dst, uint32_t voff, uint32_t soff) {
+  asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(dst)
+               : "memory");
+}
+
+// s_waitcnt vmcnt(N) for the N = 0..3 tiles' copies that may stay in flight.
+template <int CPT>
+__device__ inline void q4s_wait_tiles(int n) {
+  switch (n) {
+    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    case 1: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(CPT) : "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * CPT) : "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * CPT) : "memory"); break;
+  }
+}
+
+// LDS plan of a launch: WPC workgroups a CU.  With one, whole 64-dword copies (every wave makes CPT a
+// tile, so the waits can count them) into up to 4 ring stages; with two (8 vectors, one item a wave),
+// the copies stop at the column's end and the ring has 2 stages.
+template <int NV, int IPW, int WPC>
+struct Q4sLds {
+  static constexpr int CMAX = 4 * IPW;                  // super-blocks a column at most
+  static constexpr int NIT = 4 * CMAX;                  // items at most
+  static constexpr int NO = NV * 32;                    // outputs a tile
+  static constexpr int NCP = (36 * CMAX + 63) / 64;     // 64-dword copies a staged row
+  static constexpr int CPT = 2 * NCP;                   // copies a wave a tile
+  static constexpr int SW = (WPC == 1 ? 64 * NCP : 36 * CMAX) + 1;  // LDS dwords a staged row (odd: rows on distinct banks)
+  static constexpr int STAGE = 32 * SW * 4;             // bytes of a ring stage
+  static constexpr int RB = NV == 8 && IPW == 1 ? 2 : 1;  // step-value buffers
+  static constexpr int RES = NIT * NO * 4;              // bytes of one
+  static constexpr int BUDGET = 160 * 1024 / WPC - NIT * 3 * 16 * 4 - 64;  // the CU's share less recq, sxl
+  static constexpr int NSF = (BUDGET - RB * RES) / STAGE;
+  static constexpr int NS = WPC == 2 ? 2 : NSF > 4 ? 4 : NSF;  // ring stages
+  static constexpr int BYTES = NS * STAGE + RB * RES;
+  static_assert(NS >= 2 && BYTES <= BUDGET, "two ring stages at least, within the budget");
+  static_assert(NV * CMAX * 512 <= STAGE + RB * RES, "conversion scratch fits in the last stage + the buffers");
+};
+
+template <int NV, int IPW, int WPC>
+__global__ __launch_bounds__(1024, 4 * WPC) void k_gemv_q4s(const uint8_t* __restrict__ W, const float* __restrict__ X,
+                                                            int rows, int cols, int nv, Q4sGeo geo,
+                                                            float* __restrict__ part) {
+  static_assert(NV == 8 || NV == 16, "8 or 16 vectors a launch");
+  static_assert(IPW == 1 || IPW == 2, "one or two items a wave");
+  static_assert(WPC == 1 || (WPC == 2 && NV == 8 && IPW == 1), "two workgroups a CU: 8 vectors, one item a wave");
+  using L = Q4sLds<NV, IPW, WPC>;
+  constexpr int NIT = L::NIT, NO = L::NO, NCP = L::NCP, SW = L::SW, STAGE = L::STAGE, RB = L::RB, NS = L::NS;
+  constexpr int KV = NV / 2;  // vectors a lane folds
+  __shared__ __attribute__((aligned(16))) uint8_t lds[L::BYTES];
+  __shared__ __attribute__((aligned(16))) float recq[NIT][2][16];  // [item][Qa, Qb][vector]
+  __shared__ float sxl[NIT][NV];                                    // [item][vector]
+  float* res = reinterpret_cast<float*>(lds + NS * STAGE);          // [buffer][item][vector][row]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = lane & 31, h = lane >> 5;
+  const int col = (int)blockIdx.x % geo.ncol, pi = (int)blockIdx.x / geo.ncol;
+  const int ntl = pi < geo.ntile ? (geo.ntile - pi + geo.P - 1) / geo.P : 0;
+  if (ntl == 0) return;  // the whole workgroup
+  int cs0, cs1;          // the column's super-blocks
+  {
+    bool bk;
+    int t0, t1;
+    q4s_range(col * geo.RPC, geo.nsb, geo.KQ, cs0, t0, bk);
+    q4s_range(col * geo.RPC + geo.RPC - 1, geo.nsb, geo.KQ, t1, cs1, bk);
+  }
+  const int C = cs1 - cs0, nit = 4 * C;
+  const uint32_t lds_base = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(QVX_LDS uint8_t*)lds);
+
+  // Copy of the workgroup's jt-th tile into stage s: wave w copies rows 2w, 2w + 1 (rows past the
+  // weight repeat its last row), each as NCP copies of 64 dwords from the column's first byte on --
+  // whole ones with one workgroup a CU (past the column: the row's next bytes, or zeros past the
+  // weight: the buffer's range; every offset is in the checked vector offset), so that every wave
+  // makes CPT copies a tile and the waits can count them; with two, up to the column's end.
+  auto issue = [&](int jt, int s) __attribute__((always_inline)) {
+    const int r0 = (pi + jt * geo.P) * 32, nr = min(32, rows - r0);
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(W + (size_t)r0 * geo.row_bytes), (short)0, (int)((uint32_t)nr * geo.row_bytes), (int)kRsrcWord3);
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const int r = min(2 * wave + rr, nr - 1);
+      const uint32_t vo = (uint32_t)r * geo.row_bytes + (uint32_t)cs0 * 144u + 4u * lane;
+      const uint32_t dst = lds_base + (uint32_t)(s * STAGE + (2 * wave + rr) * SW * 4);
+#pragma unroll
+      for (int i = 0; i < NCP; ++i)
+        if (WPC == 1 || 64 * i + lane < 36 * C) q4s_copy4(rsrc, dst + 256u * i, vo + 256u * i, 0u);
+    }
+  };
+
+  // The activations of the column, every vector, converted once into the last stage + the buffers
+  // (not in use yet) in the many-vector layout -- A fragments [v][sbl][sub-block][qh / ql][32 bytes]
+  // -- and the records into recq / sxl.  Tiles 0..NS-2 are copied during the conversion.
+  constexpr int NTK = NV * L::CMAX * 32 / 1024;  // conversion tasks a thread at most
+  static_assert(NTK == 1 || NTK == 2 || NTK == 4, "one, two or four conversion tasks a thread");
+  uint8_t* fr = lds + (NS - 1) * STAGE;
+  {
+    q4s_f4 y0[NTK], y1[NTK];
+#pragma unroll
+    for (int k = 0; k < NTK; ++k) {
+      const int t = min(tid + 1024 * k, NV * C * 32 - 1);
+      const int v = t / (C * 32), r = t - v * C * 32;  // r: task of the column, 8 elements
+      const float* src = X + (size_t)min(v, nv - 1) * cols + (size_t)cs0 * 256 + 8 * r;
+      y0[k] = q4s_ldx(src);
+      y1[k] = q4s_ldx(src + 4);
+    }
+    q4s_wait_x<0, NTK>(y0, y1);
+    for (int jt = 0; jt < NS - 1 && jt < ntl; ++jt) issue(jt, jt);
+#pragma unroll
+    for (int k = 0; k < NTK; ++k) {
+      if (1024 * k + 64 * wave >= NV * C * 32) break;  // wave-uniform: no task left for this wave
+      const int T = tid + 1024 * k, t = min(T, NV * C * 32 - 1);
+      const int v = t / (C * 32), r = t - v * C * 32;
+      const bool pad = v >= nv;  // padding vectors: zero fragments and records
+      const float4 x0 = pad ? make_float4(0.0f, 0.0f, 0.0f, 0.0f) : make_float4(y0[k].x, y0[k].y, y0[k].z, y0[k].w);
+      const float4 x1 = pad ? make_float4(0.0f, 0.0f, 0.0f, 0.0f) : make_float4(y1[k].x, y1[k].y, y1[k].z, y1[k].w);
+      const XQ8 q = mx_quantize(x0, x1);  // every lane of the wave takes part
+      if (T < NV * C * 32) {
+        const int sbl = r >> 5, g = (r >> 3) & 3, pt = r & 7;
+        const int sub = 2 * g + (pt >> 2), off = 8 * (pt & 3);
+        uint8_t* base = fr + ((v * C + sbl) * 8 + sub) * 64;
+        *reinterpret_cast<uint2*>(base + off) = make_uint2(q.h0, q.h1);
+        *reinterpret_cast<uint2*>(base + 32 + off) = make_uint2(q.l0, q.l1);
+        const int it = 4 * sbl + g;
+        if (pt == 0) {
+          sxl[it][v] = q.sx;
+          recq[it][0][v] = (float)q.sq;
+        }
+        if (pt == 4) recq[it][1][v] = (float)q.sq;
+      }
+    }
+  }
+  q4s_lds_barrier();
+  // a wave's A fragments: lane (row j = (vector j / 2, part j % 2), K half h) of sub-blocks 2c, 2c + 1
+  v4i af[IPW][2];
+#pragma unroll
+  for (int i = 0; i < IPW; ++i) {
+    const int it = wave + 16 * i, sbl = it >> 2, c = it & 3, va = j >> 1;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const bool on = it < nit && va < NV;
+      const uint8_t* p = fr + ((min(va, NV - 1) * C + min(sbl, C - 1)) * 8 + 2 * c + e) * 64 + (j & 1) * 32 + 16 * h;
+      const v4i z = {0, 0, 0, 0};
+      af[i][e] = on ? *reinterpret_cast<const v4i*>(p) : z;
+    }
+  }
+  q4s_lds_barrier();  // every wave's fragments are in registers: the last stage and the buffers are free
+
+  auto fold = [&](int s, float* rb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < IPW; ++i) {
+      const int it = wave + 16 * i;
+      if (it >= nit) break;  // wave-uniform
+      const int sbl = it >> 2, c = it & 3;
+      const uint8_t* rowp = lds + s * STAGE + j * SW * 4 + sbl * 144;
+      const uint32_t* hp = reinterpret_cast<const uint32_t*>(rowp);
+      const uint32_t* qp = reinterpret_cast<const uint32_t*>(rowp + 16 + 32 * c + 16 * h);
+      const u32x4 hd = {hp[0], hp[1], hp[2], hp[3]};
+      const uint32_t q0 = qp[0], q1 = qp[1], q2 = qp[2], q3 = qp[3];
+      const v4i bl = {(int)(q0 & 0x0F0F0F0Fu), (int)(q1 & 0x0F0F0F0Fu), (int)(q2 & 0x0F0F0F0Fu), (int)(q3 & 0x0F0F0F0Fu)};
+      const v4i bh = {(int)((q0 >> 4) & 0x0F0F0F0Fu), (int)((q1 >> 4) & 0x0F0F0F0Fu), (int)((q2 >> 4) & 0x0F0F0F0Fu),
+                      (int)((q3 >> 4) & 0x0F0F0F0Fu)};
+      const i32x16_t lo = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i][0], bl, i32x16_t{}, 0, 0, 0);
+      const i32x16_t hi = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i][1], bh, i32x16_t{}, 0, 0, 0);
+      const float d = f16lo(hd.x), dmin = f16hi(hd.x);
+      float sca, scb16, mna, mnb;
+      q4k_group_scales(hd, c, sca, scb16, mna, mnb);
+      const float scb = scb16 * 16.0f;  // see the many-vector form: the same product, rounded once
+#pragma unroll
+      for (int k = 0; k < KV; ++k) {
+        const int e = 4 * (k >> 1) + 2 * (k & 1), v = 4 * (k >> 1) + 2 * h + (k & 1);
+        const int ta = (int)((uint32_t)lo[e] << 7) + lo[e + 1];
+        const int tb = (int)(((uint32_t)hi[e] << 7) + (uint32_t)hi[e + 1]);
+        const float t = __builtin_fmaf((float)tb, scb, (float)ta * sca);
+        const float w = __builtin_fmaf(recq[it][1][v], mnb, recq[it][0][v] * mna);
+        rb[(it * NV + v) * 32 + j] = __builtin_fmaf(d, t, -dmin * w);
+      }
+    }
+  };
+  auto chains = [&](int jt, const float* rb) __attribute__((always_inline)) {
+    const int tile = pi + jt * geo.P;
+#pragma unroll
+    for (int o4 = tid; o4 < 4 * NO; o4 += 1024) {
+      const int o = o4 >> 2, c = o4 & 3, v = o >> 5;
+      for (int q = 0; q < geo.RPC; ++q) {
+        const int kq = col * geo.RPC + q;
+        int s0, s1;
+        bool back;
+        q4s_range(kq, geo.nsb, geo.KQ, s0, s1, back);
+        float A = 0.0f;
+        for (int u = 0; u < s1 - s0; ++u) {
+          const int it = 4 * ((back ? s1 - 1 - u : s0 + u) - cs0) + c;
+          A = __builtin_fmaf(rb[it * NO + o], sxl[it][v], A);
+        }
+        float u2 = A + dppf<0x4E>(A);  // quad_perm [2,3,0,1]: (A0 + A2) on the quad's lanes 0, 2, (A1 + A3) on 1, 3
+        u2 = u2 + dppf<0xB1>(u2);      // quad_perm [1,0,3,2]: (A0 + A2) + (A1 + A3)
+        if (c == 0) part[((size_t)tile * geo.KQ + kq) * NO + o] = u2;
+      }
+    }
+  };
+
+  // Tile jt: wait for its copies (up to NS - 2 later tiles' may stay in flight), then, after the
+  // barrier, copy tile jt + NS - 1 into the stage of tile jt - 1 (read by every wave by now), fold
+  // tile jt into the step values, and form the range partials (8 vectors, one item a wave: of tile
+  // jt - 1 from the other buffer; else of tile jt after a second barrier).
+  for (int jt = 0; jt < ntl; ++jt) {
+    const int s = jt % NS;
+    if constexpr (NS == 2)
+      q4s_wait_vm0();
+    else
+      q4s_wait_tiles<L::CPT>(min(NS - 2, ntl - 1 - jt));
+    q4s_lds_barrier();
+    if (jt + NS - 1 < ntl) issue(jt + NS - 1, (jt + NS - 1) % NS);
+    if constexpr (RB == 2) {
+      if (jt > 0) chains(jt - 1, res + ((jt - 1) & 1) * (L::RES / 4));
+      fold(s, res + (jt & 1) * (L::RES / 4));
+    } else {
+      fold(s, res);
+      q4s_lds_barrier();
+      chains(jt, res);
+    }
+  }
+  if constexpr (RB == 2) {
+    q4s_lds_barrier();
+    chains(ntl - 1, res + ((ntl - 1) & 1) * (L::RES / 4));
+  }
+}
+
+// out[v, r] = the KQ range partials of (v, r) added in order from 0.0f (+ bias[r]).
+template <bool BIAS>
+__global__ __launch_bounds__(256) void k_q4s_sum(const float* __restrict__ part, float* __restrict__ Y,
+                                                 const float* __restrict__ bias, int rows, int nv, int KQ, int NO,
+                                                 int ntile) {
+  const int idx = (int)blockIdx.x * 256 + (int)threadIdx.x;
+  if (idx >= ntile * NO) return;
+  const int tile = idx / NO, o = idx - tile * NO, v = o >> 5, r = tile * 32 + (o & 31);
+  if (v >= nv || r >= rows) return;
+  const float* p = part + (size_t)tile * KQ * NO + o;
+  float sum = 0.0f;
+  for (int k0 = 0; k0 < KQ; k0 += 8) {  // eight partials in flight at a time, added in order
+    float b8[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) b8[k] = p[(size_t)min(k0 + k, KQ - 1) * NO];
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (k0 + k < KQ) sum += b8[k];
+  }
+  Y[(size_t)v * rows + r] = BIAS ? sum + bias[r] : sum;
+}
+
+int device_cus();
+
+// The launch geometry: the one-vector geometry's ranges grouped into columns of >= 4 super-blocks
+// where they can be (and <= 8); false when a range alone is wider than 8 super-blocks.
+static bool q4s_geometry(int rows, int cols, size_t row_bytes, Q4sGeo& g) {
+  if (gemv_many_supported(cols, row_bytes) == 0 || rows <= 0) return false;
+  MxGeo mg{};
+  (void)mx_geometry(rows, cols, row_bytes, mg);
+  g.nsb = cols / 256;
+  g.KQ = mg.KQ;
+  g.ntile = (rows + 31) / 32;
+  g.row_bytes = (uint32_t)row_bytes;
+  auto width = [&](int rpc) {  // widest column of rpc ranges
+    int w = 0;
+    for (int c0 = 0; c0 < g.KQ; c0 += rpc) {
+      int s0, s1, t0, t1;
+      bool b;
+      q4s_range(c0, g.nsb, g.KQ, s0, t0, b);
+      q4s_range(c0 + rpc - 1, g.nsb, g.KQ, t1, s1, b);
+      w = std::max(w, s1 - s0);
+    }
+    return w;
+  };
+  g.RPC = 0;
+  for (int r = 1; r <= g.KQ; ++r) {
+    if (g.KQ % r) continue;
+    const int w = width(r);
+    if (w > 8) break;
+    g.RPC = r;
+    g.C = w;
+    int lo = g.nsb;  // narrowest column
+    for (int c0 = 0; c0 < g.KQ; c0 += r) {
+      int s0, s1, t0, t1;
+      bool b;
+      q4s_range(c0, g.nsb, g.KQ, s0, t0, b);
+      q4s_range(c0 + r - 1, g.nsb, g.KQ, t1, s1, b);
+      lo = std::min(lo, s1 - s0);
+    }
+    if (lo >= 4) break;
+  }
+  if (g.RPC == 0) return false;
+  g.ncol = g.KQ / g.RPC;
+  g.P = std::max(1, std::min(g.ntile, device_cus() / g.ncol));
+  return true;
+}
+
+// 1 if the split Q4_K form takes the shape, and its workspace bytes for nvec vectors (the range
+// partials) through *ws_bytes.
+bool gemv_q4s_route(int nvec, int rows, int cols, size_t row_bytes, size_t* ws_bytes) {
+  Q4sGeo g;
+  if (nvec <= 0 || !q4s_geometry(rows, cols, row_bytes, g)) return false;
+  if (ws_bytes) *ws_bytes = (size_t)g.ntile * g.KQ * (nvec <= 8 ? 8 : 16) * 32 * 4;
+  return true;
+}
+
+// qmatmul_n over Q4_K on the split form, 16 vectors a launch (8 when the whole call has at most 8),
+// each launch followed by the in-order sum of its range partials (and the bias).
+bool launch_gemv_q4s(const void* w, const float* X, float* Y, const float* bias, int nvec, int rows, int cols,
+                     size_t row_bytes, void* ws, hipStream_t s) {
+  Q4sGeo g;
+  if (nvec <= 0 || !ws || !q4s_geometry(rows, cols, row_bytes, g)) return false;
+  const int nvp = nvec <= 8 ? 8 : 16, NO = nvp * 32;
+  const auto* wb = static_cast<const uint8_t*>(w);
+  auto* part = static_cast<float*>(ws);
+  const unsigned grid = (unsigned)(g.ncol * g.P);
+  const bool ipw2 = g.C > 4;
+  for (int v0 = 0; v0 < nvec; v0 += nvp) {
+    const int nv = std::min(nvp, nvec - v0);
+    const float* Xv = X + (size_t)v0 * cols;
+    float* Yv = Y + (size_t)v0 * rows;
+    if (nvp == 8 && !ipw2) {
+      const int P2 = std::max(1, std::min(g.ntile, 2 * device_cus() / g.ncol));
+      Q4sGeo g2 = g;
+      g2.P = P2;
+      k_gemv_q4s<8, 1, 2><<<(unsigned)(g.ncol * P2), 1024, 0, s>>>(wb, Xv, rows, cols, nv, g2, part);
+    } else if (nvp == 8) {
+      k_gemv_q4s<8, 2, 1><<<grid, 1024, 0, s>>>(wb, Xv, rows, cols, nv, g, part);
+    } else {
+      if (ipw2) k_gemv_q4s<16, 2, 1><<<grid, 1024, 0, s>>>(wb, Xv, rows, cols, nv, g, part);
+      else k_gemv_q4s<16, 1, 1><<<grid, 1024, 0, s>>>(wb, Xv, rows, cols, nv, g, part);
+    }
+    const unsigned sg = (unsigned)((g.ntile * NO + 255) / 256);
+    if (bias) k_q4s_sum<true><<<sg, 256, 0, s>>>(part, Yv, bias, rows, nv, g.KQ, NO, g.ntile);
+    else k_q4s_sum<false><<<sg, 256, 0, s>>>(part, Yv, nullptr, rows, nv, g.KQ, NO, g.ntile);
+  }
+  return true;
+}
+
 // Q4_K GEMV of nvec vectors with the activations converted once (bias may be null).  ws: the
 // gemv_many_ws_bytes workspace, 16-byte aligned.  Returns false, having launched nothing, when the
 // shape is not handled here.

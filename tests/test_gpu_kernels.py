@@ -284,6 +284,26 @@ def test_gemv_q4k_long_row_batched_form_bit_identical(cuda, rows, cols, nvec):
         np.testing.assert_array_equal(f32bits(got[v]), f32bits(single[0]))
 
 
+@pytest.mark.parametrize("rows,cols,nvec", [(1024, 4096, 12), (1000, 4096, 20), (4096, 14336, 23), (100, 8192, 5),
+                                             (4099, 14336, 9), (300, 28672, 16), (257, 10240, 7)])
+def test_gemv_q4k_split_form_bit_identical(cuda, rows, cols, nvec):
+    """The split Q4_K form (K ranges of the one-vector geometry grouped into columns over workgroups,
+    range partials summed in order by a second launch; long rows from 5 vectors, small weights from
+    12, up to 23): within tolerance of the oracle and bit-identical to one-vector calls, for columns
+    of one range (long rows) and of several, 8- and 16-vector launches (16 + 7), ragged tiles,
+    workgroups of one tile and of several; one vector is all zeros."""
+    t = qvx.Q4_K
+    rng = np.random.default_rng(rows + 11 * cols + nvec)
+    w = random_weight(t, rows, cols, rng)
+    X = rng.standard_normal((nvec, cols)).astype(np.float32)
+    X[1] = 0.0
+    got = run_gemv(cuda, w, t, X, rows, cols)
+    assert max_rel(got, oracle.matmul_f64(w, t, X, nvec, rows, cols)) <= GEMV_TOL
+    for v in range(nvec):
+        single = run_gemv(cuda, w, t, X[v:v + 1], rows, cols)
+        np.testing.assert_array_equal(f32bits(got[v]), f32bits(single[0]))
+
+
 OTHER_TYPES = [qvx.F16, qvx.BF16, qvx.Q4_1, qvx.Q5_1, qvx.Q8_1]
 
 

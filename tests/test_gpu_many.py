@@ -103,6 +103,31 @@ def test_plan_replays_many_vector_calls(cuda):
     plan.close()
 
 
+def test_plan_replays_split_q4k_calls(cuda):
+    """The split Q4_K form in a plan (range partials in the plan's workspace, with a bias on one call):
+    replays bit-identical to the direct calls, several times."""
+    t = qvx.Q4_K
+    shapes = [(4096, 14336, 8), (1024, 4096, 16)]
+    Ws = [_weight(cuda, t, r, c, seed=80 + i) for i, (r, c, n) in enumerate(shapes)]
+    Xs = [qvx.fill_normal_t(cuda.empty((n, c), dtype=cuda.float32, device="cuda"), seed=90 + i)
+          for i, (r, c, n) in enumerate(shapes)]
+    want = [_many(cuda, W, t, X, r, c) for W, X, (r, c, n) in zip(Ws, Xs, shapes)]
+    outs = [cuda.full((n, r), float("nan"), dtype=cuda.float32, device="cuda") for (r, c, n) in shapes]
+    plan = decode.Plan()
+    for i in range(2):
+        plan.add(outs[i], decode.DevWeight(Ws[i], t, *shapes[i][:2]), Xs[i], shapes[i][2])
+    plan.instantiate()
+    s = cuda.cuda.current_stream().cuda_stream
+    for rep in range(3):
+        for o in outs:
+            o.fill_(float("nan"))
+        plan.launch(s)
+        cuda.cuda.synchronize()
+        for i in range(2):
+            assert cuda.equal(outs[i].view(cuda.int32), want[i].view(cuda.int32)), (rep, i)
+    plan.close()
+
+
 def test_plan_replays_batched_q6k_calls(cuda):
     """The batched Q6_K form in a plan (block sums in the plan's workspace, rows of several blocks;
     a one-block call needs none): replays bit-identical to the direct calls, several times."""
@@ -144,10 +169,12 @@ def test_many_matches_oracle_at_encoder_batch(cuda):
 
 
 @pytest.mark.parametrize("t,rows,cols,nvec", [(qvx.Q4_K, 1000, 4096, 40), (qvx.Q4_K, 512, 4096, 3),
-                                              (qvx.Q6_K, 512, 4096, 20), (qvx.F16, 300, 512, 5)])
+                                              (qvx.Q4_K, 700, 14336, 8), (qvx.Q6_K, 512, 4096, 20),
+                                              (qvx.F16, 300, 512, 5)])
 def test_bias_is_one_add_after_the_product(cuda, t, rows, cols, nvec):
-    """qvx_qmatmul_n_bias == qvx_qmatmul_n + bias, bit for bit, on the many-vector form (its epilogue)
-    and on the routes that add the bias in a launch of its own; a null bias is qvx_qmatmul_n."""
+    """qvx_qmatmul_n_bias == qvx_qmatmul_n + bias, bit for bit, on the many-vector form (its epilogue),
+    the split Q4_K form (its sum launch) and on the routes that add the bias in a launch of its own; a
+    null bias is qvx_qmatmul_n."""
     if t == qvx.F16:
         W = cuda.randn(rows * cols, device="cuda").to(cuda.float16).view(cuda.uint8)
     else:
