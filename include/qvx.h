@@ -108,7 +108,10 @@ int qvx_qmatmul(float* d_out, const void* d_w, uint32_t type, const float* d_x, 
  * tile and K range for batches up to 32 vectors), then the weights are streamed once per 64 vectors
  * (once per 16 up to 32 vectors) -- the reference's "dequantize each block once for all nVec dot
  * products" (qmatmul.hpp:24-32); smaller batches stream them once per 8 vectors and allocate
- * nothing.  Q6_K batches of 5 vectors or more (3 or more on rows of >= 8192 elements or weights of
+ * nothing, except on rows of >= 8192 elements from 5 to 23 vectors and on weights of <= 4 Mi elements
+ * from 12 to 23, which stream them once per 16 on a split form whose K ranges are spread over
+ * workgroups (a temporary of rows/32 * KQ * 1 or 2 KiB for the range partials; KQ = 4 or 16 ranges).
+ * Q6_K batches of 5 vectors or more (3 or more on rows of >= 8192 elements or weights of
  * >= 65536 rows) with cols a multiple of 2048 stream the weights once per 16 vectors on a
  * matrix-core form whose K range is split over workgroups by 2048-element blocks; for rows of more
  * than one block it takes a stream-ordered temporary for the block sums (rows/32 * blocks * 2 or 4
