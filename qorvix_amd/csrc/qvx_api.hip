@@ -106,12 +106,14 @@ namespace {
 
 constexpr int kMaxBlock = 256;  // largest block the operator accepts (qmatmul.cpp:11)
 // Whether a Q6_K batch takes the matrix-core form (measured crossovers against the VALU kernel, four
-// vectors a launch, on MI355X, graph-replayed): from 3 vectors on rows of >= 8192 elements or
-// weights of >= 65536 rows (4096 x 14336 at 3: 17.9 against 26.7 us; 128256 x 4096 at 3: 113 against
-// 126 us on the form it replaced), else from 5 (4096 x 4096 at 4: 9.1 against 7.2 us, at 5: 9.2
-// against 11.5).
+// vectors a launch, on MI355X, graph-replayed): from 5 vectors, and from 3 (the VALU kernel's
+// three-vector calls are slow: 4096 x 4096 10.0 against 8.5 us); at 4 on weights of >= 8192 rows or
+// columns (4096 x 14336: 18.5 against 27.5 us; 4096 x 4096: 8.5 against 7.5); at 2 on weights of
+// >= 65536 rows (128256 x 4096: 88 against 99 us).
 inline bool q6_batched(int nvec, int rows, int cols) {
-  return nvec >= 5 || (nvec >= 3 && (cols >= 8192 || rows >= 65536));
+  if (nvec >= 5 || nvec == 3) return true;
+  if (nvec == 4) return cols >= 8192 || rows >= 8192;
+  return nvec == 2 && rows >= 65536;
 }
 
 inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }

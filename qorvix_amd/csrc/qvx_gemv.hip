@@ -51,7 +51,7 @@ __global__ __launch_bounds__((gemv_threads<T, NV>())) void k_gemv(const uint8_t*
 }
 
 // ---- batched Q6_K on the matrix cores ----------------------------------------------------------
-// qmatmul_n over Q6_K weights, NV (8 or 16) vectors a launch, each weight byte streamed once, and
+// qmatmul_n over Q6_K weights, NV (4, 8 or 16) vectors a launch, each weight byte streamed once, and
 // bit-identical per vector to the one-vector VALU kernel above (k_gemv<T_Q6_K, ...>):
 //  * the same slots (32 elements: quarters e and e+2 of a 16-element column range of a
 //    128-element half, Lane<T_Q6_K>), the same activation conversion (convert_task<2>), the same
@@ -240,7 +240,9 @@ __device__ inline q6s_f4 q6s_ldx(const float* p) {
 // so no use of them moves above the wait.
 template <int N>
 __device__ inline void q6s_wait_x(q6s_f4* a, q6s_f4* b, int n) {
-  if (n == 2)
+  if (n == 1)
+    asm volatile("s_waitcnt vmcnt(%2)" : "+v"(a[0]), "+v"(b[0]) : "n"(N) : "memory");
+  else if (n == 2)
     asm volatile("s_waitcnt vmcnt(%4)" : "+v"(a[0]), "+v"(a[1]), "+v"(b[0]), "+v"(b[1]) : "n"(N) : "memory");
   else
     asm volatile("s_waitcnt vmcnt(%8)"
@@ -265,12 +267,12 @@ template <int NV>
 __global__ __launch_bounds__(1024) void k_gemv_q6s(const uint8_t* __restrict__ W, const float* __restrict__ X,
                                                    float* __restrict__ Y, int rows, int cols, int nv, Q6sGeo geo,
                                                    float* __restrict__ part) {
-  static_assert(NV == 8 || NV == 16, "8 or 16 vectors a launch");
+  static_assert(NV == 4 || NV == 8 || NV == 16, "4, 8 or 16 vectors a launch");
   using L6 = Lane<T_Q6_K>;
   constexpr int NJ = NV / 4, NO = NV * 32;
   constexpr int RW = NV * 40 + 2 * NV;  // words of one pair's converted operands: records, then steps
   static_assert(16 * 2 * RW * 4 <= kQ6sStage + 16 * NO * 4, "conversion scratch fits in stage 1 + sums");
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kQ6sStage + (NV == 8 ? 2 : 1) * 16 * NO * 4];
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kQ6sStage + (NV <= 8 ? 2 : 1) * 16 * NO * 4];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ln = lane & 31, g = lane >> 5;
@@ -304,7 +306,7 @@ __global__ __launch_bounds__(1024) void k_gemv_q6s(const uint8_t* __restrict__ W
   {
     constexpr int NT = 16 * NV / 64;  // conversion tasks a lane: 8 NV a pair
     uint32_t* cw = reinterpret_cast<uint32_t*>(lds + kQ6sStage) + wave * 2 * RW;
-    static_assert(NT == 2 || NT == 4, "two or four tasks a lane");
+    static_assert(NT == 1 || NT == 2 || NT == 4, "one, two or four tasks a lane");
     q6s_f4 y0[NT], y1[NT];
 #pragma unroll
     for (int k = 0; k < NT; ++k) {
@@ -381,7 +383,7 @@ __global__ __launch_bounds__(1024) void k_gemv_q6s(const uint8_t* __restrict__ W
     }
   };
 
-  // Tile j.  With 8 vectors: one barrier a tile, after which tile j + 1 is copied into the other
+  // Tile j.  With 4 or 8 vectors: one barrier a tile, after which tile j + 1 is copied into the other
   // stage (whose tile j - 1 every wave has read), tile j is read and folded into one of two
   // step-sum buffers, and the block sums of tile j - 1 are formed from the other.  With 16 (room for
   // one buffer): tile j + 2 is copied once every wave has read tile j, and tile j's block sums are
@@ -390,7 +392,7 @@ __global__ __launch_bounds__(1024) void k_gemv_q6s(const uint8_t* __restrict__ W
   for (int j = 0; j < ntl; ++j) {
     const int s = j & 1;
     Q6Half hw;
-    if constexpr (NV == 8) {
+    if constexpr (NV <= 8) {
       q6s_wait_vm<0>();  // tile j's copies (and the block-sum stores issued since)
       q6s_lds_barrier();
       if (j + 1 < ntl) issue(j + 1, s ^ 1);
@@ -411,7 +413,7 @@ __global__ __launch_bounds__(1024) void k_gemv_q6s(const uint8_t* __restrict__ W
       combine(j, res);
     }
   }
-  if constexpr (NV == 8) {
+  if constexpr (NV <= 8) {
     if (ntl > 0) {
       q6s_lds_barrier();
       combine(ntl - 1, res + ((ntl - 1) & 1) * 16 * NO);
@@ -456,20 +458,20 @@ inline Q6sGeo q6s_geometry(int rows, int cols, size_t row_bytes) {
 bool gemv_q6s_route(int nvec, int rows, int cols, size_t row_bytes, size_t* ws_bytes) {
   if (cols <= 0 || cols % 2048 != 0 || rows <= 0 || nvec <= 0 || row_bytes > 0xFFFFFFFFull / 64) return false;
   if (ws_bytes) {
-    const int nvp = nvec <= 8 ? 8 : 16, nb = cols / 2048;
+    const int nvp = nvec <= 4 ? 4 : nvec <= 8 ? 8 : 16, nb = cols / 2048;
     *ws_bytes = nb > 1 ? (size_t)((rows + 31) / 32) * nb * nvp * 32 * 4 : 0;
   }
   return true;
 }
 
-// qmatmul_n over Q6_K on the batched form, 16 vectors a launch (8 when the whole call has at most 8),
-// each launch followed by the in-order sum of its block sums when rows have several blocks.
+// qmatmul_n over Q6_K on the batched form, 16 vectors a launch (8 or 4 when the whole call has at most
+// 8 or 4), each launch followed by the in-order sum of its block sums when rows have several blocks.
 bool launch_gemv_q6s(const void* w, const float* X, float* Y, int nvec, int rows, int cols, size_t row_bytes,
                      void* ws, hipStream_t s) {
   if (!gemv_q6s_route(nvec, rows, cols, row_bytes, nullptr)) return false;
   const Q6sGeo geo = q6s_geometry(rows, cols, row_bytes);
   if (geo.nb > 1 && !ws) return false;
-  const int nvp = nvec <= 8 ? 8 : 16, NO = nvp * 32;
+  const int nvp = nvec <= 4 ? 4 : nvec <= 8 ? 8 : 16, NO = nvp * 32;
   const auto* wb = static_cast<const uint8_t*>(w);
   auto* part = static_cast<float*>(ws);
   const unsigned grid = (unsigned)(geo.nb * geo.P);
@@ -477,7 +479,8 @@ bool launch_gemv_q6s(const void* w, const float* X, float* Y, int nvec, int rows
     const int nv = std::min(nvp, nvec - v0);
     const float* Xv = X + (size_t)v0 * cols;
     float* Yv = Y + (size_t)v0 * rows;
-    if (nvp == 8) k_gemv_q6s<8><<<grid, 1024, 0, s>>>(wb, Xv, Yv, rows, cols, nv, geo, part);
+    if (nvp == 4) k_gemv_q6s<4><<<grid, 1024, 0, s>>>(wb, Xv, Yv, rows, cols, nv, geo, part);
+    else if (nvp == 8) k_gemv_q6s<8><<<grid, 1024, 0, s>>>(wb, Xv, Yv, rows, cols, nv, geo, part);
     else k_gemv_q6s<16><<<grid, 1024, 0, s>>>(wb, Xv, Yv, rows, cols, nv, geo, part);
     if (geo.nb > 1)
       k_q6s_sum<<<(unsigned)((geo.ntile * NO + 255) / 256), 256, 0, s>>>(part, Yv, rows, nv, geo.nb, NO, geo.ntile);

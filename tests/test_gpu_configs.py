@@ -140,11 +140,12 @@ def test_gemv_q6k_lm_head_m16(cuda):
         np.testing.assert_array_equal(single.cpu().numpy().view(np.uint32), out[v].cpu().numpy().view(np.uint32))
 
 
-@pytest.mark.parametrize("rows,cols,m", [(65573, 2048, 9), (70000, 6144, 16), (128256, 4096, 5)])
+@pytest.mark.parametrize("rows,cols,m", [(65573, 2048, 9), (70000, 6144, 16), (128256, 4096, 5), (128256, 4096, 2),
+                                          (70000, 6144, 4)])
 def test_gemv_q6k_tall_weights(cuda, rows, cols, m):
     """The batched Q6_K form on weights of 65536 rows or more (a workgroup streams ~30 tiles through
-    its ring): ragged last tiles, a row of one 64-slot block and of several, 16- and 9-vector
-    launches; every vector bit-identical to a one-vector call."""
+    its ring): ragged last tiles, a row of one 64-slot block and of several, 16-, 9-, 5-, 4- and
+    2-vector launches; every vector bit-identical to a one-vector call."""
     t = qvx.Q6_K
     W, X, out = _check_gemv_slice(cuda, t, rows, cols, m, seed=8150 + m, stride=101)
     for v in range(m):

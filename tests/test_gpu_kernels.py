@@ -246,13 +246,13 @@ def test_gemv_q4k_batched_form_bit_identical(cuda, rows, cols, nvec):
 @pytest.mark.parametrize("rows,cols,nvec", [(300, 2048, 12), (17, 2048, 16), (1000, 14336, 13), (4099, 4096, 16),
                                              (64, 6144, 12), (8200, 4096, 5), (4096, 2048, 8), (257, 4096, 20),
                                              (4096, 14336, 3), (2048, 8192, 4), (33, 14336, 8), (5000, 2048, 6),
-                                             (14336, 4096, 9), (700, 4096, 24)])
+                                             (14336, 4096, 9), (700, 4096, 24), (300, 4096, 3), (8200, 2048, 4)])
 def test_gemv_q6k_batched_form_bit_identical(cuda, rows, cols, nvec):
     """The batched matrix-core Q6_K form (8 or 16 vectors a launch, K a multiple of 2048, the K range
     split over workgroups by 64-slot blocks; every case here is routed to it): within tolerance of
     the oracle and bit-identical to one-vector calls (the VALU kernel), for rows of one block (no
     running sum, no workspace) and of several, ragged 32-row tiles, grids where a workgroup takes
-    one tile and several (the two-stage ring), 3- and 4-vector calls on long rows, and launches of
+    one tile and several (the two-stage ring), 4-vector launches (3 and 4 vectors), and launches of
     16 + 4 and 16 + 8 vectors; one vector is all zeros (the signs of zero sums must agree too)."""
     t = qvx.Q6_K
     rng = np.random.default_rng(rows + 7 * cols + nvec)
