@@ -53,7 +53,8 @@ bool gemv_q4s_route(int nvec, int rows, int cols, size_t row_bytes, size_t* ws_b
 bool launch_gemv_q4s(const void* w, const float* X, float* Y, const float* bias, int nvec, int rows, int cols,
                      size_t row_bytes, void* ws, hipStream_t s);
 bool launch_gemv_q6s(const void* w, const float* X, float* Y, int nvec, int rows, int cols, size_t row_bytes,
-                     void* ws, hipStream_t s);
+                     void* ws, hipStream_t s, uint32_t* cnt);
+int gemv_q6s_counters(int nvec, int rows, int cols);
 int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M, int rows, int cols,
                  int variant, hipStream_t s, void* ws, size_t ws_cap);
 int launch_gemm16_entry(float* out, const uint16_t* X, const uint16_t* B, int M, int N, int K, bool bf16,
@@ -91,7 +92,9 @@ struct qvx_plan {
     int group;  // calls sharing a group >= 0 are independent of each other (one fork); -1: in order
     GemvEpi epi;  // fused RMSNorm / SwiGLU (rows = the weight's rows: 2 ffn for SwiGLU)
     std::vector<GemvMember> members;  // non-empty: a grouped call over X (nvec 1), out / w / type / rows unused
-    size_t ws_off = 0, ws_bytes = 0;  // its slice of the plan's workspace (the many-vector form)
+    size_t ws_off = 0, ws_bytes = 0;  // its slice of the plan's workspace (forms that take one)
+    size_t cnt_off = 0;               // its zeroed counters (cnt_n), a slice no other call shares
+    int cnt_n = 0;
   };
   std::vector<Call> calls;
   void* ws = nullptr;  // device workspace of the recorded calls, allocated by qvx_plan_instantiate
@@ -285,7 +288,10 @@ int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int
     if (ws) {
       const bool ok = form == WS_MANY ? launch_gemv_q4k_many(w, X, out, epi.bias, nvec, rows, cols, row_bytes, ws, s)
                       : form == WS_Q4S ? launch_gemv_q4s(w, X, out, epi.bias, nvec, rows, cols, row_bytes, ws, s)
-                                       : launch_gemv_q6s(w, X, out, nvec, rows, cols, row_bytes, ws, s);
+                                       : launch_gemv_q6s(w, X, out, nvec, rows, cols, row_bytes, ws, s,
+                                                         own && epi.cnt_n >= gemv_q6s_counters(nvec, rows, cols)
+                                                             ? epi.cnt
+                                                             : nullptr);
       if (!own) gemm_temp_free(ws, s);
       if (!ok) return refused();
       if (form == WS_Q6S && epi.bias) launch_add_bias(out, epi.bias, nvec, rows, s);
@@ -331,7 +337,7 @@ int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int
   if (fast && type == T_Q6_K && q6_batched(nvec, rows, cols) && !epi.flags()) {
     size_t need = 0;
     if (gemv_q6s_route(nvec, rows, cols, row_bytes, &need) && need == 0) {
-      if (!launch_gemv_q6s(w, X, out, nvec, rows, cols, row_bytes, nullptr, s)) return refused();
+      if (!launch_gemv_q6s(w, X, out, nvec, rows, cols, row_bytes, nullptr, s, nullptr)) return refused();
       return hip_status();
     }
   }
@@ -756,12 +762,18 @@ static int run_call(const qvx_plan& plan, const qvx_plan::Call& c, hipStream_t s
     epi.ws = static_cast<uint8_t*>(plan.ws) + c.ws_off;
     epi.ws_bytes = c.ws_bytes;
   }
+  if (plan.ws && c.cnt_n) {
+    epi.cnt = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(plan.ws) + c.cnt_off);
+    epi.cnt_n = c.cnt_n;
+  }
   return gemv(c.out, c.w, c.type, c.X, c.nvec, c.rows, c.cols, s, epi);
 }
 
-// Lays out the plan's workspace: each call that takes the many-vector form gets a 256-byte aligned
+// Lays out the plan's workspace: each call whose form takes a workspace gets a 256-byte aligned
 // slice; calls in order share offset 0, the calls of one fork (which run concurrently) get disjoint
-// slices.  Returns the bytes the plan needs.
+// slices.  After them, each call that can use tile counters gets its own slice of them (zeroed by
+// qvx_plan_instantiate; the kernels leave them zero, so no other data may share them).  Returns the
+// bytes the plan needs.
 static size_t plan_ws_layout(qvx_plan& plan) {
   size_t total = 0;
   for (size_t i = 0; i < plan.calls.size();) {
@@ -772,19 +784,28 @@ static size_t plan_ws_layout(qvx_plan& plan) {
     for (size_t k = i; k < i + n; ++k) {
       auto& c = plan.calls[k];
       c.ws_off = c.ws_bytes = 0;
+      c.cnt_off = 0;
+      c.cnt_n = 0;
       if (!c.members.empty() || c.cols <= 0 || c.rows <= 0) continue;
       const TypeInfo* ti = type_info(c.type);
       if (!ti || ti->block == 0) continue;
       const size_t row_bytes = (size_t)(c.cols / (int)ti->block) * ti->bytes;
       const bool fast = aligned16(c.w) && aligned16(c.X) && row_bytes % 16 == 0;
-      const size_t need = ws_route_bytes(c.type, c.nvec, c.rows, c.cols, row_bytes, fast, c.epi);
-      if (!need) continue;
+      size_t need = 0;
+      const WsForm form = ws_route(c.type, c.nvec, c.rows, c.cols, row_bytes, fast, c.epi, &need);
+      if (form == WS_NONE) continue;
       c.ws_off = off;
       c.ws_bytes = need;
       off += (need + 255) & ~(size_t)255;
+      if (form == WS_Q6S) c.cnt_n = gemv_q6s_counters(c.nvec, c.rows, c.cols);
     }
     if (off > total) total = off;
     i += n;
+  }
+  for (auto& c : plan.calls) {
+    if (!c.cnt_n) continue;
+    c.cnt_off = total;
+    total += ((size_t)c.cnt_n * 4 + 255) & ~(size_t)255;
   }
   return total;
 }
@@ -908,6 +929,12 @@ int qvx_plan_instantiate(qvx_plan* plan) {
   if (!guard.ok) return QVX_E_HIP;
   if (const size_t wsb = plan_ws_layout(*plan)) {
     if (hipMalloc(&plan->ws, wsb) != hipSuccess) {
+      plan->ws = nullptr;
+      (void)hipGetLastError();
+      return QVX_E_HIP;
+    }
+    if (hipMemset(plan->ws, 0, wsb) != hipSuccess) {  // the counters start at zero (outside any capture)
+      (void)hipFree(plan->ws);
       plan->ws = nullptr;
       (void)hipGetLastError();
       return QVX_E_HIP;

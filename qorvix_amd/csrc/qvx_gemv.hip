@@ -263,10 +263,13 @@ struct Q6sGeo {
   uint32_t row_bytes;
 };
 
+// cnt (8 vectors or fewer, 2..8 blocks a row): per-tile counters that are zero on entry and are left
+// zero; the block sums are then added in the kernel by the workgroup that counts a tile's last
+// block in, instead of by k_q6s_sum.
 template <int NV>
 __global__ __launch_bounds__(1024) void k_gemv_q6s(const uint8_t* __restrict__ W, const float* __restrict__ X,
                                                    float* __restrict__ Y, int rows, int cols, int nv, Q6sGeo geo,
-                                                   float* __restrict__ part) {
+                                                   float* __restrict__ part, uint32_t* __restrict__ cnt) {
   static_assert(NV == 4 || NV == 8 || NV == 16, "4, 8 or 16 vectors a launch");
   using L6 = Lane<T_Q6_K>;
   constexpr int NJ = NV / 4, NO = NV * 32;
@@ -376,7 +379,10 @@ __global__ __launch_bounds__(1024) void k_gemv_q6s(const uint8_t* __restrict__ W
         const int v = o >> 5, r = tile * 32 + (o & 31);
         if (geo.nb == 1) {
           if (v < nv && r < rows) Y[(size_t)v * rows + r] = u;
-        } else {
+        } else if (cnt) {  // device-coherent: read back by the tile's last workgroup in this launch
+          __hip_atomic_store(part + ((size_t)tile * geo.nb + blk) * NO + o, u, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        } else {  // read back by the sum launch
           part[((size_t)tile * geo.nb + blk) * NO + o] = u;
         }
       }
@@ -389,16 +395,50 @@ __global__ __launch_bounds__(1024) void k_gemv_q6s(const uint8_t* __restrict__ W
   // one buffer): tile j + 2 is copied once every wave has read tile j, and tile j's block sums are
   // formed after a second barrier.
   float* res = reinterpret_cast<float*>(lds + 2 * kQ6sStage);
+  // In-kernel sums (cnt): tile jt's block sums are stored during tile jt + 1.  During tile jt + 2
+  // (every wave has waited for its stores and passed the barrier) thread 0 counts the workgroup in
+  // with a wrapping increment, which leaves the counter zero again after the tile's last workgroup;
+  // at the top of tile jt + 3 (the ticket has arrived with that tile's wait) it posts whether the
+  // workgroup was the last, and that workgroup then loads the nb block sums of each output, adds them
+  // in block order from 0.0f after the fold and stores the outputs.  The loads follow the ticket
+  // through the LDS flag and a barrier (the protocol of split_k_last).
+  __shared__ int lastf[2];
+  const bool fin = NV <= 8 && cnt != nullptr;
+  auto tile_of = [&](int jt) { return pi + jt * geo.P; };
+  auto ticket = [&](int jt) __attribute__((always_inline)) {
+    return __builtin_amdgcn_atomic_inc32(cnt + tile_of(jt), (uint32_t)(geo.nb - 1), __ATOMIC_RELAXED, "agent");
+  };
+  auto final_loads = [&](int jt, float (&fv)[8]) __attribute__((always_inline)) {
+    const float* tp = part + (size_t)tile_of(jt) * geo.nb * NO + tid;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      fv[k] = __hip_atomic_load(tp + (size_t)min(k, geo.nb - 1) * NO, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+  auto final_store = [&](int jt, const float (&fv)[8]) __attribute__((always_inline)) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (k < geo.nb) sum += fv[k];
+    const int v = tid >> 5, r = tile_of(jt) * 32 + (tid & 31);
+    if (v < nv && r < rows) Y[(size_t)v * rows + r] = sum;
+  };
+  uint32_t tkt = 0;
   for (int j = 0; j < ntl; ++j) {
     const int s = j & 1;
     Q6Half hw;
     if constexpr (NV <= 8) {
-      q6s_wait_vm<0>();  // tile j's copies (and the block-sum stores issued since)
+      q6s_wait_vm<0>();  // tile j's copies (and the stores, loads and ticket issued since)
+      if (fin && j >= 3 && tid == 0) lastf[j & 1] = tkt == (uint32_t)(geo.nb - 1) ? 1 : 0;  // tile j - 3
       q6s_lds_barrier();
       if (j + 1 < ntl) issue(j + 1, s ^ 1);
       read_tile(s, hw);
+      if (fin && j >= 2 && tid == 0) tkt = ticket(j - 2);
+      const bool fl = fin && j >= 3 && lastf[j & 1] != 0;  // this workgroup sums tile j - 3
+      float fv[8];
+      if (fl && tid < NO) final_loads(j - 3, fv);
       if (j > 0) combine(j - 1, res + ((j - 1) & 1) * 16 * NO);
       fold_tile(hw, res + (j & 1) * 16 * NO);
+      if (fl && tid < NO) final_store(j - 3, fv);
     } else {
       // this wave's copies of tile j are done when at most tile j + 1's are still in flight (loads
       // complete in order; the block-sum stores in between are not counted: they may complete in
@@ -414,9 +454,27 @@ __global__ __launch_bounds__(1024) void k_gemv_q6s(const uint8_t* __restrict__ W
     }
   }
   if constexpr (NV <= 8) {
-    if (ntl > 0) {
+    const int J = ntl;
+    q6s_lds_barrier();  // the last fold is done
+    combine(J - 1, res + ((J - 1) & 1) * 16 * NO);
+    if (fin) {
+      // tiles J - 3 (its ticket is in flight), J - 2 and J - 1 (their stores complete with this wait)
+      q6s_wait_vm<0>();
+      if (tid == 0) {
+        lastf[0] = J >= 3 && tkt == (uint32_t)(geo.nb - 1) ? 1 : 0;
+        lastf[1] = J >= 2 && ticket(J - 2) == (uint32_t)(geo.nb - 1) ? 1 : 0;
+      }
+      __shared__ int lastf2;
+      if (tid == 0) lastf2 = ticket(J - 1) == (uint32_t)(geo.nb - 1) ? 1 : 0;
       q6s_lds_barrier();
-      combine(ntl - 1, res + ((ntl - 1) & 1) * 16 * NO);
+      const int fl3[3] = {lastf[0], lastf[1], lastf2};
+#pragma unroll
+      for (int t = 0; t < 3; ++t) {
+        if (fl3[t] == 0 || tid >= NO) continue;
+        float fv[8];
+        final_loads(J - 3 + t, fv);
+        final_store(J - 3 + t, fv);
+      }
     }
   }
 }
@@ -455,34 +513,51 @@ inline Q6sGeo q6s_geometry(int rows, int cols, size_t row_bytes) {
 
 // 1 if the batched form takes the shape (K a multiple of 2048, row pitch below 4 GiB), and its
 // workspace bytes for nvec vectors through *ws_bytes (the block sums; none for rows of one block).
+inline int q6s_nvp(int nvec) { return nvec <= 4 ? 4 : nvec <= 8 ? 8 : 16; }
 bool gemv_q6s_route(int nvec, int rows, int cols, size_t row_bytes, size_t* ws_bytes) {
   if (cols <= 0 || cols % 2048 != 0 || rows <= 0 || nvec <= 0 || row_bytes > 0xFFFFFFFFull / 64) return false;
   if (ws_bytes) {
-    const int nvp = nvec <= 4 ? 4 : nvec <= 8 ? 8 : 16, nb = cols / 2048;
-    *ws_bytes = nb > 1 ? (size_t)((rows + 31) / 32) * nb * nvp * 32 * 4 : 0;
+    const int nb = cols / 2048;
+    *ws_bytes = nb > 1 ? (size_t)((rows + 31) / 32) * nb * q6s_nvp(nvec) * 32 * 4 : 0;
   }
   return true;
 }
 
+// Tile counters a call can use to add its block sums in the kernel: one a 32-row tile; 0 where the
+// call has no use for them.  Only launches of 8 vectors or fewer with 2..8 blocks a row whose
+// workgroups take at most 2 tiles each use them: measured, they save the sum launch there (1024 x
+// 4096 at M = 8: 8.4 -> 7.4 us, 4096 x 4096: 9.7 -> 8.5) but cost more than it on deeper loops (4096
+// x 14336 at M = 8, 4 tiles a workgroup: 19.6 -> 20.1; the LM head at M = 4: 88 -> 97), where the
+// workgroups that come last on several tiles stretch the tail.
+int gemv_q6s_counters(int nvec, int rows, int cols) {
+  const int nb = cols / 2048, ntile = (rows + 31) / 32;
+  if (q6s_nvp(nvec) > 8 || nb < 2 || nb > 8) return 0;
+  const int P = std::max(1, std::min(ntile, device_cus() / nb));
+  return (ntile + P - 1) / P <= 2 ? ntile : 0;
+}
+
 // qmatmul_n over Q6_K on the batched form, 16 vectors a launch (8 or 4 when the whole call has at most
-// 8 or 4), each launch followed by the in-order sum of its block sums when rows have several blocks.
+// 8 or 4), each launch followed by the in-order sum of its block sums when rows have several blocks:
+// in the kernel when the call brings zeroed tile counters (cnt: gemv_q6s_counters of them, zero on
+// entry and left zero -- a plan's), else in a launch of its own.
 bool launch_gemv_q6s(const void* w, const float* X, float* Y, int nvec, int rows, int cols, size_t row_bytes,
-                     void* ws, hipStream_t s) {
+                     void* ws, hipStream_t s, uint32_t* cnt) {
   if (!gemv_q6s_route(nvec, rows, cols, row_bytes, nullptr)) return false;
   const Q6sGeo geo = q6s_geometry(rows, cols, row_bytes);
   if (geo.nb > 1 && !ws) return false;
-  const int nvp = nvec <= 4 ? 4 : nvec <= 8 ? 8 : 16, NO = nvp * 32;
+  const int nvp = q6s_nvp(nvec), NO = nvp * 32;
   const auto* wb = static_cast<const uint8_t*>(w);
   auto* part = static_cast<float*>(ws);
+  if (gemv_q6s_counters(nvec, rows, cols) == 0) cnt = nullptr;
   const unsigned grid = (unsigned)(geo.nb * geo.P);
   for (int v0 = 0; v0 < nvec; v0 += nvp) {
     const int nv = std::min(nvp, nvec - v0);
     const float* Xv = X + (size_t)v0 * cols;
     float* Yv = Y + (size_t)v0 * rows;
-    if (nvp == 4) k_gemv_q6s<4><<<grid, 1024, 0, s>>>(wb, Xv, Yv, rows, cols, nv, geo, part);
-    else if (nvp == 8) k_gemv_q6s<8><<<grid, 1024, 0, s>>>(wb, Xv, Yv, rows, cols, nv, geo, part);
-    else k_gemv_q6s<16><<<grid, 1024, 0, s>>>(wb, Xv, Yv, rows, cols, nv, geo, part);
-    if (geo.nb > 1)
+    if (nvp == 4) k_gemv_q6s<4><<<grid, 1024, 0, s>>>(wb, Xv, Yv, rows, cols, nv, geo, part, cnt);
+    else if (nvp == 8) k_gemv_q6s<8><<<grid, 1024, 0, s>>>(wb, Xv, Yv, rows, cols, nv, geo, part, cnt);
+    else k_gemv_q6s<16><<<grid, 1024, 0, s>>>(wb, Xv, Yv, rows, cols, nv, geo, part, nullptr);
+    if (geo.nb > 1 && !cnt)
       k_q6s_sum<<<(unsigned)((geo.ntile * NO + 255) / 256), 256, 0, s>>>(part, Yv, rows, nv, geo.nb, NO, geo.ntile);
   }
   return true;

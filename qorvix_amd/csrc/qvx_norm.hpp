@@ -104,8 +104,10 @@ struct GemvEpi {
   bool swiglu = false;  // weight rows interleaved in 16-row (gate, up) groups; out = silu(gate) * up
   const float* bias = nullptr;  // non-null (plain calls only): out = W . x + bias, the add last
   bool no_alloc = false;  // the call must not take stream-ordered temporaries (graph-captured plans)
-  void* ws = nullptr;     // non-null: workspace the caller owns for the many-vector Q4_K form
+  void* ws = nullptr;     // non-null: workspace the caller owns for the forms that take one
   size_t ws_bytes = 0;
+  uint32_t* cnt = nullptr;  // non-null: cnt_n counters, zero on entry, to be left zero (a plan's)
+  int cnt_n = 0;
   int flags() const { return (norm_w ? EPI_NORM : 0) | (swiglu ? EPI_SWIGLU : 0); }
 };
 
