@@ -111,12 +111,15 @@ int qvx_qmatmul(float* d_out, const void* d_w, uint32_t type, const float* d_x, 
  * nothing, except on rows of >= 8192 elements from 5 to 23 vectors and on weights of <= 4 Mi elements
  * from 12 to 23, which stream them once per 16 on a split form whose K ranges are spread over
  * workgroups (a temporary of rows/32 * KQ * 1 or 2 KiB for the range partials; KQ = 4 or 16 ranges).
- * Q6_K batches of 5 vectors or more (3 or more on rows of >= 8192 elements or weights of
- * >= 65536 rows) with cols a multiple of 2048 stream the weights once per 16 vectors on a
- * matrix-core form whose K range is split over workgroups by 2048-element blocks; for rows of more
- * than one block it takes a stream-ordered temporary for the block sums (rows/32 * blocks * 2 or 4
- * KiB; without one the batch runs on the VALU kernel, four vectors a launch).  A plan gives these
- * calls a workspace of its own, allocated by qvx_plan_instantiate, so its replays allocate nothing. */
+ * Q6_K batches of 3 vectors and of 5 or more, of 4 on weights of >= 8192 rows or columns and of 2
+ * on weights of >= 65536 rows, with cols a multiple of 2048, stream the weights once per 16 vectors
+ * (per 4 or 8 when the call has at most that many) on a matrix-core form whose K range is split over
+ * workgroups by 2048-element blocks; for rows of more than one block it takes a stream-ordered
+ * temporary for the block sums (rows/32 * blocks * 0.5, 1 or 2 KiB; without one the batch runs on
+ * the VALU kernel, four vectors a launch) and adds them in a second launch.  A plan gives these calls
+ * a workspace of its own, allocated by qvx_plan_instantiate, so its replays allocate nothing; on
+ * shallow grids (<= 8 vectors, at most two 32-row tiles a workgroup) it also gives the call one
+ * zeroed counter a 32-row tile, with which the kernel adds the block sums itself. */
 int qvx_qmatmul_n(float* d_out, const void* d_w, uint32_t type, const float* d_X, int n_vec,
                   int rows, int cols, void* stream);
 

@@ -153,6 +153,38 @@ def test_plan_replays_batched_q6k_calls(cuda):
     plan.close()
 
 
+def test_plan_adds_q6k_block_sums_in_the_kernel(cuda):
+    """Batched Q6_K calls of <= 8 vectors whose workgroups take at most two 32-row tiles add their
+    block sums in the kernel inside a plan (per-tile counters in the plan's workspace, zeroed at
+    instantiation, left zero by the tile's last workgroup); the direct calls use the sum launch.
+    Shapes: one and two tiles a workgroup, 2, 4 and 8 blocks a row, ragged rows, 3 to 8 vectors,
+    two calls in one fork (disjoint counter slices); every replay bit-identical to the direct call."""
+    t = qvx.Q6_K
+    shapes = [(1024, 4096, 8), (8192, 4096, 7), (1000, 8192, 4), (2048, 8192, 5), (500, 16384, 3)]
+    Ws = [_weight(cuda, t, r, c, seed=100 + i) for i, (r, c, n) in enumerate(shapes)]
+    Xs = [qvx.fill_normal_t(cuda.empty((n, c), dtype=cuda.float32, device="cuda"), seed=110 + i)
+          for i, (r, c, n) in enumerate(shapes)]
+    want = [_many(cuda, W, t, X, r, c) for W, X, (r, c, n) in zip(Ws, Xs, shapes)]
+    outs = [cuda.full((n, r), float("nan"), dtype=cuda.float32, device="cuda") for (r, c, n) in shapes]
+    plan = decode.Plan()
+    for i in range(3):
+        plan.add(outs[i], decode.DevWeight(Ws[i], t, *shapes[i][:2]), Xs[i], shapes[i][2])
+    plan.fork()
+    for i in (3, 4):
+        plan.add(outs[i], decode.DevWeight(Ws[i], t, *shapes[i][:2]), Xs[i], shapes[i][2])
+    plan.join()
+    plan.instantiate()
+    s = cuda.cuda.current_stream().cuda_stream
+    for rep in range(4):
+        for o in outs:
+            o.fill_(float("nan"))
+        plan.launch(s)
+        cuda.cuda.synchronize()
+        for i in range(len(shapes)):
+            assert cuda.equal(outs[i].view(cuda.int32), want[i].view(cuda.int32)), (rep, i)
+    plan.close()
+
+
 def test_many_matches_oracle_at_encoder_batch(cuda):
     """BASELINE's Q4_K 14336 x 4096 weight at 512 vectors (the verdict's encoder-size point) against the
     fp64 oracle on a row slice, within the GEMV bar."""
