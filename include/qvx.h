@@ -25,9 +25,10 @@
  *    qvx_qgemm_f16, qvx_gemm16, the many-vector form of qvx_qmatmul_n and the unfused norm route,
  *    which take stream-ordered temporaries (the converted activations, the partial tiles of a K
  *    split, or the dequantised weight) from a memory pool the library owns per device.  Each stream
- *    keeps its last temporary for its next call (no pool call between back-to-back calls), so a
- *    caller that destroys a stream must first let the qvx calls issued to it finish (synchronize the
- *    stream): a new stream may be handed the same handle.
+ *    keeps its last temporary for its next call (no pool call between back-to-back calls), and a
+ *    block of K-split tile counters (64 KiB or more, cleared once, left zero by every launch) for
+ *    the life of the process, so a caller that destroys a stream must first let the qvx calls
+ *    issued to it finish (synchronize the stream): a new stream may be handed the same handle.
  *  - Entry points ending in _host take host pointers and are synchronous: the exact calling
  *    convention of the reference's CPU operator, for a CPU-side drop-in.
  *  - Calls that overlap on one device are safe for distinct outputs; the library holds no

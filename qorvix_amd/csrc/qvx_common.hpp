@@ -163,7 +163,9 @@ inline bool lds_ready(const void* kern, LdsLimit& lim, size_t dyn) {
 // S * NA * nthr floats); the one that arrives last at the tile's counter adds them in split order
 // 0, 1, ..., S-1 into acc and returns true: it stores the tile.  The others return false and exit.
 // No workgroup waits for another.  Every split must call this (an empty K range stores zeros), and
-// the counters start at zero.  `last` is one int of LDS that no wave still reads (a word of a
+// the counters start at zero; they end at zero too (the arrival is a wrapping increment whose limit
+// is S - 1, so the last split's arrival resets the tile's counter), so a counter block that was
+// cleared once serves any number of launches in stream order.  `last` is one int of LDS that no wave still reads (a word of a
 // staging buffer once the K loop is over).
 // Visibility across the XCDs' separate L2 caches without flushing or invalidating them (a
 // device-scope fence writes back and drops the whole L2, which costs the tiles still running their
@@ -188,7 +190,7 @@ __device__ __forceinline__ bool split_k_last(float (&acc)[NA], float* __restrict
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (tid == 0)
-    *last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(S - 1);
+    *last = __builtin_amdgcn_atomic_inc32(cnt, (uint32_t)(S - 1), __ATOMIC_RELAXED, "agent") == (uint32_t)(S - 1);
   __syncthreads();
   if (!*last) return false;
   // Every partial (this split's too) is read back, so acc is free while the sum builds up in it, in

@@ -1541,6 +1541,55 @@ void gemm_temp_free(void* p, hipStream_t s) {
   (void)hipFreeAsync(p, s);
 }
 
+namespace {
+// One block of K-split tile counters per stream: made from the pool and cleared by a fill kernel in
+// stream order the first time the stream needs counters (or more of them), then kept for the life
+// of the process.  The GEMM kernels leave every counter they use at zero (split_k_last counts with a
+// wrapping increment), and launches on one stream run one after another, so the block is zero
+// whenever a launch on its stream starts and the calls need no clearing launch of their own.
+struct CntSlot {
+  int dev = -1;
+  unsigned long long sid = 0;
+  void* p = nullptr;
+  size_t n = 0;
+};
+CntSlot g_cnt_slot[kTempSlots];
+}  // namespace
+
+// At least n zeroed tile counters that the call's launches leave zero: the stream's block, or
+// nullptr under graph capture (a captured graph would then name a block that later eager calls use)
+// or when none can be had; the caller then clears counters in its own temporary.
+uint32_t* gemm_stream_counters(size_t n, hipStream_t s) {
+  hipMemPool_t pool = device_pool();
+  int dev = 0;
+  unsigned long long sid = 0;
+  if (!pool || !n || !stream_key(s, dev, sid)) return nullptr;
+  std::lock_guard<std::mutex> lk(g_slot_mu);
+  CntSlot* slot = nullptr;
+  for (auto& t : g_cnt_slot)
+    if (t.p && t.dev == dev && t.sid == sid) slot = &t;
+  if (!slot)
+    for (auto& t : g_cnt_slot)
+      if (!t.p) {
+        slot = &t;
+        break;
+      }
+  if (!slot) return nullptr;
+  if (slot->n < n) {
+    if (slot->p) (void)hipFreeAsync(slot->p, s);
+    *slot = CntSlot{};
+    const size_t m = std::max<size_t>(n, 16384);
+    void* p = nullptr;
+    if (hipMallocFromPoolAsync(&p, m * 4, pool, s) != hipSuccess) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    launch_zero(static_cast<float*>(p), m, s);
+    *slot = CntSlot{dev, sid, p, m};
+  }
+  return static_cast<uint32_t*>(slot->p);
+}
+
 // ---- per-32 Q8 activation quantiser --------------------------------------------------------------
 // One thread per block of 32 values; fp32 math as the oracle states it.
 __global__ __launch_bounds__(256) void k_quant_q8(const uint16_t* __restrict__ X, int M, int K, int8_t* __restrict__ q,
@@ -1753,16 +1802,19 @@ bool q6k8_supported(const void* w, const uint16_t* X, int K, int N) {
   return (size_t)128 * (size_t)K * 2u < (1u << 31) && (size_t)kBN * row_bytes < (1u << 31);
 }
 
+// ws: the workspace of q4k_split_bytes(p) bytes; scnt: zeroed counters to use in place of the
+// workspace's (a stream's block), or nullptr (the workspace's counters are then already zero).
 template <int VAR>
 bool launch_q6k8(float* out, const void* w, const uint16_t* X, int M, int N, int K, const Q4kPlan& p, void* ws,
-                 hipStream_t s) {
+                 uint32_t* scnt, hipStream_t s) {
   static LdsLimit lim;
   if (!lds_ready(reinterpret_cast<const void*>(&k_qgemm_q6k8<VAR>), lim, 0)) return false;
   const Q4kLaunch& L = p.l[0];
   const size_t sb = q4k_split_bytes(p);
   float* part = sb ? static_cast<float*>(ws) : nullptr;
-  uint32_t* cnt = sb ? reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(ws) + (size_t)L.ntiles * L.splits * 128 * kBN * 4)
-                     : nullptr;
+  uint32_t* cnt = !sb ? nullptr
+                 : scnt ? scnt
+                        : reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(ws) + (size_t)L.ntiles * L.splits * 128 * kBN * 4);
   if (L.splits > 1 && !ws) return false;
   Q6kGeo geo{M, N, K, (uint32_t)(K / 256) * 210u, split_per(K / 64, L.splits), 0x0F0F0F0Fu, 0x30303030u,
              0x00FF00FFu, part, cnt};
@@ -1770,15 +1822,16 @@ bool launch_q6k8(float* out, const void* w, const uint16_t* X, int M, int N, int
   return true;
 }
 
-// ws: the workspace of q4k_split_bytes(p) bytes, its counters already zero.
+// ws: the workspace of q4k_split_bytes(p) bytes; scnt as for launch_q6k8.
 template <int VAR>
 bool launch_var(float* out, const void* w, const uint16_t* X, int M, int N, int K, const Q4kPlan& p, void* ws,
-                hipStream_t s) {
+                uint32_t* scnt, hipStream_t s) {
   const size_t sb = q4k_split_bytes(p);
   float* part = sb ? static_cast<float*>(ws) : nullptr;
-  uint32_t* cnt = sb ? reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(ws) +
-                                                   (size_t)p.l[0].ntiles * p.l[0].splits * p.l[0].bm * kBN * 4)
-                     : nullptr;
+  uint32_t* cnt = !sb ? nullptr
+                 : scnt ? scnt
+                        : reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(ws) +
+                                                      (size_t)p.l[0].ntiles * p.l[0].splits * p.l[0].bm * kBN * 4);
   for (int i = 0; i < p.n; ++i)
     if (!launch_one<VAR>(out, w, X, M, N, K, p.l[i], part, cnt, s)) return false;
   return true;
@@ -1846,20 +1899,23 @@ int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M
         tmp = static_cast<uint8_t*>(gemm_ws(xbytes + sbytes, ws, ws_cap, s));
         if (!tmp) return no_mem;
       }
-      const size_t cbytes = sbytes ? (((size_t)plan.l[0].ntiles * 4 + 255) & ~(size_t)255) : 0;
-      float* cnt = sbytes ? reinterpret_cast<float*>(tmp + xbytes + sbytes - cbytes) : nullptr;
+      // the K split's counters: the stream's zeroed block for calls that may allocate, else the
+      // temporary's, cleared by the bf16 prepass or a zero kernel
+      uint32_t* scnt = sbytes && !ws ? gemm_stream_counters((size_t)plan.l[0].ntiles, s) : nullptr;
+      const size_t cbytes = sbytes && !scnt ? (((size_t)plan.l[0].ntiles * 4 + 255) & ~(size_t)255) : 0;
+      float* cnt = cbytes ? reinterpret_cast<float*>(tmp + xbytes + sbytes - cbytes) : nullptr;
       const uint16_t* Xg = X;
       if (variant == VAR_BF16) {
         k_f16_to_bf16<<<(unsigned)((n / 8 + 255) / 256), 256, 0, s>>>(
             reinterpret_cast<const uint4*>(X), reinterpret_cast<uint4*>(tmp), n / 8, reinterpret_cast<float4*>(cnt),
             cbytes / 16);
         Xg = reinterpret_cast<const uint16_t*>(tmp);
-      } else if (sbytes) {
+      } else if (cbytes) {
         launch_zero(cnt, cbytes / 4, s);
       }
-      const bool ok = variant == VAR_BF16
-                          ? launch_q6k8<VAR_BF16>(out, w, Xg, M, rows, cols, plan, sbytes ? tmp + xbytes : nullptr, s)
-                          : launch_q6k8<VAR_F16>(out, w, Xg, M, rows, cols, plan, sbytes ? tmp + xbytes : nullptr, s);
+      void* sws = sbytes ? tmp + xbytes : nullptr;
+      const bool ok = variant == VAR_BF16 ? launch_q6k8<VAR_BF16>(out, w, Xg, M, rows, cols, plan, sws, scnt, s)
+                                          : launch_q6k8<VAR_F16>(out, w, Xg, M, rows, cols, plan, sws, scnt, s);
       if (tmp) gemm_ws_release(tmp, ws, s);
       return ok ? 0 : -5;
     }
@@ -1915,19 +1971,22 @@ int launch_qgemm(float* out, const void* w, uint32_t t, const uint16_t* X, int M
       if (!tmp) return no_mem;
     }
     uint8_t* split_ws = static_cast<uint8_t*>(tmp) + xbytes;
-    const size_t cbytes = sbytes ? (((size_t)plan.l[0].ntiles * 4 + 255) & ~(size_t)255) : 0;
-    float* cnt = sbytes ? reinterpret_cast<float*>(split_ws + sbytes - cbytes) : nullptr;
+    // the K split's counters: the stream's zeroed block for calls that may allocate, else the
+    // temporary's, cleared by the bf16 prepass or a zero kernel
+    uint32_t* scnt = sbytes && !ws ? gemm_stream_counters((size_t)plan.l[0].ntiles, s) : nullptr;
+    const size_t cbytes = sbytes && !scnt ? (((size_t)plan.l[0].ntiles * 4 + 255) & ~(size_t)255) : 0;
+    float* cnt = cbytes ? reinterpret_cast<float*>(split_ws + sbytes - cbytes) : nullptr;
     const size_t ncnt4 = cbytes / 16;
     const uint16_t* Xg = X;
     if (variant == VAR_BF16) {
       k_f16_to_bf16<<<(unsigned)((n / 8 + 255) / 256), 256, 0, s>>>(
           reinterpret_cast<const uint4*>(X), static_cast<uint4*>(tmp), n / 8, reinterpret_cast<float4*>(cnt), ncnt4);
       Xg = static_cast<const uint16_t*>(tmp);
-    } else if (sbytes) {
+    } else if (cbytes) {
       launch_zero(cnt, ncnt4 * 4, s);
     }
-    const bool ok = variant == VAR_BF16 ? launch_var<VAR_BF16>(out, w, Xg, M, rows, cols, plan, split_ws, s)
-                                        : launch_var<VAR_F16>(out, w, Xg, M, rows, cols, plan, split_ws, s);
+    const bool ok = variant == VAR_BF16 ? launch_var<VAR_BF16>(out, w, Xg, M, rows, cols, plan, split_ws, scnt, s)
+                                        : launch_var<VAR_F16>(out, w, Xg, M, rows, cols, plan, split_ws, scnt, s);
     if (tmp) gemm_ws_release(tmp, ws, s);
     return ok ? 0 : -5;
   }

@@ -605,9 +605,10 @@ size_t gemm16_split_bytes(const G16Plan& pl, size_t* cbytes) {
 }
 
 // Launches the GEMM of plan pl; split_ws: gemm16_split_bytes(pl) bytes, counters (its last cbytes)
-// zero.  X and B rows are K 16-bit values (K % 64 == 0), both 16-byte aligned.
+// zero, or scnt: zeroed counters to use in place of those (a stream's block).  X and B rows are K
+// 16-bit values (K % 64 == 0), both 16-byte aligned.
 bool launch_gemm16(const G16Plan& pl, float* out, int ldy, const uint16_t* X, const uint16_t* B, int M, int N, int K,
-                   bool bf16, void* split_ws, hipStream_t s) {
+                   bool bf16, void* split_ws, hipStream_t s, uint32_t* scnt = nullptr) {
   size_t cb = 0;
   const size_t sb = gemm16_split_bytes(pl, &cb);
   if (sb && !split_ws) return false;
@@ -616,7 +617,7 @@ bool launch_gemm16(const G16Plan& pl, float* out, int ldy, const uint16_t* X, co
     const int r0 = p.col0 * kBN, nr = std::min(N - r0, p.ncols * kBN);
     if (nr <= 0) continue;
     Geo geo{M, nr, K, ldy, p.mt, p.per, sb ? static_cast<float*>(split_ws) : nullptr,
-            sb ? reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(split_ws) + sb - cb) : nullptr};
+            !sb ? nullptr : scnt ? scnt : reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(split_ws) + sb - cb)};
     const uint16_t* Bp = B + (size_t)r0 * K;
     float* op = out + r0;
     const dim3 grid((unsigned)p.ntiles, 1, (unsigned)p.splits);
@@ -643,6 +644,7 @@ void launch_zero16(void* p, size_t bytes, hipStream_t s) {
 bool launch_dequant16(uint32_t t, const void* src, uint16_t* dst, size_t n, bool bf16, hipStream_t s);
 void* gemm_temp_alloc(size_t bytes, hipStream_t s);
 void gemm_temp_free(void* p, hipStream_t s);
+uint32_t* gemm_stream_counters(size_t n, hipStream_t s);
 
 // Plain 16-bit GEMM entry (qvx_gemm16): out [M, N] = X [M, K] . B [N, K]^T, both operands bf16 or fp16.
 // Temporaries (padded copies when K % 64 != 0 or an operand is not 16-byte aligned, a K split's
@@ -675,8 +677,10 @@ int launch_gemm16_entry(float* out, const uint16_t* X, const uint16_t* B, int M,
     k_pad_rows16<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(B, reinterpret_cast<uint16_t*>(tmp + xb), N, K, Kp);
     Bg = reinterpret_cast<const uint16_t*>(tmp + xb);
   }
-  if (sb) launch_zero16(tmp + xb + bb + sb - cb, cb, s);
-  const bool ok = launch_gemm16(p, out, N, Xg, Bg, M, N, Kp, bf16, sb ? tmp + xb + bb : nullptr, s);
+  // the K split's counters: the stream's zeroed block, else the temporary's, cleared here
+  uint32_t* scnt = sb ? gemm_stream_counters((size_t)p.p[0].ntiles, s) : nullptr;
+  if (sb && !scnt) launch_zero16(tmp + xb + bb + sb - cb, cb, s);
+  const bool ok = launch_gemm16(p, out, N, Xg, Bg, M, N, Kp, bf16, sb ? tmp + xb + bb : nullptr, s, scnt);
   if (tmp) gemm_temp_free(tmp, s);
   return ok ? 0 : -5;
 }
@@ -765,8 +769,11 @@ int launch_qgemm_via16(float* out, const void* w, uint32_t t, const uint16_t* X,
       break;
     }
     uint8_t* split_ws = sb ? tmp + xb + wb + ub : nullptr;
-    if (sb) launch_zero16(split_ws + sb - cb, cb, s);
-    if (!launch_gemm16(plan, out + r0, rows, Xg, wd, M, pr, Kp, bf16, split_ws, s)) rc = -5;
+    // the K split's counters: the stream's zeroed block for calls that may allocate, else the
+    // region's, cleared here
+    uint32_t* scnt = sb && !ws ? gemm_stream_counters((size_t)plan.p[0].ntiles, s) : nullptr;
+    if (sb && !scnt) launch_zero16(split_ws + sb - cb, cb, s);
+    if (!launch_gemm16(plan, out + r0, rows, Xg, wd, M, pr, Kp, bf16, split_ws, s, scnt)) rc = -5;
   }
   if (!ws) gemm_temp_free(tmp, s);
   return rc;

@@ -552,6 +552,50 @@ def test_gemm_split_k_concurrent_streams(cuda, t):
             np.testing.assert_array_equal(outs[i][k].cpu().numpy().view(np.uint32), alone[i].view(np.uint32))
 
 
+def test_gemm_split_k_counters_reused_across_calls(cuda):
+    """Calls that may allocate take their K split's tile counters from a block the stream keeps,
+    cleared once: every launch leaves the counters it used at zero.  K-split calls of different
+    tile counts and kernels (the Q4_K and Q6_K raw-block GEMMs, the 16-bit GEMM behind Q8_0 / Q4_0),
+    fp16 and bf16, interleaved on one stream for three rounds and then on a new stream, give the
+    first round's bits every time (a counter left non-zero would make a later tile's last split
+    skip its sum, or sum too early)."""
+    cases = [(qvx.Q4_K, qvx.GEMM_F16, 128, 14336, 4096), (qvx.Q6_K, qvx.GEMM_F16, 300, 4096, 14336),
+             (qvx.Q4_K, qvx.GEMM_BF16, 37, 2048, 4096), (qvx.Q8_0, qvx.GEMM_BF16, 128, 4096, 4096),
+             (qvx.Q4_K, qvx.GEMM_F16, 200, 1024, 4096), (qvx.Q6_K, qvx.GEMM_BF16, 128, 1024, 4096),
+             (qvx.Q4_0, qvx.GEMM_F16, 96, 4096, 11008)]
+    lib = qvx.lib()
+    data = []
+    for i, (t, variant, M, rows, cols) in enumerate(cases):
+        W = qvx.empty_weight(t, rows, cols)
+        qvx.fill_synthetic_t(W, t, rows, cols, seed=90 + i, scale_mul=1e-3)
+        X = cuda.empty((M, cols), dtype=cuda.float16, device="cuda")
+        qvx.fill_normal_t(X, seed=95 + i, mul=0.5)
+        data.append((W, X))
+    assert qvx.qgemm_plan_q4k(128, 14336, 4096)[0]["splits"] > 1  # the premise: these calls split K
+    cuda.cuda.synchronize()
+
+    def round_on(stream):
+        outs = []
+        for (t, variant, M, rows, cols), (W, X) in zip(cases, data):
+            Y = cuda.full((M, rows), float("nan"), dtype=cuda.float32, device="cuda")
+            assert lib.qvx_qgemm_f16(Y.data_ptr(), W.data_ptr(), t, X.data_ptr(), M, rows, cols, variant,
+                                     stream.cuda_stream) == qvx.OK
+            outs.append(Y)
+        stream.synchronize()
+        return [o.cpu().numpy() for o in outs]
+
+    cur = cuda.cuda.current_stream()
+    first = round_on(cur)
+    for r in range(2):
+        for i, got in enumerate(round_on(cur)):
+            np.testing.assert_array_equal(got.view(np.uint32), first[i].view(np.uint32), err_msg=f"round {r} case {i}")
+    fresh = cuda.cuda.Stream()
+    for i, got in enumerate(round_on(fresh)):
+        np.testing.assert_array_equal(got.view(np.uint32), first[i].view(np.uint32), err_msg=f"new stream case {i}")
+    for i, (t, variant, M, rows, cols) in enumerate(cases):
+        assert np.isfinite(first[i]).all(), i
+
+
 GROUP_CASES = [
     # the decoder's q / k / v (Q6_K v) and gate / up of Llama-3-8B
     ("qkv", 4096, [(qvx.Q4_K, 4096), (qvx.Q4_K, 1024), (qvx.Q6_K, 1024)]),
