@@ -277,14 +277,15 @@ constexpr int kWideElems = 8192;  // elements per workgroup of the wide 16-bit d
 // this size) are copied from a 16-byte-aligned source into LDS with 16-byte loads (the tensor's last
 // bytes one at a time), then each thread decodes eight consecutive elements per round, four rounds,
 // and stores them as one 16-byte vector (a wave stores 1 KiB contiguous).  n: whole blocks.
+// The body for workgroup wg (the standalone kernel passes blockIdx.x).
 template <uint32_t T, int QK, int BB, bool BF>
-__global__ __launch_bounds__(256) void k_dequant16_wide(const uint8_t* __restrict__ src, uint4* __restrict__ dst,
-                                                        size_t n) {
+__device__ __forceinline__ void dequant16_wide_body(const uint8_t* __restrict__ src, uint4* __restrict__ dst, size_t n,
+                                                    unsigned wg) {
   constexpr int kBytes = kWideElems / QK * BB;
   static_assert(kWideElems % QK == 0 && kBytes % 16 == 0, "workgroup span must be whole blocks and 16-byte units");
   __shared__ __attribute__((aligned(16))) uint32_t sm[kBytes / 4 + 4];
   const int tid = threadIdx.x;
-  const size_t b0 = (size_t)blockIdx.x * kBytes;
+  const size_t b0 = (size_t)wg * kBytes;
   const size_t avail = min((size_t)kBytes, n / QK * BB - b0);
   const uint4* g16 = reinterpret_cast<const uint4*>(src + b0);
   for (int k = tid; k < (int)(avail / 16); k += 256) reinterpret_cast<uint4*>(sm)[k] = g16[k];
@@ -295,7 +296,7 @@ __global__ __launch_bounds__(256) void k_dequant16_wide(const uint8_t* __restric
 #pragma unroll
   for (int r = 0; r < kWideElems / 2048; ++r) {
     const int e0 = r * 2048 + 8 * tid;
-    const size_t i = (size_t)blockIdx.x * kWideElems + e0;
+    const size_t i = (size_t)wg * kWideElems + e0;
     if (i >= n) break;
     float v[8];
     deq8<T>(sb + (e0 / QK) * BB, e0 % QK, v);
@@ -310,6 +311,36 @@ __global__ __launch_bounds__(256) void k_dequant16_wide(const uint8_t* __restric
   }
 }
 
+template <uint32_t T, int QK, int BB, bool BF>
+__global__ __launch_bounds__(256) void k_dequant16_wide(const uint8_t* __restrict__ src, uint4* __restrict__ dst,
+                                                        size_t n) {
+  dequant16_wide_body<T, QK, BB, BF>(src, dst, n, blockIdx.x);
+}
+
+// The wide dequantiser (bf16) and the bf16 rounding of the GEMM's fp16 activations in one launch:
+// workgroups [0, nwg) take the weight as k_dequant16_wide does, the rest convert x (n8 groups of
+// 8 values, four groups a thread in a grid-stride loop) as the 16-bit GEMM's own prepass does
+// (round to nearest even, NaN kept quiet), so the two memory-bound passes share one launch.
+template <uint32_t T, int QK, int BB>
+__global__ __launch_bounds__(256) void k_dequant16_wide_x(const uint8_t* __restrict__ src, uint4* __restrict__ dst,
+                                                          size_t n, unsigned nwg, const uint4* __restrict__ x,
+                                                          uint4* __restrict__ xo, size_t n8) {
+  if (blockIdx.x < nwg) {
+    dequant16_wide_body<T, QK, BB, true>(src, dst, n, blockIdx.x);
+    return;
+  }
+  auto cv = [](uint32_t w) {
+    const uint32_t lo = to_bf16((float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xFFFFu)));
+    const uint32_t hi = to_bf16((float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16)));
+    return lo | (hi << 16);
+  };
+  const size_t stride = (size_t)(gridDim.x - nwg) * 256;
+  for (size_t i = (size_t)(blockIdx.x - nwg) * 256 + threadIdx.x; i < n8; i += stride) {
+    const uint4 v = x[i];
+    xo[i] = make_uint4(cv(v.x), cv(v.y), cv(v.z), cv(v.w));
+  }
+}
+
 template <bool BF>
 bool launch_dequant16_wide(uint32_t t, const uint8_t* b, uint4* d8, size_t n, hipStream_t s) {
   const unsigned grid = (unsigned)((n + kWideElems - 1) / kWideElems);
@@ -320,6 +351,32 @@ bool launch_dequant16_wide(uint32_t t, const uint8_t* b, uint4* d8, size_t n, hi
     case T_Q4_K: k_dequant16_wide<T_Q4_K, 256, 144, BF><<<grid, 256, 0, s>>>(b, d8, n); return true;
     case T_Q5_K: k_dequant16_wide<T_Q5_K, 256, 176, BF><<<grid, 256, 0, s>>>(b, d8, n); return true;
     case T_Q6_K: k_dequant16_wide<T_Q6_K, 256, 210, BF><<<grid, 256, 0, s>>>(b, d8, n); return true;
+    default: return false;
+  }
+}
+
+// The weight of n elements to bf16 and x (n8 groups of 8 fp16 values, 16-byte aligned) to bf16 in
+// one launch; false, having launched nothing, where the wide kernel does not take the weight.
+bool launch_dequant16_bf16_x(uint32_t t, const void* src, uint16_t* dst, size_t n, const uint16_t* x, uint16_t* xo,
+                             size_t n8, hipStream_t s) {
+  const size_t qk = (t == T_Q4_K || t == T_Q5_K || t == T_Q6_K) ? 256 : 32;
+  if (n == 0 || n % qk != 0 || (reinterpret_cast<uintptr_t>(src) & 15u) || (reinterpret_cast<uintptr_t>(dst) & 15u) ||
+      (reinterpret_cast<uintptr_t>(x) & 15u) || (reinterpret_cast<uintptr_t>(xo) & 15u))
+    return false;
+  const unsigned nwg = (unsigned)((n + kWideElems - 1) / kWideElems);
+  const unsigned nx = (unsigned)std::min<size_t>((n8 + 1023) / 1024, 4096);
+  const dim3 grid(nwg + nx);
+  const auto* b = static_cast<const uint8_t*>(src);
+  auto* d8 = reinterpret_cast<uint4*>(dst);
+  const auto* x8 = reinterpret_cast<const uint4*>(x);
+  auto* o8 = reinterpret_cast<uint4*>(xo);
+  switch (t) {
+    case T_Q8_0: k_dequant16_wide_x<T_Q8_0, 32, 34><<<grid, 256, 0, s>>>(b, d8, n, nwg, x8, o8, n8); return true;
+    case T_Q4_0: k_dequant16_wide_x<T_Q4_0, 32, 18><<<grid, 256, 0, s>>>(b, d8, n, nwg, x8, o8, n8); return true;
+    case T_Q5_0: k_dequant16_wide_x<T_Q5_0, 32, 22><<<grid, 256, 0, s>>>(b, d8, n, nwg, x8, o8, n8); return true;
+    case T_Q4_K: k_dequant16_wide_x<T_Q4_K, 256, 144><<<grid, 256, 0, s>>>(b, d8, n, nwg, x8, o8, n8); return true;
+    case T_Q5_K: k_dequant16_wide_x<T_Q5_K, 256, 176><<<grid, 256, 0, s>>>(b, d8, n, nwg, x8, o8, n8); return true;
+    case T_Q6_K: k_dequant16_wide_x<T_Q6_K, 256, 210><<<grid, 256, 0, s>>>(b, d8, n, nwg, x8, o8, n8); return true;
     default: return false;
   }
 }

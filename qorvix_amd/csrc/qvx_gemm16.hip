@@ -642,6 +642,8 @@ void launch_zero16(void* p, size_t bytes, hipStream_t s) {
 }
 
 bool launch_dequant16(uint32_t t, const void* src, uint16_t* dst, size_t n, bool bf16, hipStream_t s);
+bool launch_dequant16_bf16_x(uint32_t t, const void* src, uint16_t* dst, size_t n, const uint16_t* x, uint16_t* xo,
+                             size_t n8, hipStream_t s);
 void* gemm_temp_alloc(size_t bytes, hipStream_t s);
 void gemm_temp_free(void* p, hipStream_t s);
 uint32_t* gemm_stream_counters(size_t n, hipStream_t s);
@@ -735,14 +737,20 @@ int launch_qgemm_via16(float* out, const void* w, uint32_t t, const uint16_t* X,
   if (!tmp) return -5;
   const uint16_t* Xg = X;
   uint16_t* xc = reinterpret_cast<uint16_t*>(tmp);
+  // bf16 X without padding: rounded in the first panel's dequantisation launch when the wide
+  // dequantiser takes that panel (one memory-bound launch instead of two), else by its own prepass
+  bool x_pending = false;
+  const size_t xn8 = (size_t)M * cols / 8;
+  auto x_prepass = [&]() {
+    k_x_to_bf16<<<(unsigned)((xn8 + 255) / 256), 256, 0, s>>>(reinterpret_cast<const uint4*>(X),
+                                                               reinterpret_cast<uint4*>(xc), xn8, nullptr, 0);
+  };
   if (padx) {
     const size_t n = (size_t)M * Kp;
     k_pad_x16<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(X, xc, M, cols, Kp, bf16 ? 1 : 0);
     Xg = xc;
   } else if (bf16) {
-    const size_t n8 = (size_t)M * cols / 8;
-    k_x_to_bf16<<<(unsigned)((n8 + 255) / 256), 256, 0, s>>>(reinterpret_cast<const uint4*>(X),
-                                                              reinterpret_cast<uint4*>(xc), n8, nullptr, 0);
+    x_pending = true;
     Xg = xc;
   }
   uint16_t* wd = reinterpret_cast<uint16_t*>(tmp + xb);
@@ -764,9 +772,17 @@ int launch_qgemm_via16(float* out, const void* w, uint32_t t, const uint16_t* X,
       }
       const size_t n = (size_t)pr * Kp;
       k_pad_rows16<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(u, wd, pr, cols, Kp);
-    } else if (!launch_dequant16(t, wsrc, wd, (size_t)pr * cols, bf16, s)) {
-      rc = -1;
-      break;
+    } else if (x_pending && launch_dequant16_bf16_x(t, wsrc, wd, (size_t)pr * cols, X, xc, xn8, s)) {
+      x_pending = false;
+    } else {
+      if (x_pending) {
+        x_prepass();
+        x_pending = false;
+      }
+      if (!launch_dequant16(t, wsrc, wd, (size_t)pr * cols, bf16, s)) {
+        rc = -1;
+        break;
+      }
     }
     uint8_t* split_ws = sb ? tmp + xb + wb + ub : nullptr;
     // the K split's counters: the stream's zeroed block for calls that may allocate, else the

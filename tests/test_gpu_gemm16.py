@@ -165,3 +165,34 @@ def test_dequantize16_scale_edge_values(cuda, bf16):
         with np.errstate(over="ignore"):
             want, _ = _bits16(oracle.dequantize(t, w, n).astype(np.float32), bf16)
         np.testing.assert_array_equal(got, want, err_msg=f"type {t}")
+
+
+@pytest.mark.parametrize("t,rows,cols,M", [(qvx.Q8_0, 4096, 4096, 512), (qvx.Q4_0, 1024, 11008, 300),
+                                           (qvx.Q5_K, 2048, 4096, 64), (qvx.Q8_0, 256, 4128, 40)])
+def test_prefill_via16_bf16_is_its_composition(cuda, t, rows, cols, M):
+    """The bf16 prefill route for these types rounds X to bf16 in the same launch that dequantises the
+    weight (K a multiple of 64; the padded case 4128 takes its own prepass) and then runs the plain
+    16-bit GEMM: its output equals, bit for bit, qvx_dequantize16's bf16 weight times X rounded to
+    bf16 (to nearest even) through qvx_gemm16.  X carries +-Inf, NaN, a subnormal, fp16's largest
+    value and -0 in its first row."""
+    W = qvx.empty_weight(t, rows, cols)
+    qvx.fill_synthetic_t(W, t, rows, cols, seed=400 + t + M, scale_mul=1e-3)
+    X = cuda.empty((M, cols), dtype=cuda.float16, device="cuda")
+    qvx.fill_normal_t(X, seed=401 + t + M, mul=0.5)
+    X[0, :8] = cuda.tensor([float("inf"), -float("inf"), float("nan"), 6.0e-8, 65504.0, -0.0, 1 / 3, -2.5e-5],
+                           dtype=cuda.float16, device="cuda")
+    cuda.cuda.synchronize()
+    got = qvx.qgemm_t(W, t, X, rows, cols, qvx.GEMM_BF16)
+    B = qvx.dequantize16_t(W, t, rows * cols, True)
+    xb, _ = _bits16(X.cpu().numpy().astype(np.float32), True)  # fp16 NaN -> 0x7FC0, as the kernel keeps it
+    Xb = cuda.from_numpy(xb.view(np.int16)).cuda()
+    ref = cuda.full((M, rows), float("nan"), dtype=cuda.float32, device="cuda")
+    if cols % 64 == 0:
+        rc = qvx.lib().qvx_gemm16(ref.data_ptr(), Xb.data_ptr(), B.data_ptr(), M, rows, cols, qvx.GEMM_BF16,
+                                  cuda.cuda.current_stream().cuda_stream)
+        assert rc == qvx.OK, qvx.strerror(rc)
+        cuda.cuda.synchronize()
+        np.testing.assert_array_equal(got.cpu().numpy(), ref.cpu().numpy())
+    g = got.cpu().numpy()
+    assert not np.isfinite(g[0]).any()  # the Inf / NaN activations reach every output of row 0
+    assert np.isfinite(g[1:]).all()
