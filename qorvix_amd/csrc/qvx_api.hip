@@ -227,12 +227,31 @@ inline bool q4s_batch(int nvec, int rows, int cols) {
   return (cols >= 8192 && nvec >= 5) || ((int64_t)rows * cols <= ((int64_t)4 << 20) && nvec >= 12);
 }
 
+// Q6_K batches with the RMSNorm prologue: the standalone norm (the engine's canonical sum of squares
+// and x * scale * w, so the normalised activations are the bits the VALU kernel folds in) into the
+// workspace, then the batched form on them -- where the extra norm launch pays: on weights of >= 8192
+// rows or columns wherever the batched form takes the call, on smaller ones from 6 vectors (below
+// that the VALU kernel's launches with the norm folded in are as fast).
+inline size_t ws_align(size_t n) { return (n + 255) & ~size_t(255); }
+inline bool q6_norm_batched(int nvec, int rows, int cols) {
+  return q6_batched(nvec, rows, cols) && (nvec >= 6 || rows >= 8192 || cols >= 8192);
+}
+
 // The forms that take a workspace, and the bytes of the one a call takes (0: none).
-enum WsForm { WS_NONE, WS_MANY, WS_Q4S, WS_Q6S };
+enum WsForm { WS_NONE, WS_MANY, WS_Q4S, WS_Q6S, WS_Q6S_NORM };
 inline WsForm ws_route(uint32_t type, int nvec, int rows, int cols, size_t row_bytes, bool fast, const GemvEpi& epi,
                        size_t* bytes) {
   *bytes = 0;
-  if (!fast || epi.flags() || rows <= 0 || cols <= 0) return WS_NONE;
+  if (!fast || rows <= 0 || cols <= 0) return WS_NONE;
+  if (epi.flags()) {
+    if (type == T_Q6_K && epi.flags() == EPI_NORM && q6_norm_batched(nvec, rows, cols) &&
+        gemv_fast_fusable(type, cols, row_bytes, epi) && gemv_q6s_route(nvec, rows, cols, row_bytes, bytes)) {
+      *bytes += ws_align((size_t)nvec * (size_t)cols * sizeof(float));
+      return WS_Q6S_NORM;
+    }
+    *bytes = 0;
+    return WS_NONE;
+  }
   if (type == T_Q4_K) {
     if (q4s_batch(nvec, rows, cols) && gemv_q4s_route(nvec, rows, cols, row_bytes, bytes)) return WS_Q4S;
     if (many_batch(nvec, rows, cols) && gemv_many_supported(cols, row_bytes)) {
@@ -280,18 +299,27 @@ int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int
   //  * smaller Q4_K batches (q4s_batch): the K ranges split over workgroups (k_gemv_q4s), bit-identical
   //    per vector to the one-vector kernel, the bias added in its sum launch;
   //  * Q6_K batches (q6_batched): the matrix-core form with the K range split over workgroups
-  //    (k_gemv_q6s), bit-identical per vector to the VALU kernel; a bias is added after.
+  //    (k_gemv_q6s), bit-identical per vector to the VALU kernel; a bias is added after;
+  //  * Q6_K batches with the RMSNorm prologue (q6_norm_batched): the standalone norm into the
+  //    workspace, then that form on the normalised activations.
   size_t need = 0;
   if (const WsForm form = ws_route(type, nvec, rows, cols, row_bytes, fast, epi, &need); form != WS_NONE) {
     const bool own = epi.ws && epi.ws_bytes >= need;
     void* ws = own ? epi.ws : epi.no_alloc ? nullptr : gemm_temp_alloc(need, s);
     if (ws) {
-      const bool ok = form == WS_MANY ? launch_gemv_q4k_many(w, X, out, epi.bias, nvec, rows, cols, row_bytes, ws, s)
-                      : form == WS_Q4S ? launch_gemv_q4s(w, X, out, epi.bias, nvec, rows, cols, row_bytes, ws, s)
-                                       : launch_gemv_q6s(w, X, out, nvec, rows, cols, row_bytes, ws, s,
-                                                         own && epi.cnt_n >= gemv_q6s_counters(nvec, rows, cols)
-                                                             ? epi.cnt
-                                                             : nullptr);
+      uint32_t* cnt = own && epi.cnt_n >= gemv_q6s_counters(nvec, rows, cols) ? epi.cnt : nullptr;
+      bool ok;
+      if (form == WS_Q6S_NORM) {  // the normalised activations first, the block sums after them
+        const size_t xb = ws_align((size_t)nvec * (size_t)cols * sizeof(float));
+        auto* xn = static_cast<float*>(ws);
+        launch_rmsnorm(xn, X, epi.norm_w, epi.eps, nvec, cols, s);
+        ok = launch_gemv_q6s(w, xn, out, nvec, rows, cols, row_bytes, need > xb ? static_cast<uint8_t*>(ws) + xb : nullptr,
+                             s, cnt);
+      } else {
+        ok = form == WS_MANY ? launch_gemv_q4k_many(w, X, out, epi.bias, nvec, rows, cols, row_bytes, ws, s)
+             : form == WS_Q4S ? launch_gemv_q4s(w, X, out, epi.bias, nvec, rows, cols, row_bytes, ws, s)
+                              : launch_gemv_q6s(w, X, out, nvec, rows, cols, row_bytes, ws, s, cnt);
+      }
       if (!own) gemm_temp_free(ws, s);
       if (!ok) return refused();
       if (form == WS_Q6S && epi.bias) launch_add_bias(out, epi.bias, nvec, rows, s);
@@ -797,7 +825,7 @@ static size_t plan_ws_layout(qvx_plan& plan) {
       c.ws_off = off;
       c.ws_bytes = need;
       off += (need + 255) & ~(size_t)255;
-      if (form == WS_Q6S) c.cnt_n = gemv_q6s_counters(c.nvec, c.rows, c.cols);
+      if (form == WS_Q6S || form == WS_Q6S_NORM) c.cnt_n = gemv_q6s_counters(c.nvec, c.rows, c.cols);
     }
     if (off > total) total = off;
     i += n;

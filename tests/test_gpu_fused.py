@@ -125,6 +125,46 @@ def test_qmatmul_rmsnorm_batches_bit_identical(cuda, t, rows, cols):
         np.testing.assert_array_equal(got.view(np.uint32), single[:n].view(np.uint32))
 
 
+@pytest.mark.parametrize("rows,cols", [(1024, 4096), (8200, 2048), (70000, 2048)])
+def test_q6k_norm_batches_on_the_batched_form(cuda, rows, cols):
+    """Q6_K batches with the RMSNorm prologue that the batched matrix-core form takes (the standalone
+    norm into a temporary, then k_gemv_q6s: from 6 vectors on small weights, from 3 or 4 on weights of
+    >= 8192 rows or columns, pairs on >= 65536 rows) equal the one-vector fused call (the VALU kernel
+    folding the norm in) bit for bit, eagerly and replayed from a plan, whose workspace then holds
+    the normalised activations and the block sums."""
+    import ctypes as C
+    t = qvx.Q6_K
+    W = _weight(cuda, t, rows, cols, seed=rows + 3)
+    X = _x(cuda, 8, cols, seed=8, mul=2.0)
+    nw = _normw(cuda, cols, 9)
+    single = np.stack([qvx.qmatmul_rmsnorm_t(W, t, X[v], nw, EPS, rows, cols).cpu().numpy() for v in range(8)])
+    for n in (2, 3, 4, 6, 8):
+        got = qvx.qmatmul_rmsnorm_t(W, t, X[:n].contiguous(), nw, EPS, rows, cols).cpu().numpy()
+        np.testing.assert_array_equal(got.view(np.uint32), single[:n].view(np.uint32), err_msg=f"n={n}")
+    lib = qvx.lib()
+    out = cuda.full((8, rows), float("nan"), dtype=cuda.float32, device="cuda")
+    plan = C.c_void_p()
+    assert lib.qvx_plan_create(C.byref(plan)) == qvx.OK
+    try:
+        assert lib.qvx_plan_add_qmatmul_n_rmsnorm(plan, out.data_ptr(), W.data_ptr(), t, X.data_ptr(), nw.data_ptr(),
+                                                  EPS, 8, rows, cols) == qvx.OK
+        assert lib.qvx_plan_instantiate(plan) == qvx.OK
+        s = cuda.cuda.current_stream().cuda_stream
+        for rep in range(3):
+            out.fill_(float("nan"))
+            assert lib.qvx_plan_launch(plan, s) == qvx.OK
+            cuda.cuda.synchronize()
+            np.testing.assert_array_equal(out.cpu().numpy().view(np.uint32), single.view(np.uint32), err_msg=f"rep {rep}")
+    finally:
+        lib.qvx_plan_destroy(plan)
+    xn = oracle.rmsnorm(X[:2].cpu().numpy(), nw.cpu().numpy(), EPS)
+    idx = np.union1d(np.arange(0, rows, 97), [rows - 1])
+    rb = qvx.row_bytes(t, cols)
+    wsl = W.cpu().numpy().reshape(rows, rb)[idx].reshape(-1)
+    ref = oracle.matmul_f64(wsl, t, xn.astype(np.float32), 2, len(idx), cols)
+    assert max_rel(single[:2][:, idx], ref) <= GEMV_TOL
+
+
 def test_qmatmul_rmsnorm_checks(cuda):
     W = _weight(cuda, qvx.Q4_K, 64, 512, 1)
     X = _x(cuda, 1, 512, 2)
