@@ -171,8 +171,12 @@ int qvx_qmatmul_group(float* const* d_out, const void* const* d_w, const uint32_
  * qvx_qmatmul_n plus d_norm_w [cols] (NULL -> QVX_E_NULL; cols > 16384 -> QVX_E_RANGE).  Where the GEMV kernel takes the shape
  * (Q4_K and the integer-dot formats, cols a multiple of 512 up to 16384, aligned operands) the norm
  * is folded into the kernel's activation conversion: one launch, no temporary; the per-vector
- * arithmetic does not depend on n_vec, so batches are bit-identical to single vectors.  Otherwise a
- * standalone norm into a stream-ordered temporary, then qvx_qmatmul_n. */
+ * arithmetic does not depend on n_vec, so batches are bit-identical to single vectors.  Q6_K
+ * batches the batched matrix-core form takes (cols a multiple of 2048; weights of >= 8192 rows or
+ * columns, or 6 vectors or more) run the standalone norm into a stream-ordered temporary (n_vec *
+ * cols * 4 bytes beside the form's block sums) and then that form: the norm forms the same bits as
+ * the folded one, so these batches are bit-identical to single vectors too.  Otherwise a standalone
+ * norm into a stream-ordered temporary, then qvx_qmatmul_n. */
 int qvx_qmatmul_n_rmsnorm(float* d_out, const void* d_w, uint32_t type, const float* d_X,
                           const float* d_norm_w, float eps, int n_vec, int rows, int cols, void* stream);
 /* out[v, i] = silu(g[v, i]) * u[v, i], g = W_gate . xn[v], u = W_up . xn[v], xn = rmsnorm(x[v])
@@ -293,8 +297,8 @@ int qvx_plan_add_qmatmul_group(qvx_plan* plan, float* const* d_out, const void* 
                                const int* rows, int n, const float* d_x, const float* d_norm_w, float eps,
                                int cols);
 /* Append a fused call (the arguments and checks of qvx_qmatmul_n_rmsnorm / qvx_qmatmul_swiglu).  A
- * replay allocates nothing, so only calls a kernel folds the norm / SwiGLU into are accepted
- * (others -> QVX_E_SHAPE). */
+ * replay allocates nothing, so only calls a kernel folds the norm / SwiGLU into, or whose norm the
+ * plan's workspace holds (the Q6_K batches above), are accepted (others -> QVX_E_SHAPE). */
 int qvx_plan_add_qmatmul_n_rmsnorm(qvx_plan* plan, float* d_out, const void* d_w, uint32_t type,
                                    const float* d_X, const float* d_norm_w, float eps, int n_vec,
                                    int rows, int cols);
