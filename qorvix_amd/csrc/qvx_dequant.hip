@@ -28,6 +28,81 @@ __global__ __launch_bounds__(256) void k_copy_f32(const uint32_t* __restrict__ s
   if (i < n) dst[i] = src[i];
 }
 
+// Eight consecutive elements e0 .. e0 + 7 (e0 % 8 == 0) of one block in LDS, decoded with the block's
+// header read once: they always share one scale (Q8_0 / Q4_0: the block's, Q4_K: one 32-element
+// sub-block's, Q6_K: one 16-element scale group's).  Same formulas and operand order as deq_elem; the
+// fp16 scales are converted by the hardware (exact for every finite value, subnormals included).
+__device__ inline uint32_t lds_u32_at(const uint8_t* p) {  // 4 bytes at any address, from aligned dwords
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(a & ~(uintptr_t)3);
+  return align_bytes(w[1], w[0], (uint32_t)(a & 3));
+}
+__device__ inline float f16at(const uint8_t* p) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);  // 2-byte aligned
+  const uint32_t w = *reinterpret_cast<const uint32_t*>(a & ~(uintptr_t)3);
+  return (a & 2) ? f16hi(w) : f16lo(w);
+}
+
+template <uint32_t T>
+__device__ inline void deq8(const uint8_t* b, int e0, float (&v)[8]) {
+#pragma unroll
+  for (int k = 0; k < 8; ++k) v[k] = deq_elem<T>(b, e0 + k);
+}
+template <>
+__device__ inline void deq8<T_Q8_0>(const uint8_t* b, int e0, float (&v)[8]) {
+  const float d = f16at(b);
+  const uint32_t w0 = lds_u32_at(b + 2 + e0), w1 = lds_u32_at(b + 6 + e0);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    v[k] = d * (float)(int8_t)(w0 >> (8 * k));
+    v[4 + k] = d * (float)(int8_t)(w1 >> (8 * k));
+  }
+}
+template <>
+__device__ inline void deq8<T_Q4_0>(const uint8_t* b, int e0, float (&v)[8]) {
+  const float d = f16at(b);
+  const int o = e0 & 15, sh = e0 < 16 ? 0 : 4;
+  const uint32_t w0 = lds_u32_at(b + 2 + o) >> sh, w1 = lds_u32_at(b + 6 + o) >> sh;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    v[k] = (float)((int)((w0 >> (8 * k)) & 15u) - 8) * d;
+    v[4 + k] = (float)((int)((w1 >> (8 * k)) & 15u) - 8) * d;
+  }
+}
+template <>
+__device__ inline void deq8<T_Q4_K>(const uint8_t* b, int e0, float (&v)[8]) {
+  const int c = e0 >> 6, l = e0 & 63, hi = l >> 5;
+  uint32_t sc, m;
+  k4_scale_min(2 * c + hi, b + 4, sc, m);
+  const float ds = f16at(b) * (float)sc;
+  const float dm = f16at(b + 2) * (float)m;
+  const int sh = hi ? 4 : 0;
+  const uint32_t* q = reinterpret_cast<const uint32_t*>(b + 16 + 32 * c + (l & 31));  // 4-byte aligned
+  const uint32_t w0 = q[0] >> sh, w1 = q[1] >> sh;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    v[k] = ds * (float)((w0 >> (8 * k)) & 15u) - dm;
+    v[4 + k] = ds * (float)((w1 >> (8 * k)) & 15u) - dm;
+  }
+}
+template <>
+__device__ inline void deq8<T_Q6_K>(const uint8_t* b, int e0, float (&v)[8]) {
+  const int h = e0 >> 7, p = e0 & 127, quarter = p >> 5, l = p & 31;
+  const uint32_t a0 = lds_u32_at(b + 64 * h + l + 32 * (quarter & 1));
+  const uint32_t a1 = lds_u32_at(b + 64 * h + l + 32 * (quarter & 1) + 4);
+  const uint32_t h0 = lds_u32_at(b + 128 + 32 * h + l), h1 = lds_u32_at(b + 128 + 32 * h + l + 4);
+  const int nsh = (quarter & 2) ? 4 : 0, hsh = 2 * quarter;
+  const float d = f16at(b + 208);
+  const float ds = d * (float)(int8_t)b[192 + 8 * h + (l >> 4) + 2 * quarter];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int q0 = (int)(((a0 >> (8 * k + nsh)) & 15u) | (((h0 >> (8 * k + hsh)) & 3u) << 4));
+    const int q1 = (int)(((a1 >> (8 * k + nsh)) & 15u) | (((h1 >> (8 * k + hsh)) & 3u) << 4));
+    v[k] = ds * (float)(q0 - 32);
+    v[4 + k] = ds * (float)(q1 - 32);
+  }
+}
+
 constexpr int kStageElems = 2048;  // elements per workgroup of the LDS-staged kernels
 
 // Copies workgroup blockIdx.x's blocks (elements [2048 x, 2048 x + 2048) of n, whole blocks) into sm
@@ -46,28 +121,40 @@ __device__ inline void stage_blocks(const uint8_t* __restrict__ src, size_t n, u
   __syncthreads();
 }
 
-// fp32 output: dst[i] = dequant(src)[i] from the staged blocks (dst 16-byte aligned).  Q4_K / Q5_K:
-// eight consecutive elements a thread (one 32-element group: the 6-bit scale and min decoded once
-// for the eight), two 16-byte stores.  The other formats: four consecutive elements a thread per
-// round (4t .. 4t + 3, then 1024 + 4t ..), one 16-byte store each, so a wave's store covers 1 KiB
-// contiguous (measured on MI355X: Q8_0 4096 x 4096 19.9 -> 16.4 us, Q6_K 4096 x 14336 73 -> 66; Q4_K
-// on this pattern 74 -> 80, its per-element scale decode shared by four elements instead of eight).
+// fp32 output: dst[i] = dequant(src)[i] from the staged blocks (dst 16-byte aligned), stored so that
+// a wave's store covers 1 KiB contiguous.  Q4_0 / Q4_K / Q5_K: eight consecutive elements a thread
+// (one 32-element group: the block header, or the 6-bit scale and min, decoded once for the eight)
+// into LDS, then stored from there.  The other formats: four consecutive elements a thread per round
+// (4t .. 4t + 3, then 1024 + 4t ..), one 16-byte store each.  Measured on MI355X against two 16-byte
+// stores of eight elements a thread (graph-timed, weights cycled): Q4_K 14336 x 4096 73 -> 55.5 us,
+// Q4_0 11008 x 4096 51 -> 47, Q8_0 4096 x 4096 19.9 -> 16.4, Q6_K 4096 x 14336 73 -> 64; Q8_0 and
+// Q6_K on the eight-element form with LDS took 18.7 and 72.
 template <uint32_t T, int QK, int BB>
 __global__ __launch_bounds__(256) void k_dequant_lds(const uint8_t* __restrict__ src, float4* __restrict__ dst,
                                                      size_t n) {
   __shared__ uint32_t sm[kStageElems / QK * BB / 4];
   stage_blocks<QK, BB>(src, n, sm);
   const int tid = threadIdx.x;
-  if constexpr (T == T_Q4_K || T == T_Q5_K) {
-    const size_t i = (size_t)blockIdx.x * kStageElems + 8 * (size_t)tid;
-    if (i >= n) return;
+  if constexpr (T == T_Q4_0 || T == T_Q4_K || T == T_Q5_K) {
+    // eight elements a thread into LDS, then the span stored as 1 KiB a wave
+    __shared__ float4 ob[kStageElems / 4];
     const uint8_t* b = reinterpret_cast<const uint8_t*>(sm) + (8 * tid) / QK * BB;
     const int e = (8 * tid) % QK;
     float v[8];
+    if constexpr (T != T_Q5_K) {
+      deq8<T>(b, e, v);  // deq_elem's formulas and operand order, the block header decoded once
+    } else {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = deq_elem<T>(b, e + k);
-    dst[i / 4] = make_float4(v[0], v[1], v[2], v[3]);
-    dst[i / 4 + 1] = make_float4(v[4], v[5], v[6], v[7]);
+      for (int k = 0; k < 8; ++k) v[k] = deq_elem<T>(b, e + k);
+    }
+    ob[2 * tid] = make_float4(v[0], v[1], v[2], v[3]);
+    ob[2 * tid + 1] = make_float4(v[4], v[5], v[6], v[7]);
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kStageElems / 1024; ++r) {
+      const size_t i = (size_t)blockIdx.x * kStageElems + 1024 * r + 4 * tid;
+      if (i < n) dst[i / 4] = ob[256 * r + tid];
+    }
   } else {
 #pragma unroll
     for (int r = 0; r < kStageElems / 1024; ++r) {
@@ -212,81 +299,6 @@ __global__ __launch_bounds__(256) void k_dequant16_lds(const uint8_t* __restrict
 }
 
 // ---- 16-bit dequantisation, wide workgroups -------------------------------------------------------
-// Eight consecutive elements e0 .. e0 + 7 (e0 % 8 == 0) of one block in LDS, decoded with the block's
-// header read once: they always share one scale (Q8_0 / Q4_0: the block's, Q4_K: one 32-element
-// sub-block's, Q6_K: one 16-element scale group's).  Same formulas and operand order as deq_elem; the
-// fp16 scales are converted by the hardware (exact for every finite value, subnormals included).
-__device__ inline uint32_t lds_u32_at(const uint8_t* p) {  // 4 bytes at any address, from aligned dwords
-  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-  const uint32_t* w = reinterpret_cast<const uint32_t*>(a & ~(uintptr_t)3);
-  return align_bytes(w[1], w[0], (uint32_t)(a & 3));
-}
-__device__ inline float f16at(const uint8_t* p) {
-  const uintptr_t a = reinterpret_cast<uintptr_t>(p);  // 2-byte aligned
-  const uint32_t w = *reinterpret_cast<const uint32_t*>(a & ~(uintptr_t)3);
-  return (a & 2) ? f16hi(w) : f16lo(w);
-}
-
-template <uint32_t T>
-__device__ inline void deq8(const uint8_t* b, int e0, float (&v)[8]) {
-#pragma unroll
-  for (int k = 0; k < 8; ++k) v[k] = deq_elem<T>(b, e0 + k);
-}
-template <>
-__device__ inline void deq8<T_Q8_0>(const uint8_t* b, int e0, float (&v)[8]) {
-  const float d = f16at(b);
-  const uint32_t w0 = lds_u32_at(b + 2 + e0), w1 = lds_u32_at(b + 6 + e0);
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    v[k] = d * (float)(int8_t)(w0 >> (8 * k));
-    v[4 + k] = d * (float)(int8_t)(w1 >> (8 * k));
-  }
-}
-template <>
-__device__ inline void deq8<T_Q4_0>(const uint8_t* b, int e0, float (&v)[8]) {
-  const float d = f16at(b);
-  const int o = e0 & 15, sh = e0 < 16 ? 0 : 4;
-  const uint32_t w0 = lds_u32_at(b + 2 + o) >> sh, w1 = lds_u32_at(b + 6 + o) >> sh;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    v[k] = (float)((int)((w0 >> (8 * k)) & 15u) - 8) * d;
-    v[4 + k] = (float)((int)((w1 >> (8 * k)) & 15u) - 8) * d;
-  }
-}
-template <>
-__device__ inline void deq8<T_Q4_K>(const uint8_t* b, int e0, float (&v)[8]) {
-  const int c = e0 >> 6, l = e0 & 63, hi = l >> 5;
-  uint32_t sc, m;
-  k4_scale_min(2 * c + hi, b + 4, sc, m);
-  const float ds = f16at(b) * (float)sc;
-  const float dm = f16at(b + 2) * (float)m;
-  const int sh = hi ? 4 : 0;
-  const uint32_t* q = reinterpret_cast<const uint32_t*>(b + 16 + 32 * c + (l & 31));  // 4-byte aligned
-  const uint32_t w0 = q[0] >> sh, w1 = q[1] >> sh;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    v[k] = ds * (float)((w0 >> (8 * k)) & 15u) - dm;
-    v[4 + k] = ds * (float)((w1 >> (8 * k)) & 15u) - dm;
-  }
-}
-template <>
-__device__ inline void deq8<T_Q6_K>(const uint8_t* b, int e0, float (&v)[8]) {
-  const int h = e0 >> 7, p = e0 & 127, quarter = p >> 5, l = p & 31;
-  const uint32_t a0 = lds_u32_at(b + 64 * h + l + 32 * (quarter & 1));
-  const uint32_t a1 = lds_u32_at(b + 64 * h + l + 32 * (quarter & 1) + 4);
-  const uint32_t h0 = lds_u32_at(b + 128 + 32 * h + l), h1 = lds_u32_at(b + 128 + 32 * h + l + 4);
-  const int nsh = (quarter & 2) ? 4 : 0, hsh = 2 * quarter;
-  const float d = f16at(b + 208);
-  const float ds = d * (float)(int8_t)b[192 + 8 * h + (l >> 4) + 2 * quarter];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int q0 = (int)(((a0 >> (8 * k + nsh)) & 15u) | (((h0 >> (8 * k + hsh)) & 3u) << 4));
-    const int q1 = (int)(((a1 >> (8 * k + nsh)) & 15u) | (((h1 >> (8 * k + hsh)) & 3u) << 4));
-    v[k] = ds * (float)(q0 - 32);
-    v[4 + k] = ds * (float)(q1 - 32);
-  }
-}
-
 constexpr int kWideElems = 8192;  // elements per workgroup of the wide 16-bit dequantiser
 
 // A workgroup's 8192 elements are whole blocks; their bytes (a multiple of 16 in every block format at
