@@ -635,6 +635,7 @@ def main():
     ap.add_argument("--sweep-only", action="store_true", help="only the config-5 decode sweep (profiler passes)")
     ap.add_argument("--configs-only", action="store_true", help="only the configs[0..2] GEMV points (profiler passes)")
     ap.add_argument("--gemm-only", action="store_true", help="only the prefill GEMM leg (profiler passes)")
+    ap.add_argument("--dequant-only", action="store_true", help="only the fp32 dequantisation leg (profiler passes)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MiB",
                     help="also run one plain device copy of this many MiB (PMC byte-counter calibration)")
     args = ap.parse_args()
@@ -671,6 +672,11 @@ def main():
     qvx.fill_normal_t(x, seed=7)
     out = torch.empty(ROWS, dtype=torch.float32, device=dev)
     torch.cuda.synchronize()
+    if args.dequant_only:  # profiler pass over the fp32 dequantisation leg alone
+        if args.calibrate_copy:
+            calibration_copy(torch, dev, args.calibrate_copy)
+        print(json.dumps({"dequant": dequant_leg(torch, stream, t, copies)}), flush=True)
+        return
     if args.gemm_only:  # profiler pass over the prefill GEMM leg alone
         wps = [w.data_ptr() for w in copies]
         print(json.dumps({"gemm": gemm_leg(torch, stream, t, wps, copies, args.gemm_steps, cpu=not args.no_cpu)}),
