@@ -169,9 +169,14 @@ template <> struct Lane<T_Q5_K> {
 template <> struct Lane<T_Q6_K> {
   static constexpr int kR = 2;
   static constexpr int kSlotElems = 32;
+  // The 8 slots of a super-block sit on 8 consecutive lanes of one wave.  Each lane loads its ql and
+  // qh pieces as dword-aligned 16-byte windows and one dword of the super-block's last 20 bytes
+  // (scales and d); the 4-byte tails of its windows and its scale and d words are the first dwords
+  // its block's other lanes loaded (exchange), so a row costs three vector loads a lane.
   struct Raw {
     u32x4a4_t l, h;
-    uint32_t le, he, s0, s1, dd;
+    uint32_t w;    // lane u of the block: dword min(u, 4) of the scale window
+    uint32_t le, he, s0, s1, dd;  // filled by exchange
     uint32_t sh;   // byte misalignment of the pieces (0 or 2)
     uint32_t ssh;  // byte position of the first scale inside s0
   };
@@ -179,20 +184,36 @@ template <> struct Lane<T_Q6_K> {
     const int u = sig & 7;
     return 256 * (sig >> 3) + 128 * (u >> 2) + 32 * (u & 1) + 16 * ((u >> 1) & 1) + 64 * run;
   }
+  // Super-block b = sig / 8 starts at byte 210 b: its pieces are misaligned by sh = 2 (b odd) or 0.
+  // Lane u = sig % 8 (half h, piece t, bit pair e) owns ql bytes [64h + 32e + 16t, +16) and qh
+  // bytes [128 + 32h + 16t, +16); the scale window is [192 - sh, 208 - sh) in dwords 0..3 and
+  // [206, 210) in dword 4, every byte inside the super-block.
   static __device__ inline void load(const uint8_t* row, int sig, Raw& r) {
     const int b = sig >> 3, u = sig & 7, h = u >> 2, t = (u >> 1) & 1, e = u & 1;
-    const int base = 210 * b;
+    const int base = 210 * b, sh = base & 3;
     const int ol = base + 64 * h + 32 * e + 16 * t, oh = base + 128 + 32 * h + 16 * t;
-    const int os = base + 192 + 8 * h + t + 2 * e;
-    r.sh = (uint32_t)(ol & 3);
-    r.l = ldg16a4(row + (ol & ~3));
-    r.le = ldg4(row + (ol & ~3) + 16);
-    r.h = ldg16a4(row + (oh & ~3));
-    r.he = ldg4(row + (oh & ~3) + 16);
-    r.ssh = (uint32_t)(os & 3);
-    r.s0 = ldg4(row + (os & ~3));
-    r.s1 = ldg4(row + (os & ~3) + 4);
-    r.dd = ldg2(row + base + 208);
+    r.sh = (uint32_t)sh;
+    r.l = ldg16a4(row + ol - sh);
+    r.h = ldg16a4(row + oh - sh);
+    r.w = ldg4(row + (u < 4 ? base + 192 - sh + 4 * u : base + 206));
+  }
+  // The words a lane takes from its block's lanes (bl: wave lane of the block's slot 0; padding
+  // lanes pass the block of the slot they mirror).  le: the first dword after the ql window, the
+  // next ql piece's (the piece at 128 is lane 0's qh window); he: the next qh piece's (after the
+  // last one, scale dword 0); s0, s1: the dwords holding scale i = 8h + t + 2e and i + 4; dd: d.
+  static __device__ inline void exchange(Raw& r, int sig, int bl) {
+    const int u = sig & 7, h = u >> 2, t = (u >> 1) & 1, e = u & 1;
+    const int nl = 64 * h + 32 * e + 16 * t + 16, nh = 32 * h + 16 * t + 16;
+    const int ul = nl == 128 ? 0 : 4 * (nl >> 6) + 2 * ((nl >> 4) & 1) + ((nl >> 5) & 1);
+    const int uh = nh == 64 ? 0 : 4 * (nh >> 5) + 2 * ((nh >> 4) & 1);
+    const int pl = (int)(u == 0 ? r.h.x : r.l.x), ph = (int)(u == 0 ? r.w : r.h.x);
+    const int si = (int)r.sh + 8 * h + t + 2 * e, q = si >> 2, ab = 4 * bl;
+    r.le = (uint32_t)__builtin_amdgcn_ds_bpermute(ab + 4 * ul, pl);
+    r.he = (uint32_t)__builtin_amdgcn_ds_bpermute(ab + 4 * uh, ph);
+    r.s0 = (uint32_t)__builtin_amdgcn_ds_bpermute(ab + 4 * q, (int)r.w);
+    r.s1 = (uint32_t)__builtin_amdgcn_ds_bpermute(ab + 4 * (q + 1), (int)r.w);
+    r.dd = (uint32_t)__builtin_amdgcn_ds_bpermute(ab + 16, (int)r.w) >> 16;
+    r.ssh = (uint32_t)(si & 3);
   }
   static __device__ inline float row(const Raw& r, int sig, const XQ<2>& x) {
     const uint32_t e = (uint32_t)(sig & 1);
@@ -558,6 +579,9 @@ __device__ __forceinline__ void gemv_valu_body(const uint8_t* __restrict__ W, co
 #pragma unroll
   for (int v = 0; v < NV; ++v) read_xq<R>(xs + ((size_t)v * S + sig) * xq_words<R>(), x[v]);
   const float keep = sig0 < S ? 1.0f : 0.0f;
+  // wave lane of the first slot of this lane's super-block (a group starts at a multiple of 8 lanes,
+  // and its padding lanes share the wave of its last slot, whose block they mirror)
+  const int blane = (g * Sp + (sig & ~7)) & 63;
   static_assert(!CH || RMAX % PF == 0, "chunks keep the prefetch ring aligned");
   const int nchunk = CH ? ((cnt + G - 1) / G + RMAX - 1) / RMAX : 1;  // the same for every group
   for (int c = 0; c < nchunk; ++c) {
@@ -565,6 +589,7 @@ __device__ __forceinline__ void gemv_valu_body(const uint8_t* __restrict__ W, co
     float p[RMAX][NV];
 #pragma unroll
     for (int i = 0; i < RMAX; ++i) {
+      if constexpr (T == T_Q6_K) L::exchange(raw[i % PF], sig, blane);
 #pragma unroll
       for (int v = 0; v < NV; ++v) {
         p[i][v] = L::row(raw[i % PF], sig, x[v]) * (x[v].sx * keep);
