@@ -266,12 +266,6 @@ inline WsForm ws_route(uint32_t type, int nvec, int rows, int cols, size_t row_b
   *bytes = 0;
   return WS_NONE;
 }
-inline size_t ws_route_bytes(uint32_t type, int nvec, int rows, int cols, size_t row_bytes, bool fast,
-                             const GemvEpi& epi) {
-  size_t b = 0;
-  return ws_route(type, nvec, rows, cols, row_bytes, fast, epi, &b) == WS_NONE ? 0 : b;
-}
-
 int gemv(float* out, const void* w, uint32_t type, const float* X, int nvec, int rows, int cols, hipStream_t s,
          const GemvEpi& epi) {
   const TypeInfo* ti = nullptr;

@@ -165,7 +165,8 @@ template <> struct Lane<T_Q5_K> {
 // Run 0 is quarter e (low nibbles of ql[64h + 32e + 16t ..+16]), run 1 quarter e+2 (their high
 // nibbles), with 2-bit high parts from qh[32h + 16t ..+16], bits (2e, 2e+1) and (2e+4, 2e+5);
 // scales sc[8h + t + 2e] and sc[8h + t + 2e + 4].  Super-blocks are 2-byte aligned: each 16-byte
-// piece is read as a dword-aligned 20-byte window (never past its super-block) and realigned.
+// piece is read as a dword-aligned 16-byte window, completed by the 4-byte tail the lane of the next
+// piece loaded (never past its super-block), and realigned.
 template <> struct Lane<T_Q6_K> {
   static constexpr int kR = 2;
   static constexpr int kSlotElems = 32;
