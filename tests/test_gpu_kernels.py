@@ -606,6 +606,8 @@ GROUP_CASES = [
     ("ragged", 2048, [(qvx.Q4_K, 777), (qvx.Q6_K, 20000), (qvx.Q4_K, 17), (qvx.Q4_K, 1), (qvx.Q4_K, 300)]),
     # a Q6_K member walking its rows in chunks (10 rows a group)
     ("chunked", 2048, [(qvx.Q6_K, 40000), (qvx.Q4_K, 64)]),
+    # K = 2304: 72 Q6_K slots in groups of 128 lanes, the padding lanes mirroring the last slot
+    ("padded", 2304, [(qvx.Q6_K, 300), (qvx.Q4_K, 64)]),
     # outside the grouped kernel (two Q6_K members; five Q4_K; a Q8_0 member; a Q6_K row of 448
     # slots, whose VALU workgroup is not 1024 threads): member by member
     ("two_q6k", 4096, [(qvx.Q6_K, 1024), (qvx.Q6_K, 512)]),
